@@ -1,0 +1,126 @@
+// Shared device helpers for the cinnamon FP8 path on gfx950 (CDNA4).
+//
+// Arithmetic restated from the reference quantizers
+// (reference src/kernels.py:50-62 row-wise, :111-123 block-wise):
+//   amax  = maxnum-reduction of |x| over the tile (NaN elements ignored, as
+//           Triton's tl.max / tl.maximum lower to maxnum)
+//   amax  = maxnum(amax, floor)   floor = 1e-4 rounded to the INPUT dtype,
+//           because Triton computes tl.maximum(bf16_tensor, 1e-4) in bf16
+//   scale = fp32(amax) / 448      (IEEE fp32 division), or with round_scale
+//           exp2(ceil(log2(amax / 448)))
+//   code  = e4m3fn_rne(minnum(maxnum(x / scale, -448), 448))
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/cinnamon_fp8.h"
+
+namespace cin {
+
+constexpr float kFp8Max = 448.0f;
+// 1e-4 rounded to each supported input dtype (the floor of the tile amax).
+constexpr float kFloorF32 = 9.99999974737875163555e-05f;   // fp32(1e-4)
+constexpr float kFloorBF16 = 1.0013580322265625e-04f;      // bf16(1e-4)
+constexpr float kFloorF16 = 1.0001659393310546875e-04f;    // fp16(1e-4)
+
+__host__ __device__ inline float amax_floor(int dtype) {
+  return dtype == CIN_DT_BF16 ? kFloorBF16 : (dtype == CIN_DT_F16 ? kFloorF16 : kFloorF32);
+}
+
+// Scale from a floored amax.  round_scale follows torch.exp2(torch.ceil(torch.log2(v)))
+// in fp32, where torch's log2 is correctly rounded over the reachable range: for
+// v = 2^k * (1 + m * 2^-23), m > 0, fl32(log2 v) stays equal to k (so the ceiling is
+// k, not k + 1) while m is below a threshold fixed by the fp32 spacing just above
+// (k >= 0) or just below (k < 0) the integer k.
+__device__ inline float compute_scale(float amax, bool round_scale) {
+  float v = amax / kFp8Max;
+  if (!round_scale) return v;
+  uint32_t b = __float_as_uint(v);
+  if (!(v > 0.0f) || b >= 0x7f800000u) return v;   // inf/NaN pass through (exp2(inf) = inf)
+  int k = (int)(b >> 23) - 127;
+  uint32_t m = b & 0x7fffffu;
+  if (k < -126 + 1) {
+    // Not reachable: amax >= 1e-4 keeps v above 2^-22.
+    return v;
+  }
+  int e = k;
+  if (m != 0) {
+    int a = k > 0 ? k : (k < 0 ? -k - 1 : 0);
+    int j = a ? 31 - __builtin_clz((unsigned)a) : -1;
+    uint32_t t = j <= 1 ? 1u : (j == 2 ? 2u : (j == 3 ? 3u : (j == 4 ? 6u : (j == 5 ? 12u : 23u))));
+    e = (m >= t) ? k + 1 : k;
+  }
+  if (e > 127) return __uint_as_float(0x7f800000u);
+  return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
+// Clamp with maxnum/minnum semantics: NaN maps to -448 like the reference's
+// tl.minimum(tl.maximum(x, -448), 448).
+__device__ inline float clamp448(float y) {
+  return fminf(fmaxf(y, -kFp8Max), kFp8Max);
+}
+
+// Two fp32 (already clamped to [-448, 448]) -> two OCP e4m3fn codes in the low
+// 16 bits, round-to-nearest-even.  gfx950's conversion was checked bit-exact
+// against a software RNE over every finite magnitude <= 448.
+__device__ inline uint32_t cvt2_e4m3(float a, float b) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+}
+// Four clamped fp32 -> packed 4 codes (byte i = value i).
+__device__ inline uint32_t cvt4_e4m3(float a, float b, float c, float d) {
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
+// e4m3fn code -> fp32 (exact).
+__device__ inline float e4m3_to_f32(uint32_t c) {
+  uint32_t s = (c & 0x80u) << 24;
+  uint32_t e = (c >> 3) & 0xfu;
+  uint32_t m = c & 0x7u;
+  if (e == 0xfu && m == 0x7u) return __uint_as_float(s | 0x7fc00000u);
+  if (e == 0) {
+    const float v = (float)m * 0.001953125f;  // m * 2^-9, exact
+    return s ? -v : v;
+  }
+  return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+}
+
+__device__ inline float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> bf16 bits with round-to-nearest-even (NaN kept quiet).
+__device__ inline uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Load one element of dtype `dt` at element index i and widen to fp32 (exact).
+__device__ inline float load_elem(const void* p, int dt, int64_t i) {
+  if (dt == CIN_DT_BF16) return __uint_as_float(((uint32_t)((const uint16_t*)p)[i]) << 16);
+  if (dt == CIN_DT_F16) return (float)((const _Float16*)p)[i];
+  return ((const float*)p)[i];
+}
+
+// Max over the 16 lanes of a DPP row (lanes 16r..16r+15), maxnum semantics.
+__device__ inline float row16_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));  // quad [1,0,3,2]
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));  // quad [2,3,0,1]
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false))); // row_half_mirror
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false))); // row_mirror
+  return v;
+}
+
+// Max over a whole wave64.
+__device__ inline float wave_max(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace cin

@@ -1,0 +1,696 @@
+// FP8 e4m3 quantizers, dequantizer, dual (row + transposed) quantizer, row->block
+// re-quantizer and byte transpose for gfx950.  All arithmetic follows the
+// reference quantizers (src/kernels.py:19-132) as restated in cin_common.h.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "cin_common.h"
+#include "cin_runtime.h"
+
+using namespace cin;
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// ---------------------------------------------------------------------------
+// Row-wise 1x128, contiguous rows: each 16-lane DPP row owns one 128-element
+// tile (8 elements per lane, one 16-byte load for bf16/fp16, two for fp32).
+// A group walks tiles t, t + G, t + 2G, ... with U tiles loaded before use so
+// several loads are in flight per lane.
+// ---------------------------------------------------------------------------
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int DT>
+struct Vec8 {
+  float v[8];
+};
+
+template <int DT>
+__device__ inline void load8(const void* base, int64_t off, int64_t ncols, Vec8<DT>& o) {
+  // off: element offset of the lane's first element; ncols: valid elements (<= 8)
+  if (ncols >= 8) {
+    if constexpr (DT == CIN_DT_F32) {
+      const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(base) + off);
+      f32x4 a = __builtin_nontemporal_load(p);
+      f32x4 b = __builtin_nontemporal_load(p + 1);
+      o.v[0] = a[0]; o.v[1] = a[1]; o.v[2] = a[2]; o.v[3] = a[3];
+      o.v[4] = b[0]; o.v[5] = b[1]; o.v[6] = b[2]; o.v[7] = b[3];
+    } else {
+      const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + off);
+      u32x4 w = __builtin_nontemporal_load(p);
+      uint32_t ws[4] = {w[0], w[1], w[2], w[3]};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (DT == CIN_DT_BF16) {
+          o.v[2 * i] = bf16_lo(ws[i]);
+          o.v[2 * i + 1] = bf16_hi(ws[i]);
+        } else {
+          _Float16 h0, h1;
+          uint16_t b0 = (uint16_t)(ws[i] & 0xffffu), b1 = (uint16_t)(ws[i] >> 16);
+          __builtin_memcpy(&h0, &b0, 2);
+          __builtin_memcpy(&h1, &b1, 2);
+          o.v[2 * i] = (float)h0;
+          o.v[2 * i + 1] = (float)h1;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o.v[i] = (i < ncols) ? load_elem(base, DT, off + i) : 0.0f;
+  }
+}
+
+template <int DT, int U>
+__global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict__ x, int64_t N,
+                                                         int64_t sxm, int round_scale,
+                                                         uint8_t* __restrict__ q, int64_t sqm,
+                                                         float* __restrict__ sc, int64_t ssm,
+                                                         uint32_t nb, uint32_t ntiles) {
+  const uint32_t lane16 = threadIdx.x & 15u;
+  const uint32_t G = (gridDim.x * kThreads) >> 4;  // number of 16-lane groups
+  const uint32_t g0 = (blockIdx.x * kThreads + threadIdx.x) >> 4;
+  const float floor_v = amax_floor(DT);
+  const bool rs = round_scale != 0;
+  for (uint32_t tb = g0; tb < ntiles; tb += G * U) {
+    Vec8<DT> d[U];
+    uint32_t row[U], cb[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      uint32_t t = tb + (uint32_t)u * G;
+      row[u] = t / nb;
+      cb[u] = t - row[u] * nb;
+      int64_t col = (int64_t)cb[u] * 128 + lane16 * 8;
+      int64_t nc = (t < ntiles) ? (N - col) : 0;
+      load8<DT>(x, (int64_t)row[u] * sxm + col, nc < 0 ? 0 : nc, d[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      uint32_t t = tb + (uint32_t)u * G;
+      if (t >= ntiles) break;  // uniform across the 16-lane row
+      float a = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(d[u].v[i]));
+      a = row16_max(a);
+      a = fmaxf(a, floor_v);
+      const float s = compute_scale(a, rs);
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = clamp448(d[u].v[i] / s);
+      uint32_t lo = cvt4_e4m3(y[0], y[1], y[2], y[3]);
+      uint32_t hi = cvt4_e4m3(y[4], y[5], y[6], y[7]);
+      int64_t col = (int64_t)cb[u] * 128 + lane16 * 8;
+      uint8_t* qp = q + (int64_t)row[u] * sqm + col;
+      if (col + 8 <= N) {
+        *reinterpret_cast<uint2*>(qp) = make_uint2(lo, hi);
+      } else {
+        for (int i = 0; i < 8; ++i)
+          if (col + i < N) qp[i] = (uint8_t)(((i < 4 ? lo : hi) >> (8 * (i & 3))) & 0xffu);
+      }
+      if (lane16 == 0) sc[(int64_t)row[u] * ssm + cb[u]] = s;
+    }
+  }
+}
+
+// Generic row-wise: one wave per (row, tile), any block size / strides / dtype.
+__global__ __launch_bounds__(kThreads) void k_rowwise_generic(const void* __restrict__ x, int dt,
+                                                              int64_t M, int64_t N, int64_t sxm,
+                                                              int64_t sxn, int64_t block,
+                                                              int round_scale, uint8_t* q,
+                                                              int64_t sqm, float* sc, int64_t ssm,
+                                                              int64_t nb) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = ((int64_t)blockIdx.x * kThreads + threadIdx.x) >> 6;
+  const int64_t W = ((int64_t)gridDim.x * kThreads) >> 6;
+  const float floor_v = amax_floor(dt);
+  for (int64_t t = w; t < M * nb; t += W) {
+    const int64_t row = t / nb, cb = t - row * nb;
+    const int64_t c0 = cb * block;
+    const int64_t c1 = (c0 + block < N) ? c0 + block : N;
+    float a = 0.0f;
+    for (int64_t c = c0 + lane; c < c1; c += 64) a = fmaxf(a, fabsf(load_elem(x, dt, row * sxm + c * sxn)));
+    a = wave_max(a);
+    a = fmaxf(a, floor_v);
+    const float s = compute_scale(a, round_scale != 0);
+    for (int64_t c = c0 + lane; c < c1; c += 64) {
+      float y = clamp448(load_elem(x, dt, row * sxm + c * sxn) / s);
+      q[row * sqm + c] = (uint8_t)cvt2_e4m3(y, 0.0f);
+    }
+    if (lane == 0) sc[row * ssm + cb] = s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Block-wise generic: one workgroup per (bm x bn) block, two passes (the second
+// read hits L2).  Optional transposed code output.
+// ---------------------------------------------------------------------------
+__device__ inline float block_reduce_max(float v, float* red) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < kThreads / 64; ++i) r = fmaxf(r, red[i]);
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(kThreads) void k_blockwise_generic(
+    const void* __restrict__ x, int dt, int64_t M, int64_t N, int64_t sxm, int64_t sxn, int64_t bm,
+    int64_t bn, int round_scale, uint8_t* q, int64_t sqm, uint8_t* qt, int64_t sqtm, float* sc,
+    int64_t ssm, int64_t nbn) {
+  __shared__ float red[kThreads / 64];
+  const int64_t rb = blockIdx.y, cb = blockIdx.x;
+  const int64_t r0 = rb * bm, c0 = cb * bn;
+  const int64_t nr = (r0 + bm < M ? bm : M - r0), nc = (c0 + bn < N ? bn : N - c0);
+  const int64_t n = nr * nc;
+  float a = 0.0f;
+  for (int64_t i = threadIdx.x; i < n; i += kThreads) {
+    const int64_t r = r0 + i / nc, c = c0 + i % nc;
+    a = fmaxf(a, fabsf(load_elem(x, dt, r * sxm + c * sxn)));
+  }
+  a = block_reduce_max(a, red);
+  a = fmaxf(a, amax_floor(dt));
+  const float s = compute_scale(a, round_scale != 0);
+  for (int64_t i = threadIdx.x; i < n; i += kThreads) {
+    const int64_t r = r0 + i / nc, c = c0 + i % nc;
+    const float y = clamp448(load_elem(x, dt, r * sxm + c * sxn) / s);
+    const uint8_t code = (uint8_t)cvt2_e4m3(y, 0.0f);
+    if (q) q[r * sqm + c] = code;
+    if (qt) qt[c * sqtm + r] = code;
+  }
+  if (threadIdx.x == 0) sc[rb * ssm + cb] = s;
+}
+
+// Block-wise 128x128 with contiguous rows: the block stays in registers
+// (8 rows x 8 columns per thread), one HBM read.  The transposed output goes
+// through a padded LDS byte tile so both layouts are written coalesced.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_blockwise128(const void* __restrict__ x, int64_t M,
+                                                           int64_t N, int64_t sxm, int round_scale,
+                                                           uint8_t* q, int64_t sqm, uint8_t* qt,
+                                                           int64_t sqtm, float* sc, int64_t ssm) {
+  __shared__ float red[kThreads / 64];
+  __shared__ uint32_t tileT[128][128 / 4 + 1];  // transposed codes, [col][row/4] words
+  const int64_t rb = blockIdx.y, cb = blockIdx.x;
+  const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;  // rg: 0..15
+  const int64_t c = cb * 128 + lane16 * 8;
+  Vec8<DT> d[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t r = rb * 128 + rg + 16 * i;
+    const int64_t nc = (r < M) ? N - c : 0;
+    load8<DT>(x, r * sxm + c, nc < 0 ? 0 : (nc > 8 ? 8 : nc), d[i]);
+  }
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(d[i].v[j]));
+  a = block_reduce_max(a, red);
+  a = fmaxf(a, amax_floor(DT));
+  const float s = compute_scale(a, round_scale != 0);
+  uint32_t codes[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = clamp448(d[i].v[j] / s);
+    codes[i][0] = cvt4_e4m3(y[0], y[1], y[2], y[3]);
+    codes[i][1] = cvt4_e4m3(y[4], y[5], y[6], y[7]);
+  }
+  if (q) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t r = rb * 128 + rg + 16 * i;
+      if (r >= M) continue;
+      uint8_t* qp = q + r * sqm + c;
+      if (c + 8 <= N) {
+        *reinterpret_cast<uint2*>(qp) = make_uint2(codes[i][0], codes[i][1]);
+      } else {
+        for (int j = 0; j < 8; ++j)
+          if (c + j < N) qp[j] = (uint8_t)((codes[i][j >> 2] >> (8 * (j & 3))) & 0xffu);
+      }
+    }
+  }
+  if (qt) {
+    // scatter bytes into the transposed tile: tileT[col][row]
+    uint8_t* tb = reinterpret_cast<uint8_t*>(&tileT[0][0]);
+    constexpr int kRowBytes = (128 / 4 + 1) * 4;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * i] =
+            (uint8_t)((codes[i][j >> 2] >> (8 * (j & 3))) & 0xffu);
+    __syncthreads();
+    // each thread writes 16 bytes: tile column tc, rows 16*seg .. +16
+    for (int idx = threadIdx.x; idx < 128 * 8; idx += kThreads) {
+      const int tc = idx >> 3, seg = idx & 7;
+      const int64_t n = cb * 128 + tc;
+      const int64_t m0 = rb * 128 + seg * 16;
+      if (n >= N) continue;
+      const uint32_t* src = &tileT[tc][seg * 4];
+      uint8_t* dst = qt + n * sqtm + m0;
+      if (m0 + 16 <= M) {
+        *reinterpret_cast<uint4*>(dst) = make_uint4(src[0], src[1], src[2], src[3]);
+      } else {
+        for (int k = 0; k < 16; ++k)
+          if (m0 + k < M) dst[k] = (uint8_t)((src[k >> 2] >> (8 * (k & 3))) & 0xffu);
+      }
+    }
+  }
+  if (threadIdx.x == 0) sc[rb * ssm + cb] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Dual 1x128 quantization of dy (row tiles of dy and of dy^T) from one read.
+// Workgroup per 128x128 tile; thread holds rows rg + 16 i, columns lane16*8 + j.
+// ---------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x, int64_t M,
+                                                      int64_t N, int64_t sxm, int round_scale,
+                                                      uint8_t* q, int64_t sqm, float* s,
+                                                      int64_t ssm, uint8_t* qt, int64_t sqtm,
+                                                      float* st, int64_t sstm) {
+  __shared__ float colpart[16][128];
+  __shared__ float colscale[128];
+  __shared__ uint32_t tileT[128][128 / 4 + 1];
+  const int64_t rb = blockIdx.y, cb = blockIdx.x;
+  const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
+  const int64_t c = cb * 128 + lane16 * 8;
+  const bool rs = round_scale != 0;
+  const float floor_v = amax_floor(DT);
+  Vec8<DT> d[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t r = rb * 128 + rg + 16 * i;
+    const int64_t nc = (r < M) ? N - c : 0;
+    load8<DT>(x, r * sxm + c, nc < 0 ? 0 : (nc > 8 ? 8 : nc), d[i]);
+  }
+  // column partial maxima over this thread's 8 rows
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(d[i].v[j]));
+    colpart[rg][lane16 * 8 + j] = a;
+  }
+  // row tiles: quantize and store
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t r = rb * 128 + rg + 16 * i;
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(d[i].v[j]));
+    a = row16_max(a);
+    a = fmaxf(a, floor_v);
+    const float sr = compute_scale(a, rs);
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = clamp448(d[i].v[j] / sr);
+    const uint32_t lo = cvt4_e4m3(y[0], y[1], y[2], y[3]);
+    const uint32_t hi = cvt4_e4m3(y[4], y[5], y[6], y[7]);
+    if (r < M) {
+      uint8_t* qp = q + r * sqm + c;
+      if (c + 8 <= N) {
+        *reinterpret_cast<uint2*>(qp) = make_uint2(lo, hi);
+      } else {
+        for (int j = 0; j < 8; ++j)
+          if (c + j < N) qp[j] = (uint8_t)(((j < 4 ? lo : hi) >> (8 * (j & 3))) & 0xffu);
+      }
+      if (lane16 == 0) s[r * ssm + cb] = sr;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 128) {
+    float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) a = fmaxf(a, colpart[k][threadIdx.x]);
+    a = fmaxf(a, floor_v);
+    const float sc = compute_scale(a, rs);
+    colscale[threadIdx.x] = sc;
+    const int64_t n = cb * 128 + threadIdx.x;
+    if (n < N) st[n * sstm + rb] = sc;
+  }
+  __syncthreads();
+  uint8_t* tb = reinterpret_cast<uint8_t*>(&tileT[0][0]);
+  constexpr int kRowBytes = (128 / 4 + 1) * 4;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float sc = colscale[lane16 * 8 + j];
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const uint32_t p = cvt2_e4m3(clamp448(d[i].v[j] / sc), clamp448(d[i + 1].v[j] / sc));
+      tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * i] = (uint8_t)(p & 0xffu);
+      tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * (i + 1)] = (uint8_t)(p >> 8);
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 128 * 8; idx += kThreads) {
+    const int tc = idx >> 3, seg = idx & 7;
+    const int64_t n = cb * 128 + tc;
+    const int64_t m0 = rb * 128 + seg * 16;
+    if (n >= N) continue;
+    const uint32_t* src = &tileT[tc][seg * 4];
+    uint8_t* dst = qt + n * sqtm + m0;
+    if (m0 + 16 <= M) {
+      *reinterpret_cast<uint4*>(dst) = make_uint4(src[0], src[1], src[2], src[3]);
+    } else {
+      for (int k = 0; k < 16; ++k)
+        if (m0 + k < M) dst[k] = (uint8_t)((src[k >> 2] >> (8 * (k & 3))) & 0xffu);
+    }
+  }
+}
+
+// Generic dual: the two generic row-wise passes (dy row tiles, dy^T row tiles).
+// (Used only when dy rows are not contiguous / aligned.)
+
+// ---------------------------------------------------------------------------
+// Re-quantization row(1x128) -> block(128x128).  x = fp32(code) * srow (fp32
+// product, as torch's dequantize_fp8_rowwise), then the block quantizer with
+// the fp32 floor and round_scale = False.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void k_requant128(const uint8_t* __restrict__ q, int64_t M,
+                                                         int64_t K, int64_t sqm,
+                                                         const float* __restrict__ srow,
+                                                         int64_t ssm, uint8_t* qb, int64_t sqbm,
+                                                         uint8_t* qbt, int64_t sqbtm, float* sblk,
+                                                         int64_t ssbm) {
+  __shared__ float red[kThreads / 64];
+  __shared__ uint32_t tileT[128][128 / 4 + 1];
+  const int64_t rb = blockIdx.y, cb = blockIdx.x;
+  const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
+  const int64_t c = cb * 128 + lane16 * 8;
+  float v[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t r = rb * 128 + rg + 16 * i;
+    uint32_t w0 = 0, w1 = 0;
+    float sr = 0.0f;
+    if (r < M) {
+      sr = srow[r * ssm + cb];
+      const uint8_t* qp = q + r * sqm + c;
+      if (c + 8 <= K) {
+        uint2 w = *reinterpret_cast<const uint2*>(qp);
+        w0 = w.x;
+        w1 = w.y;
+      } else {
+        for (int j = 0; j < 8; ++j)
+          if (c + j < K) (j < 4 ? w0 : w1) |= (uint32_t)qp[j] << (8 * (j & 3));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t code = ((j < 4 ? w0 : w1) >> (8 * (j & 3))) & 0xffu;
+      const bool valid = (r < M) && (c + j < K);
+      v[i][j] = valid ? __fmul_rn(e4m3_to_f32(code), sr) : 0.0f;
+    }
+  }
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(v[i][j]));
+  a = block_reduce_max(a, red);
+  a = fmaxf(a, kFloorF32);
+  const float s = compute_scale(a, false);
+  uint32_t codes[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = clamp448(v[i][j] / s);
+    codes[i][0] = cvt4_e4m3(y[0], y[1], y[2], y[3]);
+    codes[i][1] = cvt4_e4m3(y[4], y[5], y[6], y[7]);
+  }
+  if (qb) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t r = rb * 128 + rg + 16 * i;
+      if (r >= M) continue;
+      uint8_t* qp = qb + r * sqbm + c;
+      if (c + 8 <= K) {
+        *reinterpret_cast<uint2*>(qp) = make_uint2(codes[i][0], codes[i][1]);
+      } else {
+        for (int j = 0; j < 8; ++j)
+          if (c + j < K) qp[j] = (uint8_t)((codes[i][j >> 2] >> (8 * (j & 3))) & 0xffu);
+      }
+    }
+  }
+  if (qbt) {
+    uint8_t* tb = reinterpret_cast<uint8_t*>(&tileT[0][0]);
+    constexpr int kRowBytes = (128 / 4 + 1) * 4;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * i] =
+            (uint8_t)((codes[i][j >> 2] >> (8 * (j & 3))) & 0xffu);
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 128 * 8; idx += kThreads) {
+      const int tc = idx >> 3, seg = idx & 7;
+      const int64_t n = cb * 128 + tc;
+      const int64_t m0 = rb * 128 + seg * 16;
+      if (n >= K) continue;
+      const uint32_t* src = &tileT[tc][seg * 4];
+      uint8_t* dst = qbt + n * sqbtm + m0;
+      if (m0 + 16 <= M) {
+        *reinterpret_cast<uint4*>(dst) = make_uint4(src[0], src[1], src[2], src[3]);
+      } else {
+        for (int k = 0; k < 16; ++k)
+          if (m0 + k < M) dst[k] = (uint8_t)((src[k >> 2] >> (8 * (k & 3))) & 0xffu);
+      }
+    }
+  }
+  if (threadIdx.x == 0) sblk[rb * ssbm + cb] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Dequantization: out = fp32(code) * scale[m / bm, n / bn]  (fp32 product),
+// stored as fp32 or as bf16 (round-to-nearest-even).  Thread = 8 columns.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void k_dequant(const uint8_t* __restrict__ q, int64_t M,
+                                                      int64_t N, int64_t sqm, int64_t sqn,
+                                                      const float* __restrict__ sc, int64_t ssm,
+                                                      int64_t ssn, int64_t bm, int64_t bn,
+                                                      void* out, int odt, int64_t som) {
+  const int64_t nchunk = cdiv(N, 8);
+  const int64_t total = M * nchunk;
+  for (int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x; t < total;
+       t += (int64_t)gridDim.x * kThreads) {
+    const int64_t m = t / nchunk, c0 = (t - m * nchunk) * 8;
+    const float* srow = sc + (m / bm) * ssm;
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t n = c0 + j;
+      v[j] = (n < N) ? __fmul_rn(e4m3_to_f32(q[m * sqm + n * sqn]), srow[(n / bn) * ssn]) : 0.0f;
+    }
+    if (odt == CIN_DT_F32) {
+      float* o = static_cast<float*>(out) + m * som + c0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (c0 + j < N) o[j] = v[j];
+    } else {
+      uint16_t* o = static_cast<uint16_t*>(out) + m * som + c0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (c0 + j < N) o[j] = (uint16_t)f32_to_bf16_bits(v[j]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Byte transpose through a 64x64 LDS tile.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void k_transpose_u8(const uint8_t* __restrict__ src,
+                                                           int64_t R, int64_t C, int64_t lds,
+                                                           uint8_t* __restrict__ dst,
+                                                           int64_t ldd) {
+  __shared__ uint8_t tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  for (int i = threadIdx.x; i < 64 * 64; i += kThreads) {
+    const int rr = i >> 6, cc = i & 63;
+    if (r0 + rr < R && c0 + cc < C) tile[rr][cc] = src[(r0 + rr) * lds + c0 + cc];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 64 * 64; i += kThreads) {
+    const int cc = i >> 6, rr = i & 63;
+    if (r0 + rr < R && c0 + cc < C) dst[(c0 + cc) * ldd + r0 + rr] = tile[rr][cc];
+  }
+}
+
+inline int elem_size(int dt) { return dt == CIN_DT_F32 ? 4 : 2; }
+inline bool valid_dtype(int dt) { return dt == CIN_DT_BF16 || dt == CIN_DT_F32 || dt == CIN_DT_F16; }
+inline bool aligned(const void* p, int a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
+
+inline unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
+  int64_t g = cdiv(work_items, per_block);
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (unsigned)g;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cin_quant_rowwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t sxm, int64_t sxn,
+                      int64_t block, int round_scale, uint8_t* q, int64_t sqm, float* scales,
+                      int64_t ssm, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(x_dtype), "quant_rowwise: unsupported x dtype %d", x_dtype);
+  CIN_CHECK_ARG(M >= 0 && N >= 0, "quant_rowwise: negative shape");
+  CIN_CHECK_ARG(block >= 1 && block <= 1024, "quant_rowwise: block %lld outside [1, 1024]",
+                (long long)block);
+  if (M == 0 || N == 0) return CIN_OK;
+  CIN_CHECK_ARG(x && q && scales, "quant_rowwise: null pointer");
+  const int64_t nb = cdiv(N, block);
+  CIN_CHECK_ARG(sqm >= N && ssm >= nb, "quant_rowwise: output row stride too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int es = elem_size(x_dtype);
+  const bool fast = block == 128 && sxn == 1 && aligned(x, 16) && ((sxm * es) % 16 == 0) &&
+                    aligned(q, 8) && (sqm % 8 == 0) && M * nb < (int64_t)1 << 31;
+  if (fast) {
+    const uint32_t ntiles = (uint32_t)(M * nb);
+    constexpr int U = 4;
+    const unsigned grid = grid_for(ntiles, (kThreads / 16) * U, 8192);
+    if (x_dtype == CIN_DT_BF16)
+      hipLaunchKernelGGL((k_rowwise128<CIN_DT_BF16, U>), grid, kThreads, 0, s, x, N, sxm,
+                         round_scale, q, sqm, scales, ssm, (uint32_t)nb, ntiles);
+    else if (x_dtype == CIN_DT_F16)
+      hipLaunchKernelGGL((k_rowwise128<CIN_DT_F16, U>), grid, kThreads, 0, s, x, N, sxm,
+                         round_scale, q, sqm, scales, ssm, (uint32_t)nb, ntiles);
+    else
+      hipLaunchKernelGGL((k_rowwise128<CIN_DT_F32, U>), grid, kThreads, 0, s, x, N, sxm,
+                         round_scale, q, sqm, scales, ssm, (uint32_t)nb, ntiles);
+  } else {
+    const unsigned grid = grid_for(M * nb, kThreads / 64, 65536);
+    hipLaunchKernelGGL(k_rowwise_generic, grid, kThreads, 0, s, x, x_dtype, M, N, sxm, sxn, block,
+                       round_scale, q, sqm, scales, ssm, nb);
+  }
+  return cin_check_launch("quant_rowwise");
+}
+
+int cin_quant_blockwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t sxm, int64_t sxn,
+                        int64_t bm, int64_t bn, int round_scale, uint8_t* q, int64_t sqm,
+                        uint8_t* qt, int64_t sqtm, float* scales, int64_t ssm, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(x_dtype), "quant_blockwise: unsupported x dtype %d", x_dtype);
+  CIN_CHECK_ARG(M >= 0 && N >= 0, "quant_blockwise: negative shape");
+  CIN_CHECK_ARG(bm >= 1 && bn >= 1 && bm <= 1024 && bn <= 1024 && bm * bn <= 65536,
+                "quant_blockwise: block %lldx%lld unsupported", (long long)bm, (long long)bn);
+  if (M == 0 || N == 0) return CIN_OK;
+  CIN_CHECK_ARG(x && scales && (q || qt), "quant_blockwise: null pointer");
+  const int64_t nbm = cdiv(M, bm), nbn = cdiv(N, bn);
+  CIN_CHECK_ARG(!q || sqm >= N, "quant_blockwise: q row stride too small");
+  CIN_CHECK_ARG(!qt || sqtm >= M, "quant_blockwise: qt row stride too small");
+  CIN_CHECK_ARG(ssm >= nbn, "quant_blockwise: scale row stride too small");
+  CIN_CHECK_ARG(nbm < 65536 && nbn < ((int64_t)1 << 31), "quant_blockwise: grid too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int es = elem_size(x_dtype);
+  const bool fast = bm == 128 && bn == 128 && sxn == 1 && aligned(x, 16) &&
+                    ((sxm * es) % 16 == 0) && (!q || (aligned(q, 8) && sqm % 8 == 0)) &&
+                    (!qt || (aligned(qt, 16) && sqtm % 16 == 0));
+  dim3 grid((unsigned)nbn, (unsigned)nbm);
+  if (fast) {
+    if (x_dtype == CIN_DT_BF16)
+      hipLaunchKernelGGL(k_blockwise128<CIN_DT_BF16>, grid, kThreads, 0, s, x, M, N, sxm,
+                         round_scale, q, sqm, qt, sqtm, scales, ssm);
+    else if (x_dtype == CIN_DT_F16)
+      hipLaunchKernelGGL(k_blockwise128<CIN_DT_F16>, grid, kThreads, 0, s, x, M, N, sxm,
+                         round_scale, q, sqm, qt, sqtm, scales, ssm);
+    else
+      hipLaunchKernelGGL(k_blockwise128<CIN_DT_F32>, grid, kThreads, 0, s, x, M, N, sxm,
+                         round_scale, q, sqm, qt, sqtm, scales, ssm);
+  } else {
+    hipLaunchKernelGGL(k_blockwise_generic, grid, kThreads, 0, s, x, x_dtype, M, N, sxm, sxn, bm,
+                       bn, round_scale, q, sqm, qt, sqtm, scales, ssm, nbn);
+  }
+  return cin_check_launch("quant_blockwise");
+}
+
+int cin_dequant(const uint8_t* q, int64_t M, int64_t N, int64_t sqm, int64_t sqn,
+                const float* scales, int64_t ssm, int64_t ssn, int64_t bm, int64_t bn, void* out,
+                int out_dtype, int64_t som, void* stream) {
+  CIN_CHECK_ARG(out_dtype == CIN_DT_BF16 || out_dtype == CIN_DT_F32,
+                "dequant: output dtype must be bf16 or fp32");
+  CIN_CHECK_ARG(M >= 0 && N >= 0 && bm >= 1 && bn >= 1, "dequant: bad shape or block");
+  if (M == 0 || N == 0) return CIN_OK;
+  CIN_CHECK_ARG(q && scales && out, "dequant: null pointer");
+  CIN_CHECK_ARG(som >= N, "dequant: output row stride too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = grid_for(M * cdiv(N, 8), kThreads, 65536);
+  hipLaunchKernelGGL(k_dequant, grid, kThreads, 0, s, q, M, N, sqm, sqn, scales, ssm, ssn, bm, bn,
+                     out, out_dtype, som);
+  return cin_check_launch("dequant");
+}
+
+int cin_quant_dual(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t sdm, int64_t sdn,
+                   int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, uint8_t* qt,
+                   int64_t sqtm, float* st, int64_t sstm, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(dy_dtype), "quant_dual: unsupported dtype %d", dy_dtype);
+  CIN_CHECK_ARG(M >= 0 && N >= 0, "quant_dual: negative shape");
+  if (M == 0 || N == 0) return CIN_OK;
+  CIN_CHECK_ARG(dy && q && s && qt && st, "quant_dual: null pointer");
+  CIN_CHECK_ARG(sqm >= N && sqtm >= M && ssm >= cdiv(N, 128) && sstm >= cdiv(M, 128),
+                "quant_dual: output row stride too small");
+  hipStream_t stream_ = static_cast<hipStream_t>(stream);
+  const int es = elem_size(dy_dtype);
+  const bool fast = sdn == 1 && aligned(dy, 16) && ((sdm * es) % 16 == 0) && aligned(q, 8) &&
+                    sqm % 8 == 0 && aligned(qt, 16) && sqtm % 16 == 0 && cdiv(M, 128) < 65536;
+  if (fast) {
+    dim3 grid((unsigned)cdiv(N, 128), (unsigned)cdiv(M, 128));
+    if (dy_dtype == CIN_DT_BF16)
+      hipLaunchKernelGGL(k_dual128<CIN_DT_BF16>, grid, kThreads, 0, stream_, dy, M, N, sdm,
+                         round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm);
+    else if (dy_dtype == CIN_DT_F16)
+      hipLaunchKernelGGL(k_dual128<CIN_DT_F16>, grid, kThreads, 0, stream_, dy, M, N, sdm,
+                         round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm);
+    else
+      hipLaunchKernelGGL(k_dual128<CIN_DT_F32>, grid, kThreads, 0, stream_, dy, M, N, sdm,
+                         round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm);
+    return cin_check_launch("quant_dual");
+  }
+  // Strided input: two generic row-wise passes (dy, then dy^T through strides).
+  int rc = cin_quant_rowwise(dy, dy_dtype, M, N, sdm, sdn, 128, round_scale, q, sqm, s, ssm, stream);
+  if (rc != CIN_OK) return rc;
+  return cin_quant_rowwise(dy, dy_dtype, N, M, sdn, sdm, 128, round_scale, qt, sqtm, st, sstm,
+                           stream);
+}
+
+int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm,
+                             const float* srow, int64_t ssm, uint8_t* qb, int64_t sqbm,
+                             uint8_t* qbt, int64_t sqbtm, float* sblk, int64_t ssbm,
+                             void* stream) {
+  CIN_CHECK_ARG(M >= 0 && K >= 0, "requant: negative shape");
+  if (M == 0 || K == 0) return CIN_OK;
+  CIN_CHECK_ARG(q && srow && sblk && (qb || qbt), "requant: null pointer");
+  CIN_CHECK_ARG(aligned(q, 8) && sqm % 8 == 0, "requant: q must be 8-byte aligned rows");
+  CIN_CHECK_ARG(!qb || (aligned(qb, 8) && sqbm % 8 == 0 && sqbm >= K),
+                "requant: qb must be 8-byte aligned rows");
+  CIN_CHECK_ARG(!qbt || (aligned(qbt, 16) && sqbtm % 16 == 0 && sqbtm >= M),
+                "requant: qbt must be 16-byte aligned rows");
+  CIN_CHECK_ARG(ssm >= cdiv(K, 128) && ssbm >= cdiv(K, 128) && cdiv(M, 128) < 65536,
+                "requant: bad scale stride");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)cdiv(K, 128), (unsigned)cdiv(M, 128));
+  hipLaunchKernelGGL(k_requant128, grid, kThreads, 0, s, q, M, K, sqm, srow, ssm, qb, sqbm, qbt,
+                     sqbtm, sblk, ssbm);
+  return cin_check_launch("requant_row_to_block");
+}
+
+int cin_transpose_u8(const uint8_t* src, int64_t R, int64_t C, int64_t lds, uint8_t* dst,
+                     int64_t ldd, void* stream) {
+  CIN_CHECK_ARG(R >= 0 && C >= 0, "transpose_u8: negative shape");
+  if (R == 0 || C == 0) return CIN_OK;
+  CIN_CHECK_ARG(src && dst && lds >= C && ldd >= R, "transpose_u8: bad pointer or stride");
+  CIN_CHECK_ARG(cdiv(R, 64) < 65536, "transpose_u8: too many rows");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)cdiv(C, 64), (unsigned)cdiv(R, 64));
+  hipLaunchKernelGGL(k_transpose_u8, grid, kThreads, 0, s, src, R, C, lds, dst, ldd);
+  return cin_check_launch("transpose_u8");
+}
+
+}  // extern "C"

@@ -1,0 +1,365 @@
+"""Drop-in replacement of the reference's FP8 ``kernels`` module for MI355X.
+
+Same public names, signatures, defaults, output dtypes/shapes and argument
+checks as reference src/kernels.py; every operator launches hand-written HIP
+kernels (gfx950) through the C ABI in include/cinnamon_fp8.h.  There is no
+Triton, no CPU path and no fallback: device tensors are required exactly where
+the reference requires CUDA tensors, and a missing native library raises.
+
+Replaced reference items (src/kernels.py):
+  quantize_fp8_rowwise      :178-216  -> cin_quant_rowwise
+  quantize_fp8_blockwise    :219-259  -> cin_quant_blockwise
+  dequantize_fp8_rowwise    :262-281  -> cin_dequant (fp32 out)
+  dequantize_fp8            :284-314  -> cin_dequant (bf16 out)
+  fp8_matmul_dsv3           :667-702  -> cin_gemm_fp8_bs
+  FP8MatmulFunction         :731-794  -> quantizers + cin_quant_dual + cin_requant_row_to_block + GEMMs
+  FP8Linear                 :797-840
+  convert_to_fp8            :843-905
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import call, dtype_code, ptr, stream_of
+
+FP8_E4M3_MAX = 448.0
+
+__all__ = [
+    "FP8_E4M3_MAX",
+    "quantize_fp8_rowwise",
+    "quantize_fp8_blockwise",
+    "dequantize_fp8_rowwise",
+    "dequantize_fp8",
+    "fp8_matmul_dsv3",
+    "fp8_gemm_bs",
+    "quantize_fp8_dual",
+    "requantize_rowwise_to_blockwise",
+    "FP8MatmulFunction",
+    "FP8Linear",
+    "convert_to_fp8",
+]
+
+
+def _require(cond: bool, msg: str) -> None:
+    # The reference checks these conditions with `assert`; keep AssertionError.
+    if not cond:
+        raise AssertionError(msg)
+
+
+def _cdiv(a: int, b: int) -> int:
+    return (a + b - 1) // b
+
+
+def _codes_u8(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype == torch.float8_e4m3fn:
+        return t.view(torch.uint8)
+    _require(t.dtype == torch.uint8, f"expected float8_e4m3fn codes, got {t.dtype}")
+    return t
+
+
+# ---------------------------------------------------------------------------
+# Quantization (reference src/kernels.py:178-259)
+# ---------------------------------------------------------------------------
+def quantize_fp8_rowwise(x: torch.Tensor, block_size: int = 128,
+                         round_scale: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """1 x block_size e4m3 quantization -> (codes [M, N] float8_e4m3fn, scales [M, ceil(N/bs)] fp32)."""
+    _require(x.is_cuda, "Input must be on CUDA")
+    _require(x.ndim == 2, "Input must be 2D for now")
+    M, N = x.shape
+    nb = _cdiv(N, block_size)
+    x_fp8 = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=x.device)
+    scales = torch.empty((M, nb), dtype=torch.float32, device=x.device)
+    call("cin_quant_rowwise", ptr(x), dtype_code(x), M, N, x.stride(0), x.stride(1), block_size,
+         int(bool(round_scale)), ptr(x_fp8), x_fp8.stride(0), ptr(scales), scales.stride(0),
+         stream_of(x))
+    return x_fp8, scales
+
+
+def quantize_fp8_blockwise(x: torch.Tensor, block_m: int = 128, block_n: int = 128,
+                           round_scale: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """block_m x block_n e4m3 quantization -> (codes [M, N], scales [ceil(M/bm), ceil(N/bn)] fp32)."""
+    _require(x.is_cuda, "Input must be on CUDA")
+    _require(x.ndim == 2, "Input must be 2D")
+    M, N = x.shape
+    x_fp8 = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=x.device)
+    scales = torch.empty((_cdiv(M, block_m), _cdiv(N, block_n)), dtype=torch.float32, device=x.device)
+    call("cin_quant_blockwise", ptr(x), dtype_code(x), M, N, x.stride(0), x.stride(1), block_m,
+         block_n, int(bool(round_scale)), ptr(x_fp8), x_fp8.stride(0), ptr(None), 0, ptr(scales),
+         scales.stride(0), stream_of(x))
+    return x_fp8, scales
+
+
+def quantize_fp8_blockwise_t(x: torch.Tensor, round_scale: bool = False,
+                             with_rowmajor: bool = True):
+    """128x128 block quantization that also emits the transposed codes [N, M].
+
+    Returns (codes [M, N] or None, codes_t [N, M], scales [ceil(M/128), ceil(N/128)]).
+    The transposed codes are the K-contiguous B operand of the dgrad GEMM.
+    """
+    _require(x.is_cuda, "Input must be on CUDA")
+    _require(x.ndim == 2, "Input must be 2D")
+    M, N = x.shape
+    q = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=x.device) if with_rowmajor else None
+    qt = torch.empty((N, M), dtype=torch.float8_e4m3fn, device=x.device)
+    scales = torch.empty((_cdiv(M, 128), _cdiv(N, 128)), dtype=torch.float32, device=x.device)
+    call("cin_quant_blockwise", ptr(x), dtype_code(x), M, N, x.stride(0), x.stride(1), 128, 128,
+         int(bool(round_scale)), ptr(q), N, ptr(qt), qt.stride(0), ptr(scales), scales.stride(0),
+         stream_of(x))
+    return q, qt, scales
+
+
+def quantize_fp8_dual(dy: torch.Tensor, round_scale: bool = False):
+    """Row tiles of dy and of dy^T from one read (reference src/kernels.py:771, :781-783).
+
+    Returns (q [M, N], s [M, ceil(N/128)], qt [N, M], st [N, ceil(M/128)]), bit-identical to
+    quantize_fp8_rowwise(dy) and quantize_fp8_rowwise(dy.t().contiguous()).
+    """
+    _require(dy.is_cuda, "Input must be on CUDA")
+    _require(dy.ndim == 2, "Input must be 2D")
+    M, N = dy.shape
+    q = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=dy.device)
+    s = torch.empty((M, _cdiv(N, 128)), dtype=torch.float32, device=dy.device)
+    qt = torch.empty((N, M), dtype=torch.float8_e4m3fn, device=dy.device)
+    st = torch.empty((N, _cdiv(M, 128)), dtype=torch.float32, device=dy.device)
+    call("cin_quant_dual", ptr(dy), dtype_code(dy), M, N, dy.stride(0), dy.stride(1),
+         int(bool(round_scale)), ptr(q), q.stride(0), ptr(s), s.stride(0), ptr(qt), qt.stride(0),
+         ptr(st), st.stride(0), stream_of(dy))
+    return q, s, qt, st
+
+
+def requantize_rowwise_to_blockwise(x_fp8: torch.Tensor, x_scale: torch.Tensor,
+                                    transposed: bool = False):
+    """quantize_fp8_blockwise(dequantize_fp8_rowwise(x_fp8, x_scale), round_scale=False)
+    without the fp32 temporary (reference src/kernels.py:784-787).
+
+    Returns (codes, scales [ceil(M/128), ceil(K/128)]); codes are [M, K], or [K, M] when
+    ``transposed`` (the K-contiguous B operand of the wgrad GEMM).
+    """
+    _require(x_fp8.is_cuda, "Input must be on CUDA")
+    M, K = x_fp8.shape
+    q = _codes_u8(x_fp8)
+    if q.stride(1) != 1 or q.stride(0) % 8 or q.data_ptr() % 8:
+        q = q.contiguous()
+    _require(x_scale.shape == (M, _cdiv(K, 128)), "row scales must be [M, ceil(K/128)]")
+    xs = x_scale if x_scale.stride(1) == 1 else x_scale.contiguous()
+    sblk = torch.empty((_cdiv(M, 128), _cdiv(K, 128)), dtype=torch.float32, device=x_fp8.device)
+    if transposed:
+        out = torch.empty((K, M), dtype=torch.float8_e4m3fn, device=x_fp8.device)
+        call("cin_requant_row_to_block", ptr(q), M, K, q.stride(0), ptr(xs), xs.stride(0),
+             ptr(None), 0, ptr(out), out.stride(0), ptr(sblk), sblk.stride(0), stream_of(q))
+    else:
+        out = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x_fp8.device)
+        call("cin_requant_row_to_block", ptr(q), M, K, q.stride(0), ptr(xs), xs.stride(0),
+             ptr(out), out.stride(0), ptr(None), 0, ptr(sblk), sblk.stride(0), stream_of(q))
+    return out, sblk
+
+
+# ---------------------------------------------------------------------------
+# Dequantization (reference src/kernels.py:262-314)
+# ---------------------------------------------------------------------------
+def dequantize_fp8_rowwise(x_fp8: torch.Tensor, scales: torch.Tensor,
+                           block_size: int = 128) -> torch.Tensor:
+    """fp32(code) * scale[row, col // block_size] -> fp32 [M, N]."""
+    _require(x_fp8.is_cuda, "Input must be on CUDA")
+    M, N = x_fp8.shape
+    q = _codes_u8(x_fp8)
+    out = torch.empty((M, N), dtype=torch.float32, device=x_fp8.device)
+    call("cin_dequant", ptr(q), M, N, q.stride(0), q.stride(1), ptr(scales), scales.stride(0),
+         scales.stride(1), 1, block_size, ptr(out), _lib.CIN_DT_F32, out.stride(0), stream_of(q))
+    return out
+
+
+def dequantize_fp8(x_fp8: torch.Tensor, scales: torch.Tensor, block_m: int = 128,
+                   block_n: int = 128) -> torch.Tensor:
+    """bf16(fp32(code) * scale[block]) -> bf16 [M, N]; block_m = 1 reads row-wise scales."""
+    _require(x_fp8.is_cuda, "Input must be on CUDA")
+    M, N = x_fp8.shape
+    q = _codes_u8(x_fp8)
+    # the reference indexes scales.flatten() as [row_block * ceil(N/bn) + col_block]
+    flat = scales.reshape(-1)
+    if flat.stride(0) != 1:
+        flat = flat.contiguous()
+    nbn = _cdiv(N, block_n)
+    _require(flat.numel() >= _cdiv(M, block_m) * nbn, "scales too small for the block grid")
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=x_fp8.device)
+    call("cin_dequant", ptr(q), M, N, q.stride(0), q.stride(1), ptr(flat), nbn, 1, block_m,
+         block_n, ptr(out), _lib.CIN_DT_BF16, out.stride(0), stream_of(q))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Block-scaled FP8 GEMM (reference src/kernels.py:588-702)
+# ---------------------------------------------------------------------------
+def _kcontig(codes: torch.Tensor, K: int) -> tuple[torch.Tensor, int]:
+    """Return a [R, Kp] K-contiguous, 16-byte aligned uint8 view/copy and Kp (K padded to 16)."""
+    q = _codes_u8(codes)
+    Kp = _cdiv(K, 16) * 16
+    if Kp == K and q.stride(1) == 1 and q.stride(0) % 16 == 0 and q.data_ptr() % 16 == 0:
+        return q, K
+    out = torch.zeros((q.shape[0], Kp), dtype=torch.uint8, device=q.device)
+    out[:, :K].copy_(q)
+    return out, Kp
+
+
+def fp8_gemm_bs(a: torch.Tensor, a_scales: torch.Tensor, b_t: torch.Tensor,
+                b_scales_nk: torch.Tensor, out_dtype: torch.dtype = torch.bfloat16,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """C[M, N] = block-scaled a[M, K] x b_t[N, K]^T.
+
+    a_scales indexed [m, kb] (1 x 128 tiles of a); b_scales_nk indexed [n // 128, kb]
+    (128 x 128 blocks of b_t).  out_dtype bf16 (RNE of the fp32 epilogue) or fp32.
+    """
+    _require(a.is_cuda and b_t.is_cuda, "Input must be on CUDA")
+    M, K = a.shape
+    N, K2 = b_t.shape
+    _require(K == K2, f"Dimension mismatch: {K} vs {K2}")
+    aq, Kp = _kcontig(a, K)
+    bq, _ = _kcontig(b_t, K)
+    _require(a_scales.shape[0] >= M and a_scales.shape[1] >= _cdiv(K, 128), "a_scales too small")
+    _require(b_scales_nk.shape[0] >= _cdiv(N, 128) and b_scales_nk.shape[1] >= _cdiv(K, 128),
+             "b_scales too small")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    _require(out.dtype in (torch.bfloat16, torch.float32) and out.stride(1) == 1,
+             "out must be bf16/fp32 with unit column stride")
+    call("cin_gemm_fp8_bs", ptr(aq), aq.stride(0), ptr(a_scales), a_scales.stride(0),
+         a_scales.stride(1), ptr(bq), bq.stride(0), ptr(b_scales_nk), b_scales_nk.stride(0),
+         b_scales_nk.stride(1), M, N, Kp, ptr(out), dtype_code(out), out.stride(0), stream_of(aq))
+    return out
+
+
+def fp8_matmul_dsv3(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor,
+                    b_scales: torch.Tensor) -> torch.Tensor:
+    """C = A @ B with A [M, K] row-wise 1x128 scaled, B [K, N] 128x128 block scaled -> bf16."""
+    M, K = a.shape
+    K2, N = b.shape
+    _require(K == K2, f"Dimension mismatch: {K} vs {K2}")
+    _require(a.is_cuda and b.is_cuda, "Input must be on CUDA")
+    # the GEMM wants B^T [N, K] K-contiguous: a transposed view of such a tensor is free,
+    # otherwise transpose the codes on the device
+    bq = _codes_u8(b)
+    if bq.stride(0) == 1 and bq.stride(1) % 16 == 0 and bq.data_ptr() % 16 == 0 and K % 16 == 0:
+        b_t = bq.t()
+    else:
+        src = bq if bq.stride(1) == 1 else bq.contiguous()
+        b_t = torch.empty((N, K), dtype=torch.uint8, device=b.device)
+        call("cin_transpose_u8", ptr(src), K, N, src.stride(0), ptr(b_t), b_t.stride(0),
+             stream_of(src))
+    # b_scales is [kb, nb]; the GEMM reads it as [nb, kb] through swapped strides
+    return fp8_gemm_bs(a, a_scales, b_t, b_scales.t(), torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# Autograd function / module / conversion (reference src/kernels.py:731-905)
+# ---------------------------------------------------------------------------
+class FP8MatmulFunction(torch.autograd.Function):
+    """DeepSeek-V3 style FP8 matmul: y = x @ weight^T with 1x128 activation tiles and
+    128x128 weight blocks (reference src/kernels.py:731-794).
+
+    Forward quantizes x row-wise and the weight block-wise (emitting the transposed
+    weight codes for dgrad) and runs one GEMM.  Backward quantizes dY once into row
+    tiles and dY^T row tiles (cin_quant_dual), re-quantizes the saved x codes into
+    transposed 128x128 blocks (cin_requant_row_to_block) and runs the dgrad and wgrad
+    GEMMs, with the same operands and rounding steps as the reference.
+    """
+
+    @staticmethod
+    def forward(ctx, x, weight, round_scale):
+        x_shape = x.shape
+        x_flat = x.reshape(-1, x_shape[-1])
+        M, K = x_flat.shape
+        N = weight.shape[0]
+        x_fp8, x_scale = quantize_fp8_rowwise(x_flat, block_size=128, round_scale=round_scale)
+        w = weight if weight.dtype == torch.float32 else weight.float()
+        w_fp8, w_fp8_t, w_scale = quantize_fp8_blockwise_t(w, round_scale=False)
+        out = fp8_gemm_bs(x_fp8, x_scale, w_fp8, w_scale, torch.bfloat16)
+        ctx.save_for_backward(x_fp8, x_scale, w_fp8_t, w_scale)
+        ctx.x_shape = x_shape
+        ctx.round_scale = round_scale
+        return out.reshape(*x_shape[:-1], N)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x_fp8, x_scale, w_fp8_t, w_scale = ctx.saved_tensors
+        x_shape = ctx.x_shape
+        grad_flat = grad_output.reshape(-1, grad_output.shape[-1])
+        g_fp8, g_scale, g_fp8_t, g_scale_t = quantize_fp8_dual(grad_flat, ctx.round_scale)
+        # dgrad: dX[M, K] = dY[M, N] . W[N, K]; B^T = W^T [K, N], block scales read as [kb, nb]
+        grad_x = fp8_gemm_bs(g_fp8, g_scale, w_fp8_t, w_scale.t(), torch.bfloat16)
+        # wgrad: dW[N, K] = dY^T[N, M] . X[M, K]; B^T = X^T block codes [K, M]
+        x_blk_t, x_sblk = requantize_rowwise_to_blockwise(x_fp8, x_scale, transposed=True)
+        grad_w = fp8_gemm_bs(g_fp8_t, g_scale_t, x_blk_t, x_sblk.t(), torch.bfloat16)
+        return grad_x.reshape(x_shape), grad_w, None
+
+
+class FP8Linear(torch.nn.Module):
+    """Linear layer with DeepSeek-V3 FP8 quantization (reference src/kernels.py:797-840).
+
+    Keeps an fp32 master ``weight`` [out, in] (init N(0, 0.02)) and an optional bias
+    added after the FP8 matmul.  On non-GPU tensors the reference runs F.linear, and so
+    does this module.
+    """
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False,
+                 round_scale: bool = False):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.round_scale = round_scale
+        self.weight = torch.nn.Parameter(torch.empty(out_features, in_features))
+        torch.nn.init.normal_(self.weight, mean=0.0, std=0.02)
+        if bias:
+            self.bias = torch.nn.Parameter(torch.zeros(out_features))
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.is_cuda:
+            out = FP8MatmulFunction.apply(x, self.weight, self.round_scale)
+        else:
+            out = torch.nn.functional.linear(x, self.weight, None)
+        if self.bias is not None:
+            out = out + self.bias
+        return out
+
+    @classmethod
+    def from_linear(cls, linear: torch.nn.Linear, round_scale: bool = False) -> "FP8Linear":
+        fp8_linear = cls(linear.in_features, linear.out_features, bias=linear.bias is not None,
+                         round_scale=round_scale)
+        fp8_linear.weight = torch.nn.Parameter(linear.weight.data.clone())
+        if linear.bias is not None:
+            fp8_linear.bias = torch.nn.Parameter(linear.bias.data.clone())
+        return fp8_linear
+
+
+_DEFAULT_EXCLUDE = ["embedding", "lm_head", "router", "norm", "attn", "indexer"]
+_ROUND_SCALE_NAMES = ["w_out", "w1", "w2"]
+
+
+def convert_to_fp8(model: torch.nn.Module, exclude_names: list | None = None) -> torch.nn.Module:
+    """Swap eligible nn.Linear modules for FP8Linear (reference src/kernels.py:843-905).
+
+    Skips names containing embedding/lm_head/router/norm/attn/indexer (plus
+    ``exclude_names``) and layers with a dimension under 128; names containing
+    w_out/w1/w2 get power-of-two activation and gradient scales.
+    """
+    exclude = (exclude_names or []) + _DEFAULT_EXCLUDE
+    for name, module in list(model.named_modules()):
+        if not isinstance(module, torch.nn.Linear):
+            continue
+        if any(ex in name for ex in exclude):
+            continue
+        if module.in_features < 128 or module.out_features < 128:
+            print(f"[FP8] Auto-excluding {name}: shape ({module.out_features}, "
+                  f"{module.in_features}) < 128")
+            continue
+        parts = name.rsplit(".", 1)
+        if len(parts) == 2:
+            parent = model.get_submodule(parts[0])
+            attr = parts[1]
+        else:
+            parent, attr = model, name
+        round_scale = any(key in name for key in _ROUND_SCALE_NAMES)
+        setattr(parent, attr, FP8Linear.from_linear(module, round_scale=round_scale))
+    return model

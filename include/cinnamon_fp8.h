@@ -1,0 +1,161 @@
+/*
+ * cinnamon_fp8.h — C ABI of the MI355X (gfx950) FP8 hot path.
+ *
+ * Every entry point below replaces one operator of the reference's FP8 path
+ * (shyampathak22/cinnamon, src/kernels.py) and is cited at its declaration.
+ * The reference binds its kernels from Python; the binding a maintainer adds
+ * is a ctypes stub (see cinnamon_amd/_lib.py), so these signatures use only
+ * plain pointers, 64-bit sizes/strides and small integer enums.
+ *
+ * Conventions shared by all entry points:
+ *   - Pointers are device pointers on the caller's current HIP device.
+ *   - Strides are in ELEMENTS, row-major unless a stride argument says
+ *     otherwise.  FP8 codes are OCP e4m3fn bytes (torch.float8_e4m3fn).
+ *   - Outputs are caller-allocated; the library allocates nothing.
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream).
+ *     Calls are asynchronous and never synchronize the device.
+ *   - Return value: CIN_OK (0) or a negative error code; cin_last_error()
+ *     returns a message for the calling thread's last failure.
+ */
+#ifndef CINNAMON_FP8_H
+#define CINNAMON_FP8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of a floating-point tensor argument. */
+enum cin_dtype { CIN_DT_BF16 = 0, CIN_DT_F32 = 1, CIN_DT_F16 = 2 };
+
+/* Return codes. */
+enum cin_status {
+  CIN_OK = 0,
+  CIN_ERR_ARG = -1,          /* invalid shape/stride/pointer/enum argument   */
+  CIN_ERR_UNSUPPORTED = -2,  /* valid but unsupported combination            */
+  CIN_ERR_HIP = -3           /* the HIP runtime reported an error            */
+};
+
+/* Library ABI version (bumped on any signature change). */
+int cin_abi_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* cin_last_error(void);
+
+/*
+ * Row-wise (1 x block) quantization.
+ * Replaces quantize_fp8_rowwise / quantize_fp8_rowwise_kernel
+ * (reference src/kernels.py:178-216 and :19-71).
+ *   x      [M, N] of dtype x_dtype, strides (sxm, sxn)
+ *   q      [M, N] e4m3 codes, row stride sqm, column stride 1
+ *   scales [M, ceil(N/block)] fp32, row stride ssm, column stride 1
+ * block in [1, 1024]; round_scale != 0 selects power-of-two scales.
+ */
+int cin_quant_rowwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t sxm, int64_t sxn,
+                      int64_t block, int round_scale, uint8_t* q, int64_t sqm, float* scales,
+                      int64_t ssm, void* stream);
+
+/*
+ * Block-wise (bm x bn) quantization.
+ * Replaces quantize_fp8_blockwise / quantize_fp8_blockwise_kernel
+ * (reference src/kernels.py:219-259 and :74-132).
+ *   x      [M, N] of dtype x_dtype, strides (sxm, sxn)
+ *   q      [M, N] codes, row stride sqm (may be NULL if qt is given)
+ *   qt     optional [N, M] codes of the transpose (row stride sqtm), or NULL;
+ *          the same codes as q, laid out K-contiguous for the dgrad GEMM
+ *   scales [ceil(M/bm), ceil(N/bn)] fp32, row stride ssm
+ * bm, bn in [1, 1024] with bm * bn <= 65536.
+ */
+int cin_quant_blockwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t sxm, int64_t sxn,
+                        int64_t bm, int64_t bn, int round_scale, uint8_t* q, int64_t sqm,
+                        uint8_t* qt, int64_t sqtm, float* scales, int64_t ssm, void* stream);
+
+/*
+ * Dequantization with (bm x bn) block scales; bm = 1 gives row-wise scales.
+ * Replaces dequantize_fp8 / dequantize_fp8_kernel (reference src/kernels.py:284-314,
+ * :135-173; bf16 output) and dequantize_fp8_rowwise (:262-281; fp32 output).
+ *   q      [M, N] codes, strides (sqm, sqn)
+ *   scales indexed [m / bm, n / bn] with strides (ssm, ssn)
+ *   out    [M, N] of dtype out_dtype (CIN_DT_BF16 or CIN_DT_F32), row stride som
+ */
+int cin_dequant(const uint8_t* q, int64_t M, int64_t N, int64_t sqm, int64_t sqn,
+                const float* scales, int64_t ssm, int64_t ssn, int64_t bm, int64_t bn,
+                void* out, int out_dtype, int64_t som, void* stream);
+
+/*
+ * Dual 1x128 quantization of a gradient in one read: row tiles of dy and row
+ * tiles of dy^T (= 128 x 1 column tiles of dy).
+ * Replaces the pair quantize_fp8_rowwise(grad_flat) and
+ * quantize_fp8_rowwise(grad_flat.t().contiguous()) in FP8MatmulFunction.backward
+ * (reference src/kernels.py:771 and :781-783).
+ *   dy [M, N] of dtype dy_dtype, strides (sdm, sdn)
+ *   q  [M, N] codes (row stride sqm) and s  [M, ceil(N/128)] (row stride ssm)
+ *   qt [N, M] codes (row stride sqtm) and st [N, ceil(M/128)] (row stride sstm)
+ */
+int cin_quant_dual(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t sdm, int64_t sdn,
+                   int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm,
+                   uint8_t* qt, int64_t sqtm, float* st, int64_t sstm, void* stream);
+
+/*
+ * Re-quantize 1x128 row-quantized codes into 128x128 blocks, bit-identical to
+ * quantize_fp8_blockwise(dequantize_fp8_rowwise(q, s), round_scale=False)
+ * (reference src/kernels.py:784-787), without the fp32 temporary.
+ *   q    [M, K] codes (row stride sqm), srow [M, ceil(K/128)] (row stride ssm)
+ *   qb   optional [M, K] block codes (row stride sqbm) or NULL
+ *   qbt  optional [K, M] block codes of the transpose (row stride sqbtm) or NULL
+ *   sblk [ceil(M/128), ceil(K/128)] block scales (row stride ssbm)
+ */
+int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm,
+                             const float* srow, int64_t ssm, uint8_t* qb, int64_t sqbm,
+                             uint8_t* qbt, int64_t sqbtm, float* sblk, int64_t ssbm, void* stream);
+
+/*
+ * Byte transpose: dst[c, r] = src[r, c] for an [R, C] matrix of codes.
+ * Replaces the code-layout copies w_fp8.t().contiguous() (reference src/kernels.py:748).
+ */
+int cin_transpose_u8(const uint8_t* src, int64_t R, int64_t C, int64_t lds, uint8_t* dst,
+                     int64_t ldd, void* stream);
+
+/*
+ * Block-scaled FP8 GEMM, both operands K-contiguous:
+ *   C[m, n] = sum_kb  sa[m, kb] * sb[n / 128, kb] * sum_{k in kb} A[m, k] * B[n, k]
+ * which is fp8_gemm_kernel / fp8_matmul_dsv3 (reference src/kernels.py:588-702)
+ * with its B operand given as B^T.  fp32 accumulation, fp32 epilogue.
+ *   A  [M, K] codes, row stride lda;  sa indexed [m, kb] with strides (ssam, ssak)
+ *   B  [N, K] codes, row stride ldb;  sb indexed [nb, kb] with strides (ssbn, ssbk)
+ *   C  [M, N] of c_dtype (CIN_DT_BF16: round-to-nearest-even of the fp32 value;
+ *      CIN_DT_F32: the fp32 value), row stride ldc
+ * Requires K % 16 == 0, lda % 16 == 0, ldb % 16 == 0 and 16-byte aligned A, B.
+ */
+int cin_gemm_fp8_bs(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam, int64_t ssak,
+                    const uint8_t* B, int64_t ldb, const float* sb, int64_t ssbn, int64_t ssbk,
+                    int64_t M, int64_t N, int64_t K, void* C, int c_dtype, int64_t ldc,
+                    void* stream);
+
+/*
+ * Grouped (MoE) block-scaled FP8 GEMM over routed experts in ONE launch with a
+ * device-side expert tile table (no host sync, no host loop):
+ *   for each expert e with rows [starts[e], ends[e]):
+ *     C[r, n] = sum_kb sa[r, kb] * sb_e[n / 128, kb] * sum_k A[r, k] * B_e[n, k]
+ * FP8 counterpart of moe_grouped_gemm / grouped_gemm_kernel (reference
+ * src/kernels.py:526-581, :440-523), with the reference's per-expert loop
+ * semantics of GroupedExperts (src/layers.py:79-86).
+ *   A  [T, K] codes (row stride lda), sa [T, ceil(K/128)] (strides ssam, ssak)
+ *   B  expert e at B + e * sbe: [N, K] codes, row stride ldb
+ *   sb expert e at sb + e * ssbe, indexed [nb, kb] with strides (ssbn, ssbk)
+ *   starts, ends  int64 device arrays of length E (rows outside every
+ *                 [starts[e], ends[e]) are not written)
+ *   C  [T, N] of c_dtype, row stride ldc
+ */
+int cin_grouped_gemm_fp8(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam,
+                         int64_t ssak, const uint8_t* B, int64_t sbe, int64_t ldb, const float* sb,
+                         int64_t ssbe, int64_t ssbn, int64_t ssbk, const int64_t* starts,
+                         const int64_t* ends, int64_t E, int64_t T, int64_t N, int64_t K, void* C,
+                         int c_dtype, int64_t ldc, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CINNAMON_FP8_H */

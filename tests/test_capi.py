@@ -1,0 +1,67 @@
+"""CPU checks of the C ABI: the library loads, exports every declared entry point, and
+rejects invalid arguments before touching the GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from cinnamon_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cinnamon_fp8.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(cin_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for name in ["cin_quant_rowwise", "cin_quant_blockwise", "cin_dequant", "cin_quant_dual",
+                 "cin_requant_row_to_block", "cin_gemm_fp8_bs", "cin_grouped_gemm_fp8",
+                 "cin_last_error", "cin_abi_version"]:
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+    # and the ctypes binding covers every compute entry point
+    assert set(declared_symbols()) - {"cin_last_error"} == set(_lib.SIGNATURES)
+
+
+def test_abi_version():
+    assert _lib.load().cin_abi_version() == 1
+
+
+def test_no_rpath_to_a_second_hip_runtime():
+    # the library must bind to the HIP runtime torch already mapped (by soname)
+    out = os.popen(f"readelf -d {_lib.library_path()}").read()
+    assert "libamdhip64.so.7" in out
+
+
+@pytest.mark.parametrize("call", [
+    ("cin_quant_rowwise", (None, 7, 4, 128, 128, 1, 128, 0, None, 128, None, 1, None)),   # bad dtype
+    ("cin_quant_rowwise", (None, 0, 4, 128, 128, 1, 0, 0, None, 128, None, 1, None)),     # block 0
+    ("cin_quant_rowwise", (None, 0, 4, 128, 128, 1, 128, 0, None, 128, None, 1, None)),   # null ptr
+    ("cin_quant_blockwise", (None, 0, 4, 4, 4, 1, 2048, 2048, 0, None, 4, None, 0, None, 1, None)),
+    ("cin_gemm_fp8_bs", (None, 32, None, 1, 1, None, 32, None, 1, 1, 4, 4, 24, None, 0, 4, None)),
+    ("cin_gemm_fp8_bs", (None, 32, None, 1, 1, None, 32, None, 1, 1, 4, 4, 32, None, 5, 4, None)),
+    ("cin_dequant", (None, 4, 4, 4, 1, None, 1, 1, 1, 128, None, 2, 4, None)),            # fp16 out
+])
+def test_invalid_arguments_rejected_without_gpu(call):
+    name, args = call
+    fn = getattr(_lib.load(), name)
+    rc = fn(*[ctypes.c_void_p(0) if a is None else a for a in args])
+    assert rc == _lib.CIN_ERR_ARG
+    assert _lib.last_error()
+
+
+def test_empty_shapes_are_noops():
+    lib = _lib.load()
+    # M == 0: nothing to do, no device touched
+    assert lib.cin_quant_rowwise(None, 0, 0, 128, 128, 1, 128, 0, None, 128, None, 1, None) == 0
+    assert lib.cin_gemm_fp8_bs(None, 32, None, 1, 1, None, 32, None, 1, 1, 0, 4, 32, None, 0, 4, None) == 0

@@ -1,0 +1,184 @@
+"""GPU parity of the block-scaled FP8 GEMMs (dense, dgrad/wgrad, grouped) against the
+oracle's dequantize-then-fp32-matmul.
+
+Tolerance (stated for the fp32 epilogue, compared in float64):
+  normwise max relative  max|Y - Yref| / max|Yref|  <= 2e-3
+  Frobenius relative     ||Y - Yref|| / ||Yref||     <= 1e-3
+and the production bf16 output must equal the round-to-nearest-even of the fp32 output.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+MAX_REL = 2e-3
+FROB_REL = 1e-3
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "fp8_golden.npz")
+
+
+def _check(got, want, what):
+    mr = orc.normwise_max_rel(got.cpu(), want)
+    fr = orc.frob_rel(got.cpu(), want)
+    assert mr <= MAX_REL and fr <= FROB_REL, f"{what}: normwise max rel {mr:.3e}, frob rel {fr:.3e}"
+    return mr, fr
+
+
+def _operands(M, N, K, seed, outliers=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    if outliers:
+        x[torch.rand(M, K, generator=g) < 0.01] *= 20
+    x = x.to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    xq, xs = orc.quant_rowwise(x)
+    wq, ws = orc.quant_blockwise(w)
+    return xq, xs, wq, ws
+
+
+def _run_fp32_and_bf16(kern, dev, xq, xs, wq, ws):
+    a, sa, b, sb = xq.to(dev), xs.to(dev), wq.to(dev), ws.to(dev)
+    y32 = kern.fp8_gemm_bs(a, sa, b, sb, torch.float32)
+    y16 = kern.fp8_gemm_bs(a, sa, b, sb, torch.bfloat16)
+    torch.cuda.synchronize()
+    return y32, y16
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (2048, 1024, 512),    # config 1
+    (8192, 2048, 7168),   # config 2 (DeepSeek-V3 projection)
+    (70, 200, 384),       # M/N tails
+    (129, 257, 144),      # K not a multiple of 128
+    (1, 128, 128),
+    (16368, 1024, 1024),  # config 5 MTP rows
+])
+def test_gemm_parity(kern, dev, M, N, K):
+    xq, xs, wq, ws = _operands(M, N, K, seed=M + N + K)
+    y32, y16 = _run_fp32_and_bf16(kern, dev, xq, xs, wq, ws)
+    want = orc.gemm_ref(xq, xs, wq.view(torch.uint8).t().contiguous(), ws.t().contiguous())
+    _check(y32, want, f"gemm {M}x{N}x{K}")
+    assert y16.dtype == torch.bfloat16
+    assert torch.equal(y16.cpu(), y32.cpu().to(torch.bfloat16)), "bf16 output is not RNE(fp32 output)"
+
+
+def test_gemm_against_golden(kern, dev):
+    d = np.load(GOLDEN)
+    a = torch.from_numpy(d["xc_row_q"]).to(dev)
+    sa = torch.from_numpy(d["xc_row_s"]).to(dev)
+    b = torch.from_numpy(d["w_blk_q"]).to(dev)
+    sb = torch.from_numpy(d["w_blk_s"]).to(dev)
+    y = kern.fp8_gemm_bs(a, sa, b, sb, torch.float32)
+    _check(y, torch.from_numpy(d["y_f32"]), "golden gemm")
+
+
+def test_fp8_matmul_dsv3_api(kern, dev):
+    """The reference signature: b is [K, N] (contiguous or a transposed view)."""
+    xq, xs, wq, ws = _operands(512, 384, 640, seed=3)
+    b_kn = wq.view(torch.uint8).t().contiguous()
+    sb_kn = ws.t().contiguous()
+    want = orc.gemm_ref(xq, xs, b_kn, sb_kn)
+    for b in (b_kn.to(dev), wq.to(dev).view(torch.uint8).t()):
+        y = kern.fp8_matmul_dsv3(xq.to(dev), b.view(torch.float8_e4m3fn), xs.to(dev), sb_kn.to(dev))
+        assert y.dtype == torch.bfloat16 and y.shape == (512, 384)
+        _check(y.float(), want, "fp8_matmul_dsv3")
+
+
+def test_gemm_deterministic(kern, dev):
+    xq, xs, wq, ws = _operands(1024, 1024, 2048, seed=12)
+    a, sa, b, sb = xq.to(dev), xs.to(dev), wq.to(dev), ws.to(dev)
+    y1 = kern.fp8_gemm_bs(a, sa, b, sb, torch.float32)
+    y2 = kern.fp8_gemm_bs(a, sa, b, sb, torch.float32)
+    assert torch.equal(y1, y2)
+
+
+# ---------------------------------------------------------------------------
+# FP8MatmulFunction forward + backward at config-4 shapes
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K,rs", [(8192, 2048, 7168, False), (300, 256, 384, True), (16368, 384, 256, False)])
+def test_fp8_linear_fwd_bwd(kern, dev, M, N, K, rs):
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(M, K, generator=g)
+    x[torch.rand(M, K, generator=g) < 0.01] *= 20
+    x = x.to(torch.bfloat16)
+    w = torch.randn(N, K, generator=g) * 0.02          # fp32 master weight
+    dy = (torch.randn(M, N, generator=g) * 1e-3).to(torch.bfloat16)
+    ref = orc.fp8_linear_ref(x, w, dy, round_scale=rs)
+
+    xd = x.to(dev).requires_grad_(True)
+    wd = w.to(dev).requires_grad_(True)
+    y = kern.FP8MatmulFunction.apply(xd, wd, rs)
+    y.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    assert y.dtype == torch.bfloat16 and xd.grad.dtype == torch.bfloat16 and wd.grad.dtype == torch.float32
+    # outputs are bf16 roundings of fp32 values: compare against the fp32 oracle with the
+    # bf16 rounding allowance (2^-8 relative per element) added to the GEMM tolerance
+    for name, got in (("y", y), ("dx", xd.grad), ("dw", wd.grad)):
+        mr = orc.normwise_max_rel(got.float().cpu(), ref[name])
+        fr = orc.frob_rel(got.float().cpu(), ref[name])
+        assert mr <= MAX_REL + 2 ** -8 and fr <= FROB_REL + 2 ** -8, f"{name}: {mr:.3e} {fr:.3e}"
+
+
+def test_fp8_linear_backward_operands_bit_exact(kern, dev):
+    """The quantized operands the backward GEMMs consume are bit-exact to the reference chain."""
+    M, N, K = 1024, 512, 768
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = torch.randn(N, K, generator=g) * 0.02
+    dy = (torch.randn(M, N, generator=g) * 1e-3).to(torch.bfloat16)
+    ref = orc.fp8_linear_ref(x, w, dy)
+    xq, xs = kern.quantize_fp8_rowwise(x.to(dev))
+    q, s, qt, st = kern.quantize_fp8_dual(dy.to(dev))
+    xbt, xbs = kern.requantize_rowwise_to_blockwise(xq, xs, transposed=True)
+    assert torch.equal(q.view(torch.uint8).cpu(), ref["g_fp8"].view(torch.uint8))
+    assert torch.equal(qt.view(torch.uint8).cpu(), ref["g_fp8_t"].view(torch.uint8))
+    assert torch.equal(st.cpu(), ref["g_scale_t"]) and torch.equal(s.cpu(), ref["g_scale"])
+    assert torch.equal(xbt.view(torch.uint8).cpu(), ref["xb_fp8"].view(torch.uint8).t())
+    assert torch.equal(xbs.cpu(), ref["xb_scale"])
+
+
+# ---------------------------------------------------------------------------
+# grouped GEMM (one launch over all experts, device-side tile table)
+# ---------------------------------------------------------------------------
+def _grouped_case(counts, N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    T = int(sum(counts))
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16)
+    E = len(counts)
+    w = (torch.randn(E, N, K, generator=g) * 0.02)
+    xq, xs = orc.quant_rowwise(x)
+    wq, ws = orc.quant_blockwise(w.reshape(E * N, K))
+    wq = wq.view(torch.uint8).view(E, N, K)
+    ws = ws.view(E, -(-N // 128), -(-K // 128))
+    ends = torch.tensor(np.cumsum(counts), dtype=torch.int64)
+    starts = ends - torch.tensor(counts, dtype=torch.int64)
+    return xq, xs, wq, ws, starts, ends
+
+
+@pytest.mark.parametrize("counts,N,K", [
+    ([300, 0, 128, 1, 555, 64, 0, 1000], 384, 512),
+    ([128] * 8, 256, 256),
+    ([4000], 512, 1024),
+])
+def test_grouped_gemm_parity(kern, dev, counts, N, K):
+    from cinnamon_amd import layers
+    xq, xs, wq, ws, starts, ends = _grouped_case(counts, N, K, seed=len(counts))
+    want = orc.grouped_gemm_ref(xq, xs, wq, ws, starts, ends)
+    out = layers.fp8_grouped_gemm(xq.to(dev), xs.to(dev), wq.to(dev), ws.to(dev), starts.to(dev),
+                                  ends.to(dev), out_dtype=torch.float32)
+    _check(out, want, f"grouped {counts}")
+    out16 = layers.fp8_grouped_gemm(xq.to(dev), xs.to(dev), wq.to(dev), ws.to(dev), starts.to(dev),
+                                    ends.to(dev), out_dtype=torch.bfloat16)
+    assert torch.equal(out16.cpu(), out.cpu().to(torch.bfloat16))
+
+
+def test_grouped_equals_dense_for_one_expert(kern, dev):
+    from cinnamon_amd import layers
+    xq, xs, wq, ws, starts, ends = _grouped_case([1000], 256, 384, seed=21)
+    a = layers.fp8_grouped_gemm(xq.to(dev), xs.to(dev), wq.to(dev), ws.to(dev), starts.to(dev),
+                                ends.to(dev), out_dtype=torch.float32)
+    b = kern.fp8_gemm_bs(xq.to(dev), xs.to(dev), wq[0].to(dev), ws[0].to(dev), torch.float32)
+    assert torch.equal(a, b)

@@ -1,0 +1,241 @@
+"""GPU parity of the HIP quantizers against the CPU oracle: codes and scales bit-exact.
+
+Inputs are generated on the CPU with seeded generators and copied to the GPU, so both
+sides see identical bits.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "fp8_golden.npz")
+
+
+def _u8(t):
+    return t.view(torch.uint8).cpu()
+
+
+def _assert_codes_equal(got, want, what):
+    got, want = _u8(got), want.view(torch.uint8)
+    if not torch.equal(got, want):
+        bad = (got != want).nonzero()
+        i = tuple(bad[0].tolist())
+        raise AssertionError(f"{what}: {bad.shape[0]} code mismatches, first at {i}: "
+                             f"got {got[i]:#x} want {want[i]:#x}")
+
+
+def _assert_scales_equal(got, want, what):
+    got = got.cpu()
+    eq = (got == want) | (torch.isnan(got) & torch.isnan(want))
+    if not eq.all():
+        bad = (~eq).nonzero()
+        i = tuple(bad[0].tolist())
+        raise AssertionError(f"{what}: {bad.shape[0]} scale mismatches, first at {i}: "
+                             f"got {got[i].item()!r} want {want[i].item()!r}")
+
+
+def _activations(M, N, seed, dtype=torch.bfloat16, outliers=True, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, N, generator=g) * std
+    if outliers:
+        x[torch.rand(M, N, generator=g) < 0.01] *= 20
+    return x.to(dtype)
+
+
+# ---------------------------------------------------------------------------
+# row-wise 1 x 128
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape,dtype,rs", [
+    ((2048, 512), torch.bfloat16, False),     # config 1 activations
+    ((8192, 7168), torch.bfloat16, False),    # config 2 activations (1% outliers x20)
+    ((16368, 1024), torch.float32, True),     # config 5 MTP rows, fp32 RMSNorm output, round_scale
+    ((70, 200), torch.bfloat16, False),       # tails in both dims
+    ((3, 1000), torch.float32, False),
+    ((1, 128), torch.float16, False),
+    ((257, 384), torch.bfloat16, True),
+])
+def test_rowwise_bit_exact(kern, dev, shape, dtype, rs):
+    x = _activations(*shape, seed=1, dtype=dtype)
+    q, s = kern.quantize_fp8_rowwise(x.to(dev), 128, rs)
+    rq, rs_ = orc.quant_rowwise(x, 128, rs)
+    assert q.dtype == torch.float8_e4m3fn and q.shape == shape
+    assert s.shape == (shape[0], -(-shape[1] // 128))
+    _assert_codes_equal(q, rq, f"codes {shape}")
+    _assert_scales_equal(s, rs_, f"scales {shape}")
+
+
+@pytest.mark.parametrize("block", [32, 64, 100, 256, 1024])
+def test_rowwise_other_block_sizes(kern, dev, block):
+    x = _activations(96, 1100, seed=2)
+    q, s = kern.quantize_fp8_rowwise(x.to(dev), block)
+    rq, rs_ = orc.quant_rowwise(x, block)
+    _assert_codes_equal(q, rq, f"codes block {block}")
+    _assert_scales_equal(s, rs_, f"scales block {block}")
+
+
+def test_rowwise_strided_input(kern, dev):
+    x = _activations(384, 256, seed=3)
+    xt = x.to(dev).t()  # non-contiguous [256, 384]
+    q, s = kern.quantize_fp8_rowwise(xt)
+    rq, rs_ = orc.quant_rowwise(x.t().contiguous())
+    _assert_codes_equal(q, rq, "strided codes")
+    _assert_scales_equal(s, rs_, "strided scales")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_rowwise_special_tiles(kern, dev, dtype):
+    x = torch.randn(8, 512, generator=torch.Generator().manual_seed(4))
+    x[0, :128] = 0.0                        # zero tile -> dtype-dependent floor
+    x[1, 128:256] *= 1e-6                   # tiny tile -> floor active
+    x[2, 5] = float("nan")                  # NaN ignored by amax, coded as -448
+    x[3, 300] = float("inf")                # inf tile: scale inf, finite -> +-0
+    x[4, 0] = -float("inf")
+    x[5, 400:512] = float("nan")
+    x[6, 7] = 3.0e38 if dtype == torch.float32 else 1e4
+    x = x.to(dtype)
+    q, s = kern.quantize_fp8_rowwise(x.to(dev))
+    rq, rs_ = orc.quant_rowwise(x)
+    _assert_codes_equal(q, rq, f"special codes {dtype}")
+    _assert_scales_equal(s, rs_, f"special scales {dtype}")
+
+
+def test_rowwise_against_golden(kern, dev):
+    d = np.load(GOLDEN)
+    x = torch.from_numpy(d["x_bf16"].view(np.int16)).view(torch.bfloat16)
+    for rs in (0, 1):
+        q, s = kern.quantize_fp8_rowwise(x.to(dev), 128, bool(rs))
+        _assert_codes_equal(q, torch.from_numpy(d[f"x_row_q_rs{rs}"]), f"golden codes rs{rs}")
+        _assert_scales_equal(s, torch.from_numpy(d[f"x_row_s_rs{rs}"]), f"golden scales rs{rs}")
+
+
+def test_rowwise_deterministic(kern, dev):
+    x = _activations(1024, 7168, seed=5).to(dev)
+    a = kern.quantize_fp8_rowwise(x)
+    b = kern.quantize_fp8_rowwise(x)
+    assert torch.equal(_u8(a[0]), _u8(b[0])) and torch.equal(a[1], b[1])
+
+
+# ---------------------------------------------------------------------------
+# block-wise 128 x 128
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape,dtype,std", [
+    ((1024, 512), torch.float32, 0.02),    # config 1 weights (fp32 master)
+    ((2048, 7168), torch.bfloat16, 0.02),  # config 2 weights
+    ((300, 200), torch.float32, 1.0),      # tails
+    ((128, 16), torch.bfloat16, 1.0),
+])
+def test_blockwise_bit_exact(kern, dev, shape, dtype, std):
+    w = _activations(*shape, seed=6, dtype=dtype, outliers=False, std=std)
+    q, s = kern.quantize_fp8_blockwise(w.to(dev))
+    rq, rs_ = orc.quant_blockwise(w)
+    _assert_codes_equal(q, rq, f"block codes {shape}")
+    _assert_scales_equal(s, rs_, f"block scales {shape}")
+    # the variant that also writes the transposed codes for dgrad
+    q2, qt, s2 = kern.quantize_fp8_blockwise_t(w.to(dev))
+    _assert_codes_equal(q2, rq, "block codes (dual layout)")
+    _assert_codes_equal(qt, rq.view(torch.uint8).t().contiguous(), "transposed block codes")
+    _assert_scales_equal(s2, rs_, "block scales (dual layout)")
+
+
+@pytest.mark.parametrize("bm,bn,rs", [(64, 64, False), (128, 1, False), (1, 128, True), (32, 256, True)])
+def test_blockwise_other_blocks(kern, dev, bm, bn, rs):
+    w = _activations(300, 520, seed=7, dtype=torch.float32)
+    q, s = kern.quantize_fp8_blockwise(w.to(dev), bm, bn, rs)
+    rq, rs_ = orc.quant_blockwise(w, bm, bn, rs)
+    _assert_codes_equal(q, rq, f"codes {bm}x{bn}")
+    _assert_scales_equal(s, rs_, f"scales {bm}x{bn}")
+
+
+def test_blockwise_against_golden(kern, dev):
+    d = np.load(GOLDEN)
+    w = torch.from_numpy(d["w_f32"])
+    q, s = kern.quantize_fp8_blockwise(w.to(dev))
+    _assert_codes_equal(q, torch.from_numpy(d["w_blk_q"]), "golden block codes")
+    _assert_scales_equal(s, torch.from_numpy(d["w_blk_s"]), "golden block scales")
+
+
+# ---------------------------------------------------------------------------
+# dual quantization of gradients (row tiles of dY and of dY^T) — config 4
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape,dtype,rs", [
+    ((8192, 2048), torch.bfloat16, False),   # config 4 dY ~ N(0, 1e-3)
+    ((8192, 2048), torch.bfloat16, True),
+    ((300, 200), torch.bfloat16, False),     # tails
+    ((256, 384), torch.float32, True),
+])
+def test_dual_bit_exact(kern, dev, shape, dtype, rs):
+    dy = _activations(*shape, seed=4, dtype=dtype, outliers=False, std=1e-3)
+    q, s, qt, st = kern.quantize_fp8_dual(dy.to(dev), rs)
+    rq, rs_ = orc.quant_rowwise(dy, 128, rs)
+    rqt, rst = orc.quant_rowwise(dy.t().contiguous(), 128, rs)
+    _assert_codes_equal(q, rq, "dual row codes")
+    _assert_scales_equal(s, rs_, "dual row scales")
+    _assert_codes_equal(qt, rqt, "dual transposed codes")
+    _assert_scales_equal(st, rst, "dual transposed scales")
+
+
+def test_dual_against_golden(kern, dev):
+    d = np.load(GOLDEN)
+    dy = torch.from_numpy(d["dy_bf16"].view(np.int16)).view(torch.bfloat16)
+    q, s, qt, st = kern.quantize_fp8_dual(dy.to(dev), True)
+    _assert_codes_equal(q, torch.from_numpy(d["dy_row_q"]), "golden dy codes")
+    _assert_scales_equal(s, torch.from_numpy(d["dy_row_s"]), "golden dy scales")
+    _assert_codes_equal(qt, torch.from_numpy(d["dyt_row_q"]), "golden dy^T codes")
+    _assert_scales_equal(st, torch.from_numpy(d["dyt_row_s"]), "golden dy^T scales")
+
+
+def test_dual_strided_input(kern, dev):
+    dy = _activations(256, 384, seed=8, std=1e-3, outliers=False)
+    g = dy.to(dev).t()  # [384, 256] non-contiguous
+    q, s, qt, st = kern.quantize_fp8_dual(g)
+    rq, rs_ = orc.quant_rowwise(dy.t().contiguous())
+    rqt, rst = orc.quant_rowwise(dy)
+    _assert_codes_equal(q, rq, "strided dual row codes")
+    _assert_codes_equal(qt, rqt, "strided dual transposed codes")
+    _assert_scales_equal(s, rs_, "strided dual row scales")
+    _assert_scales_equal(st, rst, "strided dual transposed scales")
+
+
+# ---------------------------------------------------------------------------
+# row -> block re-quantization (backward X operand) and dequantizers
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape", [(8192, 7168), (300, 200), (128, 128)])
+def test_requant_bit_exact(kern, dev, shape):
+    x = _activations(*shape, seed=2)
+    rq, rs_ = orc.quant_rowwise(x)
+    want_q, want_s = orc.quant_blockwise(orc.dequant_rowwise(rq, rs_), 128, 128, False)
+    qd, sd = rq.to(dev), rs_.to(dev)
+    qb, sb = kern.requantize_rowwise_to_blockwise(qd, sd, transposed=False)
+    _assert_codes_equal(qb, want_q, "requant codes")
+    _assert_scales_equal(sb, want_s, "requant scales")
+    qbt, sbt = kern.requantize_rowwise_to_blockwise(qd, sd, transposed=True)
+    _assert_codes_equal(qbt, want_q.view(torch.uint8).t().contiguous(), "requant transposed codes")
+    _assert_scales_equal(sbt, want_s, "requant transposed scales")
+
+
+def test_requant_against_golden(kern, dev):
+    d = np.load(GOLDEN)
+    q = torch.from_numpy(d["xc_row_q"]).to(dev)
+    s = torch.from_numpy(d["xc_row_s"]).to(dev)
+    qb, sb = kern.requantize_rowwise_to_blockwise(q, s)
+    _assert_codes_equal(qb, torch.from_numpy(d["xc_blk_q"]), "golden requant codes")
+    _assert_scales_equal(sb, torch.from_numpy(d["xc_blk_s"]), "golden requant scales")
+
+
+def test_dequantizers(kern, dev):
+    x = _activations(300, 520, seed=9)
+    rq, rs_ = orc.quant_rowwise(x)
+    got = kern.dequantize_fp8_rowwise(rq.to(dev), rs_.to(dev))
+    assert got.dtype == torch.float32
+    assert torch.equal(got.cpu(), orc.dequant_rowwise(rq, rs_))
+    got = kern.dequantize_fp8(rq.to(dev), rs_.to(dev), block_m=1, block_n=128)
+    assert got.dtype == torch.bfloat16
+    assert torch.equal(got.cpu(), orc.dequant_block_bf16(rq, rs_, 1, 128))
+    bq, bs = orc.quant_blockwise(x.float())
+    got = kern.dequantize_fp8(bq.to(dev), bs.to(dev))
+    assert torch.equal(got.cpu(), orc.dequant_block_bf16(bq, bs))

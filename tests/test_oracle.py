@@ -1,0 +1,228 @@
+"""CPU pins of the oracle (oracle/fp8_oracle.py) — no GPU needed.
+
+Each test checks the oracle against something that does not restate it: the OCP
+e4m3fn spec (textbook RNE), a correctly rounded log2, hand-derived known answers,
+identities between different oracle functions, and brute force on tiny inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8_oracle as orc
+
+
+def _bits(e, m, sign=0):
+    return np.uint32(sign) | (np.uint32(e + 127) << np.uint32(23)) | np.asarray(m, dtype=np.uint32)
+
+
+# ---------------------------------------------------------------------------
+# e4m3 cast (torch float8_e4m3fn, used by the oracle) == textbook OCP RNE
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("e", list(range(-12, 9)))
+def test_e4m3_cast_exhaustive_per_binade(e):
+    """Every fp32 of both signs in binade 2^e (e covers all non-trivial rounding)."""
+    m = np.arange(0, 1 << 23, dtype=np.uint32)
+    for sign in (0, 0x80000000):
+        v = _bits(e, m, sign).view(np.float32)
+        want = orc.e4m3_rne_np(v)
+        got = torch.from_numpy(v.copy()).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        bad = np.nonzero(got != want)[0]
+        assert bad.size == 0, f"binade {e} sign {sign:#x}: first mismatches {v[bad[:4]]}"
+
+
+def test_e4m3_cast_specials():
+    v = np.array([0.0, -0.0, 1e-30, -1e-30, 2.0**-10, 2.0**-10 * 1.0000001, 448.0, 460.0, 464.0,
+                  464.00003, -448.0, np.inf, -np.inf, np.nan, 1.0625, 1.1875, 2.0**-126],
+                 dtype=np.float32)
+    want = orc.e4m3_rne_np(v)
+    got = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert (got == want).all()
+    # hand-derived: RNE ties go to even mantissa; 1.0625 -> 1.0 (0x38), 1.1875 -> 1.25 (0x3A)
+    assert list(want[[0, 1, 6, 10, 14, 15]]) == [0x00, 0x80, 0x7E, 0xFE, 0x38, 0x3A]
+    assert want[4] == 0x00 and want[5] == 0x01  # 2^-10 is the tie between 0 and 2^-9
+    assert want[8] == 0x7E and want[9] == 0x7F  # 464 ties to 448; above it is NaN
+
+
+# ---------------------------------------------------------------------------
+# round_scale: torch exp2(ceil(log2(v))) == ceil of the correctly rounded fp32 log2,
+# == the integer threshold rule the HIP kernel uses (cin_common.h compute_scale)
+# ---------------------------------------------------------------------------
+def _kernel_rule_exponent(k, m):
+    """The HIP kernel's rule, restated: exponent of the round_scale result."""
+    if m == 0:
+        return k
+    a = k if k > 0 else (-k - 1 if k < 0 else 0)
+    j = a.bit_length() - 1 if a else -1
+    t = 1 if j <= 1 else {2: 2, 3: 3, 4: 6, 5: 12}.get(j, 23)
+    return k + 1 if m >= t else k
+
+
+def test_round_scale_thresholds_all_exponents():
+    # every exponent reachable from amax in [fp32(1e-4), fp32 max] / 448
+    ms = np.concatenate([np.arange(0, 64, dtype=np.uint32),
+                         np.random.default_rng(0).integers(64, 1 << 23, 512, dtype=np.uint32),
+                         np.array([(1 << 23) - 1], dtype=np.uint32)])
+    for k in range(-23, 120):
+        v = _bits(k, ms).view(np.float32)
+        got = torch.exp2(torch.ceil(torch.log2(torch.from_numpy(v.copy())))).numpy()
+        cr = np.exp2(np.ceil(np.log2(v.astype(np.float64)).astype(np.float32).astype(np.float64)))
+        assert (got == cr.astype(np.float32)).all(), k
+        rule = np.array([2.0 ** _kernel_rule_exponent(k, int(mm)) for mm in ms], dtype=np.float32)
+        assert (got == rule).all(), (k, ms[got != rule][:4])
+
+
+@pytest.mark.slow
+def test_round_scale_exhaustive():
+    """All 2^23 mantissas for every reachable exponent (long; run with -m slow)."""
+    m = np.arange(0, 1 << 23, dtype=np.uint32)
+    for k in range(-23, 120):
+        v = torch.from_numpy(_bits(k, m).view(np.float32).copy())
+        eq_k = (torch.log2(v) == float(k)).numpy()
+        thr = int(np.nonzero(~eq_k[1:])[0][0]) + 1
+        assert eq_k[1:thr].all() and not eq_k[thr:].any()
+        assert _kernel_rule_exponent(k, thr) == k + 1 and _kernel_rule_exponent(k, thr - 1) in (k, k + 1)
+        if thr > 1:
+            assert _kernel_rule_exponent(k, thr - 1) == k
+
+
+# ---------------------------------------------------------------------------
+# Quantizer known answers and invariants
+# ---------------------------------------------------------------------------
+def test_rowwise_known_answers_fp32():
+    x = torch.zeros(1, 128)
+    x[0, :4] = torch.tensor([448.0, 1.0, -1.0, 0.5])
+    q, s = orc.quant_rowwise(x)
+    assert s.item() == 1.0  # 448 / 448
+    assert q.view(torch.uint8)[0, :5].tolist() == [0x7E, 0x38, 0xB8, 0x30, 0x00]
+    x = torch.zeros(1, 128)
+    x[0, :2] = torch.tensor([896.0, 3.0])
+    q, s = orc.quant_rowwise(x)
+    assert s.item() == 2.0 and q.view(torch.uint8)[0, :2].tolist() == [0x7E, 0x3C]  # 3/2 = 1.5
+
+
+def test_zero_tile_floor_depends_on_input_dtype():
+    # Triton evaluates tl.maximum(bf16_tile, 1e-4) in bf16: floor = bf16(1e-4) = 1.0013580322265625e-4
+    _, s_bf = orc.quant_rowwise(torch.zeros(2, 256, dtype=torch.bfloat16))
+    _, s_32 = orc.quant_rowwise(torch.zeros(2, 256, dtype=torch.float32))
+    assert (s_bf == np.float32(1.0013580322265625e-04) / np.float32(448.0)).all()
+    assert (s_32 == np.float32(1e-4) / np.float32(448.0)).all()
+    assert s_bf[0, 0].item() != s_32[0, 0].item()
+
+
+def test_nan_and_inf_follow_maxnum_semantics():
+    x = torch.zeros(1, 128)
+    x[0, 0] = float("nan")
+    x[0, 1] = 2.0
+    x[0, 2] = -1.0
+    q, s = orc.quant_rowwise(x)
+    assert s.item() == np.float32(2.0) / np.float32(448.0)  # NaN ignored by the amax
+    c = q.view(torch.uint8)[0]
+    assert c[0].item() == 0xFE and c[1].item() == 0x7E  # NaN -> maxnum(NaN, -448) = -448
+    x = torch.zeros(1, 128)
+    x[0, 0] = float("inf")
+    x[0, 1] = -3.0
+    q, s = orc.quant_rowwise(x)
+    c = q.view(torch.uint8)[0]
+    assert s.item() == float("inf") and c[0].item() == 0xFE and c[1].item() == 0x80
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_quant_invariants_random(dtype):
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(64, 1000, generator=g)
+    x[torch.rand(64, 1000, generator=g) < 0.01] *= 20
+    x = x.to(dtype)
+    q, s = orc.quant_rowwise(x)
+    c = q.view(torch.uint8)
+    assert s.shape == (64, 8)
+    # the tile's amax element maps to +-448 and no code is NaN
+    for t in range(8):
+        tile = c[:, t * 128:(t + 1) * 128]
+        assert ((tile & 0x7F).amax(dim=1) == 0x7E).all()
+    assert not ((c & 0x7F) == 0x7F).any()
+    # |dequant - x| <= half an e4m3 spacing (times the scale) everywhere
+    y = x.float() / s.repeat_interleave(128, dim=1)[:, :1000]
+    deq = q.float()
+    spacing = torch.where(deq.abs() >= 2.0 ** -6, torch.exp2(torch.floor(torch.log2(deq.abs().clamp_min(2.0 ** -6)))) / 8,
+                          torch.full_like(deq, 2.0 ** -9))
+    assert ((deq - y).abs() <= spacing / 2 * (1 + 1e-6)).all()
+
+
+def test_column_tiles_equal_rowwise_of_transpose():
+    # quant_rowwise(dY^T) (src/kernels.py:781-783) == 128x1 column tiles of dY
+    g = torch.Generator().manual_seed(3)
+    dy = (torch.randn(300, 200, generator=g) * 1e-3).to(torch.bfloat16)
+    qt, st = orc.quant_rowwise(dy.t().contiguous())
+    qc, sc = orc.quant_blockwise(dy, 128, 1)
+    assert torch.equal(qt.view(torch.uint8), qc.view(torch.uint8).t())
+    assert torch.equal(st, sc.t())
+
+
+def test_blockwise_1xN_equals_rowwise():
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(50, 300, generator=g).to(torch.bfloat16)
+    q1, s1 = orc.quant_rowwise(x, 128)
+    q2, s2 = orc.quant_blockwise(x, 1, 128)
+    assert torch.equal(q1.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s1, s2)
+
+
+# ---------------------------------------------------------------------------
+# GEMM oracle vs brute force (src/kernels.py:634-660 loop order, fp64)
+# ---------------------------------------------------------------------------
+def test_gemm_oracle_vs_bruteforce():
+    g = torch.Generator().manual_seed(5)
+    M, N, K = 3, 130, 256
+    a, sa = orc.quant_rowwise(torch.randn(M, K, generator=g))
+    w, sw = orc.quant_blockwise(torch.randn(N, K, generator=g) * 0.02)
+    b = w.view(torch.uint8).t().contiguous()   # [K, N]
+    sb = sw.t().contiguous()                   # [kb, nb]
+    got = orc.gemm_ref(a, sa, b, sb)
+    af, bf = a.float().double(), b.view(torch.float8_e4m3fn).float().double()
+    want = torch.zeros(M, N, dtype=torch.float64)
+    for kb in range(K // 128):
+        ks = slice(kb * 128, (kb + 1) * 128)
+        for n in range(N):
+            an = af[:, ks] * sa[:, kb:kb + 1].double()
+            bn = bf[ks, n] * sb[kb, n // 128].double()
+            want[:, n] += an @ bn
+    assert orc.frob_rel(got, want) < 1e-6 and orc.normwise_max_rel(got, want) < 1e-6
+
+
+def test_fp8_linear_exact_on_representable_inputs():
+    """Inputs on the e4m3 grid with tile amax 448*2^j quantize exactly, so the whole
+    forward/backward chain must equal the float64 matmuls (catches any operand or
+    transpose mix-up in the oracle's restatement of src/kernels.py:739-794)."""
+    g = torch.Generator().manual_seed(9)
+    M, N, K = 256, 256, 384
+    grid_vals = torch.tensor([0.0, 0.5, 1.0, -1.0, 2.0, -3.0, 448.0])
+
+    def make(rows, cols, scale):
+        idx = torch.randint(0, 6, (rows, cols), generator=g)
+        v = grid_vals[idx]
+        v[:, ::128] = 448.0  # every 1x128 row tile holds 448 ...
+        v[::128, :] = 448.0  # ... and every 128x1 column tile too
+        return v * scale
+
+    x = make(M, K, 2.0 ** -4)
+    w = make(N, K, 2.0 ** -10)
+    dy = make(M, N, 2.0 ** -12)
+    r = orc.fp8_linear_ref(x, w, dy)
+    xd, wd, dyd = x.double(), w.double(), dy.double()
+    # quantization is exact here; only fp32 summation rounding remains
+    for got, want in [(r["y"], xd @ wd.t()), (r["dx"], dyd @ wd), (r["dw"], dyd.t() @ xd)]:
+        assert orc.normwise_max_rel(got, want) < 1e-6
+    # and the saved codes dequantize back to the inputs bit-exactly
+    assert torch.equal(orc.dequant_rowwise(r["x_fp8"], r["x_scale"]), x)
+    assert torch.equal(orc.dequant_block(r["w_fp8"], r["w_scale"]), w)
+    assert torch.equal(orc.dequant_rowwise(r["g_fp8_t"], r["g_scale_t"]), dy.t())
+    assert torch.equal(orc.dequant_block(r["xb_fp8"], r["xb_scale"]), x)
+
+
+def test_grouped_oracle_e1_equals_dense():
+    g = torch.Generator().manual_seed(11)
+    T, N, K = 200, 256, 256
+    a, sa = orc.quant_rowwise(torch.randn(T, K, generator=g).to(torch.bfloat16))
+    w, sw = orc.quant_blockwise(torch.randn(N, K, generator=g) * 0.02)
+    got = orc.grouped_gemm_ref(a, sa, w.view(torch.uint8)[None], sw[None], [0], [T])
+    want = orc.gemm_ref(a, sa, w.view(torch.uint8).t().contiguous(), sw.t().contiguous())
+    assert torch.equal(got, want)
