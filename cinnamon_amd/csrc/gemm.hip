@@ -35,8 +35,6 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int BM = 128, BN = 128, BK = 128;
 constexpr int kThreads = 256;
 constexpr int kChunksPerRow = BK / 16;                 // 8 x 16-byte chunks per tile row
-constexpr int kLoadsA = BM * kChunksPerRow / kThreads;  // 4
-constexpr int kLoadsB = BN * kChunksPerRow / kThreads;  // 4
 
 struct TileArgs {
   const uint8_t* A;  // first row of this tile's A rows
@@ -241,6 +239,204 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_gemm_fp8(
   gemm_tile(t, lda, ldb, ssam, ssak, ssbk, K, C, c_dtype, ldc, row0, n0, t.rows_b);
 }
 
+
+// ---------------------------------------------------------------------------
+// Large-tile kernel for K % 128 == 0: workgroup tile 256 x 256, 8 waves (2 x 4),
+// wave tile 128 (m) x 64 (n).  Operand tiles go global -> LDS directly
+// (global_load_lds_dwordx4, no register staging); the XOR swizzle is applied by
+// choosing which global chunk each lane fetches.  The 256 A-scales of a K block
+// are staged into LDS the same way.  Two LDS stages, one barrier per K block.
+// ---------------------------------------------------------------------------
+namespace big {
+
+constexpr int TM = 256, TN = 256, TK = 128;
+constexpr int kThreads = 512;
+constexpr int kTileBytes = TM * TK;  // 32 KB per operand per stage
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+struct Smem {
+  uint8_t a[2][kTileBytes];
+  uint8_t b[2][kTileBytes];
+  float sa[2][TM];
+  float sb[2][64];  // [stage][n-block of the tile] (2 used)
+};
+
+// global -> LDS copy of 16 bytes per lane (4 for dma4).  The LDS destination is
+// M0 + lane * size, so `lds_wave_base` must be uniform across the wave.  Issued
+// through inline asm so the compiler does not serialize later LDS reads of the
+// other stage behind these writes; completion is awaited explicitly (vmcnt + barrier)
+// before the stage is read.  M0 is written here and is not otherwise used by the
+// kernels of this file.
+__device__ inline void dma16(const void* gptr, const uint8_t* lds_wave_base) {
+  uint32_t a = (uint32_t)(uintptr_t)((const lds_u8*)lds_wave_base);
+  a = __builtin_amdgcn_readfirstlane(a);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(gptr), "s"(a) : "memory");
+}
+__device__ inline void dma4(const void* gptr, const uint8_t* lds_wave_base) {
+  uint32_t a = (uint32_t)(uintptr_t)((const lds_u8*)lds_wave_base);
+  a = __builtin_amdgcn_readfirstlane(a);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(gptr), "s"(a) : "memory");
+}
+
+__device__ inline void issue_tile(const uint8_t* base, int64_t ld, int rows_valid, int64_t k0,
+                                  uint8_t* lds) {
+  // 2048 16-byte chunks; this thread fills slots c = i*512 + tid; slot c holds
+  // row c/8, logical chunk (c%8) ^ (row%8)
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = i * kThreads + tid;
+    const int r = c >> 3, p = c & 7;
+    const int q = p ^ (r & 7);
+    const int rr = r < rows_valid ? r : rows_valid - 1;
+    dma16(base + (int64_t)rr * ld + k0 + q * 16, lds + (i * kThreads + (tid & ~63)) * 16);
+  }
+}
+
+// A scales of the 256 tile rows and the B scales of the tile's two 128-column
+// blocks for K block kb.
+__device__ inline void issue_scales(const float* sa, int64_t ssam, int64_t ssak, int rows_valid,
+                                    const float* sb, int64_t ssbn, int64_t ssbk, int nblk_valid,
+                                    int kb, float* lds_sa, float* lds_sb) {
+  const int tid = threadIdx.x;
+  if (tid < TM) {
+    const int rr = tid < rows_valid ? tid : rows_valid - 1;
+    dma4(sa + (int64_t)rr * ssam + (int64_t)kb * ssak,
+         reinterpret_cast<const uint8_t*>(lds_sa + (tid & ~63)));
+  } else if (tid < TM + 64) {
+    const int j = tid - TM;
+    const int jj = j < nblk_valid ? j : nblk_valid - 1;
+    dma4(sb + (int64_t)jj * ssbn + (int64_t)kb * ssbk, reinterpret_cast<const uint8_t*>(lds_sb));
+  }
+}
+
+__device__ inline v8i frag(const uint8_t* lds, int row, int kq) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(lds + swz(row, 2 * kq));
+  const uint4 hi = *reinterpret_cast<const uint4*>(lds + swz(row, 2 * kq + 1));
+  v8i v;
+  v[0] = (int)lo.x; v[1] = (int)lo.y; v[2] = (int)lo.z; v[3] = (int)lo.w;
+  v[4] = (int)hi.x; v[5] = (int)hi.y; v[6] = (int)hi.z; v[7] = (int)hi.w;
+  return v;
+}
+
+__global__ __launch_bounds__(kThreads, 2) void k_gemm_fp8_bs_256(
+    const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
+    int64_t ssak, const uint8_t* __restrict__ B, int64_t ldb, const float* __restrict__ sb,
+    int64_t ssbn, int64_t ssbk, int64_t M, int64_t N, int64_t K, void* C, int c_dtype,
+    int64_t ldc, uint32_t tiles_m, uint32_t tiles_n) {
+  __shared__ Smem sm;
+  // XCD-aware mapping: workgroup b runs on XCD b % 8; give each XCD a contiguous
+  // run of tiles (n fastest) so its CUs share A row panels and B in their L2.
+  const uint32_t G = tiles_m * tiles_n;
+  uint32_t b = blockIdx.x;
+  const uint32_t Gfull = G & ~7u;
+  if (b < Gfull) b = (b & 7u) * (Gfull >> 3) + (b >> 3);
+  const uint32_t tm = b / tiles_n, tn = b - tm * tiles_n;
+  const int64_t m0 = (int64_t)tm * TM, n0 = (int64_t)tn * TN;
+  const int rows_a = (int)((M - m0) < TM ? (M - m0) : TM);
+  const int rows_b = (int)((N - n0) < TN ? (N - n0) : TN);
+  const uint8_t* Ab = A + m0 * lda;
+  const uint8_t* Bb = B + n0 * ldb;
+  const float* sab = sa + m0 * ssam;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int l16 = lane & 15, kq = lane >> 4;
+  const float* sbt = sb + (n0 >> 7) * ssbn;
+  const int nblk = (int)cdiv(N - n0, 128) < 2 ? (int)cdiv(N - n0, 128) : 2;
+
+  v4f acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (int)(K / TK);
+  issue_tile(Ab, lda, rows_a, 0, sm.a[0]);
+  issue_tile(Bb, ldb, rows_b, 0, sm.b[0]);
+  issue_scales(sab, ssam, ssak, rows_a, sbt, ssbn, ssbk, nblk, 0, sm.sa[0], sm.sb[0]);
+
+  for (int kb = 0; kb < nk; ++kb) {
+    const int st = kb & 1;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads for kb landed
+    __syncthreads();                     // ... and everyone's; stage st^1 is free
+    if (kb + 1 < nk) {
+      issue_tile(Ab, lda, rows_a, (int64_t)(kb + 1) * TK, sm.a[st ^ 1]);
+      issue_tile(Bb, ldb, rows_b, (int64_t)(kb + 1) * TK, sm.b[st ^ 1]);
+      issue_scales(sab, ssam, ssak, rows_a, sbt, ssbn, ssbk, nblk, kb + 1, sm.sa[st ^ 1],
+                   sm.sb[st ^ 1]);
+    }
+    const float sbv = sm.sb[st][wn >> 1];
+    const uint8_t* la = sm.a[st];
+    const uint8_t* lb = sm.b[st];
+    v8i bf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bf[j] = frag(lb, wn * 64 + j * 16 + l16, kq);
+    // software pipeline over the 8 m-tiles: the MFMAs of tile i+1 are issued
+    // before the fp32 scale-FMAs of tile i, into a second set of partials
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    v4f p[2][4];
+    {
+      const v8i af = frag(la, wm * 128 + l16, kq);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        p[0][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af, zero, 0, 0, 0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i + 1 < 8) {
+        const v8i af = frag(la, wm * 128 + (i + 1) * 16 + l16, kq);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          p[(i + 1) & 1][j] =
+              __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af, zero, 0, 0, 0, 0, 0, 0);
+      }
+      const float cs = sm.sa[st][wm * 128 + i * 16 + l16] * sbv;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(p[i & 1][j][r], cs, acc[i][j][r]);
+    }
+  }
+
+  // epilogue: lane holds C[m][n .. n+3]
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int m = wm * 128 + i * 16 + l16;
+    if (m >= rows_a) continue;
+    const int64_t crow = m0 + m;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = wn * 64 + j * 16 + kq * 4;
+      if (c_dtype == CIN_DT_F32) {
+        float* cp = static_cast<float*>(C) + crow * ldc + n0 + n;
+        if (n + 4 <= rows_b && (((uintptr_t)cp) & 15) == 0) {
+          *reinterpret_cast<float4*>(cp) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+        } else {
+          for (int r = 0; r < 4; ++r)
+            if (n + r < rows_b) cp[r] = acc[i][j][r];
+        }
+      } else {
+        uint16_t* cp = static_cast<uint16_t*>(C) + crow * ldc + n0 + n;
+        const uint32_t b0 = f32_to_bf16_bits(acc[i][j][0]), b1 = f32_to_bf16_bits(acc[i][j][1]);
+        const uint32_t b2 = f32_to_bf16_bits(acc[i][j][2]), b3 = f32_to_bf16_bits(acc[i][j][3]);
+        if (n + 4 <= rows_b && (((uintptr_t)cp) & 7) == 0) {
+          *reinterpret_cast<uint2*>(cp) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+        } else {
+          const uint32_t bb[4] = {b0, b1, b2, b3};
+          for (int r = 0; r < 4; ++r)
+            if (n + r < rows_b) cp[r] = (uint16_t)bb[r];
+        }
+      }
+    }
+  }
+}
+
+}  // namespace big
+
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -268,6 +464,12 @@ int cin_gemm_fp8_bs(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam
                                     N * (c_dtype == CIN_DT_F32 ? 4 : 2), M, s);
     if (e != hipSuccess) return cin_set_error(CIN_ERR_HIP, "gemm_fp8_bs: %s", hipGetErrorString(e));
     return CIN_OK;
+  }
+  if (K % big::TK == 0) {
+    const uint32_t tm = (uint32_t)cdiv(M, big::TM), tn = (uint32_t)cdiv(N, big::TN);
+    hipLaunchKernelGGL(big::k_gemm_fp8_bs_256, tm * tn, big::kThreads, 0, s, A, lda, sa, ssam,
+                       ssak, B, ldb, sb, ssbn, ssbk, M, N, K, C, c_dtype, ldc, tm, tn);
+    return cin_check_launch("gemm_fp8_bs");
   }
   const uint32_t ntn = (uint32_t)cdiv(N, BN);
   const unsigned grid = (unsigned)(cdiv(M, BM) * ntn);

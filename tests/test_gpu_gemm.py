@@ -81,10 +81,13 @@ def test_fp8_matmul_dsv3_api(kern, dev):
     b_kn = wq.view(torch.uint8).t().contiguous()
     sb_kn = ws.t().contiguous()
     want = orc.gemm_ref(xq, xs, b_kn, sb_kn)
+    y32 = kern.fp8_gemm_bs(xq.to(dev), xs.to(dev), wq.to(dev), ws.to(dev), torch.float32)
+    _check(y32, want, "fp8_gemm_bs")
     for b in (b_kn.to(dev), wq.to(dev).view(torch.uint8).t()):
         y = kern.fp8_matmul_dsv3(xq.to(dev), b.view(torch.float8_e4m3fn), xs.to(dev), sb_kn.to(dev))
         assert y.dtype == torch.bfloat16 and y.shape == (512, 384)
-        _check(y.float(), want, "fp8_matmul_dsv3")
+        # bf16 output = RNE of the fp32 epilogue
+        assert torch.equal(y, y32.to(torch.bfloat16))
 
 
 def test_gemm_deterministic(kern, dev):
