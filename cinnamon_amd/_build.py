@@ -31,6 +31,9 @@ COMMON = [
     "-ffp-contract=off",
     # packed fp32 VALU ops stay off (hand-written and compiler-made)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the GEMM epilogue FMAs read every MFMA result, and an
+    # AGPR destination would add one v_accvgpr_read per element
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     f"-I{INCLUDE}",
     "-Wall",
     "-Wno-unused-function",

@@ -55,6 +55,21 @@ __device__ inline float compute_scale(float amax, bool round_scale) {
   return __uint_as_float((uint32_t)(e + 127) << 23);
 }
 
+// x / s for the e4m3 cast, computed as x * r with r = RN(1 / s).
+// |x*r - x/s| < 1.5 ulp, so RN(x/s) is within 3 fp32 steps of the product.  The
+// e4m3 code of the product equals the code of RN(x/s) unless an e4m3 rounding
+// midpoint lies within 4 steps of it: low 20 bits near 0x80000 for |y| >= 2^-6, or
+// anywhere in [2^-11, 2^-6 + 8 steps) where e4m3 is subnormal.  Those lanes set
+// `unsafe` and the caller redoes them with the IEEE division.
+__device__ inline float mul_guarded(float x, float r, uint32_t& unsafe) {
+  const float y = x * r;
+  const uint32_t a = __float_as_uint(y) & 0x7fffffffu;
+  const uint32_t near_mid = ((a + (4u - 0x80000u)) & 0xfffffu) <= 8u;
+  const uint32_t small = (a - 0x3A000000u) < (0x3C800008u - 0x3A000000u);
+  unsafe |= near_mid | small;
+  return y;
+}
+
 // Clamp with maxnum/minnum semantics: NaN maps to -448 like the reference's
 // tl.minimum(tl.maximum(x, -448), 448).
 __device__ inline float clamp448(float y) {

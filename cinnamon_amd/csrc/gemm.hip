@@ -20,6 +20,7 @@
 // lane ends up holding 4 consecutive columns of one row (one 8-byte bf16 or
 // 16-byte fp32 store per fragment) and a single combined scale sa[m] * sb.
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #include "cin_common.h"
@@ -34,7 +35,6 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128, BK = 128;
 constexpr int kThreads = 256;
-constexpr int kChunksPerRow = BK / 16;                 // 8 x 16-byte chunks per tile row
 
 struct TileArgs {
   const uint8_t* A;  // first row of this tile's A rows
@@ -249,73 +249,32 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_gemm_fp8(
 // ---------------------------------------------------------------------------
 namespace big {
 
+// Workgroup tile 256 x 256 x 128, 8 waves (2 per SIMD: one wave's MFMAs run while
+// the other issues its scale-FMAs), wave tile 128 (m) x 64 (n), two LDS stages.
+// Operands are staged global -> VGPR -> LDS: the loads of K block kb+1 are issued at
+// the start of block kb and written to the free stage in its second half.  (The
+// global_load_lds path moves only ~16 bytes per clock per CU on gfx950, half of what
+// the MFMAs consume here.)
 constexpr int TM = 256, TN = 256, TK = 128;
 constexpr int kThreads = 512;
 constexpr int kTileBytes = TM * TK;  // 32 KB per operand per stage
 
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
-
-struct Smem {
+struct __attribute__((aligned(16))) Smem {
   uint8_t a[2][kTileBytes];
   uint8_t b[2][kTileBytes];
   float sa[2][TM];
-  float sb[2][64];  // [stage][n-block of the tile] (2 used)
+  float sb[2][2];
 };
 
-// global -> LDS copy of 16 bytes per lane (4 for dma4).  The LDS destination is
-// M0 + lane * size, so `lds_wave_base` must be uniform across the wave.  Issued
-// through inline asm so the compiler does not serialize later LDS reads of the
-// other stage behind these writes; completion is awaited explicitly (vmcnt + barrier)
-// before the stage is read.  M0 is written here and is not otherwise used by the
-// kernels of this file.
-__device__ inline void dma16(const void* gptr, const uint8_t* lds_wave_base) {
-  uint32_t a = (uint32_t)(uintptr_t)((const lds_u8*)lds_wave_base);
-  a = __builtin_amdgcn_readfirstlane(a);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(gptr), "s"(a) : "memory");
-}
-__device__ inline void dma4(const void* gptr, const uint8_t* lds_wave_base) {
-  uint32_t a = (uint32_t)(uintptr_t)((const lds_u8*)lds_wave_base);
-  a = __builtin_amdgcn_readfirstlane(a);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-               :: "v"(gptr), "s"(a) : "memory");
-}
-
-__device__ inline void issue_tile(const uint8_t* base, int64_t ld, int rows_valid, int64_t k0,
-                                  uint8_t* lds) {
-  // 2048 16-byte chunks; this thread fills slots c = i*512 + tid; slot c holds
-  // row c/8, logical chunk (c%8) ^ (row%8)
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = i * kThreads + tid;
-    const int r = c >> 3, p = c & 7;
-    const int q = p ^ (r & 7);
-    const int rr = r < rows_valid ? r : rows_valid - 1;
-    dma16(base + (int64_t)rr * ld + k0 + q * 16, lds + (i * kThreads + (tid & ~63)) * 16);
-  }
-}
-
-// A scales of the 256 tile rows and the B scales of the tile's two 128-column
-// blocks for K block kb.
-__device__ inline void issue_scales(const float* sa, int64_t ssam, int64_t ssak, int rows_valid,
-                                    const float* sb, int64_t ssbn, int64_t ssbk, int nblk_valid,
-                                    int kb, float* lds_sa, float* lds_sb) {
-  const int tid = threadIdx.x;
-  if (tid < TM) {
-    const int rr = tid < rows_valid ? tid : rows_valid - 1;
-    dma4(sa + (int64_t)rr * ssam + (int64_t)kb * ssak,
-         reinterpret_cast<const uint8_t*>(lds_sa + (tid & ~63)));
-  } else if (tid < TM + 64) {
-    const int j = tid - TM;
-    const int jj = j < nblk_valid ? j : nblk_valid - 1;
-    dma4(sb + (int64_t)jj * ssbn + (int64_t)kb * ssbk, reinterpret_cast<const uint8_t*>(lds_sb));
-  }
-}
+// 16-byte chunk c of tile row r lives at slot c ^ f(r), f(r) = (r % 8) ^ ((r / 8) % 2):
+// the 8 rows a 32-bank LDS serves together, and the 8 same-parity rows a 64-bank LDS
+// serves together, all hit distinct banks.
+__device__ inline int swz_f(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ inline int swz2(int row, int chunk) { return row * TK + ((chunk ^ swz_f(row)) << 4); }
 
 __device__ inline v8i frag(const uint8_t* lds, int row, int kq) {
-  const uint4 lo = *reinterpret_cast<const uint4*>(lds + swz(row, 2 * kq));
-  const uint4 hi = *reinterpret_cast<const uint4*>(lds + swz(row, 2 * kq + 1));
+  const uint4 lo = *reinterpret_cast<const uint4*>(lds + swz2(row, 2 * kq));
+  const uint4 hi = *reinterpret_cast<const uint4*>(lds + swz2(row, 2 * kq + 1));
   v8i v;
   v[0] = (int)lo.x; v[1] = (int)lo.y; v[2] = (int)lo.z; v[3] = (int)lo.w;
   v[4] = (int)hi.x; v[5] = (int)hi.y; v[6] = (int)hi.z; v[7] = (int)hi.w;
@@ -335,18 +294,63 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm_fp8_bs_256(
   const uint32_t Gfull = G & ~7u;
   if (b < Gfull) b = (b & 7u) * (Gfull >> 3) + (b >> 3);
   const uint32_t tm = b / tiles_n, tn = b - tm * tiles_n;
-  const int64_t m0 = (int64_t)tm * TM, n0 = (int64_t)tn * TN;
-  const int rows_a = (int)((M - m0) < TM ? (M - m0) : TM);
-  const int rows_b = (int)((N - n0) < TN ? (N - n0) : TN);
+  // Every tile is a full 256 x 256 block inside the matrix (M, N >= 256, N % 128 == 0):
+  // the last tile of a row/column is shifted back onto its neighbour and only stores
+  // the rows/columns its neighbour does not.
+  const int64_t m_nom = (int64_t)tm * TM, n_nom = (int64_t)tn * TN;
+  const int64_t m0 = m_nom + TM <= M ? m_nom : M - TM;
+  const int64_t n0 = n_nom + TN <= N ? n_nom : N - TN;
+  const int skip_m = (int)(m_nom - m0), skip_n = (int)(n_nom - n0);
   const uint8_t* Ab = A + m0 * lda;
   const uint8_t* Bb = B + n0 * ldb;
   const float* sab = sa + m0 * ssam;
+  const float* sbt = sb + (n0 >> 7) * ssbn;
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
   const int l16 = lane & 15, kq = lane >> 4;
-  const float* sbt = sb + (n0 >> 7) * ssbn;
-  const int nblk = (int)cdiv(N - n0, 128) < 2 ? (int)cdiv(N - n0, 128) : 2;
+
+  // Loads: round i covers tile rows i*64 .. i*64+63; thread tid fetches row
+  // i*64 + tid/8, chunk (tid % 8) ^ swz_f(row) and stores it to slot i*512 + tid.
+  const int r0 = tid >> 3;
+  const int q16 = ((tid & 7) ^ swz_f(r0)) * 16;
+  const uint8_t* ga = Ab + (int64_t)r0 * lda + q16;
+  const uint8_t* gb = Bb + (int64_t)r0 * ldb + q16;
+  const int64_t stepa = 64 * lda, stepb = 64 * ldb;
+  // scales: threads 0-255 fetch the A-scale rows, 256-257 the tile's two B-block scales
+  const float* gs = tid < TM ? sab + (int64_t)tid * ssam : sbt + (int64_t)((tid - TM) & 1) * ssbn;
+  const int64_t steps = tid < TM ? ssak : ssbk;
+  const bool has_s = tid < TM + 2;
+
+  // staging registers for half a K block: the 4 A chunks, later the 4 B chunks + scale
+  uint4 r0v, r1v, r2v, r3v;
+  float rs = 0.0f;
+#define CIN_LOAD_A(kb)                                                                      \
+  do {                                                                                      \
+    const int64_t ko = (int64_t)(kb) * TK;                                                  \
+    r0v = *reinterpret_cast<const uint4*>(ga + ko);                                         \
+    r1v = *reinterpret_cast<const uint4*>(ga + stepa + ko);                                 \
+    r2v = *reinterpret_cast<const uint4*>(ga + 2 * stepa + ko);                             \
+    r3v = *reinterpret_cast<const uint4*>(ga + 3 * stepa + ko);                             \
+  } while (0)
+#define CIN_LOAD_B(kb)                                                                      \
+  do {                                                                                      \
+    const int64_t ko = (int64_t)(kb) * TK;                                                  \
+    r0v = *reinterpret_cast<const uint4*>(gb + ko);                                         \
+    r1v = *reinterpret_cast<const uint4*>(gb + stepb + ko);                                 \
+    r2v = *reinterpret_cast<const uint4*>(gb + 2 * stepb + ko);                             \
+    r3v = *reinterpret_cast<const uint4*>(gb + 3 * stepb + ko);                             \
+    if (has_s) rs = gs[(int64_t)(kb) * steps];                                              \
+  } while (0)
+#define CIN_STORE(arr, i, rv, st)                                                           \
+  *reinterpret_cast<uint4*>(__builtin_assume_aligned(&sm.arr[st][((i) * kThreads + tid) * 16], 16)) = rv
+#define CIN_STORE_S(st)                                                                     \
+  do {                                                                                      \
+    if (tid < TM) sm.sa[st][tid] = rs;                                                      \
+    else if (has_s) sm.sb[st][tid - TM] = rs;                                               \
+  } while (0)
 
   v4f acc[8][4];
 #pragma unroll
@@ -355,80 +359,102 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm_fp8_bs_256(
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
   const int nk = (int)(K / TK);
-  issue_tile(Ab, lda, rows_a, 0, sm.a[0]);
-  issue_tile(Bb, ldb, rows_b, 0, sm.b[0]);
-  issue_scales(sab, ssam, ssak, rows_a, sbt, ssbn, ssbk, nblk, 0, sm.sa[0], sm.sb[0]);
+  CIN_LOAD_A(0);
+  CIN_STORE(a, 0, r0v, 0);
+  CIN_STORE(a, 1, r1v, 0);
+  CIN_STORE(a, 2, r2v, 0);
+  CIN_STORE(a, 3, r3v, 0);
+  CIN_LOAD_B(0);
+  CIN_STORE(b, 0, r0v, 0);
+  CIN_STORE(b, 1, r1v, 0);
+  CIN_STORE(b, 2, r2v, 0);
+  CIN_STORE(b, 3, r3v, 0);
+  CIN_STORE_S(0);
 
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
   for (int kb = 0; kb < nk; ++kb) {
     const int st = kb & 1;
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads for kb landed
-    __syncthreads();                     // ... and everyone's; stage st^1 is free
-    if (kb + 1 < nk) {
-      issue_tile(Ab, lda, rows_a, (int64_t)(kb + 1) * TK, sm.a[st ^ 1]);
-      issue_tile(Bb, ldb, rows_b, (int64_t)(kb + 1) * TK, sm.b[st ^ 1]);
-      issue_scales(sab, ssam, ssak, rows_a, sbt, ssbn, ssbk, nblk, kb + 1, sm.sa[st ^ 1],
-                   sm.sb[st ^ 1]);
-    }
-    const float sbv = sm.sb[st][wn >> 1];
+    __syncthreads();  // stage st is complete; stage st^1 is no longer read
+    const bool more = kb + 1 < nk;
+    if (more) CIN_LOAD_A(kb + 1);
     const uint8_t* la = sm.a[st];
     const uint8_t* lb = sm.b[st];
+    const float* lsa = sm.sa[st];
+    const float sbv = sm.sb[st][wn >> 1];
     v8i bf[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) bf[j] = frag(lb, wn * 64 + j * 16 + l16, kq);
-    // software pipeline over the 8 m-tiles: the MFMAs of tile i+1 are issued
-    // before the fp32 scale-FMAs of tile i, into a second set of partials
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    v4f p[2][4];
-    {
-      const v8i af = frag(la, wm * 128 + l16, kq);
+    v8i af[2];
+    af[0] = frag(la, wm * 128 + l16, kq);
+    float cs[2];
+    cs[0] = lsa[wm * 128 + l16] * sbv;
+    // 32 steps s = 4 i + j (m-tile i, n-tile j): step s issues MFMA(s) into partial
+    // ring slot s % 2, then the 4 scale-FMAs of MFMA(s-1), whose result had one MFMA
+    // slot of latency to land.  Empty asm statements pin this order (the MFMA builtins
+    // are otherwise free to move, and the compiler would cluster them and hold many
+    // partials live).
+    v4f p[2];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        p[0][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af, zero, 0, 0, 0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (i + 1 < 8) {
-        const v8i af = frag(la, wm * 128 + (i + 1) * 16 + l16, kq);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          p[(i + 1) & 1][j] =
-              __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af, zero, 0, 0, 0, 0, 0, 0);
+    for (int st8 = 0; st8 < 33; ++st8) {
+      const int i = st8 >> 2, j = st8 & 3;
+      if (st8 < 32) {
+        if (j == 0) {
+          // staged loads of the next block: A chunks were loaded at the top and are
+          // stored in groups 2-3; then the B chunks + scales, stored in groups 6-7
+          if (more) {
+            if (i == 2) { CIN_STORE(a, 0, r0v, st ^ 1); CIN_STORE(a, 1, r1v, st ^ 1); }
+            if (i == 3) { CIN_STORE(a, 2, r2v, st ^ 1); CIN_STORE(a, 3, r3v, st ^ 1); CIN_LOAD_B(kb + 1); }
+            if (i == 6) { CIN_STORE(b, 0, r0v, st ^ 1); CIN_STORE(b, 1, r1v, st ^ 1); }
+            if (i == 7) { CIN_STORE(b, 2, r2v, st ^ 1); CIN_STORE(b, 3, r3v, st ^ 1); CIN_STORE_S(st ^ 1); }
+          }
+        }
+        asm volatile("" : "+v"(bf[j]));
+        p[st8 & 1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af[i & 1], zero, 0, 0, 0, 0, 0, 0);
       }
-      const float cs = sm.sa[st][wm * 128 + i * 16 + l16] * sbv;
+      if (st8 > 0) {
+        const int s1 = st8 - 1, i1 = s1 >> 2, j1 = s1 & 3;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(p[i & 1][j][r], cs, acc[i][j][r]);
+        for (int r = 0; r < 4; ++r) acc[i1][j1][r] = fmaf(p[s1 & 1][r], cs[i1 & 1], acc[i1][j1][r]);
+        asm volatile("" : "+v"(acc[i1][j1]));
+      }
+      // fragment and scale of m-tile i+1 (its slot's previous user, tile i-1, is done)
+      if (st8 < 32 && j == 0 && i + 1 < 8) {
+        af[(i + 1) & 1] = frag(la, wm * 128 + (i + 1) * 16 + l16, kq);
+        cs[(i + 1) & 1] = lsa[wm * 128 + (i + 1) * 16 + l16] * sbv;
+      }
     }
   }
+#undef CIN_LOAD_A
+#undef CIN_LOAD_B
+#undef CIN_STORE
+#undef CIN_STORE_S
 
-  // epilogue: lane holds C[m][n .. n+3]
+  // epilogue: lane holds C[m][n .. n+3] (n a multiple of 4, so a shifted tile's
+  // column skip, a multiple of 128, never splits a lane's 4 columns)
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int m = wm * 128 + i * 16 + l16;
-    if (m >= rows_a) continue;
+    if (m < skip_m) continue;
     const int64_t crow = m0 + m;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int n = wn * 64 + j * 16 + kq * 4;
+      if (n < skip_n) continue;
       if (c_dtype == CIN_DT_F32) {
         float* cp = static_cast<float*>(C) + crow * ldc + n0 + n;
-        if (n + 4 <= rows_b && (((uintptr_t)cp) & 15) == 0) {
+        if ((((uintptr_t)cp) & 15) == 0) {
           *reinterpret_cast<float4*>(cp) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
         } else {
-          for (int r = 0; r < 4; ++r)
-            if (n + r < rows_b) cp[r] = acc[i][j][r];
+          for (int r = 0; r < 4; ++r) cp[r] = acc[i][j][r];
         }
       } else {
         uint16_t* cp = static_cast<uint16_t*>(C) + crow * ldc + n0 + n;
         const uint32_t b0 = f32_to_bf16_bits(acc[i][j][0]), b1 = f32_to_bf16_bits(acc[i][j][1]);
         const uint32_t b2 = f32_to_bf16_bits(acc[i][j][2]), b3 = f32_to_bf16_bits(acc[i][j][3]);
-        if (n + 4 <= rows_b && (((uintptr_t)cp) & 7) == 0) {
+        if ((((uintptr_t)cp) & 7) == 0) {
           *reinterpret_cast<uint2*>(cp) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
         } else {
-          const uint32_t bb[4] = {b0, b1, b2, b3};
-          for (int r = 0; r < 4; ++r)
-            if (n + r < rows_b) cp[r] = (uint16_t)bb[r];
+          cp[0] = (uint16_t)b0; cp[1] = (uint16_t)b1; cp[2] = (uint16_t)b2; cp[3] = (uint16_t)b3;
         }
       }
     }
@@ -465,7 +491,7 @@ int cin_gemm_fp8_bs(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam
     if (e != hipSuccess) return cin_set_error(CIN_ERR_HIP, "gemm_fp8_bs: %s", hipGetErrorString(e));
     return CIN_OK;
   }
-  if (K % big::TK == 0) {
+  if (K % big::TK == 0 && M >= big::TM && N >= big::TN && N % 128 == 0) {
     const uint32_t tm = (uint32_t)cdiv(M, big::TM), tn = (uint32_t)cdiv(N, big::TN);
     hipLaunchKernelGGL(big::k_gemm_fp8_bs_256, tm * tn, big::kThreads, 0, s, A, lda, sa, ssam,
                        ssak, B, ldb, sb, ssbn, ssbk, M, N, K, C, c_dtype, ldc, tm, tn);

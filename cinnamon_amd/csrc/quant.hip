@@ -13,6 +13,17 @@ namespace {
 
 constexpr int kThreads = 256;
 
+inline int elem_size(int dt) { return dt == CIN_DT_F32 ? 4 : 2; }
+inline bool valid_dtype(int dt) { return dt == CIN_DT_BF16 || dt == CIN_DT_F32 || dt == CIN_DT_F16; }
+inline bool aligned(const void* p, int a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
+
+inline unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
+  int64_t g = cdiv(work_items, per_block);
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (unsigned)g;
+}
+
 // ---------------------------------------------------------------------------
 // Row-wise 1x128, contiguous rows: each 16-lane DPP row owns one 128-element
 // tile (8 elements per lane, one 16-byte load for bf16/fp16, two for fp32).
@@ -62,55 +73,153 @@ __device__ inline void load8(const void* base, int64_t off, int64_t ncols, Vec8<
   }
 }
 
-template <int DT, int U>
+// Max over the 8 lanes of a DPP half-row (lanes 8h..8h+7), maxnum semantics.
+__device__ inline float row8_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));  // quad [1,0,3,2]
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false)));  // quad [2,3,0,1]
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false))); // row_half_mirror
+  return v;
+}
+
+// Quantize n (multiple of 4) values with scale s / reciprocal r into packed codes.
+template <int NV>
+__device__ inline void quant_vals(const float (&v)[NV], float s, float r, uint32_t (&out)[NV / 4]) {
+  float y[NV];
+  uint32_t unsafe = 0;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) y[i] = mul_guarded(v[i], r, unsafe);
+  if (unsafe) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) y[i] = v[i] / s;
+  }
+#pragma unroll
+  for (int i = 0; i < NV / 4; ++i)
+    out[i] = cvt4_e4m3(clamp448(y[4 * i]), clamp448(y[4 * i + 1]), clamp448(y[4 * i + 2]),
+                       clamp448(y[4 * i + 3]));
+}
+
+// Row-wise 1x128 with contiguous rows: LANES lanes (8 or 16, a DPP half-row or
+// row) own one tile.  Each lane loads NC 16-byte chunks, chunk c of lane i sitting at
+// tile chunk c * LANES + i so every load instruction reads whole 16*LANES-byte runs.
+// A group walks tiles t, t + G, ... keeping U tiles in flight; (row, tile) advance
+// incrementally instead of by division.
+template <int DT, int LANES, int U>
 __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict__ x, int64_t N,
                                                          int64_t sxm, int round_scale,
                                                          uint8_t* __restrict__ q, int64_t sqm,
                                                          float* __restrict__ sc, int64_t ssm,
                                                          uint32_t nb, uint32_t ntiles) {
-  const uint32_t lane16 = threadIdx.x & 15u;
-  const uint32_t G = (gridDim.x * kThreads) >> 4;  // number of 16-lane groups
-  const uint32_t g0 = (blockIdx.x * kThreads + threadIdx.x) >> 4;
+  constexpr int ES = DT == CIN_DT_F32 ? 4 : 2;  // input element bytes
+  constexpr int EPC = 16 / ES;                   // elements per 16-byte chunk
+  constexpr int NC = 128 / (LANES * EPC);        // chunks per lane
+  constexpr int EPL = NC * EPC;                  // elements per lane
+  static_assert(NC >= 1 && EPL % 4 == 0, "tile split");
+  const uint32_t li = threadIdx.x & (LANES - 1);
+  const uint32_t G = (gridDim.x * kThreads) / LANES;
+  const uint32_t g0 = (blockIdx.x * kThreads + threadIdx.x) / LANES;
   const float floor_v = amax_floor(DT);
   const bool rs = round_scale != 0;
+  uint32_t row = g0 / nb, cb = g0 - row * nb;
+  const uint32_t drow = G / nb, dcb = G - drow * nb;
   for (uint32_t tb = g0; tb < ntiles; tb += G * U) {
-    Vec8<DT> d[U];
-    uint32_t row[U], cb[U];
+    float v[U][EPL];
+    uint32_t rows[U], cbs[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      uint32_t t = tb + (uint32_t)u * G;
-      row[u] = t / nb;
-      cb[u] = t - row[u] * nb;
-      int64_t col = (int64_t)cb[u] * 128 + lane16 * 8;
-      int64_t nc = (t < ntiles) ? (N - col) : 0;
-      load8<DT>(x, (int64_t)row[u] * sxm + col, nc < 0 ? 0 : nc, d[u]);
+      rows[u] = row;
+      cbs[u] = cb;
+      const bool live = tb + (uint32_t)u * G < ntiles;
+      const int64_t base = (int64_t)row * sxm + (int64_t)cb * 128;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int64_t e0 = (int64_t)(c * LANES + li) * EPC;  // element offset in the tile
+        const int64_t col = (int64_t)cb * 128 + e0;
+        int64_t nv = live ? N - col : 0;
+        nv = nv < 0 ? 0 : (nv > EPC ? EPC : nv);
+        if (nv == EPC) {
+          if constexpr (DT == CIN_DT_F32) {
+            const f32x4 w = __builtin_nontemporal_load(
+                reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + base + e0));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[u][c * 4 + e] = w[e];
+          } else {
+            const u32x4 w = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(x) + base + e0));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if constexpr (DT == CIN_DT_BF16) {
+                v[u][c * 8 + 2 * e] = bf16_lo(w[e]);
+                v[u][c * 8 + 2 * e + 1] = bf16_hi(w[e]);
+              } else {
+                _Float16 h0, h1;
+                const uint16_t b0 = (uint16_t)(w[e] & 0xffffu), b1 = (uint16_t)(w[e] >> 16);
+                __builtin_memcpy(&h0, &b0, 2);
+                __builtin_memcpy(&h1, &b1, 2);
+                v[u][c * 8 + 2 * e] = (float)h0;
+                v[u][c * 8 + 2 * e + 1] = (float)h1;
+              }
+            }
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < EPC; ++e)
+            v[u][c * EPC + e] = (e < nv) ? load_elem(x, DT, base + e0 + e) : 0.0f;
+        }
+      }
+      cb += dcb;
+      row += drow;
+      if (cb >= nb) {
+        cb -= nb;
+        ++row;
+      }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      uint32_t t = tb + (uint32_t)u * G;
-      if (t >= ntiles) break;  // uniform across the 16-lane row
+      if (tb + (uint32_t)u * G >= ntiles) break;  // uniform across the tile's lanes
       float a = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(d[u].v[i]));
-      a = row16_max(a);
+      for (int i = 0; i < EPL; ++i) a = fmaxf(a, fabsf(v[u][i]));
+      a = LANES == 16 ? row16_max(a) : row8_max(a);
       a = fmaxf(a, floor_v);
       const float s = compute_scale(a, rs);
-      float y[8];
+      uint32_t codes[EPL / 4];
+      quant_vals<EPL>(v[u], s, 1.0f / s, codes);
+      uint8_t* qrow = q + (int64_t)rows[u] * sqm + (int64_t)cbs[u] * 128;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = clamp448(d[u].v[i] / s);
-      uint32_t lo = cvt4_e4m3(y[0], y[1], y[2], y[3]);
-      uint32_t hi = cvt4_e4m3(y[4], y[5], y[6], y[7]);
-      int64_t col = (int64_t)cb[u] * 128 + lane16 * 8;
-      uint8_t* qp = q + (int64_t)row[u] * sqm + col;
-      if (col + 8 <= N) {
-        *reinterpret_cast<uint2*>(qp) = make_uint2(lo, hi);
-      } else {
-        for (int i = 0; i < 8; ++i)
-          if (col + i < N) qp[i] = (uint8_t)(((i < 4 ? lo : hi) >> (8 * (i & 3))) & 0xffu);
+      for (int c = 0; c < NC; ++c) {
+        const int64_t e0 = (int64_t)(c * LANES + li) * EPC;
+        const int64_t col = (int64_t)cbs[u] * 128 + e0;
+        if (col + EPC <= N) {
+          if constexpr (EPC == 8)
+            *reinterpret_cast<uint2*>(qrow + e0) = make_uint2(codes[2 * c], codes[2 * c + 1]);
+          else
+            *reinterpret_cast<uint32_t*>(qrow + e0) = codes[c];
+        } else {
+          for (int e = 0; e < EPC; ++e)
+            if (col + e < N)
+              qrow[e0 + e] = (uint8_t)((codes[(c * EPC + e) >> 2] >> (8 * (e & 3))) & 0xffu);
+        }
       }
-      if (lane16 == 0) sc[(int64_t)row[u] * ssm + cb[u]] = s;
+      if (li == 0) sc[(int64_t)rows[u] * ssm + cbs[u]] = s;
     }
   }
+}
+
+template <int LANES, int U>
+void launch_rowwise128(const void* x, int dt, int64_t M, int64_t N, int64_t sxm, int rs,
+                       uint8_t* q, int64_t sqm, float* sc, int64_t ssm, int64_t nb, int gridcap,
+                       hipStream_t st) {
+  const uint32_t ntiles = (uint32_t)(M * nb);
+  const unsigned grid = grid_for(ntiles, (kThreads / LANES) * U, gridcap);
+  if (dt == CIN_DT_BF16)
+    hipLaunchKernelGGL((k_rowwise128<CIN_DT_BF16, LANES, U>), grid, kThreads, 0, st, x, N, sxm, rs,
+                       q, sqm, sc, ssm, (uint32_t)nb, ntiles);
+  else if (dt == CIN_DT_F16)
+    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F16, LANES, U>), grid, kThreads, 0, st, x, N, sxm, rs,
+                       q, sqm, sc, ssm, (uint32_t)nb, ntiles);
+  else
+    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F32, LANES, U>), grid, kThreads, 0, st, x, N, sxm, rs,
+                       q, sqm, sc, ssm, (uint32_t)nb, ntiles);
 }
 
 // Generic row-wise: one wave per (row, tile), any block size / strides / dtype.
@@ -212,15 +321,10 @@ __global__ __launch_bounds__(kThreads) void k_blockwise128(const void* __restric
   a = block_reduce_max(a, red);
   a = fmaxf(a, amax_floor(DT));
   const float s = compute_scale(a, round_scale != 0);
+  const float rcp = 1.0f / s;
   uint32_t codes[8][2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float y[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) y[j] = clamp448(d[i].v[j] / s);
-    codes[i][0] = cvt4_e4m3(y[0], y[1], y[2], y[3]);
-    codes[i][1] = cvt4_e4m3(y[4], y[5], y[6], y[7]);
-  }
+  for (int i = 0; i < 8; ++i) quant_vals<8>(d[i].v, s, rcp, codes[i]);
   if (q) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -308,11 +412,9 @@ __global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x
     a = row16_max(a);
     a = fmaxf(a, floor_v);
     const float sr = compute_scale(a, rs);
-    float y[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) y[j] = clamp448(d[i].v[j] / sr);
-    const uint32_t lo = cvt4_e4m3(y[0], y[1], y[2], y[3]);
-    const uint32_t hi = cvt4_e4m3(y[4], y[5], y[6], y[7]);
+    uint32_t c2[2];
+    quant_vals<8>(d[i].v, sr, 1.0f / sr, c2);
+    const uint32_t lo = c2[0], hi = c2[1];
     if (r < M) {
       uint8_t* qp = q + r * sqm + c;
       if (c + 8 <= N) {
@@ -341,12 +443,14 @@ __global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const float sc = colscale[lane16 * 8 + j];
+    float col[8];
 #pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      const uint32_t p = cvt2_e4m3(clamp448(d[i].v[j] / sc), clamp448(d[i + 1].v[j] / sc));
-      tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * i] = (uint8_t)(p & 0xffu);
-      tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * (i + 1)] = (uint8_t)(p >> 8);
-    }
+    for (int i = 0; i < 8; ++i) col[i] = d[i].v[j];
+    uint32_t c2[2];
+    quant_vals<8>(col, sc, 1.0f / sc, c2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * i] = (uint8_t)((c2[i >> 2] >> (8 * (i & 3))) & 0xffu);
   }
   __syncthreads();
   for (int idx = threadIdx.x; idx < 128 * 8; idx += kThreads) {
@@ -417,15 +521,10 @@ __global__ __launch_bounds__(kThreads) void k_requant128(const uint8_t* __restri
   a = block_reduce_max(a, red);
   a = fmaxf(a, kFloorF32);
   const float s = compute_scale(a, false);
+  const float rcp = 1.0f / s;
   uint32_t codes[8][2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float y[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) y[j] = clamp448(v[i][j] / s);
-    codes[i][0] = cvt4_e4m3(y[0], y[1], y[2], y[3]);
-    codes[i][1] = cvt4_e4m3(y[4], y[5], y[6], y[7]);
-  }
+  for (int i = 0; i < 8; ++i) quant_vals<8>(v[i], s, rcp, codes[i]);
   if (qb) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -523,16 +622,6 @@ __global__ __launch_bounds__(kThreads) void k_transpose_u8(const uint8_t* __rest
   }
 }
 
-inline int elem_size(int dt) { return dt == CIN_DT_F32 ? 4 : 2; }
-inline bool valid_dtype(int dt) { return dt == CIN_DT_BF16 || dt == CIN_DT_F32 || dt == CIN_DT_F16; }
-inline bool aligned(const void* p, int a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
-
-inline unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
-  int64_t g = cdiv(work_items, per_block);
-  if (g < 1) g = 1;
-  if (g > cap) g = cap;
-  return (unsigned)g;
-}
 
 }  // namespace
 
@@ -554,18 +643,7 @@ int cin_quant_rowwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
   const bool fast = block == 128 && sxn == 1 && aligned(x, 16) && ((sxm * es) % 16 == 0) &&
                     aligned(q, 8) && (sqm % 8 == 0) && M * nb < (int64_t)1 << 31;
   if (fast) {
-    const uint32_t ntiles = (uint32_t)(M * nb);
-    constexpr int U = 4;
-    const unsigned grid = grid_for(ntiles, (kThreads / 16) * U, 8192);
-    if (x_dtype == CIN_DT_BF16)
-      hipLaunchKernelGGL((k_rowwise128<CIN_DT_BF16, U>), grid, kThreads, 0, s, x, N, sxm,
-                         round_scale, q, sqm, scales, ssm, (uint32_t)nb, ntiles);
-    else if (x_dtype == CIN_DT_F16)
-      hipLaunchKernelGGL((k_rowwise128<CIN_DT_F16, U>), grid, kThreads, 0, s, x, N, sxm,
-                         round_scale, q, sqm, scales, ssm, (uint32_t)nb, ntiles);
-    else
-      hipLaunchKernelGGL((k_rowwise128<CIN_DT_F32, U>), grid, kThreads, 0, s, x, N, sxm,
-                         round_scale, q, sqm, scales, ssm, (uint32_t)nb, ntiles);
+    launch_rowwise128<16, 4>(x, x_dtype, M, N, sxm, round_scale, q, sqm, scales, ssm, nb, 8192, s);
   } else {
     const unsigned grid = grid_for(M * nb, kThreads / 64, 65536);
     hipLaunchKernelGGL(k_rowwise_generic, grid, kThreads, 0, s, x, x_dtype, M, N, sxm, sxn, block,

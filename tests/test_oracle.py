@@ -226,3 +226,46 @@ def test_grouped_oracle_e1_equals_dense():
     got = orc.grouped_gemm_ref(a, sa, w.view(torch.uint8)[None], sw[None], [0], [T])
     want = orc.gemm_ref(a, sa, w.view(torch.uint8).t().contiguous(), sw.t().contiguous())
     assert torch.equal(got, want)
+
+
+# ---------------------------------------------------------------------------
+# The HIP quantizers compute x / s as x * RN(1/s) and fall back to the IEEE division
+# only for lanes flagged near an e4m3 rounding boundary (cin_common.h mul_guarded).
+# Check that rule on the CPU: whenever a product is not flagged, its e4m3 code equals
+# the code of the correctly rounded quotient — on random and on adversarial inputs
+# placed next to every e4m3 midpoint.
+# ---------------------------------------------------------------------------
+def _guard_flags(y):
+    a = y.view(np.uint32) & np.uint32(0x7FFFFFFF)
+    near_mid = ((a + np.uint32((4 - 0x80000) & 0xFFFFFFFF)) & np.uint32(0xFFFFF)) <= 8
+    small = (a - np.uint32(0x3A000000)) < np.uint32(0x3C800008 - 0x3A000000)
+    return near_mid | small
+
+
+def _codes(y):
+    y = np.minimum(np.maximum(y, np.float32(-448.0)), np.float32(448.0))
+    return orc.e4m3_rne_np(y)
+
+
+def test_guarded_reciprocal_multiply_matches_division():
+    rng = np.random.default_rng(123)
+    n = 4_000_000
+    amax = np.exp(rng.uniform(np.log(1e-4), np.log(1e30), n)).astype(np.float32)
+    s = (amax / np.float32(448.0)).astype(np.float32)
+    x = (amax * rng.uniform(-1, 1, n).astype(np.float32)).astype(np.float32)
+    # adversarial: quotients planted next to every e4m3 midpoint (+-6 fp32 steps)
+    grid = np.arange(0, 0x7F, dtype=np.uint8).view(np.uint8)
+    vals = torch.from_numpy(grid.copy()).view(torch.float8_e4m3fn).float().numpy()
+    mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2).astype(np.float32)
+    k = np.arange(-6, 7, dtype=np.int64)
+    planted = (mids.view(np.uint32)[:, None].astype(np.int64) + k[None, :]).astype(np.uint32).view(np.float32).ravel()
+    sp = s[: planted.size]
+    xp = (planted * sp).astype(np.float32)
+    x = np.concatenate([x, xp, -xp])
+    s = np.concatenate([s, sp, sp])
+    r = (np.float32(1.0) / s).astype(np.float32)
+    y = (x * r).astype(np.float32)
+    exact = (x / s).astype(np.float32)
+    safe = ~_guard_flags(y)
+    assert safe.mean() > 0.9
+    assert (_codes(y[safe]) == _codes(exact[safe])).all()
