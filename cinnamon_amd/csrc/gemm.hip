@@ -281,31 +281,25 @@ __device__ inline v8i frag(const uint8_t* lds, int row, int kq) {
   return v;
 }
 
-__global__ __launch_bounds__(kThreads, 2) void k_gemm_fp8_bs_256(
-    const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
-    int64_t ssak, const uint8_t* __restrict__ B, int64_t ldb, const float* __restrict__ sb,
-    int64_t ssbn, int64_t ssbk, int64_t M, int64_t N, int64_t K, void* C, int c_dtype,
-    int64_t ldc, uint32_t tiles_m, uint32_t tiles_n) {
-  __shared__ Smem sm;
-  // XCD-aware mapping: workgroup b runs on XCD b % 8; give each XCD a contiguous
-  // run of tiles (n fastest) so its CUs share A row panels and B in their L2.
-  const uint32_t G = tiles_m * tiles_n;
-  uint32_t b = blockIdx.x;
-  const uint32_t Gfull = G & ~7u;
-  if (b < Gfull) b = (b & 7u) * (Gfull >> 3) + (b >> 3);
-  const uint32_t tm = b / tiles_n, tn = b - tm * tiles_n;
-  // Every tile is a full 256 x 256 block inside the matrix (M, N >= 256, N % 128 == 0):
-  // the last tile of a row/column is shifted back onto its neighbour and only stores
-  // the rows/columns its neighbour does not.
-  const int64_t m_nom = (int64_t)tm * TM, n_nom = (int64_t)tn * TN;
-  const int64_t m0 = m_nom + TM <= M ? m_nom : M - TM;
-  const int64_t n0 = n_nom + TN <= N ? n_nom : N - TN;
-  const int skip_m = (int)(m_nom - m0), skip_n = (int)(n_nom - n0);
-  const uint8_t* Ab = A + m0 * lda;
-  const uint8_t* Bb = B + n0 * ldb;
-  const float* sab = sa + m0 * ssam;
-  const float* sbt = sb + (n0 >> 7) * ssbn;
+// One full 256 x 256 tile.  A / sa point at the tile's first row, B / sb at its first
+// column block; the tile stores local rows [row_lo, row_hi) and local columns >= col_lo.
+struct Tile {
+  const uint8_t* A;
+  const float* sa;
+  const uint8_t* B;
+  const float* sb;
+  void* C;  // element (0, 0) of the tile
+  int row_lo, row_hi, col_lo;
+};
 
+__device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ssam, int64_t ssak,
+                                          int64_t ldb, int64_t ssbn, int64_t ssbk, int64_t K,
+                                          int c_dtype, int64_t ldc) {
+  __shared__ Smem sm;
+  const uint8_t* Ab = T.A;
+  const uint8_t* Bb = T.B;
+  const float* sab = T.sa;
+  const float* sbt = T.sb;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -314,35 +308,36 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm_fp8_bs_256(
 
   // Loads: round i covers tile rows i*64 .. i*64+63; thread tid fetches row
   // i*64 + tid/8, chunk (tid % 8) ^ swz_f(row) and stores it to slot i*512 + tid.
+  // Addresses are a wave-uniform base (row round, K block) plus a 32-bit lane offset.
   const int r0 = tid >> 3;
-  const int q16 = ((tid & 7) ^ swz_f(r0)) * 16;
-  const uint8_t* ga = Ab + (int64_t)r0 * lda + q16;
-  const uint8_t* gb = Bb + (int64_t)r0 * ldb + q16;
+  const uint32_t q16 = (uint32_t)(((tid & 7) ^ swz_f(r0)) * 16);
+  const uint32_t offA = (uint32_t)(r0 * lda) + q16;
+  const uint32_t offB = (uint32_t)(r0 * ldb) + q16;
   const int64_t stepa = 64 * lda, stepb = 64 * ldb;
   // scales: threads 0-255 fetch the A-scale rows, 256-257 the tile's two B-block scales
-  const float* gs = tid < TM ? sab + (int64_t)tid * ssam : sbt + (int64_t)((tid - TM) & 1) * ssbn;
-  const int64_t steps = tid < TM ? ssak : ssbk;
   const bool has_s = tid < TM + 2;
-
+  const uint32_t offS = tid < TM ? (uint32_t)(tid * ssam * 4) : (uint32_t)(((tid - TM) & 1) * ssbn * 4);
+  const uint8_t* sbase = reinterpret_cast<const uint8_t*>(wave < 4 ? sab : sbt);  // uniform
+  const int64_t steps = (wave < 4 ? ssak : ssbk) * 4;
   // staging registers for half a K block: the 4 A chunks, later the 4 B chunks + scale
   uint4 r0v, r1v, r2v, r3v;
   float rs = 0.0f;
 #define CIN_LOAD_A(kb)                                                                      \
   do {                                                                                      \
-    const int64_t ko = (int64_t)(kb) * TK;                                                  \
-    r0v = *reinterpret_cast<const uint4*>(ga + ko);                                         \
-    r1v = *reinterpret_cast<const uint4*>(ga + stepa + ko);                                 \
-    r2v = *reinterpret_cast<const uint4*>(ga + 2 * stepa + ko);                             \
-    r3v = *reinterpret_cast<const uint4*>(ga + 3 * stepa + ko);                             \
+    const uint8_t* base = Ab + (int64_t)(kb) * TK;                                          \
+    r0v = *reinterpret_cast<const uint4*>(base + offA);                                     \
+    r1v = *reinterpret_cast<const uint4*>(base + stepa + offA);                             \
+    r2v = *reinterpret_cast<const uint4*>(base + 2 * stepa + offA);                         \
+    r3v = *reinterpret_cast<const uint4*>(base + 3 * stepa + offA);                         \
   } while (0)
 #define CIN_LOAD_B(kb)                                                                      \
   do {                                                                                      \
-    const int64_t ko = (int64_t)(kb) * TK;                                                  \
-    r0v = *reinterpret_cast<const uint4*>(gb + ko);                                         \
-    r1v = *reinterpret_cast<const uint4*>(gb + stepb + ko);                                 \
-    r2v = *reinterpret_cast<const uint4*>(gb + 2 * stepb + ko);                             \
-    r3v = *reinterpret_cast<const uint4*>(gb + 3 * stepb + ko);                             \
-    if (has_s) rs = gs[(int64_t)(kb) * steps];                                              \
+    const uint8_t* base = Bb + (int64_t)(kb) * TK;                                          \
+    r0v = *reinterpret_cast<const uint4*>(base + offB);                                     \
+    r1v = *reinterpret_cast<const uint4*>(base + stepb + offB);                             \
+    r2v = *reinterpret_cast<const uint4*>(base + 2 * stepb + offB);                         \
+    r3v = *reinterpret_cast<const uint4*>(base + 3 * stepb + offB);                         \
+    if (has_s) rs = *reinterpret_cast<const float*>(sbase + (int64_t)(kb) * steps + offS);  \
   } while (0)
 #define CIN_STORE(arr, i, rv, st)                                                           \
   *reinterpret_cast<uint4*>(__builtin_assume_aligned(&sm.arr[st][((i) * kThreads + tid) * 16], 16)) = rv
@@ -434,21 +429,20 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm_fp8_bs_256(
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int m = wm * 128 + i * 16 + l16;
-    if (m < skip_m) continue;
-    const int64_t crow = m0 + m;
+    if (m < T.row_lo || m >= T.row_hi) continue;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int n = wn * 64 + j * 16 + kq * 4;
-      if (n < skip_n) continue;
+      if (n < T.col_lo) continue;
       if (c_dtype == CIN_DT_F32) {
-        float* cp = static_cast<float*>(C) + crow * ldc + n0 + n;
+        float* cp = static_cast<float*>(T.C) + (int64_t)m * ldc + n;
         if ((((uintptr_t)cp) & 15) == 0) {
           *reinterpret_cast<float4*>(cp) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
         } else {
           for (int r = 0; r < 4; ++r) cp[r] = acc[i][j][r];
         }
       } else {
-        uint16_t* cp = static_cast<uint16_t*>(C) + crow * ldc + n0 + n;
+        uint16_t* cp = static_cast<uint16_t*>(T.C) + (int64_t)m * ldc + n;
         const uint32_t b0 = f32_to_bf16_bits(acc[i][j][0]), b1 = f32_to_bf16_bits(acc[i][j][1]);
         const uint32_t b2 = f32_to_bf16_bits(acc[i][j][2]), b3 = f32_to_bf16_bits(acc[i][j][3]);
         if ((((uintptr_t)cp) & 7) == 0) {
@@ -459,6 +453,82 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm_fp8_bs_256(
       }
     }
   }
+}
+
+// XCD-aware order: workgroup b runs on XCD b % 8; give each XCD a contiguous run of
+// tile ids (n fastest) so its CUs share A row panels and B in their L2.
+__device__ inline uint32_t xcd_remap(uint32_t b, uint32_t G) {
+  const uint32_t Gfull = G & ~7u;
+  return b < Gfull ? (b & 7u) * (Gfull >> 3) + (b >> 3) : b;
+}
+
+// Every tile is a full block inside the operands (M, N >= 256, N % 128 == 0): the
+// last tile of a row/column shifts back onto its neighbour and stores only the
+// rows/columns its neighbour does not.
+__global__ __launch_bounds__(kThreads, 2) void k_gemm_fp8_bs_256(
+    const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
+    int64_t ssak, const uint8_t* __restrict__ B, int64_t ldb, const float* __restrict__ sb,
+    int64_t ssbn, int64_t ssbk, int64_t M, int64_t N, int64_t K, void* C, int c_dtype,
+    int64_t ldc, uint32_t tiles_m, uint32_t tiles_n) {
+  const uint32_t b = xcd_remap(blockIdx.x, tiles_m * tiles_n);
+  const uint32_t tm = b / tiles_n, tn = b - tm * tiles_n;
+  const int64_t m_nom = (int64_t)tm * TM, n_nom = (int64_t)tn * TN;
+  const int64_t m0 = m_nom + TM <= M ? m_nom : M - TM;
+  const int64_t n0 = n_nom + TN <= N ? n_nom : N - TN;
+  const size_t es = c_dtype == CIN_DT_F32 ? 4 : 2;
+  Tile t;
+  t.A = A + m0 * lda;
+  t.sa = sa + m0 * ssam;
+  t.B = B + n0 * ldb;
+  t.sb = sb + (n0 >> 7) * ssbn;
+  t.C = static_cast<uint8_t*>(C) + (m0 * ldc + n0) * es;
+  t.row_lo = (int)(m_nom - m0);
+  t.row_hi = TM;
+  t.col_lo = (int)(n_nom - n0);
+  tile_body(t, lda, ssam, ssak, ldb, ssbn, ssbk, K, c_dtype, ldc);
+}
+
+// Grouped: tile id -> (expert, 256-row tile of the expert, n tile) through a scan of
+// the device-side expert ranges; ids past the last tile exit before any barrier.  A
+// tile that would run past the token range (T >= 256) shifts back; rows outside its
+// expert's range are computed but not stored.
+__global__ __launch_bounds__(kThreads, 2) void k_grouped_gemm_fp8_256(
+    const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
+    int64_t ssak, const uint8_t* __restrict__ B, int64_t sbe, int64_t ldb,
+    const float* __restrict__ sb, int64_t ssbe, int64_t ssbn, int64_t ssbk,
+    const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t E, int64_t Tn,
+    int64_t N, int64_t K, void* C, int c_dtype, int64_t ldc, uint32_t tiles_n, uint32_t max_tiles) {
+  const uint32_t b = xcd_remap(blockIdx.x, max_tiles * tiles_n);
+  const uint32_t tile = b / tiles_n, tn = b - tile * tiles_n;
+  int64_t acc_tiles = 0, e = -1, r_nom = 0, r_end = 0;
+  for (int64_t x = 0; x < E; ++x) {
+    int64_t s0 = starts[x], s1 = ends[x];
+    if (s0 < 0) s0 = 0;
+    if (s1 > Tn) s1 = Tn;
+    const int64_t nt = s1 > s0 ? cdiv(s1 - s0, TM) : 0;
+    if ((int64_t)tile < acc_tiles + nt) {
+      e = x;
+      r_nom = s0 + ((int64_t)tile - acc_tiles) * TM;
+      r_end = s1;
+      break;
+    }
+    acc_tiles += nt;
+  }
+  if (e < 0) return;
+  const int64_t m0 = r_nom + TM <= Tn ? r_nom : Tn - TM;
+  const int64_t n_nom = (int64_t)tn * TN;
+  const int64_t n0 = n_nom + TN <= N ? n_nom : N - TN;
+  const size_t es = c_dtype == CIN_DT_F32 ? 4 : 2;
+  Tile t;
+  t.A = A + m0 * lda;
+  t.sa = sa + m0 * ssam;
+  t.B = B + e * sbe + n0 * ldb;
+  t.sb = sb + e * ssbe + (n0 >> 7) * ssbn;
+  t.C = static_cast<uint8_t*>(C) + (m0 * ldc + n0) * es;
+  t.row_lo = (int)(r_nom - m0);
+  t.row_hi = (int)((r_end - m0) < TM ? (r_end - m0) : TM);
+  t.col_lo = (int)(n_nom - n0);
+  tile_body(t, lda, ssam, ssak, ldb, ssbn, ssbk, K, c_dtype, ldc);
 }
 
 }  // namespace big
@@ -520,6 +590,16 @@ int cin_grouped_gemm_fp8(const uint8_t* A, int64_t lda, const float* sa, int64_t
                     aligned16(A) && aligned16(B),
                 "grouped_gemm_fp8: A/B rows must be 16-byte aligned and K-contiguous");
   CIN_CHECK_ARG(ldc >= N, "grouped_gemm_fp8: bad C stride");
+  if (K % big::TK == 0 && T >= big::TM && N >= big::TN && N % 128 == 0) {
+    const int64_t mt = cdiv(T, big::TM) + E;
+    const uint32_t tn = (uint32_t)cdiv(N, big::TN);
+    CIN_CHECK_ARG(mt * tn < ((int64_t)1 << 31), "grouped_gemm_fp8: grid too large");
+    hipLaunchKernelGGL(big::k_grouped_gemm_fp8_256, (unsigned)(mt * tn), big::kThreads, 0,
+                       static_cast<hipStream_t>(stream), A, lda, sa, ssam, ssak, B, sbe, ldb, sb,
+                       ssbe, ssbn, ssbk, starts, ends, E, T, N, K, C, c_dtype, ldc, tn,
+                       (uint32_t)mt);
+    return cin_check_launch("grouped_gemm_fp8");
+  }
   const int64_t max_tiles = cdiv(T, BM) + E;
   const uint32_t ntn = (uint32_t)cdiv(N, BN);
   CIN_CHECK_ARG(max_tiles * ntn < ((int64_t)1 << 31), "grouped_gemm_fp8: grid too large");
