@@ -35,8 +35,11 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w"], default=None,
+    p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "moe_gateup", "moe_down",
+                                      "dual_quant", "requant", "dgrad", "wgrad", "copy"], default=None,
                    help="run only one kernel in a loop (for profiler runs)")
+    p.add_argument("--no-extra", action="store_true",
+                   help="skip the config-3 (MoE) and config-4 (backward) component timings")
     return p.parse_args()
 
 
@@ -105,6 +108,60 @@ def cpu_baseline():
     }
 
 
+def measured_traffic(profile="profiles/k_gemm_fp8_bs_256_config2_fwd.txt"):
+    """HBM bytes per GEMM launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    (copy-calibrated); None if the summary is absent."""
+    path = os.path.join(ROOT, profile)
+    try:
+        for line in open(path):
+            if "total" in line and "MB" in line:
+                return int(float(line.rsplit("total", 1)[1].split("MB")[0]) * 1e6), profile
+    except OSError:
+        pass
+    return None, None
+
+
+def moe_setup(dev):
+    """Config 3: 32 experts, d_model 7168, expert hidden 2048, 16384 tokens, top-8 routing
+    with Zipf(1.1) expert popularity (sampled without replacement), bf16 ~N(0,1)
+    activations and ~N(0,0.02) weights.  Large operands come from the GPU generator."""
+    import torch
+
+    from cinnamon_amd import kernels
+
+    E, D, H, T, topk = 32, 7168, 2048, 16384, 8
+    g = torch.Generator(device=dev).manual_seed(3)
+    p = torch.tensor([(e + 1) ** -1.1 for e in range(E)], device=dev)
+    sel = torch.multinomial(p.expand(T, E), topk, replacement=False, generator=g)
+    counts = torch.bincount(sel.reshape(-1), minlength=E)
+    ends = counts.cumsum(0)
+    starts = ends - counts
+    A = T * topk
+    x = torch.randn(A, D, device=dev, generator=g).to(torch.bfloat16)
+    h = torch.randn(A, H, device=dev, generator=g).to(torch.bfloat16)
+    w12 = (torch.randn(E * 2 * H, D, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    w3 = (torch.randn(E * D, H, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    w12q, w12s = kernels.quantize_fp8_blockwise(w12)
+    w3q, w3s = kernels.quantize_fp8_blockwise(w3)
+    del w12, w3
+    return dict(E=E, D=D, H=H, A=A, x=x, h=h, starts=starts, ends=ends, counts=counts,
+                w12q=w12q.view(E, 2 * H, D), w12s=w12s.view(E, 2 * H // 128, D // 128),
+                w3q=w3q.view(E, D, H), w3s=w3s.view(E, D // 128, H // 128))
+
+
+def bwd_setup(dev, xs0, w0):
+    """Config 4: backward of the config-2 shapes; dY[8192, 2048] bf16 ~N(0, 1e-3)."""
+    import torch
+
+    from cinnamon_amd import kernels
+
+    g = torch.Generator(device=dev).manual_seed(4)
+    dy = (torch.randn(M, N, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
+    xq, xs = kernels.quantize_fp8_rowwise(xs0)
+    _, wqt, ws = kernels.quantize_fp8_blockwise_t(w0.float(), with_rowmajor=False)
+    return dict(dy=dy, xq=xq, xs=xs, wqt=wqt, ws=ws)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -146,8 +203,54 @@ def main():
     def quant_w(i):
         kernels.quantize_fp8_blockwise(ws[i % nbuf])
 
+    from cinnamon_amd import layers
+
+    moe = bwd = None
+    full = args.only is None and not args.no_extra
+    if full or (args.only or "").startswith("moe"):
+        moe = moe_setup(dev)
+        hq, hs = kernels.quantize_fp8_rowwise(moe["h"])
+        xq3, xs3 = kernels.quantize_fp8_rowwise(moe["x"])
+        y12 = torch.empty((moe["A"], 2 * moe["H"]), dtype=torch.bfloat16, device=dev)
+        y3 = torch.empty((moe["A"], moe["D"]), dtype=torch.bfloat16, device=dev)
+
+    def moe_gateup(i):
+        layers.fp8_grouped_gemm(xq3, xs3, moe["w12q"], moe["w12s"], moe["starts"], moe["ends"], out=y12)
+
+    def moe_down(i):
+        layers.fp8_grouped_gemm(hq, hs, moe["w3q"], moe["w3s"], moe["starts"], moe["ends"], out=y3)
+
+    if full or args.only in ("dual_quant", "requant", "dgrad", "wgrad"):
+        bwd = bwd_setup(dev, xs[0], ws[0])
+        gq, gs, gqt, gst = kernels.quantize_fp8_dual(bwd["dy"])
+        xbt, xbs = kernels.requantize_rowwise_to_blockwise(bwd["xq"], bwd["xs"], transposed=True)
+        dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+        dw = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+
+    def dual_quant(i):
+        kernels.quantize_fp8_dual(bwd["dy"])
+
+    def requant(i):
+        kernels.requantize_rowwise_to_blockwise(bwd["xq"], bwd["xs"], transposed=True)
+
+    def dgrad(i):
+        kernels.fp8_gemm_bs(gq, gs, bwd["wqt"], bwd["ws"].t(), torch.bfloat16, out=dx)
+
+    def wgrad(i):
+        kernels.fp8_gemm_bs(gqt, gst, xbt, xbs.t(), torch.bfloat16, out=dw)
+
+    if args.only == "copy":
+        # calibration for HBM byte counters: a plain copy of 512 MiB (read 512 MiB, write 512 MiB)
+        src = torch.empty(256 * 1024 * 1024, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        us = time_loop(lambda i: dst.copy_(src), args.steps, args.warmup)
+        print(json.dumps({"only": "copy", "bytes_read": src.numel() * 2, "bytes_written": src.numel() * 2,
+                          "us_per_call": us}))
+        return
     if args.only:
-        fn = {"step": step, "gemm": gemm, "quant_x": quant_x, "quant_w": quant_w}[args.only]
+        fn = {"step": step, "gemm": gemm, "quant_x": quant_x, "quant_w": quant_w,
+              "moe_gateup": moe_gateup, "moe_down": moe_down, "dual_quant": dual_quant,
+              "requant": requant, "dgrad": dgrad, "wgrad": wgrad}[args.only]
         us = time_loop(fn, args.steps, args.warmup)
         print(json.dumps({"only": args.only, "us_per_call": us}))
         return
@@ -191,8 +294,9 @@ def main():
             "peak": PEAK_FP8_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops / PEAK_FP8_TFLOPS, 4),
-            "traffic": None,
-            "kernel": "k_gemm_fp8_bs",
+            "traffic": measured_traffic()[0],
+            "traffic_source": measured_traffic()[1],
+            "kernel": "k_gemm_fp8_bs_256",
             "algorithmic_work": "2*M*N*K = %.4g FLOP per launch" % flops,
         },
         "components": {
@@ -205,6 +309,36 @@ def main():
                                   "frac_of_hbm": round(qw_gbps / PEAK_HBM_GBPS, 4), "bytes": qw_bytes},
         },
     }
+    if moe is not None:
+        A, D, H = moe["A"], moe["D"], moe["H"]
+        gu_us = time_loop(moe_gateup, 10, 2)
+        dn_us = time_loop(moe_down, 10, 2)
+        gu_fl, dn_fl = 2.0 * A * D * 2 * H, 2.0 * A * H * D
+        out["components"]["config3_moe_forward"] = {
+            "tokens": 16384, "topk": 8, "rows": A, "experts": moe["E"],
+            "expert_rows_max": int(moe["counts"].max()), "expert_rows_min": int(moe["counts"].min()),
+            "gate_up": {"us": round(gu_us, 1), "tflops": round(gu_fl / gu_us / 1e6, 1),
+                        "frac_of_fp8_peak": round(gu_fl / gu_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
+            "down": {"us": round(dn_us, 1), "tflops": round(dn_fl / dn_us / 1e6, 1),
+                     "frac_of_fp8_peak": round(dn_fl / dn_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
+        }
+    if bwd is not None:
+        dq_us = time_loop(dual_quant, 20, 3)
+        rq_us = time_loop(requant, 20, 3)
+        dg_us = time_loop(dgrad, 20, 3)
+        wg_us = time_loop(wgrad, 20, 3)
+        dq_bytes = M * N * 2 + 2 * M * N + 4 * (M * (N // 128) + N * (M // 128))
+        rq_bytes = M * K + M * (K // 128) * 4 + K * M + (M // 128) * (K // 128) * 4
+        out["components"]["config4_backward"] = {
+            "dual_quant_dy": {"us": round(dq_us, 2), "gbps": round(dq_bytes / dq_us / 1e3, 1),
+                              "frac_of_hbm": round(dq_bytes / dq_us / 1e3 / PEAK_HBM_GBPS, 4)},
+            "requant_x_block_t": {"us": round(rq_us, 2), "gbps": round(rq_bytes / rq_us / 1e3, 1),
+                                  "frac_of_hbm": round(rq_bytes / rq_us / 1e3 / PEAK_HBM_GBPS, 4)},
+            "dgrad": {"us": round(dg_us, 1), "tflops": round(flops / dg_us / 1e6, 1),
+                      "frac_of_fp8_peak": round(flops / dg_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
+            "wgrad": {"us": round(wg_us, 1), "tflops": round(flops / wg_us / 1e6, 1),
+                      "frac_of_fp8_peak": round(flops / wg_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
+        }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))
