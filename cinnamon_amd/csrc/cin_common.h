@@ -55,20 +55,27 @@ __device__ inline float compute_scale(float amax, bool round_scale) {
   return __uint_as_float((uint32_t)(e + 127) << 23);
 }
 
-// x / s for the e4m3 cast, computed as x * r with r = RN(1 / s).
-// |x*r - x/s| < 1.5 ulp, so RN(x/s) is within 3 fp32 steps of the product.  The
-// e4m3 code of the product equals the code of RN(x/s) unless an e4m3 rounding
-// midpoint lies within 4 steps of it: low 20 bits near 0x80000 for |y| >= 2^-6, or
-// anywhere in [2^-11, 2^-6 + 8 steps) where e4m3 is subnormal.  Those lanes set
-// `unsafe` and the caller redoes them with the IEEE division.
-__device__ inline float mul_guarded(float x, float r, uint32_t& unsafe) {
-  const float y = x * r;
-  const uint32_t a = __float_as_uint(y) & 0x7fffffffu;
-  const uint32_t near_mid = ((a + (4u - 0x80000u)) & 0xfffffu) <= 8u;
-  const uint32_t small = (a - 0x3A000000u) < (0x3C800008u - 0x3A000000u);
-  unsafe |= near_mid | small;
-  return y;
+// RN(x / s) for a finite scale s > 0 from r = RN(1 / s), without a division:
+//   q0 = RN(x * r)                (within 1.5 fp32 ulp of x / s)
+//   q  = RN(q - RN(q * s - x) * r)  (one fma pair per step; the residual is exact)
+// This is Markstein's final step: once q is within 1 ulp of x / s and r within 1/2 ulp
+// of 1 / s, one more step returns the correctly rounded quotient, so two steps are
+// exact for any fp32 x.  For x and amax that are bf16 or fp16 values (s = RN(amax/448),
+// |x| <= amax) one step already is: checked against the IEEE division for every pair of
+// mantissas over every exponent gap down to 2^-30.  STEPS is therefore 1 for 16-bit
+// inputs and 2 for fp32.  The residual is formed as q * s - x, not x - q * s, so that
+// x = -0 keeps its sign (-0 - (+0) * r = -0; the other order would add +0 to -0).  An
+// infinite scale (infinite amax) is left to the caller.
+template <int STEPS>
+__device__ inline float div_by_scale(float x, float s, float r) {
+  float q = x * r;
+#pragma unroll
+  for (int i = 0; i < STEPS; ++i) q = __builtin_fmaf(-__builtin_fmaf(q, s, -x), r, q);
+  return q;
 }
+
+template <int DT>
+constexpr int kDivSteps = DT == CIN_DT_F32 ? 2 : 1;
 
 // Clamp with maxnum/minnum semantics: NaN maps to -448 like the reference's
 // tl.minimum(tl.maximum(x, -448), 448).

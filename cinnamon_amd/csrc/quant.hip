@@ -81,14 +81,16 @@ __device__ inline float row8_max(float v) {
   return v;
 }
 
-// Quantize n (multiple of 4) values with scale s / reciprocal r into packed codes.
-template <int NV>
+// Quantize NV (multiple of 4) values with scale s / reciprocal r into packed codes.
+// STEPS = correction steps of div_by_scale (1 for bf16/fp16 tiles, 2 for fp32).
+template <int NV, int STEPS>
 __device__ inline void quant_vals(const float (&v)[NV], float s, float r, uint32_t (&out)[NV / 4]) {
   float y[NV];
-  uint32_t unsafe = 0;
+  if (s < __builtin_inff()) {
 #pragma unroll
-  for (int i = 0; i < NV; ++i) y[i] = mul_guarded(v[i], r, unsafe);
-  if (unsafe) {
+    for (int i = 0; i < NV; ++i) y[i] = div_by_scale<STEPS>(v[i], s, r);
+  } else {
+    // infinite amax: x / inf is a signed zero, inf / inf NaN
 #pragma unroll
     for (int i = 0; i < NV; ++i) y[i] = v[i] / s;
   }
@@ -103,7 +105,7 @@ __device__ inline void quant_vals(const float (&v)[NV], float s, float r, uint32
 // tile chunk c * LANES + i so every load instruction reads whole 16*LANES-byte runs.
 // A group walks tiles t, t + G, ... keeping U tiles in flight; (row, tile) advance
 // incrementally instead of by division.
-template <int DT, int LANES, int U>
+template <int DT, int LANES, int U, bool FULL>
 __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict__ x, int64_t N,
                                                          int64_t sxm, int round_scale,
                                                          uint8_t* __restrict__ q, int64_t sqm,
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict_
         const int64_t col = (int64_t)cb * 128 + e0;
         int64_t nv = live ? N - col : 0;
         nv = nv < 0 ? 0 : (nv > EPC ? EPC : nv);
-        if (nv == EPC) {
+        if (FULL || nv == EPC) {
           if constexpr (DT == CIN_DT_F32) {
             const f32x4 w = __builtin_nontemporal_load(
                 reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + base + e0));
@@ -183,13 +185,13 @@ __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict_
       a = fmaxf(a, floor_v);
       const float s = compute_scale(a, rs);
       uint32_t codes[EPL / 4];
-      quant_vals<EPL>(v[u], s, 1.0f / s, codes);
+      quant_vals<EPL, kDivSteps<DT>>(v[u], s, 1.0f / s, codes);
       uint8_t* qrow = q + (int64_t)rows[u] * sqm + (int64_t)cbs[u] * 128;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int64_t e0 = (int64_t)(c * LANES + li) * EPC;
         const int64_t col = (int64_t)cbs[u] * 128 + e0;
-        if (col + EPC <= N) {
+        if (FULL || col + EPC <= N) {
           if constexpr (EPC == 8)
             *reinterpret_cast<uint2*>(qrow + e0) = make_uint2(codes[2 * c], codes[2 * c + 1]);
           else
@@ -205,21 +207,31 @@ __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict_
   }
 }
 
+template <int LANES, int U, bool FULL>
+void launch_rowwise128_t(const void* x, int dt, int64_t N, int64_t sxm, int rs, uint8_t* q,
+                         int64_t sqm, float* sc, int64_t ssm, uint32_t nb, uint32_t ntiles,
+                         unsigned grid, hipStream_t st) {
+  if (dt == CIN_DT_BF16)
+    hipLaunchKernelGGL((k_rowwise128<CIN_DT_BF16, LANES, U, FULL>), grid, kThreads, 0, st, x, N,
+                       sxm, rs, q, sqm, sc, ssm, nb, ntiles);
+  else if (dt == CIN_DT_F16)
+    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F16, LANES, U, FULL>), grid, kThreads, 0, st, x, N,
+                       sxm, rs, q, sqm, sc, ssm, nb, ntiles);
+  else
+    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F32, LANES, U, FULL>), grid, kThreads, 0, st, x, N,
+                       sxm, rs, q, sqm, sc, ssm, nb, ntiles);
+}
+
 template <int LANES, int U>
 void launch_rowwise128(const void* x, int dt, int64_t M, int64_t N, int64_t sxm, int rs,
                        uint8_t* q, int64_t sqm, float* sc, int64_t ssm, int64_t nb, int gridcap,
                        hipStream_t st) {
   const uint32_t ntiles = (uint32_t)(M * nb);
   const unsigned grid = grid_for(ntiles, (kThreads / LANES) * U, gridcap);
-  if (dt == CIN_DT_BF16)
-    hipLaunchKernelGGL((k_rowwise128<CIN_DT_BF16, LANES, U>), grid, kThreads, 0, st, x, N, sxm, rs,
-                       q, sqm, sc, ssm, (uint32_t)nb, ntiles);
-  else if (dt == CIN_DT_F16)
-    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F16, LANES, U>), grid, kThreads, 0, st, x, N, sxm, rs,
-                       q, sqm, sc, ssm, (uint32_t)nb, ntiles);
+  if (N % 128 == 0)
+    launch_rowwise128_t<LANES, U, true>(x, dt, N, sxm, rs, q, sqm, sc, ssm, (uint32_t)nb, ntiles, grid, st);
   else
-    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F32, LANES, U>), grid, kThreads, 0, st, x, N, sxm, rs,
-                       q, sqm, sc, ssm, (uint32_t)nb, ntiles);
+    launch_rowwise128_t<LANES, U, false>(x, dt, N, sxm, rs, q, sqm, sc, ssm, (uint32_t)nb, ntiles, grid, st);
 }
 
 // Generic row-wise: one wave per (row, tile), any block size / strides / dtype.
@@ -324,7 +336,7 @@ __global__ __launch_bounds__(kThreads) void k_blockwise128(const void* __restric
   const float rcp = 1.0f / s;
   uint32_t codes[8][2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) quant_vals<8>(d[i].v, s, rcp, codes[i]);
+  for (int i = 0; i < 8; ++i) quant_vals<8, kDivSteps<DT>>(d[i].v, s, rcp, codes[i]);
   if (q) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -413,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x
     a = fmaxf(a, floor_v);
     const float sr = compute_scale(a, rs);
     uint32_t c2[2];
-    quant_vals<8>(d[i].v, sr, 1.0f / sr, c2);
+    quant_vals<8, kDivSteps<DT>>(d[i].v, sr, 1.0f / sr, c2);
     const uint32_t lo = c2[0], hi = c2[1];
     if (r < M) {
       uint8_t* qp = q + r * sqm + c;
@@ -447,7 +459,7 @@ __global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x
 #pragma unroll
     for (int i = 0; i < 8; ++i) col[i] = d[i].v[j];
     uint32_t c2[2];
-    quant_vals<8>(col, sc, 1.0f / sc, c2);
+    quant_vals<8, kDivSteps<DT>>(col, sc, 1.0f / sc, c2);
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * i] = (uint8_t)((c2[i >> 2] >> (8 * (i & 3))) & 0xffu);
@@ -524,7 +536,7 @@ __global__ __launch_bounds__(kThreads) void k_requant128(const uint8_t* __restri
   const float rcp = 1.0f / s;
   uint32_t codes[8][2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) quant_vals<8>(v[i], s, rcp, codes[i]);
+  for (int i = 0; i < 8; ++i) quant_vals<8, 2>(v[i], s, rcp, codes[i]);
   if (qb) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -643,7 +655,7 @@ int cin_quant_rowwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
   const bool fast = block == 128 && sxn == 1 && aligned(x, 16) && ((sxm * es) % 16 == 0) &&
                     aligned(q, 8) && (sqm % 8 == 0) && M * nb < (int64_t)1 << 31;
   if (fast) {
-    launch_rowwise128<16, 4>(x, x_dtype, M, N, sxm, round_scale, q, sqm, scales, ssm, nb, 8192, s);
+    launch_rowwise128<8, 1>(x, x_dtype, M, N, sxm, round_scale, q, sqm, scales, ssm, nb, 16384, s);
   } else {
     const unsigned grid = grid_for(M * nb, kThreads / 64, 65536);
     hipLaunchKernelGGL(k_rowwise_generic, grid, kThreads, 0, s, x, x_dtype, M, N, sxm, sxn, block,

@@ -97,6 +97,8 @@ def test_rowwise_special_tiles(kern, dev, dtype):
     x[4, 0] = -float("inf")
     x[5, 400:512] = float("nan")
     x[6, 7] = 3.0e38 if dtype == torch.float32 else 1e4
+    x[7, :64] = -0.0                        # signed zeros keep their sign (code 0x80)
+    x[7, 256:384:2] = -0.0
     x = x.to(dtype)
     q, s = kern.quantize_fp8_rowwise(x.to(dev))
     rq, rs_ = orc.quant_rowwise(x)
@@ -140,6 +142,44 @@ def test_blockwise_bit_exact(kern, dev, shape, dtype, std):
     _assert_codes_equal(q2, rq, "block codes (dual layout)")
     _assert_codes_equal(qt, rq.view(torch.uint8).t().contiguous(), "transposed block codes")
     _assert_scales_equal(s2, rs_, "block scales (dual layout)")
+
+
+@pytest.mark.parametrize("bm,bn,rs", [(64, 64, False), (128, 1, False), (1, 128, True), (32, 256, True)])
+def _special_matrix(M, N, dtype, seed):
+    x = torch.randn(M, N, generator=torch.Generator().manual_seed(seed))
+    x[:, 0] = -0.0
+    x[5, :] = -0.0
+    x[:128, 128:256] = 0.0                   # zero block -> floor
+    x[130, 131] = float("nan")
+    x[200, 300] = float("inf")
+    x[3, 260:270] = -0.0
+    x[140:150, 140:150] *= 1e-7
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+def test_special_values_block_dual_requant(kern, dev, dtype):
+    x = _special_matrix(256, 384, dtype, seed=8)
+    q, s = kern.quantize_fp8_blockwise(x.to(dev))
+    rq, rs_ = orc.quant_blockwise(x)
+    _assert_codes_equal(q, rq, f"special block codes {dtype}")
+    _assert_scales_equal(s, rs_, f"special block scales {dtype}")
+    q, s, qt, st = kern.quantize_fp8_dual(x.to(dev))
+    rq, rs_ = orc.quant_rowwise(x)
+    rqt, rst = orc.quant_rowwise(x.t().contiguous())
+    _assert_codes_equal(q, rq, "special dual row codes")
+    _assert_scales_equal(s, rs_, "special dual row scales")
+    _assert_codes_equal(qt, rqt, "special dual transposed codes")
+    _assert_scales_equal(st, rst, "special dual transposed scales")
+    # row-wise codes with signed zeros through the re-quantization (NaN/inf excluded:
+    # the reference's requantization takes finite row-wise codes)
+    xf = x.float().nan_to_num(0.0, 0.0, 0.0).to(dtype)
+    xf[:, 0] = -0.0
+    a, sa = orc.quant_rowwise(xf)
+    qb, sb = kern.requantize_rowwise_to_blockwise(a.to(dev), sa.to(dev))
+    rqb, rsb = orc.quant_blockwise(orc.dequant_rowwise(a, sa))
+    _assert_codes_equal(qb, rqb, "special requant codes")
+    _assert_scales_equal(sb, rsb, "special requant scales")
 
 
 @pytest.mark.parametrize("bm,bn,rs", [(64, 64, False), (128, 1, False), (1, 128, True), (32, 256, True)])

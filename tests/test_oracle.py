@@ -229,43 +229,104 @@ def test_grouped_oracle_e1_equals_dense():
 
 
 # ---------------------------------------------------------------------------
-# The HIP quantizers compute x / s as x * RN(1/s) and fall back to the IEEE division
-# only for lanes flagged near an e4m3 rounding boundary (cin_common.h mul_guarded).
-# Check that rule on the CPU: whenever a product is not flagged, its e4m3 code equals
-# the code of the correctly rounded quotient — on random and on adversarial inputs
-# placed next to every e4m3 midpoint.
+# The HIP quantizers compute x / s without a division: q = RN(x * r), r = RN(1/s),
+# then STEPS corrections q = fma(-fma(q, s, -x), r, q) (cin_common.h div_by_scale),
+# one step for bf16/fp16 inputs and two for fp32.  Check on the CPU that this equals
+# the IEEE quotient: exhaustively over bf16 mantissa pairs, on a large fp16 sample and
+# on random plus midpoint-planted fp32 inputs.  The fp32 fma is emulated with one
+# rounding in float64 (TwoSum + midpoint fix-up), itself checked against exact
+# rational arithmetic.
 # ---------------------------------------------------------------------------
-def _guard_flags(y):
-    a = y.view(np.uint32) & np.uint32(0x7FFFFFFF)
-    near_mid = ((a + np.uint32((4 - 0x80000) & 0xFFFFFFFF)) & np.uint32(0xFFFFF)) <= 8
-    small = (a - np.uint32(0x3A000000)) < np.uint32(0x3C800008 - 0x3A000000)
-    return near_mid | small
+def _fma32(a, b, c):
+    a, b, c = a.astype(np.float64), b.astype(np.float64), c.astype(np.float64)
+    p = a * b                                       # exact: 24 x 24 bits
+    hi = p + c
+    bb = hi - p
+    lo = (p - (hi - bb)) + (c - bb)                 # p + c == hi + lo exactly
+    f = hi.astype(np.float32)
+    fd = f.astype(np.float64)
+    nb = np.where(fd <= hi, np.nextafter(f, np.float32(np.inf)),
+                  np.nextafter(f, np.float32(-np.inf))).astype(np.float64)
+    lower, upper = np.minimum(fd, nb), np.maximum(fd, nb)
+    tie = (hi == (lower + upper) / 2) & (lo != 0)   # double rounding only on a tie
+    return np.where(tie, np.where(lo > 0, upper, lower), fd).astype(np.float32)
 
 
-def _codes(y):
-    y = np.minimum(np.maximum(y, np.float32(-448.0)), np.float32(448.0))
-    return orc.e4m3_rne_np(y)
+def _div_by_scale(x, s, r, steps):
+    q = (x * r).astype(np.float32)
+    for _ in range(steps):
+        q = _fma32(-_fma32(q, s, -x), r, q)
+    return q
 
 
-def test_guarded_reciprocal_multiply_matches_division():
+def test_fma32_emulation_is_single_rounding():
+    from fractions import Fraction
+    rng = np.random.default_rng(5)
+    n = 3000
+    a = (rng.standard_normal(n) * 2.0 ** rng.integers(-20, 20, n)).astype(np.float32)
+    b = (rng.standard_normal(n) * 2.0 ** rng.integers(-20, 20, n)).astype(np.float32)
+    # c close to -a*b so that cancellation and ties are exercised
+    c = np.where(rng.random(n) < 0.5, -(a.astype(np.float64) * b).astype(np.float32),
+                 rng.standard_normal(n).astype(np.float32))
+    got = _fma32(a, b, c)
+    for i in range(n):
+        exact = Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i]))
+        f = np.float32(float(exact))                # float() is correctly rounded to double
+        # correct rounding to fp32: pick the nearer of the two fp32 neighbours of exact
+        lo_ = f if Fraction(float(f)) <= exact else np.nextafter(f, np.float32(-np.inf))
+        hi_ = np.nextafter(lo_, np.float32(np.inf)) if Fraction(float(lo_)) != exact else lo_
+        dlo, dhi = exact - Fraction(float(lo_)), Fraction(float(hi_)) - exact
+        want = lo_ if (dlo < dhi or (dlo == dhi and (lo_.view(np.uint32) & 1) == 0)) else hi_
+        assert got[i] == want or (got[i] == 0 and want == 0), (a[i], b[i], c[i])
+
+
+def _mantissa_pairs(bits, gaps, rng=None, sample=None):
+    m = np.arange(1 << bits, 1 << (bits + 1), dtype=np.float64)
+    for d in gaps:
+        mx, ma = np.meshgrid(m, m, indexing="ij")
+        x, amax = (mx * 2.0 ** d).ravel(), ma.ravel()
+        if sample is not None:
+            k = rng.choice(x.size, sample, replace=False)
+            x, amax = x[k], amax[k]
+        keep = x <= amax
+        yield x[keep].astype(np.float32), amax[keep].astype(np.float32)
+
+
+@pytest.mark.parametrize("bits,sample", [(7, None), (10, 40000)])
+def test_division_free_quotient_16bit_inputs(bits, sample):
+    """bf16 (7 stored mantissa bits): every (x, amax) pair; fp16 (10 bits): a sample."""
+    rng = np.random.default_rng(bits)
+    for x, amax in _mantissa_pairs(bits, range(-30, 1), rng, sample):
+        s = (amax / np.float32(448.0)).astype(np.float32)
+        r = (np.float32(1.0) / s).astype(np.float32)
+        for xs in (x, -x):
+            assert np.array_equal(_div_by_scale(xs, s, r, 1), (xs / s).astype(np.float32))
+
+
+def test_division_free_quotient_fp32_inputs():
     rng = np.random.default_rng(123)
-    n = 4_000_000
+    n = 1_000_000
     amax = np.exp(rng.uniform(np.log(1e-4), np.log(1e30), n)).astype(np.float32)
     s = (amax / np.float32(448.0)).astype(np.float32)
     x = (amax * rng.uniform(-1, 1, n).astype(np.float32)).astype(np.float32)
-    # adversarial: quotients planted next to every e4m3 midpoint (+-6 fp32 steps)
-    grid = np.arange(0, 0x7F, dtype=np.uint8).view(np.uint8)
-    vals = torch.from_numpy(grid.copy()).view(torch.float8_e4m3fn).float().numpy()
+    # quotients planted on and next to every e4m3 rounding midpoint (+-6 fp32 steps)
+    vals = torch.arange(0, 0x7F, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
     mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2).astype(np.float32)
     k = np.arange(-6, 7, dtype=np.int64)
     planted = (mids.view(np.uint32)[:, None].astype(np.int64) + k[None, :]).astype(np.uint32).view(np.float32).ravel()
+    planted = np.tile(planted, 200)
     sp = s[: planted.size]
-    xp = (planted * sp).astype(np.float32)
+    xp = (planted.astype(np.float64) * sp).astype(np.float32)
     x = np.concatenate([x, xp, -xp])
     s = np.concatenate([s, sp, sp])
     r = (np.float32(1.0) / s).astype(np.float32)
-    y = (x * r).astype(np.float32)
     exact = (x / s).astype(np.float32)
-    safe = ~_guard_flags(y)
-    assert safe.mean() > 0.9
-    assert (_codes(y[safe]) == _codes(exact[safe])).all()
+    assert np.array_equal(_div_by_scale(x, s, r, 2), exact)
+    # signed zeros keep their sign (the reference maps -0 to code 0x80)
+    z = np.array([0.0, -0.0], dtype=np.float32)
+    for steps in (1, 2):
+        q = _div_by_scale(z, s[:2], r[:2], steps)
+        assert np.array_equal(np.signbit(q), [False, True])
+    # the bare product is not enough: without a correction step codes differ
+    y0 = (x * r).astype(np.float32)
+    assert not np.array_equal(y0, exact)
