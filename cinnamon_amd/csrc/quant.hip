@@ -138,7 +138,9 @@ __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict_
         const int64_t col = (int64_t)cb * 128 + e0;
         int64_t nv = live ? N - col : 0;
         nv = nv < 0 ? 0 : (nv > EPC ? EPC : nv);
-        if (FULL || nv == EPC) {
+        // FULL only drops the column check: a tile past ntiles (u > 0 on the last
+        // iteration) has nv == 0 and loads nothing.
+        if ((FULL && live) || nv == EPC) {
           if constexpr (DT == CIN_DT_F32) {
             const f32x4 w = __builtin_nontemporal_load(
                 reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + base + e0));
