@@ -249,12 +249,18 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_gemm_fp8(
 // ---------------------------------------------------------------------------
 namespace big {
 
-// Workgroup tile 256 x 256 x 128, 8 waves (2 per SIMD: one wave's MFMAs run while
-// the other issues its scale-FMAs), wave tile 128 (m) x 64 (n), two LDS stages.
-// Operands are staged global -> VGPR -> LDS: the loads of K block kb+1 are issued at
-// the start of block kb and written to the free stage in its second half.  (The
-// global_load_lds path moves only ~16 bytes per clock per CU on gfx950, half of what
-// the MFMAs consume here.)
+// Workgroup tile 256 x 256 x 128, 8 waves (2 per SIMD), wave tile 128 (m) x 64 (n), two
+// LDS stages.  Per K block a wave issues 32 MFMAs (8 m-tiles x 4 n-tiles) and, for each,
+// the 4 scale-FMAs of the MFMA three steps earlier: the partials live in a ring of 4
+// slots, so an FMA reads a result whose MFMA finished long ago and no wave ever waits on
+// its own MFMA.  The ring runs across K blocks (the FMAs of a block's last 3 MFMAs are
+// issued at the start of the next block).
+//
+// Operands are staged global -> VGPR -> LDS a whole K block ahead: the loads of block
+// kb+2 are issued right after the barrier of block kb, and written to the free stage
+// during block kb+1.  The barrier sits before the last m-tile group, so the fragments of
+// the next block are read while that group's MFMAs run.  (global_load_lds moved only
+// ~16 bytes per clock per CU on gfx950, half of what the MFMAs consume here.)
 constexpr int TM = 256, TN = 256, TK = 128;
 constexpr int kThreads = 512;
 constexpr int kTileBytes = TM * TK;  // 32 KB per operand per stage
@@ -262,9 +268,13 @@ constexpr int kTileBytes = TM * TK;  // 32 KB per operand per stage
 struct __attribute__((aligned(16))) Smem {
   uint8_t a[2][kTileBytes];
   uint8_t b[2][kTileBytes];
-  float sa[2][TM];
+  float sa[2][TM];  // A-row scales, row r at sa_slot(r)
   float sb[2][2];
 };
+
+// Row r = 128 wm + 16 i + l of the tile is stored at (wm, l, i): the lane (wm, l) finds
+// the scales of its 8 m-tiles in 32 contiguous bytes.
+__device__ inline int sa_slot(int r) { return (r >> 7) * 128 + (r & 15) * 8 + ((r >> 4) & 7); }
 
 // 16-byte chunk c of tile row r lives at slot c ^ f(r), f(r) = (r % 8) ^ ((r / 8) % 2):
 // the 8 rows a 32-bank LDS serves together, and the 8 same-parity rows a 64-bank LDS
@@ -279,6 +289,14 @@ __device__ inline v8i frag(const uint8_t* lds, int row, int kq) {
   v[0] = (int)lo.x; v[1] = (int)lo.y; v[2] = (int)lo.z; v[3] = (int)lo.w;
   v[4] = (int)hi.x; v[5] = (int)hi.y; v[6] = (int)hi.z; v[7] = (int)hi.w;
   return v;
+}
+
+// Raw buffer resource over [p, p + bytes): loads are an SGPR base plus a 32-bit lane
+// offset, and anything past `bytes` reads as zero.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+  const int64_t cap = 0xffffffffLL;
+  const uint32_t n = (uint32_t)(bytes < cap ? bytes : cap);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)n, 0x00020000);
 }
 
 // One full 256 x 256 tile.  A / sa point at the tile's first row, B / sb at its first
@@ -296,55 +314,59 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
                                           int64_t ldb, int64_t ssbn, int64_t ssbk, int64_t K,
                                           int c_dtype, int64_t ldc) {
   __shared__ Smem sm;
-  const uint8_t* Ab = T.A;
-  const uint8_t* Bb = T.B;
-  const float* sab = T.sa;
-  const float* sbt = T.sb;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
   const int l16 = lane & 15, kq = lane >> 4;
+  const int nk = (int)(K / TK);
 
   // Loads: round i covers tile rows i*64 .. i*64+63; thread tid fetches row
   // i*64 + tid/8, chunk (tid % 8) ^ swz_f(row) and stores it to slot i*512 + tid.
-  // Addresses are a wave-uniform base (row round, K block) plus a 32-bit lane offset.
   const int r0 = tid >> 3;
   const uint32_t q16 = (uint32_t)(((tid & 7) ^ swz_f(r0)) * 16);
   const uint32_t offA = (uint32_t)(r0 * lda) + q16;
   const uint32_t offB = (uint32_t)(r0 * ldb) + q16;
-  const int64_t stepa = 64 * lda, stepb = 64 * ldb;
+  const uint32_t stepa = (uint32_t)(64 * lda), stepb = (uint32_t)(64 * ldb);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(T.A, 255 * lda + K);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(T.B, 255 * ldb + K);
   // scales: threads 0-255 fetch the A-scale rows, 256-257 the tile's two B-block scales
+  // (threads 258-511 load one of the B scales too and drop it, so that every wave issues
+  // the same loads and the compiler's memory-counter waits stay exact)
   const bool has_s = tid < TM + 2;
   const uint32_t offS = tid < TM ? (uint32_t)(tid * ssam * 4) : (uint32_t)(((tid - TM) & 1) * ssbn * 4);
-  const uint8_t* sbase = reinterpret_cast<const uint8_t*>(wave < 4 ? sab : sbt);  // uniform
-  const int64_t steps = (wave < 4 ? ssak : ssbk) * 4;
-  // staging registers for half a K block: the 4 A chunks, later the 4 B chunks + scale
-  uint4 r0v, r1v, r2v, r3v;
-  float rs = 0.0f;
-#define CIN_LOAD_A(kb)                                                                      \
-  do {                                                                                      \
-    const uint8_t* base = Ab + (int64_t)(kb) * TK;                                          \
-    r0v = *reinterpret_cast<const uint4*>(base + offA);                                     \
-    r1v = *reinterpret_cast<const uint4*>(base + stepa + offA);                             \
-    r2v = *reinterpret_cast<const uint4*>(base + 2 * stepa + offA);                         \
-    r3v = *reinterpret_cast<const uint4*>(base + 3 * stepa + offA);                         \
+  const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(T.sa, (255 * ssam + (int64_t)(nk - 1) * ssak + 1) * 4);
+  const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(T.sb, (ssbn + (int64_t)(nk - 1) * ssbk + 1) * 4);
+  const uint32_t steps = (uint32_t)((wave < 4 ? ssak : ssbk) * 4);
+
+  // staging registers: 4 chunks of one operand of one K block (A, then B), and one scale
+  uint4 g0, g1, g2, g3;
+  float gs = 0.0f;
+#define CIN_LD(rsrc, off, so) __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, so, 0))
+#define CIN_LOAD_A(kb)                                                                        \
+  do {                                                                                        \
+    const uint32_t ko = (uint32_t)(kb) * TK;                                                  \
+    g0 = CIN_LD(ra, offA, ko);                                                                \
+    g1 = CIN_LD(ra, offA, ko + stepa);                                                        \
+    g2 = CIN_LD(ra, offA, ko + 2 * stepa);                                                    \
+    g3 = CIN_LD(ra, offA, ko + 3 * stepa);                                                    \
   } while (0)
-#define CIN_LOAD_B(kb)                                                                      \
-  do {                                                                                      \
-    const uint8_t* base = Bb + (int64_t)(kb) * TK;                                          \
-    r0v = *reinterpret_cast<const uint4*>(base + offB);                                     \
-    r1v = *reinterpret_cast<const uint4*>(base + stepb + offB);                             \
-    r2v = *reinterpret_cast<const uint4*>(base + 2 * stepb + offB);                         \
-    r3v = *reinterpret_cast<const uint4*>(base + 3 * stepb + offB);                         \
-    if (has_s) rs = *reinterpret_cast<const float*>(sbase + (int64_t)(kb) * steps + offS);  \
+#define CIN_LOAD_B(kb)                                                                        \
+  do {                                                                                        \
+    const uint32_t ko = (uint32_t)(kb) * TK;                                                  \
+    g0 = CIN_LD(rb, offB, ko);                                                                \
+    g1 = CIN_LD(rb, offB, ko + stepb);                                                        \
+    g2 = CIN_LD(rb, offB, ko + 2 * stepb);                                                    \
+    g3 = CIN_LD(rb, offB, ko + 3 * stepb);                                                    \
+    gs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(                      \
+                                       wave < 4 ? rs_a : rs_b, offS, (uint32_t)(kb) * steps, 0)); \
   } while (0)
 #define CIN_STORE(arr, i, rv, st)                                                           \
   *reinterpret_cast<uint4*>(__builtin_assume_aligned(&sm.arr[st][((i) * kThreads + tid) * 16], 16)) = rv
 #define CIN_STORE_S(st)                                                                     \
   do {                                                                                      \
-    if (tid < TM) sm.sa[st][tid] = rs;                                                      \
-    else if (has_s) sm.sb[st][tid - TM] = rs;                                               \
+    if (tid < TM) sm.sa[st][sa_slot(tid)] = gs;                                             \
+    else if (has_s) sm.sb[st][tid - TM] = gs;                                               \
   } while (0)
 
   v4f acc[8][4];
@@ -353,72 +375,119 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  const int nk = (int)(K / TK);
+  // prologue: block 0 into stage 0, block 1's A chunks into the staging registers
   CIN_LOAD_A(0);
-  CIN_STORE(a, 0, r0v, 0);
-  CIN_STORE(a, 1, r1v, 0);
-  CIN_STORE(a, 2, r2v, 0);
-  CIN_STORE(a, 3, r3v, 0);
+  CIN_STORE(a, 0, g0, 0); CIN_STORE(a, 1, g1, 0); CIN_STORE(a, 2, g2, 0); CIN_STORE(a, 3, g3, 0);
   CIN_LOAD_B(0);
-  CIN_STORE(b, 0, r0v, 0);
-  CIN_STORE(b, 1, r1v, 0);
-  CIN_STORE(b, 2, r2v, 0);
-  CIN_STORE(b, 3, r3v, 0);
+  CIN_STORE(b, 0, g0, 0); CIN_STORE(b, 1, g1, 0); CIN_STORE(b, 2, g2, 0); CIN_STORE(b, 3, g3, 0);
   CIN_STORE_S(0);
+  const int kl = nk - 1;
+  CIN_LOAD_A(kl < 1 ? kl : 1);
+  __syncthreads();
+
+  // Fragment addresses.  Every fragment row is (16-aligned base) + l16, so its swizzle
+  // f(row) = f(l16) and a fragment is two ds_read_b128 at a per-lane base plus a
+  // compile-time offset (stage, m/n-tile).
+  const uint8_t* lds = reinterpret_cast<const uint8_t*>(&sm);
+  const int fsw = swz_f(l16);
+  const uint32_t fa = (uint32_t)((wm * 128 + l16) * TK + (((2 * kq) ^ fsw) << 4));
+  const uint32_t fb = (uint32_t)(offsetof(Smem, b) + (wn * 64 + l16) * TK + (((2 * kq) ^ fsw) << 4));
+  const uint32_t fs = (uint32_t)(offsetof(Smem, sa) + (wm * 128 + l16 * 8) * 4);
+  // the high 16-byte half of a fragment is chunk 2kq+1, i.e. byte offset ^ 16
+#define CIN_FRAG(base, cofs)                                                                \
+  ({                                                                                        \
+    const uint4 lo_ = *reinterpret_cast<const uint4*>(lds + (base) + (cofs));               \
+    const uint4 hi_ = *reinterpret_cast<const uint4*>(lds + ((base) ^ 16u) + (cofs));       \
+    v8i v_;                                                                                 \
+    v_[0] = (int)lo_.x; v_[1] = (int)lo_.y; v_[2] = (int)lo_.z; v_[3] = (int)lo_.w;         \
+    v_[4] = (int)hi_.x; v_[5] = (int)hi_.y; v_[6] = (int)hi_.z; v_[7] = (int)hi_.w;         \
+    v_;                                                                                     \
+  })
+#define CIN_AFRAG(stg, mt) CIN_FRAG(fa, (uint32_t)((stg) * kTileBytes + (mt) * 16 * TK))
+#define CIN_BFRAG(stg, nt) CIN_FRAG(fb, (uint32_t)((stg) * kTileBytes + (nt) * 16 * TK))
+#define CIN_SA8(stg)                                                                        \
+  do {                                                                                      \
+    const float4 lo_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4)); \
+    const float4 hi_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4 + 16)); \
+    sa8[0] = lo_.x; sa8[1] = lo_.y; sa8[2] = lo_.z; sa8[3] = lo_.w;                         \
+    sa8[4] = hi_.x; sa8[5] = hi_.y; sa8[6] = hi_.z; sa8[7] = hi_.w;                         \
+  } while (0)
 
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  v8i bf[4], af[2];
+  float cs[2], sa8[8];
+  v4f p[4] = {zero, zero, zero, zero};  // partial ring; slot s % 4 holds MFMA(s)
+  float sbv = sm.sb[0][wn >> 1];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bf[j] = CIN_BFRAG(0, j);
+  af[0] = CIN_AFRAG(0, 0);
+  CIN_SA8(0);
+  cs[0] = sa8[0] * sbv;
+  cs[1] = 0.0f;  // the "previous block" FMAs of block 0 add 0 * 0
+
+  // Step s8 = 4 i + j of a K block issues the scale-FMAs of MFMA(s8 - 3) (for s8 < 3, of
+  // m-tile 7 of the previous block) and MFMA(s8).  Block indices past the end are clamped
+  // to the last block, so every block runs the same straight-line code (the extra loads
+  // and stores are never read) and the compiler's memory-counter waits stay exact.
   for (int kb = 0; kb < nk; ++kb) {
     const int st = kb & 1;
-    __syncthreads();  // stage st is complete; stage st^1 is no longer read
-    const bool more = kb + 1 < nk;
-    if (more) CIN_LOAD_A(kb + 1);
-    const uint8_t* la = sm.a[st];
-    const uint8_t* lb = sm.b[st];
-    const float* lsa = sm.sa[st];
-    const float sbv = sm.sb[st][wn >> 1];
-    v8i bf[4];
+    const int k1 = kb + 1 < kl ? kb + 1 : kl, k2 = kb + 2 < kl ? kb + 2 : kl;
+    float sbn = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bf[j] = frag(lb, wn * 64 + j * 16 + l16, kq);
-    v8i af[2];
-    af[0] = frag(la, wm * 128 + l16, kq);
-    float cs[2];
-    cs[0] = lsa[wm * 128 + l16] * sbv;
-    // 32 steps s = 4 i + j (m-tile i, n-tile j): step s issues MFMA(s) into partial
-    // ring slot s % 2, then the 4 scale-FMAs of MFMA(s-1), whose result had one MFMA
-    // slot of latency to land.  Empty asm statements pin this order (the MFMA builtins
-    // are otherwise free to move, and the compiler would cluster them and hold many
-    // partials live).
-    v4f p[2];
+    for (int s8 = 0; s8 < 32; ++s8) {
+      const int i = s8 >> 2, j = s8 & 3;
+      {
+        const int ti = s8 >= 3 ? (s8 - 3) >> 2 : 7;
+        const int tj = (s8 + 1) & 3;
+        const float c = cs[s8 >= 3 ? ((s8 - 3) >> 2) & 1 : 1];
+        asm volatile("" : "+v"(acc[ti][tj]));
 #pragma unroll
-    for (int st8 = 0; st8 < 33; ++st8) {
-      const int i = st8 >> 2, j = st8 & 3;
-      if (st8 < 32) {
-        if (j == 0) {
-          // staged loads of the next block: A chunks were loaded at the top and are
-          // stored in groups 2-3; then the B chunks + scales, stored in groups 6-7
-          if (more) {
-            if (i == 2) { CIN_STORE(a, 0, r0v, st ^ 1); CIN_STORE(a, 1, r1v, st ^ 1); }
-            if (i == 3) { CIN_STORE(a, 2, r2v, st ^ 1); CIN_STORE(a, 3, r3v, st ^ 1); CIN_LOAD_B(kb + 1); }
-            if (i == 6) { CIN_STORE(b, 0, r0v, st ^ 1); CIN_STORE(b, 1, r1v, st ^ 1); }
-            if (i == 7) { CIN_STORE(b, 2, r2v, st ^ 1); CIN_STORE(b, 3, r3v, st ^ 1); CIN_STORE_S(st ^ 1); }
-          }
-        }
-        asm volatile("" : "+v"(bf[j]));
-        p[st8 & 1] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af[i & 1], zero, 0, 0, 0, 0, 0, 0);
+        for (int r = 0; r < 4; ++r) acc[ti][tj][r] = fmaf(p[(s8 + 1) & 3][r], c, acc[ti][tj][r]);
+        asm volatile("" : "+v"(acc[ti][tj]));
       }
-      if (st8 > 0) {
-        const int s1 = st8 - 1, i1 = s1 >> 2, j1 = s1 & 3;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i1][j1][r] = fmaf(p[s1 & 1][r], cs[i1 & 1], acc[i1][j1][r]);
-        asm volatile("" : "+v"(acc[i1][j1]));
+      // MFMA(s8), pinned between two operand fences so the FMAs cannot cross it
+      asm volatile("" : "+v"(bf[j]));
+      p[s8 & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af[i & 1], zero, 0, 0, 0, 0, 0, 0);
+      asm volatile("" : "+v"(bf[j]));
+      // fragment of m-tile i+1 (its slot's previous user, m-tile i-1, is done)
+      if (j == 0 && i < 7) af[(i + 1) & 1] = CIN_AFRAG(st, i + 1);
+      // scale of m-tile i+1 (its slot's previous user, the FMAs of m-tile i-1, are done)
+      if (j == 3 && i < 7) cs[(i + 1) & 1] = sa8[i + 1] * sbv;
+      // block kb+1 into the free stage: its A chunks were loaded at step 28 of block kb-1,
+      // its B chunks are loaded here at step 6
+      if (s8 == 4) { CIN_STORE(a, 0, g0, st ^ 1); CIN_STORE(a, 1, g1, st ^ 1); }
+      if (s8 == 6) {
+        CIN_STORE(a, 2, g2, st ^ 1); CIN_STORE(a, 3, g3, st ^ 1);
+        CIN_LOAD_B(k1);
       }
-      // fragment and scale of m-tile i+1 (its slot's previous user, tile i-1, is done)
-      if (st8 < 32 && j == 0 && i + 1 < 8) {
-        af[(i + 1) & 1] = frag(la, wm * 128 + (i + 1) * 16 + l16, kq);
-        cs[(i + 1) & 1] = lsa[wm * 128 + (i + 1) * 16 + l16] * sbv;
+      if (s8 == 18) { CIN_STORE(b, 0, g0, st ^ 1); CIN_STORE(b, 1, g1, st ^ 1); }
+      if (s8 == 22) { CIN_STORE(b, 2, g2, st ^ 1); CIN_STORE(b, 3, g3, st ^ 1); CIN_STORE_S(st ^ 1); }
+      if (s8 == 28) {
+        // stage st^1 is complete and stage st is no longer read (its last fragment,
+        // m-tile 7, was read at step 24): start block kb+2's A loads and the next block's
+        // fragments
+        __syncthreads();
+        CIN_LOAD_A(k2);
+        sbn = sm.sb[st ^ 1][wn >> 1];
+        af[0] = CIN_AFRAG(st ^ 1, 0);
+        CIN_SA8(st ^ 1);
       }
+      if (s8 >= 28) bf[j] = CIN_BFRAG(st ^ 1, j);
+      if (s8 == 31) cs[0] = sa8[0] * sbn;
     }
+    sbv = sbn;
   }
+#undef CIN_FRAG
+#undef CIN_AFRAG
+#undef CIN_BFRAG
+#undef CIN_SA8
+  // drain: FMAs of the last block's MFMAs 29-31 (m-tile 7)
+#pragma unroll
+  for (int s8 = 29; s8 < 32; ++s8) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[7][s8 & 3][r] = fmaf(p[s8 & 3][r], cs[1], acc[7][s8 & 3][r]);
+  }
+#undef CIN_LD
 #undef CIN_LOAD_A
 #undef CIN_LOAD_B
 #undef CIN_STORE
