@@ -250,17 +250,17 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_gemm_fp8(
 namespace big {
 
 // Workgroup tile 256 x 256 x 128, 8 waves (2 per SIMD), wave tile 128 (m) x 64 (n), two
-// LDS stages.  Per K block a wave issues 32 MFMAs (8 m-tiles x 4 n-tiles) and, for each,
-// the 4 scale-FMAs of the MFMA three steps earlier: the partials live in a ring of 4
-// slots, so an FMA reads a result whose MFMA finished long ago and no wave ever waits on
-// its own MFMA.  The ring runs across K blocks (the FMAs of a block's last 3 MFMAs are
-// issued at the start of the next block).
+// LDS stages.  Per K block a wave issues 32 MFMAs (8 m-tiles x 4 n-tiles) and, before
+// each, the 4 scale-FMAs of the MFMA three steps earlier: the partials live in a ring of
+// 4 slots, so an FMA reads a result whose MFMA finished long ago and no wave ever waits
+// on its own MFMA.  The ring runs across K blocks.
 //
-// Operands are staged global -> VGPR -> LDS a whole K block ahead: the loads of block
-// kb+2 are issued right after the barrier of block kb, and written to the free stage
-// during block kb+1.  The barrier sits before the last m-tile group, so the fragments of
-// the next block are read while that group's MFMAs run.  (global_load_lds moved only
-// ~16 bytes per clock per CU on gfx950, half of what the MFMAs consume here.)
+// Operands move global -> LDS by DMA (buffer_load ... lds), one K block ahead: right
+// after the barrier of block kb frees a stage, the DMA of block kb+2 into it is issued,
+// and it has a whole block to land.  No VGPR staging and no ds_write.  The barrier sits
+// before the last m-tile group, so the next block's fragments are read while that
+// group's MFMAs run.  The DMA is issued from inline assembly: the compiler treats its
+// own LDS-DMA builtin as aliasing every LDS read and would wait for it before each one.
 constexpr int TM = 256, TN = 256, TK = 128;
 constexpr int kThreads = 512;
 constexpr int kTileBytes = TM * TK;  // 32 KB per operand per stage
@@ -268,28 +268,17 @@ constexpr int kTileBytes = TM * TK;  // 32 KB per operand per stage
 struct __attribute__((aligned(16))) Smem {
   uint8_t a[2][kTileBytes];
   uint8_t b[2][kTileBytes];
-  float sa[2][TM];  // A-row scales, row r at sa_slot(r)
-  float sb[2][2];
+  float sa[2][TM];  // A-row scales, slot q holds row sa_row(q)
 };
 
-// Row r = 128 wm + 16 i + l of the tile is stored at (wm, l, i): the lane (wm, l) finds
-// the scales of its 8 m-tiles in 32 contiguous bytes.
-__device__ inline int sa_slot(int r) { return (r >> 7) * 128 + (r & 15) * 8 + ((r >> 4) & 7); }
+// Slot q = 128 wm + 8 l + i holds row 128 wm + 16 i + l: the lane (wm, l) finds the
+// scales of its 8 m-tiles in 32 contiguous bytes.
+__device__ inline int sa_row(int q) { return (q & ~127) + (q & 7) * 16 + ((q >> 3) & 15); }
 
 // 16-byte chunk c of tile row r lives at slot c ^ f(r), f(r) = (r % 8) ^ ((r / 8) % 2):
 // the 8 rows a 32-bank LDS serves together, and the 8 same-parity rows a 64-bank LDS
 // serves together, all hit distinct banks.
 __device__ inline int swz_f(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-__device__ inline int swz2(int row, int chunk) { return row * TK + ((chunk ^ swz_f(row)) << 4); }
-
-__device__ inline v8i frag(const uint8_t* lds, int row, int kq) {
-  const uint4 lo = *reinterpret_cast<const uint4*>(lds + swz2(row, 2 * kq));
-  const uint4 hi = *reinterpret_cast<const uint4*>(lds + swz2(row, 2 * kq + 1));
-  v8i v;
-  v[0] = (int)lo.x; v[1] = (int)lo.y; v[2] = (int)lo.z; v[3] = (int)lo.w;
-  v[4] = (int)hi.x; v[5] = (int)hi.y; v[6] = (int)hi.z; v[7] = (int)hi.w;
-  return v;
-}
 
 // Raw buffer resource over [p, p + bytes): loads are an SGPR base plus a 32-bit lane
 // offset, and anything past `bytes` reads as zero.
@@ -298,6 +287,19 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes)
   const uint32_t n = (uint32_t)(bytes < cap ? bytes : cap);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)n, 0x00020000);
 }
+
+// DMA of 16 (4) bytes per lane from the buffer to LDS: lane t's bytes land at LDS byte
+// address lds + 16 t (4 t).  lds is wave-uniform.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory");
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(r), "s"(soff) : "memory");
+}
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // One full 256 x 256 tile.  A / sa point at the tile's first row, B / sb at its first
 // column block; the tile stores local rows [row_lo, row_hi) and local columns >= col_lo.
@@ -320,9 +322,11 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
   const int wm = wave >> 2, wn = wave & 3;
   const int l16 = lane & 15, kq = lane >> 4;
   const int nk = (int)(K / TK);
+  const int kl = nk - 1;
 
-  // Loads: round i covers tile rows i*64 .. i*64+63; thread tid fetches row
-  // i*64 + tid/8, chunk (tid % 8) ^ swz_f(row) and stores it to slot i*512 + tid.
+  // DMA round i of an operand covers tile rows i*64 .. i*64+63: thread tid fetches row
+  // i*64 + tid/8, chunk (tid % 8) ^ swz_f(row), which lands at LDS slot i*512 + tid, i.e.
+  // wave w's lanes fill the 1 KB at slot i*512 + 64 w.
   const int r0 = tid >> 3;
   const uint32_t q16 = (uint32_t)(((tid & 7) ^ swz_f(r0)) * 16);
   const uint32_t offA = (uint32_t)(r0 * lda) + q16;
@@ -330,70 +334,34 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
   const uint32_t stepa = (uint32_t)(64 * lda), stepb = (uint32_t)(64 * ldb);
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(T.A, 255 * lda + K);
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(T.B, 255 * ldb + K);
-  // scales: threads 0-255 fetch the A-scale rows, 256-257 the tile's two B-block scales
-  // (threads 258-511 load one of the B scales too and drop it, so that every wave issues
-  // the same loads and the compiler's memory-counter waits stay exact)
-  const bool has_s = tid < TM + 2;
-  const uint32_t offS = tid < TM ? (uint32_t)(tid * ssam * 4) : (uint32_t)(((tid - TM) & 1) * ssbn * 4);
-  const __amdgpu_buffer_rsrc_t rs_a = make_rsrc(T.sa, (255 * ssam + (int64_t)(nk - 1) * ssak + 1) * 4);
-  const __amdgpu_buffer_rsrc_t rs_b = make_rsrc(T.sb, (ssbn + (int64_t)(nk - 1) * ssbk + 1) * 4);
-  const uint32_t steps = (uint32_t)((wave < 4 ? ssak : ssbk) * 4);
-
-  // staging registers: 4 chunks of one operand of one K block (A, then B), and one scale
-  uint4 g0, g1, g2, g3;
-  float gs = 0.0f;
-#define CIN_LD(rsrc, off, so) __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, so, 0))
-#define CIN_LOAD_A(kb)                                                                        \
+  // A-row scales: waves 0-3 fill the 256 slots; lane t of wave w loads row sa_row(64 w + t)
+  const __amdgpu_buffer_rsrc_t rsa = make_rsrc(T.sa, (255 * ssam + (int64_t)kl * ssak + 1) * 4);
+  const uint32_t offS = (uint32_t)(sa_row((wave & 3) * 64 + lane) * ssam * 4);
+  const uint32_t stepsa = (uint32_t)(ssak * 4);
+  // the wave's B-block scales (its 64 columns lie in one 128-column block)
+  const float* sbp = T.sb + (int64_t)(wn >> 1) * ssbn;
+  const uint32_t lds_a = (uint32_t)(uintptr_t)&sm.a[0][0] + (uint32_t)(wave * 64 * 16);
+  const uint32_t lds_b = (uint32_t)(uintptr_t)&sm.b[0][0] + (uint32_t)(wave * 64 * 16);
+  const uint32_t lds_s = (uint32_t)(uintptr_t)&sm.sa[0][0] + (uint32_t)((wave & 3) * 64 * 4);
+#define CIN_DMA(kb, stg)                                                                      \
   do {                                                                                        \
     const uint32_t ko = (uint32_t)(kb) * TK;                                                  \
-    g0 = CIN_LD(ra, offA, ko);                                                                \
-    g1 = CIN_LD(ra, offA, ko + stepa);                                                        \
-    g2 = CIN_LD(ra, offA, ko + 2 * stepa);                                                    \
-    g3 = CIN_LD(ra, offA, ko + 3 * stepa);                                                    \
+    const uint32_t so = (uint32_t)(stg) * kTileBytes;                                         \
+    _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_) {                                        \
+      dma16(ra, offA, ko + i_ * stepa, lds_a + so + i_ * kThreads * 16);                      \
+      dma16(rb, offB, ko + i_ * stepb, lds_b + so + i_ * kThreads * 16);                      \
+    }                                                                                         \
+    if (wave < 4) dma4(rsa, offS, (uint32_t)(kb) * stepsa, lds_s + (uint32_t)(stg) * TM * 4); \
   } while (0)
-#define CIN_LOAD_B(kb)                                                                        \
-  do {                                                                                        \
-    const uint32_t ko = (uint32_t)(kb) * TK;                                                  \
-    g0 = CIN_LD(rb, offB, ko);                                                                \
-    g1 = CIN_LD(rb, offB, ko + stepb);                                                        \
-    g2 = CIN_LD(rb, offB, ko + 2 * stepb);                                                    \
-    g3 = CIN_LD(rb, offB, ko + 3 * stepb);                                                    \
-    gs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(                      \
-                                       wave < 4 ? rs_a : rs_b, offS, (uint32_t)(kb) * steps, 0)); \
-  } while (0)
-#define CIN_STORE(arr, i, rv, st)                                                           \
-  *reinterpret_cast<uint4*>(__builtin_assume_aligned(&sm.arr[st][((i) * kThreads + tid) * 16], 16)) = rv
-#define CIN_STORE_S(st)                                                                     \
-  do {                                                                                      \
-    if (tid < TM) sm.sa[st][sa_slot(tid)] = gs;                                             \
-    else if (has_s) sm.sb[st][tid - TM] = gs;                                               \
-  } while (0)
-
-  v4f acc[8][4];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  // prologue: block 0 into stage 0, block 1's A chunks into the staging registers
-  CIN_LOAD_A(0);
-  CIN_STORE(a, 0, g0, 0); CIN_STORE(a, 1, g1, 0); CIN_STORE(a, 2, g2, 0); CIN_STORE(a, 3, g3, 0);
-  CIN_LOAD_B(0);
-  CIN_STORE(b, 0, g0, 0); CIN_STORE(b, 1, g1, 0); CIN_STORE(b, 2, g2, 0); CIN_STORE(b, 3, g3, 0);
-  CIN_STORE_S(0);
-  const int kl = nk - 1;
-  CIN_LOAD_A(kl < 1 ? kl : 1);
-  __syncthreads();
 
   // Fragment addresses.  Every fragment row is (16-aligned base) + l16, so its swizzle
-  // f(row) = f(l16) and a fragment is two ds_read_b128 at a per-lane base plus a
-  // compile-time offset (stage, m/n-tile).
+  // f(row) = f(l16) and a fragment is two ds_read_b128 at a per-lane base plus an
+  // (stage, m/n-tile) offset; the high half is chunk 2kq+1, i.e. byte offset ^ 16.
   const uint8_t* lds = reinterpret_cast<const uint8_t*>(&sm);
   const int fsw = swz_f(l16);
   const uint32_t fa = (uint32_t)((wm * 128 + l16) * TK + (((2 * kq) ^ fsw) << 4));
   const uint32_t fb = (uint32_t)(offsetof(Smem, b) + (wn * 64 + l16) * TK + (((2 * kq) ^ fsw) << 4));
   const uint32_t fs = (uint32_t)(offsetof(Smem, sa) + (wm * 128 + l16 * 8) * 4);
-  // the high 16-byte half of a fragment is chunk 2kq+1, i.e. byte offset ^ 16
 #define CIN_FRAG(base, cofs)                                                                \
   ({                                                                                        \
     const uint4 lo_ = *reinterpret_cast<const uint4*>(lds + (base) + (cofs));               \
@@ -413,11 +381,23 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
     sa8[4] = hi_.x; sa8[5] = hi_.y; sa8[6] = hi_.z; sa8[7] = hi_.w;                         \
   } while (0)
 
+  v4f acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // prologue: blocks 0 and 1 into stages 0 and 1
+  CIN_DMA(0, 0);
+  if (nk > 1) CIN_DMA(1, 1);
+  wait_dma();
+  __syncthreads();
+
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
   v8i bf[4], af[2];
   float cs[2], sa8[8];
   v4f p[4] = {zero, zero, zero, zero};  // partial ring; slot s % 4 holds MFMA(s)
-  float sbv = sm.sb[0][wn >> 1];
+  float sbv = sbp[0];
 #pragma unroll
   for (int j = 0; j < 4; ++j) bf[j] = CIN_BFRAG(0, j);
   af[0] = CIN_AFRAG(0, 0);
@@ -426,13 +406,11 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
   cs[1] = 0.0f;  // the "previous block" FMAs of block 0 add 0 * 0
 
   // Step s8 = 4 i + j of a K block issues the scale-FMAs of MFMA(s8 - 3) (for s8 < 3, of
-  // m-tile 7 of the previous block) and MFMA(s8).  Block indices past the end are clamped
-  // to the last block, so every block runs the same straight-line code (the extra loads
-  // and stores are never read) and the compiler's memory-counter waits stay exact.
+  // m-tile 7 of the previous block) and MFMA(s8).
   for (int kb = 0; kb < nk; ++kb) {
     const int st = kb & 1;
-    const int k1 = kb + 1 < kl ? kb + 1 : kl, k2 = kb + 2 < kl ? kb + 2 : kl;
-    float sbn = 0.0f;
+    const bool more = kb < kl;
+    const float sbn = sbp[(int64_t)(more ? kb + 1 : kb) * ssbk];
 #pragma unroll
     for (int s8 = 0; s8 < 32; ++s8) {
       const int i = s8 >> 2, j = s8 & 3;
@@ -453,45 +431,35 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
       if (j == 0 && i < 7) af[(i + 1) & 1] = CIN_AFRAG(st, i + 1);
       // scale of m-tile i+1 (its slot's previous user, the FMAs of m-tile i-1, are done)
       if (j == 3 && i < 7) cs[(i + 1) & 1] = sa8[i + 1] * sbv;
-      // block kb+1 into the free stage: its A chunks were loaded at step 28 of block kb-1,
-      // its B chunks are loaded here at step 6
-      if (s8 == 4) { CIN_STORE(a, 0, g0, st ^ 1); CIN_STORE(a, 1, g1, st ^ 1); }
-      if (s8 == 6) {
-        CIN_STORE(a, 2, g2, st ^ 1); CIN_STORE(a, 3, g3, st ^ 1);
-        CIN_LOAD_B(k1);
+      if (more) {
+        if (s8 == 28) {
+          // block kb+1's DMA (issued a block ago) has landed in stage st^1, and stage st
+          // is no longer read (its last fragment, m-tile 7, was read at step 24): after
+          // the barrier, block kb+2 goes into stage st and the next block's fragments
+          // are read
+          wait_dma();
+          __syncthreads();
+          if (kb + 2 < nk) CIN_DMA(kb + 2, st);
+          af[0] = CIN_AFRAG(st ^ 1, 0);
+          CIN_SA8(st ^ 1);
+        }
+        if (s8 >= 28) bf[j] = CIN_BFRAG(st ^ 1, j);
+        if (s8 == 31) cs[0] = sa8[0] * sbn;
       }
-      if (s8 == 18) { CIN_STORE(b, 0, g0, st ^ 1); CIN_STORE(b, 1, g1, st ^ 1); }
-      if (s8 == 22) { CIN_STORE(b, 2, g2, st ^ 1); CIN_STORE(b, 3, g3, st ^ 1); CIN_STORE_S(st ^ 1); }
-      if (s8 == 28) {
-        // stage st^1 is complete and stage st is no longer read (its last fragment,
-        // m-tile 7, was read at step 24): start block kb+2's A loads and the next block's
-        // fragments
-        __syncthreads();
-        CIN_LOAD_A(k2);
-        sbn = sm.sb[st ^ 1][wn >> 1];
-        af[0] = CIN_AFRAG(st ^ 1, 0);
-        CIN_SA8(st ^ 1);
-      }
-      if (s8 >= 28) bf[j] = CIN_BFRAG(st ^ 1, j);
-      if (s8 == 31) cs[0] = sa8[0] * sbn;
     }
     sbv = sbn;
   }
-#undef CIN_FRAG
-#undef CIN_AFRAG
-#undef CIN_BFRAG
-#undef CIN_SA8
   // drain: FMAs of the last block's MFMAs 29-31 (m-tile 7)
 #pragma unroll
   for (int s8 = 29; s8 < 32; ++s8) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[7][s8 & 3][r] = fmaf(p[s8 & 3][r], cs[1], acc[7][s8 & 3][r]);
   }
-#undef CIN_LD
-#undef CIN_LOAD_A
-#undef CIN_LOAD_B
-#undef CIN_STORE
-#undef CIN_STORE_S
+#undef CIN_DMA
+#undef CIN_FRAG
+#undef CIN_AFRAG
+#undef CIN_BFRAG
+#undef CIN_SA8
 
   // epilogue: lane holds C[m][n .. n+3] (n a multiple of 4, so a shifted tile's
   // column skip, a multiple of 128, never splits a lane's 4 columns)
