@@ -37,6 +37,12 @@ SIGNATURES: dict[str, list] = {
                         _i32, _i64, _p],
     "cin_grouped_gemm_fp8": [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _p,
                              _p, _i64, _i64, _i64, _i64, _p, _i32, _i64, _p],
+    "cin_quant_dual_grouped": [_p, _i32, _i64, _i64, _i64, _p, _p, _i64, _i32, _p, _i64, _p, _i64,
+                               _p, _i64, _p, _i64, _p],
+    "cin_requant_row_to_block_grouped": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _p, _i64,
+                                         _p, _i64, _p],
+    "cin_grouped_gemm_fp8_wgrad": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i64,
+                                   _i64, _i64, _i64, _p, _i32, _i64, _i64, _p],
 }
 
 _lock = threading.Lock()

@@ -24,6 +24,7 @@
 #include <stdint.h>
 
 #include "cin_common.h"
+#include "cin_grouped.h"
 #include "cin_runtime.h"
 
 using namespace cin;
@@ -282,10 +283,18 @@ __device__ inline int swz_f(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // Raw buffer resource over [p, p + bytes): loads are an SGPR base plus a 32-bit lane
 // offset, and anything past `bytes` reads as zero.
+// The operands are wave-uniform by construction; readfirstlane says so to the compiler,
+// so the descriptor lives in SGPRs even when it was computed from loaded values.
 __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
   const int64_t cap = 0xffffffffLL;
-  const uint32_t n = (uint32_t)(bytes < cap ? bytes : cap);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)n, 0x00020000);
+  // (readfirstlane returns int: go through uint32_t, or a low word with bit 31 set
+  // would sign-extend into the high word of the address)
+  const uint32_t n = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(bytes < cap ? bytes : cap));
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+  void* pu = (void*)(uintptr_t)((hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(pu, (short)0, (int)n, 0x00020000);
 }
 
 // DMA of 16 (4) bytes per lane from the buffer to LDS: lane t's bytes land at LDS byte
@@ -568,6 +577,55 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_gemm_fp8_256(
   tile_body(t, lda, ssam, ssak, ldb, ssbn, ssbk, K, c_dtype, ldc);
 }
 
+// Grouped weight gradient: dW_e[n, k] = sum over expert e's tokens t of
+// dC[t, n] * X[t, k], with both operands quantized per expert in 128-token chunks and
+// stored transposed on the padded token axis (cin_grouped.h): A = dC^T codes [N, Tpad],
+// B = X^T codes [K, Tpad].  Workgroup = (expert, 256 x 256 output tile); its reduction
+// runs over the expert's padded range [p_e, p_e + 128 ceil(m_e / 128)), whose padding
+// columns hold code 0.  An expert without tokens gets dW_e = 0.
+__global__ __launch_bounds__(kThreads, 2) void k_grouped_wgrad_fp8_256(
+    const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
+    const uint8_t* __restrict__ B, int64_t ldb, const float* __restrict__ sb, int64_t ssbm,
+    const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t Tn, int64_t tcap,
+    int64_t M, int64_t N, void* C, int c_dtype, int64_t ldc, int64_t sce, uint32_t tiles_m,
+    uint32_t tiles_n, uint32_t ntot) {
+  const uint32_t b = xcd_remap(blockIdx.x, ntot);
+  const uint32_t per = tiles_m * tiles_n;
+  const uint32_t e = b / per, r = b - e * per;
+  const uint32_t tm = r / tiles_n, tn = r - tm * tiles_n;
+  int64_t p, m;
+  padded_range(starts, ends, e, Tn, p, m);
+  int nk = (int)((m + TK - 1) / TK);
+  if (p + (int64_t)nk * TK > tcap) nk = 0;  // ranges inconsistent with the operands' columns
+  const int64_t m_nom = (int64_t)tm * TM, n_nom = (int64_t)tn * TN;
+  const int64_t m0 = m_nom + TM <= M ? m_nom : M - TM;
+  const int64_t n0 = n_nom + TN <= N ? n_nom : N - TN;
+  const size_t es = c_dtype == CIN_DT_F32 ? 4 : 2;
+  uint8_t* Ce = static_cast<uint8_t*>(C) + ((int64_t)e * sce + m0 * ldc + n0) * es;
+  const int row_lo = (int)(m_nom - m0), col_lo = (int)(n_nom - n0);
+  if (nk == 0) {
+    for (int idx = threadIdx.x; idx < TM * TN; idx += kThreads) {
+      const int rr = idx / TN, cc = idx - rr * TN;
+      if (rr < row_lo || cc < col_lo) continue;
+      if (c_dtype == CIN_DT_F32)
+        reinterpret_cast<float*>(Ce)[(int64_t)rr * ldc + cc] = 0.0f;
+      else
+        reinterpret_cast<uint16_t*>(Ce)[(int64_t)rr * ldc + cc] = 0;
+    }
+    return;  // uniform: before any barrier
+  }
+  Tile t;
+  t.A = A + m0 * lda + p;
+  t.sa = sa + m0 * ssam + p / TK;
+  t.B = B + n0 * ldb + p;
+  t.sb = sb + (p / TK) * ssbm + (n0 >> 7);
+  t.C = Ce;
+  t.row_lo = row_lo;
+  t.row_hi = TM;
+  t.col_lo = col_lo;
+  tile_body(t, lda, ssam, 1, ldb, 1, ssbm, (int64_t)nk * TK, c_dtype, ldc);
+}
+
 }  // namespace big
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -645,6 +703,35 @@ int cin_grouped_gemm_fp8(const uint8_t* A, int64_t lda, const float* sa, int64_t
   hipLaunchKernelGGL(k_grouped_gemm_fp8, grid, kThreads, 0, s, A, lda, sa, ssam, ssak, B, sbe, ldb,
                      sb, ssbe, ssbn, ssbk, starts, ends, E, T, N, K, C, c_dtype, ldc, ntn);
   return cin_check_launch("grouped_gemm_fp8");
+}
+
+int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam,
+                               const uint8_t* B, int64_t ldb, const float* sb, int64_t ssbm,
+                               const int64_t* starts, const int64_t* ends, int64_t E, int64_t T,
+                               int64_t tcap, int64_t N, int64_t K, void* C, int c_dtype, int64_t ldc,
+                               int64_t sce, void* stream) {
+  CIN_CHECK_ARG(c_dtype == CIN_DT_BF16 || c_dtype == CIN_DT_F32,
+                "grouped_wgrad_fp8: C dtype must be bf16 or fp32");
+  CIN_CHECK_ARG(E >= 0 && T >= 0 && N >= 0 && K >= 0, "grouped_wgrad_fp8: negative shape");
+  if (E == 0 || N == 0 || K == 0) return CIN_OK;
+  CIN_CHECK_ARG(A && B && sa && sb && starts && ends && C, "grouped_wgrad_fp8: null pointer");
+  CIN_CHECK_ARG(N >= big::TM && K >= big::TN && K % 128 == 0,
+                "grouped_wgrad_fp8: needs N >= 256, K >= 256 and K %% 128 == 0 (N=%lld, K=%lld)",
+                (long long)N, (long long)K);
+  CIN_CHECK_ARG(lda % 16 == 0 && ldb % 16 == 0 && aligned16(A) && aligned16(B),
+                "grouped_wgrad_fp8: A/B rows must be 16-byte aligned");
+  CIN_CHECK_ARG(tcap >= 0 && tcap <= lda && tcap <= ldb && tcap <= ssam * 128 &&
+                    (ssam == 0 || tcap / 128 <= ssam),
+                "grouped_wgrad_fp8: padded capacity exceeds the operand rows");
+  CIN_CHECK_ARG(ldc >= K && sce >= N * ldc, "grouped_wgrad_fp8: bad C strides");
+  CIN_CHECK_ARG(ssbm >= K / 128, "grouped_wgrad_fp8: bad B-scale stride");
+  const int64_t tm = cdiv(N, big::TM), tn = cdiv(K, big::TN);
+  CIN_CHECK_ARG(E * tm * tn < ((int64_t)1 << 31), "grouped_wgrad_fp8: grid too large");
+  const uint32_t ntot = (uint32_t)(E * tm * tn);
+  hipLaunchKernelGGL(big::k_grouped_wgrad_fp8_256, ntot, big::kThreads, 0,
+                     static_cast<hipStream_t>(stream), A, lda, sa, ssam, B, ldb, sb, ssbm, starts,
+                     ends, T, tcap, N, K, C, c_dtype, ldc, sce, (uint32_t)tm, (uint32_t)tn, ntot);
+  return cin_check_launch("grouped_wgrad_fp8");
 }
 
 }  // extern "C"

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "cin_common.h"
+#include "cin_grouped.h"
 #include "cin_runtime.h"
 
 using namespace cin;
@@ -384,19 +385,70 @@ __global__ __launch_bounds__(kThreads) void k_blockwise128(const void* __restric
 }
 
 // ---------------------------------------------------------------------------
-// Dual 1x128 quantization of dy (row tiles of dy and of dy^T) from one read.
-// Workgroup per 128x128 tile; thread holds rows rg + 16 i, columns lane16*8 + j.
+// Placement of one 128-row tile of the dual and re-quantization kernels.  Dense: tile rb
+// covers rows [128 rb, min(128 rb + 128, M)) and its transposed outputs sit at the same
+// columns.  Grouped (MoE backward): the tile is one 128-token chunk of an expert, and its
+// transposed outputs sit at the chunk's padded position; the columns past the chunk's
+// rows are written as code 0, so a GEMM reducing over the padded axis adds nothing there.
+// ---------------------------------------------------------------------------
+struct RowTile {
+  int64_t r0;  // first input row
+  int nr;      // valid rows, 1..128
+  int64_t t0;  // first column of the transposed outputs
+  int tw;      // transposed columns written: nr (dense) or 128 (padded)
+  int64_t tb;  // index of the tile's scale along the transposed axis
+};
+
+__device__ inline RowTile dense_tile(int64_t rb, int64_t M) {
+  const int64_t left = M - rb * 128;
+  const int nr = (int)(left < 128 ? left : 128);
+  return RowTile{rb * 128, nr, rb * 128, nr, rb};
+}
+
+// Grouped tile for block row `id`; false when `id` is past the last chunk or its padded
+// position would not fit in `tcap` columns (the caller's transposed row length).
+__device__ inline bool grouped_tile(const int64_t* starts, const int64_t* ends, int64_t E,
+                                    int64_t T, int64_t id, int64_t tcap, RowTile& rt) {
+  Chunk c;
+  if (!find_chunk(starts, ends, E, T, id, c) || c.t0 + 128 > tcap) return false;
+  rt = RowTile{c.r0, c.nr, c.t0, 128, c.t0 / 128};
+  return true;
+}
+
+// Write a 128 x 128 byte tile held transposed in LDS (tileT[col][row]) to
+// dst[(n0 + col) * ld + t0 + row] for the tile's first tw rows and cols < ncols.
+__device__ inline void store_tile_t(const uint32_t (*tileT)[128 / 4 + 1], uint8_t* dst_base, int64_t ld,
+                                    int64_t n0, int64_t ncols, int64_t t0, int tw) {
+  for (int idx = threadIdx.x; idx < 128 * 8; idx += kThreads) {
+    const int tc = idx >> 3, seg = idx & 7;
+    const int64_t n = n0 + tc;
+    const int m0 = seg * 16;
+    if (n >= ncols || m0 >= tw) continue;
+    const uint32_t* src = &tileT[tc][seg * 4];
+    uint8_t* dst = dst_base + n * ld + t0 + m0;
+    if (m0 + 16 <= tw && (((uintptr_t)dst) & 15u) == 0) {
+      *reinterpret_cast<uint4*>(dst) = make_uint4(src[0], src[1], src[2], src[3]);
+    } else {
+      for (int k = 0; k < 16; ++k)
+        if (m0 + k < tw) dst[k] = (uint8_t)((src[k >> 2] >> (8 * (k & 3))) & 0xffu);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dual quantization of a gradient tile (reference FP8MatmulFunction.backward,
+// src/kernels.py:771-782): 1x128 row tiles of dY and 1x128 row tiles of dY^T (= 128x1
+// column tiles of dY) from one read.  The transposed codes are written through an
+// LDS tile.
 // ---------------------------------------------------------------------------
 template <int DT>
-__global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x, int64_t M,
-                                                      int64_t N, int64_t sxm, int round_scale,
-                                                      uint8_t* q, int64_t sqm, float* s,
-                                                      int64_t ssm, uint8_t* qt, int64_t sqtm,
-                                                      float* st, int64_t sstm) {
+__device__ __forceinline__ void dual_tile(const void* __restrict__ x, int64_t N, int64_t sxm,
+                                          int round_scale, uint8_t* q, int64_t sqm, float* s,
+                                          int64_t ssm, uint8_t* qt, int64_t sqtm, float* st,
+                                          int64_t sstm, const RowTile rt, int64_t cb) {
   __shared__ float colpart[16][128];
   __shared__ float colscale[128];
   __shared__ uint32_t tileT[128][128 / 4 + 1];
-  const int64_t rb = blockIdx.y, cb = blockIdx.x;
   const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
   const int64_t c = cb * 128 + lane16 * 8;
   const bool rs = round_scale != 0;
@@ -404,9 +456,9 @@ __global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x
   Vec8<DT> d[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int64_t r = rb * 128 + rg + 16 * i;
-    const int64_t nc = (r < M) ? N - c : 0;
-    load8<DT>(x, r * sxm + c, nc < 0 ? 0 : (nc > 8 ? 8 : nc), d[i]);
+    const int ri = rg + 16 * i;
+    const int64_t nc = (ri < rt.nr) ? N - c : 0;
+    load8<DT>(x, (rt.r0 + ri) * sxm + c, nc < 0 ? 0 : (nc > 8 ? 8 : nc), d[i]);
   }
   // column partial maxima over this thread's 8 rows
 #pragma unroll
@@ -419,7 +471,8 @@ __global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x
   // row tiles: quantize and store
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int64_t r = rb * 128 + rg + 16 * i;
+    const int ri = rg + 16 * i;
+    const int64_t r = rt.r0 + ri;
     float a = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(d[i].v[j]));
@@ -429,7 +482,7 @@ __global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x
     uint32_t c2[2];
     quant_vals<8, kDivSteps<DT>>(d[i].v, sr, 1.0f / sr, c2);
     const uint32_t lo = c2[0], hi = c2[1];
-    if (r < M) {
+    if (ri < rt.nr) {
       uint8_t* qp = q + r * sqm + c;
       if (c + 8 <= N) {
         *reinterpret_cast<uint2*>(qp) = make_uint2(lo, hi);
@@ -449,7 +502,7 @@ __global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x
     const float sc = compute_scale(a, rs);
     colscale[threadIdx.x] = sc;
     const int64_t n = cb * 128 + threadIdx.x;
-    if (n < N) st[n * sstm + rb] = sc;
+    if (n < N) st[n * sstm + rt.tb] = sc;
   }
   __syncthreads();
   uint8_t* tb = reinterpret_cast<uint8_t*>(&tileT[0][0]);
@@ -467,48 +520,52 @@ __global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x
       tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * i] = (uint8_t)((c2[i >> 2] >> (8 * (i & 3))) & 0xffu);
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 128 * 8; idx += kThreads) {
-    const int tc = idx >> 3, seg = idx & 7;
-    const int64_t n = cb * 128 + tc;
-    const int64_t m0 = rb * 128 + seg * 16;
-    if (n >= N) continue;
-    const uint32_t* src = &tileT[tc][seg * 4];
-    uint8_t* dst = qt + n * sqtm + m0;
-    if (m0 + 16 <= M && (((uintptr_t)dst) & 15u) == 0) {
-      *reinterpret_cast<uint4*>(dst) = make_uint4(src[0], src[1], src[2], src[3]);
-    } else {
-      for (int k = 0; k < 16; ++k)
-        if (m0 + k < M) dst[k] = (uint8_t)((src[k >> 2] >> (8 * (k & 3))) & 0xffu);
-    }
-  }
+  store_tile_t(tileT, qt, sqtm, cb * 128, N, rt.t0, rt.tw);
 }
 
-// Generic dual: the two generic row-wise passes (dy row tiles, dy^T row tiles).
-// (Used only when dy rows are not contiguous / aligned.)
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x, int64_t M,
+                                                      int64_t N, int64_t sxm, int round_scale,
+                                                      uint8_t* q, int64_t sqm, float* s,
+                                                      int64_t ssm, uint8_t* qt, int64_t sqtm,
+                                                      float* st, int64_t sstm) {
+  dual_tile<DT>(x, N, sxm, round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm,
+                dense_tile(blockIdx.y, M), blockIdx.x);
+}
+
+// Grouped: block row = one 128-token chunk of an expert (see cin_grouped.h).  Rows
+// outside every expert range are not quantized.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_dual128_grouped(
+    const void* __restrict__ x, int64_t T, int64_t N, int64_t sxm, int round_scale, uint8_t* q,
+    int64_t sqm, float* s, int64_t ssm, uint8_t* qt, int64_t sqtm, float* st, int64_t sstm,
+    const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t E, int64_t tcap) {
+  RowTile rt;
+  if (!grouped_tile(starts, ends, E, T, blockIdx.y, tcap, rt)) return;  // before any barrier
+  dual_tile<DT>(x, N, sxm, round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm, rt, blockIdx.x);
+}
 
 // ---------------------------------------------------------------------------
 // Re-quantization row(1x128) -> block(128x128).  x = fp32(code) * srow (fp32
 // product, as torch's dequantize_fp8_rowwise), then the block quantizer with
 // the fp32 floor and round_scale = False.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void k_requant128(const uint8_t* __restrict__ q, int64_t M,
-                                                         int64_t K, int64_t sqm,
-                                                         const float* __restrict__ srow,
-                                                         int64_t ssm, uint8_t* qb, int64_t sqbm,
-                                                         uint8_t* qbt, int64_t sqbtm, float* sblk,
-                                                         int64_t ssbm) {
+__device__ __forceinline__ void requant_tile(const uint8_t* __restrict__ q, int64_t K, int64_t sqm,
+                                             const float* __restrict__ srow, int64_t ssm, uint8_t* qb,
+                                             int64_t sqbm, uint8_t* qbt, int64_t sqbtm, float* sblk,
+                                             int64_t ssbm, const RowTile rt, int64_t cb) {
   __shared__ float red[kThreads / 64];
   __shared__ uint32_t tileT[128][128 / 4 + 1];
-  const int64_t rb = blockIdx.y, cb = blockIdx.x;
   const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
   const int64_t c = cb * 128 + lane16 * 8;
   float v[8][8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int64_t r = rb * 128 + rg + 16 * i;
+    const int ri = rg + 16 * i;
+    const int64_t r = rt.r0 + ri;
     uint32_t w0 = 0, w1 = 0;
     float sr = 0.0f;
-    if (r < M) {
+    if (ri < rt.nr) {
       sr = srow[r * ssm + cb];
       const uint8_t* qp = q + r * sqm + c;
       if (c + 8 <= K) {
@@ -523,7 +580,7 @@ __global__ __launch_bounds__(kThreads) void k_requant128(const uint8_t* __restri
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t code = ((j < 4 ? w0 : w1) >> (8 * (j & 3))) & 0xffu;
-      const bool valid = (r < M) && (c + j < K);
+      const bool valid = (ri < rt.nr) && (c + j < K);
       v[i][j] = valid ? __fmul_rn(e4m3_to_f32(code), sr) : 0.0f;
     }
   }
@@ -542,9 +599,9 @@ __global__ __launch_bounds__(kThreads) void k_requant128(const uint8_t* __restri
   if (qb) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int64_t r = rb * 128 + rg + 16 * i;
-      if (r >= M) continue;
-      uint8_t* qp = qb + r * sqbm + c;
+      const int ri = rg + 16 * i;
+      if (ri >= rt.nr) continue;
+      uint8_t* qp = qb + (rt.r0 + ri) * sqbm + c;
       if (c + 8 <= K) {
         *reinterpret_cast<uint2*>(qp) = make_uint2(codes[i][0], codes[i][1]);
       } else {
@@ -563,22 +620,30 @@ __global__ __launch_bounds__(kThreads) void k_requant128(const uint8_t* __restri
         tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * i] =
             (uint8_t)((codes[i][j >> 2] >> (8 * (j & 3))) & 0xffu);
     __syncthreads();
-    for (int idx = threadIdx.x; idx < 128 * 8; idx += kThreads) {
-      const int tc = idx >> 3, seg = idx & 7;
-      const int64_t n = cb * 128 + tc;
-      const int64_t m0 = rb * 128 + seg * 16;
-      if (n >= K) continue;
-      const uint32_t* src = &tileT[tc][seg * 4];
-      uint8_t* dst = qbt + n * sqbtm + m0;
-      if (m0 + 16 <= M && (((uintptr_t)dst) & 15u) == 0) {
-        *reinterpret_cast<uint4*>(dst) = make_uint4(src[0], src[1], src[2], src[3]);
-      } else {
-        for (int k = 0; k < 16; ++k)
-          if (m0 + k < M) dst[k] = (uint8_t)((src[k >> 2] >> (8 * (k & 3))) & 0xffu);
-      }
-    }
+    store_tile_t(tileT, qbt, sqbtm, cb * 128, K, rt.t0, rt.tw);
   }
-  if (threadIdx.x == 0) sblk[rb * ssbm + cb] = s;
+  if (threadIdx.x == 0) sblk[rt.tb * ssbm + cb] = s;
+}
+
+__global__ __launch_bounds__(kThreads) void k_requant128(const uint8_t* __restrict__ q, int64_t M,
+                                                         int64_t K, int64_t sqm,
+                                                         const float* __restrict__ srow,
+                                                         int64_t ssm, uint8_t* qb, int64_t sqbm,
+                                                         uint8_t* qbt, int64_t sqbtm, float* sblk,
+                                                         int64_t ssbm) {
+  requant_tile(q, K, sqm, srow, ssm, qb, sqbm, qbt, sqbtm, sblk, ssbm, dense_tile(blockIdx.y, M),
+               blockIdx.x);
+}
+
+// Grouped: block row = one 128-token chunk of an expert; block scales are indexed by
+// the chunk's padded position, codes by the input row (qb) or the padded column (qbt).
+__global__ __launch_bounds__(kThreads) void k_requant128_grouped(
+    const uint8_t* __restrict__ q, int64_t T, int64_t K, int64_t sqm, const float* __restrict__ srow,
+    int64_t ssm, uint8_t* qb, int64_t sqbm, uint8_t* qbt, int64_t sqbtm, float* sblk, int64_t ssbm,
+    const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t E, int64_t tcap) {
+  RowTile rt;
+  if (!grouped_tile(starts, ends, E, T, blockIdx.y, tcap, rt)) return;  // before any barrier
+  requant_tile(q, K, sqm, srow, ssm, qb, sqbm, qbt, sqbtm, sblk, ssbm, rt, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -749,6 +814,54 @@ int cin_quant_dual(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t s
   if (rc != CIN_OK) return rc;
   return cin_quant_rowwise(dy, dy_dtype, N, M, sdn, sdm, 128, round_scale, qt, sqtm, st, sstm,
                            stream);
+}
+
+int cin_quant_dual_grouped(const void* dy, int dy_dtype, int64_t T, int64_t N, int64_t sdm,
+                           const int64_t* starts, const int64_t* ends, int64_t E, int round_scale,
+                           uint8_t* q, int64_t sqm, float* s, int64_t ssm, uint8_t* qt,
+                           int64_t sqtm, float* st, int64_t sstm, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(dy_dtype), "quant_dual_grouped: unsupported dtype %d", dy_dtype);
+  CIN_CHECK_ARG(T >= 0 && N >= 0 && E >= 0, "quant_dual_grouped: negative shape");
+  if (T == 0 || N == 0 || E == 0) return CIN_OK;
+  CIN_CHECK_ARG(dy && q && s && qt && st && starts && ends, "quant_dual_grouped: null pointer");
+  const int es = elem_size(dy_dtype);
+  CIN_CHECK_ARG(aligned(dy, 16) && (sdm * es) % 16 == 0 && sdm >= N,
+                "quant_dual_grouped: dy rows must be contiguous and 16-byte aligned");
+  CIN_CHECK_ARG(aligned(q, 8) && sqm % 8 == 0 && sqm >= N && ssm >= cdiv(N, 128),
+                "quant_dual_grouped: bad row-wise outputs");
+  CIN_CHECK_ARG(sqtm >= 128 && sstm >= sqtm / 128,
+                "quant_dual_grouped: transposed rows must hold the padded token axis");
+  CIN_CHECK_ARG(cdiv(T, 128) + E < 65536, "quant_dual_grouped: too many chunks");
+  hipStream_t stream_ = static_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)cdiv(N, 128), (unsigned)(cdiv(T, 128) + E));
+  if (dy_dtype == CIN_DT_BF16)
+    hipLaunchKernelGGL(k_dual128_grouped<CIN_DT_BF16>, grid, kThreads, 0, stream_, dy, T, N, sdm,
+                       round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm, starts, ends, E, sqtm);
+  else if (dy_dtype == CIN_DT_F16)
+    hipLaunchKernelGGL(k_dual128_grouped<CIN_DT_F16>, grid, kThreads, 0, stream_, dy, T, N, sdm,
+                       round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm, starts, ends, E, sqtm);
+  else
+    hipLaunchKernelGGL(k_dual128_grouped<CIN_DT_F32>, grid, kThreads, 0, stream_, dy, T, N, sdm,
+                       round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm, starts, ends, E, sqtm);
+  return cin_check_launch("quant_dual_grouped");
+}
+
+int cin_requant_row_to_block_grouped(const uint8_t* q, int64_t T, int64_t K, int64_t sqm,
+                                     const float* srow, int64_t ssm, const int64_t* starts,
+                                     const int64_t* ends, int64_t E, uint8_t* qbt, int64_t sqbtm,
+                                     float* sblk, int64_t ssbm, void* stream) {
+  CIN_CHECK_ARG(T >= 0 && K >= 0 && E >= 0, "requant_grouped: negative shape");
+  if (T == 0 || K == 0 || E == 0) return CIN_OK;
+  CIN_CHECK_ARG(q && srow && qbt && sblk && starts && ends, "requant_grouped: null pointer");
+  CIN_CHECK_ARG(aligned(q, 8) && sqm % 8 == 0 && sqm >= K, "requant_grouped: q must be 8-byte aligned rows");
+  CIN_CHECK_ARG(sqbtm >= 128 && ssm >= cdiv(K, 128) && ssbm >= cdiv(K, 128),
+                "requant_grouped: bad output strides");
+  CIN_CHECK_ARG(cdiv(T, 128) + E < 65536, "requant_grouped: too many chunks");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)cdiv(K, 128), (unsigned)(cdiv(T, 128) + E));
+  hipLaunchKernelGGL(k_requant128_grouped, grid, kThreads, 0, s, q, T, K, sqm, srow, ssm,
+                     (uint8_t*)nullptr, (int64_t)0, qbt, sqbtm, sblk, ssbm, starts, ends, E, sqbtm);
+  return cin_check_launch("requant_row_to_block_grouped");
 }
 
 int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm,

@@ -11,7 +11,8 @@ from __future__ import annotations
 import torch
 
 from ._lib import call, dtype_code, ptr, stream_of
-from .kernels import _cdiv, _kcontig, _require
+from .kernels import (_cdiv, _kcontig, _require, quantize_fp8_blockwise_t,
+                      quantize_fp8_rowwise)
 
 
 def fp8_grouped_gemm(a_codes: torch.Tensor, a_scales: torch.Tensor, w_codes: torch.Tensor,
@@ -47,3 +48,214 @@ def fp8_grouped_gemm(a_codes: torch.Tensor, a_scales: torch.Tensor, w_codes: tor
          w_scales.stride(0), w_scales.stride(1), w_scales.stride(2), ptr(starts), ptr(ends), E, T,
          N, K, ptr(out), dtype_code(out), out.stride(0), stream_of(aq))
     return out
+
+
+# ---------------------------------------------------------------------------
+# MoE backward.  The reference grouped GEMM has no backward (src/layers.py:69-75 runs
+# it without autograd); these apply the FP8MatmulFunction.backward recipe
+# (src/kernels.py:763-794) to each expert's row slice [starts[e], ends[e]).
+# ---------------------------------------------------------------------------
+def padded_capacity(T: int, E: int) -> int:
+    """Columns that always hold the padded token axis (cin_grouped.h): 128 (ceil(T/128) + E)."""
+    return 128 * (_cdiv(T, 128) + E)
+
+
+def _ranges(expert_starts: torch.Tensor, expert_ends: torch.Tensor):
+    starts = expert_starts.to(torch.int64).contiguous()
+    ends = expert_ends.to(torch.int64).contiguous()
+    _require(starts.numel() == ends.numel(), "expert_starts and expert_ends differ in length")
+    return starts, ends
+
+
+def quantize_fp8_dual_grouped(grad: torch.Tensor, expert_starts: torch.Tensor,
+                              expert_ends: torch.Tensor, round_scale: bool = False):
+    """Grouped dual quantization of an output gradient dC [T, N].
+
+    Returns (q [T, N], s [T, ceil(N/128)], qt [N, Tcap], st [N, Tcap/128]):
+      q, s   -- quantize_fp8_rowwise(dC) for every row inside an expert range (the
+                dgrad operand);
+      qt, st -- for each expert, quantize_fp8_rowwise(dC[s_e:e_e].t().contiguous())
+                stored at the expert's padded columns (the wgrad operand).
+    """
+    _require(grad.is_cuda, "Input must be on CUDA")
+    _require(grad.ndim == 2, "Input must be 2D")
+    if grad.stride(1) != 1 or (grad.stride(0) * grad.element_size()) % 16 or grad.data_ptr() % 16:
+        grad = grad.contiguous()
+    starts, ends = _ranges(expert_starts, expert_ends)
+    T, N = grad.shape
+    E = starts.numel()
+    cap = padded_capacity(T, E)
+    dev = grad.device
+    q = torch.empty((T, N), dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty((T, _cdiv(N, 128)), dtype=torch.float32, device=dev)
+    qt = torch.empty((N, cap), dtype=torch.float8_e4m3fn, device=dev)
+    st = torch.empty((N, cap // 128), dtype=torch.float32, device=dev)
+    call("cin_quant_dual_grouped", ptr(grad), dtype_code(grad), T, N, grad.stride(0), ptr(starts),
+         ptr(ends), E, int(bool(round_scale)), ptr(q), q.stride(0), ptr(s), s.stride(0), ptr(qt),
+         qt.stride(0), ptr(st), st.stride(0), stream_of(grad))
+    return q, s, qt, st
+
+
+def requantize_grouped_t(x_fp8: torch.Tensor, x_scale: torch.Tensor, expert_starts: torch.Tensor,
+                         expert_ends: torch.Tensor):
+    """Per-expert 128x128 block re-quantization of row-wise codes, transposed on the padded
+    token axis: (codes [K, Tcap], block scales [Tcap/128, ceil(K/128)]).  For each expert it
+    equals quantize_fp8_blockwise(dequantize_fp8_rowwise(x_fp8, x_scale)[s_e:e_e]) (reference
+    src/kernels.py:784-787 per slice)."""
+    _require(x_fp8.is_cuda, "Input must be on CUDA")
+    q = x_fp8.view(torch.uint8) if x_fp8.dtype == torch.float8_e4m3fn else x_fp8
+    if q.stride(1) != 1 or q.stride(0) % 8 or q.data_ptr() % 8:
+        q = q.contiguous()
+    starts, ends = _ranges(expert_starts, expert_ends)
+    T, K = q.shape
+    E = starts.numel()
+    cap = padded_capacity(T, E)
+    qbt = torch.empty((K, cap), dtype=torch.float8_e4m3fn, device=q.device)
+    sblk = torch.empty((cap // 128, _cdiv(K, 128)), dtype=torch.float32, device=q.device)
+    call("cin_requant_row_to_block_grouped", ptr(q), T, K, q.stride(0), ptr(x_scale),
+         x_scale.stride(0), ptr(starts), ptr(ends), E, ptr(qbt), qbt.stride(0), ptr(sblk),
+         sblk.stride(0), stream_of(q))
+    return qbt, sblk
+
+
+def fp8_grouped_wgrad(g_t: torch.Tensor, g_st: torch.Tensor, x_bt: torch.Tensor,
+                      x_blk: torch.Tensor, expert_starts: torch.Tensor, expert_ends: torch.Tensor,
+                      num_tokens: int, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """dW_e = dC_e^T . X_e for every expert in one launch -> [E, N, K].
+
+    g_t/g_st from quantize_fp8_dual_grouped, x_bt/x_blk from requantize_grouped_t (same
+    expert ranges over num_tokens rows).  Experts without tokens get zeros."""
+    _require(g_t.is_cuda and x_bt.is_cuda, "Input must be on CUDA")
+    starts, ends = _ranges(expert_starts, expert_ends)
+    E = starts.numel()
+    N, cap = g_t.shape
+    K = x_bt.shape[0]
+    _require(x_bt.shape[1] == cap, "operands must share the padded token axis")
+    a = g_t.view(torch.uint8)
+    b = x_bt.view(torch.uint8)
+    out = torch.empty((E, N, K), dtype=out_dtype, device=g_t.device)
+    call("cin_grouped_gemm_fp8_wgrad", ptr(a), a.stride(0), ptr(g_st), g_st.stride(0), ptr(b),
+         b.stride(0), ptr(x_blk), x_blk.stride(0), ptr(starts), ptr(ends), E, int(num_tokens), cap,
+         N, K, ptr(out), dtype_code(out), out.stride(1), out.stride(0), stream_of(a))
+    return out
+
+
+def fp8_grouped_dgrad(g_fp8: torch.Tensor, g_scale: torch.Tensor, w_codes_t: torch.Tensor,
+                      w_scales: torch.Tensor, expert_starts: torch.Tensor,
+                      expert_ends: torch.Tensor, n_out_per_expert: int,
+                      out_dtype: torch.dtype = torch.float32,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """dA[r] = dC[r] . W_e for rows r of expert e -> [T, K].
+
+    w_codes_t [K, E*N] and w_scales [E*N/128, ceil(K/128)] are quantize_fp8_blockwise_t of
+    the stacked weights W.reshape(E*N, K); n_out_per_expert = N (multiple of 128)."""
+    _require(g_fp8.is_cuda and w_codes_t.is_cuda, "Input must be on CUDA")
+    starts, ends = _ranges(expert_starts, expert_ends)
+    E = starts.numel()
+    T, N = g_fp8.shape
+    K, EN = w_codes_t.shape
+    _require(N == n_out_per_expert and EN == E * N and N % 128 == 0,
+             "w_codes_t must be [K, E*N] with N a multiple of 128")
+    aq, _ = _kcontig(g_fp8, N)
+    b = w_codes_t.view(torch.uint8)
+    if out is None:
+        out = torch.empty((T, K), dtype=out_dtype, device=g_fp8.device)
+    nbk = w_scales.stride(0)  # scale columns per row block
+    # B_e[k, n] = W_e[n, k]: codes at w_codes_t + e*N (row stride E*N); its block scales
+    # [kb_out, nb_red] are w_scales[e*N/128 + nb_red, kb_out]
+    call("cin_grouped_gemm_fp8", ptr(aq), aq.stride(0), ptr(g_scale), g_scale.stride(0),
+         g_scale.stride(1), ptr(b), N, b.stride(0), ptr(w_scales), (N // 128) * nbk, 1, nbk,
+         ptr(starts), ptr(ends), E, T, K, N, ptr(out), dtype_code(out), out.stride(0),
+         stream_of(aq))
+    return out
+
+
+class FP8GroupedExpertsFunction(torch.autograd.Function):
+    """SwiGLU experts in FP8: out = W3_e (silu(h1) * h2), [h1 h2] = W12_e x for each expert's
+    rows (reference GroupedExperts.forward, src/layers.py:56-87: GEMM(w12), silu * mul in
+    fp32, cast to the input dtype, GEMM(w3), fp32 out).  Both GEMMs use 1x128 activation
+    tiles and 128x128 per-expert weight blocks; the backward applies the
+    FP8MatmulFunction.backward recipe per expert (grouped dual quantization of the
+    gradient, grouped dgrad with the transposed weight codes, grouped re-quantization of
+    the saved inputs and grouped wgrad)."""
+
+    @staticmethod
+    def forward(ctx, sorted_x, w12, w3, expert_starts, expert_ends):
+        E, H2, D = w12.shape
+        H = H2 // 2
+        starts, ends = _ranges(expert_starts, expert_ends)
+        xq, xs = quantize_fp8_rowwise(sorted_x)
+        w12f = w12 if w12.dtype == torch.float32 else w12.float()
+        w12q, w12qt, w12s = quantize_fp8_blockwise_t(w12f.reshape(E * H2, D))
+        h12 = fp8_grouped_gemm(xq, xs, w12q.view(E, H2, D), w12s.view(E, H2 // 128, -1),
+                               starts, ends, out_dtype=torch.bfloat16,
+                               out=torch.zeros((sorted_x.shape[0], H2), dtype=torch.bfloat16,
+                                               device=sorted_x.device))
+        h1, h2 = h12.float().chunk(2, dim=-1)
+        h = (torch.nn.functional.silu(h1) * h2).to(sorted_x.dtype)
+        hq, hs = quantize_fp8_rowwise(h)
+        w3f = w3 if w3.dtype == torch.float32 else w3.float()
+        w3q, w3qt, w3s = quantize_fp8_blockwise_t(w3f.reshape(E * D, H))
+        out = fp8_grouped_gemm(hq, hs, w3q.view(E, D, H), w3s.view(E, D // 128, -1), starts, ends,
+                               out_dtype=torch.float32,
+                               out=torch.zeros((sorted_x.shape[0], D), dtype=torch.float32,
+                                               device=sorted_x.device))
+        ctx.save_for_backward(xq, xs, w12qt, w12s, h12, hq, hs, w3qt, w3s, starts, ends)
+        ctx.dims = (E, H, D)
+        ctx.x_dtype = sorted_x.dtype
+        ctx.w_dtypes = (w12.dtype, w3.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        xq, xs, w12qt, w12s, h12, hq, hs, w3qt, w3s, starts, ends = ctx.saved_tensors
+        E, H, D = ctx.dims
+        g = grad_out.contiguous()
+        gq, gs, gqt, gst = quantize_fp8_dual_grouped(g, starts, ends)
+        dh = fp8_grouped_dgrad(gq, gs, w3qt, w3s, starts, ends, D,
+                               out=torch.zeros((g.shape[0], H), dtype=torch.float32, device=g.device))
+        hbt, hblk = requantize_grouped_t(hq, hs, starts, ends)
+        dw3 = fp8_grouped_wgrad(gqt, gst, hbt, hblk, starts, ends, g.shape[0])
+        # silu(h1) * h2 in fp32 (the forward's cast to the input dtype passes the gradient)
+        h1, h2 = h12.float().chunk(2, dim=-1)
+        sig = torch.sigmoid(h1)
+        silu = h1 * sig
+        dh12 = torch.cat([dh * h2 * (sig * (1.0 + h1 * (1.0 - sig))), dh * silu], dim=-1)
+        dq, ds, dqt, dst = quantize_fp8_dual_grouped(dh12, starts, ends)
+        dx = fp8_grouped_dgrad(dq, ds, w12qt, w12s, starts, ends, 2 * H,
+                               out=torch.zeros((g.shape[0], D), dtype=torch.float32, device=g.device))
+        xbt, xblk = requantize_grouped_t(xq, xs, starts, ends)
+        dw12 = fp8_grouped_wgrad(dqt, dst, xbt, xblk, starts, ends, g.shape[0])
+        return (dx.to(ctx.x_dtype), dw12.to(ctx.w_dtypes[0]), dw3.to(ctx.w_dtypes[1]), None, None)
+
+
+class GroupedExperts(torch.nn.Module):
+    """Drop-in for the reference GroupedExperts (src/layers.py:34-87): stacked SwiGLU expert
+    weights w12 [E, 2H, D] (w1 and w2 fused) and w3 [E, D, H], N(0, 0.02) init, forward on
+    tokens sorted by expert.  On the GPU it runs FP8 (FP8GroupedExpertsFunction, with
+    autograd); on the CPU it keeps the reference's per-expert loop (src/layers.py:78-87)."""
+
+    def __init__(self, n_experts: int, d_model: int, hidden_dim: int):
+        super().__init__()
+        self.n_experts = n_experts
+        self.d_model = d_model
+        self.hidden_dim = hidden_dim
+        self.w12 = torch.nn.Parameter(torch.empty(n_experts, 2 * hidden_dim, d_model))
+        self.w3 = torch.nn.Parameter(torch.empty(n_experts, d_model, hidden_dim))
+        torch.nn.init.normal_(self.w12, mean=0.0, std=0.02)
+        torch.nn.init.normal_(self.w3, mean=0.0, std=0.02)
+
+    def forward(self, sorted_x, expert_starts, expert_ends, max_expert_tokens=None):
+        if sorted_x.is_cuda:
+            return FP8GroupedExpertsFunction.apply(sorted_x, self.w12, self.w3, expert_starts,
+                                                   expert_ends)
+        out = torch.zeros(sorted_x.size(0), self.d_model, device=sorted_x.device,
+                          dtype=sorted_x.dtype)
+        for i in range(self.n_experts):
+            start, end = int(expert_starts[i]), int(expert_ends[i])
+            if end > start:
+                h12 = torch.nn.functional.linear(sorted_x[start:end], self.w12[i])
+                h1, h2 = h12.chunk(2, dim=-1)
+                out[start:end] = torch.nn.functional.linear(torch.nn.functional.silu(h1) * h2,
+                                                            self.w3[i])
+        return out

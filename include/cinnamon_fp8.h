@@ -154,6 +154,62 @@ int cin_grouped_gemm_fp8(const uint8_t* A, int64_t lda, const float* sa, int64_t
                          const int64_t* ends, int64_t E, int64_t T, int64_t N, int64_t K, void* C,
                          int c_dtype, int64_t ldc, void* stream);
 
+/*
+ * MoE backward (grouped dgrad / wgrad).  The reference's grouped GEMM has no backward
+ * (src/kernels.py:440-581, src/layers.py:69-75 run it without autograd); these entry
+ * points apply the FP8MatmulFunction.backward recipe (src/kernels.py:763-794) to each
+ * expert's row slice [starts[e], ends[e]).
+ *
+ * Padded token axis: expert e's tokens are split into 128-token chunks aligned at its
+ * first row; chunk c sits at columns [p_e + 128 c, p_e + 128 c + 128) of the transposed
+ * outputs, p_e = sum_{e' < e} 128 * ceil(m_e' / 128), and the columns past the expert's
+ * last token hold code 0.  The padded length never exceeds 128 * (ceil(T / 128) + E);
+ * outputs sized with that many columns always suffice.
+ */
+
+/*
+ * Grouped dual quantization of the output gradient dC [T, N] (contiguous rows):
+ *   q  [T, N] 1x128 row tiles (row stride sqm), s [T, ceil(N/128)] (row stride ssm)
+ *      -- the dgrad operand, as quantize_fp8_rowwise(dC) for every row inside a range;
+ *   qt [N, Tpad] per-expert 128x1 column tiles on the padded axis (row stride sqtm =
+ *      the padded capacity), st [N, sqtm / 128] (row stride sstm >= sqtm / 128)
+ *      -- the wgrad operand, as quantize_fp8_rowwise(dC[s_e:e_e].t()) for each expert.
+ */
+int cin_quant_dual_grouped(const void* dy, int dy_dtype, int64_t T, int64_t N, int64_t sdm,
+                           const int64_t* starts, const int64_t* ends, int64_t E, int round_scale,
+                           uint8_t* q, int64_t sqm, float* s, int64_t ssm, uint8_t* qt,
+                           int64_t sqtm, float* st, int64_t sstm, void* stream);
+
+/*
+ * Grouped re-quantization of the expert inputs for wgrad: for each expert, 128x128 blocks
+ * of quantize_fp8_blockwise(dequantize_fp8_rowwise(q, srow)[s_e:e_e]) (reference
+ * src/kernels.py:784-787 per slice), written transposed on the padded axis:
+ *   q    [T, K] row-wise codes (row stride sqm), srow [T, ceil(K/128)] (row stride ssm)
+ *   qbt  [K, Tpad] block codes (row stride sqbtm = padded capacity)
+ *   sblk [sqbtm / 128, ceil(K/128)] block scales, row = padded chunk (row stride ssbm)
+ */
+int cin_requant_row_to_block_grouped(const uint8_t* q, int64_t T, int64_t K, int64_t sqm,
+                                     const float* srow, int64_t ssm, const int64_t* starts,
+                                     const int64_t* ends, int64_t E, uint8_t* qbt, int64_t sqbtm,
+                                     float* sblk, int64_t ssbm, void* stream);
+
+/*
+ * Grouped weight gradient, one launch over all experts:
+ *   C_e[n, k] = sum over expert e's padded chunks j of
+ *               sa[n, j] * sb[j, k / 128] * sum_{t in chunk j} A[n, t] * B[k, t]
+ * i.e. dW_e = dC_e^T X_e with A = qt/st of cin_quant_dual_grouped (A[N, Tpad], lda) and
+ * B = qbt/sblk of cin_requant_row_to_block_grouped (B[K, Tpad], ldb; sb row stride ssbm).
+ * T is the token count the ranges refer to; tcap the padded columns A and B hold (an
+ * expert whose padded range would pass tcap gets zeros).  C is [E, N, K] (row stride
+ * ldc, expert stride sce); experts without tokens get zeros.
+ * Needs N >= 256, K >= 256, K % 128 == 0.
+ */
+int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam,
+                               const uint8_t* B, int64_t ldb, const float* sb, int64_t ssbm,
+                               const int64_t* starts, const int64_t* ends, int64_t E, int64_t T,
+                               int64_t tcap, int64_t N, int64_t K, void* C, int c_dtype,
+                               int64_t ldc, int64_t sce, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

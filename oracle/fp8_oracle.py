@@ -202,6 +202,140 @@ def grouped_gemm_ref(a_codes, a_scales, w_codes, w_scales, starts, ends) -> torc
 
 
 # ---------------------------------------------------------------------------
+# Grouped (MoE) backward: the FP8MatmulFunction.backward recipe (src/kernels.py:763-794)
+# applied to each expert's row slice.  The reference has no grouped backward, so these
+# are defined here and pinned by the dense chain (one expert covering every row is the
+# dense backward) and by per-expert brute force in the tests.
+# ---------------------------------------------------------------------------
+def expert_slices(starts, ends, T):
+    """[(e, s, t)] with the range clamped to [0, T) (empty ranges have t == s)."""
+    out = []
+    for e in range(len(starts)):
+        s = min(max(int(starts[e]), 0), T)
+        t = min(max(int(ends[e]), s), T)
+        out.append((e, s, t))
+    return out
+
+
+def padded_offsets(starts, ends, T):
+    """Padded token-axis offset p_e and chunk count of each expert (128-token chunks)."""
+    p, offs = 0, []
+    for e, s, t in expert_slices(starts, ends, T):
+        n = -(-(t - s) // 128)
+        offs.append((p, n))
+        p += 128 * n
+    return offs
+
+
+def grouped_dual_ref(dc: torch.Tensor, starts, ends, round_scale: bool = False):
+    """Per expert: (codes, scales) of quant_rowwise(dC[s:t]) (the dgrad operand, rows
+    s..t-1) and of quant_rowwise(dC[s:t].t().contiguous()) (the wgrad operand)."""
+    out = []
+    for e, s, t in expert_slices(starts, ends, dc.shape[0]):
+        if t == s:
+            out.append(None)
+            continue
+        rq, rs = quant_rowwise(dc[s:t], 128, round_scale)                      # :771
+        tq, ts = quant_rowwise(dc[s:t].t().contiguous(), 128, round_scale)     # :781-783
+        out.append((rq, rs, tq, ts))
+    return out
+
+
+def grouped_requant_ref(x_codes: torch.Tensor, x_scales: torch.Tensor, starts, ends):
+    """Per expert: quant_blockwise(dequant_rowwise(x)[s:t]) (src/kernels.py:784-787)."""
+    xd = dequant_rowwise(x_codes, x_scales, 128)
+    out = []
+    for e, s, t in expert_slices(starts, ends, x_codes.shape[0]):
+        out.append(None if t == s else quant_blockwise(xd[s:t], 128, 128, False))
+    return out
+
+
+def grouped_dgrad_ref(g_codes, g_scales, w_codes, w_scales, starts, ends) -> torch.Tensor:
+    """dA[s:t] = dC[s:t] . W_e on dequantized operands (src/kernels.py:774 per expert).
+    w_codes [E, N, K], w_scales [E, N/128, K/128]; fp32 [T, K], 0 outside every range."""
+    T = g_codes.shape[0]
+    E, N, K = w_codes.shape
+    out = torch.zeros(T, K, dtype=torch.float32)
+    for e, s, t in expert_slices(starts, ends, T):
+        if t > s:
+            out[s:t] = gemm_ref(g_codes[s:t], g_scales[s:t], w_codes[e], w_scales[e])
+    return out
+
+
+def grouped_wgrad_ref(dual, requant, E, N, K) -> torch.Tensor:
+    """dW_e = dC_e^T . Xb_e (src/kernels.py:788 per expert) from grouped_dual_ref and
+    grouped_requant_ref outputs; fp32 [E, N, K], zeros for experts without rows."""
+    out = torch.zeros(E, N, K, dtype=torch.float32)
+    for e in range(E):
+        if dual[e] is not None:
+            _, _, tq, ts = dual[e]
+            xb, xbs = requant[e]
+            out[e] = gemm_ref(tq, ts, xb, xbs)
+    return out
+
+
+def grouped_experts_ref(x: torch.Tensor, w12: torch.Tensor, w3: torch.Tensor, starts, ends,
+                        g_out: torch.Tensor | None = None, quantize: bool = True) -> dict:
+    """FP8 SwiGLU experts (src/layers.py:69-75 with FP8 GEMMs), forward and backward.
+
+    x [T, D], w12 [E, 2H, D], w3 [E, D, H] (fp32 masters), g_out [T, D] fp32.  Every GEMM
+    is dequantize-then-fp32-matmul (gemm_ref) on operands quantized as the device path
+    does: activations and gradients 1x128 row-wise, weights 128x128, the wgrad operands
+    per expert (gradient 128x1 column tiles, inputs re-quantized to 128x128 blocks of the
+    dequantized row-wise codes); h12 is rounded to bf16 as the device stores it.  With
+    quantize=False every quantization (and the bf16 rounding) is the identity, which
+    turns this into plain fp32 SwiGLU experts and their exact gradients.
+    Returns fp32 out [T, D] and, with g_out, dx [T, D], dw12 [E, 2H, D], dw3 [E, D, H].
+    """
+    T, D = x.shape
+    E, H2, _ = w12.shape
+    H = H2 // 2
+    if quantize:
+        rowq = lambda t: dequant_rowwise(*quant_rowwise(t))                       # noqa: E731
+        blkq = lambda t: dequant_block(*quant_blockwise(t))                       # noqa: E731
+        colq = lambda t: dequant_rowwise(*quant_rowwise(t.t().contiguous())).t()  # noqa: E731
+        bf16 = lambda t: t.to(torch.bfloat16).float()                             # noqa: E731
+    else:
+        rowq = blkq = colq = bf16 = lambda t: t.float()                           # noqa: E731
+    sl = [(s, t) for _, s, t in expert_slices(starts, ends, T)]
+    r = {}
+    xd = rowq(x)
+    w12d = blkq(w12.float().reshape(E * H2, D)).view(E, H2, D)
+    w3d = blkq(w3.float().reshape(E * D, H)).view(E, D, H)
+    h12 = torch.zeros(T, H2)
+    for e, (s, t) in enumerate(sl):
+        if t > s:
+            h12[s:t] = bf16(xd[s:t] @ w12d[e].t())
+    h1, h2 = h12[:, :H], h12[:, H:]
+    h = (torch.nn.functional.silu(h1) * h2).to(x.dtype)
+    hd = rowq(h)
+    out = torch.zeros(T, D)
+    for e, (s, t) in enumerate(sl):
+        if t > s:
+            out[s:t] = hd[s:t] @ w3d[e].t()
+    r["out"] = out
+    if g_out is None:
+        return r
+    g_row = rowq(g_out)
+    dh = torch.zeros(T, H)
+    r["dw3"] = torch.zeros(E, D, H)
+    for e, (s, t) in enumerate(sl):
+        if t > s:
+            dh[s:t] = g_row[s:t] @ w3d[e]                                    # dgrad (:774)
+            r["dw3"][e] = colq(g_out[s:t]).t() @ blkq(hd[s:t])              # wgrad (:781-788)
+    sig = torch.sigmoid(h1)
+    dh12 = torch.cat([dh * h2 * (sig * (1.0 + h1 * (1.0 - sig))), dh * (h1 * sig)], dim=-1)
+    d_row = rowq(dh12)
+    r["dx"] = torch.zeros(T, D)
+    r["dw12"] = torch.zeros(E, H2, D)
+    for e, (s, t) in enumerate(sl):
+        if t > s:
+            r["dx"][s:t] = d_row[s:t] @ w12d[e]
+            r["dw12"][e] = colq(dh12[s:t]).t() @ blkq(xd[s:t])
+    return r
+
+
+# ---------------------------------------------------------------------------
 # Textbook OCP e4m3fn round-to-nearest-even (numpy; independent of torch)
 # ---------------------------------------------------------------------------
 def e4m3_rne_np(x: np.ndarray) -> np.ndarray:

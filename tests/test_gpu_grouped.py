@@ -1,0 +1,170 @@
+"""GPU parity of the MoE (grouped) backward and the FP8 GroupedExperts drop-in.
+
+Codes and scales are compared bit-exactly with the per-expert oracle; GEMM outputs with
+the GEMM tolerance of test_gpu_gemm.py (normwise max relative 2e-3, Frobenius 1e-3, in
+fp32).  Expert ranges include empty experts, single tokens and sizes that are not
+multiples of 128.
+"""
+import pytest
+import torch
+
+from oracle import fp8_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+MAX_REL = 2e-3
+FROB_REL = 1e-3
+COUNTS = [
+    [300, 0, 128, 1, 555, 64, 0, 1000],
+    [512, 512],
+    [0, 0, 700],
+]
+
+
+def _ranges(counts):
+    ends = torch.tensor(counts, dtype=torch.int64).cumsum(0)
+    return ends - torch.tensor(counts, dtype=torch.int64), ends
+
+
+def _u8(t):
+    return t.view(torch.uint8).cpu() if t.dtype == torch.float8_e4m3fn else t.cpu()
+
+
+def _check(got, want, what):
+    mr = orc.normwise_max_rel(got.float().cpu(), want)
+    fr = orc.frob_rel(got.float().cpu(), want)
+    assert mr <= MAX_REL and fr <= FROB_REL, f"{what}: normwise max rel {mr:.3e}, frob rel {fr:.3e}"
+
+
+@pytest.mark.parametrize("counts", COUNTS)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_dual_grouped_bit_exact(kern, dev, counts, dtype):
+    from cinnamon_amd import layers
+    starts, ends = _ranges(counts)
+    T, N = int(ends[-1]), 384
+    g = torch.Generator().manual_seed(len(counts))
+    dc = (torch.randn(T, N, generator=g) * 1e-3).to(dtype)
+    q, s, qt, st = layers.quantize_fp8_dual_grouped(dc.to(dev), starts.to(dev), ends.to(dev))
+    q, s, qt, st = _u8(q), s.cpu(), _u8(qt), st.cpu()
+    want = orc.grouped_dual_ref(dc, starts, ends)
+    for (e, a, b), (p, n), w in zip(orc.expert_slices(starts, ends, T),
+                                    orc.padded_offsets(starts, ends, T), want):
+        if w is None:
+            continue
+        rq, rs, tq, ts = w
+        assert torch.equal(q[a:b], rq.view(torch.uint8)) and torch.equal(s[a:b], rs), f"rows of {e}"
+        m = b - a
+        assert torch.equal(qt[:, p:p + m], tq.view(torch.uint8)), f"transposed codes of {e}"
+        assert torch.count_nonzero(qt[:, p + m:p + 128 * n]) == 0, f"padding of {e}"
+        assert torch.equal(st[:, p // 128:p // 128 + n], ts), f"transposed scales of {e}"
+
+
+@pytest.mark.parametrize("counts", COUNTS)
+def test_requant_grouped_bit_exact(kern, dev, counts):
+    from cinnamon_amd import layers
+    starts, ends = _ranges(counts)
+    T, K = int(ends[-1]), 512
+    g = torch.Generator().manual_seed(7)
+    xq, xs = orc.quant_rowwise(torch.randn(T, K, generator=g).to(torch.bfloat16))
+    qbt, sblk = layers.requantize_grouped_t(xq.to(dev), xs.to(dev), starts.to(dev), ends.to(dev))
+    qbt, sblk = _u8(qbt), sblk.cpu()
+    want = orc.grouped_requant_ref(xq, xs, starts, ends)
+    for (e, a, b), (p, n), w in zip(orc.expert_slices(starts, ends, T),
+                                    orc.padded_offsets(starts, ends, T), want):
+        if w is None:
+            continue
+        bq, bs = w
+        m = b - a
+        assert torch.equal(qbt[:, p:p + m], bq.view(torch.uint8).t()), f"codes of {e}"
+        assert torch.count_nonzero(qbt[:, p + m:p + 128 * n]) == 0, f"padding of {e}"
+        assert torch.equal(sblk[p // 128:p // 128 + n], bs), f"scales of {e}"
+
+
+@pytest.mark.parametrize("counts", COUNTS)
+def test_grouped_wgrad_and_dgrad(kern, dev, counts):
+    from cinnamon_amd import layers
+    starts, ends = _ranges(counts)
+    T, N, K = int(ends[-1]), 256, 384
+    E = len(counts)
+    g = torch.Generator().manual_seed(11)
+    dc = (torch.randn(T, N, generator=g) * 1e-3).to(torch.bfloat16)
+    xq, xs = orc.quant_rowwise(torch.randn(T, K, generator=g).to(torch.bfloat16))
+    w = torch.randn(E, N, K, generator=g) * 0.02
+    dual = orc.grouped_dual_ref(dc, starts, ends)
+    want_w = orc.grouped_wgrad_ref(dual, orc.grouped_requant_ref(xq, xs, starts, ends), E, N, K)
+    sd, ed = starts.to(dev), ends.to(dev)
+    q, s, qt, st = layers.quantize_fp8_dual_grouped(dc.to(dev), sd, ed)
+    xbt, xblk = layers.requantize_grouped_t(xq.to(dev), xs.to(dev), sd, ed)
+    dw = layers.fp8_grouped_wgrad(qt, st, xbt, xblk, sd, ed, T)
+    _check(dw, want_w, f"wgrad {counts}")
+    for e, c in enumerate(counts):
+        if c == 0:
+            assert torch.count_nonzero(dw[e]) == 0
+    # dgrad with the stacked transposed weight codes
+    wq, wqt, ws = kern.quantize_fp8_blockwise_t(w.reshape(E * N, K).to(dev))
+    dx = layers.fp8_grouped_dgrad(q, s, wqt, ws, sd, ed, N,
+                                  out=torch.zeros(T, K, device=dev))
+    gq = torch.zeros(T, N, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    gs = torch.ones(T, N // 128)
+    for (e, a, b), d in zip(orc.expert_slices(starts, ends, T), dual):
+        if d is not None:
+            gq[a:b], gs[a:b] = d[0], d[1]
+    want_x = orc.grouped_dgrad_ref(gq, gs, wq.view(torch.uint8).cpu().view(E, N, K),
+                                   ws.cpu().view(E, N // 128, -1), starts, ends)
+    _check(dx, want_x, f"dgrad {counts}")
+
+
+def test_single_expert_equals_dense_backward(kern, dev):
+    """One expert over every row (T a multiple of 128): the padded axis is the dense axis,
+    so the grouped operands and the grouped wgrad equal the dense ones bit for bit."""
+    from cinnamon_amd import layers
+    T, N, K = 1024, 256, 512
+    g = torch.Generator().manual_seed(5)
+    dc = (torch.randn(T, N, generator=g) * 1e-3).to(torch.bfloat16).to(dev)
+    xq, xs = kern.quantize_fp8_rowwise(torch.randn(T, K, generator=g).to(torch.bfloat16).to(dev))
+    sd, ed = torch.tensor([0], device=dev), torch.tensor([T], device=dev)
+    q, s, qt, st = layers.quantize_fp8_dual_grouped(dc, sd, ed)
+    dq, ds, dqt, dst = kern.quantize_fp8_dual(dc)
+    assert torch.equal(q.view(torch.uint8), dq.view(torch.uint8)) and torch.equal(s, ds)
+    assert torch.equal(qt.view(torch.uint8)[:, :T], dqt.view(torch.uint8))
+    assert torch.equal(st[:, :T // 128], dst)
+    xbt, xblk = layers.requantize_grouped_t(xq, xs, sd, ed)
+    dxbt, dxblk = kern.requantize_rowwise_to_blockwise(xq, xs, transposed=True)
+    assert torch.equal(xbt.view(torch.uint8)[:, :T], dxbt.view(torch.uint8))
+    assert torch.equal(xblk[:T // 128], dxblk)
+    dw = layers.fp8_grouped_wgrad(qt, st, xbt, xblk, sd, ed, T)
+    dense = kern.fp8_gemm_bs(dqt, dst, dxbt, dxblk.t(), torch.float32)
+    assert torch.equal(dw[0], dense)
+
+
+@pytest.mark.parametrize("counts", [[300, 0, 128, 1, 555, 64, 0, 1000], [640, 384]])
+def test_grouped_experts_fwd_bwd(kern, dev, counts):
+    from cinnamon_amd import layers
+    starts, ends = _ranges(counts)
+    T, D, H, E = int(ends[-1]), 256, 256, len(counts)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(T, D, generator=g).to(torch.bfloat16)
+    mod = layers.GroupedExperts(E, D, H)
+    with torch.no_grad():
+        mod.w12.copy_(torch.randn(E, 2 * H, D, generator=g) * 0.02)
+        mod.w3.copy_(torch.randn(E, D, H, generator=g) * 0.02)
+    dy = torch.randn(T, D, generator=g) * 1e-3
+    ref = orc.grouped_experts_ref(x, mod.w12.detach(), mod.w3.detach(), starts, ends, dy)
+    mod = mod.to(dev)
+    xd = x.to(dev).requires_grad_(True)
+    out = mod(xd, starts.to(dev), ends.to(dev))
+    out.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32 and xd.grad.dtype == torch.bfloat16
+    assert mod.w12.grad.dtype == torch.float32 and mod.w3.grad.dtype == torch.float32
+    # The module re-quantizes two GEMM outputs (h = silu(h1) h2 in the forward, dh12 in the
+    # backward).  The device's fp32 GEMM values and the oracle's differ in the last bits
+    # (summation order; h12 is also stored in bf16), and where such a value sits on an
+    # e4m3 rounding boundary its code moves by one step (1/8 of the element).  One such
+    # term changes an output by ~1% of its magnitude, so the end-to-end bound is that
+    # step, not the GEMM tolerance; the stage tests above hold every operand bit-exact and
+    # every GEMM to the GEMM tolerance.
+    for name, got in (("out", out), ("dx", xd.grad), ("dw12", mod.w12.grad), ("dw3", mod.w3.grad)):
+        mr = orc.normwise_max_rel(got.float().cpu(), ref[name])
+        fr = orc.frob_rel(got.float().cpu(), ref[name])
+        assert mr <= 4e-2 and fr <= 5e-3, f"{name}: {mr:.3e} {fr:.3e}"
