@@ -41,6 +41,8 @@ SIGNATURES: dict[str, list] = {
                                _p, _i64, _p, _i64, _p],
     "cin_requant_row_to_block_grouped": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _p, _i64,
                                          _p, _i64, _p],
+    "cin_grouped_gemm_f16": [_p, _i32, _i64, _p, _i32, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64,
+                             _p, _i64, _p],
     "cin_grouped_gemm_fp8_wgrad": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i64,
                                    _i64, _i64, _i64, _p, _i32, _i64, _i64, _p],
 }

@@ -15,6 +15,12 @@ Replaced reference items (src/kernels.py):
   FP8MatmulFunction         :731-794  -> quantizers + cin_quant_dual + cin_requant_row_to_block + GEMMs
   FP8Linear                 :797-840
   convert_to_fp8            :843-905
+  moe_grouped_gemm          :526-581  -> cin_grouped_gemm_f16 (unquantized, fp16 MFMA)
+
+Two reference names outside the FP8 path are kept so that imports resolve
+(src/attention.py:6, tests/test_kernels.py:14): lightning_indexer_fused (:392-432) and
+sparse_attention (:1292-1320).  They are plain torch on the GPU, not part of this build's
+kernels.
 """
 from __future__ import annotations
 
@@ -38,6 +44,9 @@ __all__ = [
     "FP8MatmulFunction",
     "FP8Linear",
     "convert_to_fp8",
+    "moe_grouped_gemm",
+    "lightning_indexer_fused",
+    "sparse_attention",
 ]
 
 
@@ -363,3 +372,66 @@ def convert_to_fp8(model: torch.nn.Module, exclude_names: list | None = None) ->
         round_scale = any(key in name for key in _ROUND_SCALE_NAMES)
         setattr(parent, attr, FP8Linear.from_linear(module, round_scale=round_scale))
     return model
+
+
+# ---------------------------------------------------------------------------
+# Unquantized grouped GEMM (reference src/kernels.py:526-581)
+# ---------------------------------------------------------------------------
+def moe_grouped_gemm(sorted_x: torch.Tensor, weights: torch.Tensor, expert_starts: torch.Tensor,
+                     expert_ends: torch.Tensor, max_expert_tokens: int | None = None) -> torch.Tensor:
+    """C[r] = fp16(fp16(sorted_x[r]) . fp16(weights[e])^T) for the rows r of each expert e.
+
+    sorted_x [T, d_in], weights [E, d_out, d_in] (bf16, fp16 or fp32), expert ranges as
+    device tensors -> fp16 [T, d_out].  One launch covers every expert with a device-side
+    tile table, so max_expert_tokens (a host value in the reference) is not needed and
+    is ignored.  Rows outside every range are left unset (torch.empty, as the reference).
+    """
+    _require(sorted_x.is_cuda and weights.is_cuda, "Input must be on CUDA")
+    _require(sorted_x.ndim == 2 and weights.ndim == 3, "sorted_x must be 2D and weights 3D")
+    T, d_in = sorted_x.shape
+    E, d_out, d_in2 = weights.shape
+    _require(d_in == d_in2, f"Dimension mismatch: {d_in} vs {d_in2}")
+    a = sorted_x if sorted_x.stride(1) == 1 else sorted_x.contiguous()
+    w = weights if weights.stride(2) == 1 else weights.contiguous()
+    starts = expert_starts.to(device=a.device, dtype=torch.int64).contiguous()
+    ends = expert_ends.to(device=a.device, dtype=torch.int64).contiguous()
+    _require(starts.numel() == E and ends.numel() == E, "expert ranges must have n_experts entries")
+    out = torch.empty((T, d_out), dtype=torch.float16, device=a.device)
+    call("cin_grouped_gemm_f16", ptr(a), dtype_code(a), a.stride(0), ptr(w), dtype_code(w),
+         w.stride(0), w.stride(1), ptr(starts), ptr(ends), E, T, d_out, d_in, ptr(out),
+         out.stride(0), stream_of(a))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Outside the FP8 path: torch restatements that keep the reference's names importable
+# ---------------------------------------------------------------------------
+def lightning_indexer_fused(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """I[b, i, j] = sum_h relu(q[b, i, h, :] . k[b, j, :]) * w[b, i, h] in fp32, fp16 out
+    (reference src/kernels.py:392-432).  Plain torch."""
+    _require(q.is_cuda and k.is_cuda, "Inputs must be on CUDA")
+    B, Lq, H, D = q.shape
+    s = torch.matmul(q.float().reshape(B, Lq * H, D), k.float().transpose(1, 2).contiguous())
+    s = s.relu_().reshape(B, Lq, H, -1)
+    return (s * w.float().unsqueeze(-1)).sum(dim=2).to(torch.float16)
+
+
+def sparse_attention(q, k, v, idx, scale=None):
+    """Attention of each query t over the keys idx[b, t, :] with idx <= t (reference
+    src/kernels.py:1176-1320): returns (output [B, H, L, Dv] in q's dtype, attention
+    probabilities [B, H, L, K] fp32, zero where masked).  Plain torch, autograd through the
+    output; the probabilities are returned detached, as the reference's backward ignores
+    their gradient."""
+    if scale is None:
+        scale = q.shape[-1] ** -0.5
+    B, H, L, _ = q.shape
+    valid = idx <= torch.arange(L, device=idx.device).view(1, L, 1)
+    ic = idx.clamp(0, L - 1)
+    bi = torch.arange(B, device=idx.device).view(B, 1, 1)
+    kg = k.float().permute(0, 2, 1, 3)[bi, ic].permute(0, 3, 1, 2, 4)   # [B, H, L, K, D]
+    vg = v.float().permute(0, 2, 1, 3)[bi, ic].permute(0, 3, 1, 2, 4)
+    scores = (q.float().unsqueeze(3) * kg).sum(-1) * scale
+    scores = scores.masked_fill(~valid.unsqueeze(1), float("-inf"))
+    p = torch.softmax(scores, dim=-1).nan_to_num(0.0)
+    out = (p.unsqueeze(-1) * vg).sum(3)
+    return out.to(q.dtype), p.detach()

@@ -210,6 +210,21 @@ int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, i
                                int64_t tcap, int64_t N, int64_t K, void* C, int c_dtype,
                                int64_t ldc, int64_t sce, void* stream);
 
+/*
+ * Unquantized grouped GEMM, replacing the reference's moe_grouped_gemm /
+ * grouped_gemm_kernel (src/kernels.py:526-581, :440-523) as GroupedExperts calls it
+ * (src/layers.py:71, :74): for each expert e with rows [starts[e], ends[e]),
+ *   C[r, n] = fp16( sum_k fp16(A[r, k]) * fp16(B_e[n, k]) )   (fp32 sums)
+ *   A [T, K] of a_dtype (row stride lda, K contiguous)
+ *   B expert e at B + e * sbe: [N, K] of b_dtype (row stride ldb, K contiguous)
+ *   C [T, N] fp16 (row stride ldc); rows outside every range are not written.
+ * One launch, device-side ranges (no max_expert_tokens host value needed).
+ */
+int cin_grouped_gemm_f16(const void* A, int a_dtype, int64_t lda, const void* B, int b_dtype,
+                         int64_t sbe, int64_t ldb, const int64_t* starts, const int64_t* ends,
+                         int64_t E, int64_t T, int64_t N, int64_t K, void* C, int64_t ldc,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -201,6 +201,20 @@ def grouped_gemm_ref(a_codes, a_scales, w_codes, w_scales, starts, ends) -> torc
     return out
 
 
+def grouped_gemm_f16_ref(a: torch.Tensor, w: torch.Tensor, starts, ends) -> torch.Tensor:
+    """Unquantized grouped GEMM of the reference (src/kernels.py:440-523): operands rounded
+    to fp16 (a.to(tl.float16), b.to(tl.float16)), exact products summed in fp64 here.
+    Returns the fp64 result [T, N] before the fp16 store; rows outside every range are 0."""
+    T, K = a.shape
+    E, N, _ = w.shape
+    out = torch.zeros(T, N, dtype=torch.float64)
+    a16 = a.to(torch.float16).double()
+    for e, s, t in expert_slices(starts, ends, T):
+        if t > s:
+            out[s:t] = a16[s:t] @ w[e].to(torch.float16).double().t()
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Grouped (MoE) backward: the FP8MatmulFunction.backward recipe (src/kernels.py:763-794)
 # applied to each expert's row slice.  The reference has no grouped backward, so these

@@ -330,3 +330,33 @@ def test_division_free_quotient_fp32_inputs():
     # the bare product is not enough: without a correction step codes differ
     y0 = (x * r).astype(np.float32)
     assert not np.array_equal(y0, exact)
+
+
+# ---------------------------------------------------------------------------
+# Reference names outside the FP8 path (torch restatements in cinnamon_amd.kernels)
+# ---------------------------------------------------------------------------
+def test_sparse_attention_matches_brute_force():
+    from cinnamon_amd import kernels
+    g = torch.Generator().manual_seed(3)
+    B, H, L, D, Kk = 2, 3, 9, 8, 4
+    q, k, v = (torch.randn(B, H, L, D, generator=g) for _ in range(3))
+    idx = torch.randint(0, L, (B, L, Kk), generator=g)
+    out, p = kernels.sparse_attention(q, k, v, idx, 0.5)
+    for b in range(B):
+        for h in range(H):
+            for t in range(L):
+                sel = [j for j in idx[b, t].tolist()]
+                s = torch.tensor([float(q[b, h, t] @ k[b, h, j]) * 0.5 if j <= t else float("-inf") for j in sel])
+                w = torch.softmax(s, 0) if torch.isfinite(s).any() else torch.zeros(Kk)
+                assert torch.allclose(p[b, h, t], w, atol=1e-6)
+                o = sum(w[i] * v[b, h, sel[i]] for i in range(Kk))
+                assert torch.allclose(out[b, h, t], o, atol=1e-5)
+
+
+def test_grouped_f16_oracle_single_expert_is_matmul():
+    g = torch.Generator().manual_seed(4)
+    a = torch.randn(70, 40, generator=g).to(torch.bfloat16)
+    w = torch.randn(1, 30, 40, generator=g)
+    got = orc.grouped_gemm_f16_ref(a, w, [0], [70])
+    want = a.to(torch.float16).double() @ w[0].to(torch.float16).double().t()
+    assert torch.equal(got, want)
