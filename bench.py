@@ -36,7 +36,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "moe_gateup", "moe_down",
-                                      "dual_quant", "requant", "dgrad", "wgrad", "copy"], default=None,
+                                      "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
+                                      "moe_wgrad", "moe_dgrad", "copy"], default=None,
                    help="run only one kernel in a loop (for profiler runs)")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the config-3 (MoE) and config-4 (backward) component timings")
@@ -149,6 +150,22 @@ def moe_setup(dev):
                 w3q=w3q.view(E, D, H), w3s=w3s.view(E, D // 128, H // 128))
 
 
+def moe_bwd_setup(dev, moe):
+    """Config-3 backward operands for the gate/up GEMM: dH12 [A, 2H] bf16 ~N(0, 1e-3) and the
+    stacked transposed w12 codes [D, E*2H] (the grouped dgrad's B operand)."""
+    import torch
+
+    from cinnamon_amd import kernels
+
+    g = torch.Generator(device=dev).manual_seed(33)
+    E, D, H, A = moe["E"], moe["D"], moe["H"], moe["A"]
+    dh12 = (torch.randn(A, 2 * H, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
+    w12 = (torch.randn(E * 2 * H, D, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    _, w12qt, w12s = kernels.quantize_fp8_blockwise_t(w12, with_rowmajor=False)
+    del w12
+    return dict(dh12=dh12, w12qt=w12qt, w12s=w12s)
+
+
 def bwd_setup(dev, xs0, w0):
     """Config 4: backward of the config-2 shapes; dY[8192, 2048] bf16 ~N(0, 1e-3)."""
     import torch
@@ -220,6 +237,33 @@ def main():
     def moe_down(i):
         layers.fp8_grouped_gemm(hq, hs, moe["w3q"], moe["w3s"], moe["starts"], moe["ends"], out=y3)
 
+    # config-3 backward of the gate/up GEMM (the larger one): grouped dual quantization of
+    # dH12 [A, 2H], grouped re-quantization of the saved X codes, grouped wgrad
+    # dW12 [E, 2H, D] and grouped dgrad dX [A, D]
+    mb = None
+    if full or (args.only or "").startswith("moe_") and args.only not in ("moe_gateup", "moe_down"):
+        if moe is None:
+            moe = moe_setup(dev)
+            xq3, xs3 = kernels.quantize_fp8_rowwise(moe["x"])
+        mb = moe_bwd_setup(dev, moe)
+        gq3, gs3, gqt3, gst3 = layers.quantize_fp8_dual_grouped(mb["dh12"], moe["starts"], moe["ends"])
+        xbt3, xbs3 = layers.requantize_grouped_t(xq3, xs3, moe["starts"], moe["ends"])
+        dx3 = torch.empty((moe["A"], moe["D"]), dtype=torch.bfloat16, device=dev)
+
+    def moe_dual(i):
+        layers.quantize_fp8_dual_grouped(mb["dh12"], moe["starts"], moe["ends"])
+
+    def moe_requant(i):
+        layers.requantize_grouped_t(xq3, xs3, moe["starts"], moe["ends"])
+
+    def moe_wgrad(i):
+        layers.fp8_grouped_wgrad(gqt3, gst3, xbt3, xbs3, moe["starts"], moe["ends"], moe["A"],
+                                 out_dtype=torch.bfloat16)
+
+    def moe_dgrad(i):
+        layers.fp8_grouped_dgrad(gq3, gs3, mb["w12qt"], mb["w12s"], moe["starts"], moe["ends"],
+                                 2 * moe["H"], out=dx3)
+
     if full or args.only in ("dual_quant", "requant", "dgrad", "wgrad"):
         bwd = bwd_setup(dev, xs[0], ws[0])
         gq, gs, gqt, gst = kernels.quantize_fp8_dual(bwd["dy"])
@@ -250,7 +294,8 @@ def main():
     if args.only:
         fn = {"step": step, "gemm": gemm, "quant_x": quant_x, "quant_w": quant_w,
               "moe_gateup": moe_gateup, "moe_down": moe_down, "dual_quant": dual_quant,
-              "requant": requant, "dgrad": dgrad, "wgrad": wgrad}[args.only]
+              "requant": requant, "dgrad": dgrad, "wgrad": wgrad, "moe_dual": moe_dual,
+              "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad}[args.only]
         us = time_loop(fn, args.steps, args.warmup)
         print(json.dumps({"only": args.only, "us_per_call": us}))
         return
@@ -321,6 +366,28 @@ def main():
                         "frac_of_fp8_peak": round(gu_fl / gu_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
             "down": {"us": round(dn_us, 1), "tflops": round(dn_fl / dn_us / 1e6, 1),
                      "frac_of_fp8_peak": round(dn_fl / dn_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
+        }
+    if mb is not None:
+        A, D, H = moe["A"], moe["D"], moe["H"]
+        cap = layers.padded_capacity(A, moe["E"])
+        md_us = time_loop(moe_dual, 5, 1)
+        mr_us = time_loop(moe_requant, 5, 1)
+        mw_us = time_loop(moe_wgrad, 3, 1)
+        mg_us = time_loop(moe_dgrad, 3, 1)
+        fl = 2.0 * A * D * 2 * H
+        # bytes: dual reads dH12 bf16, writes row codes + scales and padded column codes + scales;
+        # requant reads X codes + row scales, writes padded transposed codes + block scales
+        md_bytes = A * 2 * H * 2 + A * 2 * H + A * (2 * H // 128) * 4 + 2 * H * cap + 2 * H * (cap // 128) * 4
+        mr_bytes = A * D + A * (D // 128) * 4 + D * cap + (cap // 128) * (D // 128) * 4
+        out["components"]["config3_moe_backward_gateup"] = {
+            "dual_quant_grouped_dh12": {"us": round(md_us, 1), "gbps": round(md_bytes / md_us / 1e3, 1),
+                                        "frac_of_hbm": round(md_bytes / md_us / 1e3 / PEAK_HBM_GBPS, 4)},
+            "requant_grouped_x": {"us": round(mr_us, 1), "gbps": round(mr_bytes / mr_us / 1e3, 1),
+                                  "frac_of_hbm": round(mr_bytes / mr_us / 1e3 / PEAK_HBM_GBPS, 4)},
+            "wgrad_grouped_dw12": {"us": round(mw_us, 1), "tflops": round(fl / mw_us / 1e6, 1),
+                                   "frac_of_fp8_peak": round(fl / mw_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
+            "dgrad_grouped_dx": {"us": round(mg_us, 1), "tflops": round(fl / mg_us / 1e6, 1),
+                                 "frac_of_fp8_peak": round(fl / mg_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
         }
     if bwd is not None:
         dq_us = time_loop(dual_quant, 20, 3)

@@ -589,7 +589,11 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_wgrad_fp8_256(
     const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t Tn, int64_t tcap,
     int64_t M, int64_t N, void* C, int c_dtype, int64_t ldc, int64_t sce, uint32_t tiles_m,
     uint32_t tiles_n, uint32_t ntot) {
-  const uint32_t b = xcd_remap(blockIdx.x, ntot);
+  // No XCD remap here: a tile's work is its expert's token count, so contiguous runs of
+  // tile ids per XCD would give the XCD holding the popular experts most of the work.
+  // Plain ids spread every expert's tiles round-robin over the 8 XCDs.
+  const uint32_t b = blockIdx.x;
+  (void)ntot;
   const uint32_t per = tiles_m * tiles_n;
   const uint32_t e = b / per, r = b - e * per;
   const uint32_t tm = r / tiles_n, tn = r - tm * tiles_n;

@@ -311,20 +311,76 @@ __global__ __launch_bounds__(kThreads) void k_blockwise_generic(
 // Block-wise 128x128 with contiguous rows: the block stays in registers
 // (8 rows x 8 columns per thread), one HBM read.  The transposed output goes
 // through a padded LDS byte tile so both layouts are written coalesced.
+// Transposed 128 x 128 byte tiles live in LDS as [col][row] with 136-byte rows (34
+// words): a thread owning 8 consecutive rows of a column writes them as one 8-byte store.
+constexpr int kTW = 34;
+typedef uint32_t TileT[128][kTW];
+
+__device__ inline void put_col8(TileT& t, int col, int rgrp, uint32_t lo, uint32_t hi) {
+  *reinterpret_cast<uint2*>(&t[col][rgrp * 2]) = make_uint2(lo, hi);
+}
+
+// Write the tile to dst[(n0 + col) * ld + t0 + row] for its first tw rows and cols < ncols.
+__device__ inline void store_tile_t(const TileT& tileT, uint8_t* dst_base, int64_t ld, int64_t n0,
+                                    int64_t ncols, int64_t t0, int tw) {
+  for (int idx = threadIdx.x; idx < 128 * 8; idx += kThreads) {
+    const int tc = idx >> 3, seg = idx & 7;
+    const int64_t n = n0 + tc;
+    const int m0 = seg * 16;
+    if (n >= ncols || m0 >= tw) continue;
+    const uint2 w0 = *reinterpret_cast<const uint2*>(&tileT[tc][seg * 4]);
+    const uint2 w1 = *reinterpret_cast<const uint2*>(&tileT[tc][seg * 4 + 2]);
+    const uint32_t src[4] = {w0.x, w0.y, w1.x, w1.y};
+    uint8_t* dst = dst_base + n * ld + t0 + m0;
+    if (m0 + 16 <= tw && (((uintptr_t)dst) & 15u) == 0) {
+      *reinterpret_cast<uint4*>(dst) = make_uint4(src[0], src[1], src[2], src[3]);
+    } else {
+      for (int k = 0; k < 16; ++k)
+        if (m0 + k < tw) dst[k] = (uint8_t)((src[k >> 2] >> (8 * (k & 3))) & 0xffu);
+    }
+  }
+}
+
+// 4 x 4 byte transpose: rows a, b, c, d (byte k = column k) -> columns (byte k = row k).
+__device__ inline void t4x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t (&o)[4]) {
+  const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
+  const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
+  const uint32_t cd_lo = __builtin_amdgcn_perm(d, c, 0x05010400u);
+  const uint32_t cd_hi = __builtin_amdgcn_perm(d, c, 0x07030602u);
+  o[0] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u);  // a0 b0 c0 d0
+  o[1] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u);
+  o[2] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u);
+  o[3] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u);
+}
+
+// rows[i] = 8 codes of row i (2 words) -> cols[j] = 8 codes of column j, in row order.
+__device__ inline void t8x8(const uint32_t (&rows)[8][2], uint32_t (&cols)[8][2]) {
+#pragma unroll
+  for (int hr = 0; hr < 2; ++hr)      // rows 4 hr .. 4 hr + 3
+#pragma unroll
+    for (int hc = 0; hc < 2; ++hc) {  // columns 4 hc .. 4 hc + 3
+      uint32_t o[4];
+      t4x4(rows[4 * hr][hc], rows[4 * hr + 1][hc], rows[4 * hr + 2][hc], rows[4 * hr + 3][hc], o);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) cols[4 * hc + k][hr] = o[k];
+    }
+}
+
 template <int DT>
 __global__ __launch_bounds__(kThreads) void k_blockwise128(const void* __restrict__ x, int64_t M,
                                                            int64_t N, int64_t sxm, int round_scale,
                                                            uint8_t* q, int64_t sqm, uint8_t* qt,
                                                            int64_t sqtm, float* sc, int64_t ssm) {
   __shared__ float red[kThreads / 64];
-  __shared__ uint32_t tileT[128][128 / 4 + 1];  // transposed codes, [col][row/4] words
+  __shared__ TileT tileT;  // transposed codes
+  // thread (lane16, rg): rows 8 rg .. 8 rg + 7, columns 8 lane16 .. 8 lane16 + 7
   const int64_t rb = blockIdx.y, cb = blockIdx.x;
-  const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;  // rg: 0..15
+  const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
   const int64_t c = cb * 128 + lane16 * 8;
   Vec8<DT> d[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int64_t r = rb * 128 + rg + 16 * i;
+    const int64_t r = rb * 128 + rg * 8 + i;
     const int64_t nc = (r < M) ? N - c : 0;
     load8<DT>(x, r * sxm + c, nc < 0 ? 0 : (nc > 8 ? 8 : nc), d[i]);
   }
@@ -343,7 +399,7 @@ __global__ __launch_bounds__(kThreads) void k_blockwise128(const void* __restric
   if (q) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int64_t r = rb * 128 + rg + 16 * i;
+      const int64_t r = rb * 128 + rg * 8 + i;
       if (r >= M) continue;
       uint8_t* qp = q + r * sqm + c;
       if (c + 8 <= N) {
@@ -355,31 +411,13 @@ __global__ __launch_bounds__(kThreads) void k_blockwise128(const void* __restric
     }
   }
   if (qt) {
-    // scatter bytes into the transposed tile: tileT[col][row]
-    uint8_t* tb = reinterpret_cast<uint8_t*>(&tileT[0][0]);
-    constexpr int kRowBytes = (128 / 4 + 1) * 4;
+    uint32_t cols[8][2];
+    t8x8(codes, cols);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * i] =
-            (uint8_t)((codes[i][j >> 2] >> (8 * (j & 3))) & 0xffu);
+    for (int j = 0; j < 8; ++j) put_col8(tileT, lane16 * 8 + j, rg, cols[j][0], cols[j][1]);
     __syncthreads();
-    // each thread writes 16 bytes: tile column tc, rows 16*seg .. +16
-    for (int idx = threadIdx.x; idx < 128 * 8; idx += kThreads) {
-      const int tc = idx >> 3, seg = idx & 7;
-      const int64_t n = cb * 128 + tc;
-      const int64_t m0 = rb * 128 + seg * 16;
-      if (n >= N) continue;
-      const uint32_t* src = &tileT[tc][seg * 4];
-      uint8_t* dst = qt + n * sqtm + m0;
-      if (m0 + 16 <= M && (((uintptr_t)dst) & 15u) == 0) {
-        *reinterpret_cast<uint4*>(dst) = make_uint4(src[0], src[1], src[2], src[3]);
-      } else {
-        for (int k = 0; k < 16; ++k)
-          if (m0 + k < M) dst[k] = (uint8_t)((src[k >> 2] >> (8 * (k & 3))) & 0xffu);
-      }
-    }
+    const int64_t left = M - rb * 128;
+    store_tile_t(tileT, qt, sqtm, cb * 128, N, rb * 128, (int)(left < 128 ? left : 128));
   }
   if (threadIdx.x == 0) sc[rb * ssm + cb] = s;
 }
@@ -415,26 +453,6 @@ __device__ inline bool grouped_tile(const int64_t* starts, const int64_t* ends, 
   return true;
 }
 
-// Write a 128 x 128 byte tile held transposed in LDS (tileT[col][row]) to
-// dst[(n0 + col) * ld + t0 + row] for the tile's first tw rows and cols < ncols.
-__device__ inline void store_tile_t(const uint32_t (*tileT)[128 / 4 + 1], uint8_t* dst_base, int64_t ld,
-                                    int64_t n0, int64_t ncols, int64_t t0, int tw) {
-  for (int idx = threadIdx.x; idx < 128 * 8; idx += kThreads) {
-    const int tc = idx >> 3, seg = idx & 7;
-    const int64_t n = n0 + tc;
-    const int m0 = seg * 16;
-    if (n >= ncols || m0 >= tw) continue;
-    const uint32_t* src = &tileT[tc][seg * 4];
-    uint8_t* dst = dst_base + n * ld + t0 + m0;
-    if (m0 + 16 <= tw && (((uintptr_t)dst) & 15u) == 0) {
-      *reinterpret_cast<uint4*>(dst) = make_uint4(src[0], src[1], src[2], src[3]);
-    } else {
-      for (int k = 0; k < 16; ++k)
-        if (m0 + k < tw) dst[k] = (uint8_t)((src[k >> 2] >> (8 * (k & 3))) & 0xffu);
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Dual quantization of a gradient tile (reference FP8MatmulFunction.backward,
 // src/kernels.py:771-782): 1x128 row tiles of dY and 1x128 row tiles of dY^T (= 128x1
@@ -448,7 +466,8 @@ __device__ __forceinline__ void dual_tile(const void* __restrict__ x, int64_t N,
                                           int64_t sstm, const RowTile rt, int64_t cb) {
   __shared__ float colpart[16][128];
   __shared__ float colscale[128];
-  __shared__ uint32_t tileT[128][128 / 4 + 1];
+  __shared__ TileT tileT;
+  // thread (lane16, rg): rows 8 rg .. 8 rg + 7, columns 8 lane16 .. 8 lane16 + 7
   const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
   const int64_t c = cb * 128 + lane16 * 8;
   const bool rs = round_scale != 0;
@@ -456,7 +475,7 @@ __device__ __forceinline__ void dual_tile(const void* __restrict__ x, int64_t N,
   Vec8<DT> d[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int ri = rg + 16 * i;
+    const int ri = rg * 8 + i;
     const int64_t nc = (ri < rt.nr) ? N - c : 0;
     load8<DT>(x, (rt.r0 + ri) * sxm + c, nc < 0 ? 0 : (nc > 8 ? 8 : nc), d[i]);
   }
@@ -471,7 +490,7 @@ __device__ __forceinline__ void dual_tile(const void* __restrict__ x, int64_t N,
   // row tiles: quantize and store
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int ri = rg + 16 * i;
+    const int ri = rg * 8 + i;
     const int64_t r = rt.r0 + ri;
     float a = 0.0f;
 #pragma unroll
@@ -505,8 +524,6 @@ __device__ __forceinline__ void dual_tile(const void* __restrict__ x, int64_t N,
     if (n < N) st[n * sstm + rt.tb] = sc;
   }
   __syncthreads();
-  uint8_t* tb = reinterpret_cast<uint8_t*>(&tileT[0][0]);
-  constexpr int kRowBytes = (128 / 4 + 1) * 4;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const float sc = colscale[lane16 * 8 + j];
@@ -514,10 +531,8 @@ __device__ __forceinline__ void dual_tile(const void* __restrict__ x, int64_t N,
 #pragma unroll
     for (int i = 0; i < 8; ++i) col[i] = d[i].v[j];
     uint32_t c2[2];
-    quant_vals<8, kDivSteps<DT>>(col, sc, 1.0f / sc, c2);
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * i] = (uint8_t)((c2[i >> 2] >> (8 * (i & 3))) & 0xffu);
+    quant_vals<8, kDivSteps<DT>>(col, sc, 1.0f / sc, c2);  // rows 8 rg .. 8 rg + 7, in order
+    put_col8(tileT, lane16 * 8 + j, rg, c2[0], c2[1]);
   }
   __syncthreads();
   store_tile_t(tileT, qt, sqtm, cb * 128, N, rt.t0, rt.tw);
@@ -555,13 +570,14 @@ __device__ __forceinline__ void requant_tile(const uint8_t* __restrict__ q, int6
                                              int64_t sqbm, uint8_t* qbt, int64_t sqbtm, float* sblk,
                                              int64_t ssbm, const RowTile rt, int64_t cb) {
   __shared__ float red[kThreads / 64];
-  __shared__ uint32_t tileT[128][128 / 4 + 1];
+  __shared__ TileT tileT;
+  // thread (lane16, rg): rows 8 rg .. 8 rg + 7, columns 8 lane16 .. 8 lane16 + 7
   const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
   const int64_t c = cb * 128 + lane16 * 8;
   float v[8][8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int ri = rg + 16 * i;
+    const int ri = rg * 8 + i;
     const int64_t r = rt.r0 + ri;
     uint32_t w0 = 0, w1 = 0;
     float sr = 0.0f;
@@ -599,7 +615,7 @@ __device__ __forceinline__ void requant_tile(const uint8_t* __restrict__ q, int6
   if (qb) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int ri = rg + 16 * i;
+      const int ri = rg * 8 + i;
       if (ri >= rt.nr) continue;
       uint8_t* qp = qb + (rt.r0 + ri) * sqbm + c;
       if (c + 8 <= K) {
@@ -611,14 +627,10 @@ __device__ __forceinline__ void requant_tile(const uint8_t* __restrict__ q, int6
     }
   }
   if (qbt) {
-    uint8_t* tb = reinterpret_cast<uint8_t*>(&tileT[0][0]);
-    constexpr int kRowBytes = (128 / 4 + 1) * 4;
+    uint32_t cols[8][2];
+    t8x8(codes, cols);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        tb[(lane16 * 8 + j) * kRowBytes + rg + 16 * i] =
-            (uint8_t)((codes[i][j >> 2] >> (8 * (j & 3))) & 0xffu);
+    for (int j = 0; j < 8; ++j) put_col8(tileT, lane16 * 8 + j, rg, cols[j][0], cols[j][1]);
     __syncthreads();
     store_tile_t(tileT, qbt, sqbtm, cb * 128, K, rt.t0, rt.tw);
   }
