@@ -59,6 +59,40 @@ def time_loop(fn, iters, warmup):
     return start.elapsed_time(end) / iters * 1e3  # us per call
 
 
+_BUSY = []
+
+
+def kernel_loop(fn, iters, warmup):
+    """Device time per call of a component.  Copies of a 256 MiB buffer queued first keep
+    the GPU busy (at its working clock) while the host enqueues the `iters` calls, so the
+    events bracket back-to-back kernels and not the host's launch overhead (which the step
+    timing above does include)."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    # host time per call, to size the queued work that covers the enqueueing
+    t0 = time.perf_counter()
+    for i in range(3):
+        fn(i)
+    torch.cuda.synchronize()
+    host_s = (time.perf_counter() - t0) / 3
+    if not _BUSY:
+        src = torch.ones(128 * 1024 * 1024, dtype=torch.bfloat16, device="cuda")
+        _BUSY.extend([src, torch.empty_like(src)])
+    src, dst = _BUSY
+    for _ in range(2 + int(host_s * iters / 80e-6)):  # a 256 MiB copy takes ~90 us
+        dst.copy_(src)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(iters):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters * 1e3  # us per call
+
+
 def cpu_baseline():
     """Time the oracle (torch-CPU restatement of the reference path) on a bounded sample."""
     import torch
@@ -296,16 +330,17 @@ def main():
               "moe_gateup": moe_gateup, "moe_down": moe_down, "dual_quant": dual_quant,
               "requant": requant, "dgrad": dgrad, "wgrad": wgrad, "moe_dual": moe_dual,
               "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad}[args.only]
-        us = time_loop(fn, args.steps, args.warmup)
+        loop = time_loop if args.only == "step" else kernel_loop
+        us = loop(fn, args.steps, args.warmup)
         print(json.dumps({"only": args.only, "us_per_call": us}))
         return
 
     # the timed region: exactly `steps` steps, synchronized on both sides
     torch.cuda.synchronize()
     step_us = time_loop(step, args.steps, args.warmup)
-    gemm_us = time_loop(gemm, max(args.steps, 50), 5)
-    qx_us = time_loop(quant_x, max(args.steps, 50), 5)
-    qw_us = time_loop(quant_w, max(args.steps, 50), 5)
+    gemm_us = kernel_loop(gemm, max(args.steps, 50), 5)
+    qx_us = kernel_loop(quant_x, max(args.steps, 50), 5)
+    qw_us = kernel_loop(quant_w, max(args.steps, 50), 5)
 
     flops = 2.0 * M * N * K
     qx_bytes = M * K * 2 + M * K + M * (K // 128) * 4        # read bf16, write e4m3 + scales
@@ -356,8 +391,8 @@ def main():
     }
     if moe is not None:
         A, D, H = moe["A"], moe["D"], moe["H"]
-        gu_us = time_loop(moe_gateup, 10, 2)
-        dn_us = time_loop(moe_down, 10, 2)
+        gu_us = kernel_loop(moe_gateup, 10, 2)
+        dn_us = kernel_loop(moe_down, 10, 2)
         gu_fl, dn_fl = 2.0 * A * D * 2 * H, 2.0 * A * H * D
         out["components"]["config3_moe_forward"] = {
             "tokens": 16384, "topk": 8, "rows": A, "experts": moe["E"],
@@ -370,10 +405,10 @@ def main():
     if mb is not None:
         A, D, H = moe["A"], moe["D"], moe["H"]
         cap = layers.padded_capacity(A, moe["E"])
-        md_us = time_loop(moe_dual, 5, 1)
-        mr_us = time_loop(moe_requant, 5, 1)
-        mw_us = time_loop(moe_wgrad, 3, 1)
-        mg_us = time_loop(moe_dgrad, 3, 1)
+        md_us = kernel_loop(moe_dual, 5, 1)
+        mr_us = kernel_loop(moe_requant, 5, 1)
+        mw_us = kernel_loop(moe_wgrad, 3, 1)
+        mg_us = kernel_loop(moe_dgrad, 3, 1)
         fl = 2.0 * A * D * 2 * H
         # bytes: dual reads dH12 bf16, writes row codes + scales and padded column codes + scales;
         # requant reads X codes + row scales, writes padded transposed codes + block scales
@@ -390,10 +425,10 @@ def main():
                                  "frac_of_fp8_peak": round(fl / mg_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
         }
     if bwd is not None:
-        dq_us = time_loop(dual_quant, 20, 3)
-        rq_us = time_loop(requant, 20, 3)
-        dg_us = time_loop(dgrad, 20, 3)
-        wg_us = time_loop(wgrad, 20, 3)
+        dq_us = kernel_loop(dual_quant, 20, 3)
+        rq_us = kernel_loop(requant, 20, 3)
+        dg_us = kernel_loop(dgrad, 20, 3)
+        wg_us = kernel_loop(wgrad, 20, 3)
         dq_bytes = M * N * 2 + 2 * M * N + 4 * (M * (N // 128) + N * (M // 128))
         rq_bytes = M * K + M * (K // 128) * 4 + K * M + (M // 128) * (K // 128) * 4
         out["components"]["config4_backward"] = {

@@ -126,6 +126,35 @@ __device__ inline float load_elem(const void* p, int dt, int64_t i) {
   return ((const float*)p)[i];
 }
 
+// Max over the 16 lanes of a DPP row for values that are >= 0 and not NaN (maxima of
+// |x| started from 0 under maxnum): their bit patterns order as unsigned integers, so each
+// step is one v_max_u32 with a DPP operand and needs no NaN quieting.
+__device__ inline float row16_max_pos(float a) {
+  uint32_t u = __float_as_uint(a);
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0xB1, 0xF, 0xF, true));   // quad [1,0,3,2]
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x4E, 0xF, 0xF, true));   // quad [2,3,0,1]
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x141, 0xF, 0xF, true));  // row_half_mirror
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x140, 0xF, 0xF, true));  // row_mirror
+  return __uint_as_float(u);
+}
+
+// The same over the 8 lanes of a DPP half-row.
+__device__ inline float row8_max_pos(float a) {
+  uint32_t u = __float_as_uint(a);
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0xB1, 0xF, 0xF, true));   // quad [1,0,3,2]
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x4E, 0xF, 0xF, true));   // quad [2,3,0,1]
+  u = max(u, (uint32_t)__builtin_amdgcn_mov_dpp((int)u, 0x141, 0xF, 0xF, true));  // row_half_mirror
+  return __uint_as_float(u);
+}
+
+// The same over a whole wave64.
+__device__ inline float wave_max_pos(float a) {
+  uint32_t u = __float_as_uint(row16_max_pos(a));
+  u = max(u, (uint32_t)__shfl_xor((int)u, 16));
+  u = max(u, (uint32_t)__shfl_xor((int)u, 32));
+  return __uint_as_float(u);
+}
+
 // Max over the 16 lanes of a DPP row (lanes 16r..16r+15), maxnum semantics.
 __device__ inline float row16_max(float v) {
   v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false)));  // quad [1,0,3,2]
@@ -141,6 +170,22 @@ __device__ inline float wave_max(float v) {
   v = fmaxf(v, __shfl_xor(v, 16));
   v = fmaxf(v, __shfl_xor(v, 32));
   return v;
+}
+
+// Raw buffer resource over [p, p + bytes): accesses are an SGPR base plus a 32-bit lane
+// offset, and anything past `bytes` reads as zero and is not written.
+// The operands are wave-uniform by construction; readfirstlane says so to the compiler,
+// so the descriptor lives in SGPRs even when it was computed from loaded values.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+  const int64_t cap = 0xffffffffLL;
+  // (readfirstlane returns int: go through uint32_t, or a low word with bit 31 set
+  // would sign-extend into the high word of the address)
+  const uint32_t n = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(bytes < cap ? bytes : cap));
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+  void* pu = (void*)(uintptr_t)((hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(pu, (short)0, (int)n, 0x00020000);
 }
 
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -281,22 +281,6 @@ __device__ inline int sa_row(int q) { return (q & ~127) + (q & 7) * 16 + ((q >> 
 // serves together, all hit distinct banks.
 __device__ inline int swz_f(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-// Raw buffer resource over [p, p + bytes): loads are an SGPR base plus a 32-bit lane
-// offset, and anything past `bytes` reads as zero.
-// The operands are wave-uniform by construction; readfirstlane says so to the compiler,
-// so the descriptor lives in SGPRs even when it was computed from loaded values.
-__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
-  const int64_t cap = 0xffffffffLL;
-  // (readfirstlane returns int: go through uint32_t, or a low word with bit 31 set
-  // would sign-extend into the high word of the address)
-  const uint32_t n = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(bytes < cap ? bytes : cap));
-  const uint64_t a = (uint64_t)(uintptr_t)p;
-  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
-  void* pu = (void*)(uintptr_t)((hi << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(pu, (short)0, (int)n, 0x00020000);
-}
-
 // DMA of 16 (4) bytes per lane from the buffer to LDS: lane t's bytes land at LDS byte
 // address lds + 16 t (4 t).  lds is wave-uniform.
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, uint32_t lds) {

@@ -17,6 +17,9 @@ constexpr int kThreads = 256;
 inline int elem_size(int dt) { return dt == CIN_DT_F32 ? 4 : 2; }
 inline bool valid_dtype(int dt) { return dt == CIN_DT_BF16 || dt == CIN_DT_F32 || dt == CIN_DT_F16; }
 inline bool aligned(const void* p, int a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
+// 128 rows of `rowbytes` bytes span less than 2 GiB: 32-bit buffer offsets reach every
+// byte of a 128-row tile.
+inline bool tile_fits32(int64_t rowbytes) { return rowbytes >= 0 && rowbytes < ((int64_t)1 << 24); }
 
 inline unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
   int64_t g = cdiv(work_items, per_block);
@@ -366,296 +369,743 @@ __device__ inline void t8x8(const uint32_t (&rows)[8][2], uint32_t (&cols)[8][2]
     }
 }
 
-template <int DT>
-__global__ __launch_bounds__(kThreads) void k_blockwise128(const void* __restrict__ x, int64_t M,
-                                                           int64_t N, int64_t sxm, int round_scale,
-                                                           uint8_t* q, int64_t sqm, uint8_t* qt,
-                                                           int64_t sqtm, float* sc, int64_t ssm) {
-  __shared__ float red[kThreads / 64];
-  __shared__ TileT tileT;  // transposed codes
-  // thread (lane16, rg): rows 8 rg .. 8 rg + 7, columns 8 lane16 .. 8 lane16 + 7
-  const int64_t rb = blockIdx.y, cb = blockIdx.x;
-  const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
-  const int64_t c = cb * 128 + lane16 * 8;
-  Vec8<DT> d[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int64_t r = rb * 128 + rg * 8 + i;
-    const int64_t nc = (r < M) ? N - c : 0;
-    load8<DT>(x, r * sxm + c, nc < 0 ? 0 : (nc > 8 ? 8 : nc), d[i]);
+// ---------------------------------------------------------------------------
+// 128 x 128 tile kernels: block quantization, dual quantization and row -> block
+// re-quantization, dense and grouped.  A workgroup of 256 threads walks tiles
+// t, t + G, t + 2G, ... (G = workgroups resident on the device at once).  Thread
+// (lane16, rg) owns rows 8 rg .. 8 rg + 7 and columns 8 lane16 .. 8 lane16 + 7 of a tile.
+// The raw input of the next tile is loaded into a second register set while the current
+// one is quantized; the two sets alternate, so no register copy waits on a load.
+//
+// Column blocks that run past the last column (N % 128 != 0) go to a second launch with
+// EDGE = true, whose element-wise loads and stores are masked.  The main launch addresses
+// a tile through buffer descriptors whose range ends after the tile's last valid row:
+// rows past it read as zero and are not written, with no per-row test.
+// ---------------------------------------------------------------------------
+struct TileGeo {
+  int64_t r0;   // first input row
+  int64_t t0;   // first column of the transposed outputs; t0 / 128 indexes their scales
+  uint32_t cb;  // column block
+  int nr;       // valid rows, 1..128; 0 = no tile (nothing written)
+  int tw;       // transposed columns written: nr (dense) or 128 (padded axis)
+};
+
+// Dense tiles: t -> (row block t / nbc, column block cb0 + t % nbc).
+struct DenseTiles {
+  int64_t M;
+  uint32_t nbc, cb0;
+  __device__ void operator()(uint32_t t, TileGeo& g) const {
+    const uint32_t rb = t / nbc;
+    g.cb = cb0 + (t - rb * nbc);
+    g.r0 = (int64_t)rb * 128;
+    const int64_t left = M - g.r0;
+    g.nr = (int)(left < 128 ? left : 128);
+    g.t0 = g.r0;
+    g.tw = g.nr;
   }
-  float a = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(d[i].v[j]));
-  a = block_reduce_max(a, red);
-  a = fmaxf(a, amax_floor(DT));
-  const float s = compute_scale(a, round_scale != 0);
-  const float rcp = 1.0f / s;
-  uint32_t codes[8][2];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) quant_vals<8, kDivSteps<DT>>(d[i].v, s, rcp, codes[i]);
-  if (q) {
+};
+
+// Grouped tiles (MoE backward): t -> (128-token chunk t / nbc of the expert-sorted rows,
+// column block cb0 + t % nbc); the chunk's transposed outputs sit at its padded position
+// (cin_grouped.h).  A workgroup visits increasing t, so the expert cursor only moves
+// forward.  Chunks past the last one, or whose padded position does not fit in tcap
+// columns, are no tile.
+struct GroupedTiles {
+  const int64_t* starts;
+  const int64_t* ends;
+  int64_t T, tcap;
+  int32_t E;
+  uint32_t nbc, cb0;
+  // cursor: expert e owns rows [s0, s1), chunks [seen, seen + n) and padded columns from pad
+  int32_t e;
+  uint32_t seen, n;
+  int64_t pad, s0, s1;
+  __device__ void start() {
+    e = 0;
+    seen = 0;
+    pad = 0;
+    load_expert();
+  }
+  __device__ void load_expert() {
+    // The ranges are read through the constant address space: they do not change during
+    // the kernel, so the loads are scalar and wait on nothing but themselves (a vector
+    // load would wait behind the tile loads and stores in flight).
+    typedef __attribute__((address_space(4))) const int64_t cint64;
+    int64_t a = 0, b = 0;
+    if (e < E) {
+      a = ((const cint64*)starts)[e];
+      b = ((const cint64*)ends)[e];
+      if (a < 0) a = 0;
+      if (b > T) b = T;
+      if (b < a) b = a;
+    }
+    s0 = a;
+    s1 = b;
+    n = (uint32_t)((b - a + 127) / 128);
+  }
+  __device__ void operator()(uint32_t t, TileGeo& g) {
+    const uint32_t id = t / nbc;
+    g.cb = cb0 + (t - id * nbc);
+    while (e < E && id >= seen + n) {
+      seen += n;
+      pad += 128 * (int64_t)n;
+      ++e;
+      load_expert();
+    }
+    const int64_t k = (int64_t)(id - seen);
+    g.r0 = s0 + 128 * k;
+    g.t0 = pad + 128 * k;
+    g.tw = 128;
+    const int64_t left = s1 - g.r0;
+    g.nr = (e < E && g.t0 + 128 <= tcap) ? (int)(left < 128 ? left : 128) : 0;
+    if (g.nr == 0) g.r0 = g.t0 = 0;  // nothing is read or written for it
+  }
+};
+
+__device__ inline GroupedTiles grouped_tiles(const int64_t* starts, const int64_t* ends, int64_t E,
+                                             int64_t T, int64_t tcap, uint32_t nbc, uint32_t cb0) {
+  GroupedTiles g;
+  g.starts = starts;
+  g.ends = ends;
+  g.E = (int32_t)E;
+  g.T = T;
+  g.tcap = tcap;
+  g.nbc = nbc;
+  g.cb0 = cb0;
+  g.start();
+  return g;
+}
+
+// Walk the workgroup's tiles with the next tile's raw input loaded ahead.  The ahead
+// load is unconditional, so every path issues the same loads and the wait before a
+// tile's use covers that tile only; when no tile is left it loads an empty one (no valid
+// rows: the main launch's buffer range is empty and nothing is read from memory).
+template <typename Raw, typename Geo, typename Load, typename Proc>
+__device__ __forceinline__ void tile_loop(uint32_t ntiles, Geo& geo, Load load, Proc proc) {
+  uint32_t t = blockIdx.x;
+  const uint32_t G = gridDim.x;
+  if (t >= ntiles) return;
+  Raw ra, rb;
+  TileGeo ga, gb;
+  geo(t, ga);
+  load(ga, ra);
+  for (;;) {
+    const uint32_t t1 = t + G;
+    const bool h1 = t1 < ntiles;
+    if (h1) {
+      geo(t1, gb);
+    } else {
+      gb = ga;
+      gb.nr = 0;
+    }
+    load(gb, rb);
+    proc(ga, ra);
+    if (!h1) break;
+    const uint32_t t2 = t1 + G;
+    const bool h2 = t2 < ntiles;
+    if (h2) {
+      geo(t2, ga);
+    } else {
+      ga = gb;
+      ga.nr = 0;
+    }
+    load(ga, ra);
+    proc(gb, rb);
+    if (!h2) break;
+    t = t2;
+  }
+}
+
+// Bytes from a tile's first row to the end of its last valid row (128 elements of
+// `es` bytes in), in a row-major operand with rows `rowb` bytes apart.
+__device__ inline int64_t tile_extent(int nr, int64_t rowb, int es) {
+  return nr > 0 ? (int64_t)(nr - 1) * rowb + 128 * es : 0;
+}
+
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+constexpr int kNT = 2;  // buffer cache policy: non-temporal (streamed through once)
+
+// Raw input bits of a thread's 8 x 8 piece (bf16/fp16: 4 words per row, fp32: 8).
+template <int DT>
+struct RawIn {
+  uint32_t w[8][DT == CIN_DT_F32 ? 8 : 4];
+};
+
+// Load a thread's piece of a tile.  Main launch: one 16-byte buffer load per row (two
+// for fp32); rows past the tile read zero.  EDGE: element loads at clamped (in-bounds)
+// addresses, zeroed outside the tile.
+template <int DT, bool EDGE>
+__device__ __forceinline__ void load_in(const void* __restrict__ x, int64_t sxm, int64_t N,
+                                        const TileGeo& g, RawIn<DT>& o) {
+  constexpr int ES = DT == CIN_DT_F32 ? 4 : 2;
+  const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
+  if constexpr (!EDGE) {
+    const int64_t rowb = sxm * ES;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(
+        static_cast<const char*>(x) + (g.r0 * sxm + (int64_t)g.cb * 128) * ES, tile_extent(g.nr, rowb, ES));
+    const uint32_t v0 = (uint32_t)(rg * 8) * (uint32_t)rowb + (uint32_t)(lane16 * 8 * ES);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int64_t r = rb * 128 + rg * 8 + i;
-      if (r >= M) continue;
-      uint8_t* qp = q + r * sqm + c;
-      if (c + 8 <= N) {
-        *reinterpret_cast<uint2*>(qp) = make_uint2(codes[i][0], codes[i][1]);
-      } else {
-        for (int j = 0; j < 8; ++j)
-          if (c + j < N) qp[j] = (uint8_t)((codes[i][j >> 2] >> (8 * (j & 3))) & 0xffu);
+      const uint32_t off = v0 + (uint32_t)i * (uint32_t)rowb;
+      const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNT);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o.w[i][k] = a[k];
+      if constexpr (DT == CIN_DT_F32) {
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, kNT);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) o.w[i][4 + k] = b[k];
       }
     }
+  } else {
+    const int64_t c = (int64_t)g.cb * 128 + lane16 * 8;
+    const int lastr = g.nr > 0 ? g.nr - 1 : 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int ri = rg * 8 + i;
+      const int64_t row = g.r0 + (ri < lastr ? ri : lastr);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const bool ok = ri < g.nr && c + j < N;
+        const int64_t off = row * sxm + (c + j < N ? c + j : N - 1);
+        if constexpr (DT == CIN_DT_F32) {
+          const uint32_t b = static_cast<const uint32_t*>(x)[off];
+          o.w[i][j] = ok ? b : 0u;
+        } else {
+          const uint32_t b = static_cast<const uint16_t*>(x)[off];
+          const uint32_t v = ok ? b : 0u;
+          if (j & 1)
+            o.w[i][j >> 1] |= v << 16;
+          else
+            o.w[i][j >> 1] = v;
+        }
+      }
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float in_val(const RawIn<DT>& r, int i, int j) {
+  if constexpr (DT == CIN_DT_F32) {
+    return __uint_as_float(r.w[i][j]);
+  } else if constexpr (DT == CIN_DT_BF16) {
+    const uint32_t w = r.w[i][j >> 1];
+    return (j & 1) ? bf16_hi(w) : bf16_lo(w);
+  } else {
+    const uint32_t w = r.w[i][j >> 1];
+    const uint16_t b = (uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu));
+    _Float16 h;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+  }
+}
+
+// The 8 values of row i of a piece.
+template <int DT>
+__device__ __forceinline__ void row_vals(const RawIn<DT>& r, int i, float (&v)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = in_val<DT>(r, i, j);
+}
+
+// Divisor for quant8: an infinite scale (infinite amax) divides by 1 with reciprocal
+// 1 / inf = 0, which yields x / inf (signed zeros; NaN for an inf or NaN x).
+__device__ __forceinline__ float divisor(float s) { return s == __builtin_inff() ? 1.0f : s; }
+
+// Quantize 8 values with divisor d = divisor(s) and reciprocal r = 1 / s into two packed
+// code words.
+template <int STEPS>
+__device__ __forceinline__ void quant8(const float (&v)[8], float d, float r, uint32_t (&out)[2]) {
+  float y[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = clamp448(div_by_scale<STEPS>(v[i], d, r));
+  out[0] = cvt4_e4m3(y[0], y[1], y[2], y[3]);
+  out[1] = cvt4_e4m3(y[4], y[5], y[6], y[7]);
+}
+
+// Hide a value's origin from the compiler: what is computed from it after this point is
+// computed again rather than kept in registers across the barriers between, and it is
+// not treated as a load from an array.
+__device__ __forceinline__ void opaque(uint32_t& w) { asm volatile("" : "+v"(w)); }
+__device__ __forceinline__ void opaquef(float& w) { asm volatile("" : "+v"(w)); }
+
+template <int L>
+__device__ __forceinline__ float row_bcast(float v) {  // lane L of each 16-lane DPP row
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + L, 0xF, 0xF, true));
+}
+
+// Divisors and reciprocals of a thread's 8 rows from their amax values, which are equal
+// across each 16-lane row: lane l computes row l % 8 once and the results are broadcast.
+// Returns the scale of row l % 8 (for the scale store).
+__device__ __forceinline__ float row_scales8(const float (&ra)[8], float floor_v, bool rs,
+                                             float (&d)[8], float (&r)[8]) {
+  // ra[l % 8] as a tree of selects on the bits of l.  The values pass through opaque()
+  // first: selects between loads of one array would be folded into an indexed load,
+  // which puts the array in scratch memory.
+  float x0 = ra[0], x1 = ra[1], x2 = ra[2], x3 = ra[3], x4 = ra[4], x5 = ra[5], x6 = ra[6], x7 = ra[7];
+  opaquef(x0); opaquef(x1); opaquef(x2); opaquef(x3);
+  opaquef(x4); opaquef(x5); opaquef(x6); opaquef(x7);
+  const bool b0 = threadIdx.x & 1, b1 = threadIdx.x & 2, b2 = threadIdx.x & 4;
+  const float a01 = b0 ? x1 : x0, a23 = b0 ? x3 : x2, a45 = b0 ? x5 : x4, a67 = b0 ? x7 : x6;
+  const float a = b2 ? (b1 ? a67 : a45) : (b1 ? a23 : a01);
+  const float sv = compute_scale(fmaxf(a, floor_v), rs);
+  const float dv = divisor(sv), rv = 1.0f / sv;
+  d[0] = row_bcast<0>(dv); r[0] = row_bcast<0>(rv);
+  d[1] = row_bcast<1>(dv); r[1] = row_bcast<1>(rv);
+  d[2] = row_bcast<2>(dv); r[2] = row_bcast<2>(rv);
+  d[3] = row_bcast<3>(dv); r[3] = row_bcast<3>(rv);
+  d[4] = row_bcast<4>(dv); r[4] = row_bcast<4>(rv);
+  d[5] = row_bcast<5>(dv); r[5] = row_bcast<5>(rv);
+  d[6] = row_bcast<6>(dv); r[6] = row_bcast<6>(rv);
+  d[7] = row_bcast<7>(dv); r[7] = row_bcast<7>(rv);
+  return sv;
+}
+
+// Row-major code output of a tile: main launch through a buffer descriptor (rows past
+// the tile are out of range), EDGE through masked byte stores.
+template <bool EDGE>
+struct RowOut {
+  __amdgpu_buffer_rsrc_t r;
+  uint32_t v0, step;
+  uint8_t* base;
+  int64_t ld, c, N;
+  int nr, rg;
+  __device__ RowOut(uint8_t* q, int64_t sqm, int64_t N_, const TileGeo& g) {
+    const int lane16 = threadIdx.x & 15;
+    rg = threadIdx.x >> 4;
+    if constexpr (!EDGE) {
+      r = make_rsrc(q + g.r0 * sqm + (int64_t)g.cb * 128, tile_extent(g.nr, sqm, 1));
+      v0 = (uint32_t)(rg * 8) * (uint32_t)sqm + (uint32_t)(lane16 * 8);
+      step = (uint32_t)sqm;
+    } else {
+      base = q + g.r0 * sqm;
+      ld = sqm;
+      c = (int64_t)g.cb * 128 + lane16 * 8;
+      N = N_;
+      nr = g.nr;
+    }
+  }
+  __device__ void put(int i, const uint32_t (&w)[2]) const {
+    if constexpr (!EDGE) {
+      u32x2 x;
+      x[0] = w[0];
+      x[1] = w[1];
+      __builtin_amdgcn_raw_buffer_store_b64(x, r, v0 + (uint32_t)i * step, 0, kNT);
+    } else {
+      const int ri = rg * 8 + i;
+      if (ri >= nr) return;
+      uint8_t* d = base + ri * ld + c;
+      for (int j = 0; j < 8; ++j)
+        if (c + j < N) d[j] = (uint8_t)((w[j >> 2] >> (8 * (j & 3))) & 0xffu);
+    }
+  }
+};
+
+// Write the transposed LDS tile: whole 16-byte pieces through a buffer descriptor when
+// the tile is complete (128 x 128) and the output rows are 16-byte aligned, else the
+// masked writer.
+template <bool EDGE>
+__device__ __forceinline__ void put_tile_t(const TileT& tileT, uint8_t* qt, int64_t sqtm, int64_t N,
+                                           const TileGeo& g, bool vec_t) {
+  if (!EDGE && vec_t && g.tw == 128) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(qt + (int64_t)g.cb * 128 * sqtm + g.t0, 127 * sqtm + 128);
+    const int tc0 = threadIdx.x >> 3, seg = threadIdx.x & 7;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int tc = tc0 + 32 * k;
+      const uint2 w0 = *reinterpret_cast<const uint2*>(&tileT[tc][seg * 4]);
+      const uint2 w1 = *reinterpret_cast<const uint2*>(&tileT[tc][seg * 4 + 2]);
+      u32x4 x;
+      x[0] = w0.x;
+      x[1] = w0.y;
+      x[2] = w1.x;
+      x[3] = w1.y;
+      __builtin_amdgcn_raw_buffer_store_b128(x, r, (uint32_t)tc * (uint32_t)sqtm + (uint32_t)(seg * 16), 0,
+                                             kNT);
+    }
+  } else {
+    store_tile_t(tileT, qt, sqtm, (int64_t)g.cb * 128, N, g.t0, g.tw);
+  }
+}
+
+// Block amax over the workgroup (two barriers); v >= 0 and not NaN.
+__device__ __forceinline__ float block_max_pos(float v, float* red) {
+  v = wave_max_pos(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  uint32_t r = __float_as_uint(red[0]);
+#pragma unroll
+  for (int i = 1; i < kThreads / 64; ++i) r = max(r, __float_as_uint(red[i]));
+  __syncthreads();
+  return __uint_as_float(r);
+}
+
+
+// ----------------------------- block 128 x 128 -----------------------------
+// Reference quantize_fp8_blockwise (src/kernels.py:94-132) for 128 x 128 blocks; the
+// transposed codes serve the dgrad operand (src/kernels.py:784-788).
+struct BlockSmem {
+  float red[kThreads / 64];
+  TileT tileT;
+};
+
+template <int DT, bool EDGE>
+__device__ __forceinline__ void block_body(RawIn<DT>& raw, const TileGeo& g, int64_t N, bool rs,
+                                           uint8_t* q, int64_t sqm, uint8_t* qt, int64_t sqtm,
+                                           bool vec_t, float* sc, int64_t ssm, BlockSmem& sm) {
+  const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float v[8];
+    row_vals<DT>(raw, i, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(v[j]));
+  }
+  a = fmaxf(block_max_pos(a, sm.red), amax_floor(DT));
+  const float s = compute_scale(a, rs);
+  const float d = divisor(s), r = 1.0f / s;
+  uint32_t codes[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+#pragma unroll
+    for (int k = 0; k < (int)(sizeof(raw.w[0]) / sizeof(raw.w[0][0])); ++k) opaque(raw.w[i][k]);
+    float v[8];
+    row_vals<DT>(raw, i, v);
+    quant8<kDivSteps<DT>>(v, d, r, codes[i]);
+  }
+  if (q) {
+    const RowOut<EDGE> out(q, sqm, N, g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out.put(i, codes[i]);
   }
   if (qt) {
     uint32_t cols[8][2];
     t8x8(codes, cols);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) put_col8(tileT, lane16 * 8 + j, rg, cols[j][0], cols[j][1]);
+    for (int j = 0; j < 8; ++j) put_col8(sm.tileT, lane16 * 8 + j, rg, cols[j][0], cols[j][1]);
     __syncthreads();
-    const int64_t left = M - rb * 128;
-    store_tile_t(tileT, qt, sqtm, cb * 128, N, rb * 128, (int)(left < 128 ? left : 128));
+    put_tile_t<EDGE>(sm.tileT, qt, sqtm, N, g, vec_t);
   }
-  if (threadIdx.x == 0) sc[rb * ssm + cb] = s;
+  if (threadIdx.x == 0) sc[(g.t0 >> 7) * ssm + g.cb] = s;
 }
 
-// ---------------------------------------------------------------------------
-// Placement of one 128-row tile of the dual and re-quantization kernels.  Dense: tile rb
-// covers rows [128 rb, min(128 rb + 128, M)) and its transposed outputs sit at the same
-// columns.  Grouped (MoE backward): the tile is one 128-token chunk of an expert, and its
-// transposed outputs sit at the chunk's padded position; the columns past the chunk's
-// rows are written as code 0, so a GEMM reducing over the padded axis adds nothing there.
-// ---------------------------------------------------------------------------
-struct RowTile {
-  int64_t r0;  // first input row
-  int nr;      // valid rows, 1..128
-  int64_t t0;  // first column of the transposed outputs
-  int tw;      // transposed columns written: nr (dense) or 128 (padded)
-  int64_t tb;  // index of the tile's scale along the transposed axis
-};
-
-__device__ inline RowTile dense_tile(int64_t rb, int64_t M) {
-  const int64_t left = M - rb * 128;
-  const int nr = (int)(left < 128 ? left : 128);
-  return RowTile{rb * 128, nr, rb * 128, nr, rb};
+// (4 waves per SIMD fit the bf16/fp16 main kernel without spills)
+template <int DT, bool EDGE>
+__global__ __launch_bounds__(kThreads, (DT == CIN_DT_F32 || EDGE) ? 1 : 4) void k_blockwise128(const void* __restrict__ x, int64_t M,
+                                                           int64_t N, int64_t sxm, int round_scale,
+                                                           uint8_t* q, int64_t sqm, uint8_t* qt,
+                                                           int64_t sqtm, int vec_t, float* sc,
+                                                           int64_t ssm, uint32_t nbc, uint32_t cb0,
+                                                           uint32_t ntiles) {
+  __shared__ BlockSmem sm;
+  DenseTiles geo{M, nbc, cb0};
+  const bool rs = round_scale != 0;
+  tile_loop<RawIn<DT>>(
+      ntiles, geo, [&](const TileGeo& g, RawIn<DT>& r) { load_in<DT, EDGE>(x, sxm, N, g, r); },
+      [&](const TileGeo& g, RawIn<DT>& r) {
+        block_body<DT, EDGE>(r, g, N, rs, q, sqm, qt, sqtm, vec_t != 0, sc, ssm, sm);
+      });
 }
 
-// Grouped tile for block row `id`; false when `id` is past the last chunk or its padded
-// position would not fit in `tcap` columns (the caller's transposed row length).
-__device__ inline bool grouped_tile(const int64_t* starts, const int64_t* ends, int64_t E,
-                                    int64_t T, int64_t id, int64_t tcap, RowTile& rt) {
-  Chunk c;
-  if (!find_chunk(starts, ends, E, T, id, c) || c.t0 + 128 > tcap) return false;
-  rt = RowTile{c.r0, c.nr, c.t0, 128, c.t0 / 128};
-  return true;
-}
-
-// ---------------------------------------------------------------------------
+// ----------------------------- dual 1x128 / 128x1 -----------------------------
 // Dual quantization of a gradient tile (reference FP8MatmulFunction.backward,
 // src/kernels.py:771-782): 1x128 row tiles of dY and 1x128 row tiles of dY^T (= 128x1
-// column tiles of dY) from one read.  The transposed codes are written through an
-// LDS tile.
-// ---------------------------------------------------------------------------
-template <int DT>
-__device__ __forceinline__ void dual_tile(const void* __restrict__ x, int64_t N, int64_t sxm,
-                                          int round_scale, uint8_t* q, int64_t sqm, float* s,
-                                          int64_t ssm, uint8_t* qt, int64_t sqtm, float* st,
-                                          int64_t sstm, const RowTile rt, int64_t cb) {
-  __shared__ float colpart[16][128];
-  __shared__ float colscale[128];
-  __shared__ TileT tileT;
-  // thread (lane16, rg): rows 8 rg .. 8 rg + 7, columns 8 lane16 .. 8 lane16 + 7
+// column tiles of dY) from one read.  Column amax goes through LDS partials; the
+// transposed codes through an LDS tile.
+struct DualSmem {
+  float colpart[16][128];
+  float coldiv[128];
+  float colrcp[128];
+  TileT tileT;
+};
+
+template <int DT, bool EDGE>
+__device__ __forceinline__ void dual_body(RawIn<DT>& raw, const TileGeo& g, int64_t N, bool rs,
+                                          uint8_t* q, int64_t sqm, float* s, int64_t ssm,
+                                          uint8_t* qt, int64_t sqtm, bool vec_t, float* st,
+                                          int64_t sstm, DualSmem& sm) {
+  constexpr int NW = (int)(sizeof(raw.w[0]) / sizeof(raw.w[0][0]));
   const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
-  const int64_t c = cb * 128 + lane16 * 8;
-  const bool rs = round_scale != 0;
   const float floor_v = amax_floor(DT);
-  Vec8<DT> d[8];
+  // Values are widened from the raw bits at each of their three uses (maxima, row codes,
+  // column codes) rather than held as 64 floats across the barriers.
+  float ra[8];
+  {
+    float cm[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int ri = rg * 8 + i;
-    const int64_t nc = (ri < rt.nr) ? N - c : 0;
-    load8<DT>(x, (rt.r0 + ri) * sxm + c, nc < 0 ? 0 : (nc > 8 ? 8 : nc), d[i]);
-  }
-  // column partial maxima over this thread's 8 rows
+    for (int j = 0; j < 8; ++j) cm[j] = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    float a = 0.0f;
+    for (int i = 0; i < 8; ++i) {
+      float v[8];
+      row_vals<DT>(raw, i, v);
+      float a = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(d[i].v[j]));
-    colpart[rg][lane16 * 8 + j] = a;
-  }
-  // row tiles: quantize and store
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int ri = rg * 8 + i;
-    const int64_t r = rt.r0 + ri;
-    float a = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(d[i].v[j]));
-    a = row16_max(a);
-    a = fmaxf(a, floor_v);
-    const float sr = compute_scale(a, rs);
-    uint32_t c2[2];
-    quant_vals<8, kDivSteps<DT>>(d[i].v, sr, 1.0f / sr, c2);
-    const uint32_t lo = c2[0], hi = c2[1];
-    if (ri < rt.nr) {
-      uint8_t* qp = q + r * sqm + c;
-      if (c + 8 <= N) {
-        *reinterpret_cast<uint2*>(qp) = make_uint2(lo, hi);
-      } else {
-        for (int j = 0; j < 8; ++j)
-          if (c + j < N) qp[j] = (uint8_t)(((j < 4 ? lo : hi) >> (8 * (j & 3))) & 0xffu);
+      for (int j = 0; j < 8; ++j) {
+        a = fmaxf(a, fabsf(v[j]));
+        cm[j] = fmaxf(cm[j], fabsf(v[j]));
       }
-      if (lane16 == 0) s[r * ssm + cb] = sr;
+      ra[i] = a;
     }
+    // column partial maxima over this thread's 8 rows
+    *reinterpret_cast<float4*>(&sm.colpart[rg][lane16 * 8]) = make_float4(cm[0], cm[1], cm[2], cm[3]);
+    *reinterpret_cast<float4*>(&sm.colpart[rg][lane16 * 8 + 4]) = make_float4(cm[4], cm[5], cm[6], cm[7]);
+  }
+  // row tiles
+  {
+    float dr[8], rr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ra[i] = row16_max_pos(ra[i]);
+    const float own = row_scales8(ra, floor_v, rs, dr, rr);
+    const RowOut<EDGE> out(q, sqm, N, g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int k = 0; k < NW; ++k) opaque(raw.w[i][k]);
+      float v[8];
+      row_vals<DT>(raw, i, v);
+      uint32_t w[2];
+      quant8<kDivSteps<DT>>(v, dr[i], rr[i], w);
+      out.put(i, w);
+    }
+    const int ro = rg * 8 + (lane16 & 7);
+    if (lane16 < 8 && ro < g.nr) s[(g.r0 + ro) * ssm + g.cb] = own;
   }
   __syncthreads();
   if (threadIdx.x < 128) {
-    float a = 0.0f;
+    uint32_t a = 0u;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) a = fmaxf(a, colpart[k][threadIdx.x]);
-    a = fmaxf(a, floor_v);
-    const float sc = compute_scale(a, rs);
-    colscale[threadIdx.x] = sc;
-    const int64_t n = cb * 128 + threadIdx.x;
-    if (n < N) st[n * sstm + rt.tb] = sc;
+    for (int k = 0; k < 16; ++k) a = max(a, __float_as_uint(sm.colpart[k][threadIdx.x]));
+    const float sc = compute_scale(fmaxf(__uint_as_float(a), floor_v), rs);
+    sm.coldiv[threadIdx.x] = divisor(sc);
+    sm.colrcp[threadIdx.x] = 1.0f / sc;
+    const int64_t n = (int64_t)g.cb * 128 + threadIdx.x;
+    if (!EDGE || n < N) st[n * sstm + (g.t0 >> 7)] = sc;
   }
   __syncthreads();
+  {
+    const float4 d0 = *reinterpret_cast<const float4*>(&sm.coldiv[lane16 * 8]);
+    const float4 d1 = *reinterpret_cast<const float4*>(&sm.coldiv[lane16 * 8 + 4]);
+    const float4 r0 = *reinterpret_cast<const float4*>(&sm.colrcp[lane16 * 8]);
+    const float4 r1 = *reinterpret_cast<const float4*>(&sm.colrcp[lane16 * 8 + 4]);
+    const float cd[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+    const float cr[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float sc = colscale[lane16 * 8 + j];
-    float col[8];
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) col[i] = d[i].v[j];
-    uint32_t c2[2];
-    quant_vals<8, kDivSteps<DT>>(col, sc, 1.0f / sc, c2);  // rows 8 rg .. 8 rg + 7, in order
-    put_col8(tileT, lane16 * 8 + j, rg, c2[0], c2[1]);
+      for (int k = 0; k < NW; ++k) opaque(raw.w[i][k]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float col[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) col[i] = in_val<DT>(raw, i, j);
+      uint32_t w[2];
+      quant8<kDivSteps<DT>>(col, cd[j], cr[j], w);  // rows 8 rg .. 8 rg + 7, in order
+      put_col8(sm.tileT, lane16 * 8 + j, rg, w[0], w[1]);
+    }
   }
   __syncthreads();
-  store_tile_t(tileT, qt, sqtm, cb * 128, N, rt.t0, rt.tw);
+  put_tile_t<EDGE>(sm.tileT, qt, sqtm, N, g, vec_t);
 }
 
-template <int DT>
+template <int DT, bool EDGE, typename Geo>
+__device__ __forceinline__ void dual_run(Geo& geo, uint32_t ntiles, const void* __restrict__ x,
+                                         int64_t N, int64_t sxm, bool rs, uint8_t* q, int64_t sqm,
+                                         float* s, int64_t ssm, uint8_t* qt, int64_t sqtm, bool vec_t,
+                                         float* st, int64_t sstm, DualSmem& sm) {
+  tile_loop<RawIn<DT>>(
+      ntiles, geo, [&](const TileGeo& g, RawIn<DT>& r) { load_in<DT, EDGE>(x, sxm, N, g, r); },
+      [&](const TileGeo& g, RawIn<DT>& r) {
+        if (g.nr == 0) return;  // uniform over the workgroup
+        dual_body<DT, EDGE>(r, g, N, rs, q, sqm, s, ssm, qt, sqtm, vec_t, st, sstm, sm);
+      });
+}
+
+template <int DT, bool EDGE>
 __global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x, int64_t M,
                                                       int64_t N, int64_t sxm, int round_scale,
                                                       uint8_t* q, int64_t sqm, float* s,
                                                       int64_t ssm, uint8_t* qt, int64_t sqtm,
-                                                      float* st, int64_t sstm) {
-  dual_tile<DT>(x, N, sxm, round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm,
-                dense_tile(blockIdx.y, M), blockIdx.x);
+                                                      int vec_t, float* st, int64_t sstm,
+                                                      uint32_t nbc, uint32_t cb0, uint32_t ntiles) {
+  __shared__ DualSmem sm;
+  DenseTiles geo{M, nbc, cb0};
+  dual_run<DT, EDGE>(geo, ntiles, x, N, sxm, round_scale != 0, q, sqm, s, ssm, qt, sqtm, vec_t != 0,
+                     st, sstm, sm);
 }
 
-// Grouped: block row = one 128-token chunk of an expert (see cin_grouped.h).  Rows
-// outside every expert range are not quantized.
-template <int DT>
+// Grouped: tiles are 128-token chunks of the experts (cin_grouped.h).  Rows outside
+// every expert range are not quantized.
+template <int DT, bool EDGE>
 __global__ __launch_bounds__(kThreads) void k_dual128_grouped(
     const void* __restrict__ x, int64_t T, int64_t N, int64_t sxm, int round_scale, uint8_t* q,
-    int64_t sqm, float* s, int64_t ssm, uint8_t* qt, int64_t sqtm, float* st, int64_t sstm,
-    const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t E, int64_t tcap) {
-  RowTile rt;
-  if (!grouped_tile(starts, ends, E, T, blockIdx.y, tcap, rt)) return;  // before any barrier
-  dual_tile<DT>(x, N, sxm, round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm, rt, blockIdx.x);
+    int64_t sqm, float* s, int64_t ssm, uint8_t* qt, int64_t sqtm, int vec_t, float* st,
+    int64_t sstm, const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t E,
+    int64_t tcap, uint32_t nbc, uint32_t cb0, uint32_t ntiles) {
+  __shared__ DualSmem sm;
+  GroupedTiles geo = grouped_tiles(starts, ends, E, T, tcap, nbc, cb0);
+  dual_run<DT, EDGE>(geo, ntiles, x, N, sxm, round_scale != 0, q, sqm, s, ssm, qt, sqtm, vec_t != 0,
+                     st, sstm, sm);
 }
 
-// ---------------------------------------------------------------------------
-// Re-quantization row(1x128) -> block(128x128).  x = fp32(code) * srow (fp32
-// product, as torch's dequantize_fp8_rowwise), then the block quantizer with
-// the fp32 floor and round_scale = False.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void requant_tile(const uint8_t* __restrict__ q, int64_t K, int64_t sqm,
-                                             const float* __restrict__ srow, int64_t ssm, uint8_t* qb,
-                                             int64_t sqbm, uint8_t* qbt, int64_t sqbtm, float* sblk,
-                                             int64_t ssbm, const RowTile rt, int64_t cb) {
-  __shared__ float red[kThreads / 64];
-  __shared__ TileT tileT;
-  // thread (lane16, rg): rows 8 rg .. 8 rg + 7, columns 8 lane16 .. 8 lane16 + 7
+// ----------------------------- row -> block re-quantization -----------------------------
+// x = fp32(code) * srow (fp32 product, as the reference's dequantize_fp8_rowwise), then
+// the block quantizer with the fp32 floor and round_scale = False (reference
+// src/kernels.py:784-788 re-quantizes the saved row-wise X this way).
+struct RawQ {
+  uint32_t w[8][2];  // 8 codes per row
+  float sr[8];       // row scale of each row (0 for rows past the tile)
+};
+
+template <bool EDGE>
+__device__ __forceinline__ void load_q(const uint8_t* __restrict__ q, int64_t sqm, int64_t K,
+                                       const float* __restrict__ srow, int64_t ssm,
+                                       const TileGeo& g, RawQ& o) {
   const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
-  const int64_t c = cb * 128 + lane16 * 8;
-  float v[8][8];
+  if constexpr (!EDGE) {
+    const __amdgpu_buffer_rsrc_t r =
+        make_rsrc(q + g.r0 * sqm + (int64_t)g.cb * 128, tile_extent(g.nr, sqm, 1));
+    const __amdgpu_buffer_rsrc_t rsc =
+        make_rsrc(srow + g.r0 * ssm + g.cb, g.nr > 0 ? ((int64_t)(g.nr - 1) * ssm + 1) * 4 : 0);
+    const uint32_t v0 = (uint32_t)(rg * 8) * (uint32_t)sqm + (uint32_t)(lane16 * 8);
+    const uint32_t s0 = (uint32_t)(rg * 8) * (uint32_t)(ssm * 4);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int ri = rg * 8 + i;
-    const int64_t r = rt.r0 + ri;
-    uint32_t w0 = 0, w1 = 0;
-    float sr = 0.0f;
-    if (ri < rt.nr) {
-      sr = srow[r * ssm + cb];
-      const uint8_t* qp = q + r * sqm + c;
-      if (c + 8 <= K) {
-        uint2 w = *reinterpret_cast<const uint2*>(qp);
-        w0 = w.x;
-        w1 = w.y;
-      } else {
-        for (int j = 0; j < 8; ++j)
-          if (c + j < K) (j < 4 ? w0 : w1) |= (uint32_t)qp[j] << (8 * (j & 3));
-      }
+    for (int i = 0; i < 8; ++i) {
+      const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(r, v0 + (uint32_t)i * (uint32_t)sqm, 0, kNT);
+      o.w[i][0] = w[0];
+      o.w[i][1] = w[1];
+      o.sr[i] = __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(rsc, s0 + (uint32_t)i * (uint32_t)(ssm * 4), 0, 0));
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t code = ((j < 4 ? w0 : w1) >> (8 * (j & 3))) & 0xffu;
-      const bool valid = (ri < rt.nr) && (c + j < K);
-      v[i][j] = valid ? __fmul_rn(e4m3_to_f32(code), sr) : 0.0f;
-    }
-  }
-  float a = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) a = fmaxf(a, fabsf(v[i][j]));
-  a = block_reduce_max(a, red);
-  a = fmaxf(a, kFloorF32);
-  const float s = compute_scale(a, false);
-  const float rcp = 1.0f / s;
-  uint32_t codes[8][2];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) quant_vals<8, 2>(v[i], s, rcp, codes[i]);
-  if (qb) {
+  } else {
+    const int64_t c = (int64_t)g.cb * 128 + lane16 * 8;
+    const int lastr = g.nr > 0 ? g.nr - 1 : 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int ri = rg * 8 + i;
-      if (ri >= rt.nr) continue;
-      uint8_t* qp = qb + (rt.r0 + ri) * sqbm + c;
-      if (c + 8 <= K) {
-        *reinterpret_cast<uint2*>(qp) = make_uint2(codes[i][0], codes[i][1]);
-      } else {
-        for (int j = 0; j < 8; ++j)
-          if (c + j < K) qp[j] = (uint8_t)((codes[i][j >> 2] >> (8 * (j & 3))) & 0xffu);
+      const bool rok = ri < g.nr;
+      const int64_t row = g.r0 + (ri < lastr ? ri : lastr);
+      const float sv = srow[row * ssm + g.cb];
+      o.sr[i] = rok ? sv : 0.0f;
+      o.w[i][0] = o.w[i][1] = 0u;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const bool ok = rok && c + j < K;
+        const uint32_t b = q[row * sqm + (c + j < K ? c + j : K - 1)];
+        o.w[i][j >> 2] |= (ok ? b : 0u) << (8 * (j & 3));
       }
     }
+  }
+}
+
+// fp32(code) of the 8 codes of a row (hardware e4m3fn -> fp32, exact).
+__device__ __forceinline__ void codes_f32(const uint32_t (&w)[2], float (&f)[8]) {
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], true);
+    f[4 * k] = lo[0];
+    f[4 * k + 1] = lo[1];
+    f[4 * k + 2] = hi[0];
+    f[4 * k + 3] = hi[1];
+  }
+}
+
+struct RequantSmem {
+  float red[kThreads / 64];
+  TileT tileT;
+};
+
+template <bool EDGE>
+__device__ __forceinline__ void requant_body(RawQ& raw, const TileGeo& g, int64_t K, uint8_t* qb,
+                                             int64_t sqbm, uint8_t* qbt, int64_t sqbtm, bool vec_t,
+                                             float* sblk, int64_t ssbm, RequantSmem& sm) {
+  const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
+  const int64_t c = (int64_t)g.cb * 128 + lane16 * 8;
+  // Block amax.  |fl(c sr)| = fl(|c| |sr|) is monotone in |c|, so a row's largest
+  // magnitude is fl(max |c| * |sr|); NaN products are skipped either way.
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float f[8];
+    codes_f32(raw.w[i], f);
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(f[j]));
+    a = fmaxf(a, __fmul_rn(m, fabsf(raw.sr[i])));
+  }
+  a = fmaxf(block_max_pos(a, sm.red), kFloorF32);
+  const float s = compute_scale(a, false);
+  const float d = divisor(s), r = 1.0f / s;
+  uint32_t codes[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    opaque(raw.w[i][0]);
+    opaque(raw.w[i][1]);
+    float v[8];
+    codes_f32(raw.w[i], v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[j] = __fmul_rn(v[j], raw.sr[i]);
+      if (EDGE && !(rg * 8 + i < g.nr && c + j < K)) v[j] = 0.0f;  // not 0 * srow: srow may be inf
+    }
+    quant8<2>(v, d, r, codes[i]);
+  }
+  if (qb) {
+    const RowOut<EDGE> out(qb, sqbm, K, g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out.put(i, codes[i]);
   }
   if (qbt) {
     uint32_t cols[8][2];
     t8x8(codes, cols);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) put_col8(tileT, lane16 * 8 + j, rg, cols[j][0], cols[j][1]);
+    for (int j = 0; j < 8; ++j) put_col8(sm.tileT, lane16 * 8 + j, rg, cols[j][0], cols[j][1]);
     __syncthreads();
-    store_tile_t(tileT, qbt, sqbtm, cb * 128, K, rt.t0, rt.tw);
+    put_tile_t<EDGE>(sm.tileT, qbt, sqbtm, K, g, vec_t);
   }
-  if (threadIdx.x == 0) sblk[rt.tb * ssbm + cb] = s;
+  if (threadIdx.x == 0) sblk[(g.t0 >> 7) * ssbm + g.cb] = s;
 }
 
+template <bool EDGE, typename Geo>
+__device__ __forceinline__ void requant_run(Geo& geo, uint32_t ntiles, const uint8_t* __restrict__ q,
+                                            int64_t K, int64_t sqm, const float* __restrict__ srow,
+                                            int64_t ssm, uint8_t* qb, int64_t sqbm, uint8_t* qbt,
+                                            int64_t sqbtm, bool vec_t, float* sblk, int64_t ssbm,
+                                            RequantSmem& sm) {
+  tile_loop<RawQ>(
+      ntiles, geo, [&](const TileGeo& g, RawQ& r) { load_q<EDGE>(q, sqm, K, srow, ssm, g, r); },
+      [&](const TileGeo& g, RawQ& r) {
+        if (g.nr == 0) return;  // uniform over the workgroup
+        requant_body<EDGE>(r, g, K, qb, sqbm, qbt, sqbtm, vec_t, sblk, ssbm, sm);
+      });
+}
+
+template <bool EDGE>
 __global__ __launch_bounds__(kThreads) void k_requant128(const uint8_t* __restrict__ q, int64_t M,
                                                          int64_t K, int64_t sqm,
                                                          const float* __restrict__ srow,
                                                          int64_t ssm, uint8_t* qb, int64_t sqbm,
-                                                         uint8_t* qbt, int64_t sqbtm, float* sblk,
-                                                         int64_t ssbm) {
-  requant_tile(q, K, sqm, srow, ssm, qb, sqbm, qbt, sqbtm, sblk, ssbm, dense_tile(blockIdx.y, M),
-               blockIdx.x);
+                                                         uint8_t* qbt, int64_t sqbtm, int vec_t,
+                                                         float* sblk, int64_t ssbm, uint32_t nbc,
+                                                         uint32_t cb0, uint32_t ntiles) {
+  __shared__ RequantSmem sm;
+  DenseTiles geo{M, nbc, cb0};
+  requant_run<EDGE>(geo, ntiles, q, K, sqm, srow, ssm, qb, sqbm, qbt, sqbtm, vec_t != 0, sblk, ssbm,
+                    sm);
 }
 
-// Grouped: block row = one 128-token chunk of an expert; block scales are indexed by
-// the chunk's padded position, codes by the input row (qb) or the padded column (qbt).
+// Grouped: tiles are 128-token chunks of the experts; block scales are indexed by the
+// chunk's padded position, codes by the input row (qb) or the padded column (qbt).
+template <bool EDGE>
 __global__ __launch_bounds__(kThreads) void k_requant128_grouped(
     const uint8_t* __restrict__ q, int64_t T, int64_t K, int64_t sqm, const float* __restrict__ srow,
-    int64_t ssm, uint8_t* qb, int64_t sqbm, uint8_t* qbt, int64_t sqbtm, float* sblk, int64_t ssbm,
-    const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t E, int64_t tcap) {
-  RowTile rt;
-  if (!grouped_tile(starts, ends, E, T, blockIdx.y, tcap, rt)) return;  // before any barrier
-  requant_tile(q, K, sqm, srow, ssm, qb, sqbm, qbt, sqbtm, sblk, ssbm, rt, blockIdx.x);
+    int64_t ssm, uint8_t* qb, int64_t sqbm, uint8_t* qbt, int64_t sqbtm, int vec_t, float* sblk,
+    int64_t ssbm, const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t E,
+    int64_t tcap, uint32_t nbc, uint32_t cb0, uint32_t ntiles) {
+  __shared__ RequantSmem sm;
+  GroupedTiles geo = grouped_tiles(starts, ends, E, T, tcap, nbc, cb0);
+  requant_run<EDGE>(geo, ntiles, q, K, sqm, srow, ssm, qb, sqbm, qbt, sqbtm, vec_t != 0, sblk, ssbm,
+                    sm);
 }
 
 // ---------------------------------------------------------------------------
@@ -714,6 +1164,31 @@ __global__ __launch_bounds__(kThreads) void k_transpose_u8(const uint8_t* __rest
 }
 
 
+// Workgroups for a persistent tile kernel: as many as the device holds at once (from the
+// kernel's occupancy and the device's CU count), at most one per tile.
+template <auto Kernel>
+unsigned resident_grid(uint32_t ntiles) {
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(Kernel),
+                                                     kThreads, 0) != hipSuccess || n < 1)
+      n = 1;
+    per_cu = n;
+  }
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+      n = 256;
+    cus[dev] = n;
+  }
+  const int64_t g = (int64_t)per_cu * cus[dev];
+  return (unsigned)(g < (int64_t)ntiles ? g : (int64_t)ntiles);
+}
+
 }  // namespace
 
 extern "C" {
@@ -756,23 +1231,40 @@ int cin_quant_blockwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_
   CIN_CHECK_ARG(!q || sqm >= N, "quant_blockwise: q row stride too small");
   CIN_CHECK_ARG(!qt || sqtm >= M, "quant_blockwise: qt row stride too small");
   CIN_CHECK_ARG(ssm >= nbn, "quant_blockwise: scale row stride too small");
-  CIN_CHECK_ARG(nbm < 65536 && nbn < ((int64_t)1 << 31), "quant_blockwise: grid too large");
+  CIN_CHECK_ARG(nbm < 65536 && nbm * nbn < ((int64_t)1 << 31), "quant_blockwise: grid too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int es = elem_size(x_dtype);
   const bool fast = bm == 128 && bn == 128 && sxn == 1 && aligned(x, 16) &&
-                    ((sxm * es) % 16 == 0) && (!q || (aligned(q, 8) && sqm % 8 == 0));
-  dim3 grid((unsigned)nbn, (unsigned)nbm);
+                    ((sxm * es) % 16 == 0) && tile_fits32(sxm * es) &&
+                    (!q || (aligned(q, 8) && sqm % 8 == 0 && tile_fits32(sqm)));
   if (fast) {
+    const int vec_t = qt && aligned(qt, 16) && sqtm % 16 == 0 && tile_fits32(sqtm);
+    // column blocks 0 .. nfull-1 whole; the last one, when partial, in an EDGE launch
+    const uint32_t nfull = (uint32_t)(N / 128), nrb = (uint32_t)nbm;
+#define CIN_BLOCK128(DT, EDGE, NBC, CB0)                                                   \
+  do {                                                                                     \
+    const uint32_t nt = nrb * (NBC);                                                       \
+    const unsigned grid_ = resident_grid<k_blockwise128<DT, EDGE>>(nt);                  \
+    hipLaunchKernelGGL((k_blockwise128<DT, EDGE>), grid_,                                  \
+                       kThreads, 0, s, x, M, N, sxm, round_scale, q, sqm, qt, sqtm, vec_t, scales, \
+                       ssm,                                                                \
+                       (uint32_t)(NBC), (uint32_t)(CB0), nt);                             \
+  } while (0)
+#define CIN_BLOCK128_ALL(DT)                                         \
+  do {                                                               \
+    if (nfull > 0) CIN_BLOCK128(DT, false, nfull, 0);                \
+    if (N % 128 != 0) CIN_BLOCK128(DT, true, 1, nfull);              \
+  } while (0)
     if (x_dtype == CIN_DT_BF16)
-      hipLaunchKernelGGL(k_blockwise128<CIN_DT_BF16>, grid, kThreads, 0, s, x, M, N, sxm,
-                         round_scale, q, sqm, qt, sqtm, scales, ssm);
+      CIN_BLOCK128_ALL(CIN_DT_BF16);
     else if (x_dtype == CIN_DT_F16)
-      hipLaunchKernelGGL(k_blockwise128<CIN_DT_F16>, grid, kThreads, 0, s, x, M, N, sxm,
-                         round_scale, q, sqm, qt, sqtm, scales, ssm);
+      CIN_BLOCK128_ALL(CIN_DT_F16);
     else
-      hipLaunchKernelGGL(k_blockwise128<CIN_DT_F32>, grid, kThreads, 0, s, x, M, N, sxm,
-                         round_scale, q, sqm, qt, sqtm, scales, ssm);
+      CIN_BLOCK128_ALL(CIN_DT_F32);
+#undef CIN_BLOCK128_ALL
+#undef CIN_BLOCK128
   } else {
+    dim3 grid((unsigned)nbn, (unsigned)nbm);
     hipLaunchKernelGGL(k_blockwise_generic, grid, kThreads, 0, s, x, x_dtype, M, N, sxm, sxn, bm,
                        bn, round_scale, q, sqm, qt, sqtm, scales, ssm, nbn);
   }
@@ -807,18 +1299,33 @@ int cin_quant_dual(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t s
   hipStream_t stream_ = static_cast<hipStream_t>(stream);
   const int es = elem_size(dy_dtype);
   const bool fast = sdn == 1 && aligned(dy, 16) && ((sdm * es) % 16 == 0) && aligned(q, 8) &&
-                    sqm % 8 == 0 && cdiv(M, 128) < 65536;
+                    sqm % 8 == 0 && tile_fits32(sdm * es) && tile_fits32(sqm) &&
+                    cdiv(M, 128) * cdiv(N, 128) < ((int64_t)1 << 31);
   if (fast) {
-    dim3 grid((unsigned)cdiv(N, 128), (unsigned)cdiv(M, 128));
+    const int vec_t = aligned(qt, 16) && sqtm % 16 == 0 && tile_fits32(sqtm);
+    const uint32_t nfull = (uint32_t)(N / 128), nrb = (uint32_t)cdiv(M, 128);
+#define CIN_DUAL128(DT, EDGE, NBC, CB0)                                                        \
+  do {                                                                                         \
+    const uint32_t nt = nrb * (NBC);                                                           \
+    const unsigned grid_ = resident_grid<k_dual128<DT, EDGE>>(nt);                             \
+    hipLaunchKernelGGL((k_dual128<DT, EDGE>), grid_, kThreads, 0,                              \
+                       stream_, dy, M, N, sdm, round_scale, q, sqm, s, ssm, qt, sqtm, vec_t, st,  \
+                       sstm,                                                                   \
+                       (uint32_t)(NBC), (uint32_t)(CB0), nt);                                  \
+  } while (0)
+#define CIN_DUAL128_ALL(DT)                                   \
+  do {                                                        \
+    if (nfull > 0) CIN_DUAL128(DT, false, nfull, 0);          \
+    if (N % 128 != 0) CIN_DUAL128(DT, true, 1, nfull);        \
+  } while (0)
     if (dy_dtype == CIN_DT_BF16)
-      hipLaunchKernelGGL(k_dual128<CIN_DT_BF16>, grid, kThreads, 0, stream_, dy, M, N, sdm,
-                         round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm);
+      CIN_DUAL128_ALL(CIN_DT_BF16);
     else if (dy_dtype == CIN_DT_F16)
-      hipLaunchKernelGGL(k_dual128<CIN_DT_F16>, grid, kThreads, 0, stream_, dy, M, N, sdm,
-                         round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm);
+      CIN_DUAL128_ALL(CIN_DT_F16);
     else
-      hipLaunchKernelGGL(k_dual128<CIN_DT_F32>, grid, kThreads, 0, stream_, dy, M, N, sdm,
-                         round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm);
+      CIN_DUAL128_ALL(CIN_DT_F32);
+#undef CIN_DUAL128_ALL
+#undef CIN_DUAL128
     return cin_check_launch("quant_dual");
   }
   // Strided input: two generic row-wise passes (dy, then dy^T through strides).
@@ -843,18 +1350,34 @@ int cin_quant_dual_grouped(const void* dy, int dy_dtype, int64_t T, int64_t N, i
                 "quant_dual_grouped: bad row-wise outputs");
   CIN_CHECK_ARG(sqtm >= 128 && sstm >= sqtm / 128,
                 "quant_dual_grouped: transposed rows must hold the padded token axis");
-  CIN_CHECK_ARG(cdiv(T, 128) + E < 65536, "quant_dual_grouped: too many chunks");
+  CIN_CHECK_ARG((cdiv(T, 128) + E) * cdiv(N, 128) < ((int64_t)1 << 31),
+                "quant_dual_grouped: too many tiles");
+  CIN_CHECK_ARG(tile_fits32(sdm * es) && tile_fits32(sqm) && tile_fits32(sqtm),
+                "quant_dual_grouped: row strides too large");
+  const int vec_t = aligned(qt, 16) && sqtm % 16 == 0;
   hipStream_t stream_ = static_cast<hipStream_t>(stream);
-  dim3 grid((unsigned)cdiv(N, 128), (unsigned)(cdiv(T, 128) + E));
+  const uint32_t nfull = (uint32_t)(N / 128), nch = (uint32_t)(cdiv(T, 128) + E);
+#define CIN_DUALG(DT, EDGE, NBC, CB0)                                                           \
+  do {                                                                                          \
+    const uint32_t nt = nch * (NBC);                                                            \
+    const unsigned grid_ = resident_grid<k_dual128_grouped<DT, EDGE>>(nt);                      \
+    hipLaunchKernelGGL((k_dual128_grouped<DT, EDGE>), grid_,                                    \
+                       kThreads, 0, stream_, dy, T, N, sdm, round_scale, q, sqm, s, ssm, qt, sqtm, \
+                       vec_t, st, sstm, starts, ends, E, sqtm, (uint32_t)(NBC), (uint32_t)(CB0), nt); \
+  } while (0)
+#define CIN_DUALG_ALL(DT)                                   \
+  do {                                                      \
+    if (nfull > 0) CIN_DUALG(DT, false, nfull, 0);          \
+    if (N % 128 != 0) CIN_DUALG(DT, true, 1, nfull);        \
+  } while (0)
   if (dy_dtype == CIN_DT_BF16)
-    hipLaunchKernelGGL(k_dual128_grouped<CIN_DT_BF16>, grid, kThreads, 0, stream_, dy, T, N, sdm,
-                       round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm, starts, ends, E, sqtm);
+    CIN_DUALG_ALL(CIN_DT_BF16);
   else if (dy_dtype == CIN_DT_F16)
-    hipLaunchKernelGGL(k_dual128_grouped<CIN_DT_F16>, grid, kThreads, 0, stream_, dy, T, N, sdm,
-                       round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm, starts, ends, E, sqtm);
+    CIN_DUALG_ALL(CIN_DT_F16);
   else
-    hipLaunchKernelGGL(k_dual128_grouped<CIN_DT_F32>, grid, kThreads, 0, stream_, dy, T, N, sdm,
-                       round_scale, q, sqm, s, ssm, qt, sqtm, st, sstm, starts, ends, E, sqtm);
+    CIN_DUALG_ALL(CIN_DT_F32);
+#undef CIN_DUALG_ALL
+#undef CIN_DUALG
   return cin_check_launch("quant_dual_grouped");
 }
 
@@ -868,11 +1391,25 @@ int cin_requant_row_to_block_grouped(const uint8_t* q, int64_t T, int64_t K, int
   CIN_CHECK_ARG(aligned(q, 8) && sqm % 8 == 0 && sqm >= K, "requant_grouped: q must be 8-byte aligned rows");
   CIN_CHECK_ARG(sqbtm >= 128 && ssm >= cdiv(K, 128) && ssbm >= cdiv(K, 128),
                 "requant_grouped: bad output strides");
-  CIN_CHECK_ARG(cdiv(T, 128) + E < 65536, "requant_grouped: too many chunks");
+  CIN_CHECK_ARG((cdiv(T, 128) + E) * cdiv(K, 128) < ((int64_t)1 << 31),
+                "requant_grouped: too many tiles");
+  CIN_CHECK_ARG(tile_fits32(sqm) && tile_fits32(ssm * 4) && tile_fits32(sqbtm),
+                "requant_grouped: row strides too large");
+  const int vec_t = aligned(qbt, 16) && sqbtm % 16 == 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 grid((unsigned)cdiv(K, 128), (unsigned)(cdiv(T, 128) + E));
-  hipLaunchKernelGGL(k_requant128_grouped, grid, kThreads, 0, s, q, T, K, sqm, srow, ssm,
-                     (uint8_t*)nullptr, (int64_t)0, qbt, sqbtm, sblk, ssbm, starts, ends, E, sqbtm);
+  const uint32_t nfull = (uint32_t)(K / 128), nch = (uint32_t)(cdiv(T, 128) + E);
+#define CIN_REQG(EDGE, NBC, CB0)                                                                  \
+  do {                                                                                            \
+    const uint32_t nt = nch * (NBC);                                                              \
+    const unsigned grid_ = resident_grid<k_requant128_grouped<EDGE>>(nt);                         \
+    hipLaunchKernelGGL(k_requant128_grouped<EDGE>, grid_,                                         \
+                       kThreads, 0, s, q, T, K, sqm, srow, ssm, (uint8_t*)nullptr, (int64_t)0, qbt, \
+                       sqbtm, vec_t, sblk, ssbm, starts, ends, E, sqbtm, (uint32_t)(NBC),         \
+                       (uint32_t)(CB0), nt);                                                        \
+  } while (0)
+  if (nfull > 0) CIN_REQG(false, nfull, 0);
+  if (K % 128 != 0) CIN_REQG(true, 1, nfull);
+#undef CIN_REQG
   return cin_check_launch("requant_row_to_block_grouped");
 }
 
@@ -887,12 +1424,24 @@ int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm
   CIN_CHECK_ARG(!qb || (aligned(qb, 8) && sqbm % 8 == 0 && sqbm >= K),
                 "requant: qb must be 8-byte aligned rows");
   CIN_CHECK_ARG(!qbt || sqbtm >= M, "requant: qbt row stride too small");
-  CIN_CHECK_ARG(ssm >= cdiv(K, 128) && ssbm >= cdiv(K, 128) && cdiv(M, 128) < 65536,
-                "requant: bad scale stride");
+  CIN_CHECK_ARG(ssm >= cdiv(K, 128) && ssbm >= cdiv(K, 128), "requant: bad scale stride");
+  CIN_CHECK_ARG(cdiv(M, 128) * cdiv(K, 128) < ((int64_t)1 << 31), "requant: too many tiles");
+  CIN_CHECK_ARG(tile_fits32(sqm) && tile_fits32(ssm * 4) && (!qb || tile_fits32(sqbm)),
+                "requant: row strides too large");
+  const int vec_t = qbt && aligned(qbt, 16) && sqbtm % 16 == 0 && tile_fits32(sqbtm);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 grid((unsigned)cdiv(K, 128), (unsigned)cdiv(M, 128));
-  hipLaunchKernelGGL(k_requant128, grid, kThreads, 0, s, q, M, K, sqm, srow, ssm, qb, sqbm, qbt,
-                     sqbtm, sblk, ssbm);
+  const uint32_t nfull = (uint32_t)(K / 128), nrb = (uint32_t)cdiv(M, 128);
+#define CIN_REQ(EDGE, NBC, CB0)                                                                 \
+  do {                                                                                          \
+    const uint32_t nt = nrb * (NBC);                                                            \
+    const unsigned grid_ = resident_grid<k_requant128<EDGE>>(nt);                               \
+    hipLaunchKernelGGL(k_requant128<EDGE>, grid_, kThreads, 0, s, q,                            \
+                       M, K, sqm, srow, ssm, qb, sqbm, qbt, sqbtm, vec_t, sblk, ssbm, (uint32_t)(NBC), \
+                       (uint32_t)(CB0), nt);                                                    \
+  } while (0)
+  if (nfull > 0) CIN_REQ(false, nfull, 0);
+  if (K % 128 != 0) CIN_REQ(true, 1, nfull);
+#undef CIN_REQ
   return cin_check_launch("requant_row_to_block");
 }
 

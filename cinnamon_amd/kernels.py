@@ -67,6 +67,18 @@ def _codes_u8(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def _rows8(q: torch.Tensor) -> torch.Tensor:
+    """2-D uint8 codes with unit column stride and 8-byte aligned rows (the tile kernels
+    read 8 codes at a time): q itself when it qualifies, else a copy whose rows are padded
+    to a multiple of 8 bytes."""
+    if q.stride(1) == 1 and q.stride(0) % 8 == 0 and q.data_ptr() % 8 == 0:
+        return q
+    M, K = q.shape
+    buf = torch.empty((M, _cdiv(max(K, 1), 8) * 8), dtype=torch.uint8, device=q.device)
+    buf[:, :K].copy_(q)
+    return buf[:, :K]
+
+
 # ---------------------------------------------------------------------------
 # Quantization (reference src/kernels.py:178-259)
 # ---------------------------------------------------------------------------
@@ -147,9 +159,7 @@ def requantize_rowwise_to_blockwise(x_fp8: torch.Tensor, x_scale: torch.Tensor,
     """
     _require(x_fp8.is_cuda, "Input must be on CUDA")
     M, K = x_fp8.shape
-    q = _codes_u8(x_fp8)
-    if q.stride(1) != 1 or q.stride(0) % 8 or q.data_ptr() % 8:
-        q = q.contiguous()
+    q = _rows8(_codes_u8(x_fp8))
     _require(x_scale.shape == (M, _cdiv(K, 128)), "row scales must be [M, ceil(K/128)]")
     xs = x_scale if x_scale.stride(1) == 1 else x_scale.contiguous()
     sblk = torch.empty((_cdiv(M, 128), _cdiv(K, 128)), dtype=torch.float32, device=x_fp8.device)

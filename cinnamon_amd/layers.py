@@ -11,7 +11,7 @@ from __future__ import annotations
 import torch
 
 from ._lib import call, dtype_code, ptr, stream_of
-from .kernels import (_cdiv, _kcontig, _require, quantize_fp8_blockwise_t,
+from .kernels import (_cdiv, _codes_u8, _rows8, _kcontig, _require, quantize_fp8_blockwise_t,
                       quantize_fp8_rowwise)
 
 
@@ -103,9 +103,7 @@ def requantize_grouped_t(x_fp8: torch.Tensor, x_scale: torch.Tensor, expert_star
     equals quantize_fp8_blockwise(dequantize_fp8_rowwise(x_fp8, x_scale)[s_e:e_e]) (reference
     src/kernels.py:784-787 per slice)."""
     _require(x_fp8.is_cuda, "Input must be on CUDA")
-    q = x_fp8.view(torch.uint8) if x_fp8.dtype == torch.float8_e4m3fn else x_fp8
-    if q.stride(1) != 1 or q.stride(0) % 8 or q.data_ptr() % 8:
-        q = q.contiguous()
+    q = _rows8(_codes_u8(x_fp8))
     starts, ends = _ranges(expert_starts, expert_ends)
     T, K = q.shape
     E = starts.numel()

@@ -144,7 +144,6 @@ def test_blockwise_bit_exact(kern, dev, shape, dtype, std):
     _assert_scales_equal(s2, rs_, "block scales (dual layout)")
 
 
-@pytest.mark.parametrize("bm,bn,rs", [(64, 64, False), (128, 1, False), (1, 128, True), (32, 256, True)])
 def _special_matrix(M, N, dtype, seed):
     x = torch.randn(M, N, generator=torch.Generator().manual_seed(seed))
     x[:, 0] = -0.0
@@ -279,3 +278,53 @@ def test_dequantizers(kern, dev):
     bq, bs = orc.quant_blockwise(x.float())
     got = kern.dequantize_fp8(bq.to(dev), bs.to(dev))
     assert torch.equal(got.cpu(), orc.dequant_block_bf16(bq, bs))
+
+
+# ---------------------------------------------------------------------------
+# 128 x 128 tile kernels: many tiles per workgroup, ragged last row block and column
+# block (the column edge runs as a launch of its own)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,dtype", [
+    (1000, 1100, torch.bfloat16),
+    (2050, 4100, torch.float16),
+    (4096, 640, torch.float32),
+])
+def test_tile_kernels_ragged_many_tiles(kern, dev, M, N, dtype):
+    x = _activations(M, N, seed=11, dtype=dtype)
+    rq, rs_ = orc.quant_blockwise(x)
+    q2, qt, s2 = kern.quantize_fp8_blockwise_t(x.to(dev))
+    _assert_codes_equal(q2, rq, "block codes")
+    _assert_codes_equal(qt, rq.view(torch.uint8).t().contiguous(), "block transposed codes")
+    _assert_scales_equal(s2, rs_, "block scales")
+    q, s, qt, st = kern.quantize_fp8_dual(x.to(dev))
+    rq, rs_ = orc.quant_rowwise(x)
+    rqt, rst = orc.quant_rowwise(x.t().contiguous())
+    _assert_codes_equal(q, rq, "dual row codes")
+    _assert_scales_equal(s, rs_, "dual row scales")
+    _assert_codes_equal(qt, rqt, "dual transposed codes")
+    _assert_scales_equal(st, rst, "dual transposed scales")
+    want_q, want_s = orc.quant_blockwise(orc.dequant_rowwise(rq, rs_), 128, 128, False)
+    qbt, sbt = kern.requantize_rowwise_to_blockwise(q.view(torch.float8_e4m3fn), s, transposed=True)
+    _assert_codes_equal(qbt, want_q.view(torch.uint8).t().contiguous(), "requant transposed codes")
+    _assert_scales_equal(sbt, want_s, "requant scales")
+
+
+def test_requant_every_code(kern, dev):
+    """All 256 e4m3fn codes (NaN codes included) through the re-quantization: the
+    hardware code -> fp32 conversion against torch's, with row scales spanning many
+    binades and one infinite row scale (its tile's scale is inf: finite values -> +-0,
+    inf and NaN -> NaN -> -448)."""
+    g = torch.Generator().manual_seed(21)
+    M, K = 384, 512
+    codes = torch.stack([torch.randperm(256, generator=g)[: K // 2].repeat(2) for _ in range(M)])
+    codes = codes.to(torch.uint8).view(torch.float8_e4m3fn)
+    scales = torch.exp2(torch.randint(-20, 20, (M, K // 128), generator=g).float())
+    scales *= 1 + torch.rand(M, K // 128, generator=g)
+    scales[300, 2] = float("inf")
+    want_q, want_s = orc.quant_blockwise(orc.dequant_rowwise(codes, scales), 128, 128, False)
+    qb, sb = kern.requantize_rowwise_to_blockwise(codes.to(dev), scales.to(dev), transposed=False)
+    _assert_codes_equal(qb, want_q, "every-code requant codes")
+    _assert_scales_equal(sb, want_s, "every-code requant scales")
+    qbt, sbt = kern.requantize_rowwise_to_blockwise(codes.to(dev), scales.to(dev), transposed=True)
+    _assert_codes_equal(qbt, want_q.view(torch.uint8).t().contiguous(), "every-code requant^T codes")
+    _assert_scales_equal(sbt, want_s, "every-code requant^T scales")
