@@ -257,8 +257,9 @@ namespace big {
 // on its own MFMA.  The ring runs across K blocks.
 //
 // Operands move global -> LDS by DMA (buffer_load ... lds), one K block ahead: right
-// after the barrier of block kb frees a stage, the DMA of block kb+2 into it is issued,
-// and it has a whole block to land.  No VGPR staging and no ds_write.  The barrier sits
+// after the barrier of block kb frees a stage, the DMA of block kb+2 into it starts (its
+// four row groups are issued 8 steps apart), and it has a whole block to land.  No VGPR
+// staging and no ds_write.  The barrier sits
 // before the last m-tile group, so the next block's fragments are read while that
 // group's MFMAs run.  The DMA is issued from inline assembly: the compiler treats its
 // own LDS-DMA builtin as aliasing every LDS read and would wait for it before each one.
@@ -336,15 +337,20 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
   const uint32_t lds_a = (uint32_t)(uintptr_t)&sm.a[0][0] + (uint32_t)(wave * 64 * 16);
   const uint32_t lds_b = (uint32_t)(uintptr_t)&sm.b[0][0] + (uint32_t)(wave * 64 * 16);
   const uint32_t lds_s = (uint32_t)(uintptr_t)&sm.sa[0][0] + (uint32_t)((wave & 3) * 64 * 4);
-#define CIN_DMA(kb, stg)                                                                      \
+// Row group g (tile rows 64 g .. 64 g + 63) of both operands for block kb into stage stg;
+// group 0 also brings the block's A-row scales.
+#define CIN_DMA_GROUP(kb, stg, g)                                                             \
   do {                                                                                        \
     const uint32_t ko = (uint32_t)(kb) * TK;                                                  \
     const uint32_t so = (uint32_t)(stg) * kTileBytes;                                         \
-    _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_) {                                        \
-      dma16(ra, offA, ko + i_ * stepa, lds_a + so + i_ * kThreads * 16);                      \
-      dma16(rb, offB, ko + i_ * stepb, lds_b + so + i_ * kThreads * 16);                      \
-    }                                                                                         \
-    if (wave < 4) dma4(rsa, offS, (uint32_t)(kb) * stepsa, lds_s + (uint32_t)(stg) * TM * 4); \
+    dma16(ra, offA, ko + (g) * stepa, lds_a + so + (g) * kThreads * 16);                      \
+    dma16(rb, offB, ko + (g) * stepb, lds_b + so + (g) * kThreads * 16);                      \
+    if ((g) == 0 && wave < 4)                                                                 \
+      dma4(rsa, offS, (uint32_t)(kb) * stepsa, lds_s + (uint32_t)(stg) * TM * 4);             \
+  } while (0)
+#define CIN_DMA(kb, stg)                                                                      \
+  do {                                                                                        \
+    _Pragma("unroll") for (int g_ = 0; g_ < 4; ++g_) CIN_DMA_GROUP(kb, stg, g_);              \
   } while (0)
 
   // Fragment addresses.  Every fragment row is (16-aligned base) + l16, so its swizzle
@@ -420,19 +426,24 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
       asm volatile("" : "+v"(bf[j]));
       p[s8 & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af[i & 1], zero, 0, 0, 0, 0, 0, 0);
       asm volatile("" : "+v"(bf[j]));
+      // row groups 1-3 of block kb+1 (group 0 went out after the previous barrier), one
+      // every 8 steps: a burst of 8 DMA issues per wave stalls the MFMA issue more than
+      // the same issues spread over the block
+      if ((s8 == 4 || s8 == 12 || s8 == 20) && kb >= 1 && kb + 1 < nk)
+        CIN_DMA_GROUP(kb + 1, st ^ 1, (s8 + 4) >> 3);
       // fragment of m-tile i+1 (its slot's previous user, m-tile i-1, is done)
       if (j == 0 && i < 7) af[(i + 1) & 1] = CIN_AFRAG(st, i + 1);
       // scale of m-tile i+1 (its slot's previous user, the FMAs of m-tile i-1, are done)
       if (j == 3 && i < 7) cs[(i + 1) & 1] = sa8[i + 1] * sbv;
       if (more) {
         if (s8 == 28) {
-          // block kb+1's DMA (issued a block ago) has landed in stage st^1, and stage st
-          // is no longer read (its last fragment, m-tile 7, was read at step 24): after
-          // the barrier, block kb+2 goes into stage st and the next block's fragments
-          // are read
+          // block kb+1's DMA (issued since the previous barrier) has landed in stage st^1,
+          // and stage st is no longer read (its last fragment, m-tile 7, was read at step
+          // 24): after the barrier, block kb+2 starts into stage st (row group 0 now, the
+          // rest during the next block) and the next block's fragments are read
           wait_dma();
           __syncthreads();
-          if (kb + 2 < nk) CIN_DMA(kb + 2, st);
+          if (kb + 2 < nk) CIN_DMA_GROUP(kb + 2, st, 0);
           af[0] = CIN_AFRAG(st ^ 1, 0);
           CIN_SA8(st ^ 1);
         }
@@ -449,6 +460,7 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
     for (int r = 0; r < 4; ++r) acc[7][s8 & 3][r] = fmaf(p[s8 & 3][r], cs[1], acc[7][s8 & 3][r]);
   }
 #undef CIN_DMA
+#undef CIN_DMA_GROUP
 #undef CIN_FRAG
 #undef CIN_AFRAG
 #undef CIN_BFRAG
