@@ -45,6 +45,7 @@ SIGNATURES: dict[str, list] = {
                              _p, _i64, _p],
     "cin_grouped_gemm_fp8_wgrad": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i64,
                                    _i64, _i64, _i64, _p, _i32, _i64, _i64, _p],
+    "cin_silu_mul_quant_rowwise": [_p, _i32, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p, _i64, _p],
 }
 
 _lock = threading.Lock()
@@ -100,11 +101,13 @@ def call(name: str, *args) -> None:
         raise CinnamonLibraryError(msg)
 
 
-def dtype_code(t: torch.Tensor) -> int:
+def dtype_code(t) -> int:
+    """CIN_DT_* code of a tensor's dtype (or of a torch.dtype)."""
+    dt = t if isinstance(t, torch.dtype) else t.dtype
     try:
-        return _DTYPE_CODE[t.dtype]
+        return _DTYPE_CODE[dt]
     except KeyError:
-        raise ValueError(f"unsupported dtype {t.dtype}; expected bfloat16, float16 or float32") from None
+        raise ValueError(f"unsupported dtype {dt}; expected bfloat16, float16 or float32") from None
 
 
 def stream_of(t: torch.Tensor) -> ctypes.c_void_p:

@@ -1164,6 +1164,59 @@ __global__ __launch_bounds__(kThreads) void k_transpose_u8(const uint8_t* __rest
 }
 
 
+// ---------------------------------------------------------------------------
+// SwiGLU activation fused into the row-wise quantizer (reference GroupedExperts.forward,
+// src/layers.py:72-74): h = silu(h12[:, :H]) * h12[:, H:] in fp32, rounded to the
+// activation dtype OT, then the 1x128 tiles of h exactly as quantize_fp8_rowwise(h)
+// (src/kernels.py:19-71).  silu(a) = a / (1 + exp(-a)) with an IEEE division: the
+// operations of torch's GPU silu, so the codes equal quantizing torch's h.  A 16-lane DPP
+// row owns one tile, 8 consecutive elements per lane.
+// ---------------------------------------------------------------------------
+template <int OT>
+__device__ __forceinline__ float round_to(float h) {
+  if constexpr (OT == CIN_DT_BF16) return __uint_as_float(f32_to_bf16_bits(h) << 16);
+  else if constexpr (OT == CIN_DT_F16) return (float)(_Float16)h;
+  else return h;
+}
+
+template <int IT, int OT>
+__global__ __launch_bounds__(kThreads) void k_silu_mul_rowwise128(
+    const void* __restrict__ h12, int64_t s12, int64_t H, int round_scale, uint8_t* __restrict__ q,
+    int64_t sqm, float* __restrict__ sc, int64_t ssm, uint32_t nb, uint32_t ntiles) {
+  const int li = threadIdx.x & 15;
+  const uint32_t G = (gridDim.x * kThreads) / 16;
+  const bool rs = round_scale != 0;
+  for (uint32_t t = (blockIdx.x * kThreads + threadIdx.x) / 16; t < ntiles; t += G) {
+    const uint32_t row = t / nb, cb = t - row * nb;
+    const int64_t c = (int64_t)cb * 128 + li * 8;
+    int64_t nv = H - c;
+    nv = nv < 0 ? 0 : (nv > 8 ? 8 : nv);
+    Vec8<IT> a, b;
+    load8<IT>(h12, (int64_t)row * s12 + c, nv, a);
+    load8<IT>(h12, (int64_t)row * s12 + H + c, nv, b);
+    float v[8];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float x = a.v[j];
+      const float silu = x / (1.0f + expf(-x));
+      v[j] = j < nv ? round_to<OT>(silu * b.v[j]) : 0.0f;
+      m = fmaxf(m, fabsf(v[j]));
+    }
+    m = row16_max_pos(m);
+    const float sv = compute_scale(fmaxf(m, amax_floor(OT)), rs);
+    uint32_t w[2];
+    quant8<kDivSteps<OT>>(v, divisor(sv), 1.0f / sv, w);
+    uint8_t* qp = q + (int64_t)row * sqm + c;
+    if (nv == 8) {
+      *reinterpret_cast<uint2*>(qp) = make_uint2(w[0], w[1]);
+    } else {
+      for (int j = 0; j < nv; ++j) qp[j] = (uint8_t)((w[j >> 2] >> (8 * (j & 3))) & 0xffu);
+    }
+    if (li == 0) sc[(int64_t)row * ssm + cb] = sv;
+  }
+}
+
 // Workgroups for a persistent tile kernel: as many as the device holds at once (from the
 // kernel's occupancy and the device's CU count), at most one per tile.
 template <auto Kernel>
@@ -1443,6 +1496,43 @@ int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm
   if (K % 128 != 0) CIN_REQ(true, 1, nfull);
 #undef CIN_REQ
   return cin_check_launch("requant_row_to_block");
+}
+
+int cin_silu_mul_quant_rowwise(const void* h12, int in_dtype, int64_t M, int64_t H, int64_t s12,
+                               int out_dtype, int round_scale, uint8_t* q, int64_t sqm,
+                               float* scales, int64_t ssm, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(in_dtype) && valid_dtype(out_dtype), "silu_mul_quant: unsupported dtype");
+  CIN_CHECK_ARG(M >= 0 && H >= 0, "silu_mul_quant: negative shape");
+  if (M == 0 || H == 0) return CIN_OK;
+  CIN_CHECK_ARG(h12 && q && scales, "silu_mul_quant: null pointer");
+  const int es = elem_size(in_dtype);
+  CIN_CHECK_ARG(aligned(h12, 16) && (s12 * es) % 16 == 0 && (H * es) % 16 == 0 && s12 >= 2 * H,
+                "silu_mul_quant: h12 rows must hold 2H elements at 16-byte aligned offsets");
+  CIN_CHECK_ARG(aligned(q, 8) && sqm % 8 == 0 && sqm >= H && ssm >= cdiv(H, 128),
+                "silu_mul_quant: bad outputs");
+  const int64_t nb = cdiv(H, 128);
+  CIN_CHECK_ARG(M * nb < ((int64_t)1 << 31), "silu_mul_quant: too many tiles");
+  const uint32_t ntiles = (uint32_t)(M * nb);
+  const unsigned grid = grid_for(ntiles, kThreads / 16, 16384);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define CIN_SILU(IT, OT)                                                                        \
+  hipLaunchKernelGGL((k_silu_mul_rowwise128<IT, OT>), grid, kThreads, 0, s, h12, s12, H,         \
+                     round_scale, q, sqm, scales, ssm, (uint32_t)nb, ntiles)
+#define CIN_SILU_OT(IT)                                                                         \
+  do {                                                                                          \
+    if (out_dtype == CIN_DT_BF16) CIN_SILU(IT, CIN_DT_BF16);                                    \
+    else if (out_dtype == CIN_DT_F16) CIN_SILU(IT, CIN_DT_F16);                                 \
+    else CIN_SILU(IT, CIN_DT_F32);                                                              \
+  } while (0)
+  if (in_dtype == CIN_DT_BF16)
+    CIN_SILU_OT(CIN_DT_BF16);
+  else if (in_dtype == CIN_DT_F16)
+    CIN_SILU_OT(CIN_DT_F16);
+  else
+    CIN_SILU_OT(CIN_DT_F32);
+#undef CIN_SILU_OT
+#undef CIN_SILU
+  return cin_check_launch("silu_mul_quant_rowwise");
 }
 
 int cin_transpose_u8(const uint8_t* src, int64_t R, int64_t C, int64_t lds, uint8_t* dst,

@@ -168,6 +168,25 @@ def fp8_grouped_dgrad(g_fp8: torch.Tensor, g_scale: torch.Tensor, w_codes_t: tor
     return out
 
 
+def silu_mul_quantize_fp8(h12: torch.Tensor, out_dtype: torch.dtype | None = None,
+                          round_scale: bool = False):
+    """quantize_fp8_rowwise((silu(h1) * h2).to(out_dtype)) with [h1 h2] = h12.float().chunk(2, -1),
+    in one pass over h12 (reference src/layers.py:72-74 feeding src/kernels.py:178-216).
+    h12 [M, 2H] (bf16, fp16 or fp32, H a multiple of 8); out_dtype defaults to h12's dtype.
+    Returns (codes float8_e4m3fn [M, H], scales fp32 [M, ceil(H/128)])."""
+    _require(h12.is_cuda, "Input must be on CUDA")
+    _require(h12.ndim == 2 and h12.shape[1] % 2 == 0, "h12 must be [M, 2H]")
+    out_dtype = out_dtype or h12.dtype
+    M, H = h12.shape[0], h12.shape[1] // 2
+    x = h12 if (h12.stride(1) == 1 and h12.data_ptr() % 16 == 0
+                and (h12.stride(0) * h12.element_size()) % 16 == 0) else h12.contiguous()
+    q = torch.empty((M, H), dtype=torch.float8_e4m3fn, device=h12.device)
+    s = torch.empty((M, _cdiv(H, 128)), dtype=torch.float32, device=h12.device)
+    call("cin_silu_mul_quant_rowwise", ptr(x), dtype_code(x), M, H, x.stride(0), dtype_code(out_dtype),
+         int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), stream_of(x))
+    return q, s
+
+
 class FP8GroupedExpertsFunction(torch.autograd.Function):
     """SwiGLU experts in FP8: out = W3_e (silu(h1) * h2), [h1 h2] = W12_e x for each expert's
     rows (reference GroupedExperts.forward, src/layers.py:56-87: GEMM(w12), silu * mul in
@@ -189,9 +208,7 @@ class FP8GroupedExpertsFunction(torch.autograd.Function):
                                starts, ends, out_dtype=torch.bfloat16,
                                out=torch.zeros((sorted_x.shape[0], H2), dtype=torch.bfloat16,
                                                device=sorted_x.device))
-        h1, h2 = h12.float().chunk(2, dim=-1)
-        h = (torch.nn.functional.silu(h1) * h2).to(sorted_x.dtype)
-        hq, hs = quantize_fp8_rowwise(h)
+        hq, hs = silu_mul_quantize_fp8(h12, out_dtype=sorted_x.dtype)
         w3f = w3 if w3.dtype == torch.float32 else w3.float()
         w3q, w3qt, w3s = quantize_fp8_blockwise_t(w3f.reshape(E * D, H))
         out = fp8_grouped_gemm(hq, hs, w3q.view(E, D, H), w3s.view(E, D // 128, -1), starts, ends,

@@ -225,6 +225,20 @@ int cin_grouped_gemm_f16(const void* A, int a_dtype, int64_t lda, const void* B,
                          int64_t E, int64_t T, int64_t N, int64_t K, void* C, int64_t ldc,
                          void* stream);
 
+/*
+ * SwiGLU activation fused into the row-wise quantizer.  Replaces, in the experts' forward
+ * (reference GroupedExperts.forward, src/layers.py:72-74), the chain
+ *   h1, h2 = h12.float().chunk(2, -1);  h = (silu(h1) * h2).to(dtype)
+ * followed by quantize_fp8_rowwise(h) (src/kernels.py:178-216) before the down GEMM:
+ *   h12    [M, 2H] of in_dtype (row stride s12; both halves 16-byte aligned)
+ *   q      [M, H] codes (row stride sqm), scales [M, ceil(H/128)] (row stride ssm)
+ *   out_dtype is the dtype h is rounded to before quantization (the activation dtype).
+ * silu(a) = a / (1 + exp(-a)) with an IEEE division, torch's GPU formula.
+ */
+int cin_silu_mul_quant_rowwise(const void* h12, int in_dtype, int64_t M, int64_t H, int64_t s12,
+                               int out_dtype, int round_scale, uint8_t* q, int64_t sqm,
+                               float* scales, int64_t ssm, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -168,3 +168,36 @@ def test_grouped_experts_fwd_bwd(kern, dev, counts):
         mr = orc.normwise_max_rel(got.float().cpu(), ref[name])
         fr = orc.frob_rel(got.float().cpu(), ref[name])
         assert mr <= 4e-2 and fr <= 5e-3, f"{name}: {mr:.3e} {fr:.3e}"
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU fused into the row-wise quantizer (experts' forward, src/layers.py:72-74)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("M,H,in_dt,out_dt", [
+    (1000, 1024, torch.bfloat16, torch.bfloat16),
+    (300, 200, torch.bfloat16, torch.bfloat16),    # partial last tile (H % 128 != 0)
+    (257, 512, torch.float32, torch.float32),
+    (64, 384, torch.float32, torch.bfloat16),
+    (33, 256, torch.float16, torch.float16),
+])
+def test_silu_mul_quant_equals_unfused_chain(kern, dev, M, H, in_dt, out_dt):
+    from cinnamon_amd import layers
+
+    g = torch.Generator().manual_seed(40)
+    h12 = (torch.randn(M, 2 * H, generator=g) * 3).to(in_dt)
+    h12[0, :8] = float("nan")
+    h12[1, H:H + 4] = float("inf")
+    h12[2, :] = 0.0
+    d = h12.to(dev)
+    q, s = layers.silu_mul_quantize_fp8(d, out_dtype=out_dt)
+    # the unfused chain on the GPU: torch's silu and product, then the row-wise quantizer
+    h1, h2 = d.float().chunk(2, dim=-1)
+    rq, rs_ = kern.quantize_fp8_rowwise((torch.nn.functional.silu(h1) * h2).to(out_dt))
+    assert torch.equal(q.view(torch.uint8), rq.view(torch.uint8)), \
+        f"{(q.view(torch.uint8) != rq.view(torch.uint8)).sum().item()} codes differ"
+    assert torch.equal(s.nan_to_num(nan=-1.0), rs_.nan_to_num(nan=-1.0))
+    # and against the CPU oracle chain, where torch's CPU silu may differ by an ulp
+    ch1, ch2 = h12.float().chunk(2, dim=-1)
+    oq, os_ = orc.quant_rowwise((torch.nn.functional.silu(ch1) * ch2).to(out_dt))
+    diff = (q.view(torch.uint8).cpu() != oq.view(torch.uint8)).float().mean().item()
+    assert diff < 1e-3, f"{diff:.2e} of the codes differ from the CPU chain"
