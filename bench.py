@@ -37,7 +37,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "moe_gateup", "moe_down",
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
-                                      "moe_wgrad", "moe_dgrad", "copy"], default=None,
+                                      "moe_wgrad", "moe_dgrad", "moe_layer", "copy"], default=None,
                    help="run only one kernel in a loop (for profiler runs)")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the config-3 (MoE) and config-4 (backward) component timings")
@@ -298,6 +298,26 @@ def main():
         layers.fp8_grouped_dgrad(gq3, gs3, mb["w12qt"], mb["w12s"], moe["starts"], moe["ends"],
                                  2 * moe["H"], out=dx3)
 
+    # config 3 experts layer end to end (layers.GroupedExperts, FP8 forward and backward):
+    # weights quantized inside every call, as in training
+    ml = None
+    if full or args.only == "moe_layer":
+        if moe is None:
+            moe = moe_setup(dev)
+        g3 = torch.Generator(device=dev).manual_seed(34)
+        ml = layers.GroupedExperts(moe["E"], moe["D"], moe["H"]).to(dev)
+        ml_x = moe["x"].detach().clone().requires_grad_(True)
+        ml_g = torch.randn(moe["A"], moe["D"], device=dev, generator=g3) * 1e-3
+
+    def moe_layer(i):
+        ml_x.grad = None
+        ml.zero_grad(set_to_none=True)
+        ml(ml_x, moe["starts"], moe["ends"]).backward(ml_g)
+
+    def moe_layer_fwd(i):
+        with torch.no_grad():
+            ml(ml_x, moe["starts"], moe["ends"])
+
     if full or args.only in ("dual_quant", "requant", "dgrad", "wgrad"):
         bwd = bwd_setup(dev, xs[0], ws[0])
         gq, gs, gqt, gst = kernels.quantize_fp8_dual(bwd["dy"])
@@ -329,7 +349,8 @@ def main():
         fn = {"step": step, "gemm": gemm, "quant_x": quant_x, "quant_w": quant_w,
               "moe_gateup": moe_gateup, "moe_down": moe_down, "dual_quant": dual_quant,
               "requant": requant, "dgrad": dgrad, "wgrad": wgrad, "moe_dual": moe_dual,
-              "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad}[args.only]
+              "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad,
+              "moe_layer": moe_layer}[args.only]
         loop = time_loop if args.only == "step" else kernel_loop
         us = loop(fn, args.steps, args.warmup)
         print(json.dumps({"only": args.only, "us_per_call": us}))
@@ -401,6 +422,19 @@ def main():
                         "frac_of_fp8_peak": round(gu_fl / gu_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
             "down": {"us": round(dn_us, 1), "tflops": round(dn_fl / dn_us / 1e6, 1),
                      "frac_of_fp8_peak": round(dn_fl / dn_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
+        }
+    if ml is not None:
+        A, D, H = moe["A"], moe["D"], moe["H"]
+        f_ms = time_loop(moe_layer_fwd, 3, 1) / 1e3
+        fb_ms = time_loop(moe_layer, 3, 1) / 1e3
+        fl = 2.0 * A * D * 2 * H + 2.0 * A * H * D
+        out["components"]["config3_experts_layer"] = {
+            "what": "layers.GroupedExperts (FP8) on the config-3 rows: weight quantization, "
+                    "gate/up GEMM, SwiGLU + quantization, down GEMM; backward adds the grouped "
+                    "dual/re-quantizers, SwiGLU backward, dgrad and wgrad of both GEMMs",
+            "forward_ms": round(f_ms, 2), "forward_backward_ms": round(fb_ms, 2),
+            "tokens_per_s_fwd_bwd": round(moe["A"] / (fb_ms * 1e-3) / 8),
+            "gemm_tflops_fwd_bwd": round(3 * fl / (fb_ms * 1e-3) / 1e12, 1),
         }
     if mb is not None:
         A, D, H = moe["A"], moe["D"], moe["H"]

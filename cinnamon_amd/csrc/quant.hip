@@ -1217,6 +1217,43 @@ __global__ __launch_bounds__(kThreads) void k_silu_mul_rowwise128(
   }
 }
 
+// ---------------------------------------------------------------------------
+// SwiGLU backward in one pass: for h = silu(h1) * h2 with [h1 h2] = h12,
+//   dh12[:, :H] = dh * h2 * (sig * (1 + h1 * (1 - sig))),  dh12[:, H:] = dh * (h1 * sig),
+// sig = 1 / (1 + exp(-h1)), every product and sum rounded to fp32 in that order (the
+// elementwise chain it replaces computes the same way, one rounding per operation).
+// A thread owns 4 consecutive columns of a row.
+// ---------------------------------------------------------------------------
+template <int IT>
+__global__ __launch_bounds__(kThreads) void k_swiglu_backward(
+    const float* __restrict__ dh, int64_t sdm, const void* __restrict__ h12, int64_t s12,
+    int64_t M, int64_t H, float* __restrict__ dh12, int64_t som) {
+  const int64_t nq = H / 4;
+  const int64_t total = M * nq;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * kThreads) {
+    const int64_t r = i / nq, j = (i - r * nq) * 4;
+    const f32x4 g = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(dh + r * sdm + j));
+    const float gv[4] = {g[0], g[1], g[2], g[3]};
+    float a[4], b[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      a[k] = load_elem(h12, IT, r * s12 + j + k);
+      b[k] = load_elem(h12, IT, r * s12 + H + j + k);
+    }
+    float d1[4], d2[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float sig = 1.0f / (1.0f + expf(-a[k]));
+      const float t = sig * (1.0f + a[k] * (1.0f - sig));
+      d1[k] = gv[k] * b[k] * t;
+      d2[k] = gv[k] * (a[k] * sig);
+    }
+    *reinterpret_cast<float4*>(dh12 + r * som + j) = make_float4(d1[0], d1[1], d1[2], d1[3]);
+    *reinterpret_cast<float4*>(dh12 + r * som + H + j) = make_float4(d2[0], d2[1], d2[2], d2[3]);
+  }
+}
+
 // Workgroups for a persistent tile kernel: as many as the device holds at once (from the
 // kernel's occupancy and the device's CU count), at most one per tile.
 template <auto Kernel>
@@ -1533,6 +1570,29 @@ int cin_silu_mul_quant_rowwise(const void* h12, int in_dtype, int64_t M, int64_t
 #undef CIN_SILU_OT
 #undef CIN_SILU
   return cin_check_launch("silu_mul_quant_rowwise");
+}
+
+int cin_swiglu_backward(const float* dh, int64_t sdm, const void* h12, int h12_dtype, int64_t s12,
+                        int64_t M, int64_t H, float* dh12, int64_t som, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(h12_dtype), "swiglu_backward: unsupported h12 dtype %d", h12_dtype);
+  CIN_CHECK_ARG(M >= 0 && H >= 0, "swiglu_backward: negative shape");
+  if (M == 0 || H == 0) return CIN_OK;
+  CIN_CHECK_ARG(dh && h12 && dh12, "swiglu_backward: null pointer");
+  CIN_CHECK_ARG(H % 4 == 0 && aligned(dh, 16) && sdm % 4 == 0 && sdm >= H && aligned(dh12, 16) &&
+                    som % 4 == 0 && som >= 2 * H && s12 >= 2 * H,
+                "swiglu_backward: H must be a multiple of 4 with 16-byte aligned fp32 rows");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = grid_for(M * (H / 4), kThreads, 65536);
+  if (h12_dtype == CIN_DT_BF16)
+    hipLaunchKernelGGL(k_swiglu_backward<CIN_DT_BF16>, grid, kThreads, 0, s, dh, sdm, h12, s12, M, H,
+                       dh12, som);
+  else if (h12_dtype == CIN_DT_F16)
+    hipLaunchKernelGGL(k_swiglu_backward<CIN_DT_F16>, grid, kThreads, 0, s, dh, sdm, h12, s12, M, H,
+                       dh12, som);
+  else
+    hipLaunchKernelGGL(k_swiglu_backward<CIN_DT_F32>, grid, kThreads, 0, s, dh, sdm, h12, s12, M, H,
+                       dh12, som);
+  return cin_check_launch("swiglu_backward");
 }
 
 int cin_transpose_u8(const uint8_t* src, int64_t R, int64_t C, int64_t lds, uint8_t* dst,

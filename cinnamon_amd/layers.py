@@ -187,6 +187,21 @@ def silu_mul_quantize_fp8(h12: torch.Tensor, out_dtype: torch.dtype | None = Non
     return q, s
 
 
+def swiglu_backward(dh: torch.Tensor, h12: torch.Tensor) -> torch.Tensor:
+    """Gradient of h = silu(h1) * h2 ([h1 h2] = h12.float().chunk(2, -1)) with respect to
+    h12, from dh [M, H] fp32, in one pass: [dh * h2 * silu'(h1), dh * silu(h1)] fp32 [M, 2H]."""
+    _require(dh.is_cuda and h12.is_cuda, "Input must be on CUDA")
+    M, H = dh.shape
+    _require(h12.shape == (M, 2 * H), "h12 must be [M, 2H]")
+    g = dh if (dh.dtype == torch.float32 and dh.stride(1) == 1 and dh.stride(0) % 4 == 0
+               and dh.data_ptr() % 16 == 0) else dh.float().contiguous()
+    x = h12 if h12.stride(1) == 1 else h12.contiguous()
+    out = torch.empty((M, 2 * H), dtype=torch.float32, device=dh.device)
+    call("cin_swiglu_backward", ptr(g), g.stride(0), ptr(x), dtype_code(x), x.stride(0), M, H,
+         ptr(out), out.stride(0), stream_of(g))
+    return out
+
+
 class FP8GroupedExpertsFunction(torch.autograd.Function):
     """SwiGLU experts in FP8: out = W3_e (silu(h1) * h2), [h1 h2] = W12_e x for each expert's
     rows (reference GroupedExperts.forward, src/layers.py:56-87: GEMM(w12), silu * mul in
@@ -232,10 +247,7 @@ class FP8GroupedExpertsFunction(torch.autograd.Function):
         hbt, hblk = requantize_grouped_t(hq, hs, starts, ends)
         dw3 = fp8_grouped_wgrad(gqt, gst, hbt, hblk, starts, ends, g.shape[0])
         # silu(h1) * h2 in fp32 (the forward's cast to the input dtype passes the gradient)
-        h1, h2 = h12.float().chunk(2, dim=-1)
-        sig = torch.sigmoid(h1)
-        silu = h1 * sig
-        dh12 = torch.cat([dh * h2 * (sig * (1.0 + h1 * (1.0 - sig))), dh * silu], dim=-1)
+        dh12 = swiglu_backward(dh, h12)
         dq, ds, dqt, dst = quantize_fp8_dual_grouped(dh12, starts, ends)
         dx = fp8_grouped_dgrad(dq, ds, w12qt, w12s, starts, ends, 2 * H,
                                out=torch.zeros((g.shape[0], D), dtype=torch.float32, device=g.device))

@@ -239,6 +239,19 @@ int cin_silu_mul_quant_rowwise(const void* h12, int in_dtype, int64_t M, int64_t
                                int out_dtype, int round_scale, uint8_t* q, int64_t sqm,
                                float* scales, int64_t ssm, void* stream);
 
+/*
+ * SwiGLU backward in one pass, replacing the elementwise chain of the experts' backward
+ * (the derivative of src/layers.py:72-73, h = silu(h1) * h2 with [h1 h2] = h12):
+ *   dh12[:, :H] = dh * h2 * (sig * (1 + h1 * (1 - sig))),  dh12[:, H:] = dh * (h1 * sig)
+ * with sig = 1 / (1 + exp(-h1)), in fp32 with one rounding per operation in that order.
+ *   dh   [M, H] fp32 (row stride sdm), h12 [M, 2H] of h12_dtype (row stride s12)
+ *   dh12 [M, 2H] fp32 (row stride som).  H % 4 == 0; fp32 rows 16-byte aligned.
+ * No counterpart in the reference (its grouped GEMM has no backward); the FP8 experts'
+ * backward (layers.FP8GroupedExpertsFunction) calls it.
+ */
+int cin_swiglu_backward(const float* dh, int64_t sdm, const void* h12, int h12_dtype, int64_t s12,
+                        int64_t M, int64_t H, float* dh12, int64_t som, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

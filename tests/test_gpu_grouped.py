@@ -201,3 +201,18 @@ def test_silu_mul_quant_equals_unfused_chain(kern, dev, M, H, in_dt, out_dt):
     oq, os_ = orc.quant_rowwise((torch.nn.functional.silu(ch1) * ch2).to(out_dt))
     diff = (q.view(torch.uint8).cpu() != oq.view(torch.uint8)).float().mean().item()
     assert diff < 1e-3, f"{diff:.2e} of the codes differ from the CPU chain"
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_swiglu_backward_equals_elementwise_chain(kern, dev, dt):
+    from cinnamon_amd import layers
+
+    g = torch.Generator().manual_seed(41)
+    M, H = 517, 384
+    h12 = (torch.randn(M, 2 * H, generator=g) * 4).to(dt).to(dev)
+    dh = (torch.randn(M, H, generator=g) * 1e-3).to(dev)
+    got = layers.swiglu_backward(dh, h12)
+    h1, h2 = h12.float().chunk(2, dim=-1)
+    sig = torch.sigmoid(h1)
+    want = torch.cat([dh * h2 * (sig * (1.0 + h1 * (1.0 - sig))), dh * (h1 * sig)], dim=-1)
+    assert torch.equal(got, want), f"max abs diff {(got - want).abs().max().item()}"
