@@ -47,6 +47,7 @@ SIGNATURES: dict[str, list] = {
                                    _i64, _i64, _i64, _p, _i32, _i64, _i64, _p],
     "cin_silu_mul_quant_rowwise": [_p, _i32, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p, _i64, _p],
     "cin_swiglu_backward": [_p, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p],
+    "cin_zero_rows_outside_ranges": [_p, _i64, _i64, _i64, _p, _p, _i64, _p],
 }
 
 _lock = threading.Lock()

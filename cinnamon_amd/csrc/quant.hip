@@ -1254,6 +1254,30 @@ __global__ __launch_bounds__(kThreads) void k_swiglu_backward(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Zero the rows of a [T, ncols] matrix that lie outside every expert range: the grouped
+// kernels never write them, and with ranges that cover all rows (a router's counts)
+// this reads the ranges and writes nothing.  A thread owns a row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void k_zero_uncovered(uint8_t* __restrict__ C, int64_t ldc_bytes,
+                                                             int64_t row_bytes, int64_t T,
+                                                             const int64_t* __restrict__ starts,
+                                                             const int64_t* __restrict__ ends,
+                                                             int64_t E) {
+  typedef __attribute__((address_space(4))) const int64_t cint64;
+  const int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (r >= T) return;
+  bool covered = false;
+  for (int64_t e = 0; e < E && !covered; ++e)
+    covered = r >= ((const cint64*)starts)[e] && r < ((const cint64*)ends)[e];
+  if (covered) return;
+  uint8_t* p = C + r * ldc_bytes;
+  int64_t i = 0;
+  if ((((uintptr_t)p) & 15) == 0)
+    for (; i + 16 <= row_bytes; i += 16) *reinterpret_cast<uint4*>(p + i) = make_uint4(0, 0, 0, 0);
+  for (; i < row_bytes; ++i) p[i] = 0;
+}
+
 // Workgroups for a persistent tile kernel: as many as the device holds at once (from the
 // kernel's occupancy and the device's CU count), at most one per tile.
 template <auto Kernel>
@@ -1593,6 +1617,20 @@ int cin_swiglu_backward(const float* dh, int64_t sdm, const void* h12, int h12_d
     hipLaunchKernelGGL(k_swiglu_backward<CIN_DT_F32>, grid, kThreads, 0, s, dh, sdm, h12, s12, M, H,
                        dh12, som);
   return cin_check_launch("swiglu_backward");
+}
+
+int cin_zero_rows_outside_ranges(void* C, int64_t ldc_bytes, int64_t row_bytes, int64_t T,
+                                 const int64_t* starts, const int64_t* ends, int64_t E,
+                                 void* stream) {
+  CIN_CHECK_ARG(T >= 0 && E >= 0 && row_bytes >= 0 && ldc_bytes >= row_bytes,
+                "zero_rows_outside_ranges: bad shape");
+  if (T == 0 || row_bytes == 0) return CIN_OK;
+  CIN_CHECK_ARG(C && (E == 0 || (starts && ends)), "zero_rows_outside_ranges: null pointer");
+  CIN_CHECK_ARG(cdiv(T, kThreads) < ((int64_t)1 << 31), "zero_rows_outside_ranges: too many rows");
+  hipLaunchKernelGGL(k_zero_uncovered, (unsigned)cdiv(T, kThreads), kThreads, 0,
+                     static_cast<hipStream_t>(stream), static_cast<uint8_t*>(C), ldc_bytes,
+                     row_bytes, T, starts, ends, E);
+  return cin_check_launch("zero_rows_outside_ranges");
 }
 
 int cin_transpose_u8(const uint8_t* src, int64_t R, int64_t C, int64_t lds, uint8_t* dst,

@@ -168,6 +168,15 @@ def fp8_grouped_dgrad(g_fp8: torch.Tensor, g_scale: torch.Tensor, w_codes_t: tor
     return out
 
 
+def _empty_rows_zeroed(T: int, ncols: int, dtype: torch.dtype, device, starts, ends) -> torch.Tensor:
+    """torch.empty((T, ncols)) whose rows outside every expert range are zero (the grouped
+    kernels write exactly the rows inside the ranges)."""
+    out = torch.empty((T, ncols), dtype=dtype, device=device)
+    call("cin_zero_rows_outside_ranges", ptr(out), out.stride(0) * out.element_size(),
+         ncols * out.element_size(), T, ptr(starts), ptr(ends), starts.numel(), stream_of(out))
+    return out
+
+
 def silu_mul_quantize_fp8(h12: torch.Tensor, out_dtype: torch.dtype | None = None,
                           round_scale: bool = False):
     """quantize_fp8_rowwise((silu(h1) * h2).to(out_dtype)) with [h1 h2] = h12.float().chunk(2, -1),
@@ -219,17 +228,18 @@ class FP8GroupedExpertsFunction(torch.autograd.Function):
         xq, xs = quantize_fp8_rowwise(sorted_x)
         w12f = w12 if w12.dtype == torch.float32 else w12.float()
         w12q, w12qt, w12s = quantize_fp8_blockwise_t(w12f.reshape(E * H2, D))
+        T = sorted_x.shape[0]
         h12 = fp8_grouped_gemm(xq, xs, w12q.view(E, H2, D), w12s.view(E, H2 // 128, -1),
                                starts, ends, out_dtype=torch.bfloat16,
-                               out=torch.zeros((sorted_x.shape[0], H2), dtype=torch.bfloat16,
-                                               device=sorted_x.device))
+                               out=_empty_rows_zeroed(T, H2, torch.bfloat16, sorted_x.device,
+                                                      starts, ends))
         hq, hs = silu_mul_quantize_fp8(h12, out_dtype=sorted_x.dtype)
         w3f = w3 if w3.dtype == torch.float32 else w3.float()
         w3q, w3qt, w3s = quantize_fp8_blockwise_t(w3f.reshape(E * D, H))
         out = fp8_grouped_gemm(hq, hs, w3q.view(E, D, H), w3s.view(E, D // 128, -1), starts, ends,
                                out_dtype=torch.float32,
-                               out=torch.zeros((sorted_x.shape[0], D), dtype=torch.float32,
-                                               device=sorted_x.device))
+                               out=_empty_rows_zeroed(T, D, torch.float32, sorted_x.device,
+                                                      starts, ends))
         ctx.save_for_backward(xq, xs, w12qt, w12s, h12, hq, hs, w3qt, w3s, starts, ends)
         ctx.dims = (E, H, D)
         ctx.x_dtype = sorted_x.dtype
@@ -242,15 +252,18 @@ class FP8GroupedExpertsFunction(torch.autograd.Function):
         E, H, D = ctx.dims
         g = grad_out.contiguous()
         gq, gs, gqt, gst = quantize_fp8_dual_grouped(g, starts, ends)
+        T = g.shape[0]
         dh = fp8_grouped_dgrad(gq, gs, w3qt, w3s, starts, ends, D,
-                               out=torch.zeros((g.shape[0], H), dtype=torch.float32, device=g.device))
+                               out=_empty_rows_zeroed(T, H, torch.float32, g.device, starts, ends))
         hbt, hblk = requantize_grouped_t(hq, hs, starts, ends)
         dw3 = fp8_grouped_wgrad(gqt, gst, hbt, hblk, starts, ends, g.shape[0])
         # silu(h1) * h2 in fp32 (the forward's cast to the input dtype passes the gradient)
         dh12 = swiglu_backward(dh, h12)
         dq, ds, dqt, dst = quantize_fp8_dual_grouped(dh12, starts, ends)
+        # dx straight in the input dtype: the GEMM's bf16 store is the RNE of its fp32 value
+        dx_dtype = ctx.x_dtype if ctx.x_dtype in (torch.bfloat16, torch.float32) else torch.float32
         dx = fp8_grouped_dgrad(dq, ds, w12qt, w12s, starts, ends, 2 * H,
-                               out=torch.zeros((g.shape[0], D), dtype=torch.float32, device=g.device))
+                               out=_empty_rows_zeroed(T, D, dx_dtype, g.device, starts, ends))
         xbt, xblk = requantize_grouped_t(xq, xs, starts, ends)
         dw12 = fp8_grouped_wgrad(dqt, dst, xbt, xblk, starts, ends, g.shape[0])
         return (dx.to(ctx.x_dtype), dw12.to(ctx.w_dtypes[0]), dw3.to(ctx.w_dtypes[1]), None, None)

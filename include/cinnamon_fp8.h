@@ -252,6 +252,17 @@ int cin_silu_mul_quant_rowwise(const void* h12, int in_dtype, int64_t M, int64_t
 int cin_swiglu_backward(const float* dh, int64_t sdm, const void* h12, int h12_dtype, int64_t s12,
                         int64_t M, int64_t H, float* dh12, int64_t som, void* stream);
 
+/*
+ * Zero the rows r of a [T, *] matrix (rows ldc_bytes apart, row_bytes written) with r outside
+ * every range [starts[e], ends[e]).  The grouped GEMMs leave such rows untouched (as the
+ * reference's moe_grouped_gemm leaves them unset, src/kernels.py:550); callers that need
+ * them zero call this instead of zero-filling the whole output.  No counterpart in the
+ * reference.
+ */
+int cin_zero_rows_outside_ranges(void* C, int64_t ldc_bytes, int64_t row_bytes, int64_t T,
+                                 const int64_t* starts, const int64_t* ends, int64_t E,
+                                 void* stream);
+
 #ifdef __cplusplus
 }
 #endif

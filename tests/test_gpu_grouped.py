@@ -216,3 +216,16 @@ def test_swiglu_backward_equals_elementwise_chain(kern, dev, dt):
     sig = torch.sigmoid(h1)
     want = torch.cat([dh * h2 * (sig * (1.0 + h1 * (1.0 - sig))), dh * (h1 * sig)], dim=-1)
     assert torch.equal(got, want), f"max abs diff {(got - want).abs().max().item()}"
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_zero_rows_outside_ranges(kern, dev, dt):
+    from cinnamon_amd import layers
+
+    starts = torch.tensor([0, 50, 70, 70], dtype=torch.int64, device=dev)
+    ends = torch.tensor([10, 60, 70, 65], dtype=torch.int64, device=dev)  # an empty, an inverted range
+    out = layers._empty_rows_zeroed(100, 33, dt, dev, starts, ends)
+    covered = torch.zeros(100, dtype=torch.bool)
+    covered[0:10] = True
+    covered[50:60] = True
+    assert torch.equal(out[~covered.to(dev)].float().cpu(), torch.zeros(int((~covered).sum()), 33))
