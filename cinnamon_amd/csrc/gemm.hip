@@ -258,8 +258,8 @@ namespace big {
 //
 // Operands move global -> LDS by DMA (buffer_load ... lds), one K block ahead: right
 // after the barrier of block kb frees a stage, the DMA of block kb+2 into it starts (its
-// four row groups are issued 8 steps apart), and it has a whole block to land.  No VGPR
-// staging and no ds_write.  The barrier sits
+// four row groups are issued at steps 28, 30, 2 and 6), and it has most of a block to
+// land.  No VGPR staging and no ds_write.  The barrier sits
 // before the last m-tile group, so the next block's fragments are read while that
 // group's MFMAs run.  The DMA is issued from inline assembly: the compiler treats its
 // own LDS-DMA builtin as aliasing every LDS read and would wait for it before each one.
@@ -271,6 +271,13 @@ struct __attribute__((aligned(16))) Smem {
   uint8_t a[2][kTileBytes];
   uint8_t b[2][kTileBytes];
   float sa[2][TM];  // A-row scales, slot q holds row sa_row(q)
+};
+// After the K loop the same LDS stages a bf16 C tile: 256 rows of 512 bytes, each padded
+// by 32 bytes so that the 16 rows of one fragment store fall on distinct bank groups.
+constexpr int kCStride = TN * 2 + 32;
+union SmemAll {
+  Smem s;
+  uint8_t c[TM * kCStride];
 };
 
 // Slot q = 128 wm + 8 l + i holds row 128 wm + 16 i + l: the lane (wm, l) finds the
@@ -309,7 +316,8 @@ struct Tile {
 __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ssam, int64_t ssak,
                                           int64_t ldb, int64_t ssbn, int64_t ssbk, int64_t K,
                                           int c_dtype, int64_t ldc) {
-  __shared__ Smem sm;
+  __shared__ SmemAll smu;
+  Smem& sm = smu.s;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -426,11 +434,11 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
       asm volatile("" : "+v"(bf[j]));
       p[s8 & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af[i & 1], zero, 0, 0, 0, 0, 0, 0);
       asm volatile("" : "+v"(bf[j]));
-      // row groups 1-3 of block kb+1 (group 0 went out after the previous barrier), one
-      // every 8 steps: a burst of 8 DMA issues per wave stalls the MFMA issue more than
-      // the same issues spread over the block
-      if ((s8 == 4 || s8 == 12 || s8 == 20) && kb >= 1 && kb + 1 < nk)
-        CIN_DMA_GROUP(kb + 1, st ^ 1, (s8 + 4) >> 3);
+      // row groups 2 and 3 of block kb+1 (groups 0 and 1 went out after the previous
+      // barrier), 4 steps apart: a burst of DMA issues stalls the MFMA issue, and
+      // issuing them early leaves them 22 steps to land before the next barrier
+      if ((s8 == 2 || s8 == 6) && kb >= 1 && kb + 1 < nk)
+        CIN_DMA_GROUP(kb + 1, st ^ 1, s8 == 2 ? 2 : 3);
       // fragment of m-tile i+1 (its slot's previous user, m-tile i-1, is done)
       if (j == 0 && i < 7) af[(i + 1) & 1] = CIN_AFRAG(st, i + 1);
       // scale of m-tile i+1 (its slot's previous user, the FMAs of m-tile i-1, are done)
@@ -439,14 +447,16 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
         if (s8 == 28) {
           // block kb+1's DMA (issued since the previous barrier) has landed in stage st^1,
           // and stage st is no longer read (its last fragment, m-tile 7, was read at step
-          // 24): after the barrier, block kb+2 starts into stage st (row group 0 now, the
-          // rest during the next block) and the next block's fragments are read
+          // 24): after the barrier, block kb+2 starts into stage st (row group 0 now,
+          // group 1 at step 30, groups 2 and 3 early in the next block) and the next
+          // block's fragments are read
           wait_dma();
           __syncthreads();
           if (kb + 2 < nk) CIN_DMA_GROUP(kb + 2, st, 0);
           af[0] = CIN_AFRAG(st ^ 1, 0);
           CIN_SA8(st ^ 1);
         }
+        if (s8 == 30 && kb + 2 < nk) CIN_DMA_GROUP(kb + 2, st, 1);
         if (s8 >= 28) bf[j] = CIN_BFRAG(st ^ 1, j);
         if (s8 == 31) cs[0] = sa8[0] * sbn;
       }
@@ -466,6 +476,35 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
 #undef CIN_BFRAG
 #undef CIN_SA8
 
+  // bf16 epilogue through LDS: the fragments go to a row-major tile, then every wave
+  // stores 32 whole rows, 512 contiguous bytes per row (the direct stores below write
+  // each row in 32-byte pieces).  All tiles finish together, so the 32 MB or so of C
+  // leave in one burst bounded by HBM write bandwidth; full rows keep it near that bound.
+  if (c_dtype != CIN_DT_F32 && ((((uintptr_t)T.C) & 15) == 0) && (ldc & 7) == 0) {
+    __syncthreads();  // every wave is past its last fragment read
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int m = wm * 128 + i * 16 + l16;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = wn * 64 + j * 16 + kq * 4;
+        const uint32_t b0 = f32_to_bf16_bits(acc[i][j][0]), b1 = f32_to_bf16_bits(acc[i][j][1]);
+        const uint32_t b2 = f32_to_bf16_bits(acc[i][j][2]), b3 = f32_to_bf16_bits(acc[i][j][3]);
+        *reinterpret_cast<uint2*>(&smu.c[m * kCStride + n * 2]) =
+            make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+      }
+    }
+    __syncthreads();
+    const int half = lane >> 5, c16 = lane & 31;  // lane: row half, 16-byte column chunk
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = wave * 32 + r * 2 + half;
+      const uint4 v = *reinterpret_cast<const uint4*>(&smu.c[m * kCStride + c16 * 16]);
+      if (m >= T.row_lo && m < T.row_hi && c16 * 8 >= T.col_lo)
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.C) + (int64_t)m * ldc + c16 * 8) = v;
+    }
+    return;
+  }
   // epilogue: lane holds C[m][n .. n+3] (n a multiple of 4, so a shifted tile's
   // column skip, a multiple of 128, never splits a lane's 4 columns)
 #pragma unroll
