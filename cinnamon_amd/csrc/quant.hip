@@ -405,6 +405,26 @@ struct DenseTiles {
   }
 };
 
+// Dense tiles in column-block-major order: t -> (row block t % nrb, column block
+// cb0 + t / nrb).  The re-quantizer walks its tiles this way: the workgroups in flight
+// then write whole rows of the transposed output together, which measured 8% faster on
+// the config-4 shape than the row-block-major walk (the dual quantizer, with a
+// row-wise output as well, measured slower in this order and keeps the other).
+struct DenseTilesCM {
+  int64_t M;
+  uint32_t nrb, cb0;
+  __device__ void operator()(uint32_t t, TileGeo& g) const {
+    const uint32_t cbl = t / nrb;
+    const uint32_t rb = t - cbl * nrb;
+    g.cb = cb0 + cbl;
+    g.r0 = (int64_t)rb * 128;
+    const int64_t left = M - g.r0;
+    g.nr = (int)(left < 128 ? left : 128);
+    g.t0 = g.r0;
+    g.tw = g.nr;
+  }
+};
+
 // Grouped tiles (MoE backward): t -> (128-token chunk t / nbc of the expert-sorted rows,
 // column block cb0 + t % nbc); the chunk's transposed outputs sit at its padded position
 // (cin_grouped.h).  A workgroup visits increasing t, so the expert cursor only moves
@@ -1089,7 +1109,8 @@ __global__ __launch_bounds__(kThreads) void k_requant128(const uint8_t* __restri
                                                          float* sblk, int64_t ssbm, uint32_t nbc,
                                                          uint32_t cb0, uint32_t ntiles) {
   __shared__ RequantSmem sm;
-  DenseTiles geo{M, nbc, cb0};
+  (void)nbc;
+  DenseTilesCM geo{M, (uint32_t)((M + 127) >> 7), cb0};
   requant_run<EDGE>(geo, ntiles, q, K, sqm, srow, ssm, qb, sqbm, qbt, sqbtm, vec_t != 0, sblk, ssbm,
                     sm);
 }
