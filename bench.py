@@ -82,7 +82,9 @@ def kernel_loop(fn, iters, warmup):
         src = torch.ones(128 * 1024 * 1024, dtype=torch.bfloat16, device="cuda")
         _BUSY.extend([src, torch.empty_like(src)])
     src, dst = _BUSY
-    for _ in range(2 + int(host_s * iters / 80e-6)):  # a 256 MiB copy takes ~90 us
+    # a 256 MiB copy takes ~90 us; twice the measured host time, since a profiler's
+    # per-launch cost varies from call to call
+    for _ in range(2 + int(2 * host_s * iters / 80e-6)):
         dst.copy_(src)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
