@@ -17,6 +17,11 @@ Replaced reference items (src/kernels.py):
   convert_to_fp8            :843-905
   moe_grouped_gemm          :526-581  -> cin_grouped_gemm_f16 (unquantized, fp16 MFMA)
 
+Every launch is registered as a torch operator (namespace ``cinnamon_amd``) with a
+shape function, so torch.compile traces through these functions (the reference
+compiles its training model, src/train.py:703) instead of breaking the graph at a
+native call; the public functions keep the reference's argument checks in front.
+
 Two reference names outside the FP8 path are kept so that imports resolve
 (src/attention.py:6, tests/test_kernels.py:14): lightning_indexer_fused (:392-432) and
 sparse_attention (:1292-1320).  They are plain torch on the GPU, not part of this build's
@@ -48,6 +53,15 @@ __all__ = [
     "lightning_indexer_fused",
     "sparse_attention",
 ]
+
+
+def custom_op(name: str, schema: str):
+    """Register the decorated launch as the torch operator cinnamon_amd::<name> with an
+    explicit schema; the caller attaches its shape function with ``register_fake``.  The
+    operators allocate their outputs and never mutate their inputs."""
+    def deco(fn):
+        return torch.library.custom_op(f"cinnamon_amd::{name}", fn, mutates_args=(), schema=schema)
+    return deco
 
 
 def _require(cond: bool, msg: str) -> None:
@@ -87,14 +101,25 @@ def quantize_fp8_rowwise(x: torch.Tensor, block_size: int = 128,
     """1 x block_size e4m3 quantization -> (codes [M, N] float8_e4m3fn, scales [M, ceil(N/bs)] fp32)."""
     _require(x.is_cuda, "Input must be on CUDA")
     _require(x.ndim == 2, "Input must be 2D for now")
+    return _quant_rowwise_op(x, int(block_size), bool(round_scale))
+
+
+@custom_op("quant_rowwise", "(Tensor x, int block_size, bool round_scale) -> (Tensor, Tensor)")
+def _quant_rowwise_op(x, block_size, round_scale):
     M, N = x.shape
-    nb = _cdiv(N, block_size)
     x_fp8 = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=x.device)
-    scales = torch.empty((M, nb), dtype=torch.float32, device=x.device)
+    scales = torch.empty((M, _cdiv(N, block_size)), dtype=torch.float32, device=x.device)
     call("cin_quant_rowwise", ptr(x), dtype_code(x), M, N, x.stride(0), x.stride(1), block_size,
-         int(bool(round_scale)), ptr(x_fp8), x_fp8.stride(0), ptr(scales), scales.stride(0),
+         int(round_scale), ptr(x_fp8), x_fp8.stride(0), ptr(scales), scales.stride(0),
          stream_of(x))
     return x_fp8, scales
+
+
+@_quant_rowwise_op.register_fake
+def _(x, block_size, round_scale):
+    M, N = x.shape
+    return (x.new_empty((M, N), dtype=torch.float8_e4m3fn),
+            x.new_empty((M, _cdiv(N, block_size)), dtype=torch.float32))
 
 
 def quantize_fp8_blockwise(x: torch.Tensor, block_m: int = 128, block_n: int = 128,
@@ -102,13 +127,26 @@ def quantize_fp8_blockwise(x: torch.Tensor, block_m: int = 128, block_n: int = 1
     """block_m x block_n e4m3 quantization -> (codes [M, N], scales [ceil(M/bm), ceil(N/bn)] fp32)."""
     _require(x.is_cuda, "Input must be on CUDA")
     _require(x.ndim == 2, "Input must be 2D")
+    return _quant_blockwise_op(x, int(block_m), int(block_n), bool(round_scale))
+
+
+@custom_op("quant_blockwise",
+           "(Tensor x, int block_m, int block_n, bool round_scale) -> (Tensor, Tensor)")
+def _quant_blockwise_op(x, block_m, block_n, round_scale):
     M, N = x.shape
     x_fp8 = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=x.device)
     scales = torch.empty((_cdiv(M, block_m), _cdiv(N, block_n)), dtype=torch.float32, device=x.device)
     call("cin_quant_blockwise", ptr(x), dtype_code(x), M, N, x.stride(0), x.stride(1), block_m,
-         block_n, int(bool(round_scale)), ptr(x_fp8), x_fp8.stride(0), ptr(None), 0, ptr(scales),
+         block_n, int(round_scale), ptr(x_fp8), x_fp8.stride(0), ptr(None), 0, ptr(scales),
          scales.stride(0), stream_of(x))
     return x_fp8, scales
+
+
+@_quant_blockwise_op.register_fake
+def _(x, block_m, block_n, round_scale):
+    M, N = x.shape
+    return (x.new_empty((M, N), dtype=torch.float8_e4m3fn),
+            x.new_empty((_cdiv(M, block_m), _cdiv(N, block_n)), dtype=torch.float32))
 
 
 def quantize_fp8_blockwise_t(x: torch.Tensor, round_scale: bool = False,
@@ -120,14 +158,30 @@ def quantize_fp8_blockwise_t(x: torch.Tensor, round_scale: bool = False,
     """
     _require(x.is_cuda, "Input must be on CUDA")
     _require(x.ndim == 2, "Input must be 2D")
+    q, qt, scales = _quant_blockwise_t_op(x, bool(round_scale), bool(with_rowmajor))
+    return (q if with_rowmajor else None), qt, scales
+
+
+@custom_op("quant_blockwise_t",
+           "(Tensor x, bool round_scale, bool with_rowmajor) -> (Tensor, Tensor, Tensor)")
+def _quant_blockwise_t_op(x, round_scale, with_rowmajor):
+    # without the row-major codes the first output is an empty [0, N] placeholder
     M, N = x.shape
-    q = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=x.device) if with_rowmajor else None
+    q = torch.empty((M if with_rowmajor else 0, N), dtype=torch.float8_e4m3fn, device=x.device)
     qt = torch.empty((N, M), dtype=torch.float8_e4m3fn, device=x.device)
     scales = torch.empty((_cdiv(M, 128), _cdiv(N, 128)), dtype=torch.float32, device=x.device)
     call("cin_quant_blockwise", ptr(x), dtype_code(x), M, N, x.stride(0), x.stride(1), 128, 128,
-         int(bool(round_scale)), ptr(q), N, ptr(qt), qt.stride(0), ptr(scales), scales.stride(0),
-         stream_of(x))
+         int(round_scale), ptr(q) if with_rowmajor else ptr(None), N, ptr(qt), qt.stride(0),
+         ptr(scales), scales.stride(0), stream_of(x))
     return q, qt, scales
+
+
+@_quant_blockwise_t_op.register_fake
+def _(x, round_scale, with_rowmajor):
+    M, N = x.shape
+    return (x.new_empty((M if with_rowmajor else 0, N), dtype=torch.float8_e4m3fn),
+            x.new_empty((N, M), dtype=torch.float8_e4m3fn),
+            x.new_empty((_cdiv(M, 128), _cdiv(N, 128)), dtype=torch.float32))
 
 
 def quantize_fp8_dual(dy: torch.Tensor, round_scale: bool = False):
@@ -138,15 +192,29 @@ def quantize_fp8_dual(dy: torch.Tensor, round_scale: bool = False):
     """
     _require(dy.is_cuda, "Input must be on CUDA")
     _require(dy.ndim == 2, "Input must be 2D")
+    return _quant_dual_op(dy, bool(round_scale))
+
+
+@custom_op("quant_dual", "(Tensor dy, bool round_scale) -> (Tensor, Tensor, Tensor, Tensor)")
+def _quant_dual_op(dy, round_scale):
     M, N = dy.shape
     q = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=dy.device)
     s = torch.empty((M, _cdiv(N, 128)), dtype=torch.float32, device=dy.device)
     qt = torch.empty((N, M), dtype=torch.float8_e4m3fn, device=dy.device)
     st = torch.empty((N, _cdiv(M, 128)), dtype=torch.float32, device=dy.device)
     call("cin_quant_dual", ptr(dy), dtype_code(dy), M, N, dy.stride(0), dy.stride(1),
-         int(bool(round_scale)), ptr(q), q.stride(0), ptr(s), s.stride(0), ptr(qt), qt.stride(0),
+         int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), ptr(qt), qt.stride(0),
          ptr(st), st.stride(0), stream_of(dy))
     return q, s, qt, st
+
+
+@_quant_dual_op.register_fake
+def _(dy, round_scale):
+    M, N = dy.shape
+    return (dy.new_empty((M, N), dtype=torch.float8_e4m3fn),
+            dy.new_empty((M, _cdiv(N, 128)), dtype=torch.float32),
+            dy.new_empty((N, M), dtype=torch.float8_e4m3fn),
+            dy.new_empty((N, _cdiv(M, 128)), dtype=torch.float32))
 
 
 def requantize_rowwise_to_blockwise(x_fp8: torch.Tensor, x_scale: torch.Tensor,
@@ -159,8 +227,16 @@ def requantize_rowwise_to_blockwise(x_fp8: torch.Tensor, x_scale: torch.Tensor,
     """
     _require(x_fp8.is_cuda, "Input must be on CUDA")
     M, K = x_fp8.shape
-    q = _rows8(_codes_u8(x_fp8))
+    _require(x_fp8.dtype in (torch.float8_e4m3fn, torch.uint8),
+             f"expected float8_e4m3fn codes, got {x_fp8.dtype}")
     _require(x_scale.shape == (M, _cdiv(K, 128)), "row scales must be [M, ceil(K/128)]")
+    return _requant_op(x_fp8, x_scale, bool(transposed))
+
+
+@custom_op("requant_row_to_block", "(Tensor x_fp8, Tensor x_scale, bool transposed) -> (Tensor, Tensor)")
+def _requant_op(x_fp8, x_scale, transposed):
+    M, K = x_fp8.shape
+    q = _rows8(_codes_u8(x_fp8))
     xs = x_scale if x_scale.stride(1) == 1 else x_scale.contiguous()
     sblk = torch.empty((_cdiv(M, 128), _cdiv(K, 128)), dtype=torch.float32, device=x_fp8.device)
     if transposed:
@@ -174,6 +250,13 @@ def requantize_rowwise_to_blockwise(x_fp8: torch.Tensor, x_scale: torch.Tensor,
     return out, sblk
 
 
+@_requant_op.register_fake
+def _(x_fp8, x_scale, transposed):
+    M, K = x_fp8.shape
+    return (x_fp8.new_empty((K, M) if transposed else (M, K), dtype=torch.float8_e4m3fn),
+            x_fp8.new_empty((_cdiv(M, 128), _cdiv(K, 128)), dtype=torch.float32))
+
+
 # ---------------------------------------------------------------------------
 # Dequantization (reference src/kernels.py:262-314)
 # ---------------------------------------------------------------------------
@@ -181,6 +264,12 @@ def dequantize_fp8_rowwise(x_fp8: torch.Tensor, scales: torch.Tensor,
                            block_size: int = 128) -> torch.Tensor:
     """fp32(code) * scale[row, col // block_size] -> fp32 [M, N]."""
     _require(x_fp8.is_cuda, "Input must be on CUDA")
+    _codes_u8(x_fp8)
+    return _dequant_rowwise_op(x_fp8, scales, int(block_size))
+
+
+@custom_op("dequant_rowwise", "(Tensor x_fp8, Tensor scales, int block_size) -> Tensor")
+def _dequant_rowwise_op(x_fp8, scales, block_size):
     M, N = x_fp8.shape
     q = _codes_u8(x_fp8)
     out = torch.empty((M, N), dtype=torch.float32, device=x_fp8.device)
@@ -189,10 +278,24 @@ def dequantize_fp8_rowwise(x_fp8: torch.Tensor, scales: torch.Tensor,
     return out
 
 
+@_dequant_rowwise_op.register_fake
+def _(x_fp8, scales, block_size):
+    return x_fp8.new_empty(x_fp8.shape, dtype=torch.float32)
+
+
 def dequantize_fp8(x_fp8: torch.Tensor, scales: torch.Tensor, block_m: int = 128,
                    block_n: int = 128) -> torch.Tensor:
     """bf16(fp32(code) * scale[block]) -> bf16 [M, N]; block_m = 1 reads row-wise scales."""
     _require(x_fp8.is_cuda, "Input must be on CUDA")
+    M, N = x_fp8.shape
+    _codes_u8(x_fp8)
+    _require(scales.numel() >= _cdiv(M, block_m) * _cdiv(N, block_n),
+             "scales too small for the block grid")
+    return _dequant_op(x_fp8, scales, int(block_m), int(block_n))
+
+
+@custom_op("dequant", "(Tensor x_fp8, Tensor scales, int block_m, int block_n) -> Tensor")
+def _dequant_op(x_fp8, scales, block_m, block_n):
     M, N = x_fp8.shape
     q = _codes_u8(x_fp8)
     # the reference indexes scales.flatten() as [row_block * ceil(N/bn) + col_block]
@@ -200,11 +303,15 @@ def dequantize_fp8(x_fp8: torch.Tensor, scales: torch.Tensor, block_m: int = 128
     if flat.stride(0) != 1:
         flat = flat.contiguous()
     nbn = _cdiv(N, block_n)
-    _require(flat.numel() >= _cdiv(M, block_m) * nbn, "scales too small for the block grid")
     out = torch.empty((M, N), dtype=torch.bfloat16, device=x_fp8.device)
     call("cin_dequant", ptr(q), M, N, q.stride(0), q.stride(1), ptr(flat), nbn, 1, block_m,
          block_n, ptr(out), _lib.CIN_DT_BF16, out.stride(0), stream_of(q))
     return out
+
+
+@_dequant_op.register_fake
+def _(x_fp8, scales, block_m, block_n):
+    return x_fp8.new_empty(x_fp8.shape, dtype=torch.bfloat16)
 
 
 # ---------------------------------------------------------------------------
@@ -233,19 +340,38 @@ def fp8_gemm_bs(a: torch.Tensor, a_scales: torch.Tensor, b_t: torch.Tensor,
     M, K = a.shape
     N, K2 = b_t.shape
     _require(K == K2, f"Dimension mismatch: {K} vs {K2}")
-    aq, Kp = _kcontig(a, K)
-    bq, _ = _kcontig(b_t, K)
     _require(a_scales.shape[0] >= M and a_scales.shape[1] >= _cdiv(K, 128), "a_scales too small")
     _require(b_scales_nk.shape[0] >= _cdiv(N, 128) and b_scales_nk.shape[1] >= _cdiv(K, 128),
              "b_scales too small")
     if out is None:
-        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+        _require(out_dtype in (torch.bfloat16, torch.float32), "out_dtype must be bf16 or fp32")
+        return _gemm_bs_op(a, a_scales, b_t, b_scales_nk, out_dtype)
     _require(out.dtype in (torch.bfloat16, torch.float32) and out.stride(1) == 1,
              "out must be bf16/fp32 with unit column stride")
+    return _gemm_bs_into(a, a_scales, b_t, b_scales_nk, out)
+
+
+def _gemm_bs_into(a, a_scales, b_t, b_scales_nk, out):
+    M, K = a.shape
+    N = b_t.shape[0]
+    aq, Kp = _kcontig(a, K)
+    bq, _ = _kcontig(b_t, K)
     call("cin_gemm_fp8_bs", ptr(aq), aq.stride(0), ptr(a_scales), a_scales.stride(0),
          a_scales.stride(1), ptr(bq), bq.stride(0), ptr(b_scales_nk), b_scales_nk.stride(0),
          b_scales_nk.stride(1), M, N, Kp, ptr(out), dtype_code(out), out.stride(0), stream_of(aq))
     return out
+
+
+@custom_op("gemm_fp8_bs",
+           "(Tensor a, Tensor a_scales, Tensor b_t, Tensor b_scales_nk, ScalarType out_dtype) -> Tensor")
+def _gemm_bs_op(a, a_scales, b_t, b_scales_nk, out_dtype):
+    out = torch.empty((a.shape[0], b_t.shape[0]), dtype=out_dtype, device=a.device)
+    return _gemm_bs_into(a, a_scales, b_t, b_scales_nk, out)
+
+
+@_gemm_bs_op.register_fake
+def _(a, a_scales, b_t, b_scales_nk, out_dtype):
+    return a.new_empty((a.shape[0], b_t.shape[0]), dtype=out_dtype)
 
 
 def fp8_matmul_dsv3(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor,
@@ -261,12 +387,23 @@ def fp8_matmul_dsv3(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor,
     if bq.stride(0) == 1 and bq.stride(1) % 16 == 0 and bq.data_ptr() % 16 == 0 and K % 16 == 0:
         b_t = bq.t()
     else:
-        src = bq if bq.stride(1) == 1 else bq.contiguous()
-        b_t = torch.empty((N, K), dtype=torch.uint8, device=b.device)
-        call("cin_transpose_u8", ptr(src), K, N, src.stride(0), ptr(b_t), b_t.stride(0),
-             stream_of(src))
+        b_t = _transpose_u8_op(bq)
     # b_scales is [kb, nb]; the GEMM reads it as [nb, kb] through swapped strides
     return fp8_gemm_bs(a, a_scales, b_t, b_scales.t(), torch.bfloat16)
+
+
+@custom_op("transpose_u8", "(Tensor src) -> Tensor")
+def _transpose_u8_op(src):
+    R, C = src.shape
+    s = src if src.stride(1) == 1 else src.contiguous()
+    out = torch.empty((C, R), dtype=torch.uint8, device=src.device)
+    call("cin_transpose_u8", ptr(s), R, C, s.stride(0), ptr(out), out.stride(0), stream_of(s))
+    return out
+
+
+@_transpose_u8_op.register_fake
+def _(src):
+    return src.new_empty((src.shape[1], src.shape[0]), dtype=torch.uint8)
 
 
 # ---------------------------------------------------------------------------
@@ -406,11 +543,23 @@ def moe_grouped_gemm(sorted_x: torch.Tensor, weights: torch.Tensor, expert_start
     starts = expert_starts.to(device=a.device, dtype=torch.int64).contiguous()
     ends = expert_ends.to(device=a.device, dtype=torch.int64).contiguous()
     _require(starts.numel() == E and ends.numel() == E, "expert ranges must have n_experts entries")
+    return _grouped_f16_op(a, w, starts, ends)
+
+
+@custom_op("grouped_gemm_f16", "(Tensor a, Tensor w, Tensor starts, Tensor ends) -> Tensor")
+def _grouped_f16_op(a, w, starts, ends):
+    T, d_in = a.shape
+    E, d_out, _ = w.shape
     out = torch.empty((T, d_out), dtype=torch.float16, device=a.device)
     call("cin_grouped_gemm_f16", ptr(a), dtype_code(a), a.stride(0), ptr(w), dtype_code(w),
          w.stride(0), w.stride(1), ptr(starts), ptr(ends), E, T, d_out, d_in, ptr(out),
          out.stride(0), stream_of(a))
     return out
+
+
+@_grouped_f16_op.register_fake
+def _(a, w, starts, ends):
+    return a.new_empty((a.shape[0], w.shape[1]), dtype=torch.float16)
 
 
 # ---------------------------------------------------------------------------

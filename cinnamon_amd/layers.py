@@ -11,43 +11,67 @@ from __future__ import annotations
 import torch
 
 from ._lib import call, dtype_code, ptr, stream_of
-from .kernels import (_cdiv, _codes_u8, _rows8, _kcontig, _require, quantize_fp8_blockwise_t,
-                      quantize_fp8_rowwise)
+from .kernels import (_cdiv, _codes_u8, _rows8, _kcontig, _require, custom_op,
+                      quantize_fp8_blockwise_t, quantize_fp8_rowwise)
 
 
 def fp8_grouped_gemm(a_codes: torch.Tensor, a_scales: torch.Tensor, w_codes: torch.Tensor,
                      w_scales: torch.Tensor, expert_starts: torch.Tensor,
                      expert_ends: torch.Tensor, out_dtype: torch.dtype = torch.bfloat16,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
+                     out: torch.Tensor | None = None,
+                     zero_uncovered: bool = False) -> torch.Tensor:
     """out[r] = A[r] x W_e^T for every row r in [starts[e], ends[e]), all experts in one launch.
 
     a_codes [T, K] e4m3 (1x128 scales a_scales [T, ceil(K/128)]), w_codes [E, N, K] e4m3
     (per-expert 128x128 block scales w_scales [E, ceil(N/128), ceil(K/128)]), expert
     ranges as int64 device tensors (no host sync).  Rows outside every range are left
-    untouched (as in the reference, whose output is torch.empty).
+    untouched (as in the reference, whose output is torch.empty), or zeroed with
+    ``zero_uncovered`` when the output is allocated here.
     """
     _require(a_codes.is_cuda and w_codes.is_cuda, "Input must be on CUDA")
     T, K = a_codes.shape
     E, N, K2 = w_codes.shape
     _require(K == K2, f"Dimension mismatch: {K} vs {K2}")
     _require(K % 16 == 0, "grouped GEMM needs K % 16 == 0")
-    aq, _ = _kcontig(a_codes, K)
-    wq = w_codes.view(torch.uint8) if w_codes.dtype == torch.float8_e4m3fn else w_codes
-    if wq.stride(2) != 1 or wq.stride(1) % 16 or wq.stride(0) % 16 or wq.data_ptr() % 16:
-        wq = wq.contiguous()
     _require(w_scales.shape[0] == E and w_scales.shape[1] >= _cdiv(N, 128)
              and w_scales.shape[2] >= _cdiv(K, 128), "w_scales must be [E, ceil(N/128), ceil(K/128)]")
     starts = expert_starts.to(torch.int64)
     ends = expert_ends.to(torch.int64)
     _require(starts.numel() == E and ends.numel() == E, "expert ranges must have E entries")
     if out is None:
-        out = torch.empty((T, N), dtype=out_dtype, device=a_codes.device)
+        return _grouped_gemm_op(a_codes, a_scales, w_codes, w_scales, starts, ends, out_dtype,
+                                bool(zero_uncovered))
     _require(out.stride(1) == 1, "out must have unit column stride")
+    return _grouped_gemm_into(a_codes, a_scales, w_codes, w_scales, starts, ends, out)
+
+
+def _grouped_gemm_into(a_codes, a_scales, w_codes, w_scales, starts, ends, out):
+    T, K = a_codes.shape
+    E, N, _ = w_codes.shape
+    aq, _ = _kcontig(a_codes, K)
+    wq = w_codes.view(torch.uint8) if w_codes.dtype == torch.float8_e4m3fn else w_codes
+    if wq.stride(2) != 1 or wq.stride(1) % 16 or wq.stride(0) % 16 or wq.data_ptr() % 16:
+        wq = wq.contiguous()
     call("cin_grouped_gemm_fp8", ptr(aq), aq.stride(0), ptr(a_scales), a_scales.stride(0),
          a_scales.stride(1), ptr(wq), wq.stride(0), wq.stride(1), ptr(w_scales),
          w_scales.stride(0), w_scales.stride(1), w_scales.stride(2), ptr(starts), ptr(ends), E, T,
          N, K, ptr(out), dtype_code(out), out.stride(0), stream_of(aq))
     return out
+
+
+@custom_op("grouped_gemm_fp8", "(Tensor a_codes, Tensor a_scales, Tensor w_codes, Tensor w_scales, "
+           "Tensor starts, Tensor ends, ScalarType out_dtype, bool zero_uncovered) -> Tensor")
+def _grouped_gemm_op(a_codes, a_scales, w_codes, w_scales, starts, ends, out_dtype, zero_uncovered):
+    T = a_codes.shape[0]
+    N = w_codes.shape[1]
+    out = (_empty_rows_zeroed(T, N, out_dtype, a_codes.device, starts, ends) if zero_uncovered
+           else torch.empty((T, N), dtype=out_dtype, device=a_codes.device))
+    return _grouped_gemm_into(a_codes, a_scales, w_codes, w_scales, starts, ends, out)
+
+
+@_grouped_gemm_op.register_fake
+def _(a_codes, a_scales, w_codes, w_scales, starts, ends, out_dtype, zero_uncovered):
+    return a_codes.new_empty((a_codes.shape[0], w_codes.shape[1]), dtype=out_dtype)
 
 
 # ---------------------------------------------------------------------------
@@ -79,9 +103,15 @@ def quantize_fp8_dual_grouped(grad: torch.Tensor, expert_starts: torch.Tensor,
     """
     _require(grad.is_cuda, "Input must be on CUDA")
     _require(grad.ndim == 2, "Input must be 2D")
+    starts, ends = _ranges(expert_starts, expert_ends)
+    return _dual_grouped_op(grad, starts, ends, bool(round_scale))
+
+
+@custom_op("quant_dual_grouped",
+           "(Tensor grad, Tensor starts, Tensor ends, bool round_scale) -> (Tensor, Tensor, Tensor, Tensor)")
+def _dual_grouped_op(grad, starts, ends, round_scale):
     if grad.stride(1) != 1 or (grad.stride(0) * grad.element_size()) % 16 or grad.data_ptr() % 16:
         grad = grad.contiguous()
-    starts, ends = _ranges(expert_starts, expert_ends)
     T, N = grad.shape
     E = starts.numel()
     cap = padded_capacity(T, E)
@@ -91,9 +121,19 @@ def quantize_fp8_dual_grouped(grad: torch.Tensor, expert_starts: torch.Tensor,
     qt = torch.empty((N, cap), dtype=torch.float8_e4m3fn, device=dev)
     st = torch.empty((N, cap // 128), dtype=torch.float32, device=dev)
     call("cin_quant_dual_grouped", ptr(grad), dtype_code(grad), T, N, grad.stride(0), ptr(starts),
-         ptr(ends), E, int(bool(round_scale)), ptr(q), q.stride(0), ptr(s), s.stride(0), ptr(qt),
+         ptr(ends), E, int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), ptr(qt),
          qt.stride(0), ptr(st), st.stride(0), stream_of(grad))
     return q, s, qt, st
+
+
+@_dual_grouped_op.register_fake
+def _(grad, starts, ends, round_scale):
+    T, N = grad.shape
+    cap = padded_capacity(T, starts.numel())
+    return (grad.new_empty((T, N), dtype=torch.float8_e4m3fn),
+            grad.new_empty((T, _cdiv(N, 128)), dtype=torch.float32),
+            grad.new_empty((N, cap), dtype=torch.float8_e4m3fn),
+            grad.new_empty((N, cap // 128), dtype=torch.float32))
 
 
 def requantize_grouped_t(x_fp8: torch.Tensor, x_scale: torch.Tensor, expert_starts: torch.Tensor,
@@ -103,8 +143,15 @@ def requantize_grouped_t(x_fp8: torch.Tensor, x_scale: torch.Tensor, expert_star
     equals quantize_fp8_blockwise(dequantize_fp8_rowwise(x_fp8, x_scale)[s_e:e_e]) (reference
     src/kernels.py:784-787 per slice)."""
     _require(x_fp8.is_cuda, "Input must be on CUDA")
-    q = _rows8(_codes_u8(x_fp8))
+    _codes_u8(x_fp8)
     starts, ends = _ranges(expert_starts, expert_ends)
+    return _requant_grouped_op(x_fp8, x_scale, starts, ends)
+
+
+@custom_op("requant_row_to_block_grouped",
+           "(Tensor x_fp8, Tensor x_scale, Tensor starts, Tensor ends) -> (Tensor, Tensor)")
+def _requant_grouped_op(x_fp8, x_scale, starts, ends):
+    q = _rows8(_codes_u8(x_fp8))
     T, K = q.shape
     E = starts.numel()
     cap = padded_capacity(T, E)
@@ -116,6 +163,14 @@ def requantize_grouped_t(x_fp8: torch.Tensor, x_scale: torch.Tensor, expert_star
     return qbt, sblk
 
 
+@_requant_grouped_op.register_fake
+def _(x_fp8, x_scale, starts, ends):
+    T, K = x_fp8.shape
+    cap = padded_capacity(T, starts.numel())
+    return (x_fp8.new_empty((K, cap), dtype=torch.float8_e4m3fn),
+            x_fp8.new_empty((cap // 128, _cdiv(K, 128)), dtype=torch.float32))
+
+
 def fp8_grouped_wgrad(g_t: torch.Tensor, g_st: torch.Tensor, x_bt: torch.Tensor,
                       x_blk: torch.Tensor, expert_starts: torch.Tensor, expert_ends: torch.Tensor,
                       num_tokens: int, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
@@ -125,10 +180,16 @@ def fp8_grouped_wgrad(g_t: torch.Tensor, g_st: torch.Tensor, x_bt: torch.Tensor,
     expert ranges over num_tokens rows).  Experts without tokens get zeros."""
     _require(g_t.is_cuda and x_bt.is_cuda, "Input must be on CUDA")
     starts, ends = _ranges(expert_starts, expert_ends)
+    _require(x_bt.shape[1] == g_t.shape[1], "operands must share the padded token axis")
+    return _grouped_wgrad_op(g_t, g_st, x_bt, x_blk, starts, ends, int(num_tokens), out_dtype)
+
+
+@custom_op("grouped_wgrad_fp8", "(Tensor g_t, Tensor g_st, Tensor x_bt, Tensor x_blk, Tensor starts, "
+           "Tensor ends, int num_tokens, ScalarType out_dtype) -> Tensor")
+def _grouped_wgrad_op(g_t, g_st, x_bt, x_blk, starts, ends, num_tokens, out_dtype):
     E = starts.numel()
     N, cap = g_t.shape
     K = x_bt.shape[0]
-    _require(x_bt.shape[1] == cap, "operands must share the padded token axis")
     a = g_t.view(torch.uint8)
     b = x_bt.view(torch.uint8)
     out = torch.empty((E, N, K), dtype=out_dtype, device=g_t.device)
@@ -138,11 +199,17 @@ def fp8_grouped_wgrad(g_t: torch.Tensor, g_st: torch.Tensor, x_bt: torch.Tensor,
     return out
 
 
+@_grouped_wgrad_op.register_fake
+def _(g_t, g_st, x_bt, x_blk, starts, ends, num_tokens, out_dtype):
+    return g_t.new_empty((starts.numel(), g_t.shape[0], x_bt.shape[0]), dtype=out_dtype)
+
+
 def fp8_grouped_dgrad(g_fp8: torch.Tensor, g_scale: torch.Tensor, w_codes_t: torch.Tensor,
                       w_scales: torch.Tensor, expert_starts: torch.Tensor,
                       expert_ends: torch.Tensor, n_out_per_expert: int,
                       out_dtype: torch.dtype = torch.float32,
-                      out: torch.Tensor | None = None) -> torch.Tensor:
+                      out: torch.Tensor | None = None,
+                      zero_uncovered: bool = False) -> torch.Tensor:
     """dA[r] = dC[r] . W_e for rows r of expert e -> [T, K].
 
     w_codes_t [K, E*N] and w_scales [E*N/128, ceil(K/128)] are quantize_fp8_blockwise_t of
@@ -154,10 +221,18 @@ def fp8_grouped_dgrad(g_fp8: torch.Tensor, g_scale: torch.Tensor, w_codes_t: tor
     K, EN = w_codes_t.shape
     _require(N == n_out_per_expert and EN == E * N and N % 128 == 0,
              "w_codes_t must be [K, E*N] with N a multiple of 128")
+    if out is None:
+        return _grouped_dgrad_op(g_fp8, g_scale, w_codes_t, w_scales, starts, ends, out_dtype,
+                                 bool(zero_uncovered))
+    return _grouped_dgrad_into(g_fp8, g_scale, w_codes_t, w_scales, starts, ends, out)
+
+
+def _grouped_dgrad_into(g_fp8, g_scale, w_codes_t, w_scales, starts, ends, out):
+    E = starts.numel()
+    T, N = g_fp8.shape
+    K = w_codes_t.shape[0]
     aq, _ = _kcontig(g_fp8, N)
     b = w_codes_t.view(torch.uint8)
-    if out is None:
-        out = torch.empty((T, K), dtype=out_dtype, device=g_fp8.device)
     nbk = w_scales.stride(0)  # scale columns per row block
     # B_e[k, n] = W_e[n, k]: codes at w_codes_t + e*N (row stride E*N); its block scales
     # [kb_out, nb_red] are w_scales[e*N/128 + nb_red, kb_out]
@@ -166,6 +241,20 @@ def fp8_grouped_dgrad(g_fp8: torch.Tensor, g_scale: torch.Tensor, w_codes_t: tor
          ptr(starts), ptr(ends), E, T, K, N, ptr(out), dtype_code(out), out.stride(0),
          stream_of(aq))
     return out
+
+
+@custom_op("grouped_dgrad_fp8", "(Tensor g_fp8, Tensor g_scale, Tensor w_codes_t, Tensor w_scales, "
+           "Tensor starts, Tensor ends, ScalarType out_dtype, bool zero_uncovered) -> Tensor")
+def _grouped_dgrad_op(g_fp8, g_scale, w_codes_t, w_scales, starts, ends, out_dtype, zero_uncovered):
+    T, K = g_fp8.shape[0], w_codes_t.shape[0]
+    out = (_empty_rows_zeroed(T, K, out_dtype, g_fp8.device, starts, ends) if zero_uncovered
+           else torch.empty((T, K), dtype=out_dtype, device=g_fp8.device))
+    return _grouped_dgrad_into(g_fp8, g_scale, w_codes_t, w_scales, starts, ends, out)
+
+
+@_grouped_dgrad_op.register_fake
+def _(g_fp8, g_scale, w_codes_t, w_scales, starts, ends, out_dtype, zero_uncovered):
+    return g_fp8.new_empty((g_fp8.shape[0], w_codes_t.shape[0]), dtype=out_dtype)
 
 
 def _empty_rows_zeroed(T: int, ncols: int, dtype: torch.dtype, device, starts, ends) -> torch.Tensor:
@@ -185,7 +274,11 @@ def silu_mul_quantize_fp8(h12: torch.Tensor, out_dtype: torch.dtype | None = Non
     Returns (codes float8_e4m3fn [M, H], scales fp32 [M, ceil(H/128)])."""
     _require(h12.is_cuda, "Input must be on CUDA")
     _require(h12.ndim == 2 and h12.shape[1] % 2 == 0, "h12 must be [M, 2H]")
-    out_dtype = out_dtype or h12.dtype
+    return _silu_mul_quant_op(h12, out_dtype or h12.dtype, bool(round_scale))
+
+
+@custom_op("silu_mul_quant_rowwise", "(Tensor h12, ScalarType out_dtype, bool round_scale) -> (Tensor, Tensor)")
+def _silu_mul_quant_op(h12, out_dtype, round_scale):
     M, H = h12.shape[0], h12.shape[1] // 2
     x = h12 if (h12.stride(1) == 1 and h12.data_ptr() % 16 == 0
                 and (h12.stride(0) * h12.element_size()) % 16 == 0) else h12.contiguous()
@@ -196,12 +289,25 @@ def silu_mul_quantize_fp8(h12: torch.Tensor, out_dtype: torch.dtype | None = Non
     return q, s
 
 
+@_silu_mul_quant_op.register_fake
+def _(h12, out_dtype, round_scale):
+    M, H = h12.shape[0], h12.shape[1] // 2
+    return (h12.new_empty((M, H), dtype=torch.float8_e4m3fn),
+            h12.new_empty((M, _cdiv(H, 128)), dtype=torch.float32))
+
+
 def swiglu_backward(dh: torch.Tensor, h12: torch.Tensor) -> torch.Tensor:
     """Gradient of h = silu(h1) * h2 ([h1 h2] = h12.float().chunk(2, -1)) with respect to
     h12, from dh [M, H] fp32, in one pass: [dh * h2 * silu'(h1), dh * silu(h1)] fp32 [M, 2H]."""
     _require(dh.is_cuda and h12.is_cuda, "Input must be on CUDA")
     M, H = dh.shape
     _require(h12.shape == (M, 2 * H), "h12 must be [M, 2H]")
+    return _swiglu_backward_op(dh, h12)
+
+
+@custom_op("swiglu_backward", "(Tensor dh, Tensor h12) -> Tensor")
+def _swiglu_backward_op(dh, h12):
+    M, H = dh.shape
     g = dh if (dh.dtype == torch.float32 and dh.stride(1) == 1 and dh.stride(0) % 4 == 0
                and dh.data_ptr() % 16 == 0) else dh.float().contiguous()
     x = h12 if h12.stride(1) == 1 else h12.contiguous()
@@ -209,6 +315,11 @@ def swiglu_backward(dh: torch.Tensor, h12: torch.Tensor) -> torch.Tensor:
     call("cin_swiglu_backward", ptr(g), g.stride(0), ptr(x), dtype_code(x), x.stride(0), M, H,
          ptr(out), out.stride(0), stream_of(g))
     return out
+
+
+@_swiglu_backward_op.register_fake
+def _(dh, h12):
+    return dh.new_empty((dh.shape[0], 2 * dh.shape[1]), dtype=torch.float32)
 
 
 class FP8GroupedExpertsFunction(torch.autograd.Function):
@@ -228,18 +339,13 @@ class FP8GroupedExpertsFunction(torch.autograd.Function):
         xq, xs = quantize_fp8_rowwise(sorted_x)
         w12f = w12 if w12.dtype == torch.float32 else w12.float()
         w12q, w12qt, w12s = quantize_fp8_blockwise_t(w12f.reshape(E * H2, D))
-        T = sorted_x.shape[0]
         h12 = fp8_grouped_gemm(xq, xs, w12q.view(E, H2, D), w12s.view(E, H2 // 128, -1),
-                               starts, ends, out_dtype=torch.bfloat16,
-                               out=_empty_rows_zeroed(T, H2, torch.bfloat16, sorted_x.device,
-                                                      starts, ends))
+                               starts, ends, out_dtype=torch.bfloat16, zero_uncovered=True)
         hq, hs = silu_mul_quantize_fp8(h12, out_dtype=sorted_x.dtype)
         w3f = w3 if w3.dtype == torch.float32 else w3.float()
         w3q, w3qt, w3s = quantize_fp8_blockwise_t(w3f.reshape(E * D, H))
         out = fp8_grouped_gemm(hq, hs, w3q.view(E, D, H), w3s.view(E, D // 128, -1), starts, ends,
-                               out_dtype=torch.float32,
-                               out=_empty_rows_zeroed(T, D, torch.float32, sorted_x.device,
-                                                      starts, ends))
+                               out_dtype=torch.float32, zero_uncovered=True)
         ctx.save_for_backward(xq, xs, w12qt, w12s, h12, hq, hs, w3qt, w3s, starts, ends)
         ctx.dims = (E, H, D)
         ctx.x_dtype = sorted_x.dtype
@@ -252,9 +358,8 @@ class FP8GroupedExpertsFunction(torch.autograd.Function):
         E, H, D = ctx.dims
         g = grad_out.contiguous()
         gq, gs, gqt, gst = quantize_fp8_dual_grouped(g, starts, ends)
-        T = g.shape[0]
-        dh = fp8_grouped_dgrad(gq, gs, w3qt, w3s, starts, ends, D,
-                               out=_empty_rows_zeroed(T, H, torch.float32, g.device, starts, ends))
+        dh = fp8_grouped_dgrad(gq, gs, w3qt, w3s, starts, ends, D, out_dtype=torch.float32,
+                               zero_uncovered=True)
         hbt, hblk = requantize_grouped_t(hq, hs, starts, ends)
         dw3 = fp8_grouped_wgrad(gqt, gst, hbt, hblk, starts, ends, g.shape[0])
         # silu(h1) * h2 in fp32 (the forward's cast to the input dtype passes the gradient)
@@ -262,8 +367,8 @@ class FP8GroupedExpertsFunction(torch.autograd.Function):
         dq, ds, dqt, dst = quantize_fp8_dual_grouped(dh12, starts, ends)
         # dx straight in the input dtype: the GEMM's bf16 store is the RNE of its fp32 value
         dx_dtype = ctx.x_dtype if ctx.x_dtype in (torch.bfloat16, torch.float32) else torch.float32
-        dx = fp8_grouped_dgrad(dq, ds, w12qt, w12s, starts, ends, 2 * H,
-                               out=_empty_rows_zeroed(T, D, dx_dtype, g.device, starts, ends))
+        dx = fp8_grouped_dgrad(dq, ds, w12qt, w12s, starts, ends, 2 * H, out_dtype=dx_dtype,
+                               zero_uncovered=True)
         xbt, xblk = requantize_grouped_t(xq, xs, starts, ends)
         dw12 = fp8_grouped_wgrad(dqt, dst, xbt, xblk, starts, ends, g.shape[0])
         return (dx.to(ctx.x_dtype), dw12.to(ctx.w_dtypes[0]), dw3.to(ctx.w_dtypes[1]), None, None)

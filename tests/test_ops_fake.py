@@ -1,0 +1,160 @@
+"""The torch operators behind the drop-in functions (CPU, no GPU needed).
+
+Every launch is registered as a cinnamon_amd:: operator with a shape function, so
+torch.compile traces through FP8Linear and the FP8 experts instead of breaking the graph
+at a native call (the reference compiles its model, src/train.py:703).  Here the shape
+functions run on fake CUDA tensors: the public functions must return the shapes, dtypes
+and device the real kernels produce (tests/test_gpu_*.py check the real ones against the
+oracle), and a fake-mode trace of FP8Linear and GroupedExperts forward + backward must
+consist of these operators and plain torch ops only.
+"""
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+from torch.fx.experimental.proxy_tensor import make_fx
+
+from cinnamon_amd import kernels, layers
+
+OPS = ["quant_rowwise", "quant_blockwise", "quant_blockwise_t", "quant_dual", "requant_row_to_block",
+       "dequant_rowwise", "dequant", "gemm_fp8_bs", "transpose_u8", "grouped_gemm_f16",
+       "grouped_gemm_fp8", "quant_dual_grouped", "requant_row_to_block_grouped",
+       "grouped_wgrad_fp8", "grouped_dgrad_fp8", "silu_mul_quant_rowwise", "swiglu_backward"]
+F8, F32, BF16 = torch.float8_e4m3fn, torch.float32, torch.bfloat16
+
+
+def _meta(t):
+    return tuple(t.shape), t.dtype, t.device.type
+
+
+def test_every_operator_is_registered():
+    for name in OPS:
+        assert hasattr(torch.ops.cinnamon_amd, name), name
+
+
+def test_shape_functions_match_the_kernels_outputs():
+    with FakeTensorMode():
+        dev = "cuda"
+        x = torch.empty(300, 1100, dtype=BF16, device=dev)
+        q, s = kernels.quantize_fp8_rowwise(x)
+        assert _meta(q) == ((300, 1100), F8, "cuda") and _meta(s) == ((300, 9), F32, "cuda")
+        q, s = kernels.quantize_fp8_rowwise(x, block_size=64)
+        assert s.shape == (300, 18)
+        q, s = kernels.quantize_fp8_blockwise(x)
+        assert _meta(q) == ((300, 1100), F8, "cuda") and _meta(s) == ((3, 9), F32, "cuda")
+        q, qt, s = kernels.quantize_fp8_blockwise_t(x)
+        assert q.shape == (300, 1100) and qt.shape == (1100, 300) and s.shape == (3, 9)
+        q, qt, s = kernels.quantize_fp8_blockwise_t(x, with_rowmajor=False)
+        assert q is None and qt.shape == (1100, 300)
+        q, s, qt, st = kernels.quantize_fp8_dual(x)
+        assert [t.shape for t in (q, s, qt, st)] == [(300, 1100), (300, 9), (1100, 300), (1100, 3)]
+        assert [t.dtype for t in (q, s, qt, st)] == [F8, F32, F8, F32]
+        xq, xs = kernels.quantize_fp8_rowwise(x)
+        b, bs = kernels.requantize_rowwise_to_blockwise(xq, xs)
+        assert _meta(b) == ((300, 1100), F8, "cuda") and bs.shape == (3, 9)
+        b, bs = kernels.requantize_rowwise_to_blockwise(xq, xs, transposed=True)
+        assert b.shape == (1100, 300)
+        assert _meta(kernels.dequantize_fp8_rowwise(xq, xs)) == ((300, 1100), F32, "cuda")
+        wq, ws = kernels.quantize_fp8_blockwise(x)
+        assert _meta(kernels.dequantize_fp8(wq, ws)) == ((300, 1100), BF16, "cuda")
+        a = torch.empty(256, 512, dtype=F8, device=dev)
+        sa = torch.empty(256, 4, dtype=F32, device=dev)
+        bt = torch.empty(384, 512, dtype=F8, device=dev)
+        sbt = torch.empty(3, 4, dtype=F32, device=dev)
+        assert _meta(kernels.fp8_gemm_bs(a, sa, bt, sbt)) == ((256, 384), BF16, "cuda")
+        assert kernels.fp8_gemm_bs(a, sa, bt, sbt, F32).dtype == F32
+        bkn = torch.empty(512, 384, dtype=F8, device=dev)   # B [K, N], row-major: transposed on device
+        assert _meta(kernels.fp8_matmul_dsv3(a, bkn, sa, sbt.t())) == ((256, 384), BF16, "cuda")
+        # grouped
+        T, E, D, H = 1000, 4, 256, 384
+        starts = torch.tensor([0, 100, 100, 600], device=dev)
+        ends = torch.tensor([100, 100, 600, 1000], device=dev)
+        xg = torch.empty(T, D, dtype=BF16, device=dev)
+        w = torch.empty(E, H, D, dtype=F32, device=dev)
+        assert _meta(kernels.moe_grouped_gemm(xg, w, starts, ends)) == ((T, H), torch.float16, "cuda")
+        aq, asc = kernels.quantize_fp8_rowwise(xg)
+        wq, wqt, wsc = kernels.quantize_fp8_blockwise_t(w.reshape(E * H, D))
+        out = layers.fp8_grouped_gemm(aq, asc, wq.view(E, H, D), wsc.view(E, H // 128, -1), starts, ends)
+        assert _meta(out) == ((T, H), BF16, "cuda")
+        g = torch.empty(T, H, dtype=BF16, device=dev)
+        cap = layers.padded_capacity(T, E)
+        gq, gs, gqt, gst = layers.quantize_fp8_dual_grouped(g, starts, ends)
+        assert [t.shape for t in (gq, gs, gqt, gst)] == [(T, H), (T, 3), (H, cap), (H, cap // 128)]
+        xbt, xblk = layers.requantize_grouped_t(aq, asc, starts, ends)
+        assert xbt.shape == (D, cap) and xblk.shape == (cap // 128, 2) and xbt.dtype == F8
+        dw = layers.fp8_grouped_wgrad(gqt, gst, xbt, xblk, starts, ends, T)
+        assert _meta(dw) == ((E, H, D), F32, "cuda")
+        dx = layers.fp8_grouped_dgrad(gq, gs, wqt, wsc, starts, ends, H, zero_uncovered=True)
+        assert _meta(dx) == ((T, D), F32, "cuda")
+        h12 = torch.empty(T, 2 * H, dtype=BF16, device=dev)
+        hq, hs = layers.silu_mul_quantize_fp8(h12)
+        assert _meta(hq) == ((T, H), F8, "cuda") and hs.shape == (T, 3)
+        dh = torch.empty(T, H, dtype=F32, device=dev)
+        assert _meta(layers.swiglu_backward(dh, h12)) == ((T, 2 * H), F32, "cuda")
+
+
+def _op_targets(gm):
+    names = set()
+    for n in gm.graph.nodes:
+        if n.op == "call_function":
+            names.add(str(n.target))
+    return names
+
+
+class _Ctx:
+    """Stands in for autograd's ctx: without a GPU the autograd engine cannot run a
+    backward pass on fake CUDA tensors, so the trace calls forward and backward directly."""
+
+    def save_for_backward(self, *tensors):
+        self.saved_tensors = tensors
+
+
+@pytest.mark.parametrize("round_scale", [False, True])
+def test_fp8_linear_forward_backward_traces_to_operators(round_scale):
+    fn = kernels.FP8MatmulFunction
+
+    def step(x, w, gy):
+        ctx = _Ctx()
+        y = fn.forward(ctx, x, w, round_scale)
+        dx, dw, _ = fn.backward(ctx, gy)
+        return y, dx, dw
+
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        w = torch.empty(384, 512, dtype=F32, device="cuda")
+        x = torch.empty(4, 64, 512, dtype=BF16, device="cuda")
+        gy = torch.empty(4, 64, 384, dtype=BF16, device="cuda")
+        gm = make_fx(step, tracing_mode="fake")(x, w, gy)
+        y, dx, dw = step(x, w, gy)
+        assert _meta(y) == ((4, 64, 384), BF16, "cuda")
+        assert _meta(dx) == ((4, 64, 512), BF16, "cuda") and _meta(dw) == ((384, 512), BF16, "cuda")
+    ops = _op_targets(gm)
+    for name in ["quant_rowwise", "quant_blockwise_t", "gemm_fp8_bs", "quant_dual",
+                 "requant_row_to_block"]:
+        assert any(f"cinnamon_amd.{name}" in o for o in ops), (name, ops)
+
+
+def test_grouped_experts_forward_backward_traces_to_operators():
+    fn = layers.FP8GroupedExpertsFunction
+    T, E, D, H = 700, 4, 256, 256
+
+    def step(x, w12, w3, starts, ends, gy):
+        ctx = _Ctx()
+        y = fn.forward(ctx, x, w12, w3, starts, ends)
+        dx, dw12, dw3, _, _ = fn.backward(ctx, gy)
+        return y, dx, dw12, dw3
+
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        w12 = torch.empty(E, 2 * H, D, dtype=F32, device="cuda")
+        w3 = torch.empty(E, D, H, dtype=F32, device="cuda")
+        starts = torch.empty(E, dtype=torch.int64, device="cuda")
+        ends = torch.empty(E, dtype=torch.int64, device="cuda")
+        x = torch.empty(T, D, dtype=BF16, device="cuda")
+        gy = torch.empty(T, D, dtype=F32, device="cuda")
+        gm = make_fx(step, tracing_mode="fake")(x, w12, w3, starts, ends, gy)
+        y, dx, dw12, dw3 = step(x, w12, w3, starts, ends, gy)
+        assert _meta(y) == ((T, D), F32, "cuda") and _meta(dx) == ((T, D), BF16, "cuda")
+        assert _meta(dw12) == ((E, 2 * H, D), F32, "cuda") and _meta(dw3) == ((E, D, H), F32, "cuda")
+    ops = _op_targets(gm)
+    for name in ["grouped_gemm_fp8", "silu_mul_quant_rowwise", "quant_dual_grouped",
+                 "grouped_dgrad_fp8", "requant_row_to_block_grouped", "grouped_wgrad_fp8",
+                 "swiglu_backward"]:
+        assert any(f"cinnamon_amd.{name}" in o for o in ops), (name, ops)
