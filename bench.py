@@ -158,6 +158,27 @@ def measured_traffic(profile="profiles/k_gemm_fp8_bs_256_config2_fwd.txt"):
     return None, None
 
 
+def measured_mfma(profile="profiles/k_gemm_fp8_bs_256_config2_fwd.txt"):
+    """The committed rocprofv3 MFMA-counter figures of the GEMM: FP8 FLOP per launch
+    (SQ_INSTS_VALU_MFMA_MOPS_F8 x 512), average clock (GRBM_GUI_ACTIVE) and MfmaUtil
+    (SQ_VALU_MFMA_BUSY_CYCLES over active cycles x SIMDs); None if the summary is absent."""
+    out = {}
+    try:
+        for line in open(os.path.join(ROOT, profile)):
+            if "SQ_INSTS_VALU_MFMA_MOPS_F8 x 512 =" in line:
+                out["mfma_flop_per_launch"] = float(line.split("=")[1].split("GFLOP")[0]) * 1e9
+            elif "MHz average clock" in line:
+                out["clock_mhz"] = float(line.split("->")[1].split("MHz")[0])
+            elif line.strip().startswith("MfmaUtil"):
+                out["mfma_util"] = round(float(line.rsplit("=", 1)[1].strip().rstrip("%")) / 100, 4)
+    except (OSError, ValueError, IndexError):
+        return None
+    if len(out) != 3:
+        return None
+    out["source"] = profile
+    return out
+
+
 def moe_setup(dev):
     """Config 3: 32 experts, d_model 7168, expert hidden 2048, 16384 tokens, top-8 routing
     with Zipf(1.1) expert popularity (sampled without replacement), bf16 ~N(0,1)
@@ -399,6 +420,7 @@ def main():
             "frac": round(gemm_tflops / PEAK_FP8_TFLOPS, 4),
             "traffic": measured_traffic()[0],
             "traffic_source": measured_traffic()[1],
+            "counters": measured_mfma(),
             "kernel": "k_gemm_fp8_bs_256",
             "algorithmic_work": "2*M*N*K = %.4g FLOP per launch" % flops,
         },
