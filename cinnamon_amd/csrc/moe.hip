@@ -1,0 +1,446 @@
+// MoE dispatch and combine on the device: the permute / unpermute around the grouped
+// expert GEMMs (reference src/layers.py:126-157), with no host synchronisation.
+//
+//   route    : stable counting sort of the flattened top-k expert ids.  perm[r] is the
+//              flattened assignment (token * k + slot) at sorted position r, inv is its
+//              inverse, starts/ends/counts are the experts' row ranges (int64, on the
+//              device: the reference's bincount + cumsum + `.item()`).  Ids outside [0, E)
+//              are dropped: inv = -1 for them and perm = -1 at the unused tail positions.
+//   gather   : the row-wise quantizer reads x rows through perm (quant.hip,
+//              cin_moe_gather_quant_rowwise); its backward is gather_sum here.
+//   combine  : out[t] = sum over the token's assignments of sorted_out[r] * score[t, slot],
+//              added in increasing sorted position: the order of a sequential
+//              scatter_add_ over sorted rows (reference :152-154).  Its backward gives the
+//              sorted-row gradient and the score gradient.
+//
+// Every kernel checks the indices it follows against the sizes it was given, so a bad
+// map costs a wrong row, never an access outside the buffers.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "cin_common.h"
+#include "cin_runtime.h"
+
+using namespace cin;
+
+namespace {
+
+constexpr int kRT = 256;           // threads of the route kernels
+constexpr int kRounds = 8;         // assignments per thread in a route block
+constexpr int kChunk = kRT * kRounds;
+constexpr int kMaxExperts = 4096;  // LDS counters of the route kernels
+constexpr int kMaxTopK = 16;       // positions a combine thread sorts in registers
+
+inline bool valid_dtype(int dt) { return dt == CIN_DT_BF16 || dt == CIN_DT_F32 || dt == CIN_DT_F16; }
+
+__device__ inline uint16_t f32_to_f16_bits(float f) {
+  const _Float16 h = (_Float16)f;  // round to nearest even
+  uint16_t b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
+
+// Sum over the 64 lanes (a fixed butterfly: the same inputs give the same bits).
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// Per-block expert histogram.
+__global__ __launch_bounds__(kRT) void k_route_hist(const int64_t* __restrict__ idx, int64_t A,
+                                                    int32_t E, int32_t* __restrict__ blockcounts) {
+  __shared__ int hist[kMaxExperts];
+  for (int e = threadIdx.x; e < E; e += kRT) hist[e] = 0;
+  __syncthreads();
+  const int64_t b0 = (int64_t)blockIdx.x * kChunk;
+  for (int r = 0; r < kRounds; ++r) {
+    const int64_t i = b0 + r * kRT + threadIdx.x;
+    if (i < A) {
+      const int64_t e = idx[i];
+      if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kRT) blockcounts[(int64_t)blockIdx.x * E + e] = hist[e];
+}
+
+// One workgroup: per-expert totals, expert ranges, and each (block, expert)'s first
+// sorted position; the unused tail of perm (dropped ids) gets -1.
+__global__ __launch_bounds__(kRT) void k_route_scan(int32_t* __restrict__ blockcounts,
+                                                    int32_t nblocks, int32_t E, int64_t A,
+                                                    int64_t* __restrict__ counts,
+                                                    int64_t* __restrict__ starts,
+                                                    int64_t* __restrict__ ends,
+                                                    int64_t* __restrict__ perm) {
+  __shared__ int64_t tot[kMaxExperts];
+  __shared__ int64_t total_s;
+  for (int e = threadIdx.x; e < E; e += kRT) {
+    int64_t run = 0;
+    for (int b = 0; b < nblocks; ++b) {
+      const int64_t j = (int64_t)b * E + e;
+      const int32_t c = blockcounts[j];
+      blockcounts[j] = (int32_t)run;  // becomes the block's offset within the expert
+      run += c;
+    }
+    tot[e] = run;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t s = 0;
+    for (int e = 0; e < E; ++e) {
+      const int64_t c = tot[e];
+      tot[e] = s;
+      s += c;
+    }
+    total_s = s;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += kRT) {
+    const int64_t st = tot[e];
+    const int64_t en = e + 1 < E ? tot[e + 1] : total_s;
+    starts[e] = st;
+    ends[e] = en;
+    counts[e] = en - st;
+  }
+  for (int64_t j = threadIdx.x; j < (int64_t)nblocks * E; j += kRT)
+    blockcounts[j] += (int32_t)tot[j % E];
+  for (int64_t r = total_s + threadIdx.x; r < A; r += kRT) perm[r] = -1;
+}
+
+// Stable scatter: an assignment's sorted position is its block's first position for its
+// expert, plus the assignments of that expert earlier in the block.  A block walks its
+// assignments in rounds of 256 in index order; within a round a thread counts the equal
+// ids of lower threads.
+__global__ __launch_bounds__(kRT) void k_route_scatter(const int64_t* __restrict__ idx, int64_t A,
+                                                       int32_t E,
+                                                       const int32_t* __restrict__ blockbase,
+                                                       int64_t* __restrict__ perm,
+                                                       int32_t* __restrict__ inv) {
+  __shared__ int running[kMaxExperts];
+  __shared__ int se[kRT];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += kRT) running[e] = 0;
+  const int64_t b0 = (int64_t)blockIdx.x * kChunk;
+  for (int r = 0; r < kRounds; ++r) {
+    const int64_t i = b0 + r * kRT + tid;
+    int e = -1;
+    if (i < A) {
+      const int64_t v = idx[i];
+      e = (v >= 0 && v < E) ? (int)v : -1;
+    }
+    se[tid] = e;
+    __syncthreads();  // also orders the previous round's running[] updates
+    int rank = 0;
+    bool last = true;
+    if (e >= 0) {
+      for (int j = 0; j < tid; ++j) rank += se[j] == e;
+      for (int j = tid + 1; j < kRT; ++j)
+        if (se[j] == e) {
+          last = false;
+          break;
+        }
+      const int64_t pos = (int64_t)blockbase[(int64_t)blockIdx.x * E + e] + running[e] + rank;
+      if (pos >= 0 && pos < A) {
+        perm[pos] = i;
+        inv[i] = (int32_t)pos;
+      }
+    } else if (i < A) {
+      inv[i] = -1;
+    }
+    __syncthreads();  // every thread has read running[] for this round
+    if (e >= 0 && last) running[e] += rank + 1;
+  }
+}
+
+// Sorted positions of token t's assignments in increasing order, with their slots; the
+// missing ones (dropped ids, slots past k) get INT32_MAX and sort last.  A fixed
+// compare-swap network keeps every index a compile-time one (registers, no scratch).
+// Returns the number of valid positions.
+__device__ inline int token_positions(const int32_t* __restrict__ inv, int64_t t, int k, int64_t A,
+                                      int32_t (&pos)[kMaxTopK], int32_t (&slot)[kMaxTopK]) {
+  int n = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxTopK; ++j) {
+    const int32_t p = j < k ? inv[t * k + j] : -1;
+    const bool ok = p >= 0 && p < A;
+    pos[j] = ok ? p : INT32_MAX;
+    slot[j] = j;
+    n += ok;
+  }
+#pragma unroll
+  for (int i = 0; i < kMaxTopK - 1; ++i) {
+#pragma unroll
+    for (int j = 0; j < kMaxTopK - 1 - i; ++j) {
+      if (pos[j] > pos[j + 1]) {
+        const int32_t tp = pos[j], ts = slot[j];
+        pos[j] = pos[j + 1];
+        slot[j] = slot[j + 1];
+        pos[j + 1] = tp;
+        slot[j + 1] = ts;
+      }
+    }
+  }
+  return n;
+}
+
+template <int DT>
+__device__ inline void load4(const void* base, int64_t off, int64_t nv, float (&v)[4]) {
+  if constexpr (DT == CIN_DT_F32) {
+    const float* p = static_cast<const float*>(base) + off;
+    if (nv >= 4 && (((uintptr_t)p) & 15) == 0) {
+      const float4 w = *reinterpret_cast<const float4*>(p);
+      v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
+    } else {
+      for (int e = 0; e < 4; ++e) v[e] = e < nv ? p[e] : 0.0f;
+    }
+  } else {
+    for (int e = 0; e < 4; ++e) v[e] = e < nv ? load_elem(base, DT, off + e) : 0.0f;
+  }
+}
+
+template <int OT>
+__device__ inline void store4(void* base, int64_t off, int64_t nv, const float (&v)[4]) {
+  if constexpr (OT == CIN_DT_F32) {
+    float* p = static_cast<float*>(base) + off;
+    if (nv >= 4 && (((uintptr_t)p) & 15) == 0) {
+      *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      for (int e = 0; e < 4; ++e)
+        if (e < nv) p[e] = v[e];
+    }
+  } else {
+    uint16_t* p = static_cast<uint16_t*>(base) + off;
+    for (int e = 0; e < 4; ++e)
+      if (e < nv) p[e] = OT == CIN_DT_BF16 ? (uint16_t)f32_to_bf16_bits(v[e]) : f32_to_f16_bits(v[e]);
+  }
+}
+
+// dx[t] = sum of g[r] over token t's sorted positions r (increasing r), fp32 sums.
+// One wave per token; lane l covers columns 4 l + 256 i.
+template <int GT, int OT>
+__global__ __launch_bounds__(kRT) void k_moe_gather_sum(const void* __restrict__ g, int64_t sgm,
+                                                        const int32_t* __restrict__ inv,
+                                                        int64_t T, int k, int64_t A, int64_t N,
+                                                        void* __restrict__ out, int64_t som) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = ((int64_t)blockIdx.x * kRT + threadIdx.x) >> 6;
+  if (t >= T) return;  // uniform per wave
+  int32_t pos[kMaxTopK], slot[kMaxTopK];
+  const int n = token_positions(inv, t, k, A, pos, slot);
+  for (int64_t c = (int64_t)lane * 4; c < N; c += 256) {
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j) {
+      if (j < n) {
+        float v[4];
+        load4<GT>(g, (int64_t)pos[j] * sgm + c, N - c, v);
+        for (int e = 0; e < 4; ++e) acc[e] = acc[e] + v[e];
+      }
+    }
+    store4<OT>(out, t * som + c, N - c, acc);
+  }
+}
+
+template <int ST>
+__device__ inline float score_at(const void* s, int64_t off) {
+  return load_elem(s, ST, off);
+}
+
+// out[t] = sum over the token's positions r (increasing) of y[r] * score[t, slot(r)]:
+// a product then an add, both rounded (built without contraction), fp32.  One wave per
+// token; lane l covers columns 4 l + 256 i.
+template <int ST>
+__global__ __launch_bounds__(kRT) void k_moe_combine(const float* __restrict__ y, int64_t sym,
+                                                     const void* __restrict__ scores,
+                                                     int64_t ssm, const int32_t* __restrict__ inv,
+                                                     int64_t T, int k, int64_t A, int64_t N,
+                                                     float* __restrict__ out, int64_t som) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = ((int64_t)blockIdx.x * kRT + threadIdx.x) >> 6;
+  if (t >= T) return;  // uniform per wave
+  int32_t pos[kMaxTopK], slot[kMaxTopK];
+  const int n = token_positions(inv, t, k, A, pos, slot);
+  float w[kMaxTopK];
+#pragma unroll
+  for (int j = 0; j < kMaxTopK; ++j) w[j] = j < n ? score_at<ST>(scores, t * ssm + slot[j]) : 0.0f;
+  for (int64_t c = (int64_t)lane * 4; c < N; c += 256) {
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j) {
+      if (j < n) {
+        float v[4];
+        load4<CIN_DT_F32>(y, (int64_t)pos[j] * sym + c, N - c, v);
+        for (int e = 0; e < 4; ++e) acc[e] = acc[e] + v[e] * w[j];
+      }
+    }
+    store4<CIN_DT_F32>(out, t * som + c, N - c, acc);
+  }
+}
+
+// Combine backward, sorted-row gradient: dy[r] = dout[t] * score[t, slot] for the
+// assignment at position r (zero rows at the unused tail).  Thread = (row, 4 columns).
+template <int ST>
+__global__ __launch_bounds__(kRT) void k_moe_combine_bwd_rows(const float* __restrict__ dout,
+                                                              int64_t sdm,
+                                                              const void* __restrict__ scores,
+                                                              int64_t ssm,
+                                                              const int64_t* __restrict__ perm,
+                                                              int64_t T, int k, int64_t A,
+                                                              int64_t N, float* __restrict__ dy,
+                                                              int64_t sym) {
+  const int64_t nq = (N + 3) / 4;
+  const int64_t id = (int64_t)blockIdx.x * kRT + threadIdx.x;
+  if (id >= A * nq) return;
+  const int64_t r = id / nq, c = (id - r * nq) * 4;
+  const int64_t i = perm[r];
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (i >= 0 && i < T * k) {
+    const int64_t t = i / k, j = i - t * k;
+    const float w = score_at<ST>(scores, t * ssm + j);
+    load4<CIN_DT_F32>(dout, t * sdm + c, N - c, v);
+    for (int e = 0; e < 4; ++e) v[e] = v[e] * w;
+  }
+  store4<CIN_DT_F32>(dy, r * sym + c, N - c, v);
+}
+
+// Combine backward, score gradient: dscore[t, j] = sum_c dout[t, c] * y[inv[t k + j], c],
+// fp32; one wave per (token, slot), lanes over columns, then a wave sum.
+__global__ __launch_bounds__(kRT) void k_moe_combine_bwd_scores(const float* __restrict__ dout,
+                                                                int64_t sdm,
+                                                                const float* __restrict__ y,
+                                                                int64_t sym,
+                                                                const int32_t* __restrict__ inv,
+                                                                int64_t T, int k, int64_t A,
+                                                                int64_t N,
+                                                                float* __restrict__ dscores) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = ((int64_t)blockIdx.x * kRT + threadIdx.x) >> 6;
+  if (w >= T * k) return;  // uniform per wave
+  const int64_t t = w / k;
+  const int32_t p = inv[w];
+  float acc = 0.0f;
+  if (p >= 0 && p < A) {
+    const float* a = dout + t * sdm;
+    const float* b = y + (int64_t)p * sym;
+    for (int64_t c = lane; c < N; c += 64) acc += a[c] * b[c];
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) dscores[w] = acc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cin_moe_route(const int64_t* idx, int64_t T, int64_t k, int64_t E, int64_t* perm, int32_t* inv,
+                  int64_t* counts, int64_t* starts, int64_t* ends, int32_t* workspace,
+                  int64_t workspace_elems, void* stream) {
+  CIN_CHECK_ARG(T >= 0 && k >= 1 && E >= 1, "moe_route: need T >= 0, k >= 1, E >= 1");
+  CIN_CHECK_ARG(E <= kMaxExperts, "moe_route: at most %d experts", kMaxExperts);
+  const int64_t A = T * k;
+  CIN_CHECK_ARG(A < ((int64_t)1 << 31), "moe_route: T*k must fit in 31 bits");
+  CIN_CHECK_ARG(idx && perm && inv && counts && starts && ends && (A == 0 || workspace),
+                "moe_route: null pointer");
+  const int64_t nblocks = cdiv(A, kChunk);
+  CIN_CHECK_ARG(workspace_elems >= nblocks * E, "moe_route: workspace needs %lld int32",
+                (long long)(nblocks * E));
+  CIN_CHECK_ARG(nblocks < 65536, "moe_route: too many assignments");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (nblocks > 0) hipLaunchKernelGGL(k_route_hist, (unsigned)nblocks, kRT, 0, s, idx, A, (int32_t)E, workspace);
+  hipLaunchKernelGGL(k_route_scan, 1, kRT, 0, s, workspace, (int32_t)nblocks, (int32_t)E, A, counts,
+                     starts, ends, perm);
+  if (nblocks > 0)
+    hipLaunchKernelGGL(k_route_scatter, (unsigned)nblocks, kRT, 0, s, idx, A, (int32_t)E, workspace,
+                       perm, inv);
+  return cin_check_launch("moe_route");
+}
+
+int cin_moe_route_workspace(int64_t T, int64_t k, int64_t E) {
+  if (T < 0 || k < 1 || E < 1) return 0;
+  const int64_t n = cdiv(T * k, kChunk) * E;
+  return n > INT32_MAX ? INT32_MAX : (int)n;
+}
+
+int cin_moe_gather_sum(const void* g, int g_dtype, int64_t sgm, const int32_t* inv, int64_t T,
+                       int64_t k, int64_t A, int64_t N, void* out, int out_dtype, int64_t som,
+                       void* stream) {
+  CIN_CHECK_ARG(valid_dtype(g_dtype) && valid_dtype(out_dtype), "moe_gather_sum: unsupported dtype");
+  CIN_CHECK_ARG(T >= 0 && k >= 1 && k <= kMaxTopK && A >= 0 && N >= 0,
+                "moe_gather_sum: need k in [1, %d] and non-negative sizes", kMaxTopK);
+  if (T == 0 || N == 0) return CIN_OK;
+  CIN_CHECK_ARG(g && inv && out && sgm >= N && som >= N, "moe_gather_sum: bad pointers or strides");
+  CIN_CHECK_ARG(cdiv(T * 64, kRT) < ((int64_t)1 << 31), "moe_gather_sum: grid too large");
+  const unsigned grid = (unsigned)cdiv(T * 64, kRT);  // one wave per token
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define CIN_GS(GT, OT) \
+  hipLaunchKernelGGL((k_moe_gather_sum<GT, OT>), grid, kRT, 0, s, g, sgm, inv, T, (int)k, A, N, out, som)
+  if (g_dtype == CIN_DT_F32) {
+    if (out_dtype == CIN_DT_F32) CIN_GS(CIN_DT_F32, CIN_DT_F32);
+    else if (out_dtype == CIN_DT_BF16) CIN_GS(CIN_DT_F32, CIN_DT_BF16);
+    else CIN_GS(CIN_DT_F32, CIN_DT_F16);
+  } else if (g_dtype == CIN_DT_BF16) {
+    if (out_dtype == CIN_DT_F32) CIN_GS(CIN_DT_BF16, CIN_DT_F32);
+    else if (out_dtype == CIN_DT_BF16) CIN_GS(CIN_DT_BF16, CIN_DT_BF16);
+    else CIN_GS(CIN_DT_BF16, CIN_DT_F16);
+  } else {
+    if (out_dtype == CIN_DT_F32) CIN_GS(CIN_DT_F16, CIN_DT_F32);
+    else if (out_dtype == CIN_DT_BF16) CIN_GS(CIN_DT_F16, CIN_DT_BF16);
+    else CIN_GS(CIN_DT_F16, CIN_DT_F16);
+  }
+#undef CIN_GS
+  return cin_check_launch("moe_gather_sum");
+}
+
+int cin_moe_combine(const float* y, int64_t sym, const void* scores, int s_dtype, int64_t ssm,
+                    const int32_t* inv, int64_t T, int64_t k, int64_t A, int64_t N, float* out,
+                    int64_t som, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(s_dtype), "moe_combine: unsupported score dtype %d", s_dtype);
+  CIN_CHECK_ARG(T >= 0 && k >= 1 && k <= kMaxTopK && A >= 0 && N >= 0,
+                "moe_combine: need k in [1, %d] and non-negative sizes", kMaxTopK);
+  if (T == 0 || N == 0) return CIN_OK;
+  CIN_CHECK_ARG(y && scores && inv && out && sym >= N && som >= N && ssm >= k,
+                "moe_combine: bad pointers or strides");
+  CIN_CHECK_ARG(cdiv(T * 64, kRT) < ((int64_t)1 << 31), "moe_combine: grid too large");
+  const unsigned grid = (unsigned)cdiv(T * 64, kRT);  // one wave per token
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (s_dtype == CIN_DT_F32)
+    hipLaunchKernelGGL((k_moe_combine<CIN_DT_F32>), grid, kRT, 0, s, y, sym, scores, ssm, inv, T, (int)k, A, N, out, som);
+  else if (s_dtype == CIN_DT_BF16)
+    hipLaunchKernelGGL((k_moe_combine<CIN_DT_BF16>), grid, kRT, 0, s, y, sym, scores, ssm, inv, T, (int)k, A, N, out, som);
+  else
+    hipLaunchKernelGGL((k_moe_combine<CIN_DT_F16>), grid, kRT, 0, s, y, sym, scores, ssm, inv, T, (int)k, A, N, out, som);
+  return cin_check_launch("moe_combine");
+}
+
+int cin_moe_combine_backward(const float* dout, int64_t sdm, const float* y, int64_t sym,
+                             const void* scores, int s_dtype, int64_t ssm, const int64_t* perm,
+                             const int32_t* inv, int64_t T, int64_t k, int64_t A, int64_t N,
+                             float* dy, int64_t sdym, float* dscores, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(s_dtype), "moe_combine_backward: unsupported score dtype %d", s_dtype);
+  CIN_CHECK_ARG(T >= 0 && k >= 1 && A >= 0 && N >= 0, "moe_combine_backward: bad sizes");
+  CIN_CHECK_ARG(A <= T * k, "moe_combine_backward: more sorted rows than assignments");
+  CIN_CHECK_ARG(dout && y && scores && perm && inv && dy && dscores, "moe_combine_backward: null pointer");
+  CIN_CHECK_ARG(sdm >= N && sym >= N && sdym >= N && ssm >= k, "moe_combine_backward: bad strides");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (A > 0 && N > 0) {
+    const int64_t work = A * cdiv(N, 4);
+    CIN_CHECK_ARG(cdiv(work, kRT) < ((int64_t)1 << 31), "moe_combine_backward: grid too large");
+    const unsigned grid = (unsigned)cdiv(work, kRT);
+    if (s_dtype == CIN_DT_F32)
+      hipLaunchKernelGGL((k_moe_combine_bwd_rows<CIN_DT_F32>), grid, kRT, 0, s, dout, sdm, scores, ssm, perm, T, (int)k, A, N, dy, sdym);
+    else if (s_dtype == CIN_DT_BF16)
+      hipLaunchKernelGGL((k_moe_combine_bwd_rows<CIN_DT_BF16>), grid, kRT, 0, s, dout, sdm, scores, ssm, perm, T, (int)k, A, N, dy, sdym);
+    else
+      hipLaunchKernelGGL((k_moe_combine_bwd_rows<CIN_DT_F16>), grid, kRT, 0, s, dout, sdm, scores, ssm, perm, T, (int)k, A, N, dy, sdym);
+  }
+  if (T > 0) {
+    const int64_t waves = T * k;
+    CIN_CHECK_ARG(cdiv(waves * 64, kRT) < ((int64_t)1 << 31), "moe_combine_backward: grid too large");
+    hipLaunchKernelGGL(k_moe_combine_bwd_scores, (unsigned)cdiv(waves * 64, kRT), kRT, 0, s, dout, sdm,
+                       y, sym, inv, T, (int)k, A, N, dscores);
+  }
+  return cin_check_launch("moe_combine_backward");
+}
+
+}  // extern "C"

@@ -108,13 +108,17 @@ __device__ inline void quant_vals(const float (&v)[NV], float s, float r, uint32
 // row) own one tile.  Each lane loads NC 16-byte chunks, chunk c of lane i sitting at
 // tile chunk c * LANES + i so every load instruction reads whole 16*LANES-byte runs.
 // A group walks tiles t, t + G, ... keeping U tiles in flight; (row, tile) advance
-// incrementally instead of by division.
-template <int DT, int LANES, int U, bool FULL>
+// incrementally instead of by division.  GATHER: output row r quantizes input row
+// rowmap[r] / rowdiv (the MoE dispatch gather); a map entry that is negative or past
+// src_rows gives a zero row.
+template <int DT, int LANES, int U, bool FULL, bool GATHER = false>
 __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict__ x, int64_t N,
                                                          int64_t sxm, int round_scale,
                                                          uint8_t* __restrict__ q, int64_t sqm,
                                                          float* __restrict__ sc, int64_t ssm,
-                                                         uint32_t nb, uint32_t ntiles) {
+                                                         uint32_t nb, uint32_t ntiles,
+                                                         const int64_t* __restrict__ rowmap = nullptr,
+                                                         int64_t rowdiv = 1, int64_t src_rows = 0) {
   constexpr int ES = DT == CIN_DT_F32 ? 4 : 2;  // input element bytes
   constexpr int EPC = 16 / ES;                   // elements per 16-byte chunk
   constexpr int NC = 128 / (LANES * EPC);        // chunks per lane
@@ -134,8 +138,17 @@ __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict_
     for (int u = 0; u < U; ++u) {
       rows[u] = row;
       cbs[u] = cb;
-      const bool live = tb + (uint32_t)u * G < ntiles;
-      const int64_t base = (int64_t)row * sxm + (int64_t)cb * 128;
+      bool live = tb + (uint32_t)u * G < ntiles;
+      int64_t srow = row;
+      if constexpr (GATHER) {
+        const int64_t m = live ? rowmap[row] : -1;
+        srow = m >= 0 ? m / rowdiv : -1;
+        if (srow < 0 || srow >= src_rows) {
+          srow = 0;
+          live = false;  // loads nothing: the tile quantizes zeros
+        }
+      }
+      const int64_t base = srow * sxm + (int64_t)cb * 128;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int64_t e0 = (int64_t)(c * LANES + li) * EPC;  // element offset in the tile
@@ -213,19 +226,20 @@ __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict_
   }
 }
 
-template <int LANES, int U, bool FULL>
+template <int LANES, int U, bool FULL, bool GATHER = false>
 void launch_rowwise128_t(const void* x, int dt, int64_t N, int64_t sxm, int rs, uint8_t* q,
                          int64_t sqm, float* sc, int64_t ssm, uint32_t nb, uint32_t ntiles,
-                         unsigned grid, hipStream_t st) {
+                         unsigned grid, hipStream_t st, const int64_t* rowmap = nullptr,
+                         int64_t rowdiv = 1, int64_t src_rows = 0) {
   if (dt == CIN_DT_BF16)
-    hipLaunchKernelGGL((k_rowwise128<CIN_DT_BF16, LANES, U, FULL>), grid, kThreads, 0, st, x, N,
-                       sxm, rs, q, sqm, sc, ssm, nb, ntiles);
+    hipLaunchKernelGGL((k_rowwise128<CIN_DT_BF16, LANES, U, FULL, GATHER>), grid, kThreads, 0, st,
+                       x, N, sxm, rs, q, sqm, sc, ssm, nb, ntiles, rowmap, rowdiv, src_rows);
   else if (dt == CIN_DT_F16)
-    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F16, LANES, U, FULL>), grid, kThreads, 0, st, x, N,
-                       sxm, rs, q, sqm, sc, ssm, nb, ntiles);
+    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F16, LANES, U, FULL, GATHER>), grid, kThreads, 0, st,
+                       x, N, sxm, rs, q, sqm, sc, ssm, nb, ntiles, rowmap, rowdiv, src_rows);
   else
-    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F32, LANES, U, FULL>), grid, kThreads, 0, st, x, N,
-                       sxm, rs, q, sqm, sc, ssm, nb, ntiles);
+    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F32, LANES, U, FULL, GATHER>), grid, kThreads, 0, st,
+                       x, N, sxm, rs, q, sqm, sc, ssm, nb, ntiles, rowmap, rowdiv, src_rows);
 }
 
 template <int LANES, int U>
@@ -1351,6 +1365,33 @@ int cin_quant_rowwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
                        round_scale, q, sqm, scales, ssm, nb);
   }
   return cin_check_launch("quant_rowwise");
+}
+
+int cin_moe_gather_quant_rowwise(const void* x, int x_dtype, int64_t src_rows, int64_t N,
+                                 int64_t sxm, const int64_t* rowmap, int64_t rows, int64_t rowdiv,
+                                 int round_scale, uint8_t* q, int64_t sqm, float* scales,
+                                 int64_t ssm, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(x_dtype), "moe_gather_quant: unsupported x dtype %d", x_dtype);
+  CIN_CHECK_ARG(src_rows >= 0 && N >= 0 && rows >= 0 && rowdiv >= 1,
+                "moe_gather_quant: negative shape or row divisor < 1");
+  if (rows == 0 || N == 0) return CIN_OK;
+  CIN_CHECK_ARG(x && rowmap && q && scales, "moe_gather_quant: null pointer");
+  const int64_t nb = cdiv(N, 128);
+  CIN_CHECK_ARG(sqm >= N && ssm >= nb, "moe_gather_quant: output row stride too small");
+  const int es = elem_size(x_dtype);
+  CIN_CHECK_ARG(aligned(x, 16) && (sxm * es) % 16 == 0 && sxm >= N && aligned(q, 8) && sqm % 8 == 0,
+                "moe_gather_quant: x rows must be contiguous and 16-byte aligned, q rows 8-byte aligned");
+  CIN_CHECK_ARG(rows * nb < (int64_t)1 << 31, "moe_gather_quant: too many tiles");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint32_t ntiles = (uint32_t)(rows * nb);
+  const unsigned grid = grid_for(ntiles, kThreads / 8, 16384);
+  if (N % 128 == 0)
+    launch_rowwise128_t<8, 1, true, true>(x, x_dtype, N, sxm, round_scale, q, sqm, scales, ssm,
+                                          (uint32_t)nb, ntiles, grid, s, rowmap, rowdiv, src_rows);
+  else
+    launch_rowwise128_t<8, 1, false, true>(x, x_dtype, N, sxm, round_scale, q, sqm, scales, ssm,
+                                           (uint32_t)nb, ntiles, grid, s, rowmap, rowdiv, src_rows);
+  return cin_check_launch("moe_gather_quant_rowwise");
 }
 
 int cin_quant_blockwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t sxm, int64_t sxn,

@@ -322,6 +322,49 @@ def _(dh, h12):
     return dh.new_empty((dh.shape[0], 2 * dh.shape[1]), dtype=torch.float32)
 
 
+def experts_forward(xq: torch.Tensor, xs: torch.Tensor, w12: torch.Tensor, w3: torch.Tensor,
+                    starts: torch.Tensor, ends: torch.Tensor, h_dtype: torch.dtype):
+    """FP8 SwiGLU experts on 1x128-quantized sorted rows (xq, xs): GEMM(w12), silu(h1) * h2
+    in fp32 cast to h_dtype and quantized in the same pass, GEMM(w3), fp32 out (reference
+    GroupedExperts.forward, src/layers.py:71-75).  Returns (out [T, D] fp32, saved tensors for
+    experts_backward).  Rows outside every expert range are zero."""
+    E, H2, D = w12.shape
+    H = H2 // 2
+    w12f = w12 if w12.dtype == torch.float32 else w12.float()
+    w12q, w12qt, w12s = quantize_fp8_blockwise_t(w12f.reshape(E * H2, D))
+    h12 = fp8_grouped_gemm(xq, xs, w12q.view(E, H2, D), w12s.view(E, H2 // 128, -1),
+                           starts, ends, out_dtype=torch.bfloat16, zero_uncovered=True)
+    hq, hs = silu_mul_quantize_fp8(h12, out_dtype=h_dtype)
+    w3f = w3 if w3.dtype == torch.float32 else w3.float()
+    w3q, w3qt, w3s = quantize_fp8_blockwise_t(w3f.reshape(E * D, H))
+    out = fp8_grouped_gemm(hq, hs, w3q.view(E, D, H), w3s.view(E, D // 128, -1), starts, ends,
+                           out_dtype=torch.float32, zero_uncovered=True)
+    return out, (xq, xs, w12qt, w12s, h12, hq, hs, w3qt, w3s, starts, ends)
+
+
+def experts_backward(saved, grad_out: torch.Tensor, dx_dtype: torch.dtype):
+    """Backward of experts_forward: the FP8MatmulFunction.backward recipe (reference
+    src/kernels.py:763-794) applied per expert to both GEMMs.  Returns (dx [T, D] in dx_dtype
+    (bf16 or fp32; its bf16 store is the RNE of the fp32 value), dw12 fp32, dw3 fp32)."""
+    xq, xs, w12qt, w12s, h12, hq, hs, w3qt, w3s, starts, ends = saved
+    D = xq.shape[1]
+    H = hq.shape[1]
+    g = grad_out.contiguous()
+    gq, gs, gqt, gst = quantize_fp8_dual_grouped(g, starts, ends)
+    dh = fp8_grouped_dgrad(gq, gs, w3qt, w3s, starts, ends, D, out_dtype=torch.float32,
+                           zero_uncovered=True)
+    hbt, hblk = requantize_grouped_t(hq, hs, starts, ends)
+    dw3 = fp8_grouped_wgrad(gqt, gst, hbt, hblk, starts, ends, g.shape[0])
+    # silu(h1) * h2 in fp32 (the forward's cast to the input dtype passes the gradient)
+    dh12 = swiglu_backward(dh, h12)
+    dq, ds, dqt, dst = quantize_fp8_dual_grouped(dh12, starts, ends)
+    dx = fp8_grouped_dgrad(dq, ds, w12qt, w12s, starts, ends, 2 * H, out_dtype=dx_dtype,
+                           zero_uncovered=True)
+    xbt, xblk = requantize_grouped_t(xq, xs, starts, ends)
+    dw12 = fp8_grouped_wgrad(dqt, dst, xbt, xblk, starts, ends, g.shape[0])
+    return dx, dw12, dw3
+
+
 class FP8GroupedExpertsFunction(torch.autograd.Function):
     """SwiGLU experts in FP8: out = W3_e (silu(h1) * h2), [h1 h2] = W12_e x for each expert's
     rows (reference GroupedExperts.forward, src/layers.py:56-87: GEMM(w12), silu * mul in
@@ -333,44 +376,19 @@ class FP8GroupedExpertsFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, sorted_x, w12, w3, expert_starts, expert_ends):
-        E, H2, D = w12.shape
-        H = H2 // 2
         starts, ends = _ranges(expert_starts, expert_ends)
         xq, xs = quantize_fp8_rowwise(sorted_x)
-        w12f = w12 if w12.dtype == torch.float32 else w12.float()
-        w12q, w12qt, w12s = quantize_fp8_blockwise_t(w12f.reshape(E * H2, D))
-        h12 = fp8_grouped_gemm(xq, xs, w12q.view(E, H2, D), w12s.view(E, H2 // 128, -1),
-                               starts, ends, out_dtype=torch.bfloat16, zero_uncovered=True)
-        hq, hs = silu_mul_quantize_fp8(h12, out_dtype=sorted_x.dtype)
-        w3f = w3 if w3.dtype == torch.float32 else w3.float()
-        w3q, w3qt, w3s = quantize_fp8_blockwise_t(w3f.reshape(E * D, H))
-        out = fp8_grouped_gemm(hq, hs, w3q.view(E, D, H), w3s.view(E, D // 128, -1), starts, ends,
-                               out_dtype=torch.float32, zero_uncovered=True)
-        ctx.save_for_backward(xq, xs, w12qt, w12s, h12, hq, hs, w3qt, w3s, starts, ends)
-        ctx.dims = (E, H, D)
+        out, saved = experts_forward(xq, xs, w12, w3, starts, ends, sorted_x.dtype)
+        ctx.save_for_backward(*saved)
         ctx.x_dtype = sorted_x.dtype
         ctx.w_dtypes = (w12.dtype, w3.dtype)
         return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        xq, xs, w12qt, w12s, h12, hq, hs, w3qt, w3s, starts, ends = ctx.saved_tensors
-        E, H, D = ctx.dims
-        g = grad_out.contiguous()
-        gq, gs, gqt, gst = quantize_fp8_dual_grouped(g, starts, ends)
-        dh = fp8_grouped_dgrad(gq, gs, w3qt, w3s, starts, ends, D, out_dtype=torch.float32,
-                               zero_uncovered=True)
-        hbt, hblk = requantize_grouped_t(hq, hs, starts, ends)
-        dw3 = fp8_grouped_wgrad(gqt, gst, hbt, hblk, starts, ends, g.shape[0])
-        # silu(h1) * h2 in fp32 (the forward's cast to the input dtype passes the gradient)
-        dh12 = swiglu_backward(dh, h12)
-        dq, ds, dqt, dst = quantize_fp8_dual_grouped(dh12, starts, ends)
         # dx straight in the input dtype: the GEMM's bf16 store is the RNE of its fp32 value
         dx_dtype = ctx.x_dtype if ctx.x_dtype in (torch.bfloat16, torch.float32) else torch.float32
-        dx = fp8_grouped_dgrad(dq, ds, w12qt, w12s, starts, ends, 2 * H, out_dtype=dx_dtype,
-                               zero_uncovered=True)
-        xbt, xblk = requantize_grouped_t(xq, xs, starts, ends)
-        dw12 = fp8_grouped_wgrad(dqt, dst, xbt, xblk, starts, ends, g.shape[0])
+        dx, dw12, dw3 = experts_backward(ctx.saved_tensors, grad_out, dx_dtype)
         return (dx.to(ctx.x_dtype), dw12.to(ctx.w_dtypes[0]), dw3.to(ctx.w_dtypes[1]), None, None)
 
 

@@ -263,6 +263,73 @@ int cin_zero_rows_outside_ranges(void* C, int64_t ldc_bytes, int64_t row_bytes, 
                                  const int64_t* starts, const int64_t* ends, int64_t E,
                                  void* stream);
 
+/* ---------------------------- MoE dispatch / combine ---------------------------- */
+
+/*
+ * Device-side routing: a stable counting sort of the flattened top-k expert ids.
+ * Replaces the sort / bincount / cumsum / .item() of MoE.forward (reference
+ * src/layers.py:133-148).
+ *   idx       [T, k] int64 expert ids (contiguous); ids outside [0, E) are dropped
+ *   perm      [T*k] int64: perm[r] = t*k + j of the assignment at sorted position r
+ *             (the reference's sort_order, in stable order); -1 past the last kept one
+ *   inv       [T*k] int32: sorted position of assignment t*k + j, -1 if dropped
+ *   counts, starts, ends  [E] int64 expert row ranges (bincount, cumsum)
+ *   workspace int32, at least cin_moe_route_workspace(T, k, E) elements
+ * E <= 4096, T*k < 2^31.
+ */
+int cin_moe_route(const int64_t* idx, int64_t T, int64_t k, int64_t E, int64_t* perm, int32_t* inv,
+                  int64_t* counts, int64_t* starts, int64_t* ends, int32_t* workspace,
+                  int64_t workspace_elems, void* stream);
+int cin_moe_route_workspace(int64_t T, int64_t k, int64_t E);
+
+/*
+ * Dispatch gather fused into the 1x128 row-wise quantizer: row r of q / scales is
+ * quantize_fp8_rowwise(x[rowmap[r] / rowdiv]) bit for bit; a negative or out-of-range map
+ * entry gives a zero row.  Replaces sorted_x = flat_x[token_indices] (reference
+ * src/layers.py:139-141) followed by the activation quantization of the grouped GEMM
+ * (src/kernels.py:178-216): the gathered bf16 rows are never written.
+ *   x [src_rows, N], rows 16-byte aligned (sxm elements apart); rowmap [rows] int64
+ *   (perm from cin_moe_route, rowdiv = k); q [rows, N] (8-byte aligned rows),
+ *   scales [rows, ceil(N/128)] fp32.
+ */
+int cin_moe_gather_quant_rowwise(const void* x, int x_dtype, int64_t src_rows, int64_t N,
+                                 int64_t sxm, const int64_t* rowmap, int64_t rows, int64_t rowdiv,
+                                 int round_scale, uint8_t* q, int64_t sqm, float* scales,
+                                 int64_t ssm, void* stream);
+
+/*
+ * Backward of the dispatch gather: out[t] = sum over token t's sorted positions r
+ * (increasing r, fp32 sums) of g[r]; the gradient of flat_x[token_indices] (reference
+ * src/layers.py:140).  g [A, N] (g_dtype, row stride sgm), inv [T*k] from cin_moe_route,
+ * out [T, N] (out_dtype, row stride som).  k <= 16.
+ */
+int cin_moe_gather_sum(const void* g, int g_dtype, int64_t sgm, const int32_t* inv, int64_t T,
+                       int64_t k, int64_t A, int64_t N, void* out, int out_dtype, int64_t som,
+                       void* stream);
+
+/*
+ * Weighted combine: out[t] = sum over token t's sorted positions r, in increasing r, of
+ * y[r] * score[t, slot(r)], fp32 (product and sum each rounded), i.e. the reference's
+ * weighted_out = sorted_out * sorted_scores[:, None] followed by a sequential
+ * routed_out.scatter_add_ (src/layers.py:151-154).  y [A, N] fp32, scores [T, k]
+ * (s_dtype, row stride ssm), out [T, N] fp32.  k <= 16.
+ */
+int cin_moe_combine(const float* y, int64_t sym, const void* scores, int s_dtype, int64_t ssm,
+                    const int32_t* inv, int64_t T, int64_t k, int64_t A, int64_t N, float* out,
+                    int64_t som, void* stream);
+
+/*
+ * Backward of cin_moe_combine: dy[r] = dout[t] * score[t, j] for the assignment t*k + j at
+ * sorted position r (zero rows where perm is -1), and dscores[t, j] = sum_c dout[t, c] *
+ * y[inv[t*k + j], c] (fp32, 0 for dropped assignments); the autograd of reference
+ * src/layers.py:151-154.  dout [T, N] fp32, y [A, N] fp32, dy [A, N] fp32, dscores [T, k]
+ * fp32 contiguous.
+ */
+int cin_moe_combine_backward(const float* dout, int64_t sdm, const float* y, int64_t sym,
+                             const void* scores, int s_dtype, int64_t ssm, const int64_t* perm,
+                             const int32_t* inv, int64_t T, int64_t k, int64_t A, int64_t N,
+                             float* dy, int64_t sdym, float* dscores, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

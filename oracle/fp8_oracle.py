@@ -24,6 +24,8 @@ Functions and the reference lines they restate:
   gemm_ref                src/kernels.py:618-664 as dequantize-then-fp32-matmul
   fp8_linear_ref          src/kernels.py:739-794 (FP8MatmulFunction fwd/bwd)
   grouped_gemm_ref        src/layers.py:79-86 loop semantics on FP8 operands
+  moe_dispatch_ref        src/layers.py:133-148 (sort, token_indices, bincount, cumsum)
+  moe_combine_ref         src/layers.py:151-154 (gated scatter_add_ of sorted rows)
 """
 from __future__ import annotations
 
@@ -347,6 +349,42 @@ def grouped_experts_ref(x: torch.Tensor, w12: torch.Tensor, w3: torch.Tensor, st
             r["dx"][s:t] = d_row[s:t] @ w12d[e]
             r["dw12"][e] = colq(dh12[s:t]).t() @ blkq(xd[s:t])
     return r
+
+
+# ---------------------------------------------------------------------------
+# MoE dispatch / combine (reference src/layers.py:126-157)
+# ---------------------------------------------------------------------------
+def moe_dispatch_ref(top_idx: torch.Tensor, n_experts: int):
+    """The reference's routing bookkeeping (src/layers.py:133-148) on the CPU:
+    expanded_idx = top_idx.view(-1); sorted_idx, sort_order = expanded_idx.sort();
+    token_indices = sort_order // top_k; expert_counts = bincount; expert_ends = cumsum;
+    expert_starts = [0, ends[:-1]].  The sort is the stable one (the reference's torch.sort
+    may order equal ids differently; the build's device sort is stable).
+    Returns (sort_order, token_indices, counts, starts, ends), all int64."""
+    k = top_idx.shape[1]
+    expanded_idx = top_idx.reshape(-1).to(torch.int64)
+    _, sort_order = torch.sort(expanded_idx, stable=True)
+    token_indices = sort_order // k
+    counts = torch.bincount(expanded_idx, minlength=n_experts)
+    ends = counts.cumsum(0)
+    starts = torch.cat([torch.zeros(1, dtype=torch.long), ends[:-1]])
+    return sort_order, token_indices, counts, starts, ends
+
+
+def moe_combine_ref(sorted_out: torch.Tensor, top_scores: torch.Tensor, sort_order: torch.Tensor,
+                    n_tokens: int) -> torch.Tensor:
+    """The reference's gated combine (src/layers.py:137,151-154): sorted_scores =
+    top_scores.view(-1)[sort_order]; weighted_out = sorted_out * sorted_scores[:, None];
+    routed_out = zeros(n_tokens, d, dtype=weighted_out.dtype).scatter_add_(0,
+    token_indices[:, None].expand_as(weighted_out), weighted_out).  On the CPU, scatter_add_
+    adds the rows in index order, i.e. each token's terms in increasing sorted position."""
+    k = top_scores.shape[1]
+    sorted_scores = top_scores.reshape(-1)[sort_order]
+    token_indices = sort_order // k
+    weighted_out = sorted_out * sorted_scores[:, None]
+    out = torch.zeros(n_tokens, sorted_out.shape[1], dtype=weighted_out.dtype)
+    out.scatter_add_(0, token_indices.unsqueeze(1).expand_as(weighted_out), weighted_out)
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -51,6 +51,12 @@ def test_no_rpath_to_a_second_hip_runtime():
     ("cin_gemm_fp8_bs", (None, 32, None, 1, 1, None, 32, None, 1, 1, 4, 4, 24, None, 0, 4, None)),
     ("cin_gemm_fp8_bs", (None, 32, None, 1, 1, None, 32, None, 1, 1, 4, 4, 32, None, 5, 4, None)),
     ("cin_dequant", (None, 4, 4, 4, 1, None, 1, 1, 1, 128, None, 2, 4, None)),            # fp16 out
+    ("cin_moe_route", (None, 16, 2, 0, None, None, None, None, None, None, 0, None)),        # E = 0
+    ("cin_moe_route", (None, 16, 2, 5000, None, None, None, None, None, None, 0, None)),     # E > 4096
+    ("cin_moe_route", (None, 16, 2, 8, None, None, None, None, None, None, 0, None)),        # null ptrs
+    ("cin_moe_gather_sum", (None, 1, 8, None, 4, 17, 68, 8, None, 1, 8, None)),              # k > 16
+    ("cin_moe_combine", (None, 8, None, 7, 2, None, 4, 2, 8, 8, None, 8, None)),             # bad dtype
+    ("cin_moe_gather_quant_rowwise", (None, 0, 4, 256, 256, None, 8, 0, 0, None, 256, None, 2, None)),
 ])
 def test_invalid_arguments_rejected_without_gpu(call):
     name, args = call
@@ -65,3 +71,12 @@ def test_empty_shapes_are_noops():
     # M == 0: nothing to do, no device touched
     assert lib.cin_quant_rowwise(None, 0, 0, 128, 128, 1, 128, 0, None, 128, None, 1, None) == 0
     assert lib.cin_gemm_fp8_bs(None, 32, None, 1, 1, None, 32, None, 1, 1, 0, 4, 32, None, 0, 4, None) == 0
+    assert lib.cin_moe_gather_sum(None, 1, 8, None, 0, 2, 0, 8, None, 1, 8, None) == 0
+    assert lib.cin_moe_combine(None, 8, None, 1, 2, None, 0, 2, 0, 8, None, 8, None) == 0
+
+
+def test_moe_route_workspace_size():
+    lib = _lib.load()
+    assert lib.cin_moe_route_workspace(16384, 8, 32) == 64 * 32   # 2048 assignments per block
+    assert lib.cin_moe_route_workspace(1, 1, 4) == 4
+    assert lib.cin_moe_route_workspace(0, 8, 4) == 0

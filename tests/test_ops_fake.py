@@ -13,12 +13,13 @@ import torch
 from torch._subclasses.fake_tensor import FakeTensorMode
 from torch.fx.experimental.proxy_tensor import make_fx
 
-from cinnamon_amd import kernels, layers
+from cinnamon_amd import kernels, layers, moe
 
 OPS = ["quant_rowwise", "quant_blockwise", "quant_blockwise_t", "quant_dual", "requant_row_to_block",
        "dequant_rowwise", "dequant", "gemm_fp8_bs", "transpose_u8", "grouped_gemm_f16",
        "grouped_gemm_fp8", "quant_dual_grouped", "requant_row_to_block_grouped",
-       "grouped_wgrad_fp8", "grouped_dgrad_fp8", "silu_mul_quant_rowwise", "swiglu_backward"]
+       "grouped_wgrad_fp8", "grouped_dgrad_fp8", "silu_mul_quant_rowwise", "swiglu_backward",
+       "moe_route", "moe_gather_quant_rowwise", "moe_gather_sum", "moe_combine", "moe_combine_backward"]
 F8, F32, BF16 = torch.float8_e4m3fn, torch.float32, torch.bfloat16
 
 
@@ -157,4 +158,39 @@ def test_grouped_experts_forward_backward_traces_to_operators():
     for name in ["grouped_gemm_fp8", "silu_mul_quant_rowwise", "quant_dual_grouped",
                  "grouped_dgrad_fp8", "requant_row_to_block_grouped", "grouped_wgrad_fp8",
                  "swiglu_backward"]:
+        assert any(f"cinnamon_amd.{name}" in o for o in ops), (name, ops)
+
+
+def test_moe_dispatch_shape_functions_and_trace():
+    T, k, E, D, H = 600, 4, 8, 256, 256
+
+    def step(x, w12, w3, top_idx, scores, dout):
+        perm, inv, counts, starts, ends = moe.moe_route(top_idx, E)
+        ctx = _Ctx()
+        ys = moe.FP8RoutedExpertsFunction.forward(ctx, x, w12, w3, perm, inv, starts, ends, k)
+        out = moe.moe_combine(ys, scores, inv)
+        dys, dsc = moe.moe_combine_backward(dout, ys, scores, perm, inv)
+        dx, dw12, dw3, *_ = moe.FP8RoutedExpertsFunction.backward(ctx, dys)
+        return perm, inv, counts, ys, out, dys, dsc, dx, dw12, dw3
+
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        x = torch.empty(T, D, dtype=BF16, device="cuda")
+        w12 = torch.empty(E, 2 * H, D, dtype=F32, device="cuda")
+        w3 = torch.empty(E, D, H, dtype=F32, device="cuda")
+        top_idx = torch.empty(T, k, dtype=torch.int64, device="cuda")
+        scores = torch.empty(T, k, dtype=BF16, device="cuda")
+        dout = torch.empty(T, D, dtype=F32, device="cuda")
+        gm = make_fx(step, tracing_mode="fake")(x, w12, w3, top_idx, scores, dout)
+        perm, inv, counts, ys, out, dys, dsc, dx, dw12, dw3 = step(x, w12, w3, top_idx, scores, dout)
+        assert _meta(perm) == ((T * k,), torch.int64, "cuda") and _meta(inv) == ((T * k,), torch.int32, "cuda")
+        assert _meta(counts) == ((E,), torch.int64, "cuda")
+        assert _meta(ys) == ((T * k, D), F32, "cuda") and _meta(out) == ((T, D), F32, "cuda")
+        assert _meta(dys) == ((T * k, D), F32, "cuda") and _meta(dsc) == ((T, k), F32, "cuda")
+        assert _meta(dx) == ((T, D), BF16, "cuda") and dw12.shape == (E, 2 * H, D) and dw3.shape == (E, D, H)
+        q, s = moe.moe_gather_quantize(x, perm, k)
+        assert _meta(q) == ((T * k, D), F8, "cuda") and _meta(s) == ((T * k, 2), F32, "cuda")
+        assert _meta(moe.moe_gather_sum(dys, inv, k, BF16)) == ((T, D), BF16, "cuda")
+    ops = _op_targets(gm)
+    for name in ["moe_route", "moe_gather_quant_rowwise", "moe_combine", "moe_combine_backward",
+                 "moe_gather_sum", "grouped_gemm_fp8", "grouped_wgrad_fp8"]:
         assert any(f"cinnamon_amd.{name}" in o for o in ops), (name, ops)
