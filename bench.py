@@ -37,7 +37,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "moe_gateup", "moe_down",
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
-                                      "moe_wgrad", "moe_dgrad", "moe_layer", "copy"], default=None,
+                                      "moe_wgrad", "moe_dgrad", "moe_layer", "moe_route",
+                                      "moe_gather", "moe_combine", "copy"], default=None,
                    help="run only one kernel in a loop (for profiler runs)")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the config-3 (MoE) and config-4 (backward) component timings")
@@ -202,7 +203,7 @@ def moe_setup(dev):
     w12q, w12s = kernels.quantize_fp8_blockwise(w12)
     w3q, w3s = kernels.quantize_fp8_blockwise(w3)
     del w12, w3
-    return dict(E=E, D=D, H=H, A=A, x=x, h=h, starts=starts, ends=ends, counts=counts,
+    return dict(E=E, D=D, H=H, A=A, T=T, topk=topk, sel=sel, x=x, h=h, starts=starts, ends=ends, counts=counts,
                 w12q=w12q.view(E, 2 * H, D), w12s=w12s.view(E, 2 * H // 128, D // 128),
                 w3q=w3q.view(E, D, H), w3s=w3s.view(E, D // 128, H // 128))
 
@@ -341,6 +342,52 @@ def main():
         with torch.no_grad():
             ml(ml_x, moe["starts"], moe["ends"])
 
+    # config 3 dispatch and combine around the experts (cinnamon_amd.moe) against the
+    # reference's torch formulation of the same block (src/layers.py:133-154)
+    md = None
+    if full or args.only in ("moe_route", "moe_gather", "moe_combine"):
+        from cinnamon_amd import moe as moe_ops
+        if moe is None:
+            moe = moe_setup(dev)
+        g4 = torch.Generator(device=dev).manual_seed(35)
+        T3, k3 = moe["T"], moe["topk"]
+        sc3 = torch.rand(T3, k3, device=dev, generator=g4)
+        sc3 = (sc3 / sc3.sum(-1, keepdim=True)).to(torch.bfloat16)
+        md = dict(x=moe["x"][:T3], sel=moe["sel"], scores=sc3,
+                  ys=torch.randn(moe["A"], moe["D"], device=dev, generator=g4))
+        md["perm"], md["inv"], *_ = moe_ops.moe_route(md["sel"], moe["E"])
+
+    def moe_route(i):
+        moe_ops.moe_route(md["sel"], moe["E"])
+
+    def moe_gather(i):
+        moe_ops.moe_gather_quantize(md["x"], md["perm"], moe["topk"], inv=md["inv"])
+
+    def moe_combine(i):
+        moe_ops.moe_combine(md["ys"], md["scores"], md["inv"])
+
+    def moe_dispatch_fused(i):
+        perm, inv, *_ = moe_ops.moe_route(md["sel"], moe["E"])
+        moe_ops.moe_gather_quantize(md["x"], perm, moe["topk"], inv=inv)
+
+    def moe_dispatch_torch(i):
+        k = moe["topk"]
+        _, order = md["sel"].reshape(-1).sort()
+        tok = order // k
+        sorted_x = md["x"][tok]
+        cnt = torch.bincount(md["sel"].reshape(-1), minlength=moe["E"])
+        cnt.cumsum(0)
+        int(cnt.max().item())
+        kernels.quantize_fp8_rowwise(sorted_x)
+
+    def moe_combine_torch(i):
+        k = moe["topk"]
+        _, order = md["sel"].reshape(-1).sort()
+        tok = order // k
+        w = md["ys"] * md["scores"].reshape(-1)[order][:, None]
+        torch.zeros(moe["T"], moe["D"], device=dev, dtype=w.dtype).scatter_add_(
+            0, tok.unsqueeze(1).expand_as(w), w)
+
     if full or args.only in ("dual_quant", "requant", "dgrad", "wgrad"):
         bwd = bwd_setup(dev, xs[0], ws[0])
         gq, gs, gqt, gst = kernels.quantize_fp8_dual(bwd["dy"])
@@ -373,7 +420,8 @@ def main():
               "moe_gateup": moe_gateup, "moe_down": moe_down, "dual_quant": dual_quant,
               "requant": requant, "dgrad": dgrad, "wgrad": wgrad, "moe_dual": moe_dual,
               "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad,
-              "moe_layer": moe_layer}[args.only]
+              "moe_layer": moe_layer, "moe_route": moe_route, "moe_gather": moe_gather,
+              "moe_combine": moe_combine}[args.only]
         loop = time_loop if args.only == "step" else kernel_loop
         us = loop(fn, args.steps, args.warmup)
         print(json.dumps({"only": args.only, "us_per_call": us}))
@@ -459,6 +507,31 @@ def main():
             "forward_ms": round(f_ms, 2), "forward_backward_ms": round(fb_ms, 2),
             "tokens_per_s_fwd_bwd": round(moe["A"] / (fb_ms * 1e-3) / 8),
             "gemm_tflops_fwd_bwd": round(3 * fl / (fb_ms * 1e-3) / 1e12, 1),
+        }
+    if md is not None:
+        A, D, T3 = moe["A"], moe["D"], moe["T"]
+        r_us = kernel_loop(moe_route, 20, 3)
+        g_us = kernel_loop(moe_gather, 10, 2)
+        c_us = kernel_loop(moe_combine, 5, 1)
+        fused_us = time_loop(moe_dispatch_fused, 5, 1)
+        torch_us = time_loop(moe_dispatch_torch, 5, 1)
+        ctorch_us = time_loop(moe_combine_torch, 3, 1)
+        # bytes: the gather reads each token row once (its k re-reads hit the caches) and
+        # writes A code rows + scales; the combine reads the fp32 sorted rows and writes the
+        # fp32 token rows
+        g_bytes = T3 * D * 2 + A * D + A * (D // 128) * 4
+        c_bytes = A * D * 4 + T3 * D * 4 + A * 2 + A * 4
+        out["components"]["config3_moe_dispatch"] = {
+            "what": "cinnamon_amd.moe on the config-3 routing (16384 tokens, top-8, 32 Zipf experts, "
+                    "d 7168) against the reference's torch formulation on the same GPU",
+            "route_us": round(r_us, 1),
+            "gather_quant_us": round(g_us, 1), "gather_quant_gbps": round(g_bytes / g_us / 1e3, 1),
+            "gather_quant_frac_of_hbm": round(g_bytes / g_us / 1e3 / PEAK_HBM_GBPS, 4),
+            "dispatch_us": round(fused_us, 1),
+            "torch_sort_gather_bincount_item_quant_us": round(torch_us, 1),
+            "combine_us": round(c_us, 1), "combine_gbps": round(c_bytes / c_us / 1e3, 1),
+            "combine_frac_of_hbm": round(c_bytes / c_us / 1e3 / PEAK_HBM_GBPS, 4),
+            "torch_sort_mul_scatter_add_us": round(ctorch_us, 1),
         }
     if mb is not None:
         A, D, H = moe["A"], moe["D"], moe["H"]

@@ -26,10 +26,11 @@ using namespace cin;
 namespace {
 
 constexpr int kRT = 256;           // threads of the route kernels
-constexpr int kRounds = 8;         // assignments per thread in a route block
+constexpr int kRounds = 4;         // assignments per thread in a route block
 constexpr int kChunk = kRT * kRounds;
 constexpr int kMaxExperts = 4096;  // LDS counters of the route kernels
 constexpr int kMaxTopK = 16;       // positions a combine thread sorts in registers
+constexpr int kStage = 8192;       // int32 entries of the count matrix staged in LDS by the scan
 
 inline bool valid_dtype(int dt) { return dt == CIN_DT_BF16 || dt == CIN_DT_F32 || dt == CIN_DT_F16; }
 
@@ -66,27 +67,43 @@ __global__ __launch_bounds__(kRT) void k_route_hist(const int64_t* __restrict__ 
 }
 
 // One workgroup: per-expert totals, expert ranges, and each (block, expert)'s first
-// sorted position; the unused tail of perm (dropped ids) gets -1.
-__global__ __launch_bounds__(kRT) void k_route_scan(int32_t* __restrict__ blockcounts,
+// sorted position (base = starts[e] + the expert's assignments in earlier blocks); the
+// unused tail of perm (dropped ids) gets -1.  The [nblocks, E] count matrix is staged
+// through LDS in row chunks (coalesced loads and stores); a thread owns an expert's
+// running sum.
+__global__ __launch_bounds__(kRT) void k_route_scan(const int32_t* __restrict__ blockcounts,
                                                     int32_t nblocks, int32_t E, int64_t A,
+                                                    int32_t* __restrict__ blockbase,
                                                     int64_t* __restrict__ counts,
                                                     int64_t* __restrict__ starts,
                                                     int64_t* __restrict__ ends,
                                                     int64_t* __restrict__ perm) {
+  __shared__ int32_t stage[kStage];
   __shared__ int64_t tot[kMaxExperts];
   __shared__ int64_t total_s;
-  for (int e = threadIdx.x; e < E; e += kRT) {
-    int64_t run = 0;
-    for (int b = 0; b < nblocks; ++b) {
-      const int64_t j = (int64_t)b * E + e;
-      const int32_t c = blockcounts[j];
-      blockcounts[j] = (int32_t)run;  // becomes the block's offset within the expert
-      run += c;
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += kRT) tot[e] = 0;
+  const int rows_per = kStage / E >= 1 ? kStage / E : 1;  // E <= kMaxExperts <= kStage
+  for (int b0 = 0; b0 < nblocks; b0 += rows_per) {
+    const int nb = nblocks - b0 < rows_per ? nblocks - b0 : rows_per;
+    const int64_t n = (int64_t)nb * E;
+    __syncthreads();  // the previous chunk's stores have read stage[]
+    for (int64_t j = tid; j < n; j += kRT) stage[j] = blockcounts[(int64_t)b0 * E + j];
+    __syncthreads();
+    for (int e = tid; e < E; e += kRT) {
+      int64_t run = tot[e];
+      for (int b = 0; b < nb; ++b) {
+        const int32_t c = stage[b * E + e];
+        stage[b * E + e] = (int32_t)run;
+        run += c;
+      }
+      tot[e] = run;
     }
-    tot[e] = run;
+    __syncthreads();
+    for (int64_t j = tid; j < n; j += kRT) blockbase[(int64_t)b0 * E + j] = stage[j];
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     int64_t s = 0;
     for (int e = 0; e < E; ++e) {
       const int64_t c = tot[e];
@@ -96,60 +113,62 @@ __global__ __launch_bounds__(kRT) void k_route_scan(int32_t* __restrict__ blockc
     total_s = s;
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += kRT) {
+  for (int e = tid; e < E; e += kRT) {
     const int64_t st = tot[e];
     const int64_t en = e + 1 < E ? tot[e + 1] : total_s;
     starts[e] = st;
     ends[e] = en;
     counts[e] = en - st;
   }
-  for (int64_t j = threadIdx.x; j < (int64_t)nblocks * E; j += kRT)
-    blockcounts[j] += (int32_t)tot[j % E];
-  for (int64_t r = total_s + threadIdx.x; r < A; r += kRT) perm[r] = -1;
+  // the two barriers above order the chunk stores before these updates
+  for (int64_t j = tid; j < (int64_t)nblocks * E; j += kRT) blockbase[j] += (int32_t)tot[j % E];
+  for (int64_t r = total_s + tid; r < A; r += kRT) perm[r] = -1;
 }
 
 // Stable scatter: an assignment's sorted position is its block's first position for its
-// expert, plus the assignments of that expert earlier in the block.  A block walks its
-// assignments in rounds of 256 in index order; within a round a thread counts the equal
-// ids of lower threads.
-__global__ __launch_bounds__(kRT) void k_route_scatter(const int64_t* __restrict__ idx, int64_t A,
-                                                       int32_t E,
-                                                       const int32_t* __restrict__ blockbase,
-                                                       int64_t* __restrict__ perm,
-                                                       int32_t* __restrict__ inv) {
+// expert, plus the assignments of that expert earlier in the block.  One wave per block
+// walks the block's assignments in rounds of 64 in index order.  In a round, 12 ballots
+// over the bits of the id (E <= 4096) give each lane the mask of lanes holding the same
+// id; its rank is the number of those below it, and the group's highest lane advances
+// the expert's LDS counter (its read by the group precedes the update in program order).
+constexpr int kIdBits = 12;
+static_assert((1 << kIdBits) >= kMaxExperts, "ids must fit the ballot bits");
+__global__ __launch_bounds__(64) void k_route_scatter(const int64_t* __restrict__ idx, int64_t A,
+                                                      int32_t E,
+                                                      const int32_t* __restrict__ blockbase,
+                                                      int64_t* __restrict__ perm,
+                                                      int32_t* __restrict__ inv) {
   __shared__ int running[kMaxExperts];
-  __shared__ int se[kRT];
-  const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += kRT) running[e] = 0;
+  const int lane = threadIdx.x;
+  for (int e = lane; e < E; e += 64) running[e] = 0;
+  __syncthreads();
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   const int64_t b0 = (int64_t)blockIdx.x * kChunk;
-  for (int r = 0; r < kRounds; ++r) {
-    const int64_t i = b0 + r * kRT + tid;
+  for (int r = 0; r < kChunk / 64; ++r) {
+    const int64_t i = b0 + r * 64 + lane;
     int e = -1;
     if (i < A) {
       const int64_t v = idx[i];
       e = (v >= 0 && v < E) ? (int)v : -1;
     }
-    se[tid] = e;
-    __syncthreads();  // also orders the previous round's running[] updates
-    int rank = 0;
-    bool last = true;
+    uint64_t peers = __ballot(e >= 0);
+#pragma unroll
+    for (int b = 0; b < kIdBits; ++b) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
     if (e >= 0) {
-      for (int j = 0; j < tid; ++j) rank += se[j] == e;
-      for (int j = tid + 1; j < kRT; ++j)
-        if (se[j] == e) {
-          last = false;
-          break;
-        }
+      const int rank = __popcll(peers & below);
       const int64_t pos = (int64_t)blockbase[(int64_t)blockIdx.x * E + e] + running[e] + rank;
       if (pos >= 0 && pos < A) {
         perm[pos] = i;
         inv[i] = (int32_t)pos;
       }
+      if (lane == 63 - __clzll(peers)) running[e] += __popcll(peers);
     } else if (i < A) {
       inv[i] = -1;
     }
-    __syncthreads();  // every thread has read running[] for this round
-    if (e >= 0 && last) running[e] += rank + 1;
   }
 }
 
@@ -343,22 +362,23 @@ int cin_moe_route(const int64_t* idx, int64_t T, int64_t k, int64_t E, int64_t* 
   CIN_CHECK_ARG(idx && perm && inv && counts && starts && ends && (A == 0 || workspace),
                 "moe_route: null pointer");
   const int64_t nblocks = cdiv(A, kChunk);
-  CIN_CHECK_ARG(workspace_elems >= nblocks * E, "moe_route: workspace needs %lld int32",
-                (long long)(nblocks * E));
-  CIN_CHECK_ARG(nblocks < 65536, "moe_route: too many assignments");
+  CIN_CHECK_ARG(workspace_elems >= 2 * nblocks * E, "moe_route: workspace needs %lld int32",
+                (long long)(2 * nblocks * E));
+  CIN_CHECK_ARG(nblocks < ((int64_t)1 << 20), "moe_route: too many assignments");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  int32_t* blockbase = workspace + nblocks * E;
   if (nblocks > 0) hipLaunchKernelGGL(k_route_hist, (unsigned)nblocks, kRT, 0, s, idx, A, (int32_t)E, workspace);
-  hipLaunchKernelGGL(k_route_scan, 1, kRT, 0, s, workspace, (int32_t)nblocks, (int32_t)E, A, counts,
-                     starts, ends, perm);
+  hipLaunchKernelGGL(k_route_scan, 1, kRT, 0, s, workspace, (int32_t)nblocks, (int32_t)E, A, blockbase,
+                     counts, starts, ends, perm);
   if (nblocks > 0)
-    hipLaunchKernelGGL(k_route_scatter, (unsigned)nblocks, kRT, 0, s, idx, A, (int32_t)E, workspace,
+    hipLaunchKernelGGL(k_route_scatter, (unsigned)nblocks, 64, 0, s, idx, A, (int32_t)E, blockbase,
                        perm, inv);
   return cin_check_launch("moe_route");
 }
 
 int cin_moe_route_workspace(int64_t T, int64_t k, int64_t E) {
   if (T < 0 || k < 1 || E < 1) return 0;
-  const int64_t n = cdiv(T * k, kChunk) * E;
+  const int64_t n = 2 * cdiv(T * k, kChunk) * E;
   return n > INT32_MAX ? INT32_MAX : (int)n;
 }
 

@@ -108,16 +108,20 @@ __device__ inline void quant_vals(const float (&v)[NV], float s, float r, uint32
 // row) own one tile.  Each lane loads NC 16-byte chunks, chunk c of lane i sitting at
 // tile chunk c * LANES + i so every load instruction reads whole 16*LANES-byte runs.
 // A group walks tiles t, t + G, ... keeping U tiles in flight; (row, tile) advance
-// incrementally instead of by division.  GATHER: output row r quantizes input row
-// rowmap[r] / rowdiv (the MoE dispatch gather); a map entry that is negative or past
-// src_rows gives a zero row.
-template <int DT, int LANES, int U, bool FULL, bool GATHER = false>
+// incrementally instead of by division.  MAP selects the MoE dispatch forms:
+//   kMapGather : output row r quantizes input row rowmap[r] / rowdiv (int64 map); a map
+//                entry that is negative or past src_rows gives a zero row;
+//   kMapScatter: input row t is quantized once and its codes and scale go to the output
+//                rows rowmap[t * rowdiv + j] (int32 map), j < rowdiv, that lie in
+//                [0, src_rows) (src_rows = output rows here).
+constexpr int kMapNone = 0, kMapGather = 1, kMapScatter = 2;
+template <int DT, int LANES, int U, bool FULL, int MAP = kMapNone>
 __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict__ x, int64_t N,
                                                          int64_t sxm, int round_scale,
                                                          uint8_t* __restrict__ q, int64_t sqm,
                                                          float* __restrict__ sc, int64_t ssm,
                                                          uint32_t nb, uint32_t ntiles,
-                                                         const int64_t* __restrict__ rowmap = nullptr,
+                                                         const void* __restrict__ rowmap = nullptr,
                                                          int64_t rowdiv = 1, int64_t src_rows = 0) {
   constexpr int ES = DT == CIN_DT_F32 ? 4 : 2;  // input element bytes
   constexpr int EPC = 16 / ES;                   // elements per 16-byte chunk
@@ -140,8 +144,8 @@ __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict_
       cbs[u] = cb;
       bool live = tb + (uint32_t)u * G < ntiles;
       int64_t srow = row;
-      if constexpr (GATHER) {
-        const int64_t m = live ? rowmap[row] : -1;
+      if constexpr (MAP == kMapGather) {
+        const int64_t m = live ? static_cast<const int64_t*>(rowmap)[row] : -1;
         srow = m >= 0 ? m / rowdiv : -1;
         if (srow < 0 || srow >= src_rows) {
           srow = 0;
@@ -205,40 +209,48 @@ __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict_
       const float s = compute_scale(a, rs);
       uint32_t codes[EPL / 4];
       quant_vals<EPL, kDivSteps<DT>>(v[u], s, 1.0f / s, codes);
-      uint8_t* qrow = q + (int64_t)rows[u] * sqm + (int64_t)cbs[u] * 128;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int64_t e0 = (int64_t)(c * LANES + li) * EPC;
-        const int64_t col = (int64_t)cbs[u] * 128 + e0;
-        if (FULL || col + EPC <= N) {
-          if constexpr (EPC == 8)
-            *reinterpret_cast<uint2*>(qrow + e0) = make_uint2(codes[2 * c], codes[2 * c + 1]);
-          else
-            *reinterpret_cast<uint32_t*>(qrow + e0) = codes[c];
-        } else {
-          for (int e = 0; e < EPC; ++e)
-            if (col + e < N)
-              qrow[e0 + e] = (uint8_t)((codes[(c * EPC + e) >> 2] >> (8 * (e & 3))) & 0xffu);
+      const int nout = MAP == kMapScatter ? (int)rowdiv : 1;
+      for (int j = 0; j < nout; ++j) {
+        int64_t orow = rows[u];
+        if constexpr (MAP == kMapScatter) {
+          orow = static_cast<const int32_t*>(rowmap)[(int64_t)rows[u] * rowdiv + j];
+          if (orow < 0 || orow >= src_rows) continue;
         }
+        uint8_t* qrow = q + orow * sqm + (int64_t)cbs[u] * 128;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int64_t e0 = (int64_t)(c * LANES + li) * EPC;
+          const int64_t col = (int64_t)cbs[u] * 128 + e0;
+          if (FULL || col + EPC <= N) {
+            if constexpr (EPC == 8)
+              *reinterpret_cast<uint2*>(qrow + e0) = make_uint2(codes[2 * c], codes[2 * c + 1]);
+            else
+              *reinterpret_cast<uint32_t*>(qrow + e0) = codes[c];
+          } else {
+            for (int e = 0; e < EPC; ++e)
+              if (col + e < N)
+                qrow[e0 + e] = (uint8_t)((codes[(c * EPC + e) >> 2] >> (8 * (e & 3))) & 0xffu);
+          }
+        }
+        if (li == 0) sc[orow * ssm + cbs[u]] = s;
       }
-      if (li == 0) sc[(int64_t)rows[u] * ssm + cbs[u]] = s;
     }
   }
 }
 
-template <int LANES, int U, bool FULL, bool GATHER = false>
+template <int LANES, int U, bool FULL, int MAP = kMapNone>
 void launch_rowwise128_t(const void* x, int dt, int64_t N, int64_t sxm, int rs, uint8_t* q,
                          int64_t sqm, float* sc, int64_t ssm, uint32_t nb, uint32_t ntiles,
-                         unsigned grid, hipStream_t st, const int64_t* rowmap = nullptr,
+                         unsigned grid, hipStream_t st, const void* rowmap = nullptr,
                          int64_t rowdiv = 1, int64_t src_rows = 0) {
   if (dt == CIN_DT_BF16)
-    hipLaunchKernelGGL((k_rowwise128<CIN_DT_BF16, LANES, U, FULL, GATHER>), grid, kThreads, 0, st,
+    hipLaunchKernelGGL((k_rowwise128<CIN_DT_BF16, LANES, U, FULL, MAP>), grid, kThreads, 0, st,
                        x, N, sxm, rs, q, sqm, sc, ssm, nb, ntiles, rowmap, rowdiv, src_rows);
   else if (dt == CIN_DT_F16)
-    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F16, LANES, U, FULL, GATHER>), grid, kThreads, 0, st,
+    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F16, LANES, U, FULL, MAP>), grid, kThreads, 0, st,
                        x, N, sxm, rs, q, sqm, sc, ssm, nb, ntiles, rowmap, rowdiv, src_rows);
   else
-    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F32, LANES, U, FULL, GATHER>), grid, kThreads, 0, st,
+    hipLaunchKernelGGL((k_rowwise128<CIN_DT_F32, LANES, U, FULL, MAP>), grid, kThreads, 0, st,
                        x, N, sxm, rs, q, sqm, sc, ssm, nb, ntiles, rowmap, rowdiv, src_rows);
 }
 
@@ -1386,12 +1398,63 @@ int cin_moe_gather_quant_rowwise(const void* x, int x_dtype, int64_t src_rows, i
   const uint32_t ntiles = (uint32_t)(rows * nb);
   const unsigned grid = grid_for(ntiles, kThreads / 8, 16384);
   if (N % 128 == 0)
-    launch_rowwise128_t<8, 1, true, true>(x, x_dtype, N, sxm, round_scale, q, sqm, scales, ssm,
-                                          (uint32_t)nb, ntiles, grid, s, rowmap, rowdiv, src_rows);
+    launch_rowwise128_t<8, 1, true, kMapGather>(x, x_dtype, N, sxm, round_scale, q, sqm, scales,
+                                                ssm, (uint32_t)nb, ntiles, grid, s, rowmap, rowdiv,
+                                                src_rows);
   else
-    launch_rowwise128_t<8, 1, false, true>(x, x_dtype, N, sxm, round_scale, q, sqm, scales, ssm,
-                                           (uint32_t)nb, ntiles, grid, s, rowmap, rowdiv, src_rows);
+    launch_rowwise128_t<8, 1, false, kMapGather>(x, x_dtype, N, sxm, round_scale, q, sqm, scales,
+                                                 ssm, (uint32_t)nb, ntiles, grid, s, rowmap,
+                                                 rowdiv, src_rows);
   return cin_check_launch("moe_gather_quant_rowwise");
+}
+
+// Output rows that no assignment reaches (perm[r] < 0: the tail after dropped ids) get the
+// quantization of a zero row: codes 0 and the scale of the amax floor.  A thread owns a
+// row; routed rows (all of them when no id was dropped) return at once.
+__global__ __launch_bounds__(kThreads) void k_zero_unrouted(const int64_t* __restrict__ perm,
+                                                            int64_t rows, int64_t N, int dt,
+                                                            int round_scale, uint8_t* q,
+                                                            int64_t sqm, float* sc, int64_t ssm) {
+  const int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (r >= rows || perm[r] >= 0) return;
+  const float s = compute_scale(amax_floor(dt), round_scale != 0);
+  for (int64_t b = 0; b < (N + 127) / 128; ++b) sc[r * ssm + b] = s;
+  uint8_t* p = q + r * sqm;  // 8-byte aligned (q and sqm are)
+  int64_t c = 0;
+  for (; c + 8 <= N; c += 8) *reinterpret_cast<uint2*>(p + c) = make_uint2(0u, 0u);
+  for (; c < N; ++c) p[c] = 0;
+}
+
+int cin_moe_scatter_quant_rowwise(const void* x, int x_dtype, int64_t T, int64_t N, int64_t sxm,
+                                  const int32_t* inv, int64_t k, const int64_t* perm, int64_t rows,
+                                  int round_scale, uint8_t* q, int64_t sqm, float* scales,
+                                  int64_t ssm, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(x_dtype), "moe_scatter_quant: unsupported x dtype %d", x_dtype);
+  CIN_CHECK_ARG(T >= 0 && N >= 0 && rows >= 0 && k >= 1, "moe_scatter_quant: bad sizes");
+  if (N == 0 || (T == 0 && rows == 0)) return CIN_OK;
+  CIN_CHECK_ARG(x && inv && perm && q && scales, "moe_scatter_quant: null pointer");
+  const int64_t nb = cdiv(N, 128);
+  CIN_CHECK_ARG(sqm >= N && ssm >= nb, "moe_scatter_quant: output row stride too small");
+  const int es = elem_size(x_dtype);
+  CIN_CHECK_ARG(aligned(x, 16) && (sxm * es) % 16 == 0 && sxm >= N && aligned(q, 8) && sqm % 8 == 0,
+                "moe_scatter_quant: x rows must be contiguous and 16-byte aligned, q rows 8-byte aligned");
+  CIN_CHECK_ARG(T * nb < (int64_t)1 << 31 && cdiv(rows, kThreads) < (int64_t)1 << 31,
+                "moe_scatter_quant: too many tiles");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (T > 0) {
+    const uint32_t ntiles = (uint32_t)(T * nb);
+    const unsigned grid = grid_for(ntiles, kThreads / 8, 16384);
+    if (N % 128 == 0)
+      launch_rowwise128_t<8, 1, true, kMapScatter>(x, x_dtype, N, sxm, round_scale, q, sqm, scales,
+                                                   ssm, (uint32_t)nb, ntiles, grid, s, inv, k, rows);
+    else
+      launch_rowwise128_t<8, 1, false, kMapScatter>(x, x_dtype, N, sxm, round_scale, q, sqm, scales,
+                                                    ssm, (uint32_t)nb, ntiles, grid, s, inv, k, rows);
+  }
+  if (rows > 0)
+    hipLaunchKernelGGL(k_zero_unrouted, (unsigned)cdiv(rows, kThreads), kThreads, 0, s, perm, rows, N,
+                       x_dtype, round_scale, q, sqm, scales, ssm);
+  return cin_check_launch("moe_scatter_quant_rowwise");
 }
 
 int cin_quant_blockwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t sxm, int64_t sxn,

@@ -25,7 +25,7 @@ from . import layers
 from ._lib import call, dtype_code, ptr, stream_of
 from .kernels import _cdiv, _require, custom_op
 
-_ROUTE_CHUNK = 2048  # assignments per route workgroup (csrc/moe.hip kChunk)
+_ROUTE_CHUNK = 1024  # assignments per route workgroup (csrc/moe.hip kChunk)
 MAX_EXPERTS = 4096
 MAX_TOP_K = 16
 
@@ -61,7 +61,7 @@ def _route_op(idx, n_experts):
     counts = torch.empty(n_experts, dtype=torch.int64, device=dev)
     starts = torch.empty(n_experts, dtype=torch.int64, device=dev)
     ends = torch.empty(n_experts, dtype=torch.int64, device=dev)
-    nws = max(1, _cdiv(A, _ROUTE_CHUNK) * n_experts)
+    nws = max(1, 2 * _cdiv(A, _ROUTE_CHUNK) * n_experts)
     ws = torch.empty(nws, dtype=torch.int32, device=dev)
     call("cin_moe_route", ptr(idx), T, k, n_experts, ptr(perm), ptr(inv), ptr(counts), ptr(starts),
          ptr(ends), ptr(ws), nws, stream_of(idx))
@@ -80,13 +80,20 @@ def _(idx, n_experts):
 # ---------------------------------------------------------------------------
 # Gather fused into the 1x128 quantization, and its backward (reference :139-141)
 # ---------------------------------------------------------------------------
-def moe_gather_quantize(x: torch.Tensor, perm: torch.Tensor, top_k: int, round_scale: bool = False):
+def moe_gather_quantize(x: torch.Tensor, perm: torch.Tensor, top_k: int, round_scale: bool = False,
+                        inv: torch.Tensor | None = None):
     """quantize_fp8_rowwise(x[perm // top_k]) bit for bit, without the gathered rows:
-    (codes float8_e4m3fn [A, D], scales fp32 [A, ceil(D/128)]); rows where perm is -1 are
-    zero codes."""
+    (codes float8_e4m3fn [A, D], scales fp32 [A, ceil(D/128)]); rows where perm is -1 get the
+    quantization of a zero row.  With ``inv`` (moe_route's inverse map) each token row is
+    quantized once and written to its top_k sorted rows (one read of x instead of top_k);
+    without it each sorted row reads its token row."""
     _require(x.is_cuda and perm.is_cuda, "Input must be on CUDA")
     _require(x.ndim == 2 and perm.ndim == 1, "x must be [n_tokens, d] and perm 1-D")
     _require(top_k >= 1, "top_k must be >= 1")
+    if inv is not None:
+        _require(inv.numel() == x.shape[0] * top_k, "inv must hold n_tokens * top_k entries")
+        return _scatter_quant_op(x, perm.to(torch.int64), inv.to(torch.int32), int(top_k),
+                                 bool(round_scale))
     return _gather_quant_op(x, perm.to(torch.int64), int(top_k), bool(round_scale))
 
 
@@ -101,8 +108,7 @@ def _codes_rows8(A, D, like):
 @custom_op("moe_gather_quant_rowwise",
            "(Tensor x, Tensor perm, int top_k, bool round_scale) -> (Tensor, Tensor)")
 def _gather_quant_op(x, perm, top_k, round_scale):
-    if not (x.stride(1) == 1 and x.data_ptr() % 16 == 0 and (x.stride(0) * x.element_size()) % 16 == 0):
-        x = x.contiguous()
+    x = _x_rows16(x)
     A = perm.numel()
     T, D = x.shape
     pm = perm.contiguous()
@@ -115,6 +121,31 @@ def _gather_quant_op(x, perm, top_k, round_scale):
 
 @_gather_quant_op.register_fake
 def _(x, perm, top_k, round_scale):
+    A, D = perm.shape[0], x.shape[1]
+    return _codes_rows8(A, D, x), x.new_empty((A, _cdiv(D, 128)), dtype=torch.float32)
+
+
+def _x_rows16(x):
+    ok = x.stride(1) == 1 and x.data_ptr() % 16 == 0 and (x.stride(0) * x.element_size()) % 16 == 0
+    return x if ok else x.contiguous()
+
+
+@custom_op("moe_scatter_quant_rowwise",
+           "(Tensor x, Tensor perm, Tensor inv, int top_k, bool round_scale) -> (Tensor, Tensor)")
+def _scatter_quant_op(x, perm, inv, top_k, round_scale):
+    x = _x_rows16(x)
+    A = perm.numel()
+    T, D = x.shape
+    pm, iv = perm.contiguous(), inv.contiguous()
+    q = _codes_rows8(A, D, x)
+    s = torch.empty((A, _cdiv(D, 128)), dtype=torch.float32, device=x.device)
+    call("cin_moe_scatter_quant_rowwise", ptr(x), dtype_code(x), T, D, x.stride(0), ptr(iv), top_k,
+         ptr(pm), A, int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), stream_of(x))
+    return q, s
+
+
+@_scatter_quant_op.register_fake
+def _(x, perm, inv, top_k, round_scale):
     A, D = perm.shape[0], x.shape[1]
     return _codes_rows8(A, D, x), x.new_empty((A, _cdiv(D, 128)), dtype=torch.float32)
 
@@ -219,7 +250,7 @@ class FP8RoutedExpertsFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, w12, w3, perm, inv, starts, ends, top_k):
-        xq, xs = moe_gather_quantize(x, perm, top_k)
+        xq, xs = moe_gather_quantize(x, perm, top_k, inv=inv)
         out, saved = layers.experts_forward(xq, xs, w12, w3, starts, ends, x.dtype)
         ctx.save_for_backward(*saved, inv)
         ctx.top_k = top_k

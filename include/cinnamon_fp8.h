@@ -298,6 +298,18 @@ int cin_moe_gather_quant_rowwise(const void* x, int x_dtype, int64_t src_rows, i
                                  int64_t ssm, void* stream);
 
 /*
+ * The same codes and scales as cin_moe_gather_quant_rowwise(x, perm, k), computed from the
+ * token side: token row t is quantized once and written to its sorted rows inv[t*k + j]
+ * (one read of x instead of k); rows r with perm[r] < 0 get the zero-row quantization.
+ *   x [T, N] (16-byte aligned rows), inv [T*k] int32 and perm [rows] int64 from
+ *   cin_moe_route, q [rows, N] (8-byte aligned rows), scales [rows, ceil(N/128)].
+ */
+int cin_moe_scatter_quant_rowwise(const void* x, int x_dtype, int64_t T, int64_t N, int64_t sxm,
+                                  const int32_t* inv, int64_t k, const int64_t* perm, int64_t rows,
+                                  int round_scale, uint8_t* q, int64_t sqm, float* scales,
+                                  int64_t ssm, void* stream);
+
+/*
  * Backward of the dispatch gather: out[t] = sum over token t's sorted positions r
  * (increasing r, fp32 sums) of g[r]; the gradient of flat_x[token_indices] (reference
  * src/layers.py:140).  g [A, N] (g_dtype, row stride sgm), inv [T*k] from cin_moe_route,

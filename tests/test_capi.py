@@ -77,6 +77,6 @@ def test_empty_shapes_are_noops():
 
 def test_moe_route_workspace_size():
     lib = _lib.load()
-    assert lib.cin_moe_route_workspace(16384, 8, 32) == 64 * 32   # 2048 assignments per block
-    assert lib.cin_moe_route_workspace(1, 1, 4) == 4
+    assert lib.cin_moe_route_workspace(16384, 8, 32) == 2 * 128 * 32   # 1024 assignments per block
+    assert lib.cin_moe_route_workspace(1, 1, 4) == 8
     assert lib.cin_moe_route_workspace(0, 8, 4) == 0

@@ -62,27 +62,32 @@ def test_gather_quantize_equals_quantize_of_gather(dev, dtype, D):
     x = (torch.randn(T, D, generator=g) * 3).to(dtype).to(dev)
     x[5, :300] = 0  # a zero tile
     perm, inv, *_ = moe.moe_route(top_idx.to(dev), E)
-    q, s = moe.moe_gather_quantize(x, perm, k)
     rq, rs = kernels.quantize_fp8_rowwise(x[perm // k])
-    assert torch.equal(q.view(torch.uint8), rq.view(torch.uint8)) and torch.equal(s, rs)
+    for form in (None, inv):  # gather from the sorted side, scatter from the token side
+        q, s = moe.moe_gather_quantize(x, perm, k, inv=form)
+        assert torch.equal(q.view(torch.uint8), rq.view(torch.uint8)) and torch.equal(s, rs)
     # round_scale path and a strided x
     xs = torch.zeros(T, D + 64, dtype=dtype, device=dev)[:, :D]
     xs.copy_(x)
-    q2, s2 = moe.moe_gather_quantize(xs, perm, k, round_scale=True)
     rq2, rs2 = kernels.quantize_fp8_rowwise(x[perm // k], round_scale=True)
-    assert torch.equal(q2.view(torch.uint8), rq2.view(torch.uint8)) and torch.equal(s2, rs2)
+    for form in (None, inv):
+        q2, s2 = moe.moe_gather_quantize(xs, perm, k, round_scale=True, inv=form)
+        assert torch.equal(q2.view(torch.uint8), rq2.view(torch.uint8)) and torch.equal(s2, rs2)
 
 
 def test_gather_quantize_dropped_rows_are_zero(dev):
     x = torch.randn(4, 256, device=dev).to(torch.bfloat16)
     top_idx = torch.tensor([[0, 9], [1, 0], [9, 9], [1, 1]], device=dev)  # 9 is dropped (E = 2)
-    perm, *_ = moe.moe_route(top_idx, 2)
-    q, s = moe.moe_gather_quantize(x, perm, 2)
+    perm, inv, *_ = moe.moe_route(top_idx, 2)
     kept = int((perm >= 0).sum())
     assert kept == 5
     rq, rs = kernels.quantize_fp8_rowwise(x[perm[:kept] // 2])
-    assert torch.equal(q[:kept].view(torch.uint8), rq.view(torch.uint8)) and torch.equal(s[:kept], rs)
-    assert int(q[kept:].view(torch.uint8).count_nonzero()) == 0
+    zq, zs = kernels.quantize_fp8_rowwise(torch.zeros(1, 256, dtype=x.dtype, device=dev))
+    for form in (None, inv):
+        q, s = moe.moe_gather_quantize(x, perm, 2, inv=form)
+        assert torch.equal(q[:kept].view(torch.uint8), rq.view(torch.uint8)) and torch.equal(s[:kept], rs)
+        assert int(q[kept:].view(torch.uint8).count_nonzero()) == 0
+        assert torch.equal(s[kept:], zs.expand(len(perm) - kept, -1))
 
 
 def _ordered_token_sums(rows, inv, T, k, weights=None):

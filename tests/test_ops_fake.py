@@ -19,7 +19,8 @@ OPS = ["quant_rowwise", "quant_blockwise", "quant_blockwise_t", "quant_dual", "r
        "dequant_rowwise", "dequant", "gemm_fp8_bs", "transpose_u8", "grouped_gemm_f16",
        "grouped_gemm_fp8", "quant_dual_grouped", "requant_row_to_block_grouped",
        "grouped_wgrad_fp8", "grouped_dgrad_fp8", "silu_mul_quant_rowwise", "swiglu_backward",
-       "moe_route", "moe_gather_quant_rowwise", "moe_gather_sum", "moe_combine", "moe_combine_backward"]
+       "moe_route", "moe_gather_quant_rowwise", "moe_scatter_quant_rowwise", "moe_gather_sum",
+       "moe_combine", "moe_combine_backward"]
 F8, F32, BF16 = torch.float8_e4m3fn, torch.float32, torch.bfloat16
 
 
@@ -189,8 +190,10 @@ def test_moe_dispatch_shape_functions_and_trace():
         assert _meta(dx) == ((T, D), BF16, "cuda") and dw12.shape == (E, 2 * H, D) and dw3.shape == (E, D, H)
         q, s = moe.moe_gather_quantize(x, perm, k)
         assert _meta(q) == ((T * k, D), F8, "cuda") and _meta(s) == ((T * k, 2), F32, "cuda")
+        q, s = moe.moe_gather_quantize(x, perm, k, inv=inv)
+        assert _meta(q) == ((T * k, D), F8, "cuda") and _meta(s) == ((T * k, 2), F32, "cuda")
         assert _meta(moe.moe_gather_sum(dys, inv, k, BF16)) == ((T, D), BF16, "cuda")
     ops = _op_targets(gm)
-    for name in ["moe_route", "moe_gather_quant_rowwise", "moe_combine", "moe_combine_backward",
+    for name in ["moe_route", "moe_scatter_quant_rowwise", "moe_combine", "moe_combine_backward",
                  "moe_gather_sum", "grouped_gemm_fp8", "grouped_wgrad_fp8"]:
         assert any(f"cinnamon_amd.{name}" in o for o in ops), (name, ops)
