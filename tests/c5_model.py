@@ -167,6 +167,7 @@ class MoE(nn.Module):
         self.shared_experts = nn.ModuleList([SwiGLU(c.d_model, c.hidden_dim) for _ in range(c.n_shared)])
         self.router = nn.Linear(c.d_model, c.n_routed, bias=False)
         self.register_buffer("expert_bias", torch.zeros(c.n_routed))
+        self.device_dispatch = False  # FP8 mode: route / dispatch / combine with cinnamon_amd.moe
 
     def forward(self, x):
         B, L, d = x.shape
@@ -176,14 +177,21 @@ class MoE(nn.Module):
         gates = scores.gather(-1, top_idx)
         gates = gates / (gates.sum(-1, keepdim=True) + 1e-9)
         flat = x.reshape(-1, d)
-        expert_of, order = top_idx.reshape(-1).sort()
-        token = order // self.top_k
-        counts = torch.bincount(expert_of, minlength=self.n_routed)
-        ends = counts.cumsum(0)
-        starts = ends - counts
-        out = self.routed_experts(flat[token], starts, ends)
-        out = out * gates.reshape(-1)[order][:, None]
-        routed = torch.zeros_like(flat).index_add_(0, token, out.to(flat.dtype)).view(B, L, d)
+        if self.device_dispatch and x.is_cuda:
+            from cinnamon_amd import moe as moe_ops
+            routed, counts = moe_ops.routed_experts(self.routed_experts, flat,
+                                                    top_idx.reshape(-1, self.top_k),
+                                                    gates.reshape(-1, self.top_k))
+            routed = routed.to(flat.dtype).view(B, L, d)
+        else:
+            expert_of, order = top_idx.reshape(-1).sort()
+            token = order // self.top_k
+            counts = torch.bincount(expert_of, minlength=self.n_routed)
+            ends = counts.cumsum(0)
+            starts = ends - counts
+            out = self.routed_experts(flat[token], starts, ends)
+            out = out * gates.reshape(-1)[order][:, None]
+            routed = torch.zeros_like(flat).index_add_(0, token, out.to(flat.dtype)).view(B, L, d)
         if self.training:
             with torch.no_grad():
                 expected = top_idx.numel() / self.n_routed
@@ -266,7 +274,8 @@ def loss_fn(model: C5Model, ids: torch.Tensor):
 
 def to_fp8(model: C5Model) -> C5Model:
     """The FP8 mode: eligible Linears -> FP8Linear (convert_to_fp8's rules), routed experts ->
-    layers.GroupedExperts with the same weights."""
+    layers.GroupedExperts with the same weights, routed through cinnamon_amd.moe (device
+    routing, dispatch fused into the quantization, device combine)."""
     from cinnamon_amd import kernels, layers
 
     model = copy.deepcopy(model)
@@ -277,6 +286,7 @@ def to_fp8(model: C5Model) -> C5Model:
             new.w12.copy_(old.w12)
             new.w3.copy_(old.w3)
         blk.moe.routed_experts = new
+        blk.moe.device_dispatch = True
     return kernels.convert_to_fp8(model)
 
 
