@@ -299,7 +299,7 @@ def main():
     # dH12 [A, 2H], grouped re-quantization of the saved X codes, grouped wgrad
     # dW12 [E, 2H, D] and grouped dgrad dX [A, D]
     mb = None
-    if full or (args.only or "").startswith("moe_") and args.only not in ("moe_gateup", "moe_down"):
+    if full or args.only in ("moe_dual", "moe_requant", "moe_wgrad", "moe_dgrad"):
         if moe is None:
             moe = moe_setup(dev)
             xq3, xs3 = kernels.quantize_fp8_rowwise(moe["x"])

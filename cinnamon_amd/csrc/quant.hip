@@ -1350,6 +1350,23 @@ unsigned resident_grid(uint32_t ntiles) {
   return (unsigned)(g < (int64_t)ntiles ? g : (int64_t)ntiles);
 }
 
+// Output rows that no assignment reaches (perm[r] < 0: the tail after dropped ids) get the
+// quantization of a zero row: codes 0 and the scale of the amax floor.  A thread owns a
+// row; routed rows (all of them when no id was dropped) return at once.
+__global__ __launch_bounds__(kThreads) void k_zero_unrouted(const int64_t* __restrict__ perm,
+                                                            int64_t rows, int64_t N, int dt,
+                                                            int round_scale, uint8_t* q,
+                                                            int64_t sqm, float* sc, int64_t ssm) {
+  const int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (r >= rows || perm[r] >= 0) return;
+  const float s = compute_scale(amax_floor(dt), round_scale != 0);
+  for (int64_t b = 0; b < (N + 127) / 128; ++b) sc[r * ssm + b] = s;
+  uint8_t* p = q + r * sqm;  // 8-byte aligned (q and sqm are)
+  int64_t c = 0;
+  for (; c + 8 <= N; c += 8) *reinterpret_cast<uint2*>(p + c) = make_uint2(0u, 0u);
+  for (; c < N; ++c) p[c] = 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1406,23 +1423,6 @@ int cin_moe_gather_quant_rowwise(const void* x, int x_dtype, int64_t src_rows, i
                                                  ssm, (uint32_t)nb, ntiles, grid, s, rowmap,
                                                  rowdiv, src_rows);
   return cin_check_launch("moe_gather_quant_rowwise");
-}
-
-// Output rows that no assignment reaches (perm[r] < 0: the tail after dropped ids) get the
-// quantization of a zero row: codes 0 and the scale of the amax floor.  A thread owns a
-// row; routed rows (all of them when no id was dropped) return at once.
-__global__ __launch_bounds__(kThreads) void k_zero_unrouted(const int64_t* __restrict__ perm,
-                                                            int64_t rows, int64_t N, int dt,
-                                                            int round_scale, uint8_t* q,
-                                                            int64_t sqm, float* sc, int64_t ssm) {
-  const int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (r >= rows || perm[r] >= 0) return;
-  const float s = compute_scale(amax_floor(dt), round_scale != 0);
-  for (int64_t b = 0; b < (N + 127) / 128; ++b) sc[r * ssm + b] = s;
-  uint8_t* p = q + r * sqm;  // 8-byte aligned (q and sqm are)
-  int64_t c = 0;
-  for (; c + 8 <= N; c += 8) *reinterpret_cast<uint2*>(p + c) = make_uint2(0u, 0u);
-  for (; c < N; ++c) p[c] = 0;
 }
 
 int cin_moe_scatter_quant_rowwise(const void* x, int x_dtype, int64_t T, int64_t N, int64_t sxm,
