@@ -49,6 +49,7 @@ __all__ = [
     "FP8MatmulFunction",
     "FP8Linear",
     "convert_to_fp8",
+    "set_weight_cache",
     "moe_grouped_gemm",
     "lightning_indexer_fused",
     "sparse_attention",
@@ -421,14 +422,18 @@ class FP8MatmulFunction(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, x, weight, round_scale):
+    def forward(ctx, x, weight, round_scale, weight_fp8=None):
+        # weight_fp8: optional (codes, transposed codes, scales) of this weight from
+        # quantize_fp8_blockwise_t, e.g. FP8Linear's weight cache
         x_shape = x.shape
         x_flat = x.reshape(-1, x_shape[-1])
         M, K = x_flat.shape
         N = weight.shape[0]
         x_fp8, x_scale = quantize_fp8_rowwise(x_flat, block_size=128, round_scale=round_scale)
-        w = weight if weight.dtype == torch.float32 else weight.float()
-        w_fp8, w_fp8_t, w_scale = quantize_fp8_blockwise_t(w, round_scale=False)
+        if weight_fp8 is None:
+            w = weight if weight.dtype == torch.float32 else weight.float()
+            weight_fp8 = quantize_fp8_blockwise_t(w, round_scale=False)
+        w_fp8, w_fp8_t, w_scale = weight_fp8
         out = fp8_gemm_bs(x_fp8, x_scale, w_fp8, w_scale, torch.bfloat16)
         ctx.save_for_backward(x_fp8, x_scale, w_fp8_t, w_scale)
         ctx.x_shape = x_shape
@@ -446,7 +451,35 @@ class FP8MatmulFunction(torch.autograd.Function):
         # wgrad: dW[N, K] = dY^T[N, M] . X[M, K]; B^T = X^T block codes [K, M]
         x_blk_t, x_sblk = requantize_rowwise_to_blockwise(x_fp8, x_scale, transposed=True)
         grad_w = fp8_gemm_bs(g_fp8_t, g_scale_t, x_blk_t, x_sblk.t(), torch.bfloat16)
-        return grad_x.reshape(x_shape), grad_w, None
+        return grad_x.reshape(x_shape), grad_w, None, None
+
+
+class WeightCache:
+    """Quantized copies of a parameter, rebuilt only when the parameter changes.
+
+    The key is the parameter's version counter (bumped by every in-place update: optimizer
+    steps, copy_, load_state_dict), its storage pointer (re-assignment) and its dtype/shape.
+    Writes through ``param.data`` do not bump the version counter; callers that update
+    weights that way must call ``clear()``.  Never used while torch.compile traces."""
+
+    def __init__(self):
+        self.key = None
+        self.value = None
+
+    def get(self, params, build):
+        key = tuple((p._version, p.data_ptr(), p.dtype, tuple(p.shape)) for p in params)
+        if key != self.key:
+            self.value = None  # release the old copies before building the new ones
+            self.value = build()
+            self.key = key
+        return self.value
+
+    def clear(self):
+        self.key = self.value = None
+
+
+def _weight_cache_active(module) -> bool:
+    return module.cache_weights and not torch.compiler.is_compiling()
 
 
 class FP8Linear(torch.nn.Module):
@@ -454,7 +487,10 @@ class FP8Linear(torch.nn.Module):
 
     Keeps an fp32 master ``weight`` [out, in] (init N(0, 0.02)) and an optional bias
     added after the FP8 matmul.  On non-GPU tensors the reference runs F.linear, and so
-    does this module.
+    does this module.  With ``cache_weights`` (off by default; see set_weight_cache) the
+    weight's codes are kept between forwards until the weight changes, instead of
+    re-quantizing on every forward as the reference does (src/kernels.py:747-749): with
+    gradient accumulation the weight is quantized once per optimizer step.
     """
 
     def __init__(self, in_features: int, out_features: int, bias: bool = False,
@@ -463,6 +499,8 @@ class FP8Linear(torch.nn.Module):
         self.in_features = in_features
         self.out_features = out_features
         self.round_scale = round_scale
+        self.cache_weights = False
+        self._wcache = WeightCache()
         self.weight = torch.nn.Parameter(torch.empty(out_features, in_features))
         torch.nn.init.normal_(self.weight, mean=0.0, std=0.02)
         if bias:
@@ -472,7 +510,12 @@ class FP8Linear(torch.nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.is_cuda:
-            out = FP8MatmulFunction.apply(x, self.weight, self.round_scale)
+            wq = None
+            if _weight_cache_active(self):
+                w = self.weight.detach()
+                wq = self._wcache.get([self.weight], lambda: quantize_fp8_blockwise_t(
+                    w if w.dtype == torch.float32 else w.float(), round_scale=False))
+            out = FP8MatmulFunction.apply(x, self.weight, self.round_scale, wq)
         else:
             out = torch.nn.functional.linear(x, self.weight, None)
         if self.bias is not None:
@@ -487,6 +530,18 @@ class FP8Linear(torch.nn.Module):
         if linear.bias is not None:
             fp8_linear.bias = torch.nn.Parameter(linear.bias.data.clone())
         return fp8_linear
+
+
+def set_weight_cache(model: torch.nn.Module, enabled: bool = True) -> torch.nn.Module:
+    """Turn the quantized-weight cache of every FP8Linear and FP8 expert layer in ``model``
+    on or off (off clears it).  With the cache on, weights are quantized once per change
+    (per optimizer step) instead of once per forward."""
+    for m in model.modules():
+        if hasattr(m, "cache_weights") and hasattr(m, "_wcache"):
+            m.cache_weights = bool(enabled)
+            if not enabled:
+                m._wcache.clear()
+    return model
 
 
 _DEFAULT_EXCLUDE = ["embedding", "lm_head", "router", "norm", "attn", "indexer"]

@@ -11,8 +11,9 @@ from __future__ import annotations
 import torch
 
 from ._lib import call, dtype_code, ptr, stream_of
-from .kernels import (_cdiv, _codes_u8, _rows8, _kcontig, _require, custom_op,
-                      quantize_fp8_blockwise_t, quantize_fp8_rowwise)
+from .kernels import (WeightCache, _cdiv, _codes_u8, _rows8, _kcontig, _require,
+                      _weight_cache_active, custom_op, quantize_fp8_blockwise_t,
+                      quantize_fp8_rowwise)
 
 
 def fp8_grouped_gemm(a_codes: torch.Tensor, a_scales: torch.Tensor, w_codes: torch.Tensor,
@@ -322,21 +323,35 @@ def _(dh, h12):
     return dh.new_empty((dh.shape[0], 2 * dh.shape[1]), dtype=torch.float32)
 
 
-def experts_forward(xq: torch.Tensor, xs: torch.Tensor, w12: torch.Tensor, w3: torch.Tensor,
-                    starts: torch.Tensor, ends: torch.Tensor, h_dtype: torch.dtype):
-    """FP8 SwiGLU experts on 1x128-quantized sorted rows (xq, xs): GEMM(w12), silu(h1) * h2
-    in fp32 cast to h_dtype and quantized in the same pass, GEMM(w3), fp32 out (reference
-    GroupedExperts.forward, src/layers.py:71-75).  Returns (out [T, D] fp32, saved tensors for
-    experts_backward).  Rows outside every expert range are zero."""
+def quantize_expert_weights(w12: torch.Tensor, w3: torch.Tensor):
+    """Per-expert 128x128 quantization of the stacked SwiGLU weights, with the transposed
+    codes the backward needs: ((w12q, w12qt, w12s), (w3q, w3qt, w3s)) from
+    quantize_fp8_blockwise_t of w12 [E*2H, D] and w3 [E*D, H] (blocks never straddle two
+    experts: 2H and D are multiples of 128)."""
     E, H2, D = w12.shape
     H = H2 // 2
     w12f = w12 if w12.dtype == torch.float32 else w12.float()
-    w12q, w12qt, w12s = quantize_fp8_blockwise_t(w12f.reshape(E * H2, D))
+    w3f = w3 if w3.dtype == torch.float32 else w3.float()
+    return (quantize_fp8_blockwise_t(w12f.reshape(E * H2, D)),
+            quantize_fp8_blockwise_t(w3f.reshape(E * D, H)))
+
+
+def experts_forward(xq: torch.Tensor, xs: torch.Tensor, w12: torch.Tensor, w3: torch.Tensor,
+                    starts: torch.Tensor, ends: torch.Tensor, h_dtype: torch.dtype,
+                    weights_fp8=None):
+    """FP8 SwiGLU experts on 1x128-quantized sorted rows (xq, xs): GEMM(w12), silu(h1) * h2
+    in fp32 cast to h_dtype and quantized in the same pass, GEMM(w3), fp32 out (reference
+    GroupedExperts.forward, src/layers.py:71-75).  weights_fp8: optional
+    quantize_expert_weights(w12, w3) (a weight cache).  Returns (out [T, D] fp32, saved
+    tensors for experts_backward).  Rows outside every expert range are zero."""
+    E, H2, D = w12.shape
+    H = H2 // 2
+    if weights_fp8 is None:
+        weights_fp8 = quantize_expert_weights(w12, w3)
+    (w12q, w12qt, w12s), (w3q, w3qt, w3s) = weights_fp8
     h12 = fp8_grouped_gemm(xq, xs, w12q.view(E, H2, D), w12s.view(E, H2 // 128, -1),
                            starts, ends, out_dtype=torch.bfloat16, zero_uncovered=True)
     hq, hs = silu_mul_quantize_fp8(h12, out_dtype=h_dtype)
-    w3f = w3 if w3.dtype == torch.float32 else w3.float()
-    w3q, w3qt, w3s = quantize_fp8_blockwise_t(w3f.reshape(E * D, H))
     out = fp8_grouped_gemm(hq, hs, w3q.view(E, D, H), w3s.view(E, D // 128, -1), starts, ends,
                            out_dtype=torch.float32, zero_uncovered=True)
     return out, (xq, xs, w12qt, w12s, h12, hq, hs, w3qt, w3s, starts, ends)
@@ -375,10 +390,10 @@ class FP8GroupedExpertsFunction(torch.autograd.Function):
     the saved inputs and grouped wgrad)."""
 
     @staticmethod
-    def forward(ctx, sorted_x, w12, w3, expert_starts, expert_ends):
+    def forward(ctx, sorted_x, w12, w3, expert_starts, expert_ends, weights_fp8=None):
         starts, ends = _ranges(expert_starts, expert_ends)
         xq, xs = quantize_fp8_rowwise(sorted_x)
-        out, saved = experts_forward(xq, xs, w12, w3, starts, ends, sorted_x.dtype)
+        out, saved = experts_forward(xq, xs, w12, w3, starts, ends, sorted_x.dtype, weights_fp8)
         ctx.save_for_backward(*saved)
         ctx.x_dtype = sorted_x.dtype
         ctx.w_dtypes = (w12.dtype, w3.dtype)
@@ -389,7 +404,8 @@ class FP8GroupedExpertsFunction(torch.autograd.Function):
         # dx straight in the input dtype: the GEMM's bf16 store is the RNE of its fp32 value
         dx_dtype = ctx.x_dtype if ctx.x_dtype in (torch.bfloat16, torch.float32) else torch.float32
         dx, dw12, dw3 = experts_backward(ctx.saved_tensors, grad_out, dx_dtype)
-        return (dx.to(ctx.x_dtype), dw12.to(ctx.w_dtypes[0]), dw3.to(ctx.w_dtypes[1]), None, None)
+        return (dx.to(ctx.x_dtype), dw12.to(ctx.w_dtypes[0]), dw3.to(ctx.w_dtypes[1]), None, None,
+                None)
 
 
 class GroupedExperts(torch.nn.Module):
@@ -405,13 +421,23 @@ class GroupedExperts(torch.nn.Module):
         self.hidden_dim = hidden_dim
         self.w12 = torch.nn.Parameter(torch.empty(n_experts, 2 * hidden_dim, d_model))
         self.w3 = torch.nn.Parameter(torch.empty(n_experts, d_model, hidden_dim))
+        self.cache_weights = False  # kernels.set_weight_cache
+        self._wcache = WeightCache()
         torch.nn.init.normal_(self.w12, mean=0.0, std=0.02)
         torch.nn.init.normal_(self.w3, mean=0.0, std=0.02)
+
+    def quantized_weights(self):
+        """The experts' FP8 weights for this forward: from the weight cache when it is on,
+        else freshly quantized (the reference re-quantizes on every forward)."""
+        if not _weight_cache_active(self):
+            return None
+        w12, w3 = self.w12.detach(), self.w3.detach()
+        return self._wcache.get([self.w12, self.w3], lambda: quantize_expert_weights(w12, w3))
 
     def forward(self, sorted_x, expert_starts, expert_ends, max_expert_tokens=None):
         if sorted_x.is_cuda:
             return FP8GroupedExpertsFunction.apply(sorted_x, self.w12, self.w3, expert_starts,
-                                                   expert_ends)
+                                                   expert_ends, self.quantized_weights())
         out = torch.zeros(sorted_x.size(0), self.d_model, device=sorted_x.device,
                           dtype=sorted_x.dtype)
         for i in range(self.n_experts):

@@ -249,9 +249,9 @@ class FP8RoutedExpertsFunction(torch.autograd.Function):
     sums each token's sorted-row gradients (fp32) into dx."""
 
     @staticmethod
-    def forward(ctx, x, w12, w3, perm, inv, starts, ends, top_k):
+    def forward(ctx, x, w12, w3, perm, inv, starts, ends, top_k, weights_fp8=None):
         xq, xs = moe_gather_quantize(x, perm, top_k, inv=inv)
-        out, saved = layers.experts_forward(xq, xs, w12, w3, starts, ends, x.dtype)
+        out, saved = layers.experts_forward(xq, xs, w12, w3, starts, ends, x.dtype, weights_fp8)
         ctx.save_for_backward(*saved, inv)
         ctx.top_k = top_k
         ctx.x_dtype = x.dtype
@@ -263,7 +263,8 @@ class FP8RoutedExpertsFunction(torch.autograd.Function):
         *saved, inv = ctx.saved_tensors
         dxs, dw12, dw3 = layers.experts_backward(tuple(saved), grad_out, torch.float32)
         dx = moe_gather_sum(dxs, inv, ctx.top_k, ctx.x_dtype)
-        return (dx, dw12.to(ctx.w_dtypes[0]), dw3.to(ctx.w_dtypes[1]), None, None, None, None, None)
+        return (dx, dw12.to(ctx.w_dtypes[0]), dw3.to(ctx.w_dtypes[1]), None, None, None, None, None,
+                None)
 
 
 class MoECombineFunction(torch.autograd.Function):
@@ -296,5 +297,6 @@ def routed_experts(experts: layers.GroupedExperts, x: torch.Tensor, top_idx: tor
     k = top_idx.shape[1]
     _require(1 <= k <= MAX_TOP_K, f"top_k must be in [1, {MAX_TOP_K}]")
     perm, inv, counts, starts, ends = moe_route(top_idx, experts.n_experts)
-    sorted_out = FP8RoutedExpertsFunction.apply(x, experts.w12, experts.w3, perm, inv, starts, ends, k)
+    sorted_out = FP8RoutedExpertsFunction.apply(x, experts.w12, experts.w3, perm, inv, starts, ends, k,
+                                                experts.quantized_weights())
     return MoECombineFunction.apply(sorted_out, top_scores, perm, inv), counts

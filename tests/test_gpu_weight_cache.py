@@ -1,0 +1,127 @@
+"""FP8 weight cache (GPU): weights quantized once per change instead of once per forward.
+
+The reference re-quantizes every weight on every forward (src/kernels.py:747-749), so with
+gradient accumulation the same weight is quantized once per micro-step.  With
+kernels.set_weight_cache the FP8 layers keep their codes until the parameter changes:
+- outputs and gradients must equal the uncached layer's bit for bit;
+- the weight must be quantized once per optimizer step;
+- any in-place update, copy_ or re-assignment of the parameter must invalidate the codes.
+"""
+import pytest
+import torch
+
+from cinnamon_amd import kernels, layers, moe
+
+pytestmark = pytest.mark.gpu
+
+
+class _Counter:
+    def __init__(self, monkeypatch, module, name):
+        self.n = 0
+        real = getattr(module, name)
+
+        def wrapped(*a, **k):
+            self.n += 1
+            return real(*a, **k)
+
+        monkeypatch.setattr(module, name, wrapped)
+
+
+def _linear_pair(dev, seed=0):
+    torch.manual_seed(seed)
+    a = kernels.FP8Linear(512, 384, round_scale=False).to(dev)
+    b = kernels.FP8Linear(512, 384, round_scale=False).to(dev)
+    b.load_state_dict(a.state_dict())
+    kernels.set_weight_cache(b, True)
+    return a, b
+
+
+def test_linear_cache_bit_identical_and_once_per_step(dev, monkeypatch):
+    a, b = _linear_pair(dev)
+    opt_a = torch.optim.AdamW(a.parameters(), lr=1e-3)
+    opt_b = torch.optim.AdamW(b.parameters(), lr=1e-3)
+    quants = _Counter(monkeypatch, kernels, "quantize_fp8_blockwise_t")
+    g = torch.Generator().manual_seed(1)
+    for step in range(3):
+        for micro in range(4):  # gradient accumulation
+            x = torch.randn(2, 256, 512, generator=g).to(torch.bfloat16).to(dev)
+            ya, yb = a(x), b(x)
+            assert torch.equal(ya, yb), (step, micro)
+            ya.float().square().mean().backward()
+            yb.float().square().mean().backward()
+        assert torch.equal(a.weight.grad, b.weight.grad)
+        opt_a.step()
+        opt_b.step()
+        opt_a.zero_grad()
+        opt_b.zero_grad()
+    # a quantizes every forward (3 x 4); b once per optimizer step (3)
+    assert quants.n == 12 + 3
+    assert torch.equal(a.weight, b.weight)
+
+
+def test_linear_cache_invalidation(dev, monkeypatch):
+    a, b = _linear_pair(dev, seed=2)
+    x = torch.randn(64, 512, device=dev).to(torch.bfloat16)
+    quants = _Counter(monkeypatch, kernels, "quantize_fp8_blockwise_t")
+    b(x)
+    b(x)
+    assert quants.n == 1
+    with torch.no_grad():
+        b.weight.mul_(1.5)  # in-place: version bump
+        a.weight.mul_(1.5)
+    assert torch.equal(b(x), a(x))
+    assert quants.n == 3  # b re-quantized once, a once
+    new = torch.randn(384, 512, device=dev) * 0.02
+    with torch.no_grad():
+        b.weight.copy_(new)
+        a.weight.copy_(new)
+    assert torch.equal(b(x), a(x))
+    b.weight = torch.nn.Parameter(torch.randn(384, 512, device=dev) * 0.02)  # re-assignment
+    a.weight = torch.nn.Parameter(b.weight.detach().clone())
+    assert torch.equal(b(x), a(x))
+    kernels.set_weight_cache(b, False)
+    assert b._wcache.value is None and not b.cache_weights
+
+
+def test_experts_cache_bit_identical_and_once_per_step(dev, monkeypatch):
+    torch.manual_seed(3)
+    E, D, H = 4, 256, 256
+    a = layers.GroupedExperts(E, D, H).to(dev)
+    b = layers.GroupedExperts(E, D, H).to(dev)
+    b.load_state_dict(a.state_dict())
+    kernels.set_weight_cache(b, True)
+    counts = torch.tensor([300, 0, 170, 530])
+    ends = counts.cumsum(0).to(dev)
+    starts = ends - counts.to(dev)
+    quants = _Counter(monkeypatch, layers, "quantize_expert_weights")
+    g = torch.Generator().manual_seed(4)
+    for micro in range(3):
+        x = torch.randn(int(counts.sum()), D, generator=g).to(torch.bfloat16).to(dev)
+        ya, yb = a(x, starts, ends), b(x, starts, ends)
+        assert torch.equal(ya, yb)
+        ya.square().mean().backward()
+        yb.square().mean().backward()
+    assert torch.equal(a.w12.grad, b.w12.grad) and torch.equal(a.w3.grad, b.w3.grad)
+    assert quants.n == 3 + 1
+    with torch.no_grad():
+        b.w3.add_(1e-3)
+        a.w3.add_(1e-3)
+    x = torch.randn(int(counts.sum()), D, generator=g).to(torch.bfloat16).to(dev)
+    assert torch.equal(a(x, starts, ends), b(x, starts, ends))
+    assert quants.n == 4 + 2
+
+
+def test_routed_experts_use_the_cache(dev, monkeypatch):
+    torch.manual_seed(5)
+    E, D, H, T, k = 8, 256, 256, 512, 2
+    experts = layers.GroupedExperts(E, D, H).to(dev)
+    kernels.set_weight_cache(experts, True)
+    g = torch.Generator().manual_seed(6)
+    top_idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(dev)
+    scores = torch.rand(T, k, generator=g).to(dev)
+    quants = _Counter(monkeypatch, layers, "quantize_expert_weights")
+    outs = []
+    for _ in range(2):
+        x = torch.randn(T, D, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16).to(dev)
+        outs.append(moe.routed_experts(experts, x, top_idx, scores)[0])
+    assert quants.n == 1 and torch.equal(outs[0], outs[1])

@@ -117,7 +117,7 @@ def test_fp8_linear_forward_backward_traces_to_operators(round_scale):
     def step(x, w, gy):
         ctx = _Ctx()
         y = fn.forward(ctx, x, w, round_scale)
-        dx, dw, _ = fn.backward(ctx, gy)
+        dx, dw, *_ = fn.backward(ctx, gy)
         return y, dx, dw
 
     with FakeTensorMode(allow_non_fake_inputs=True):
@@ -141,7 +141,7 @@ def test_grouped_experts_forward_backward_traces_to_operators():
     def step(x, w12, w3, starts, ends, gy):
         ctx = _Ctx()
         y = fn.forward(ctx, x, w12, w3, starts, ends)
-        dx, dw12, dw3, _, _ = fn.backward(ctx, gy)
+        dx, dw12, dw3, *_ = fn.backward(ctx, gy)
         return y, dx, dw12, dw3
 
     with FakeTensorMode(allow_non_fake_inputs=True):
