@@ -38,7 +38,7 @@ def parse():
     p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "moe_gateup", "moe_down",
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
                                       "moe_wgrad", "moe_dgrad", "moe_layer", "moe_route",
-                                      "moe_gather", "moe_combine", "copy"], default=None,
+                                      "moe_gather", "moe_combine", "indexer", "copy"], default=None,
                    help="run only one kernel in a loop (for profiler runs)")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the config-3 (MoE) and config-4 (backward) component timings")
@@ -388,6 +388,34 @@ def main():
         torch.zeros(moe["T"], moe["D"], device=dev, dtype=w.dtype).scatter_add_(
             0, tok.unsqueeze(1).expand_as(w), w)
 
+    # DSA indexer scores on FP8 q / k (src/attention.py:288-300) at the model's indexer shape:
+    # 4 heads, d_indexer_head 64 widened to 128 by PoPE, 16 sequences of 1024 tokens
+    ix = None
+    if full or args.only == "indexer":
+        g5 = torch.Generator(device=dev).manual_seed(36)
+        IB, IL, IH, ID = 16, 1024, 4, 128
+        ix = dict(q=torch.randn(IB, IL, IH, ID, device=dev, generator=g5).to(torch.bfloat16),
+                  k=torch.randn(IB, IL, ID, device=dev, generator=g5).to(torch.bfloat16),
+                  w=torch.randn(IB, IL, IH, device=dev, generator=g5) * 0.5, shape=(IB, IL, IH, ID))
+        q8, qsc = kernels.quantize_fp8_rowwise(ix["q"].reshape(-1, ID), block_size=128)
+        k8, ksc = kernels.quantize_fp8_rowwise(ix["k"].reshape(-1, ID), block_size=128)
+        ix["q8"], ix["qs"] = q8.view(IB, IL, IH, ID), qsc.view(IB, IL, IH)
+        ix["k8"], ix["ks"] = k8.view(IB, IL, ID), ksc.view(IB, IL)
+
+    def indexer(i):
+        torch.ops.cinnamon_amd.indexer_scores_fp8(ix["q8"], ix["qs"], ix["k8"], ix["ks"], ix["w"], 0.125)
+
+    def indexer_full(i):
+        kernels.indexer_scores_fp8(ix["q"], ix["k"], ix["w"], 0.125)
+
+    def indexer_torch(i):
+        IB, IL, IH, ID = ix["shape"]
+        q8, qsc = kernels.quantize_fp8_rowwise(ix["q"].reshape(-1, ID), block_size=128)
+        k8, ksc = kernels.quantize_fp8_rowwise(ix["k"].reshape(-1, ID), block_size=128)
+        logits = torch.einsum("bthd,bsd->bths", q8.view(IB, IL, IH, ID).float(), k8.view(IB, IL, ID).float())
+        logits = torch.relu(logits) * (qsc.view(IB, IL, IH) * ix["w"] * 0.125).unsqueeze(-1)
+        logits.sum(dim=2) * ksc.view(IB, IL).unsqueeze(1)
+
     if full or args.only in ("dual_quant", "requant", "dgrad", "wgrad"):
         bwd = bwd_setup(dev, xs[0], ws[0])
         gq, gs, gqt, gst = kernels.quantize_fp8_dual(bwd["dy"])
@@ -421,7 +449,7 @@ def main():
               "requant": requant, "dgrad": dgrad, "wgrad": wgrad, "moe_dual": moe_dual,
               "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad,
               "moe_layer": moe_layer, "moe_route": moe_route, "moe_gather": moe_gather,
-              "moe_combine": moe_combine}[args.only]
+              "moe_combine": moe_combine, "indexer": indexer}[args.only]
         loop = time_loop if args.only == "step" else kernel_loop
         us = loop(fn, args.steps, args.warmup)
         print(json.dumps({"only": args.only, "us_per_call": us}))
@@ -532,6 +560,24 @@ def main():
             "combine_us": round(c_us, 1), "combine_gbps": round(c_bytes / c_us / 1e3, 1),
             "combine_frac_of_hbm": round(c_bytes / c_us / 1e3 / PEAK_HBM_GBPS, 4),
             "torch_sort_mul_scatter_add_us": round(ctorch_us, 1),
+        }
+    if ix is not None:
+        IB, IL, IH, ID = ix["shape"]
+        k_us = kernel_loop(indexer, 20, 3)
+        f_us = time_loop(indexer_full, 10, 2)
+        t_us = time_loop(indexer_torch, 5, 1)
+        # bytes: q and k codes + scales + weights read once, scores written once (fp32)
+        i_bytes = IB * IL * IH * ID + IB * IL * ID + IB * IL * IH * 8 + IB * IL * 4 + IB * IL * IL * 4
+        i_flops = 2.0 * IB * IL * IL * IH * ID
+        out["components"]["config5_indexer_scores"] = {
+            "what": "kernels.indexer_scores_fp8 on 16 x 1024 tokens, 4 heads, d 128, against the "
+                    "reference's FP8 einsum formulation (quantize, fp32 einsum, relu, weight, head "
+                    "sum) on the same GPU",
+            "kernel_us": round(k_us, 1), "kernel_gbps": round(i_bytes / k_us / 1e3, 1),
+            "kernel_frac_of_hbm": round(i_bytes / k_us / 1e3 / PEAK_HBM_GBPS, 4),
+            "kernel_tflops": round(i_flops / k_us / 1e6, 1),
+            "with_quantization_us": round(f_us, 1),
+            "torch_einsum_us": round(t_us, 1),
         }
     if mb is not None:
         A, D, H = moe["A"], moe["D"], moe["H"]

@@ -50,6 +50,7 @@ __all__ = [
     "FP8Linear",
     "convert_to_fp8",
     "set_weight_cache",
+    "indexer_scores_fp8",
     "moe_grouped_gemm",
     "lightning_indexer_fused",
     "sparse_attention",
@@ -615,6 +616,48 @@ def _grouped_f16_op(a, w, starts, ends):
 @_grouped_f16_op.register_fake
 def _(a, w, starts, ends):
     return a.new_empty((a.shape[0], w.shape[1]), dtype=torch.float16)
+
+
+# ---------------------------------------------------------------------------
+# DSA indexer scoring on FP8 q / k (reference src/attention.py:288-300)
+# ---------------------------------------------------------------------------
+def indexer_scores_fp8(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor,
+                       softmax_scale: float) -> torch.Tensor:
+    """The FP8 branch of DSAIndexer.forward up to the mask (reference
+    src/attention.py:288-300): q [B, L, H, d] and k [B, S, d] quantized row-wise (1x128,
+    the first scale of each row), scores [B, L, S] fp32 = k_scale * sum_h
+    relu(q_codes . k_codes) * (q_scale * weights * softmax_scale).  One fused kernel; the
+    reference's [B, L, H, S] fp32 logits are never written.  weights [B, L, H]."""
+    _require(q.is_cuda and k.is_cuda and weights.is_cuda, "Input must be on CUDA")
+    _require(q.ndim == 4 and k.ndim == 3 and weights.shape == q.shape[:3],
+             "q must be [B, L, H, d], k [B, S, d], weights [B, L, H]")
+    B, L, H, d = q.shape
+    _require(k.shape[0] == B and k.shape[2] == d, "k must be [B, S, d] with q's B and d")
+    _require(d % 32 == 0 and 32 <= d <= 256, "head dim must be a multiple of 32 in [32, 256]")
+    S = k.shape[1]
+    q_fp8, q_scale = quantize_fp8_rowwise(q.reshape(-1, d).contiguous(), block_size=128)
+    k_fp8, k_scale = quantize_fp8_rowwise(k.reshape(-1, d).contiguous(), block_size=128)
+    qs = q_scale.view(B, L, H, -1)[..., 0].contiguous()
+    ks = k_scale.view(B, S, -1)[..., 0].contiguous()
+    return _indexer_op(q_fp8.view(B, L, H, d), qs, k_fp8.view(B, S, d), ks,
+                       weights.float().contiguous(), float(softmax_scale))
+
+
+@custom_op("indexer_scores_fp8",
+           "(Tensor q8, Tensor q_scale, Tensor k8, Tensor k_scale, Tensor weights, float softmax_scale) -> Tensor")
+def _indexer_op(q8, q_scale, k8, k_scale, weights, softmax_scale):
+    B, L, H, d = q8.shape
+    S = k8.shape[1]
+    qc, kc = _codes_u8(q8).contiguous(), _codes_u8(k8).contiguous()
+    out = torch.empty((B, L, S), dtype=torch.float32, device=q8.device)
+    call("cin_indexer_scores_fp8", ptr(qc), ptr(q_scale.contiguous()), ptr(kc), ptr(k_scale.contiguous()),
+         ptr(weights.contiguous()), B, L, S, H, d, softmax_scale, ptr(out), stream_of(qc))
+    return out
+
+
+@_indexer_op.register_fake
+def _(q8, q_scale, k8, k_scale, weights, softmax_scale):
+    return q8.new_empty((q8.shape[0], q8.shape[1], k8.shape[1]), dtype=torch.float32)
 
 
 # ---------------------------------------------------------------------------

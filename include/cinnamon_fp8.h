@@ -263,6 +263,21 @@ int cin_zero_rows_outside_ranges(void* C, int64_t ldc_bytes, int64_t row_bytes, 
                                  const int64_t* starts, const int64_t* ends, int64_t E,
                                  void* stream);
 
+/*
+ * DSA indexer scoring on FP8 codes, fused (no [B, L, H, S] logits):
+ *   scores[b,t,s] = k_scale[b,s] * sum_h relu(sum_d q8[b,t,h,d] k8[b,s,d])
+ *                                 * ((q_scale[b,t,h] * weights[b,t,h]) * softmax_scale)
+ * Replaces the FP8 branch of DSAIndexer.forward (reference src/attention.py:288-300) after
+ * its two row-wise quantizations: q_scale / k_scale are the first 1x128 scale of each row
+ * (:296-297).  All arrays contiguous: q8 [B, L, H, d] and k8 [B, S, d] e4m3 codes (8-byte
+ * aligned), q_scale and weights [B, L, H] fp32, k_scale [B, S] fp32, scores [B, L, S] fp32.
+ * d a multiple of 32 in [32, 256].
+ */
+int cin_indexer_scores_fp8(const uint8_t* q8, const float* q_scale, const uint8_t* k8,
+                           const float* k_scale, const float* weights, int64_t B, int64_t L,
+                           int64_t S, int64_t H, int64_t d, float softmax_scale, float* scores,
+                           void* stream);
+
 /* ---------------------------- MoE dispatch / combine ---------------------------- */
 
 /*

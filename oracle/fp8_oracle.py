@@ -26,6 +26,7 @@ Functions and the reference lines they restate:
   grouped_gemm_ref        src/layers.py:79-86 loop semantics on FP8 operands
   moe_dispatch_ref        src/layers.py:133-148 (sort, token_indices, bincount, cumsum)
   moe_combine_ref         src/layers.py:151-154 (gated scatter_add_ of sorted rows)
+  indexer_scores_fp8_ref  src/attention.py:288-300 (DSA indexer scoring on FP8 q / k)
 """
 from __future__ import annotations
 
@@ -349,6 +350,29 @@ def grouped_experts_ref(x: torch.Tensor, w12: torch.Tensor, w3: torch.Tensor, st
             r["dx"][s:t] = d_row[s:t] @ w12d[e]
             r["dw12"][e] = colq(dh12[s:t]).t() @ blkq(xd[s:t])
     return r
+
+
+# ---------------------------------------------------------------------------
+# DSA indexer scoring in FP8 (reference src/attention.py:288-300)
+# ---------------------------------------------------------------------------
+def indexer_scores_fp8_ref(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor,
+                           softmax_scale: float) -> torch.Tensor:
+    """The reference's FP8 index scores (src/attention.py:288-300) on the CPU:
+    q [B, L, H, d], k [B, S, d] quantized row-wise in 1x128 tiles (the first scale of each
+    row is used, :296-297), logits = einsum('bthd,bsd->bths') of the codes in fp32,
+    relu(logits) * (q_scale * weights * softmax_scale), summed over the heads, times
+    k_scale.  weights [B, L, H] fp32.  Returns scores [B, L, S] fp32 (before the mask)."""
+    B, L, H, d = q.shape
+    S = k.shape[1]
+    q_fp8, q_scale = quant_rowwise(q.reshape(-1, d).contiguous(), block_size=128)
+    k_fp8, k_scale = quant_rowwise(k.reshape(-1, d).contiguous(), block_size=128)
+    q_fp8 = q_fp8.view(B, L, H, d)
+    k_fp8 = k_fp8.view(B, S, d)
+    q_scale = q_scale.view(B, L, H, -1)[..., 0]
+    k_scale = k_scale.view(B, S, -1)[..., 0]
+    logits = torch.einsum('bthd,bsd->bths', q_fp8.float(), k_fp8.float())
+    logits = torch.relu(logits) * (q_scale * weights * softmax_scale).unsqueeze(-1)
+    return logits.sum(dim=2) * k_scale.unsqueeze(1)
 
 
 # ---------------------------------------------------------------------------

@@ -20,7 +20,7 @@ OPS = ["quant_rowwise", "quant_blockwise", "quant_blockwise_t", "quant_dual", "r
        "grouped_gemm_fp8", "quant_dual_grouped", "requant_row_to_block_grouped",
        "grouped_wgrad_fp8", "grouped_dgrad_fp8", "silu_mul_quant_rowwise", "swiglu_backward",
        "moe_route", "moe_gather_quant_rowwise", "moe_scatter_quant_rowwise", "moe_gather_sum",
-       "moe_combine", "moe_combine_backward"]
+       "moe_combine", "moe_combine_backward", "indexer_scores_fp8"]
 F8, F32, BF16 = torch.float8_e4m3fn, torch.float32, torch.bfloat16
 
 
@@ -92,6 +92,11 @@ def test_shape_functions_match_the_kernels_outputs():
         assert _meta(hq) == ((T, H), F8, "cuda") and hs.shape == (T, 3)
         dh = torch.empty(T, H, dtype=F32, device=dev)
         assert _meta(layers.swiglu_backward(dh, h12)) == ((T, 2 * H), F32, "cuda")
+        # indexer scores
+        qi = torch.empty(2, 100, 4, 128, dtype=BF16, device=dev)
+        ki = torch.empty(2, 90, 128, dtype=BF16, device=dev)
+        wi = torch.empty(2, 100, 4, dtype=F32, device=dev)
+        assert _meta(kernels.indexer_scores_fp8(qi, ki, wi, 0.125)) == ((2, 100, 90), F32, "cuda")
 
 
 def _op_targets(gm):
