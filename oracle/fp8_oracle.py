@@ -27,6 +27,9 @@ Functions and the reference lines they restate:
   moe_dispatch_ref        src/layers.py:133-148 (sort, token_indices, bincount, cumsum)
   moe_combine_ref         src/layers.py:151-154 (gated scatter_add_ of sorted rows)
   indexer_scores_fp8_ref  src/attention.py:288-300 (DSA indexer scoring on FP8 q / k)
+The MoE functions are pinned by tests/test_oracle_moe.py; indexer_scores_fp8_ref by
+tests/test_oracle_indexer.py (the reference's non-FP8 formula on lossless inputs, the
+first-scale rule, the ReLU, power-of-two homogeneity).
 """
 from __future__ import annotations
 
