@@ -38,7 +38,8 @@ def parse():
     p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "moe_gateup", "moe_down",
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
                                       "moe_wgrad", "moe_dgrad", "moe_layer", "moe_route",
-                                      "moe_gather", "moe_combine", "indexer", "copy"], default=None,
+                                      "moe_gather", "moe_combine", "indexer", "indexer_wgrad", "copy"],
+                   default=None,
                    help="run only one kernel in a loop (for profiler runs)")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the config-3 (MoE) and config-4 (backward) component timings")
@@ -391,7 +392,7 @@ def main():
     # DSA indexer scores on FP8 q / k (src/attention.py:288-300) at the model's indexer shape:
     # 4 heads, d_indexer_head 64 widened to 128 by PoPE, 16 sequences of 1024 tokens
     ix = None
-    if full or args.only == "indexer":
+    if full or args.only in ("indexer", "indexer_wgrad"):
         g5 = torch.Generator(device=dev).manual_seed(36)
         IB, IL, IH, ID = 16, 1024, 4, 128
         ix = dict(q=torch.randn(IB, IL, IH, ID, device=dev, generator=g5).to(torch.bfloat16),
@@ -401,12 +402,20 @@ def main():
         k8, ksc = kernels.quantize_fp8_rowwise(ix["k"].reshape(-1, ID), block_size=128)
         ix["q8"], ix["qs"] = q8.view(IB, IL, IH, ID), qsc.view(IB, IL, IH)
         ix["k8"], ix["ks"] = k8.view(IB, IL, ID), ksc.view(IB, IL)
+        ix["g"] = torch.randn(IB, IL, IL, device=dev, generator=g5)
 
     def indexer(i):
         torch.ops.cinnamon_amd.indexer_scores_fp8(ix["q8"], ix["qs"], ix["k8"], ix["ks"], ix["w"], 0.125)
 
+    def indexer_wgrad(i):
+        torch.ops.cinnamon_amd.indexer_weights_grad_fp8(ix["q8"], ix["qs"], ix["k8"], ix["ks"], ix["g"], 0.125)
+
     def indexer_full(i):
         kernels.indexer_scores_fp8(ix["q"], ix["k"], ix["w"], 0.125)
+
+    def indexer_full_fwd_bwd(i):
+        w = ix["w"].detach().requires_grad_(True)
+        kernels.indexer_scores_fp8(ix["q"], ix["k"], w, 0.125).backward(ix["g"])
 
     def indexer_torch(i):
         IB, IL, IH, ID = ix["shape"]
@@ -414,7 +423,16 @@ def main():
         k8, ksc = kernels.quantize_fp8_rowwise(ix["k"].reshape(-1, ID), block_size=128)
         logits = torch.einsum("bthd,bsd->bths", q8.view(IB, IL, IH, ID).float(), k8.view(IB, IL, ID).float())
         logits = torch.relu(logits) * (qsc.view(IB, IL, IH) * ix["w"] * 0.125).unsqueeze(-1)
-        logits.sum(dim=2) * ksc.view(IB, IL).unsqueeze(1)
+        return logits.sum(dim=2) * ksc.view(IB, IL).unsqueeze(1)
+
+    def indexer_torch_fwd_bwd(i):
+        w = ix["w"].detach().requires_grad_(True)
+        IB, IL, IH, ID = ix["shape"]
+        q8, qsc = kernels.quantize_fp8_rowwise(ix["q"].reshape(-1, ID), block_size=128)
+        k8, ksc = kernels.quantize_fp8_rowwise(ix["k"].reshape(-1, ID), block_size=128)
+        logits = torch.einsum("bthd,bsd->bths", q8.view(IB, IL, IH, ID).float(), k8.view(IB, IL, ID).float())
+        logits = torch.relu(logits) * (qsc.view(IB, IL, IH) * w * 0.125).unsqueeze(-1)
+        (logits.sum(dim=2) * ksc.view(IB, IL).unsqueeze(1)).backward(ix["g"])
 
     if full or args.only in ("dual_quant", "requant", "dgrad", "wgrad"):
         bwd = bwd_setup(dev, xs[0], ws[0])
@@ -449,7 +467,7 @@ def main():
               "requant": requant, "dgrad": dgrad, "wgrad": wgrad, "moe_dual": moe_dual,
               "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad,
               "moe_layer": moe_layer, "moe_route": moe_route, "moe_gather": moe_gather,
-              "moe_combine": moe_combine, "indexer": indexer}[args.only]
+              "moe_combine": moe_combine, "indexer": indexer, "indexer_wgrad": indexer_wgrad}[args.only]
         loop = time_loop if args.only == "step" else kernel_loop
         us = loop(fn, args.steps, args.warmup)
         print(json.dumps({"only": args.only, "us_per_call": us}))
@@ -564,8 +582,11 @@ def main():
     if ix is not None:
         IB, IL, IH, ID = ix["shape"]
         k_us = kernel_loop(indexer, 20, 3)
+        kb_us = kernel_loop(indexer_wgrad, 20, 3)
         f_us = time_loop(indexer_full, 10, 2)
         t_us = time_loop(indexer_torch, 5, 1)
+        fb_us = time_loop(indexer_full_fwd_bwd, 10, 2)
+        tb_us = time_loop(indexer_torch_fwd_bwd, 3, 1)
         # bytes: q and k codes + scales + weights read once, scores written once (fp32)
         i_bytes = IB * IL * IH * ID + IB * IL * ID + IB * IL * IH * 8 + IB * IL * 4 + IB * IL * IL * 4
         i_flops = 2.0 * IB * IL * IL * IH * ID
@@ -576,8 +597,12 @@ def main():
             "kernel_us": round(k_us, 1), "kernel_gbps": round(i_bytes / k_us / 1e3, 1),
             "kernel_frac_of_hbm": round(i_bytes / k_us / 1e3 / PEAK_HBM_GBPS, 4),
             "kernel_tflops": round(i_flops / k_us / 1e6, 1),
+            "weights_grad_kernel_us": round(kb_us, 1),
+            "weights_grad_kernel_frac_of_hbm": round(i_bytes / kb_us / 1e3 / PEAK_HBM_GBPS, 4),
             "with_quantization_us": round(f_us, 1),
             "torch_einsum_us": round(t_us, 1),
+            "forward_backward_us": round(fb_us, 1),
+            "torch_einsum_forward_backward_us": round(tb_us, 1),
         }
     if mb is not None:
         A, D, H = moe["A"], moe["D"], moe["H"]

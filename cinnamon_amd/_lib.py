@@ -50,6 +50,9 @@ SIGNATURES: dict[str, list] = {
     "cin_zero_rows_outside_ranges": [_p, _i64, _i64, _i64, _p, _p, _i64, _p],
     "cin_indexer_scores_fp8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p,
                                _p],
+    "cin_indexer_weights_grad": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p,
+                                 _i64, _p, _p],
+    "cin_indexer_weights_grad_workspace": [_i64, _i64, _i64, _i64],
     "cin_moe_route": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _p],
     "cin_moe_route_workspace": [_i64, _i64, _i64],
     "cin_moe_gather_quant_rowwise": [_p, _i32, _i64, _i64, _i64, _p, _i64, _i64, _i32, _p, _i64, _p,
@@ -61,6 +64,9 @@ SIGNATURES: dict[str, list] = {
     "cin_moe_combine_backward": [_p, _i64, _p, _i64, _p, _i32, _i64, _p, _p, _i64, _i64, _i64, _i64,
                                  _p, _i64, _p, _p],
 }
+
+# entry points that return something other than an int status
+RESTYPES = {"cin_indexer_weights_grad_workspace": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -94,7 +100,7 @@ def load() -> ctypes.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
         lib.cin_last_error.argtypes = []
         lib.cin_last_error.restype = ctypes.c_char_p
         _lib = lib

@@ -56,52 +56,59 @@ __device__ inline v8i frag32(const uint8_t* row, bool ok, int kq, int c) {
   return v;
 }
 
-// D = head dim (multiple of 32, <= 256), HG = heads whose q fragments are held at once.
-// vec: k_scale and scores rows are 16-byte aligned (S % 4 == 0 and aligned bases).
-template <int D, int HG>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_indexer_scores_fp8(
-    const uint8_t* __restrict__ q8, const float* __restrict__ qs, const uint8_t* __restrict__ k8,
-    const float* __restrict__ ks, const float* __restrict__ w, int64_t L, int64_t S, int64_t H,
-    float softmax_scale, float* __restrict__ out, int64_t tiles_t, int64_t tiles_s, int xcd_rotate,
-    int vec) {
-  constexpr int NC = (D + 127) / 128;           // 128-byte slices of d
-  constexpr int RS = D + 16;                    // LDS key row stride (bytes)
-  constexpr int CH = D / 16;                    // 16-byte chunks per key row
-  constexpr int PER = (kKT * CH + kThreads - 1) / kThreads;
-  constexpr int OS = kKT + 4;                   // staging row stride (floats)
-  __shared__ __attribute__((aligned(16))) uint8_t kl[2][kKT * RS];
-  __shared__ __attribute__((aligned(16))) float ksl[2][kKT];
-  __shared__ __attribute__((aligned(16))) float ost[4 * 16 * OS];
+// Waves per SIMD the register allocation aims for: two workgroups per CU fit in LDS up to
+// d = 160 (2 x (2 key buffers + staging) <= 160 KB), one beyond.
+template <int D>
+constexpr int kMinWaves = D <= 160 ? 2 : 1;
 
+// Workgroup -> (batch, 64-token tile, 512-key range).  With xcd_rotate (grid a multiple of
+// 8) XCD x = blockIdx % 8 runs the contiguous tiles [x n/8, (x+1) n/8).
+struct Tile {
+  int64_t b, tt, sw, s_begin, s_end;
+  int nsub;
+};
+
+__device__ inline Tile tile_of(int64_t S, int64_t tiles_t, int64_t tiles_s, int xcd_rotate) {
   int64_t tile = blockIdx.x;
-  if (xcd_rotate) {  // grid is a multiple of 8: XCD x = blockIdx % 8 runs tiles [x n/8, (x+1) n/8)
+  if (xcd_rotate) {
     const int64_t per = gridDim.x >> 3;
     tile = (tile & 7) * per + (tile >> 3);
   }
-  const int64_t b = tile / (tiles_t * tiles_s);
-  const int64_t rem = tile - b * tiles_t * tiles_s;
-  const int64_t tt = rem / tiles_s, sw = rem - tt * tiles_s;
-  const int64_t s_begin = sw * kKPW;
-  const int64_t s_end = s_begin + kKPW < S ? s_begin + kKPW : S;
-  const int nsub = (int)((s_end - s_begin + kKT - 1) / kKT);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int l16 = lane & 15, kq = lane >> 4;
+  Tile t;
+  t.b = tile / (tiles_t * tiles_s);
+  const int64_t rem = tile - t.b * tiles_t * tiles_s;
+  t.tt = rem / tiles_s;
+  t.sw = rem - t.tt * tiles_s;
+  t.s_begin = t.sw * kKPW;
+  t.s_end = t.s_begin + kKPW < S ? t.s_begin + kKPW : S;
+  t.nsub = (int)((t.s_end - t.s_begin + kKT - 1) / kKT);
+  return t;
+}
 
-  // ---- key sub-tile staging: global -> registers (issued early) -> LDS
+// One 128-key sub-tile of codes and k_scale: global -> registers (issued early) -> LDS rows
+// of d + 16 bytes (the 16 lanes of a 16-byte fragment read hit 16 distinct bank groups,
+// d / 16 + 1 being odd).  Keys past the range read as zero.
+template <int D>
+struct KeyStage {
+  static constexpr int RS = D + 16;
+  static constexpr int CH = D / 16;
+  static constexpr int PER = (kKT * CH + kThreads - 1) / kThreads;
   uint4 pre[PER];
-  v4f kpre = {0.0f, 0.0f, 0.0f, 0.0f};
-  auto load_sub = [&](int i) {
+  v4f kpre;
+
+  __device__ void load(const uint8_t* k8, const float* ks, int64_t b, int64_t S, int64_t s_sub,
+                       int64_t s_end, int vec) {
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
       const int idx = threadIdx.x + u * kThreads;
       const int row = idx / CH, c = idx - row * CH;
-      const int64_t s = s_begin + (int64_t)i * kKT + row;
+      const int64_t s = s_sub + row;
       pre[u] = uint4{0u, 0u, 0u, 0u};
       if (idx < kKT * CH && s < s_end) pre[u] = *reinterpret_cast<const uint4*>(k8 + (b * S + s) * D + 16 * c);
     }
+    kpre = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     if (threadIdx.x < kKT / 4) {
-      const int64_t s0 = s_begin + (int64_t)i * kKT + 4 * threadIdx.x;
-      kpre = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      const int64_t s0 = s_sub + 4 * threadIdx.x;
       if (vec && s0 + 4 <= s_end) {
         kpre = *reinterpret_cast<const v4f*>(ks + b * S + s0);
       } else {
@@ -109,19 +116,41 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
           if (s0 + r < s_end) kpre[r] = ks[b * S + s0 + r];
       }
     }
-  };
-  auto store_sub = [&](int buf) {
+  }
+  __device__ void store(uint8_t* kl, float* ksl) const {
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
       const int idx = threadIdx.x + u * kThreads;
       const int row = idx / CH, c = idx - row * CH;
-      if (idx < kKT * CH) *reinterpret_cast<uint4*>(&kl[buf][row * RS + 16 * c]) = pre[u];
+      if (idx < kKT * CH) *reinterpret_cast<uint4*>(&kl[row * RS + 16 * c]) = pre[u];
     }
-    if (threadIdx.x < kKT / 4) *reinterpret_cast<v4f*>(&ksl[buf][4 * threadIdx.x]) = kpre;
-  };
+    if (threadIdx.x < kKT / 4) *reinterpret_cast<v4f*>(&ksl[4 * threadIdx.x]) = kpre;
+  }
+};
 
-  // ---- the wave's tokens: q fragments and head weights for HG heads
-  const int64_t tok = tt * kTT + wave * 16 + l16;
+// D = head dim (multiple of 32, <= 256), HG = heads whose q fragments are held at once.
+// vec: k_scale and scores rows are 16-byte aligned (S % 4 == 0 and aligned bases).
+template <int D, int HG>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWaves<D>, 8))) void k_indexer_scores_fp8(
+    const uint8_t* __restrict__ q8, const float* __restrict__ qs, const uint8_t* __restrict__ k8,
+    const float* __restrict__ ks, const float* __restrict__ w, int64_t L, int64_t S, int64_t H,
+    float softmax_scale, float* __restrict__ out, int64_t tiles_t, int64_t tiles_s, int xcd_rotate,
+    int vec) {
+  constexpr int NC = (D + 127) / 128;           // 128-byte slices of d
+  constexpr int RS = KeyStage<D>::RS;
+  constexpr int OS = kKT + 4;                   // staging row stride (floats)
+  __shared__ __attribute__((aligned(16))) uint8_t kl[2][kKT * RS];
+  __shared__ __attribute__((aligned(16))) float ksl[2][kKT];
+  __shared__ __attribute__((aligned(16))) float ost[4 * 16 * OS];
+
+  const Tile tl = tile_of(S, tiles_t, tiles_s, xcd_rotate);
+  const int64_t b = tl.b;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l16 = lane & 15, kq = lane >> 4;
+  KeyStage<D> stage;
+
+  // the wave's tokens: q fragments and head weights for HG heads
+  const int64_t tok = tl.tt * kTT + wave * 16 + l16;
   const bool tok_ok = tok < L;
   const uint8_t* qrow = q8 + (b * L + (tok_ok ? tok : 0)) * H * D;
   const int64_t orow = (b * L + (tok_ok ? tok : 0)) * H;
@@ -138,14 +167,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
   };
   const bool one_group = H <= HG;
 
-  load_sub(0);
+  stage.load(k8, ks, b, S, tl.s_begin, tl.s_end, vec);
   load_q(0);
-  store_sub(0);
+  stage.store(kl[0], ksl[0]);
   __syncthreads();
   float* my = ost + wave * 16 * OS;
-  for (int i = 0; i < nsub; ++i) {
+  for (int i = 0; i < tl.nsub; ++i) {
     const int buf = i & 1;
-    if (i + 1 < nsub) load_sub(i + 1);
+    if (i + 1 < tl.nsub) stage.load(k8, ks, b, S, tl.s_begin + (int64_t)(i + 1) * kKT, tl.s_end, vec);
     // Each 16-key tile's head sum goes straight to the wave's staging rows; a later head
     // group continues the sum from there (same increasing head order).  The staging rows
     // belong to this wave alone and a wave's LDS accesses complete in order, so no
@@ -182,25 +211,160 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 8))
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
       const int row = 2 * it + (lane >> 5), c4 = lane & 31;
-      const int64_t t = tt * kTT + wave * 16 + row;
-      const int64_t s0 = s_begin + (int64_t)i * kKT + 4 * c4;
+      const int64_t t = tl.tt * kTT + wave * 16 + row;
+      const int64_t s0 = tl.s_begin + (int64_t)i * kKT + 4 * c4;
       const v4f v = *reinterpret_cast<const v4f*>(&my[row * OS + 4 * c4]);
       if (t < L) {
         float* o = out + (b * L + t) * S + s0;
-        if (vec && s0 + 4 <= s_end) {
+        if (vec && s0 + 4 <= tl.s_end) {
           __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(o));
         } else {
           for (int r = 0; r < 4; ++r)
-            if (s0 + r < s_end) o[r] = v[r];
+            if (s0 + r < tl.s_end) o[r] = v[r];
         }
       }
     }
     __builtin_amdgcn_wave_barrier();
-    if (i + 1 < nsub) {
-      store_sub(buf ^ 1);
+    if (i + 1 < tl.nsub) {
+      stage.store(kl[buf ^ 1], ksl[buf ^ 1]);
       __syncthreads();
     }
   }
+}
+
+// Gradient of the scores with respect to the head weights (the reference's autograd through
+// src/attention.py:298-300; q and k come from the non-differentiable quantizer):
+//   G[b, t, h] = sum_s relu(logit[b, t, h, s]) * (dscores[b, t, s] * k_scale[b, s])
+//   dweights   = (G * softmax_scale) * q_scale
+// Same tiling as the forward.  Each wave stages its 16 tokens' dscores rows of a sub-tile
+// through LDS (512-byte row segments in, 4 consecutive keys per lane out), recomputes the
+// logits with the MFMA and sums per (token, head) in registers.  The 4 lanes of a token
+// are summed with cross-lane adds, and each workgroup writes its key range's partial sum
+// to partial[sw][b][t][h]; k_indexer_wgrad_finish adds the ranges in increasing order.
+// Heads beyond HG take further passes over the key range.
+template <int D, int HG>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWaves<D>, 8))) void k_indexer_wgrad_fp8(
+    const uint8_t* __restrict__ q8, const uint8_t* __restrict__ k8, const float* __restrict__ ks,
+    const float* __restrict__ gs, int64_t B, int64_t L, int64_t S, int64_t H,
+    float* __restrict__ partial, int64_t tiles_t, int64_t tiles_s, int xcd_rotate, int vec) {
+  constexpr int NC = (D + 127) / 128;
+  constexpr int RS = KeyStage<D>::RS;
+  constexpr int OS = kKT + 4;
+  __shared__ __attribute__((aligned(16))) uint8_t kl[2][kKT * RS];
+  __shared__ __attribute__((aligned(16))) float ksl[2][kKT];
+  __shared__ __attribute__((aligned(16))) float gst[4 * 16 * OS];
+
+  const Tile tl = tile_of(S, tiles_t, tiles_s, xcd_rotate);
+  const int64_t b = tl.b;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l16 = lane & 15, kq = lane >> 4;
+  KeyStage<D> stage;
+  const int64_t tok = tl.tt * kTT + wave * 16 + l16;
+  const bool tok_ok = tok < L;
+  const uint8_t* qrow = q8 + (b * L + (tok_ok ? tok : 0)) * H * D;
+  float* my = gst + wave * 16 * OS;
+
+  // the wave's dscores rows of one sub-tile, 8 x 16 bytes per lane (zero past L or the range)
+  v4f gpre[8];
+  auto load_g = [&](int64_t s_sub) {
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int row = 2 * it + (lane >> 5), c4 = lane & 31;
+      const int64_t t = tl.tt * kTT + wave * 16 + row;
+      const int64_t s0 = s_sub + 4 * c4;
+      gpre[it] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      if (t < L) {
+        const float* g = gs + (b * L + t) * S + s0;
+        if (vec && s0 + 4 <= tl.s_end) {
+          gpre[it] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(g));
+        } else {
+          for (int r = 0; r < 4; ++r)
+            if (s0 + r < tl.s_end) gpre[it][r] = g[r];
+        }
+      }
+    }
+  };
+  auto store_g = [&]() {
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int row = 2 * it + (lane >> 5), c4 = lane & 31;
+      *reinterpret_cast<v4f*>(&my[row * OS + 4 * c4]) = gpre[it];
+    }
+  };
+
+  for (int64_t h0 = 0; h0 < H; h0 += HG) {
+    v8i qf[HG][NC];
+#pragma unroll
+    for (int g = 0; g < HG; ++g) {
+      const bool ok = tok_ok && h0 + g < H;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) qf[g][c] = frag32<D>(qrow + (h0 + g) * D, ok, kq, c);
+    }
+    float acc[HG];
+#pragma unroll
+    for (int g = 0; g < HG; ++g) acc[g] = 0.0f;
+    if (h0 > 0) __syncthreads();  // the previous pass is done with both key buffers
+    stage.load(k8, ks, b, S, tl.s_begin, tl.s_end, vec);
+    load_g(tl.s_begin);
+    stage.store(kl[0], ksl[0]);
+    store_g();
+    __syncthreads();
+    for (int i = 0; i < tl.nsub; ++i) {
+      const int buf = i & 1;
+      const bool more = i + 1 < tl.nsub;
+      if (more) {
+        stage.load(k8, ks, b, S, tl.s_begin + (int64_t)(i + 1) * kKT, tl.s_end, vec);
+        load_g(tl.s_begin + (int64_t)(i + 1) * kKT);
+      }
+#pragma unroll 2
+      for (int j = 0; j < 8; ++j) {
+        const uint8_t* kr = &kl[buf][(16 * j + l16) * RS];
+        v8i kf[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) kf[c] = frag32<D>(kr, true, kq, c);
+        const v4f gv = *reinterpret_cast<const v4f*>(&my[l16 * OS + 16 * j + 4 * kq]);
+        const v4f kv = *reinterpret_cast<const v4f*>(&ksl[buf][16 * j + 4 * kq]);
+        const v4f dx = v4f{gv[0] * kv[0], gv[1] * kv[1], gv[2] * kv[2], gv[3] * kv[3]};
+#pragma unroll
+        for (int g = 0; g < HG; ++g) {
+          v4f p = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+            p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(kf[c], qf[g][c], p, 0, 0, 0, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[g] = acc[g] + fmaxf(p[r], 0.0f) * dx[r];
+        }
+      }
+      if (more) {
+        // this wave's reads of its staging rows precede the overwrite (in-order LDS)
+        store_g();
+        stage.store(kl[buf ^ 1], ksl[buf ^ 1]);
+        __syncthreads();
+      }
+    }
+    // lanes l16, l16 + 16, l16 + 32, l16 + 48 hold the same token: add them
+#pragma unroll
+    for (int g = 0; g < HG; ++g) {
+      acc[g] += __shfl_xor(acc[g], 16);
+      acc[g] += __shfl_xor(acc[g], 32);
+    }
+    if (kq == 0 && tok_ok) {
+#pragma unroll
+      for (int g = 0; g < HG; ++g)
+        if (h0 + g < H) partial[((tl.sw * B + b) * L + tok) * H + h0 + g] = acc[g];
+    }
+  }
+}
+
+// dweights[i] = ((sum over key ranges, increasing) * softmax_scale) * q_scale[i], i over B L H.
+__global__ void k_indexer_wgrad_finish(const float* __restrict__ partial, const float* __restrict__ qs,
+                                       int64_t n, int64_t ranges, float softmax_scale,
+                                       float* __restrict__ dw) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float g = 0.0f;
+  for (int64_t r = 0; r < ranges; ++r) g = g + partial[r * n + i];
+  dw[i] = (g * softmax_scale) * qs[i];
 }
 
 template <int D, int HG>
@@ -210,6 +374,14 @@ void launch_indexer(unsigned grid, hipStream_t st, const uint8_t* q8, const floa
                     int xcd_rotate, int vec) {
   hipLaunchKernelGGL((k_indexer_scores_fp8<D, HG>), grid, kThreads, 0, st, q8, qs, k8, ks, w, L, S,
                      H, softmax_scale, out, tiles_t, tiles_s, xcd_rotate, vec);
+}
+
+template <int D, int HG>
+void launch_wgrad(unsigned grid, hipStream_t st, const uint8_t* q8, const uint8_t* k8,
+                  const float* ks, const float* gs, int64_t B, int64_t L, int64_t S, int64_t H,
+                  float* partial, int64_t tiles_t, int64_t tiles_s, int xcd_rotate, int vec) {
+  hipLaunchKernelGGL((k_indexer_wgrad_fp8<D, HG>), grid, kThreads, 0, st, q8, k8, ks, gs, B, L, S,
+                     H, partial, tiles_t, tiles_s, xcd_rotate, vec);
 }
 
 }  // namespace
@@ -245,6 +417,51 @@ int cin_indexer_scores_fp8(const uint8_t* q8, const float* q_scale, const uint8_
 #undef CIN_INDEXER_CASE
   }
   return cin_check_launch("indexer_scores_fp8");
+}
+
+int64_t cin_indexer_weights_grad_workspace(int64_t B, int64_t L, int64_t S, int64_t H) {
+  if (B < 0 || L < 0 || S < 0 || H < 0) return 0;
+  return cdiv(S, kKPW) * B * L * H;
+}
+
+int cin_indexer_weights_grad(const uint8_t* q8, const float* q_scale, const uint8_t* k8,
+                             const float* k_scale, const float* grad_scores, int64_t B, int64_t L,
+                             int64_t S, int64_t H, int64_t d, float softmax_scale, float* workspace,
+                             int64_t workspace_len, float* grad_weights, void* stream) {
+  CIN_CHECK_ARG(B >= 0 && L >= 0 && S >= 0 && H >= 1, "indexer_weights_grad: bad sizes");
+  CIN_CHECK_ARG(d >= 32 && d <= 256 && d % 32 == 0,
+                "indexer_weights_grad: head dim %lld must be a multiple of 32 in [32, 256]", (long long)d);
+  if (B == 0 || L == 0) return CIN_OK;
+  CIN_CHECK_ARG(q_scale && grad_weights, "indexer_weights_grad: null pointer");
+  const int64_t tiles_t = cdiv(L, kTT), tiles_s = cdiv(S, kKPW);
+  CIN_CHECK_ARG(workspace_len >= tiles_s * B * L * H,
+                "indexer_weights_grad: workspace of %lld floats, %lld needed", (long long)workspace_len,
+                (long long)(tiles_s * B * L * H));
+  CIN_CHECK_ARG(B * tiles_t * tiles_s < ((int64_t)1 << 31) && B * L * H < ((int64_t)1 << 40),
+                "indexer_weights_grad: grid too large");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (S > 0) {
+    CIN_CHECK_ARG(q8 && k8 && k_scale && grad_scores && workspace, "indexer_weights_grad: null pointer");
+    CIN_CHECK_ARG((((uintptr_t)q8) & 15) == 0 && (((uintptr_t)k8) & 15) == 0,
+                  "indexer_weights_grad: code buffers must be 16-byte aligned");
+    const unsigned grid = (unsigned)(B * tiles_t * tiles_s);
+    const int xcd_rotate = grid % 8 == 0;
+    const int vec = S % 4 == 0 && (((uintptr_t)k_scale) & 15) == 0 && (((uintptr_t)grad_scores) & 15) == 0;
+    switch (d / 32) {
+#define CIN_WGRAD_CASE(n, hg)                                                                   \
+  case n:                                                                                       \
+    launch_wgrad<32 * n, hg>(grid, st, q8, k8, k_scale, grad_scores, B, L, S, H, workspace,     \
+                             tiles_t, tiles_s, xcd_rotate, vec);                                \
+    break;
+      CIN_WGRAD_CASE(1, 4) CIN_WGRAD_CASE(2, 4) CIN_WGRAD_CASE(3, 4) CIN_WGRAD_CASE(4, 4)
+      CIN_WGRAD_CASE(5, 2) CIN_WGRAD_CASE(6, 2) CIN_WGRAD_CASE(7, 2) CIN_WGRAD_CASE(8, 2)
+#undef CIN_WGRAD_CASE
+    }
+  }
+  const int64_t n = B * L * H;
+  hipLaunchKernelGGL(k_indexer_wgrad_finish, (unsigned)cdiv(n, 256), 256, 0, st, workspace, q_scale, n,
+                     tiles_s, softmax_scale, grad_weights);
+  return cin_check_launch("indexer_weights_grad");
 }
 
 }  // extern "C"

@@ -627,7 +627,11 @@ def indexer_scores_fp8(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor,
     src/attention.py:288-300): q [B, L, H, d] and k [B, S, d] quantized row-wise (1x128,
     the first scale of each row), scores [B, L, S] fp32 = k_scale * sum_h
     relu(q_codes . k_codes) * (q_scale * weights * softmax_scale).  One fused kernel; the
-    reference's [B, L, H, S] fp32 logits are never written.  weights [B, L, H]."""
+    reference's [B, L, H, S] fp32 logits are never written.  weights [B, L, H].
+
+    Differentiable in `weights` only, as the reference's branch is: its q and k pass through
+    the quantizer, which carries no gradient (the scores feed the indexer's KL loss,
+    src/attention.py:480-502, whose gradient reaches weights_proj alone)."""
     _require(q.is_cuda and k.is_cuda and weights.is_cuda, "Input must be on CUDA")
     _require(q.ndim == 4 and k.ndim == 3 and weights.shape == q.shape[:3],
              "q must be [B, L, H, d], k [B, S, d], weights [B, L, H]")
@@ -635,8 +639,8 @@ def indexer_scores_fp8(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor,
     _require(k.shape[0] == B and k.shape[2] == d, "k must be [B, S, d] with q's B and d")
     _require(d % 32 == 0 and 32 <= d <= 256, "head dim must be a multiple of 32 in [32, 256]")
     S = k.shape[1]
-    q_fp8, q_scale = quantize_fp8_rowwise(q.reshape(-1, d).contiguous(), block_size=128)
-    k_fp8, k_scale = quantize_fp8_rowwise(k.reshape(-1, d).contiguous(), block_size=128)
+    q_fp8, q_scale = quantize_fp8_rowwise(q.detach().reshape(-1, d).contiguous(), block_size=128)
+    k_fp8, k_scale = quantize_fp8_rowwise(k.detach().reshape(-1, d).contiguous(), block_size=128)
     qs = q_scale.view(B, L, H, -1)[..., 0].contiguous()
     ks = k_scale.view(B, S, -1)[..., 0].contiguous()
     return _indexer_op(q_fp8.view(B, L, H, d), qs, k_fp8.view(B, S, d), ks,
@@ -658,6 +662,43 @@ def _indexer_op(q8, q_scale, k8, k_scale, weights, softmax_scale):
 @_indexer_op.register_fake
 def _(q8, q_scale, k8, k_scale, weights, softmax_scale):
     return q8.new_empty((q8.shape[0], q8.shape[1], k8.shape[1]), dtype=torch.float32)
+
+
+@custom_op("indexer_weights_grad_fp8",
+           "(Tensor q8, Tensor q_scale, Tensor k8, Tensor k_scale, Tensor grad_scores, float softmax_scale) -> Tensor")
+def _indexer_wgrad_op(q8, q_scale, k8, k_scale, grad_scores, softmax_scale):
+    B, L, H, d = q8.shape
+    S = k8.shape[1]
+    qc, kc = _codes_u8(q8).contiguous(), _codes_u8(k8).contiguous()
+    g = grad_scores.float().contiguous()
+    nws = max(1, _cdiv(S, 512) * B * L * H)  # one partial per 512-key range
+    ws = torch.empty(nws, dtype=torch.float32, device=q8.device)
+    dw = torch.empty((B, L, H), dtype=torch.float32, device=q8.device)
+    call("cin_indexer_weights_grad", ptr(qc), ptr(q_scale.contiguous()), ptr(kc), ptr(k_scale.contiguous()),
+         ptr(g), B, L, S, H, d, softmax_scale, ptr(ws), nws, ptr(dw), stream_of(qc))
+    return dw
+
+
+@_indexer_wgrad_op.register_fake
+def _(q8, q_scale, k8, k_scale, grad_scores, softmax_scale):
+    return q8.new_empty(q8.shape[:3], dtype=torch.float32)
+
+
+def _indexer_setup(ctx, inputs, output):
+    q8, q_scale, k8, k_scale, _weights, softmax_scale = inputs
+    ctx.save_for_backward(q8, q_scale, k8, k_scale)
+    ctx.softmax_scale = softmax_scale
+
+
+def _indexer_backward(ctx, grad):
+    q8, q_scale, k8, k_scale = ctx.saved_tensors
+    dw = None
+    if ctx.needs_input_grad[4]:
+        dw = _indexer_wgrad_op(q8, q_scale, k8, k_scale, grad, ctx.softmax_scale)
+    return None, None, None, None, dw, None
+
+
+_indexer_op.register_autograd(_indexer_backward, setup_context=_indexer_setup)
 
 
 # ---------------------------------------------------------------------------

@@ -278,6 +278,23 @@ int cin_indexer_scores_fp8(const uint8_t* q8, const float* q_scale, const uint8_
                            int64_t S, int64_t H, int64_t d, float softmax_scale, float* scores,
                            void* stream);
 
+/*
+ * Gradient of cin_indexer_scores_fp8's scores with respect to `weights`, the reference's
+ * autograd through its FP8 branch (src/attention.py:298-300; the codes come from the
+ * quantizer and carry no gradient, so q and k get none):
+ *   grad_weights[b,t,h] = ((sum_s relu(logit[b,t,h,s]) * (grad_scores[b,t,s] * k_scale[b,s]))
+ *                          * softmax_scale) * q_scale[b,t,h]
+ * with logit as in cin_indexer_scores_fp8.  grad_scores [B, L, S] and grad_weights [B, L, H]
+ * fp32, contiguous.  workspace: fp32, at least cin_indexer_weights_grad_workspace(B, L, S, H)
+ * elements (one partial sum per 512-key range, added in increasing range order, so the
+ * result is deterministic).  Same layouts and limits as cin_indexer_scores_fp8.
+ */
+int cin_indexer_weights_grad(const uint8_t* q8, const float* q_scale, const uint8_t* k8,
+                             const float* k_scale, const float* grad_scores, int64_t B, int64_t L,
+                             int64_t S, int64_t H, int64_t d, float softmax_scale, float* workspace,
+                             int64_t workspace_len, float* grad_weights, void* stream);
+int64_t cin_indexer_weights_grad_workspace(int64_t B, int64_t L, int64_t S, int64_t H);
+
 /* ---------------------------- MoE dispatch / combine ---------------------------- */
 
 /*

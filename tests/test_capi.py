@@ -14,7 +14,7 @@ HEADER = os.path.join(ROOT, "include", "cinnamon_fp8.h")
 
 def declared_symbols():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(cin_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(cin_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_entry_points():
@@ -61,6 +61,8 @@ def test_no_rpath_to_a_second_hip_runtime():
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 2, 288, 0.1, None, None)),  # d > 256
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 0, 64, 0.1, None, None)),   # H = 0
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 2, 64, 0.1, None, None)),   # null ptrs
+    ("cin_indexer_weights_grad", (None, None, None, None, None, 1, 8, 8, 2, 48, 0.1, None, 16, None, None)),
+    ("cin_indexer_weights_grad", (None, None, None, None, None, 1, 8, 8, 2, 64, 0.1, None, 15, None, None)),
 ])
 def test_invalid_arguments_rejected_without_gpu(call):
     name, args = call
@@ -78,6 +80,13 @@ def test_empty_shapes_are_noops():
     assert lib.cin_moe_gather_sum(None, 1, 8, None, 0, 2, 0, 8, None, 1, 8, None) == 0
     assert lib.cin_moe_combine(None, 8, None, 1, 2, None, 0, 2, 0, 8, None, 8, None) == 0
     assert lib.cin_indexer_scores_fp8(None, None, None, None, None, 1, 0, 8, 2, 64, 0.1, None, None) == 0
+
+
+def test_indexer_weights_grad_workspace_size():
+    lib = _lib.load()
+    assert lib.cin_indexer_weights_grad_workspace(16, 1024, 1024, 4) == 2 * 16 * 1024 * 4  # 512-key ranges
+    assert lib.cin_indexer_weights_grad_workspace(2, 100, 513, 3) == 2 * 2 * 100 * 3
+    assert lib.cin_indexer_weights_grad_workspace(64, 32768, 32768, 64) == 64 * 64 * 32768 * 64  # > 2^31
 
 
 def test_moe_route_workspace_size():

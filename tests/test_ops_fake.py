@@ -20,7 +20,7 @@ OPS = ["quant_rowwise", "quant_blockwise", "quant_blockwise_t", "quant_dual", "r
        "grouped_gemm_fp8", "quant_dual_grouped", "requant_row_to_block_grouped",
        "grouped_wgrad_fp8", "grouped_dgrad_fp8", "silu_mul_quant_rowwise", "swiglu_backward",
        "moe_route", "moe_gather_quant_rowwise", "moe_scatter_quant_rowwise", "moe_gather_sum",
-       "moe_combine", "moe_combine_backward", "indexer_scores_fp8"]
+       "moe_combine", "moe_combine_backward", "indexer_scores_fp8", "indexer_weights_grad_fp8"]
 F8, F32, BF16 = torch.float8_e4m3fn, torch.float32, torch.bfloat16
 
 
@@ -97,6 +97,12 @@ def test_shape_functions_match_the_kernels_outputs():
         ki = torch.empty(2, 90, 128, dtype=BF16, device=dev)
         wi = torch.empty(2, 100, 4, dtype=F32, device=dev)
         assert _meta(kernels.indexer_scores_fp8(qi, ki, wi, 0.125)) == ((2, 100, 90), F32, "cuda")
+        q8i = torch.empty(2, 100, 4, 128, dtype=F8, device=dev)
+        k8i = torch.empty(2, 90, 128, dtype=F8, device=dev)
+        dwi = torch.ops.cinnamon_amd.indexer_weights_grad_fp8(
+            q8i, torch.empty(2, 100, 4, device=dev), k8i, torch.empty(2, 90, device=dev),
+            torch.empty(2, 100, 90, device=dev), 0.125)
+        assert _meta(dwi) == ((2, 100, 4), F32, "cuda")
 
 
 def _op_targets(gm):
