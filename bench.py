@@ -38,7 +38,7 @@ def parse():
     p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "moe_gateup", "moe_down",
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
                                       "moe_wgrad", "moe_dgrad", "moe_layer", "moe_route",
-                                      "moe_gather", "moe_combine", "indexer", "indexer_wgrad", "copy"],
+                                      "moe_gather", "moe_combine", "indexer", "indexer_wgrad", "indexer_full", "copy"],
                    default=None,
                    help="run only one kernel in a loop (for profiler runs)")
     p.add_argument("--no-extra", action="store_true",
@@ -392,7 +392,7 @@ def main():
     # DSA indexer scores on FP8 q / k (src/attention.py:288-300) at the model's indexer shape:
     # 4 heads, d_indexer_head 64 widened to 128 by PoPE, 16 sequences of 1024 tokens
     ix = None
-    if full or args.only in ("indexer", "indexer_wgrad"):
+    if full or args.only in ("indexer", "indexer_wgrad", "indexer_full"):
         g5 = torch.Generator(device=dev).manual_seed(36)
         IB, IL, IH, ID = 16, 1024, 4, 128
         ix = dict(q=torch.randn(IB, IL, IH, ID, device=dev, generator=g5).to(torch.bfloat16),
@@ -467,7 +467,8 @@ def main():
               "requant": requant, "dgrad": dgrad, "wgrad": wgrad, "moe_dual": moe_dual,
               "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad,
               "moe_layer": moe_layer, "moe_route": moe_route, "moe_gather": moe_gather,
-              "moe_combine": moe_combine, "indexer": indexer, "indexer_wgrad": indexer_wgrad}[args.only]
+              "moe_combine": moe_combine, "indexer": indexer, "indexer_wgrad": indexer_wgrad,
+              "indexer_full": indexer_full}[args.only]
         loop = time_loop if args.only == "step" else kernel_loop
         us = loop(fn, args.steps, args.warmup)
         print(json.dumps({"only": args.only, "us_per_call": us}))

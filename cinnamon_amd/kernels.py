@@ -639,12 +639,38 @@ def indexer_scores_fp8(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor,
     _require(k.shape[0] == B and k.shape[2] == d, "k must be [B, S, d] with q's B and d")
     _require(d % 32 == 0 and 32 <= d <= 256, "head dim must be a multiple of 32 in [32, 256]")
     S = k.shape[1]
-    q_fp8, q_scale = quantize_fp8_rowwise(q.detach().reshape(-1, d).contiguous(), block_size=128)
-    k_fp8, k_scale = quantize_fp8_rowwise(k.detach().reshape(-1, d).contiguous(), block_size=128)
-    qs = q_scale.view(B, L, H, -1)[..., 0].contiguous()
-    ks = k_scale.view(B, S, -1)[..., 0].contiguous()
-    return _indexer_op(q_fp8.view(B, L, H, d), qs, k_fp8.view(B, S, d), ks,
-                       weights.float().contiguous(), float(softmax_scale))
+    q8, qs, k8, ks = _indexer_quant_op(q.detach(), k.detach())
+    return _indexer_op(q8, qs, k8, ks, weights.float().contiguous(), float(softmax_scale))
+
+
+def _aligned16(t: torch.Tensor) -> torch.Tensor:
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+@custom_op("indexer_quantize", "(Tensor q, Tensor k) -> (Tensor, Tensor, Tensor, Tensor)")
+def _indexer_quant_op(q, k):
+    """Both row-wise 1x128 quantizations of the indexer (src/attention.py:292-297) in one
+    call, keeping only each row's first scale: (q codes [B, L, H, d], q_scale [B, L, H],
+    k codes [B, S, d], k_scale [B, S]), bit-identical to quantize_fp8_rowwise."""
+    B, L, H, d = q.shape
+    S = k.shape[1]
+    q, k = _aligned16(q), _aligned16(k)
+    q8 = torch.empty((B, L, H, d), dtype=torch.float8_e4m3fn, device=q.device)
+    k8 = torch.empty((B, S, d), dtype=torch.float8_e4m3fn, device=q.device)
+    qs = torch.empty((B, L, H), dtype=torch.float32, device=q.device)
+    ks = torch.empty((B, S), dtype=torch.float32, device=q.device)
+    call("cin_indexer_quantize", ptr(q), dtype_code(q), ptr(k), dtype_code(k), B, L, S, H, d, ptr(q8),
+         ptr(qs), ptr(k8), ptr(ks), stream_of(q))
+    return q8, qs, k8, ks
+
+
+@_indexer_quant_op.register_fake
+def _(q, k):
+    B, L, H, d = q.shape
+    S = k.shape[1]
+    return (q.new_empty((B, L, H, d), dtype=torch.float8_e4m3fn), q.new_empty((B, L, H), dtype=torch.float32),
+            q.new_empty((B, S, d), dtype=torch.float8_e4m3fn), q.new_empty((B, S), dtype=torch.float32))
 
 
 @custom_op("indexer_scores_fp8",

@@ -273,6 +273,17 @@ int cin_zero_rows_outside_ranges(void* C, int64_t ldc_bytes, int64_t row_bytes, 
  * aligned), q_scale and weights [B, L, H] fp32, k_scale [B, S] fp32, scores [B, L, S] fp32.
  * d a multiple of 32 in [32, 256].
  */
+/*
+ * The two row-wise quantizations of DSAIndexer.forward's FP8 branch (reference
+ * src/attention.py:292-297) in one call: q [B*L*H, d] and k [B*S, d] (contiguous, 16-byte
+ * aligned, bf16/fp16/fp32) -> e4m3 codes (same layout, 8-byte aligned) and the FIRST 1x128
+ * scale of each row only, q_scale [B*L*H] and k_scale [B*S] fp32, the `[..., 0]` the
+ * reference keeps.  Codes and scales are bit-identical to cin_quant_rowwise(block 128).
+ */
+int cin_indexer_quantize(const void* q, int q_dtype, const void* k, int k_dtype, int64_t B,
+                         int64_t L, int64_t S, int64_t H, int64_t d, uint8_t* q8, float* q_scale,
+                         uint8_t* k8, float* k_scale, void* stream);
+
 int cin_indexer_scores_fp8(const uint8_t* q8, const float* q_scale, const uint8_t* k8,
                            const float* k_scale, const float* weights, int64_t B, int64_t L,
                            int64_t S, int64_t H, int64_t d, float softmax_scale, float* scores,

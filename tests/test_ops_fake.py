@@ -20,7 +20,7 @@ OPS = ["quant_rowwise", "quant_blockwise", "quant_blockwise_t", "quant_dual", "r
        "grouped_gemm_fp8", "quant_dual_grouped", "requant_row_to_block_grouped",
        "grouped_wgrad_fp8", "grouped_dgrad_fp8", "silu_mul_quant_rowwise", "swiglu_backward",
        "moe_route", "moe_gather_quant_rowwise", "moe_scatter_quant_rowwise", "moe_gather_sum",
-       "moe_combine", "moe_combine_backward", "indexer_scores_fp8", "indexer_weights_grad_fp8"]
+       "moe_combine", "moe_combine_backward", "indexer_scores_fp8", "indexer_weights_grad_fp8", "indexer_quantize"]
 F8, F32, BF16 = torch.float8_e4m3fn, torch.float32, torch.bfloat16
 
 
