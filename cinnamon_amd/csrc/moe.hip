@@ -236,7 +236,9 @@ __device__ inline void store4(void* base, int64_t off, int64_t nv, const float (
 }
 
 // dx[t] = sum of g[r] over token t's sorted positions r (increasing r), fp32 sums.
-// One wave per token; lane l covers columns 4 l + 256 i.
+// One wave per token; lane l covers columns 8 l + 512 i (two 16-byte pieces per row and
+// step: the rows sit at scattered sorted positions, and 2 KB runs per row read ~6% faster
+// than 1 KB runs).
 template <int GT, int OT>
 __global__ __launch_bounds__(kRT) void k_moe_gather_sum(const void* __restrict__ g, int64_t sgm,
                                                         const int32_t* __restrict__ inv,
@@ -247,17 +249,21 @@ __global__ __launch_bounds__(kRT) void k_moe_gather_sum(const void* __restrict__
   if (t >= T) return;  // uniform per wave
   int32_t pos[kMaxTopK], slot[kMaxTopK];
   const int n = token_positions(inv, t, k, A, pos, slot);
-  for (int64_t c = (int64_t)lane * 4; c < N; c += 256) {
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int64_t c = (int64_t)lane * 8; c < N; c += 512) {
+    float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
     for (int j = 0; j < kMaxTopK; ++j) {
       if (j < n) {
-        float v[4];
-        load4<GT>(g, (int64_t)pos[j] * sgm + c, N - c, v);
-        for (int e = 0; e < 4; ++e) acc[e] = acc[e] + v[e];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          float v[4];
+          load4<GT>(g, (int64_t)pos[j] * sgm + c + 4 * u, N - c - 4 * u, v);
+          for (int e = 0; e < 4; ++e) acc[u][e] = acc[u][e] + v[e];
+        }
       }
     }
-    store4<OT>(out, t * som + c, N - c, acc);
+    store4<OT>(out, t * som + c, N - c, acc[0]);
+    store4<OT>(out, t * som + c + 4, N - c - 4, acc[1]);
   }
 }
 
@@ -268,7 +274,7 @@ __device__ inline float score_at(const void* s, int64_t off) {
 
 // out[t] = sum over the token's positions r (increasing) of y[r] * score[t, slot(r)]:
 // a product then an add, both rounded (built without contraction), fp32.  One wave per
-// token; lane l covers columns 4 l + 256 i.
+// token; lane l covers columns 8 l + 512 i (as k_moe_gather_sum).
 template <int ST>
 __global__ __launch_bounds__(kRT) void k_moe_combine(const float* __restrict__ y, int64_t sym,
                                                      const void* __restrict__ scores,
@@ -283,17 +289,21 @@ __global__ __launch_bounds__(kRT) void k_moe_combine(const float* __restrict__ y
   float w[kMaxTopK];
 #pragma unroll
   for (int j = 0; j < kMaxTopK; ++j) w[j] = j < n ? score_at<ST>(scores, t * ssm + slot[j]) : 0.0f;
-  for (int64_t c = (int64_t)lane * 4; c < N; c += 256) {
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int64_t c = (int64_t)lane * 8; c < N; c += 512) {
+    float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
     for (int j = 0; j < kMaxTopK; ++j) {
       if (j < n) {
-        float v[4];
-        load4<CIN_DT_F32>(y, (int64_t)pos[j] * sym + c, N - c, v);
-        for (int e = 0; e < 4; ++e) acc[e] = acc[e] + v[e] * w[j];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          float v[4];
+          load4<CIN_DT_F32>(y, (int64_t)pos[j] * sym + c + 4 * u, N - c - 4 * u, v);
+          for (int e = 0; e < 4; ++e) acc[u][e] = acc[u][e] + v[e] * w[j];
+        }
       }
     }
-    store4<CIN_DT_F32>(out, t * som + c, N - c, acc);
+    store4<CIN_DT_F32>(out, t * som + c, N - c, acc[0]);
+    store4<CIN_DT_F32>(out, t * som + c + 4, N - c - 4, acc[1]);
   }
 }
 
