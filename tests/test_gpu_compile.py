@@ -65,6 +65,24 @@ def test_compiled_fp8_experts_match_eager(dev):
         assert torch.equal(a, b)
 
 
+def test_compiled_indexer_scores_match_eager(dev):
+    """The FP8 indexer scoring (src/attention.py:288-300) and its weights gradient in one
+    compiled graph: same kernels, bit-identical scores and gradients."""
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(2, 200, 4, 128, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(2, 200, 128, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(2, 200, 4, generator=g) * 0.5).to(dev).requires_grad_(True)
+    gs = torch.randn(2, 200, 200, generator=g).to(dev)
+
+    def step(w):
+        return (kernels.indexer_scores_fp8(q, k, w, 0.125) * gs).sum()
+
+    l0, g0 = _grads(step, [w], w)
+    compiled = torch.compile(step, backend="aot_eager", fullgraph=True)
+    l1, g1 = _grads(compiled, [w], w)
+    assert torch.equal(l0, l1) and torch.equal(g0[0], g1[0])
+
+
 def test_opcheck_operators(dev):
     g = torch.Generator(device=dev).manual_seed(2)
     x = torch.randn(256, 384, device=dev, generator=g).to(torch.bfloat16)
@@ -91,3 +109,13 @@ def test_opcheck_operators(dev):
                           test_utils=f8)
     dh = torch.randn(256, 256, device=dev, generator=g)
     torch.library.opcheck(ops.swiglu_backward.default, (dh, h12), test_utils=full)
+    # indexer: quantization (fp8 outputs), scores and weights gradient (uint8 code inputs)
+    qi = torch.randn(2, 70, 4, 128, device=dev, generator=g).to(torch.bfloat16)
+    ki = torch.randn(2, 90, 128, device=dev, generator=g).to(torch.bfloat16)
+    torch.library.opcheck(ops.indexer_quantize.default, (qi, ki), test_utils=f8)
+    q8i, qsi, k8i, ksi = ops.indexer_quantize(qi, ki)
+    wi = torch.randn(2, 70, 4, device=dev, generator=g)
+    args = (q8i.view(torch.uint8), qsi, k8i.view(torch.uint8), ksi)
+    torch.library.opcheck(ops.indexer_scores_fp8.default, (*args, wi, 0.125), test_utils=full)
+    gsi = torch.randn(2, 70, 90, device=dev, generator=g)
+    torch.library.opcheck(ops.indexer_weights_grad_fp8.default, (*args, gsi, 0.125), test_utils=full)

@@ -30,6 +30,7 @@ def _inputs(B, L, S, H, d, dtype, seed):
 
 
 def _check(got, want):
+    got, want = got.detach(), want.detach()
     assert got.shape == want.shape and got.dtype == torch.float32
     normwise = float((got - want).abs().max() / want.abs().max())
     frob = orc.frob_rel(got, want)
@@ -79,6 +80,33 @@ def test_weights_gradient_matches_the_reference_autograd(dev, B, L, S, H, d):
     wr = w.clone().requires_grad_(True)
     orc.indexer_scores_fp8_ref(q, k, wr, scale).backward(g)
     _check(wd.grad.cpu(), wr.grad)
+
+
+def test_decode_shapes_bf16_weights_and_strided_inputs(dev):
+    """One query token (decode), one key, 16 heads; bf16 weights (the gradient comes back
+    in bf16); q and k as strided views of wider buffers."""
+    g = torch.Generator().manual_seed(12)
+    for B, L, S, H, d in [(3, 1, 1, 16, 64), (2, 1, 300, 16, 128), (1, 5, 1, 2, 32)]:
+        qb = torch.randn(B, L, H, d + 32, generator=g).to(torch.bfloat16)
+        kb = torch.randn(B, S, d + 64, generator=g).to(torch.bfloat16)
+        q, k = qb[..., 16:16 + d], kb[..., 32:32 + d]
+        w = (torch.randn(B, L, H, generator=g) * 0.3).to(torch.bfloat16)
+        gs = torch.randn(B, L, S, generator=g)
+        wd = w.to(dev).requires_grad_(True)
+        got = kernels.indexer_scores_fp8(qb.to(dev)[..., 16:16 + d], kb.to(dev)[..., 32:32 + d], wd, d ** -0.5)
+        got.backward(gs.to(dev))
+        wr = w.float().requires_grad_(True)
+        want = orc.indexer_scores_fp8_ref(q.contiguous(), k.contiguous(), wr, d ** -0.5)
+        want.backward(gs)
+        _check(got.cpu(), want)
+        assert wd.grad.dtype == torch.bfloat16
+        assert _close_bf16(wd.grad.cpu(), wr.grad)
+
+
+def _close_bf16(got, want):
+    """bf16 gradient: within one bf16 rounding of the fp32 reference gradient (plus the
+    kernel's fp32 tolerance)."""
+    return bool(((got.float() - want).abs() <= 2 ** -8 * want.abs() + 1e-4 * want.abs().max()).all())
 
 
 def test_weights_gradient_is_deterministic(dev):
