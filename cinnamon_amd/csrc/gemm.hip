@@ -33,6 +33,7 @@ namespace {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128, BK = 128;
 constexpr int kThreads = 256;
@@ -488,7 +489,8 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
   // bf16 epilogue through LDS: the fragments go to a row-major tile, then every wave
   // stores 32 whole rows, 512 contiguous bytes per row (the direct stores below write
   // each row in 32-byte pieces).  All tiles finish together, so the 32 MB or so of C
-  // leave in one burst bounded by HBM write bandwidth; full rows keep it near that bound.
+  // leave in one burst bounded by HBM write bandwidth; full rows keep it near that bound,
+  // and non-temporal stores (C is not read again by this kernel) shave ~1% more.
   if (c_dtype != CIN_DT_F32 && ((((uintptr_t)T.C) & 15) == 0) && (ldc & 7) == 0) {
     __syncthreads();  // every wave is past its last fragment read
 #pragma unroll
@@ -510,7 +512,8 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
       const int m = wave * 32 + r * 2 + half;
       const uint4 v = *reinterpret_cast<const uint4*>(&smu.c[m * kCStride + c16 * 16]);
       if (m >= T.row_lo && m < T.row_hi && c16 * 8 >= T.col_lo)
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(T.C) + (int64_t)m * ldc + c16 * 8) = v;
+        __builtin_nontemporal_store(u32x4v{v.x, v.y, v.z, v.w},
+                                    reinterpret_cast<u32x4v*>(static_cast<uint16_t*>(T.C) + (int64_t)m * ldc + c16 * 8));
     }
     return;
   }
