@@ -66,11 +66,35 @@ __global__ __launch_bounds__(kRT) void k_route_hist(const int64_t* __restrict__ 
   for (int e = threadIdx.x; e < E; e += kRT) blockcounts[(int64_t)blockIdx.x * E + e] = hist[e];
 }
 
+// Exclusive prefix sum over kRT values held one per thread (Hillis-Steele in LDS); returns
+// the thread's exclusive prefix and leaves the total in *total.
+__device__ inline int64_t block_exclusive_scan(int64_t v, int64_t* buf, int64_t* total) {
+  const int tid = threadIdx.x;
+  buf[tid] = v;
+  __syncthreads();
+#pragma unroll
+  for (int off = 1; off < kRT; off <<= 1) {
+    const int64_t add = tid >= off ? buf[tid - off] : 0;
+    __syncthreads();
+    buf[tid] += add;
+    __syncthreads();
+  }
+  const int64_t incl = buf[tid];
+  *total = buf[kRT - 1];
+  __syncthreads();  // buf is reused by the caller
+  return incl - v;
+}
+
 // One workgroup: per-expert totals, expert ranges, and each (block, expert)'s first
-// sorted position (base = starts[e] + the expert's assignments in earlier blocks); the
-// unused tail of perm (dropped ids) gets -1.  The [nblocks, E] count matrix is staged
-// through LDS in row chunks (coalesced loads and stores); a thread owns an expert's
-// running sum.
+// sorted position: base = starts[e] + the expert's assignments in earlier blocks.  The
+// unused tail of perm (dropped ids) gets -1.
+//   1. totals: LDS atomics over the [nblocks, E] count matrix;
+//   2. starts: exclusive scan of the totals, each thread owning a run of experts;
+//   3. bases: the count matrix in row chunks staged through LDS (coalesced loads and
+//      stores); within a chunk, P = kRT / E threads per expert (at least 1) each sum a run
+//      of blocks, a scan over each expert's P run sums gives every run its offset, and
+//      each run is rewritten as exclusive prefixes; the expert's running total carries
+//      across chunks.
 __global__ __launch_bounds__(kRT) void k_route_scan(const int32_t* __restrict__ blockcounts,
                                                     int32_t nblocks, int32_t E, int64_t A,
                                                     int32_t* __restrict__ blockbase,
@@ -79,50 +103,83 @@ __global__ __launch_bounds__(kRT) void k_route_scan(const int32_t* __restrict__ 
                                                     int64_t* __restrict__ ends,
                                                     int64_t* __restrict__ perm) {
   __shared__ int32_t stage[kStage];
-  __shared__ int64_t tot[kMaxExperts];
-  __shared__ int64_t total_s;
+  __shared__ int32_t tot32[kMaxExperts];
+  __shared__ int64_t run[kMaxExperts];   // starts[e] + the expert's assignments so far
+  __shared__ int64_t scan_buf[kRT];
   const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += kRT) tot[e] = 0;
+  for (int e = tid; e < E; e += kRT) tot32[e] = 0;
+  __syncthreads();
+  // 1. totals (each total <= A < 2^31)
+  const int64_t nall = (int64_t)nblocks * E;
+  for (int64_t j = tid; j < nall; j += kRT) atomicAdd(&tot32[j % E], blockcounts[j]);
+  __syncthreads();
+  // 2. starts: thread t owns experts [t * per, (t + 1) * per)
+  const int per = (E + kRT - 1) / kRT;
+  const int e0 = tid * per;
+  int64_t mine = 0;
+  for (int e = e0; e < e0 + per && e < E; ++e) mine += tot32[e];
+  int64_t total = 0;
+  int64_t acc = block_exclusive_scan(mine, scan_buf, &total);
+  for (int e = e0; e < e0 + per && e < E; ++e) {
+    const int64_t c = tot32[e];
+    starts[e] = acc;
+    ends[e] = acc + c;
+    counts[e] = c;
+    run[e] = acc;
+    acc += c;
+  }
+  // 3. bases
+  const int P = E <= kRT ? kRT / E : 1;             // threads per expert
   const int rows_per = kStage / E >= 1 ? kStage / E : 1;  // E <= kMaxExperts <= kStage
   for (int b0 = 0; b0 < nblocks; b0 += rows_per) {
     const int nb = nblocks - b0 < rows_per ? nblocks - b0 : rows_per;
     const int64_t n = (int64_t)nb * E;
-    __syncthreads();  // the previous chunk's stores have read stage[]
+    __syncthreads();  // stage[] and run[] are free (previous chunk stored, starts written)
     for (int64_t j = tid; j < n; j += kRT) stage[j] = blockcounts[(int64_t)b0 * E + j];
     __syncthreads();
-    for (int e = tid; e < E; e += kRT) {
-      int64_t run = tot[e];
-      for (int b = 0; b < nb; ++b) {
-        const int32_t c = stage[b * E + e];
-        stage[b * E + e] = (int32_t)run;
-        run += c;
+    const int len = (nb + P - 1) / P;               // blocks per run
+    int64_t rsum = 0;
+    int e = -1, p = 0;
+    if (E <= kRT) {
+      if (tid < E * P) {
+        e = tid / P;
+        p = tid - e * P;
+        for (int b = p * len; b < (p + 1) * len && b < nb; ++b) rsum += stage[b * E + e];
       }
-      tot[e] = run;
+      // offsets of the runs within each expert: the P runs of an expert are P
+      // consecutive threads, so a segmented scan of width P over scan_buf gives them
+      scan_buf[tid] = rsum;
+      __syncthreads();
+      int64_t off = 0;
+      if (e >= 0)
+        for (int q = 0; q < p; ++q) off += scan_buf[tid - p + q];
+      __syncthreads();
+      if (e >= 0) {
+        int64_t r = run[e] + off;
+        for (int b = p * len; b < (p + 1) * len && b < nb; ++b) {
+          const int32_t c = stage[b * E + e];
+          stage[b * E + e] = (int32_t)r;
+          r += c;
+        }
+      }
+      __syncthreads();
+      if (e >= 0 && p == P - 1) run[e] += off + rsum;  // the last run ends the expert's chunk
+    } else {
+      // E > kRT: one thread walks each expert's blocks
+      for (int ee = tid; ee < E; ee += kRT) {
+        int64_t r = run[ee];
+        for (int b = 0; b < nb; ++b) {
+          const int32_t c = stage[b * E + ee];
+          stage[b * E + ee] = (int32_t)r;
+          r += c;
+        }
+        run[ee] = r;
+      }
     }
     __syncthreads();
     for (int64_t j = tid; j < n; j += kRT) blockbase[(int64_t)b0 * E + j] = stage[j];
   }
-  __syncthreads();
-  if (tid == 0) {
-    int64_t s = 0;
-    for (int e = 0; e < E; ++e) {
-      const int64_t c = tot[e];
-      tot[e] = s;
-      s += c;
-    }
-    total_s = s;
-  }
-  __syncthreads();
-  for (int e = tid; e < E; e += kRT) {
-    const int64_t st = tot[e];
-    const int64_t en = e + 1 < E ? tot[e + 1] : total_s;
-    starts[e] = st;
-    ends[e] = en;
-    counts[e] = en - st;
-  }
-  // the two barriers above order the chunk stores before these updates
-  for (int64_t j = tid; j < (int64_t)nblocks * E; j += kRT) blockbase[j] += (int32_t)tot[j % E];
-  for (int64_t r = total_s + tid; r < A; r += kRT) perm[r] = -1;
+  for (int64_t r = total + tid; r < A; r += kRT) perm[r] = -1;
 }
 
 // Stable scatter: an assignment's sorted position is its block's first position for its
