@@ -437,8 +437,8 @@ int cin_indexer_weights_grad(const uint8_t* q8, const float* q_scale, const uint
   CIN_CHECK_ARG(workspace_len >= tiles_s * B * L * H,
                 "indexer_weights_grad: workspace of %lld floats, %lld needed", (long long)workspace_len,
                 (long long)(tiles_s * B * L * H));
-  CIN_CHECK_ARG(B * tiles_t * tiles_s < ((int64_t)1 << 31) && B * L * H < ((int64_t)1 << 40),
-                "indexer_weights_grad: grid too large");
+  CIN_CHECK_ARG(B * tiles_t * tiles_s < ((int64_t)1 << 31) && B * L * H < ((int64_t)1 << 38),
+                "indexer_weights_grad: grid too large");  // finish grid: B L H / 256 < 2^30
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (S > 0) {
     CIN_CHECK_ARG(q8 && k8 && k_scale && grad_scores && workspace, "indexer_weights_grad: null pointer");
