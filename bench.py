@@ -357,6 +357,7 @@ def main():
         md = dict(x=moe["x"][:T3], sel=moe["sel"], scores=sc3,
                   ys=torch.randn(moe["A"], moe["D"], device=dev, generator=g4))
         md["perm"], md["inv"], *_ = moe_ops.moe_route(md["sel"], moe["E"])
+        md["ys16"] = md["ys"].half()  # routed_experts stores the sorted outputs in fp16
 
     def moe_route(i):
         moe_ops.moe_route(md["sel"], moe["E"])
@@ -365,7 +366,7 @@ def main():
         moe_ops.moe_gather_quantize(md["x"], md["perm"], moe["topk"], inv=md["inv"])
 
     def moe_combine(i):
-        moe_ops.moe_combine(md["ys"], md["scores"], md["inv"])
+        moe_ops.moe_combine(md["ys16"], md["scores"], md["inv"])
 
     def moe_dispatch_fused(i):
         perm, inv, *_ = moe_ops.moe_route(md["sel"], moe["E"])
@@ -564,10 +565,10 @@ def main():
         torch_us = time_loop(moe_dispatch_torch, 5, 1)
         ctorch_us = time_loop(moe_combine_torch, 3, 1)
         # bytes: the gather reads each token row once (its k re-reads hit the caches) and
-        # writes A code rows + scales; the combine reads the fp32 sorted rows and writes the
-        # fp32 token rows
+        # writes A code rows + scales; the combine reads the fp16 sorted rows and writes the
+        # fp32 token rows (the torch formulation reads the reference's fp32 sorted_out)
         g_bytes = T3 * D * 2 + A * D + A * (D // 128) * 4
-        c_bytes = A * D * 4 + T3 * D * 4 + A * 2 + A * 4
+        c_bytes = A * D * 2 + T3 * D * 4 + A * 2 + A * 4
         out["components"]["config3_moe_dispatch"] = {
             "what": "cinnamon_amd.moe on the config-3 routing (16384 tokens, top-8, 32 Zipf experts, "
                     "d 7168) against the reference's torch formulation on the same GPU",

@@ -119,6 +119,27 @@ __device__ inline uint32_t f32_to_bf16_bits(float f) {
   return u >> 16;
 }
 
+// fp32 -> fp16 bits, round to nearest even (overflow to inf, as a torch .half()).
+__device__ inline uint16_t f32_to_f16_bits(float f) {
+  const _Float16 h = (_Float16)f;
+  uint16_t b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
+
+// fp32 -> the bits of a 16-bit output dtype (CIN_DT_F16 or CIN_DT_BF16), RNE.
+__device__ inline uint32_t f32_to_half_bits(int dt, float f) {
+  return dt == CIN_DT_F16 ? (uint32_t)f32_to_f16_bits(f) : f32_to_bf16_bits(f);
+}
+
+// The bits of a 16-bit dtype (CIN_DT_F16 or CIN_DT_BF16) widened to fp32 (exact).
+__device__ inline float half_bits_to_f32(int dt, uint16_t bits) {
+  if (dt == CIN_DT_BF16) return __uint_as_float((uint32_t)bits << 16);
+  _Float16 h;
+  __builtin_memcpy(&h, &bits, 2);
+  return (float)h;
+}
+
 // Load one element of dtype `dt` at element index i and widen to fp32 (exact).
 __device__ inline float load_elem(const void* p, int dt, int64_t i) {
   if (dt == CIN_DT_BF16) return __uint_as_float(((uint32_t)((const uint16_t*)p)[i]) << 16);

@@ -172,8 +172,8 @@ __device__ inline void gemm_tile(const TileArgs& t, int64_t lda, int64_t ldb, in
         }
       } else {
         uint16_t* cp = static_cast<uint16_t*>(Cp) + crow * ldc + ccol;
-        const uint32_t b0 = f32_to_bf16_bits(acc[i][j][0]), b1 = f32_to_bf16_bits(acc[i][j][1]);
-        const uint32_t b2 = f32_to_bf16_bits(acc[i][j][2]), b3 = f32_to_bf16_bits(acc[i][j][3]);
+        const uint32_t b0 = f32_to_half_bits(c_dtype, acc[i][j][0]), b1 = f32_to_half_bits(c_dtype, acc[i][j][1]);
+        const uint32_t b2 = f32_to_half_bits(c_dtype, acc[i][j][2]), b3 = f32_to_half_bits(c_dtype, acc[i][j][3]);
         if (n + 4 <= ncols_valid && (((uintptr_t)cp) & 7) == 0) {
           *reinterpret_cast<uint2*>(cp) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
         } else {
@@ -499,8 +499,8 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n = wn * 64 + j * 16 + kq * 4;
-        const uint32_t b0 = f32_to_bf16_bits(acc[i][j][0]), b1 = f32_to_bf16_bits(acc[i][j][1]);
-        const uint32_t b2 = f32_to_bf16_bits(acc[i][j][2]), b3 = f32_to_bf16_bits(acc[i][j][3]);
+        const uint32_t b0 = f32_to_half_bits(c_dtype, acc[i][j][0]), b1 = f32_to_half_bits(c_dtype, acc[i][j][1]);
+        const uint32_t b2 = f32_to_half_bits(c_dtype, acc[i][j][2]), b3 = f32_to_half_bits(c_dtype, acc[i][j][3]);
         *reinterpret_cast<uint2*>(&smu.c[m * kCStride + n * 2]) =
             make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
       }
@@ -536,8 +536,8 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
         }
       } else {
         uint16_t* cp = static_cast<uint16_t*>(T.C) + (int64_t)m * ldc + n;
-        const uint32_t b0 = f32_to_bf16_bits(acc[i][j][0]), b1 = f32_to_bf16_bits(acc[i][j][1]);
-        const uint32_t b2 = f32_to_bf16_bits(acc[i][j][2]), b3 = f32_to_bf16_bits(acc[i][j][3]);
+        const uint32_t b0 = f32_to_half_bits(c_dtype, acc[i][j][0]), b1 = f32_to_half_bits(c_dtype, acc[i][j][1]);
+        const uint32_t b2 = f32_to_half_bits(c_dtype, acc[i][j][2]), b3 = f32_to_half_bits(c_dtype, acc[i][j][3]);
         if ((((uintptr_t)cp) & 7) == 0) {
           *reinterpret_cast<uint2*>(cp) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
         } else {
@@ -689,8 +689,8 @@ int cin_gemm_fp8_bs(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam
                     const uint8_t* B, int64_t ldb, const float* sb, int64_t ssbn, int64_t ssbk,
                     int64_t M, int64_t N, int64_t K, void* C, int c_dtype, int64_t ldc,
                     void* stream) {
-  CIN_CHECK_ARG(c_dtype == CIN_DT_BF16 || c_dtype == CIN_DT_F32,
-                "gemm_fp8_bs: C dtype must be bf16 or fp32");
+  CIN_CHECK_ARG(c_dtype == CIN_DT_BF16 || c_dtype == CIN_DT_F16 || c_dtype == CIN_DT_F32,
+                "gemm_fp8_bs: C dtype must be bf16, fp16 or fp32");
   CIN_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "gemm_fp8_bs: negative shape");
   if (M == 0 || N == 0) return CIN_OK;
   CIN_CHECK_ARG(C && ldc >= N, "gemm_fp8_bs: bad C");
@@ -725,8 +725,8 @@ int cin_grouped_gemm_fp8(const uint8_t* A, int64_t lda, const float* sa, int64_t
                          int64_t ssbe, int64_t ssbn, int64_t ssbk, const int64_t* starts,
                          const int64_t* ends, int64_t E, int64_t T, int64_t N, int64_t K, void* C,
                          int c_dtype, int64_t ldc, void* stream) {
-  CIN_CHECK_ARG(c_dtype == CIN_DT_BF16 || c_dtype == CIN_DT_F32,
-                "grouped_gemm_fp8: C dtype must be bf16 or fp32");
+  CIN_CHECK_ARG(c_dtype == CIN_DT_BF16 || c_dtype == CIN_DT_F16 || c_dtype == CIN_DT_F32,
+                "grouped_gemm_fp8: C dtype must be bf16, fp16 or fp32");
   CIN_CHECK_ARG(E >= 0 && T >= 0 && N >= 0 && K >= 0, "grouped_gemm_fp8: negative shape");
   if (E == 0 || T == 0 || N == 0) return CIN_OK;
   CIN_CHECK_ARG(A && B && sa && sb && starts && ends && C, "grouped_gemm_fp8: null pointer");
@@ -761,8 +761,8 @@ int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, i
                                const int64_t* starts, const int64_t* ends, int64_t E, int64_t T,
                                int64_t tcap, int64_t N, int64_t K, void* C, int c_dtype, int64_t ldc,
                                int64_t sce, void* stream) {
-  CIN_CHECK_ARG(c_dtype == CIN_DT_BF16 || c_dtype == CIN_DT_F32,
-                "grouped_wgrad_fp8: C dtype must be bf16 or fp32");
+  CIN_CHECK_ARG(c_dtype == CIN_DT_BF16 || c_dtype == CIN_DT_F16 || c_dtype == CIN_DT_F32,
+                "grouped_wgrad_fp8: C dtype must be bf16, fp16 or fp32");
   CIN_CHECK_ARG(E >= 0 && T >= 0 && N >= 0 && K >= 0, "grouped_wgrad_fp8: negative shape");
   if (E == 0 || N == 0 || K == 0) return CIN_OK;
   CIN_CHECK_ARG(A && B && sa && sb && starts && ends && C, "grouped_wgrad_fp8: null pointer");

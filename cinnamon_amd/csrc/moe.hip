@@ -34,12 +34,6 @@ constexpr int kStage = 8192;       // int32 entries of the count matrix staged i
 
 inline bool valid_dtype(int dt) { return dt == CIN_DT_BF16 || dt == CIN_DT_F32 || dt == CIN_DT_F16; }
 
-__device__ inline uint16_t f32_to_f16_bits(float f) {
-  const _Float16 h = (_Float16)f;  // round to nearest even
-  uint16_t b;
-  __builtin_memcpy(&b, &h, 2);
-  return b;
-}
 
 // Sum over the 64 lanes (a fixed butterfly: the same inputs give the same bits).
 __device__ inline float wave_sum(float v) {
@@ -271,7 +265,16 @@ __device__ inline void load4(const void* base, int64_t off, int64_t nv, float (&
       for (int e = 0; e < 4; ++e) v[e] = e < nv ? p[e] : 0.0f;
     }
   } else {
-    for (int e = 0; e < 4; ++e) v[e] = e < nv ? load_elem(base, DT, off + e) : 0.0f;
+    const uint16_t* p = static_cast<const uint16_t*>(base) + off;
+    if (nv >= 4 && (((uintptr_t)p) & 7) == 0) {
+      const uint2 w = *reinterpret_cast<const uint2*>(p);
+      const uint32_t h[2] = {w.x, w.y};
+      for (int e = 0; e < 4; ++e) {
+        v[e] = half_bits_to_f32(DT, (uint16_t)(h[e >> 1] >> (16 * (e & 1))));
+      }
+    } else {
+      for (int e = 0; e < 4; ++e) v[e] = e < nv ? load_elem(base, DT, off + e) : 0.0f;
+    }
   }
 }
 
@@ -287,8 +290,14 @@ __device__ inline void store4(void* base, int64_t off, int64_t nv, const float (
     }
   } else {
     uint16_t* p = static_cast<uint16_t*>(base) + off;
-    for (int e = 0; e < 4; ++e)
-      if (e < nv) p[e] = OT == CIN_DT_BF16 ? (uint16_t)f32_to_bf16_bits(v[e]) : f32_to_f16_bits(v[e]);
+    uint32_t b[4];
+    for (int e = 0; e < 4; ++e) b[e] = f32_to_half_bits(OT, v[e]);
+    if (nv >= 4 && (((uintptr_t)p) & 7) == 0) {
+      *reinterpret_cast<uint2*>(p) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+    } else {
+      for (int e = 0; e < 4; ++e)
+        if (e < nv) p[e] = (uint16_t)b[e];
+    }
   }
 }
 
@@ -332,8 +341,8 @@ __device__ inline float score_at(const void* s, int64_t off) {
 // out[t] = sum over the token's positions r (increasing) of y[r] * score[t, slot(r)]:
 // a product then an add, both rounded (built without contraction), fp32.  One wave per
 // token; lane l covers columns 8 l + 512 i (as k_moe_gather_sum).
-template <int ST>
-__global__ __launch_bounds__(kRT) void k_moe_combine(const float* __restrict__ y, int64_t sym,
+template <int YT, int ST>
+__global__ __launch_bounds__(kRT) void k_moe_combine(const void* __restrict__ y, int64_t sym,
                                                      const void* __restrict__ scores,
                                                      int64_t ssm, const int32_t* __restrict__ inv,
                                                      int64_t T, int k, int64_t A, int64_t N,
@@ -354,7 +363,7 @@ __global__ __launch_bounds__(kRT) void k_moe_combine(const float* __restrict__ y
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           float v[4];
-          load4<CIN_DT_F32>(y, (int64_t)pos[j] * sym + c + 4 * u, N - c - 4 * u, v);
+          load4<YT>(y, (int64_t)pos[j] * sym + c + 4 * u, N - c - 4 * u, v);
           for (int e = 0; e < 4; ++e) acc[u][e] = acc[u][e] + v[e] * w[j];
         }
       }
@@ -366,14 +375,14 @@ __global__ __launch_bounds__(kRT) void k_moe_combine(const float* __restrict__ y
 
 // Combine backward, sorted-row gradient: dy[r] = dout[t] * score[t, slot] for the
 // assignment at position r (zero rows at the unused tail).  Thread = (row, 4 columns).
-template <int ST>
+template <int ST, int DT>
 __global__ __launch_bounds__(kRT) void k_moe_combine_bwd_rows(const float* __restrict__ dout,
                                                               int64_t sdm,
                                                               const void* __restrict__ scores,
                                                               int64_t ssm,
                                                               const int64_t* __restrict__ perm,
                                                               int64_t T, int k, int64_t A,
-                                                              int64_t N, float* __restrict__ dy,
+                                                              int64_t N, void* __restrict__ dy,
                                                               int64_t sym) {
   const int64_t nq = (N + 3) / 4;
   const int64_t id = (int64_t)blockIdx.x * kRT + threadIdx.x;
@@ -387,14 +396,15 @@ __global__ __launch_bounds__(kRT) void k_moe_combine_bwd_rows(const float* __res
     load4<CIN_DT_F32>(dout, t * sdm + c, N - c, v);
     for (int e = 0; e < 4; ++e) v[e] = v[e] * w;
   }
-  store4<CIN_DT_F32>(dy, r * sym + c, N - c, v);
+  store4<DT>(dy, r * sym + c, N - c, v);
 }
 
 // Combine backward, score gradient: dscore[t, j] = sum_c dout[t, c] * y[inv[t k + j], c],
 // fp32; one wave per (token, slot), lanes over columns, then a wave sum.
+template <int YT>
 __global__ __launch_bounds__(kRT) void k_moe_combine_bwd_scores(const float* __restrict__ dout,
                                                                 int64_t sdm,
-                                                                const float* __restrict__ y,
+                                                                const void* __restrict__ y,
                                                                 int64_t sym,
                                                                 const int32_t* __restrict__ inv,
                                                                 int64_t T, int k, int64_t A,
@@ -408,8 +418,8 @@ __global__ __launch_bounds__(kRT) void k_moe_combine_bwd_scores(const float* __r
   float acc = 0.0f;
   if (p >= 0 && p < A) {
     const float* a = dout + t * sdm;
-    const float* b = y + (int64_t)p * sym;
-    for (int64_t c = lane; c < N; c += 64) acc += a[c] * b[c];
+    const int64_t yb = (int64_t)p * sym;
+    for (int64_t c = lane; c < N; c += 64) acc += a[c] * load_elem(y, YT, yb + c);
   }
   acc = wave_sum(acc);
   if (lane == 0) dscores[w] = acc;
@@ -479,10 +489,11 @@ int cin_moe_gather_sum(const void* g, int g_dtype, int64_t sgm, const int32_t* i
   return cin_check_launch("moe_gather_sum");
 }
 
-int cin_moe_combine(const float* y, int64_t sym, const void* scores, int s_dtype, int64_t ssm,
-                    const int32_t* inv, int64_t T, int64_t k, int64_t A, int64_t N, float* out,
-                    int64_t som, void* stream) {
-  CIN_CHECK_ARG(valid_dtype(s_dtype), "moe_combine: unsupported score dtype %d", s_dtype);
+int cin_moe_combine(const void* y, int y_dtype, int64_t sym, const void* scores, int s_dtype,
+                    int64_t ssm, const int32_t* inv, int64_t T, int64_t k, int64_t A, int64_t N,
+                    float* out, int64_t som, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(s_dtype) && valid_dtype(y_dtype), "moe_combine: unsupported dtype (y %d, scores %d)",
+                y_dtype, s_dtype);
   CIN_CHECK_ARG(T >= 0 && k >= 1 && k <= kMaxTopK && A >= 0 && N >= 0,
                 "moe_combine: need k in [1, %d] and non-negative sizes", kMaxTopK);
   if (T == 0 || N == 0) return CIN_OK;
@@ -491,20 +502,30 @@ int cin_moe_combine(const float* y, int64_t sym, const void* scores, int s_dtype
   CIN_CHECK_ARG(cdiv(T * 64, kRT) < ((int64_t)1 << 31), "moe_combine: grid too large");
   const unsigned grid = (unsigned)cdiv(T * 64, kRT);  // one wave per token
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (s_dtype == CIN_DT_F32)
-    hipLaunchKernelGGL((k_moe_combine<CIN_DT_F32>), grid, kRT, 0, s, y, sym, scores, ssm, inv, T, (int)k, A, N, out, som);
-  else if (s_dtype == CIN_DT_BF16)
-    hipLaunchKernelGGL((k_moe_combine<CIN_DT_BF16>), grid, kRT, 0, s, y, sym, scores, ssm, inv, T, (int)k, A, N, out, som);
-  else
-    hipLaunchKernelGGL((k_moe_combine<CIN_DT_F16>), grid, kRT, 0, s, y, sym, scores, ssm, inv, T, (int)k, A, N, out, som);
+#define CIN_COMB(YT, ST) \
+  hipLaunchKernelGGL((k_moe_combine<YT, ST>), grid, kRT, 0, s, y, sym, scores, ssm, inv, T, (int)k, A, N, out, som)
+#define CIN_COMB_S(YT)                          \
+  if (s_dtype == CIN_DT_F32) CIN_COMB(YT, CIN_DT_F32);       \
+  else if (s_dtype == CIN_DT_BF16) CIN_COMB(YT, CIN_DT_BF16); \
+  else CIN_COMB(YT, CIN_DT_F16);
+  if (y_dtype == CIN_DT_F32) {
+    CIN_COMB_S(CIN_DT_F32)
+  } else if (y_dtype == CIN_DT_F16) {
+    CIN_COMB_S(CIN_DT_F16)
+  } else {
+    CIN_COMB_S(CIN_DT_BF16)
+  }
+#undef CIN_COMB_S
+#undef CIN_COMB
   return cin_check_launch("moe_combine");
 }
 
-int cin_moe_combine_backward(const float* dout, int64_t sdm, const float* y, int64_t sym,
+int cin_moe_combine_backward(const float* dout, int64_t sdm, const void* y, int y_dtype, int64_t sym,
                              const void* scores, int s_dtype, int64_t ssm, const int64_t* perm,
                              const int32_t* inv, int64_t T, int64_t k, int64_t A, int64_t N,
-                             float* dy, int64_t sdym, float* dscores, void* stream) {
-  CIN_CHECK_ARG(valid_dtype(s_dtype), "moe_combine_backward: unsupported score dtype %d", s_dtype);
+                             void* dy, int64_t sdym, float* dscores, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(s_dtype) && valid_dtype(y_dtype),
+                "moe_combine_backward: unsupported dtype (y %d, scores %d)", y_dtype, s_dtype);
   CIN_CHECK_ARG(T >= 0 && k >= 1 && A >= 0 && N >= 0, "moe_combine_backward: bad sizes");
   CIN_CHECK_ARG(A <= T * k, "moe_combine_backward: more sorted rows than assignments");
   CIN_CHECK_ARG(dout && y && scores && perm && inv && dy && dscores, "moe_combine_backward: null pointer");
@@ -514,18 +535,32 @@ int cin_moe_combine_backward(const float* dout, int64_t sdm, const float* y, int
     const int64_t work = A * cdiv(N, 4);
     CIN_CHECK_ARG(cdiv(work, kRT) < ((int64_t)1 << 31), "moe_combine_backward: grid too large");
     const unsigned grid = (unsigned)cdiv(work, kRT);
-    if (s_dtype == CIN_DT_F32)
-      hipLaunchKernelGGL((k_moe_combine_bwd_rows<CIN_DT_F32>), grid, kRT, 0, s, dout, sdm, scores, ssm, perm, T, (int)k, A, N, dy, sdym);
-    else if (s_dtype == CIN_DT_BF16)
-      hipLaunchKernelGGL((k_moe_combine_bwd_rows<CIN_DT_BF16>), grid, kRT, 0, s, dout, sdm, scores, ssm, perm, T, (int)k, A, N, dy, sdym);
-    else
-      hipLaunchKernelGGL((k_moe_combine_bwd_rows<CIN_DT_F16>), grid, kRT, 0, s, dout, sdm, scores, ssm, perm, T, (int)k, A, N, dy, sdym);
+#define CIN_ROWS(ST, DT) \
+  hipLaunchKernelGGL((k_moe_combine_bwd_rows<ST, DT>), grid, kRT, 0, s, dout, sdm, scores, ssm, perm, T, (int)k, A, N, dy, sdym)
+#define CIN_ROWS_S(DT)                          \
+  if (s_dtype == CIN_DT_F32) CIN_ROWS(CIN_DT_F32, DT);       \
+  else if (s_dtype == CIN_DT_BF16) CIN_ROWS(CIN_DT_BF16, DT); \
+  else CIN_ROWS(CIN_DT_F16, DT);
+    if (y_dtype == CIN_DT_F32) {
+      CIN_ROWS_S(CIN_DT_F32)
+    } else if (y_dtype == CIN_DT_F16) {
+      CIN_ROWS_S(CIN_DT_F16)
+    } else {
+      CIN_ROWS_S(CIN_DT_BF16)
+    }
+#undef CIN_ROWS_S
+#undef CIN_ROWS
   }
   if (T > 0) {
     const int64_t waves = T * k;
     CIN_CHECK_ARG(cdiv(waves * 64, kRT) < ((int64_t)1 << 31), "moe_combine_backward: grid too large");
-    hipLaunchKernelGGL(k_moe_combine_bwd_scores, (unsigned)cdiv(waves * 64, kRT), kRT, 0, s, dout, sdm,
-                       y, sym, inv, T, (int)k, A, N, dscores);
+    const unsigned grid = (unsigned)cdiv(waves * 64, kRT);
+    if (y_dtype == CIN_DT_F32)
+      hipLaunchKernelGGL(k_moe_combine_bwd_scores<CIN_DT_F32>, grid, kRT, 0, s, dout, sdm, y, sym, inv, T, (int)k, A, N, dscores);
+    else if (y_dtype == CIN_DT_F16)
+      hipLaunchKernelGGL(k_moe_combine_bwd_scores<CIN_DT_F16>, grid, kRT, 0, s, dout, sdm, y, sym, inv, T, (int)k, A, N, dscores);
+    else
+      hipLaunchKernelGGL(k_moe_combine_bwd_scores<CIN_DT_BF16>, grid, kRT, 0, s, dout, sdm, y, sym, inv, T, (int)k, A, N, dscores);
   }
   return cin_check_launch("moe_combine_backward");
 }

@@ -338,12 +338,13 @@ def quantize_expert_weights(w12: torch.Tensor, w3: torch.Tensor):
 
 def experts_forward(xq: torch.Tensor, xs: torch.Tensor, w12: torch.Tensor, w3: torch.Tensor,
                     starts: torch.Tensor, ends: torch.Tensor, h_dtype: torch.dtype,
-                    weights_fp8=None):
+                    weights_fp8=None, out_dtype: torch.dtype = torch.float32):
     """FP8 SwiGLU experts on 1x128-quantized sorted rows (xq, xs): GEMM(w12), silu(h1) * h2
-    in fp32 cast to h_dtype and quantized in the same pass, GEMM(w3), fp32 out (reference
-    GroupedExperts.forward, src/layers.py:71-75).  weights_fp8: optional
-    quantize_expert_weights(w12, w3) (a weight cache).  Returns (out [T, D] fp32, saved
-    tensors for experts_backward).  Rows outside every expert range are zero."""
+    in fp32 cast to h_dtype and quantized in the same pass, GEMM(w3), out_dtype out
+    (reference GroupedExperts.forward, src/layers.py:71-75: fp32 values of an fp16 GEMM;
+    out_dtype fp16 stores them at that precision).  weights_fp8: optional
+    quantize_expert_weights(w12, w3) (a weight cache).  Returns (out [T, D], saved tensors
+    for experts_backward).  Rows outside every expert range are zero."""
     E, H2, D = w12.shape
     H = H2 // 2
     if weights_fp8 is None:
@@ -353,7 +354,7 @@ def experts_forward(xq: torch.Tensor, xs: torch.Tensor, w12: torch.Tensor, w3: t
                            starts, ends, out_dtype=torch.bfloat16, zero_uncovered=True)
     hq, hs = silu_mul_quantize_fp8(h12, out_dtype=h_dtype)
     out = fp8_grouped_gemm(hq, hs, w3q.view(E, D, H), w3s.view(E, D // 128, -1), starts, ends,
-                           out_dtype=torch.float32, zero_uncovered=True)
+                           out_dtype=out_dtype, zero_uncovered=True)
     return out, (xq, xs, w12qt, w12s, h12, hq, hs, w3qt, w3s, starts, ends)
 
 

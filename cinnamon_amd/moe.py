@@ -182,12 +182,14 @@ def _(g, inv, top_k, out_dtype):
 # ---------------------------------------------------------------------------
 def moe_combine(sorted_out: torch.Tensor, top_scores: torch.Tensor, inv: torch.Tensor) -> torch.Tensor:
     """routed_out [T, D] fp32 = sum over token t's assignments of sorted_out[r] *
-    top_scores[t, j], added in increasing sorted position r."""
+    top_scores[t, j], added in increasing sorted position r (sorted_out fp32, fp16 or bf16,
+    widened exactly)."""
     _require(sorted_out.is_cuda and top_scores.is_cuda and inv.is_cuda, "Input must be on CUDA")
     _require(top_scores.ndim == 2 and 1 <= top_scores.shape[1] <= MAX_TOP_K,
              f"top_scores must be [n_tokens, top_k] with top_k <= {MAX_TOP_K}")
     _require(inv.numel() == top_scores.numel(), "inv must hold n_tokens * top_k entries")
-    _require(sorted_out.dtype == torch.float32, "sorted_out must be fp32 (the experts' output)")
+    _require(sorted_out.dtype in (torch.float32, torch.float16, torch.bfloat16),
+             "sorted_out must be fp32, fp16 or bf16 (the experts' output)")
     return _combine_op(sorted_out, top_scores, inv.to(torch.int32))
 
 
@@ -199,8 +201,8 @@ def _combine_op(y, scores, inv):
     T, k = sc.shape
     A, D = yc.shape
     out = torch.empty((T, D), dtype=torch.float32, device=y.device)
-    call("cin_moe_combine", ptr(yc), yc.stride(0), ptr(sc), dtype_code(sc), sc.stride(0), ptr(iv), T, k,
-         A, D, ptr(out), out.stride(0), stream_of(yc))
+    call("cin_moe_combine", ptr(yc), dtype_code(yc), yc.stride(0), ptr(sc), dtype_code(sc), sc.stride(0),
+         ptr(iv), T, k, A, D, ptr(out), out.stride(0), stream_of(yc))
     return out
 
 
@@ -211,7 +213,8 @@ def _(y, scores, inv):
 
 def moe_combine_backward(dout: torch.Tensor, sorted_out: torch.Tensor, top_scores: torch.Tensor,
                          perm: torch.Tensor, inv: torch.Tensor):
-    """Gradients of moe_combine: (d sorted_out [A, D] fp32, d top_scores [T, k] fp32)."""
+    """Gradients of moe_combine: (d sorted_out [A, D] in sorted_out's dtype (RNE of the fp32
+    product), d top_scores [T, k] fp32)."""
     _require(dout.is_cuda and sorted_out.is_cuda, "Input must be on CUDA")
     return _combine_bwd_op(dout.float(), sorted_out, top_scores, perm.to(torch.int64),
                            inv.to(torch.int32))
@@ -226,17 +229,17 @@ def _combine_bwd_op(dout, y, scores, perm, inv):
     pm, iv = perm.contiguous(), inv.contiguous()
     T, k = sc.shape
     A, D = yc.shape
-    dy = torch.empty((A, D), dtype=torch.float32, device=y.device)
+    dy = torch.empty((A, D), dtype=y.dtype, device=y.device)
     ds = torch.empty((T, k), dtype=torch.float32, device=y.device)
-    call("cin_moe_combine_backward", ptr(dc), dc.stride(0), ptr(yc), yc.stride(0), ptr(sc),
-         dtype_code(sc), sc.stride(0), ptr(pm), ptr(iv), T, k, A, D, ptr(dy), dy.stride(0), ptr(ds),
-         stream_of(yc))
+    call("cin_moe_combine_backward", ptr(dc), dc.stride(0), ptr(yc), dtype_code(yc), yc.stride(0),
+         ptr(sc), dtype_code(sc), sc.stride(0), ptr(pm), ptr(iv), T, k, A, D, ptr(dy), dy.stride(0),
+         ptr(ds), stream_of(yc))
     return dy, ds
 
 
 @_combine_bwd_op.register_fake
 def _(dout, y, scores, perm, inv):
-    return (y.new_empty(y.shape, dtype=torch.float32),
+    return (y.new_empty(y.shape, dtype=y.dtype),
             y.new_empty(scores.shape, dtype=torch.float32))
 
 
@@ -244,14 +247,17 @@ def _(dout, y, scores, perm, inv):
 # Autograd and the routed-experts block
 # ---------------------------------------------------------------------------
 class FP8RoutedExpertsFunction(torch.autograd.Function):
-    """Sorted expert outputs [A, D] fp32 of the FP8 SwiGLU experts applied to x's rows in
-    routed order: the gather is fused into the activation quantization, and the backward
-    sums each token's sorted-row gradients (fp32) into dx."""
+    """Sorted expert outputs [A, D] of the FP8 SwiGLU experts applied to x's rows in routed
+    order, stored in fp16: the reference's routed experts return fp16 GEMM results
+    (src/layers.py:69-75), and fp16 halves the traffic of the down GEMM's output, the
+    combine and its backward.  The gather is fused into the activation quantization, and
+    the backward sums each token's sorted-row gradients (fp32) into dx."""
 
     @staticmethod
     def forward(ctx, x, w12, w3, perm, inv, starts, ends, top_k, weights_fp8=None):
         xq, xs = moe_gather_quantize(x, perm, top_k, inv=inv)
-        out, saved = layers.experts_forward(xq, xs, w12, w3, starts, ends, x.dtype, weights_fp8)
+        out, saved = layers.experts_forward(xq, xs, w12, w3, starts, ends, x.dtype, weights_fp8,
+                                            out_dtype=torch.float16)
         ctx.save_for_backward(*saved, inv)
         ctx.top_k = top_k
         ctx.x_dtype = x.dtype

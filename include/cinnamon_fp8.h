@@ -124,7 +124,7 @@ int cin_transpose_u8(const uint8_t* src, int64_t R, int64_t C, int64_t lds, uint
  * with its B operand given as B^T.  fp32 accumulation, fp32 epilogue.
  *   A  [M, K] codes, row stride lda;  sa indexed [m, kb] with strides (ssam, ssak)
  *   B  [N, K] codes, row stride ldb;  sb indexed [nb, kb] with strides (ssbn, ssbk)
- *   C  [M, N] of c_dtype (CIN_DT_BF16: round-to-nearest-even of the fp32 value;
+ *   C  [M, N] of c_dtype (CIN_DT_BF16 or CIN_DT_F16: round-to-nearest-even of the fp32 value;
  *      CIN_DT_F32: the fp32 value), row stride ldc
  * Requires K % 16 == 0, lda % 16 == 0, ldb % 16 == 0 and 16-byte aligned A, B.
  */
@@ -366,24 +366,26 @@ int cin_moe_gather_sum(const void* g, int g_dtype, int64_t sgm, const int32_t* i
  * Weighted combine: out[t] = sum over token t's sorted positions r, in increasing r, of
  * y[r] * score[t, slot(r)], fp32 (product and sum each rounded), i.e. the reference's
  * weighted_out = sorted_out * sorted_scores[:, None] followed by a sequential
- * routed_out.scatter_add_ (src/layers.py:151-154).  y [A, N] fp32, scores [T, k]
+ * routed_out.scatter_add_ (src/layers.py:151-154).  y [A, N] of y_dtype (fp32, or fp16 as
+ * the reference's expert outputs, src/layers.py:69-75, widened exactly), scores [T, k]
  * (s_dtype, row stride ssm), out [T, N] fp32.  k <= 16.
  */
-int cin_moe_combine(const float* y, int64_t sym, const void* scores, int s_dtype, int64_t ssm,
-                    const int32_t* inv, int64_t T, int64_t k, int64_t A, int64_t N, float* out,
-                    int64_t som, void* stream);
+int cin_moe_combine(const void* y, int y_dtype, int64_t sym, const void* scores, int s_dtype,
+                    int64_t ssm, const int32_t* inv, int64_t T, int64_t k, int64_t A, int64_t N,
+                    float* out, int64_t som, void* stream);
 
 /*
  * Backward of cin_moe_combine: dy[r] = dout[t] * score[t, j] for the assignment t*k + j at
  * sorted position r (zero rows where perm is -1), and dscores[t, j] = sum_c dout[t, c] *
  * y[inv[t*k + j], c] (fp32, 0 for dropped assignments); the autograd of reference
- * src/layers.py:151-154.  dout [T, N] fp32, y [A, N] fp32, dy [A, N] fp32, dscores [T, k]
+ * src/layers.py:151-154.  dout [T, N] fp32, y [A, N] and dy [A, N] of y_dtype (dy rounded to
+ * it, RNE), dscores [T, k]
  * fp32 contiguous.
  */
-int cin_moe_combine_backward(const float* dout, int64_t sdm, const float* y, int64_t sym,
+int cin_moe_combine_backward(const float* dout, int64_t sdm, const void* y, int y_dtype, int64_t sym,
                              const void* scores, int s_dtype, int64_t ssm, const int64_t* perm,
                              const int32_t* inv, int64_t T, int64_t k, int64_t A, int64_t N,
-                             float* dy, int64_t sdym, float* dscores, void* stream);
+                             void* dy, int64_t sdym, float* dscores, void* stream);
 
 #ifdef __cplusplus
 }

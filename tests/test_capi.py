@@ -55,7 +55,8 @@ def test_no_rpath_to_a_second_hip_runtime():
     ("cin_moe_route", (None, 16, 2, 5000, None, None, None, None, None, None, 0, None)),     # E > 4096
     ("cin_moe_route", (None, 16, 2, 8, None, None, None, None, None, None, 0, None)),        # null ptrs
     ("cin_moe_gather_sum", (None, 1, 8, None, 4, 17, 68, 8, None, 1, 8, None)),              # k > 16
-    ("cin_moe_combine", (None, 8, None, 7, 2, None, 4, 2, 8, 8, None, 8, None)),             # bad dtype
+    ("cin_moe_combine", (None, 1, 8, None, 7, 2, None, 4, 2, 8, 8, None, 8, None)),          # bad score dtype
+    ("cin_moe_combine", (None, 5, 8, None, 1, 2, None, 4, 2, 8, 8, None, 8, None)),          # bad y dtype
     ("cin_moe_gather_quant_rowwise", (None, 0, 4, 256, 256, None, 8, 0, 0, None, 256, None, 2, None)),
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 2, 48, 0.1, None, None)),   # d % 32
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 2, 288, 0.1, None, None)),  # d > 256
@@ -78,7 +79,7 @@ def test_empty_shapes_are_noops():
     assert lib.cin_quant_rowwise(None, 0, 0, 128, 128, 1, 128, 0, None, 128, None, 1, None) == 0
     assert lib.cin_gemm_fp8_bs(None, 32, None, 1, 1, None, 32, None, 1, 1, 0, 4, 32, None, 0, 4, None) == 0
     assert lib.cin_moe_gather_sum(None, 1, 8, None, 0, 2, 0, 8, None, 1, 8, None) == 0
-    assert lib.cin_moe_combine(None, 8, None, 1, 2, None, 0, 2, 0, 8, None, 8, None) == 0
+    assert lib.cin_moe_combine(None, 1, 8, None, 1, 2, None, 0, 2, 0, 8, None, 8, None) == 0
     assert lib.cin_indexer_scores_fp8(None, None, None, None, None, 1, 0, 8, 2, 64, 0.1, None, None) == 0
 
 

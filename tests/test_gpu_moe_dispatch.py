@@ -8,9 +8,10 @@ MoE.forward routing block (src/layers.py:126-157).
   increasing sorted position, the order of a sequential scatter_add_).
 - Combine backward: the row gradient is exact; the score gradient (a 7168-term dot
   product) is within 1e-5 relative of fp64.
-- routed_experts end to end: sorted expert outputs, routed output and weight gradients
-  equal the unfused composition (route -> x[token_indices] -> GroupedExperts -> combine)
-  bit for bit. dx and the score gradients agree within the stated tolerances.
+- routed_experts end to end: sorted expert outputs (stored in fp16, as the reference's
+  fp16 expert GEMMs return them), routed output and weight gradients equal the unfused
+  composition (route -> x[token_indices] -> GroupedExperts -> fp16 -> combine); dx and the
+  score gradients agree within the stated tolerances.
 """
 import pytest
 import torch
@@ -113,34 +114,37 @@ def test_gather_sum_in_sorted_order(dev, gdtype, odtype):
     assert torch.equal(out.cpu(), want)
 
 
-@pytest.mark.parametrize("sdtype", [torch.bfloat16, torch.float32])
-def test_combine_equals_reference_scatter_add(dev, sdtype):
+@pytest.mark.parametrize("sdtype,ydtype", [(torch.bfloat16, torch.float32), (torch.float32, torch.float32),
+                                           (torch.float32, torch.float16), (torch.bfloat16, torch.float16)])
+def test_combine_equals_reference_scatter_add(dev, sdtype, ydtype):
     T, k, E, D = 512, 8, 32, 7168
     top_idx, scores = _routing(T, k, E, seed=7)
     scores = scores.to(sdtype)
-    y = torch.randn(T * k, D, generator=torch.Generator().manual_seed(8))
+    y = torch.randn(T * k, D, generator=torch.Generator().manual_seed(8)).to(ydtype).float()
     perm, inv, *_ = moe.moe_route(top_idx.to(dev), E)
-    out = moe.moe_combine(y.to(dev), scores.to(dev), inv)
+    out = moe.moe_combine(y.to(ydtype).to(dev), scores.to(dev), inv)
     order, *_ = orc.moe_dispatch_ref(top_idx, E)
     want = orc.moe_combine_ref(y, scores, order, T)
     assert torch.equal(out.cpu(), want)
 
 
-def test_combine_backward(dev):
+@pytest.mark.parametrize("ydtype", [torch.float32, torch.float16])
+def test_combine_backward(dev, ydtype):
     T, k, E, D = 256, 4, 10, 7168
     top_idx, scores = _routing(T, k, E, seed=9)
     scores = scores.to(torch.bfloat16)
     g = torch.Generator().manual_seed(10)
-    y = torch.randn(T * k, D, generator=g)
+    y = torch.randn(T * k, D, generator=g).to(ydtype).float()
     dout = torch.randn(T, D, generator=g)
     perm, inv, *_ = moe.moe_route(top_idx.to(dev), E)
-    dy, ds = moe.moe_combine_backward(dout.to(dev), y.to(dev), scores.to(dev), perm, inv)
+    dy, ds = moe.moe_combine_backward(dout.to(dev), y.to(ydtype).to(dev), scores.to(dev), perm, inv)
+    assert dy.dtype == ydtype  # the row gradient in y's dtype: RNE of the fp32 product
     # reference autograd of weighted_out = sorted_out * sorted_scores[:, None] + scatter_add_
     order, *_ = orc.moe_dispatch_ref(top_idx, E)
     yr = y.clone().requires_grad_(True)
     sr = scores.float().clone().requires_grad_(True)
     orc.moe_combine_ref(yr, sr, order, T).backward(dout)
-    assert torch.equal(dy.cpu(), yr.grad)
+    assert torch.equal(dy.cpu(), yr.grad.to(ydtype))
     exact = torch.zeros(T, k, dtype=torch.float64)
     pos = inv.cpu().long().view(T, k)
     for j in range(k):
@@ -172,7 +176,7 @@ def test_routed_experts_equal_the_unfused_composition(dev):
     xu = x.clone().requires_grad_(True)
     su = scores.clone().requires_grad_(True)
     sorted_x = xu[perm // k]
-    sorted_out = experts(sorted_x, starts, ends)
+    sorted_out = experts(sorted_x, starts, ends).half().float()
     sorted_scores = su.reshape(-1)[perm]
     weighted = sorted_out * sorted_scores[:, None]
     out_u = torch.zeros(T, D, device=dev, dtype=weighted.dtype)

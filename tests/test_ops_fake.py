@@ -196,8 +196,9 @@ def test_moe_dispatch_shape_functions_and_trace():
         perm, inv, counts, ys, out, dys, dsc, dx, dw12, dw3 = step(x, w12, w3, top_idx, scores, dout)
         assert _meta(perm) == ((T * k,), torch.int64, "cuda") and _meta(inv) == ((T * k,), torch.int32, "cuda")
         assert _meta(counts) == ((E,), torch.int64, "cuda")
-        assert _meta(ys) == ((T * k, D), F32, "cuda") and _meta(out) == ((T, D), F32, "cuda")
-        assert _meta(dys) == ((T * k, D), F32, "cuda") and _meta(dsc) == ((T, k), F32, "cuda")
+        # sorted expert outputs and their gradient in fp16 (the reference's expert GEMMs are fp16)
+        assert _meta(ys) == ((T * k, D), torch.float16, "cuda") and _meta(out) == ((T, D), F32, "cuda")
+        assert _meta(dys) == ((T * k, D), torch.float16, "cuda") and _meta(dsc) == ((T, k), F32, "cuda")
         assert _meta(dx) == ((T, D), BF16, "cuda") and dw12.shape == (E, 2 * H, D) and dw3.shape == (E, D, H)
         q, s = moe.moe_gather_quantize(x, perm, k)
         assert _meta(q) == ((T * k, D), F8, "cuda") and _meta(s) == ((T * k, 2), F32, "cuda")
