@@ -278,6 +278,20 @@ __device__ inline void load4(const void* base, int64_t off, int64_t nv, float (&
   }
 }
 
+// 8 consecutive 16-bit values (bf16 or fp16) widened to fp32; one 16-byte load when whole
+// and aligned, zeros past nv.
+template <int DT>
+__device__ inline void load8h(const void* base, int64_t off, int64_t nv, float (&v)[8]) {
+  const uint16_t* p = static_cast<const uint16_t*>(base) + off;
+  if (nv >= 8 && (((uintptr_t)p) & 15) == 0) {
+    const uint4 w = *reinterpret_cast<const uint4*>(p);
+    const uint32_t h[4] = {w.x, w.y, w.z, w.w};
+    for (int e = 0; e < 8; ++e) v[e] = half_bits_to_f32(DT, (uint16_t)(h[e >> 1] >> (16 * (e & 1))));
+  } else {
+    for (int e = 0; e < 8; ++e) v[e] = e < nv ? load_elem(base, DT, off + e) : 0.0f;
+  }
+}
+
 template <int OT>
 __device__ inline void store4(void* base, int64_t off, int64_t nv, const float (&v)[4]) {
   if constexpr (OT == CIN_DT_F32) {
@@ -340,7 +354,8 @@ __device__ inline float score_at(const void* s, int64_t off) {
 
 // out[t] = sum over the token's positions r (increasing) of y[r] * score[t, slot(r)]:
 // a product then an add, both rounded (built without contraction), fp32.  One wave per
-// token; lane l covers columns 8 l + 512 i (as k_moe_gather_sum).
+// token; lane l covers columns 8 l + 512 i of fp32 rows (as k_moe_gather_sum) and
+// 16 l + 1024 i of 16-bit rows: 2 KB runs per scattered row either way.
 template <int YT, int ST>
 __global__ __launch_bounds__(kRT) void k_moe_combine(const void* __restrict__ y, int64_t sym,
                                                      const void* __restrict__ scores,
@@ -355,21 +370,46 @@ __global__ __launch_bounds__(kRT) void k_moe_combine(const void* __restrict__ y,
   float w[kMaxTopK];
 #pragma unroll
   for (int j = 0; j < kMaxTopK; ++j) w[j] = j < n ? score_at<ST>(scores, t * ssm + slot[j]) : 0.0f;
-  for (int64_t c = (int64_t)lane * 8; c < N; c += 512) {
-    float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  if constexpr (YT == CIN_DT_F32) {
+    for (int64_t c = (int64_t)lane * 8; c < N; c += 512) {
+      float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j) {
-      if (j < n) {
+      for (int j = 0; j < kMaxTopK; ++j) {
+        if (j < n) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          float v[4];
-          load4<YT>(y, (int64_t)pos[j] * sym + c + 4 * u, N - c - 4 * u, v);
-          for (int e = 0; e < 4; ++e) acc[u][e] = acc[u][e] + v[e] * w[j];
+          for (int u = 0; u < 2; ++u) {
+            float v[4];
+            load4<YT>(y, (int64_t)pos[j] * sym + c + 4 * u, N - c - 4 * u, v);
+            for (int e = 0; e < 4; ++e) acc[u][e] = acc[u][e] + v[e] * w[j];
+          }
         }
       }
+      store4<CIN_DT_F32>(out, t * som + c, N - c, acc[0]);
+      store4<CIN_DT_F32>(out, t * som + c + 4, N - c - 4, acc[1]);
     }
-    store4<CIN_DT_F32>(out, t * som + c, N - c, acc[0]);
-    store4<CIN_DT_F32>(out, t * som + c + 4, N - c - 4, acc[1]);
+  } else {
+    // 16-bit rows: 16 columns per lane (two 16-byte loads), the same 2 KB runs per row
+    for (int64_t c = (int64_t)lane * 16; c < N; c += 1024) {
+      float acc[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kMaxTopK; ++j) {
+        if (j < n) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            float v[8];
+            load8h<YT>(y, (int64_t)pos[j] * sym + c + 8 * u, N - c - 8 * u, v);
+            for (int e = 0; e < 8; ++e) acc[8 * u + e] = acc[8 * u + e] + v[e] * w[j];
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a4[4] = {acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+        store4<CIN_DT_F32>(out, t * som + c + 4 * q, N - c - 4 * q, a4);
+      }
+    }
   }
 }
 
