@@ -38,7 +38,7 @@ def parse():
     p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "moe_gateup", "moe_down",
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
                                       "moe_wgrad", "moe_dgrad", "moe_layer", "moe_route",
-                                      "moe_gather", "moe_combine", "indexer", "indexer_wgrad", "indexer_full", "copy"],
+                                      "moe_gather", "moe_combine", "moe_combine_bwd", "indexer", "indexer_wgrad", "indexer_full", "copy"],
                    default=None,
                    help="run only one kernel in a loop (for profiler runs)")
     p.add_argument("--no-extra", action="store_true",
@@ -346,7 +346,7 @@ def main():
     # config 3 dispatch and combine around the experts (cinnamon_amd.moe) against the
     # reference's torch formulation of the same block (src/layers.py:133-154)
     md = None
-    if full or args.only in ("moe_route", "moe_gather", "moe_combine"):
+    if full or args.only in ("moe_route", "moe_gather", "moe_combine", "moe_combine_bwd"):
         from cinnamon_amd import moe as moe_ops
         if moe is None:
             moe = moe_setup(dev)
@@ -358,6 +358,7 @@ def main():
                   ys=torch.randn(moe["A"], moe["D"], device=dev, generator=g4))
         md["perm"], md["inv"], *_ = moe_ops.moe_route(md["sel"], moe["E"])
         md["ys16"] = md["ys"].half()  # routed_experts stores the sorted outputs in fp16
+        md["dout"] = torch.randn(T3, moe["D"], device=dev, generator=g4)
 
     def moe_route(i):
         moe_ops.moe_route(md["sel"], moe["E"])
@@ -367,6 +368,9 @@ def main():
 
     def moe_combine(i):
         moe_ops.moe_combine(md["ys16"], md["scores"], md["inv"])
+
+    def moe_combine_bwd(i):
+        moe_ops.moe_combine_backward(md["dout"], md["ys16"], md["scores"], md["perm"], md["inv"])
 
     def moe_dispatch_fused(i):
         perm, inv, *_ = moe_ops.moe_route(md["sel"], moe["E"])
@@ -468,7 +472,7 @@ def main():
               "requant": requant, "dgrad": dgrad, "wgrad": wgrad, "moe_dual": moe_dual,
               "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad,
               "moe_layer": moe_layer, "moe_route": moe_route, "moe_gather": moe_gather,
-              "moe_combine": moe_combine, "indexer": indexer, "indexer_wgrad": indexer_wgrad,
+              "moe_combine": moe_combine, "moe_combine_bwd": moe_combine_bwd, "indexer": indexer, "indexer_wgrad": indexer_wgrad,
               "indexer_full": indexer_full}[args.only]
         loop = time_loop if args.only == "step" else kernel_loop
         us = loop(fn, args.steps, args.warmup)
@@ -561,6 +565,7 @@ def main():
         r_us = kernel_loop(moe_route, 20, 3)
         g_us = kernel_loop(moe_gather, 10, 2)
         c_us = kernel_loop(moe_combine, 5, 1)
+        cb_us = kernel_loop(moe_combine_bwd, 5, 1)
         fused_us = time_loop(moe_dispatch_fused, 5, 1)
         torch_us = time_loop(moe_dispatch_torch, 5, 1)
         ctorch_us = time_loop(moe_combine_torch, 3, 1)
@@ -580,6 +585,7 @@ def main():
             "combine_us": round(c_us, 1), "combine_gbps": round(c_bytes / c_us / 1e3, 1),
             "combine_frac_of_hbm": round(c_bytes / c_us / 1e3 / PEAK_HBM_GBPS, 4),
             "torch_sort_mul_scatter_add_us": round(ctorch_us, 1),
+            "combine_backward_us": round(cb_us, 1),
         }
     if ix is not None:
         IB, IL, IH, ID = ix["shape"]

@@ -119,8 +119,12 @@ __device__ inline uint32_t f32_to_bf16_bits(float f) {
   return u >> 16;
 }
 
-// fp32 -> fp16 bits, round to nearest even (overflow to inf, as a torch .half()).
+// fp32 -> fp16 bits, round to nearest even (overflow to inf, as a torch .half()).  The
+// empty asm pins f as an fp32 value: otherwise the compiler may fuse the multiply or FMA
+// that produced it with this conversion into one mixed-precision instruction (one rounding
+// of the exact result to fp16), which differs from fp32-then-fp16 at fp32 ties.
 __device__ inline uint16_t f32_to_f16_bits(float f) {
+  asm volatile("" : "+v"(f));
   const _Float16 h = (_Float16)f;
   uint16_t b;
   __builtin_memcpy(&b, &h, 2);

@@ -413,56 +413,88 @@ __global__ __launch_bounds__(kRT) void k_moe_combine(const void* __restrict__ y,
   }
 }
 
-// Combine backward, sorted-row gradient: dy[r] = dout[t] * score[t, slot] for the
-// assignment at position r (zero rows at the unused tail).  Thread = (row, 4 columns).
-template <int ST, int DT>
-__global__ __launch_bounds__(kRT) void k_moe_combine_bwd_rows(const float* __restrict__ dout,
-                                                              int64_t sdm,
-                                                              const void* __restrict__ scores,
-                                                              int64_t ssm,
-                                                              const int64_t* __restrict__ perm,
-                                                              int64_t T, int k, int64_t A,
-                                                              int64_t N, void* __restrict__ dy,
-                                                              int64_t sym) {
-  const int64_t nq = (N + 3) / 4;
-  const int64_t id = (int64_t)blockIdx.x * kRT + threadIdx.x;
-  if (id >= A * nq) return;
-  const int64_t r = id / nq, c = (id - r * nq) * 4;
-  const int64_t i = perm[r];
-  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (i >= 0 && i < T * k) {
-    const int64_t t = i / k, j = i - t * k;
-    const float w = score_at<ST>(scores, t * ssm + j);
-    load4<CIN_DT_F32>(dout, t * sdm + c, N - c, v);
-    for (int e = 0; e < 4; ++e) v[e] = v[e] * w;
+// Combine backward, both gradients in one pass per token (one wave): the token's dout row
+// is read once; for each of its sorted positions r (increasing), y[r] is read for the score
+// gradient dscore[t, j] = sum_c dout[t, c] * y[r, c] (lane l over columns 8 l + 512 i, then
+// a wave sum) and dy[r] = dout[t] * score[t, j] is written in y's dtype.  Slots whose
+// assignment was dropped get dscore 0; the dy rows no assignment maps to are zeroed by
+// k_moe_zero_unmapped_rows.
+template <int ST, int YT>
+__global__ __launch_bounds__(kRT) void k_moe_combine_bwd_tokens(
+    const float* __restrict__ dout, int64_t sdm, const void* __restrict__ y, int64_t sym,
+    const void* __restrict__ scores, int64_t ssm, const int32_t* __restrict__ inv, int64_t T,
+    int k, int64_t A, int64_t N, void* __restrict__ dy, int64_t sdym, float* __restrict__ dscores) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = ((int64_t)blockIdx.x * kRT + threadIdx.x) >> 6;
+  if (t >= T) return;  // uniform per wave
+  int32_t pos[kMaxTopK], slot[kMaxTopK];
+  const int n = token_positions(inv, t, k, A, pos, slot);
+  float w[kMaxTopK], acc[kMaxTopK];
+#pragma unroll
+  for (int j = 0; j < kMaxTopK; ++j) {
+    w[j] = j < n ? score_at<ST>(scores, t * ssm + slot[j]) : 0.0f;
+    acc[j] = 0.0f;
   }
-  store4<DT>(dy, r * sym + c, N - c, v);
+  const int64_t db = t * sdm;
+  for (int64_t c = (int64_t)lane * 8; c < N; c += 512) {
+    float a[2][4];
+    load4<CIN_DT_F32>(dout, db + c, N - c, a[0]);
+    load4<CIN_DT_F32>(dout, db + c + 4, N - c - 4, a[1]);
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j) {
+      if (j < n) {
+        const int64_t yb = (int64_t)pos[j] * sym;
+        float b[8];
+        if constexpr (YT == CIN_DT_F32) {
+          float b0[4], b1[4];
+          load4<CIN_DT_F32>(y, yb + c, N - c, b0);
+          load4<CIN_DT_F32>(y, yb + c + 4, N - c - 4, b1);
+          for (int e = 0; e < 4; ++e) {
+            b[e] = b0[e];
+            b[4 + e] = b1[e];
+          }
+        } else {
+          load8h<YT>(y, yb + c, N - c, b);
+        }
+        for (int e = 0; e < 8; ++e) acc[j] += a[e >> 2][e & 3] * b[e];
+        float d0[4], d1[4];
+        for (int e = 0; e < 4; ++e) {
+          d0[e] = a[0][e] * w[j];
+          d1[e] = a[1][e] * w[j];
+        }
+        const int64_t ob = (int64_t)pos[j] * sdym;
+        store4<YT>(dy, ob + c, N - c, d0);
+        store4<YT>(dy, ob + c + 4, N - c - 4, d1);
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kMaxTopK; ++j) {
+    if (j < n) {
+      const float sum = wave_sum(acc[j]);
+      if (lane == 0) dscores[t * k + slot[j]] = sum;
+    }
+  }
+  for (int j = lane; j < k; j += 64) {
+    const int32_t p = inv[t * k + j];
+    if (p < 0 || p >= A) dscores[t * k + j] = 0.0f;
+  }
 }
 
-// Combine backward, score gradient: dscore[t, j] = sum_c dout[t, c] * y[inv[t k + j], c],
-// fp32; one wave per (token, slot), lanes over columns, then a wave sum.
-template <int YT>
-__global__ __launch_bounds__(kRT) void k_moe_combine_bwd_scores(const float* __restrict__ dout,
-                                                                int64_t sdm,
-                                                                const void* __restrict__ y,
-                                                                int64_t sym,
-                                                                const int32_t* __restrict__ inv,
+// dy rows that no assignment maps to (perm[r] < 0) are zero.  One wave per row; the rows
+// an assignment maps to exit at once.
+template <int DT>
+__global__ __launch_bounds__(kRT) void k_moe_zero_unmapped_rows(const int64_t* __restrict__ perm,
                                                                 int64_t T, int k, int64_t A,
-                                                                int64_t N,
-                                                                float* __restrict__ dscores) {
+                                                                int64_t N, void* __restrict__ dy,
+                                                                int64_t sdym) {
   const int lane = threadIdx.x & 63;
-  const int64_t w = ((int64_t)blockIdx.x * kRT + threadIdx.x) >> 6;
-  if (w >= T * k) return;  // uniform per wave
-  const int64_t t = w / k;
-  const int32_t p = inv[w];
-  float acc = 0.0f;
-  if (p >= 0 && p < A) {
-    const float* a = dout + t * sdm;
-    const int64_t yb = (int64_t)p * sym;
-    for (int64_t c = lane; c < N; c += 64) acc += a[c] * load_elem(y, YT, yb + c);
-  }
-  acc = wave_sum(acc);
-  if (lane == 0) dscores[w] = acc;
+  const int64_t r = ((int64_t)blockIdx.x * kRT + threadIdx.x) >> 6;
+  if (r >= A) return;
+  const int64_t i = perm[r];
+  if (i >= 0 && i < T * k) return;  // uniform per wave
+  const float z[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int64_t c = (int64_t)lane * 4; c < N; c += 256) store4<DT>(dy, r * sdym + c, N - c, z);
 }
 
 }  // namespace
@@ -572,35 +604,35 @@ int cin_moe_combine_backward(const float* dout, int64_t sdm, const void* y, int 
   CIN_CHECK_ARG(sdm >= N && sym >= N && sdym >= N && ssm >= k, "moe_combine_backward: bad strides");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (A > 0 && N > 0) {
-    const int64_t work = A * cdiv(N, 4);
-    CIN_CHECK_ARG(cdiv(work, kRT) < ((int64_t)1 << 31), "moe_combine_backward: grid too large");
-    const unsigned grid = (unsigned)cdiv(work, kRT);
-#define CIN_ROWS(ST, DT) \
-  hipLaunchKernelGGL((k_moe_combine_bwd_rows<ST, DT>), grid, kRT, 0, s, dout, sdm, scores, ssm, perm, T, (int)k, A, N, dy, sdym)
-#define CIN_ROWS_S(DT)                          \
-  if (s_dtype == CIN_DT_F32) CIN_ROWS(CIN_DT_F32, DT);       \
-  else if (s_dtype == CIN_DT_BF16) CIN_ROWS(CIN_DT_BF16, DT); \
-  else CIN_ROWS(CIN_DT_F16, DT);
-    if (y_dtype == CIN_DT_F32) {
-      CIN_ROWS_S(CIN_DT_F32)
-    } else if (y_dtype == CIN_DT_F16) {
-      CIN_ROWS_S(CIN_DT_F16)
-    } else {
-      CIN_ROWS_S(CIN_DT_BF16)
-    }
-#undef CIN_ROWS_S
-#undef CIN_ROWS
+    CIN_CHECK_ARG(cdiv(A * 64, kRT) < ((int64_t)1 << 31), "moe_combine_backward: grid too large");
+    const unsigned grid = (unsigned)cdiv(A * 64, kRT);  // one wave per sorted row
+    if (y_dtype == CIN_DT_F32)
+      hipLaunchKernelGGL(k_moe_zero_unmapped_rows<CIN_DT_F32>, grid, kRT, 0, s, perm, T, (int)k, A, N, dy, sdym);
+    else if (y_dtype == CIN_DT_F16)
+      hipLaunchKernelGGL(k_moe_zero_unmapped_rows<CIN_DT_F16>, grid, kRT, 0, s, perm, T, (int)k, A, N, dy, sdym);
+    else
+      hipLaunchKernelGGL(k_moe_zero_unmapped_rows<CIN_DT_BF16>, grid, kRT, 0, s, perm, T, (int)k, A, N, dy, sdym);
   }
   if (T > 0) {
-    const int64_t waves = T * k;
-    CIN_CHECK_ARG(cdiv(waves * 64, kRT) < ((int64_t)1 << 31), "moe_combine_backward: grid too large");
-    const unsigned grid = (unsigned)cdiv(waves * 64, kRT);
-    if (y_dtype == CIN_DT_F32)
-      hipLaunchKernelGGL(k_moe_combine_bwd_scores<CIN_DT_F32>, grid, kRT, 0, s, dout, sdm, y, sym, inv, T, (int)k, A, N, dscores);
-    else if (y_dtype == CIN_DT_F16)
-      hipLaunchKernelGGL(k_moe_combine_bwd_scores<CIN_DT_F16>, grid, kRT, 0, s, dout, sdm, y, sym, inv, T, (int)k, A, N, dscores);
-    else
-      hipLaunchKernelGGL(k_moe_combine_bwd_scores<CIN_DT_BF16>, grid, kRT, 0, s, dout, sdm, y, sym, inv, T, (int)k, A, N, dscores);
+    CIN_CHECK_ARG(k <= kMaxTopK, "moe_combine_backward: k must be at most %d", kMaxTopK);
+    CIN_CHECK_ARG(cdiv(T * 64, kRT) < ((int64_t)1 << 31), "moe_combine_backward: grid too large");
+    const unsigned grid = (unsigned)cdiv(T * 64, kRT);  // one wave per token
+#define CIN_TOK(ST, YT)                                                                          \
+  hipLaunchKernelGGL((k_moe_combine_bwd_tokens<ST, YT>), grid, kRT, 0, s, dout, sdm, y, sym, scores, ssm, \
+                     inv, T, (int)k, A, N, dy, sdym, dscores)
+#define CIN_TOK_S(YT)                           \
+  if (s_dtype == CIN_DT_F32) CIN_TOK(CIN_DT_F32, YT);       \
+  else if (s_dtype == CIN_DT_BF16) CIN_TOK(CIN_DT_BF16, YT); \
+  else CIN_TOK(CIN_DT_F16, YT);
+    if (y_dtype == CIN_DT_F32) {
+      CIN_TOK_S(CIN_DT_F32)
+    } else if (y_dtype == CIN_DT_F16) {
+      CIN_TOK_S(CIN_DT_F16)
+    } else {
+      CIN_TOK_S(CIN_DT_BF16)
+    }
+#undef CIN_TOK_S
+#undef CIN_TOK
   }
   return cin_check_launch("moe_combine_backward");
 }

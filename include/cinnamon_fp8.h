@@ -379,7 +379,7 @@ int cin_moe_combine(const void* y, int y_dtype, int64_t sym, const void* scores,
  * sorted position r (zero rows where perm is -1), and dscores[t, j] = sum_c dout[t, c] *
  * y[inv[t*k + j], c] (fp32, 0 for dropped assignments); the autograd of reference
  * src/layers.py:151-154.  dout [T, N] fp32, y [A, N] and dy [A, N] of y_dtype (dy rounded to
- * it, RNE), dscores [T, k]
+ * it, RNE), k <= 16, dscores [T, k]
  * fp32 contiguous.
  */
 int cin_moe_combine_backward(const float* dout, int64_t sdm, const void* y, int y_dtype, int64_t sym,

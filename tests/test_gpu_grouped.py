@@ -229,3 +229,24 @@ def test_zero_rows_outside_ranges(kern, dev, dt):
     covered[0:10] = True
     covered[50:60] = True
     assert torch.equal(out[~covered.to(dev)].float().cpu(), torch.zeros(int((~covered).sum()), 33))
+
+
+def test_fp16_output_is_rne_of_fp32(kern, dev):
+    """The grouped FP8 GEMM's fp16 output (the routed experts' sorted outputs) is the
+    round-to-nearest-even of its fp32 output, ties included (no fused single rounding)."""
+    from cinnamon_amd import layers
+
+    g = torch.Generator().manual_seed(21)
+    E, N, K = 3, 512, 768
+    counts = [300, 0, 470]
+    starts, ends = _ranges(counts)
+    T = sum(counts)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(E, N, K, generator=g) * 0.05).to(dev)
+    xq, xs = kern.quantize_fp8_rowwise(x)
+    wq, ws = kern.quantize_fp8_blockwise(w.reshape(E * N, K))
+    args = (xq, xs, wq.view(E, N, K), ws.view(E, N // 128, -1), starts.to(dev), ends.to(dev))
+    y32 = layers.fp8_grouped_gemm(*args, out_dtype=torch.float32, zero_uncovered=True)
+    y16 = layers.fp8_grouped_gemm(*args, out_dtype=torch.float16, zero_uncovered=True)
+    assert y16.dtype == torch.float16
+    assert torch.equal(y16, y32.half())
