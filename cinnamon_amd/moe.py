@@ -251,7 +251,7 @@ class FP8RoutedExpertsFunction(torch.autograd.Function):
     order, stored in fp16: the reference's routed experts return fp16 GEMM results
     (src/layers.py:69-75), and fp16 halves the traffic of the down GEMM's output, the
     combine and its backward.  The gather is fused into the activation quantization, and
-    the backward sums each token's sorted-row gradients (fp32) into dx."""
+    the backward sums each token's sorted-row gradients (bf16, added in fp32) into dx."""
 
     @staticmethod
     def forward(ctx, x, w12, w3, perm, inv, starts, ends, top_k, weights_fp8=None):
@@ -267,7 +267,9 @@ class FP8RoutedExpertsFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         *saved, inv = ctx.saved_tensors
-        dxs, dw12, dw3 = layers.experts_backward(tuple(saved), grad_out, torch.float32)
+        # sorted-row input gradients in bf16 (fp32's range; each token's sum is rounded to
+        # x's dtype anyway): half the traffic of the dgrad's output and of the gather-sum
+        dxs, dw12, dw3 = layers.experts_backward(tuple(saved), grad_out, torch.bfloat16)
         dx = moe_gather_sum(dxs, inv, ctx.top_k, ctx.x_dtype)
         return (dx, dw12.to(ctx.w_dtypes[0]), dw3.to(ctx.w_dtypes[1]), None, None, None, None, None,
                 None)
