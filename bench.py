@@ -343,6 +343,43 @@ def main():
         with torch.no_grad():
             ml(ml_x, moe["starts"], moe["ends"])
 
+    # the whole routed block of MoE.forward (src/layers.py:126-157), forward + backward, on
+    # the same FP8 experts: cinnamon_amd.moe.routed_experts against the reference's torch
+    # routing (sort, gather, bincount, .item(), gated scatter_add_) around them
+    def moe_routed_setup():
+        g6 = torch.Generator(device=dev).manual_seed(37)
+        T3, k3 = moe["T"], moe["topk"]
+        sc = torch.rand(T3, k3, device=dev, generator=g6)
+        return dict(x=moe["x"][:T3].detach().clone().requires_grad_(True),
+                    sc=(sc / sc.sum(-1, keepdim=True)).requires_grad_(True),
+                    dout=torch.randn(T3, moe["D"], device=dev, generator=g6) * 1e-3)
+
+    def moe_routed_fused(i):
+        r = mr
+        r["x"].grad = r["sc"].grad = None
+        ml.zero_grad(set_to_none=True)
+        out, _ = moe_ops_r.routed_experts(ml, r["x"], moe["sel"], r["sc"])
+        out.backward(r["dout"])
+
+    def moe_routed_torch(i):
+        r = mr
+        r["x"].grad = r["sc"].grad = None
+        ml.zero_grad(set_to_none=True)
+        k3 = moe["topk"]
+        flat = moe["sel"].reshape(-1)
+        sorted_idx, order = flat.sort()
+        tok = order // k3
+        sorted_x = r["x"][tok]
+        cnt = torch.bincount(sorted_idx, minlength=moe["E"])
+        ends = cnt.cumsum(0)
+        starts = ends - cnt
+        int(cnt.max().item())
+        sorted_out = ml(sorted_x, starts, ends)
+        w = sorted_out * r["sc"].reshape(-1)[order][:, None]
+        out = torch.zeros(moe["T"], moe["D"], device=dev, dtype=w.dtype)
+        out.scatter_add_(0, tok.unsqueeze(1).expand_as(w), w)
+        out.backward(r["dout"])
+
     # config 3 dispatch and combine around the experts (cinnamon_amd.moe) against the
     # reference's torch formulation of the same block (src/layers.py:133-154)
     md = None
@@ -548,6 +585,11 @@ def main():
                      "frac_of_fp8_peak": round(dn_fl / dn_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
         }
     if ml is not None:
+        from cinnamon_amd import moe as moe_ops_r
+        mr = moe_routed_setup()
+        rf_ms = time_loop(moe_routed_fused, 3, 1) / 1e3
+        rt_ms = time_loop(moe_routed_torch, 3, 1) / 1e3
+        del mr
         A, D, H = moe["A"], moe["D"], moe["H"]
         f_ms = time_loop(moe_layer_fwd, 3, 1) / 1e3
         fb_ms = time_loop(moe_layer, 3, 1) / 1e3
@@ -558,6 +600,8 @@ def main():
                     "dual/re-quantizers, SwiGLU backward, dgrad and wgrad of both GEMMs",
             "forward_ms": round(f_ms, 2), "forward_backward_ms": round(fb_ms, 2),
             "tokens_per_s_fwd_bwd": round(moe["A"] / (fb_ms * 1e-3) / 8),
+            "routed_block_fwd_bwd_ms": round(rf_ms, 2),
+            "routed_block_fwd_bwd_ms_torch_routing": round(rt_ms, 2),
             "gemm_tflops_fwd_bwd": round(3 * fl / (fb_ms * 1e-3) / 1e12, 1),
         }
     if md is not None:
