@@ -626,8 +626,10 @@ def indexer_scores_fp8(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor,
     """The FP8 branch of DSAIndexer.forward up to the mask (reference
     src/attention.py:288-300): q [B, L, H, d] and k [B, S, d] quantized row-wise (1x128,
     the first scale of each row), scores [B, L, S] fp32 = k_scale * sum_h
-    relu(q_codes . k_codes) * (q_scale * weights * softmax_scale).  One fused kernel; the
-    reference's [B, L, H, S] fp32 logits are never written.  weights [B, L, H].
+    relu(q_codes . k_codes) * (q_scale * weights * softmax_scale).  Two launches: both
+    quantizations (first scales only), then one scoring kernel; the reference's
+    [B, L, H, S] fp32 logits are never written.  weights [B, L, H]; d a multiple of 32 up
+    to 256.
 
     Differentiable in `weights` only, as the reference's branch is: its q and k pass through
     the quantizer, which carries no gradient (the scores feed the indexer's KL loss,
