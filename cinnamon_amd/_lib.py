@@ -63,7 +63,7 @@ SIGNATURES: dict[str, list] = {
                                       _p, _i64, _p],
     "cin_moe_combine": [_p, _i32, _i64, _p, _i32, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "cin_moe_combine_backward": [_p, _i64, _p, _i32, _i64, _p, _i32, _i64, _p, _p, _i64, _i64, _i64,
-                                 _i64, _p, _i64, _p, _p],
+                                 _i64, _p, _i32, _i64, _p, _p],
 }
 
 # entry points that return something other than an int status

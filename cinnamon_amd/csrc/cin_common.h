@@ -4,8 +4,9 @@
 // (reference src/kernels.py:50-62 row-wise, :111-123 block-wise):
 //   amax  = maxnum-reduction of |x| over the tile (NaN elements ignored, as
 //           Triton's tl.max / tl.maximum lower to maxnum)
-//   amax  = maxnum(amax, floor)   floor = 1e-4 rounded to the INPUT dtype,
-//           because Triton computes tl.maximum(bf16_tensor, 1e-4) in bf16
+//   amax  = maxnum(amax, fp32(1e-4)) for every input dtype: Triton's tl.max widens
+//           bf16/fp16 to fp32 before it reduces (triton/language/standard.py, max),
+//           so tl.maximum(abs_max, 1e-4) compares two fp32 values
 //   scale = fp32(amax) / 448      (IEEE fp32 division), or with round_scale
 //           exp2(ceil(log2(amax / 448)))
 //   code  = e4m3fn_rne(minnum(maxnum(x / scale, -448), 448))
@@ -19,14 +20,10 @@
 namespace cin {
 
 constexpr float kFp8Max = 448.0f;
-// 1e-4 rounded to each supported input dtype (the floor of the tile amax).
+// Floor of the tile amax: fp32(1e-4) whatever the input dtype.
 constexpr float kFloorF32 = 9.99999974737875163555e-05f;   // fp32(1e-4)
-constexpr float kFloorBF16 = 1.0013580322265625e-04f;      // bf16(1e-4)
-constexpr float kFloorF16 = 1.0001659393310546875e-04f;    // fp16(1e-4)
 
-__host__ __device__ inline float amax_floor(int dtype) {
-  return dtype == CIN_DT_BF16 ? kFloorBF16 : (dtype == CIN_DT_F16 ? kFloorF16 : kFloorF32);
-}
+__host__ __device__ inline float amax_floor(int /*dtype*/) { return kFloorF32; }
 
 // Scale from a floored amax.  round_scale follows torch.exp2(torch.ceil(torch.log2(v)))
 // in fp32, where torch's log2 is correctly rounded over the reachable range: for
@@ -62,7 +59,8 @@ __device__ inline float compute_scale(float amax, bool round_scale) {
 // of 1 / s, one more step returns the correctly rounded quotient, so two steps are
 // exact for any fp32 x.  For x and amax that are bf16 or fp16 values (s = RN(amax/448),
 // |x| <= amax) one step already is: checked against the IEEE division for every pair of
-// mantissas over every exponent gap down to 2^-30.  STEPS is therefore 1 for 16-bit
+// mantissas over every exponent gap down to 2^-30, and for every bf16 and fp16 x below
+// the floor with s = RN(fp32(1e-4) / 448) (a floored tile).  STEPS is therefore 1 for 16-bit
 // inputs and 2 for fp32.  The residual is formed as q * s - x, not x - q * s, so that
 // x = -0 keeps its sign (-0 - (+0) * r = -0; the other order would add +0 to -0).  An
 // infinite scale (infinite amax) is left to the caller.

@@ -441,13 +441,13 @@ __global__ __launch_bounds__(kRT) void k_moe_combine(const void* __restrict__ y,
 // Combine backward, both gradients in one pass per token (one wave): the token's dout row
 // is read once; for each of its sorted positions r (increasing), y[r] is read for the score
 // gradient dscore[t, j] = sum_c dout[t, c] * y[r, c] (lane l over columns 8 l + 512 i, then
-// a wave sum) and dy[r] = dout[t] * score[t, j] is written in y's dtype.  Slots whose
-// assignment was dropped get dscore 0; the dy rows no assignment maps to are zeroed by
-// k_moe_zero_unmapped_rows.
-template <int ST, int YT>
+// a wave sum) and dy[r] = dout[t] * score[t, j] is written in dy's dtype DT (RNE of the
+// fp32 product).  Slots whose assignment was dropped get dscore 0; the dy rows no
+// assignment maps to are zeroed by k_moe_zero_unmapped_rows.
+template <int YT, int DT>
 __global__ __launch_bounds__(kRT) void k_moe_combine_bwd_tokens(
     const float* __restrict__ dout, int64_t sdm, const void* __restrict__ y, int64_t sym,
-    const void* __restrict__ scores, int64_t ssm, const int32_t* __restrict__ inv, int64_t T,
+    const void* __restrict__ scores, int st, int64_t ssm, const int32_t* __restrict__ inv, int64_t T,
     int k, int64_t A, int64_t N, void* __restrict__ dy, int64_t sdym, float* __restrict__ dscores) {
   const int lane = threadIdx.x & 63;
   const int64_t t = ((int64_t)blockIdx.x * kRT + threadIdx.x) >> 6;
@@ -457,7 +457,7 @@ __global__ __launch_bounds__(kRT) void k_moe_combine_bwd_tokens(
   float w[kMaxTopK], acc[kMaxTopK];
 #pragma unroll
   for (int j = 0; j < kMaxTopK; ++j) {
-    w[j] = j < n ? score_at<ST>(scores, t * ssm + slot[j]) : 0.0f;
+    w[j] = j < n ? load_elem(scores, st, t * ssm + slot[j]) : 0.0f;
     acc[j] = 0.0f;
   }
   const int64_t db = t * sdm;
@@ -488,8 +488,8 @@ __global__ __launch_bounds__(kRT) void k_moe_combine_bwd_tokens(
           d1[e] = a[1][e] * w[j];
         }
         const int64_t ob = (int64_t)pos[j] * sdym;
-        store4<YT>(dy, ob + c, N - c, d0);
-        store4<YT>(dy, ob + c + 4, N - c - 4, d1);
+        store4<DT>(dy, ob + c, N - c, d0);
+        store4<DT>(dy, ob + c + 4, N - c - 4, d1);
       }
     }
   }
@@ -620,9 +620,10 @@ int cin_moe_combine(const void* y, int y_dtype, int64_t sym, const void* scores,
 int cin_moe_combine_backward(const float* dout, int64_t sdm, const void* y, int y_dtype, int64_t sym,
                              const void* scores, int s_dtype, int64_t ssm, const int64_t* perm,
                              const int32_t* inv, int64_t T, int64_t k, int64_t A, int64_t N,
-                             void* dy, int64_t sdym, float* dscores, void* stream) {
-  CIN_CHECK_ARG(valid_dtype(s_dtype) && valid_dtype(y_dtype),
-                "moe_combine_backward: unsupported dtype (y %d, scores %d)", y_dtype, s_dtype);
+                             void* dy, int dy_dtype, int64_t sdym, float* dscores, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(s_dtype) && valid_dtype(y_dtype) && valid_dtype(dy_dtype),
+                "moe_combine_backward: unsupported dtype (y %d, scores %d, dy %d)", y_dtype, s_dtype,
+                dy_dtype);
   CIN_CHECK_ARG(T >= 0 && k >= 1 && A >= 0 && N >= 0, "moe_combine_backward: bad sizes");
   CIN_CHECK_ARG(A <= T * k, "moe_combine_backward: more sorted rows than assignments");
   CIN_CHECK_ARG(dout && y && scores && perm && inv && dy && dscores, "moe_combine_backward: null pointer");
@@ -631,9 +632,9 @@ int cin_moe_combine_backward(const float* dout, int64_t sdm, const void* y, int 
   if (A > 0 && N > 0) {
     CIN_CHECK_ARG(cdiv(A * 64, kRT) < ((int64_t)1 << 31), "moe_combine_backward: grid too large");
     const unsigned grid = (unsigned)cdiv(A * 64, kRT);  // one wave per sorted row
-    if (y_dtype == CIN_DT_F32)
+    if (dy_dtype == CIN_DT_F32)
       hipLaunchKernelGGL(k_moe_zero_unmapped_rows<CIN_DT_F32>, grid, kRT, 0, s, perm, T, (int)k, A, N, dy, sdym);
-    else if (y_dtype == CIN_DT_F16)
+    else if (dy_dtype == CIN_DT_F16)
       hipLaunchKernelGGL(k_moe_zero_unmapped_rows<CIN_DT_F16>, grid, kRT, 0, s, perm, T, (int)k, A, N, dy, sdym);
     else
       hipLaunchKernelGGL(k_moe_zero_unmapped_rows<CIN_DT_BF16>, grid, kRT, 0, s, perm, T, (int)k, A, N, dy, sdym);
@@ -642,21 +643,21 @@ int cin_moe_combine_backward(const float* dout, int64_t sdm, const void* y, int 
     CIN_CHECK_ARG(k <= kMaxTopK, "moe_combine_backward: k must be at most %d", kMaxTopK);
     CIN_CHECK_ARG(cdiv(T * 64, kRT) < ((int64_t)1 << 31), "moe_combine_backward: grid too large");
     const unsigned grid = (unsigned)cdiv(T * 64, kRT);  // one wave per token
-#define CIN_TOK(ST, YT)                                                                          \
-  hipLaunchKernelGGL((k_moe_combine_bwd_tokens<ST, YT>), grid, kRT, 0, s, dout, sdm, y, sym, scores, ssm, \
-                     inv, T, (int)k, A, N, dy, sdym, dscores)
-#define CIN_TOK_S(YT)                           \
-  if (s_dtype == CIN_DT_F32) CIN_TOK(CIN_DT_F32, YT);       \
-  else if (s_dtype == CIN_DT_BF16) CIN_TOK(CIN_DT_BF16, YT); \
-  else CIN_TOK(CIN_DT_F16, YT);
+#define CIN_TOK(YT, DT)                                                                          \
+  hipLaunchKernelGGL((k_moe_combine_bwd_tokens<YT, DT>), grid, kRT, 0, s, dout, sdm, y, sym, scores, \
+                     s_dtype, ssm, inv, T, (int)k, A, N, dy, sdym, dscores)
+#define CIN_TOK_D(YT)                                        \
+  if (dy_dtype == CIN_DT_F32) CIN_TOK(YT, CIN_DT_F32);       \
+  else if (dy_dtype == CIN_DT_BF16) CIN_TOK(YT, CIN_DT_BF16); \
+  else CIN_TOK(YT, CIN_DT_F16);
     if (y_dtype == CIN_DT_F32) {
-      CIN_TOK_S(CIN_DT_F32)
+      CIN_TOK_D(CIN_DT_F32)
     } else if (y_dtype == CIN_DT_F16) {
-      CIN_TOK_S(CIN_DT_F16)
+      CIN_TOK_D(CIN_DT_F16)
     } else {
-      CIN_TOK_S(CIN_DT_BF16)
+      CIN_TOK_D(CIN_DT_BF16)
     }
-#undef CIN_TOK_S
+#undef CIN_TOK_D
 #undef CIN_TOK
   }
   return cin_check_launch("moe_combine_backward");

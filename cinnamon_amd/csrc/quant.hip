@@ -1230,7 +1230,10 @@ __global__ __launch_bounds__(kThreads) void k_transpose_u8(const uint8_t* __rest
 template <int OT>
 __device__ __forceinline__ float round_to(float h) {
   if constexpr (OT == CIN_DT_BF16) return __uint_as_float(f32_to_bf16_bits(h) << 16);
-  else if constexpr (OT == CIN_DT_F16) return (float)(_Float16)h;
+  // through the pinned conversion: a bare (_Float16)(silu * b) lets the compiler fuse the
+  // product and the conversion into v_fma_mixlo_f16 with a +0 addend, which rounds the
+  // exact product once and turns a -0 product (an exactly zero input) into +0
+  else if constexpr (OT == CIN_DT_F16) return half_bits_to_f32(CIN_DT_F16, f32_to_f16_bits(h));
   else return h;
 }
 

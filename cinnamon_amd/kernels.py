@@ -246,9 +246,14 @@ def _requant_op(x_fp8, x_scale, transposed):
         call("cin_requant_row_to_block", ptr(q), M, K, q.stride(0), ptr(xs), xs.stride(0),
              ptr(None), 0, ptr(out), out.stride(0), ptr(sblk), sblk.stride(0), stream_of(q))
     else:
-        out = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x_fp8.device)
+        # the kernel stores 8 codes at a time: rows of a K that is not a multiple of 8 go
+        # to a padded buffer, and the caller gets a contiguous copy
+        K8 = _cdiv(K, 8) * 8
+        out = torch.empty((M, K8), dtype=torch.float8_e4m3fn, device=x_fp8.device)
         call("cin_requant_row_to_block", ptr(q), M, K, q.stride(0), ptr(xs), xs.stride(0),
              ptr(out), out.stride(0), ptr(None), 0, ptr(sblk), sblk.stride(0), stream_of(q))
+        if K8 != K:
+            out = out[:, :K].contiguous()
     return out, sblk
 
 
@@ -264,7 +269,20 @@ def _(x_fp8, x_scale, transposed):
 # ---------------------------------------------------------------------------
 def dequantize_fp8_rowwise(x_fp8: torch.Tensor, scales: torch.Tensor,
                            block_size: int = 128) -> torch.Tensor:
-    """fp32(code) * scale[row, col // block_size] -> fp32 [M, N]."""
+    """fp32(code) * scale[row, col // block_size] -> fp32 [M, N].
+
+    The reference's function is plain torch (src/kernels.py:262-281) and so runs on CPU
+    tensors too; a CPU tensor takes the same product here (pad to whole tiles, one fp32
+    multiply per element, drop the padding).  GPU tensors run the HIP dequantizer."""
+    if x_fp8.device.type == "cpu":
+        M, N = x_fp8.shape
+        nb = scales.shape[1]
+        x = x_fp8.float()          # exact: every e4m3 code is an fp32 value
+        pad = nb * block_size - N
+        if pad > 0:
+            x = torch.nn.functional.pad(x, (0, pad))
+        x = (x.view(M, nb, block_size) * scales.view(M, nb, 1)).view(M, nb * block_size)
+        return x[:, :N] if pad > 0 else x
     _require(x_fp8.is_cuda, "Input must be on CUDA")
     _codes_u8(x_fp8)
     return _dequant_rowwise_op(x_fp8, scales, int(block_size))

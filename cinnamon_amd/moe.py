@@ -30,8 +30,7 @@ MAX_EXPERTS = 4096
 MAX_TOP_K = 16
 
 __all__ = ["moe_route", "moe_gather_quantize", "moe_gather_sum", "moe_combine",
-           "moe_combine_backward", "FP8RoutedExpertsFunction", "MoECombineFunction",
-           "routed_experts"]
+           "moe_combine_backward", "RoutedExpertsFunction", "routed_experts"]
 
 
 # ---------------------------------------------------------------------------
@@ -126,8 +125,17 @@ def _(x, perm, top_k, round_scale):
 
 
 def _x_rows16(x):
-    ok = x.stride(1) == 1 and x.data_ptr() % 16 == 0 and (x.stride(0) * x.element_size()) % 16 == 0
-    return x if ok else x.contiguous()
+    """x with unit column stride and 16-byte aligned rows (the quantizer loads 16 bytes at a
+    time): x itself when it qualifies, else a copy whose rows are padded to 16 bytes (the
+    padding is never read: the kernel loads the last chunk of a row element by element)."""
+    es = x.element_size()
+    if x.stride(1) == 1 and x.data_ptr() % 16 == 0 and (x.stride(0) * es) % 16 == 0:
+        return x
+    T, D = x.shape
+    per = 16 // es
+    buf = x.new_empty((T, _cdiv(max(D, 1), per) * per))
+    buf[:, :D].copy_(x)
+    return buf[:, :D]
 
 
 @custom_op("moe_scatter_quant_rowwise",
@@ -212,82 +220,89 @@ def _(y, scores, inv):
 
 
 def moe_combine_backward(dout: torch.Tensor, sorted_out: torch.Tensor, top_scores: torch.Tensor,
-                         perm: torch.Tensor, inv: torch.Tensor):
-    """Gradients of moe_combine: (d sorted_out [A, D] in sorted_out's dtype (RNE of the fp32
-    product), d top_scores [T, k] fp32)."""
+                         perm: torch.Tensor, inv: torch.Tensor, dy_dtype: torch.dtype | None = None):
+    """Gradients of moe_combine: (d sorted_out [A, D], d top_scores [T, k] fp32).
+
+    d sorted_out is the fp32 product dout * score rounded (RNE) to dy_dtype.  By default that
+    is fp32 for fp32 sorted outputs and bf16 for 16-bit ones: a loss averaged over many
+    tokens gives row gradients of 1e-6 and below, which fp16 holds only as subnormals (and
+    flushes below 6e-8), while bf16 keeps fp32's range, and the experts' FP8 quantizer that
+    reads it keeps 3 mantissa bits in any case."""
     _require(dout.is_cuda and sorted_out.is_cuda, "Input must be on CUDA")
+    if dy_dtype is None:
+        dy_dtype = torch.float32 if sorted_out.dtype == torch.float32 else torch.bfloat16
+    _require(dy_dtype in (torch.float32, torch.bfloat16, torch.float16), "dy_dtype must be fp32, bf16 or fp16")
     return _combine_bwd_op(dout.float(), sorted_out, top_scores, perm.to(torch.int64),
-                           inv.to(torch.int32))
+                           inv.to(torch.int32), dy_dtype)
 
 
 @custom_op("moe_combine_backward",
-           "(Tensor dout, Tensor y, Tensor scores, Tensor perm, Tensor inv) -> (Tensor, Tensor)")
-def _combine_bwd_op(dout, y, scores, perm, inv):
+           "(Tensor dout, Tensor y, Tensor scores, Tensor perm, Tensor inv, ScalarType dy_dtype)"
+           " -> (Tensor, Tensor)")
+def _combine_bwd_op(dout, y, scores, perm, inv, dy_dtype):
     dc = dout if dout.stride(1) == 1 else dout.contiguous()
     yc = y if y.stride(1) == 1 else y.contiguous()
     sc = scores if scores.stride(1) == 1 else scores.contiguous()
     pm, iv = perm.contiguous(), inv.contiguous()
     T, k = sc.shape
     A, D = yc.shape
-    dy = torch.empty((A, D), dtype=y.dtype, device=y.device)
+    dy = torch.empty((A, D), dtype=dy_dtype, device=y.device)
     ds = torch.empty((T, k), dtype=torch.float32, device=y.device)
     call("cin_moe_combine_backward", ptr(dc), dc.stride(0), ptr(yc), dtype_code(yc), yc.stride(0),
-         ptr(sc), dtype_code(sc), sc.stride(0), ptr(pm), ptr(iv), T, k, A, D, ptr(dy), dy.stride(0),
-         ptr(ds), stream_of(yc))
+         ptr(sc), dtype_code(sc), sc.stride(0), ptr(pm), ptr(iv), T, k, A, D, ptr(dy), dtype_code(dy),
+         dy.stride(0), ptr(ds), stream_of(yc))
     return dy, ds
 
 
 @_combine_bwd_op.register_fake
-def _(dout, y, scores, perm, inv):
-    return (y.new_empty(y.shape, dtype=y.dtype),
+def _(dout, y, scores, perm, inv, dy_dtype):
+    return (y.new_empty(y.shape, dtype=dy_dtype),
             y.new_empty(scores.shape, dtype=torch.float32))
 
 
 # ---------------------------------------------------------------------------
 # Autograd and the routed-experts block
 # ---------------------------------------------------------------------------
-class FP8RoutedExpertsFunction(torch.autograd.Function):
-    """Sorted expert outputs [A, D] of the FP8 SwiGLU experts applied to x's rows in routed
-    order, stored in fp16: the reference's routed experts return fp16 GEMM results
-    (src/layers.py:69-75), and fp16 halves the traffic of the down GEMM's output, the
-    combine and its backward.  The gather is fused into the activation quantization, and
-    the backward sums each token's sorted-row gradients (bf16, added in fp32) into dx."""
+class RoutedExpertsFunction(torch.autograd.Function):
+    """The routed block as one autograd node: gather-quantize -> FP8 SwiGLU experts ->
+    weighted combine, with gradients for x, the expert weights and the routing scores.
+
+    The sorted expert outputs [A, D] are stored in fp16: the reference's routed experts
+    return fp16 GEMM results (src/layers.py:69-75), and fp16 halves the traffic of the down
+    GEMM's output, the combine and its backward.  They stay inside this node, so their
+    gradient is not cast back to fp16 by autograd: the combine backward writes it in bf16
+    (fp32's range) for the experts' backward, and the sorted-row input gradients come back
+    in bf16 too, each token's sum added in fp32 and rounded once to x's dtype."""
 
     @staticmethod
-    def forward(ctx, x, w12, w3, perm, inv, starts, ends, top_k, weights_fp8=None):
-        xq, xs = moe_gather_quantize(x, perm, top_k, inv=inv)
-        out, saved = layers.experts_forward(xq, xs, w12, w3, starts, ends, x.dtype, weights_fp8,
-                                            out_dtype=torch.float16)
-        ctx.save_for_backward(*saved, inv)
+    def forward(ctx, x, w12, w3, top_scores, perm, inv, starts, ends, top_k, weights_fp8=None):
+        ys, saved = RoutedExpertsFunction.experts(x, w12, w3, perm, inv, starts, ends, top_k, weights_fp8)
+        ctx.save_for_backward(*saved, ys, top_scores, perm, inv)
         ctx.top_k = top_k
         ctx.x_dtype = x.dtype
         ctx.w_dtypes = (w12.dtype, w3.dtype)
-        return out
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        *saved, inv = ctx.saved_tensors
-        # sorted-row input gradients in bf16 (fp32's range; each token's sum is rounded to
-        # x's dtype anyway): half the traffic of the dgrad's output and of the gather-sum
-        dxs, dw12, dw3 = layers.experts_backward(tuple(saved), grad_out, torch.bfloat16)
-        dx = moe_gather_sum(dxs, inv, ctx.top_k, ctx.x_dtype)
-        return (dx, dw12.to(ctx.w_dtypes[0]), dw3.to(ctx.w_dtypes[1]), None, None, None, None, None,
-                None)
-
-
-class MoECombineFunction(torch.autograd.Function):
-    """routed_out = combine(sorted_out, top_scores) with gradients for both inputs."""
-
-    @staticmethod
-    def forward(ctx, sorted_out, top_scores, perm, inv):
-        ctx.save_for_backward(sorted_out, top_scores, perm, inv)
-        return moe_combine(sorted_out, top_scores, inv)
+        return moe_combine(ys, top_scores, inv)
 
     @staticmethod
     def backward(ctx, dout):
-        sorted_out, top_scores, perm, inv = ctx.saved_tensors
-        dy, ds = moe_combine_backward(dout, sorted_out, top_scores, perm, inv)
-        return dy, ds.to(top_scores.dtype), None, None
+        *saved, ys, top_scores, perm, inv = ctx.saved_tensors
+        dy, ds = moe_combine_backward(dout, ys, top_scores, perm, inv)
+        dx, dw12, dw3 = RoutedExpertsFunction.experts_backward(tuple(saved), dy, inv, ctx.top_k, ctx.x_dtype)
+        return (dx, dw12.to(ctx.w_dtypes[0]), dw3.to(ctx.w_dtypes[1]), ds.to(top_scores.dtype),
+                None, None, None, None, None, None)
+
+    @staticmethod
+    def experts(x, w12, w3, perm, inv, starts, ends, top_k, weights_fp8=None):
+        """Sorted expert outputs (fp16 [A, D]) and the tensors their backward needs."""
+        xq, xs = moe_gather_quantize(x, perm, top_k, inv=inv)
+        return layers.experts_forward(xq, xs, w12, w3, starts, ends, x.dtype, weights_fp8,
+                                      out_dtype=torch.float16)
+
+    @staticmethod
+    def experts_backward(saved, dy, inv, top_k, x_dtype):
+        """(dx, dw12, dw3) from the sorted outputs' gradient dy [A, D] (bf16 or fp32)."""
+        dxs, dw12, dw3 = layers.experts_backward(saved, dy, torch.bfloat16)
+        return moe_gather_sum(dxs, inv, top_k, x_dtype), dw12, dw3
 
 
 def routed_experts(experts: layers.GroupedExperts, x: torch.Tensor, top_idx: torch.Tensor,
@@ -305,6 +320,6 @@ def routed_experts(experts: layers.GroupedExperts, x: torch.Tensor, top_idx: tor
     k = top_idx.shape[1]
     _require(1 <= k <= MAX_TOP_K, f"top_k must be in [1, {MAX_TOP_K}]")
     perm, inv, counts, starts, ends = moe_route(top_idx, experts.n_experts)
-    sorted_out = FP8RoutedExpertsFunction.apply(x, experts.w12, experts.w3, perm, inv, starts, ends, k,
-                                                experts.quantized_weights())
-    return MoECombineFunction.apply(sorted_out, top_scores, perm, inv), counts
+    out = RoutedExpertsFunction.apply(x, experts.w12, experts.w3, top_scores, perm, inv, starts, ends, k,
+                                      experts.quantized_weights())
+    return out, counts

@@ -378,14 +378,14 @@ int cin_moe_combine(const void* y, int y_dtype, int64_t sym, const void* scores,
  * Backward of cin_moe_combine: dy[r] = dout[t] * score[t, j] for the assignment t*k + j at
  * sorted position r (zero rows where perm is -1), and dscores[t, j] = sum_c dout[t, c] *
  * y[inv[t*k + j], c] (fp32, 0 for dropped assignments); the autograd of reference
- * src/layers.py:151-154.  dout [T, N] fp32, y [A, N] and dy [A, N] of y_dtype (dy rounded to
- * it, RNE), k <= 16, dscores [T, k]
- * fp32 contiguous.
+ * src/layers.py:151-154.  dout [T, N] fp32, y [A, N] of y_dtype, dy [A, N] of dy_dtype (the
+ * fp32 product rounded to it, RNE; bf16 keeps fp32's range for small gradients where fp16
+ * would flush them), k <= 16, dscores [T, k] fp32 contiguous.
  */
 int cin_moe_combine_backward(const float* dout, int64_t sdm, const void* y, int y_dtype, int64_t sym,
                              const void* scores, int s_dtype, int64_t ssm, const int64_t* perm,
                              const int32_t* inv, int64_t T, int64_t k, int64_t A, int64_t N,
-                             void* dy, int64_t sdym, float* dscores, void* stream);
+                             void* dy, int dy_dtype, int64_t sdym, float* dscores, void* stream);
 
 #ifdef __cplusplus
 }

@@ -7,14 +7,18 @@ baseline), never as the thing measured or shipped.  The product path
 (cinnamon_amd) never calls it.
 
 Third-party arithmetic the reference relies on (not vendored in /root/reference):
-  * Triton 3.5.1 (uv.lock:2385-2386): scalar type promotion makes
-    tl.maximum(bf16_tile, 1e-4) a bf16 op (floor = bf16(1e-4)) while tl.maximum /
-    tl.minimum / tl.max lower to maxnum (NaN ignored); fp32 '/' is IEEE division.
+  * Triton 3.5.1 (uv.lock:2385-2386): tl.max widens bf16/fp16 tiles to fp32 before
+    reducing (language/standard.py, max) and tl.maximum promotes both operands, so
+    tl.maximum(tl.max(tl.abs(x)), 1e-4) floors at fp32(1e-4) for every input dtype;
+    tl.maximum / tl.minimum / tl.max lower to maxnum (NaN ignored); fp32 '/' is IEEE
+    division.
   * torch 2.9.1 (uv.lock:2308-2309): the float8_e4m3fn dtype and its RNE cast;
     torch.log2 (used for round_scale).
-Both are pinned by tests/test_oracle.py: the cast against a textbook OCP e4m3fn
-round-to-nearest-even (e4m3_rne_np, written from the OCP FP8 spec), and log2 by
-enumeration against a correctly rounded fp32 log2.
+Both are pinned by tests/test_oracle.py: the floor against scales and codes that
+Triton's own interpreter produced for zero and tiny bf16/fp16/fp32 tiles
+(tests/golden/triton_floor.npz, written by tests/golden/gen_triton_floor.py), the
+cast against a textbook OCP e4m3fn round-to-nearest-even (e4m3_rne_np, written from
+the OCP FP8 spec), and log2 by enumeration against a correctly rounded fp32 log2.
 
 Functions and the reference lines they restate:
   quant_rowwise           src/kernels.py:38-71   (+ wrapper :178-216)
@@ -44,9 +48,9 @@ _FP8_MAX_T = torch.tensor(FP8_MAX, dtype=torch.float32)
 # Scalar semantics
 # ---------------------------------------------------------------------------
 def amax_floor(dtype: torch.dtype) -> torch.Tensor:
-    """1e-4 in the input dtype, widened to fp32 (src/kernels.py:53, :114 under Triton typing)."""
-    if dtype in (torch.bfloat16, torch.float16):
-        return torch.tensor(1e-4, dtype=dtype).float()
+    """fp32(1e-4) for every input dtype (src/kernels.py:53, :114 under Triton typing:
+    the tile amax of a bf16/fp16 tile is already fp32 when it meets the floor)."""
+    del dtype
     return torch.tensor(1e-4, dtype=torch.float32)
 
 

@@ -188,6 +188,7 @@ def test_silu_mul_quant_equals_unfused_chain(kern, dev, M, H, in_dt, out_dt):
     h12[0, :8] = float("nan")
     h12[1, H:H + 4] = float("inf")
     h12[2, :] = 0.0
+    h12[3, :H] = -0.0   # silu(-0) * h2: exact signed-zero products keep their sign (0x80 codes)
     d = h12.to(dev)
     q, s = layers.silu_mul_quantize_fp8(d, out_dtype=out_dt)
     # the unfused chain on the GPU: torch's silu and product, then the row-wise quantizer

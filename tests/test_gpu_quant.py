@@ -90,7 +90,7 @@ def test_rowwise_strided_input(kern, dev):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
 def test_rowwise_special_tiles(kern, dev, dtype):
     x = torch.randn(8, 512, generator=torch.Generator().manual_seed(4))
-    x[0, :128] = 0.0                        # zero tile -> dtype-dependent floor
+    x[0, :128] = 0.0                        # zero tile -> fp32(1e-4) floor
     x[1, 128:256] *= 1e-6                   # tiny tile -> floor active
     x[2, 5] = float("nan")                  # NaN ignored by amax, coded as -448
     x[3, 300] = float("inf")                # inf tile: scale inf, finite -> +-0
@@ -328,3 +328,35 @@ def test_requant_every_code(kern, dev):
     qbt, sbt = kern.requantize_rowwise_to_blockwise(codes.to(dev), scales.to(dev), transposed=True)
     _assert_codes_equal(qbt, want_q.view(torch.uint8).t().contiguous(), "every-code requant^T codes")
     _assert_scales_equal(sbt, want_s, "every-code requant^T scales")
+
+
+# ---------------------------------------------------------------------------
+# the hardware e4m3 cast, exhaustively: every fp32 in the 21 binades that round
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("e", list(range(-12, 9)))
+def test_e4m3_cast_exhaustive_through_rowwise(kern, dev, e):
+    """Every fp32 of both signs in binade 2^e (e = -12 .. 8, the binades where the e4m3fn
+    cast rounds), quantized by quantize_fp8_rowwise with a 448 pivot at the head of each
+    tile: the scale is 448 / 448 = 1 and x / 1 = x, so each code is the cast of x itself.
+    Compared with torch's CPU cast, which tests/test_oracle.py pins to the textbook OCP
+    round-to-nearest-even on the same binades.  In binade 8 only |x| <= 448 is reachable
+    (the quantizer clamps to +-448 before the cast)."""
+    n = 1 << 23
+    if e == 8:
+        n = 3 * (1 << 21) + 1          # 256 * (1 + m / 2^23) <= 448
+    m = torch.arange(0, n, dtype=torch.int64)
+    bits = ((e + 127) << 23) | m
+    for sign in (0, 1):
+        b = bits | (sign << 31)
+        v = (b - (1 << 32) * (b >= (1 << 31)).long()).to(torch.int32).view(torch.float32)
+        rows = -(-n // 127)
+        tiles = torch.zeros(rows * 127, dtype=torch.float32)
+        tiles[:n] = v
+        x = torch.cat([torch.full((rows, 1), 448.0), tiles.view(rows, 127)], dim=1)
+        q, s = kern.quantize_fp8_rowwise(x.to(dev))
+        assert bool((s == 1.0).all())
+        got = q.view(torch.uint8)[:, 1:].reshape(-1)[:n].cpu()
+        want = v.to(torch.float8_e4m3fn).view(torch.uint8)
+        bad = (got != want).nonzero()
+        assert bad.numel() == 0, f"binade {e} sign {sign}: {bad.numel()} codes differ, first x = {v[bad[0]].item()!r}"
+        assert bool((q.view(torch.uint8)[:, 0] == 0x7E).all())

@@ -178,11 +178,10 @@ def test_moe_dispatch_shape_functions_and_trace():
 
     def step(x, w12, w3, top_idx, scores, dout):
         perm, inv, counts, starts, ends = moe.moe_route(top_idx, E)
-        ctx = _Ctx()
-        ys = moe.FP8RoutedExpertsFunction.forward(ctx, x, w12, w3, perm, inv, starts, ends, k)
+        ys, saved = moe.RoutedExpertsFunction.experts(x, w12, w3, perm, inv, starts, ends, k)
         out = moe.moe_combine(ys, scores, inv)
         dys, dsc = moe.moe_combine_backward(dout, ys, scores, perm, inv)
-        dx, dw12, dw3, *_ = moe.FP8RoutedExpertsFunction.backward(ctx, dys)
+        dx, dw12, dw3 = moe.RoutedExpertsFunction.experts_backward(saved, dys, inv, k, x.dtype)
         return perm, inv, counts, ys, out, dys, dsc, dx, dw12, dw3
 
     with FakeTensorMode(allow_non_fake_inputs=True):
@@ -196,9 +195,10 @@ def test_moe_dispatch_shape_functions_and_trace():
         perm, inv, counts, ys, out, dys, dsc, dx, dw12, dw3 = step(x, w12, w3, top_idx, scores, dout)
         assert _meta(perm) == ((T * k,), torch.int64, "cuda") and _meta(inv) == ((T * k,), torch.int32, "cuda")
         assert _meta(counts) == ((E,), torch.int64, "cuda")
-        # sorted expert outputs and their gradient in fp16 (the reference's expert GEMMs are fp16)
+        # sorted expert outputs in fp16 (the reference's expert GEMMs are fp16), their gradient
+        # in bf16 (fp32's range for small gradients)
         assert _meta(ys) == ((T * k, D), torch.float16, "cuda") and _meta(out) == ((T, D), F32, "cuda")
-        assert _meta(dys) == ((T * k, D), torch.float16, "cuda") and _meta(dsc) == ((T, k), F32, "cuda")
+        assert _meta(dys) == ((T * k, D), BF16, "cuda") and _meta(dsc) == ((T, k), F32, "cuda")
         assert _meta(dx) == ((T, D), BF16, "cuda") and dw12.shape == (E, 2 * H, D) and dw3.shape == (E, D, H)
         q, s = moe.moe_gather_quantize(x, perm, k)
         assert _meta(q) == ((T * k, D), F8, "cuda") and _meta(s) == ((T * k, 2), F32, "cuda")

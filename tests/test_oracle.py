@@ -4,6 +4,8 @@ Each test checks the oracle against something that does not restate it: the OCP
 e4m3fn spec (textbook RNE), a correctly rounded log2, hand-derived known answers,
 identities between different oracle functions, and brute force on tiny inputs.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -100,13 +102,52 @@ def test_rowwise_known_answers_fp32():
     assert s.item() == 2.0 and q.view(torch.uint8)[0, :2].tolist() == [0x7E, 0x3C]  # 3/2 = 1.5
 
 
-def test_zero_tile_floor_depends_on_input_dtype():
-    # Triton evaluates tl.maximum(bf16_tile, 1e-4) in bf16: floor = bf16(1e-4) = 1.0013580322265625e-4
-    _, s_bf = orc.quant_rowwise(torch.zeros(2, 256, dtype=torch.bfloat16))
-    _, s_32 = orc.quant_rowwise(torch.zeros(2, 256, dtype=torch.float32))
-    assert (s_bf == np.float32(1.0013580322265625e-04) / np.float32(448.0)).all()
-    assert (s_32 == np.float32(1e-4) / np.float32(448.0)).all()
-    assert s_bf[0, 0].item() != s_32[0, 0].item()
+_TRITON_FLOOR = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "triton_floor.npz")
+_FLOOR_DTYPES = (("bf16", torch.bfloat16), ("f16", torch.float16), ("f32", torch.float32))
+
+
+def _from_bits(b, dt):
+    return torch.from_numpy(b.view(np.int32) if dt == torch.float32 else b.view(np.int16)).view(dt)
+
+
+def test_zero_tile_scale_known_answer_every_dtype():
+    # Triton's interpreter printed 2.2321428616578487e-07 = fp32(1e-4) / 448 for zero
+    # bf16, fp16 and fp32 tiles alike (tests/golden/gen_triton_floor.py).
+    for dt in (torch.bfloat16, torch.float16, torch.float32):
+        for fn in (lambda x: orc.quant_rowwise(x), lambda x: orc.quant_blockwise(x)):
+            q, s = fn(torch.zeros(130, 256, dtype=dt))
+            assert (s == 2.2321428616578487e-07).all(), dt
+            assert (q.view(torch.uint8) == 0).all()
+
+
+@pytest.mark.parametrize("name,dt", _FLOOR_DTYPES)
+def test_floor_matches_triton_typing(name, dt):
+    """Scales and codes of zero, tiny (N(0, 2e-5)), floor-edge and ordinary tiles against
+    what Triton itself computed for the same inputs (tests/golden/triton_floor.npz).
+
+    The fixture's codes are Triton's fp32 quotient cast by torch's RNE cast (pinned to the
+    textbook cast above).  Elements whose input is NaN are left out of the code
+    comparison: the interpreter lowers tl.maximum's maxnumf to np.maximum, which keeps
+    NaN, while compiled Triton emits maxnumf and maps NaN to -448 (code 0xFE); the scale
+    of a tile holding a NaN is compared like every other."""
+    d = np.load(_TRITON_FLOOR)
+    x = _from_bits(d[f"row_x_{name}"], dt)
+    nan = torch.isnan(x.float()).numpy()
+    assert nan.sum() == 1
+    floored = 0
+    for rs in (0, 1):
+        q, s = orc.quant_rowwise(x, 128, bool(rs))
+        want_s = d[f"row_s_{name}_rs{rs}"]
+        assert np.array_equal(s.numpy().view(np.uint32), want_s.view(np.uint32))
+        got = q.view(torch.uint8).numpy()
+        assert np.array_equal(got[~nan], d[f"row_q_{name}_rs{rs}"][~nan])
+        floored += int((want_s == np.float32(1e-4) / np.float32(448.0)).sum())
+    assert floored >= 20   # most tiles of this input take the floor
+    xb = _from_bits(d[f"blk_x_{name}"], dt)
+    nan = torch.isnan(xb.float()).numpy()
+    q, s = orc.quant_blockwise(xb, 128, 128, False)
+    assert np.array_equal(s.numpy().view(np.uint32), d[f"blk_s_{name}"].view(np.uint32))
+    assert np.array_equal(q.view(torch.uint8).numpy()[~nan], d[f"blk_q_{name}"][~nan])
 
 
 def test_nan_and_inf_follow_maxnum_semantics():
@@ -301,6 +342,21 @@ def test_division_free_quotient_16bit_inputs(bits, sample):
         r = (np.float32(1.0) / s).astype(np.float32)
         for xs in (x, -x):
             assert np.array_equal(_div_by_scale(xs, s, r, 1), (xs / s).astype(np.float32))
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_division_free_quotient_floored_16bit_tiles(dt):
+    """A floored 16-bit tile divides by s = RN(fp32(1e-4) / 448), which no 16-bit amax
+    produces: one correction step is still exact for every value of the dtype below the
+    floor (all of them, both signs)."""
+    every = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(dt).float().numpy()
+    floor = np.float32(1e-4)
+    x = every[np.isfinite(every) & (np.abs(every) < floor)]
+    assert x.size > 3000
+    s = np.full_like(x, np.float32(floor / np.float32(448.0)))
+    r = (np.float32(1.0) / s).astype(np.float32)
+    want = (x / s).astype(np.float32)
+    assert np.array_equal(_div_by_scale(x, s, r, 1).view(np.uint32), want.view(np.uint32))
 
 
 def test_division_free_quotient_fp32_inputs():
