@@ -56,6 +56,7 @@ SIGNATURES: dict[str, list] = {
     "cin_indexer_weights_grad_workspace": [_i64, _i64, _i64, _i64],
     "cin_moe_route": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _p],
     "cin_moe_route_workspace": [_i64, _i64, _i64],
+    "cin_moe_route_noalloc": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p],
     "cin_moe_gather_quant_rowwise": [_p, _i32, _i64, _i64, _i64, _p, _i64, _i64, _i32, _p, _i64, _p,
                                      _i64, _p],
     "cin_moe_gather_sum": [_p, _i32, _i64, _p, _i64, _i64, _i64, _i64, _p, _i32, _i64, _p],

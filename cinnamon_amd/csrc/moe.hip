@@ -18,10 +18,19 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "cin_common.h"
 #include "cin_runtime.h"
 
 using namespace cin;
+
+// Scratch of cin_moe_route_noalloc: the route's [nblocks, E] per-block counts and bases
+// (int32), for callers that cannot allocate.  Each GPU the library runs on holds its own
+// copy (4 MiB) until the process ends.  Host code never passes this name to a kernel: it
+// is a host-side stand-in, and the device address comes from hipGetSymbolAddress.
+constexpr int64_t kRouteScratchElems = (int64_t)1 << 20;
+static __device__ __align__(256) int32_t scratch[kRouteScratchElems];
 
 namespace {
 
@@ -522,23 +531,20 @@ __global__ __launch_bounds__(kRT) void k_moe_zero_unmapped_rows(const int64_t* _
   for (int64_t c = (int64_t)lane * 4; c < N; c += 256) store4<DT>(dy, r * sdym + c, N - c, z);
 }
 
-}  // namespace
-
-extern "C" {
-
-int cin_moe_route(const int64_t* idx, int64_t T, int64_t k, int64_t E, int64_t* perm, int32_t* inv,
-                  int64_t* counts, int64_t* starts, int64_t* ends, int32_t* workspace,
-                  int64_t workspace_elems, void* stream) {
-  CIN_CHECK_ARG(T >= 0 && k >= 1 && E >= 1, "moe_route: need T >= 0, k >= 1, E >= 1");
-  CIN_CHECK_ARG(E <= kMaxExperts, "moe_route: at most %d experts", kMaxExperts);
+// The route's three launches over a caller's int32 workspace of ws_elems entries.
+int route_launch(const char* name, const int64_t* idx, int64_t T, int64_t k, int64_t E, int64_t* perm,
+                 int32_t* inv, int64_t* counts, int64_t* starts, int64_t* ends, int32_t* workspace,
+                 int64_t workspace_elems, void* stream) {
+  CIN_CHECK_ARG(T >= 0 && k >= 1 && E >= 1, "%s: need T >= 0, k >= 1, E >= 1", name);
+  CIN_CHECK_ARG(E <= kMaxExperts, "%s: at most %d experts", name, kMaxExperts);
   const int64_t A = T * k;
-  CIN_CHECK_ARG(A < ((int64_t)1 << 31), "moe_route: T*k must fit in 31 bits");
+  CIN_CHECK_ARG(A < ((int64_t)1 << 31), "%s: T*k must fit in 31 bits", name);
   CIN_CHECK_ARG(idx && perm && inv && counts && starts && ends && (A == 0 || workspace),
-                "moe_route: null pointer");
+                "%s: null pointer", name);
   const int64_t nblocks = cdiv(A, kChunk);
-  CIN_CHECK_ARG(workspace_elems >= 2 * nblocks * E, "moe_route: workspace needs %lld int32",
+  CIN_CHECK_ARG(workspace_elems >= 2 * nblocks * E, "%s: workspace needs %lld int32", name,
                 (long long)(2 * nblocks * E));
-  CIN_CHECK_ARG(nblocks < ((int64_t)1 << 20), "moe_route: too many assignments");
+  CIN_CHECK_ARG(nblocks < ((int64_t)1 << 20), "%s: too many assignments", name);
   hipStream_t s = static_cast<hipStream_t>(stream);
   int32_t* blockbase = workspace + nblocks * E;
   if (nblocks > 0) hipLaunchKernelGGL(k_route_hist, (unsigned)nblocks, kRT, 0, s, idx, A, (int32_t)E, workspace);
@@ -547,7 +553,62 @@ int cin_moe_route(const int64_t* idx, int64_t T, int64_t k, int64_t E, int64_t* 
   if (nblocks > 0)
     hipLaunchKernelGGL(k_route_scatter, (unsigned)nblocks, 64, 0, s, idx, A, (int32_t)E, blockbase,
                        perm, inv);
-  return cin_check_launch("moe_route");
+  return cin_check_launch(name);
+}
+
+// Device address of `scratch` on the current device, looked up once per device (with that
+// device current) and kept.  Every call on one GPU shares that GPU's array: the route
+// overwrites all of the entries it reads, so nothing needs clearing between calls, and
+// calls that overlap on one GPU (two streams, or two host threads) race on it.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch_ptr[kMaxDevices] = {};
+
+int route_scratch(int32_t** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return cin_set_error(CIN_ERR_HIP, "moe_route_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return cin_set_error(CIN_ERR_UNSUPPORTED, "moe_route_noalloc: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return cin_set_error(CIN_ERR_HIP, "moe_route_noalloc: hipGetSymbolAddress(scratch): %s",
+                           hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return CIN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cin_moe_route(const int64_t* idx, int64_t T, int64_t k, int64_t E, int64_t* perm, int32_t* inv,
+                  int64_t* counts, int64_t* starts, int64_t* ends, int32_t* workspace,
+                  int64_t workspace_elems, void* stream) {
+  return route_launch("moe_route", idx, T, k, E, perm, inv, counts, starts, ends, workspace,
+                      workspace_elems, stream);
+}
+
+int cin_moe_route_noalloc(const int64_t* idx, int64_t T, int64_t k, int64_t E, int64_t* perm,
+                          int32_t* inv, int64_t* counts, int64_t* starts, int64_t* ends,
+                          void* stream) {
+  CIN_CHECK_ARG(T >= 0 && k >= 1 && E >= 1, "moe_route_noalloc: need T >= 0, k >= 1, E >= 1");
+  const int64_t need = 2 * cdiv(T * k, kChunk) * E;
+  CIN_CHECK_ARG(need <= kRouteScratchElems,
+                "moe_route_noalloc: needs %lld int32 of scratch (2 * ceil(T*k / %d) * E), the "
+                "library holds %lld; use cin_moe_route with a workspace",
+                (long long)need, kChunk, (long long)kRouteScratchElems);
+  int32_t* ws = nullptr;
+  const int rc = route_scratch(&ws);
+  if (rc != CIN_OK) return rc;
+  return route_launch("moe_route_noalloc", idx, T, k, E, perm, inv, counts, starts, ends, ws,
+                      kRouteScratchElems, stream);
 }
 
 int cin_moe_route_workspace(int64_t T, int64_t k, int64_t E) {

@@ -326,6 +326,21 @@ int cin_moe_route(const int64_t* idx, int64_t T, int64_t k, int64_t E, int64_t* 
 int cin_moe_route_workspace(int64_t T, int64_t k, int64_t E);
 
 /*
+ * cin_moe_route without a workspace argument: it allocates nothing (no hipMalloc, no
+ * allocating library call) and keeps its [nblocks, E] counts and bases in a scratch array
+ * the library holds on each GPU: 1,048,576 int32 (4 MiB), so it needs
+ * 2 * ceil(T*k / 1024) * E <= 1,048,576 (= cin_moe_route_workspace(T, k, E)), and rejects
+ * larger routes with CIN_ERR_ARG.  Same outputs as cin_moe_route.  Calls that overlap on
+ * one GPU (two streams or two host threads) share the array and race; the array needs no
+ * clearing between calls.
+ * No counterpart in the reference: it is for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ */
+int cin_moe_route_noalloc(const int64_t* idx, int64_t T, int64_t k, int64_t E, int64_t* perm,
+                          int32_t* inv, int64_t* counts, int64_t* starts, int64_t* ends,
+                          void* stream);
+
+/*
  * Dispatch gather fused into the 1x128 row-wise quantizer: row r of q / scales is
  * quantize_fp8_rowwise(x[rowmap[r] / rowdiv]) bit for bit; a negative or out-of-range map
  * entry gives a zero row.  Replaces sorted_x = flat_x[token_indices] (reference
