@@ -38,7 +38,7 @@ def parse():
     p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "moe_gateup", "moe_down",
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
                                       "moe_wgrad", "moe_dgrad", "moe_layer", "moe_route",
-                                      "moe_gather", "moe_combine", "moe_combine_bwd", "indexer", "indexer_wgrad", "indexer_full", "copy"],
+                                      "moe_gather", "moe_combine", "moe_combine_bwd", "indexer", "indexer_wgrad", "indexer_full", "copy", "mfma_ceiling"],
                    default=None,
                    help="run only one kernel in a loop (for profiler runs)")
     p.add_argument("--no-extra", action="store_true",
@@ -97,37 +97,173 @@ def kernel_loop(fn, iters, warmup):
     return start.elapsed_time(end) / iters * 1e3  # us per call
 
 
+def mfma_ceiling_setup(dev):
+    """bench_ceiling.so (bench_ceiling.hip): the GEMM's inner MFMA + promotion-FMA mix with
+    no memory traffic, on random e4m3 operand bytes (NaN codes excluded).  Returns
+    (callable(promote) -> None, FLOP per launch)."""
+    import ctypes
+
+    import torch
+
+    path = os.path.join(ROOT, "bench_ceiling.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} not found: build it with __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    lib.bench_mfma_ceiling.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_void_p]
+    blocks, iters = 256, 200
+    g = torch.Generator(device=dev).manual_seed(7)
+    codes = torch.randint(0, 256, (blocks * 512 * 48 * 4,), dtype=torch.uint8, device=dev, generator=g)
+    codes = torch.where((codes & 0x7F) == 0x7F, codes - 1, codes)
+    out = torch.empty(blocks * 512, dtype=torch.float32, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def run(promote):
+        rc = lib.bench_mfma_ceiling(ctypes.c_void_p(codes.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                                    blocks, iters, int(promote), st)
+        if rc != 0:
+            raise RuntimeError(f"bench_mfma_ceiling failed ({rc})")
+
+    return run, float(blocks * 8 * iters * 32) * 2 * 16 * 16 * 128
+
+
+def _cpu_time(fn, runs, warmup=1):
+    """Median wall time (s) of fn() over `runs` timed runs after `warmup` untimed ones."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
 def cpu_baseline():
-    """Time the oracle (torch-CPU restatement of the reference path) on a bounded sample."""
+    """Time the oracle (torch-CPU restatement of the reference path, src/kernels.py:50-62,
+    111-123, 262-281 and the fp32 matmul of the dequantized operands) per config, on all host
+    cores.  Each config reports its quantize time and its dequantize + matmul time: configs 1,
+    2 and 4 in full, config 3 on 128 rows of each of 4 experts with the full config's time
+    scaled from that sample (about 40 s of CPU work in all)."""
     import torch
 
     from oracle import fp8_oracle as orc
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    rows = 512
-    g = torch.Generator().manual_seed(2)
-    x = torch.randn(rows, K, generator=g)
-    x[torch.rand(rows, K, generator=g) < 0.01] *= 20
-    x = x.to(torch.bfloat16)
-    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    runs = 3
+    res = {}
 
-    def step():
-        xq, xs = orc.quant_rowwise(x)
-        wq, ws = orc.quant_blockwise(w)
-        return orc.gemm_ref(xq, xs, wq.view(torch.uint8).t().contiguous(), ws.t().contiguous())
+    def gen(seed, *shape, std=1.0, outliers=False):
+        g = torch.Generator().manual_seed(seed)
+        x = torch.randn(*shape, generator=g) * std
+        if outliers:
+            x[torch.rand(*shape, generator=g) < 0.01] *= 20
+        return x.to(torch.bfloat16)
 
-    step()
-    ts = []
-    t_end = time.perf_counter() + 15.0
-    while time.perf_counter() < t_end or len(ts) < 3:
-        t0 = time.perf_counter()
-        step()
-        ts.append(time.perf_counter() - t0)
-        if len(ts) >= 10:
-            break
-    ts.sort()
-    t = ts[len(ts) // 2]
+    def t_kn(codes):
+        return codes.view(torch.uint8).t().contiguous()
+
+    def record(name, rows, full_rows, q_s, mm_s, flop, what, fixed_q_s=0.0, fixed_scale=1.0):
+        # fixed_q_s: the part of the quantize time that does not scale with the rows (the
+        # weights), which the full config has fixed_scale times of
+        scale = full_rows / rows
+        res[name] = {"sample": what, "rows": rows, "full_rows": full_rows,
+                     "quantize_ms": round(q_s * 1e3, 2), "dequant_matmul_ms": round(mm_s * 1e3, 2),
+                     "tflops": round(flop / (q_s + mm_s) / 1e12, 4),
+                     "full_config_ms_estimate": round(((q_s - fixed_q_s) * scale + fixed_q_s * fixed_scale
+                                                        + mm_s * scale) * 1e3, 1)}
+
+    # config 1: X[2048, 512], W[1024, 512] (seed 1), always in full
+    x1, w1 = gen(1, 2048, 512), gen(1, 1024, 512, std=0.02)
+    q1 = _cpu_time(lambda: (orc.quant_rowwise(x1), orc.quant_blockwise(w1)), runs)
+    a1, s1 = orc.quant_rowwise(x1)
+    b1, t1 = orc.quant_blockwise(w1)
+    mm1 = _cpu_time(lambda: orc.gemm_ref(a1, s1, t_kn(b1), t1.t().contiguous()), runs)
+    record("config1", 2048, 2048, q1, mm1, 2.0 * 2048 * 1024 * 512, "X[2048,512] x W[1024,512]^T, in full")
+
+    # config 2: X[M, 7168] rows (seed 2), W[2048, 7168] quantized in full
+    r2 = M
+    x2, w2 = gen(2, r2, K, outliers=True), gen(2, N, K, std=0.02)
+    q2 = _cpu_time(lambda: (orc.quant_rowwise(x2), orc.quant_blockwise(w2)), runs)
+    a2, s2 = orc.quant_rowwise(x2)
+    b2, t2 = orc.quant_blockwise(w2)
+    bkn, tkn = t_kn(b2), t2.t().contiguous()
+    mm2 = _cpu_time(lambda: orc.gemm_ref(a2, s2, bkn, tkn), runs)
+    qw2 = _cpu_time(lambda: orc.quant_blockwise(w2), runs)
+    record("config2", r2, M, q2, mm2, 2.0 * r2 * N * K,
+           "X[8192,7168] x W[2048,7168]^T in full", fixed_q_s=qw2)
+
+    # config 4: the backward of config 2 on r4 token rows: dual quantization of dY[r4, 2048]
+    # (seed 4), re-quantization of the rows' X codes into 128x128 blocks, dgrad
+    # dY.W -> [r4, 7168] and the wgrad contribution dY^T.X -> [2048, 7168]
+    r4 = M
+    dy = gen(4, r4, N, std=1e-3)
+    xa, xsa = a2[:r4], s2[:r4]
+
+    def c4_quant():
+        orc.quant_rowwise(dy, 128, True)
+        orc.quant_rowwise(dy.t().contiguous(), 128, True)
+        orc.quant_blockwise(orc.dequant_rowwise(xa, xsa), 128, 128, False)
+
+    q4 = _cpu_time(c4_quant, runs)
+    gq, gs = orc.quant_rowwise(dy, 128, True)
+    gqt, gst = orc.quant_rowwise(dy.t().contiguous(), 128, True)
+    xb, xbs = orc.quant_blockwise(orc.dequant_rowwise(xa, xsa), 128, 128, False)
+
+    def c4_mm():
+        orc.gemm_ref(gq, gs, b2.view(torch.uint8), t2)        # dgrad: B = W [2048, 7168]
+        orc.gemm_ref(gqt, gst, xb.view(torch.uint8), xbs)     # wgrad: B = X blocks [r4, 7168]
+
+    mm4 = _cpu_time(c4_mm, runs)
+    record("config4", r4, M, q4, mm4, 2 * 2.0 * r4 * N * K,
+           "dY[8192,2048] in full: dual quant, X re-quant, dgrad and wgrad")
+
+    # config 3: 4 of the 32 experts (the two largest and the two smallest of the Zipf routing,
+    # seed 3), r3 rows of each: gate/up [r3,7168]x[4096,7168]^T and down [r3,2048]x[7168,2048]^T,
+    # both expert weights quantized per expert
+    g3 = torch.Generator().manual_seed(3)
+    pz = torch.tensor([(e + 1) ** -1.1 for e in range(32)])
+    cnt = torch.bincount(torch.multinomial(pz.expand(16384, 32), 8, replacement=False, generator=g3).reshape(-1),
+                         minlength=32)
+    order = cnt.argsort(descending=True)
+    experts = [int(order[0]), int(order[1]), int(order[-2]), int(order[-1])]
+    r3 = [128] * 4
+    xs3 = [gen(30 + i, r, K) for i, r in enumerate(r3)]
+    hs3 = [gen(40 + i, r, 2048) for i, r in enumerate(r3)]
+    w12 = [gen(50 + i, 4096, K, std=0.02) for i in range(4)]
+    w3 = [gen(60 + i, K, 2048, std=0.02) for i in range(4)]
+
+    def c3_quant():
+        for i in range(4):
+            orc.quant_rowwise(xs3[i])
+            orc.quant_rowwise(hs3[i])
+            orc.quant_blockwise(w12[i])
+            orc.quant_blockwise(w3[i])
+
+    q3 = _cpu_time(c3_quant, runs)
+    ops = []
+    for i in range(4):
+        xa3, xs3_ = orc.quant_rowwise(xs3[i])
+        ha3, hs3_ = orc.quant_rowwise(hs3[i])
+        wa, wsa = orc.quant_blockwise(w12[i])
+        wb, wsb = orc.quant_blockwise(w3[i])
+        ops.append((xa3, xs3_, t_kn(wa), wsa.t().contiguous(), ha3, hs3_, t_kn(wb), wsb.t().contiguous()))
+
+    def c3_mm():
+        for xa3, xs3_, wa, wsa, ha3, hs3_, wb, wsb in ops:
+            orc.gemm_ref(xa3, xs3_, wa, wsa)
+            orc.gemm_ref(ha3, hs3_, wb, wsb)
+
+    mm3 = _cpu_time(c3_mm, runs)
+    qw3 = _cpu_time(lambda: [(orc.quant_blockwise(w12[i]), orc.quant_blockwise(w3[i])) for i in range(4)],
+                    runs)
+    record("config3", sum(r3), int(cnt.sum()), q3, mm3, sum(2.0 * r * K * 4096 + 2.0 * r * 2048 * K for r in r3),
+           f"experts {experts} (rows {[int(cnt[e]) for e in experts]}), 128 rows of each; gate/up and down, "
+           "both weights quantized (full-config estimate: all 131072 rows and the 32 experts' weights)",
+           fixed_q_s=qw3, fixed_scale=8.0)
+
     model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -136,14 +272,16 @@ def cpu_baseline():
                 break
     except OSError:
         pass
+    c2 = res["config2"]
     return {
-        "value": 2.0 * rows * N * K / t / 1e12,
+        "value": c2["tflops"],
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"config-2 step on X rows 0..{rows - 1} (W fully quantized each step): "
-                  f"oracle row/block quantize + dequantize + fp32 matmul, median of {len(ts)} runs, "
-                  f"{t * 1e3:.0f} ms/step; CPU {model}",
+        "sample": f"config 2 forward in full (X[8192,7168], W[2048,7168]): oracle quantize "
+                  f"{c2['quantize_ms']} ms + dequantize and fp32 matmul {c2['dequant_matmul_ms']} ms, median of "
+                  f"{runs}; configs 1, 3 (4 experts x 128 rows) and 4 in per_config; CPU {model}",
+        "per_config": res,
     }
 
 
@@ -495,6 +633,15 @@ def main():
     def wgrad(i):
         kernels.fp8_gemm_bs(gqt, gst, xbt, xbs.t(), torch.bfloat16, out=dw)
 
+    if args.only == "mfma_ceiling":
+        run_ceiling, ceil_flop = mfma_ceiling_setup(dev)
+        res = {}
+        for promote in (1, 0):
+            us = kernel_loop(lambda i: run_ceiling(promote), args.steps, args.warmup)
+            res["promotion" if promote else "hardware_accumulation"] = {
+                "us_per_call": us, "tflops": ceil_flop / us / 1e6}
+        print(json.dumps({"only": "mfma_ceiling", **res}))
+        return
     if args.only == "copy":
         # calibration for HBM byte counters: a plain copy of 512 MiB (read 512 MiB, write 512 MiB)
         src = torch.empty(256 * 1024 * 1024, dtype=torch.bfloat16, device=dev).fill_(1.0)
@@ -522,6 +669,12 @@ def main():
     gemm_us = kernel_loop(gemm, max(args.steps, 50), 5)
     qx_us = kernel_loop(quant_x, max(args.steps, 50), 5)
     qw_us = kernel_loop(quant_w, max(args.steps, 50), 5)
+    # the MFMA rate this GPU sustains on random e4m3 operands under its power limit, for the
+    # GEMM's own MFMA + promotion-FMA mix with no memory traffic at all
+    run_ceiling, ceil_flop = mfma_ceiling_setup(dev)
+    ceil_us = kernel_loop(lambda i: run_ceiling(1), 20, 3)
+    ceil_hw_us = kernel_loop(lambda i: run_ceiling(0), 20, 3)
+    ceil_tflops, ceil_hw_tflops = ceil_flop / ceil_us / 1e6, ceil_flop / ceil_hw_us / 1e6
 
     flops = 2.0 * M * N * K
     qx_bytes = M * K * 2 + M * K + M * (K // 128) * 4        # read bf16, write e4m3 + scales
@@ -558,6 +711,16 @@ def main():
             "traffic": measured_traffic()[0],
             "traffic_source": measured_traffic()[1],
             "counters": measured_mfma(),
+            "ceiling": {
+                "what": "register-only loop of the GEMM's MFMA + per-block promotion FMA mix on random "
+                        "e4m3 operands (bench_ceiling.hip): the rate the power limit allows with no "
+                        "operand traffic; with MFMA accumulation in hardware instead (no block "
+                        "scales to apply) for comparison",
+                "tflops": round(ceil_tflops, 1),
+                "frac_of_peak": round(ceil_tflops / PEAK_FP8_TFLOPS, 4),
+                "hardware_accumulation_tflops": round(ceil_hw_tflops, 1),
+                "gemm_frac_of_ceiling": round(gemm_tflops / ceil_tflops, 4),
+            },
             "kernel": "k_gemm_fp8_bs_256",
             "algorithmic_work": "2*M*N*K = %.4g FLOP per launch" % flops,
         },

@@ -74,5 +74,18 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+def build_bench_ceiling() -> str:
+    """Compile bench.py's calibration kernel (bench_ceiling.hip at the repo root, not part of
+    the library) into bench_ceiling.so beside it; returns its path."""
+    root = os.path.dirname(HERE)
+    src, out = os.path.join(root, "bench_ceiling.hip"), os.path.join(root, "bench_ceiling.so")
+    cmd = [HIPCC, *COMMON, "-shared", src, "-o", out]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{p.stdout}\n{p.stderr}")
+    return out
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
+    print(build_bench_ceiling())
