@@ -3,8 +3,10 @@
 Same public names, signatures, defaults, output dtypes/shapes and argument
 checks as reference src/kernels.py; every operator launches hand-written HIP
 kernels (gfx950) through the C ABI in include/cinnamon_fp8.h.  There is no
-Triton, no CPU path and no fallback: device tensors are required exactly where
-the reference requires CUDA tensors, and a missing native library raises.
+Triton and no fallback: device tensors are required exactly where the reference
+requires CUDA tensors, and a missing native library raises.  The one CPU path is
+the reference's own: dequantize_fp8_rowwise is plain torch there (:262-281) and runs
+on CPU tensors here too.
 
 Replaced reference items (src/kernels.py):
   quantize_fp8_rowwise      :178-216  -> cin_quant_rowwise

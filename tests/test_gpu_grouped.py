@@ -251,3 +251,66 @@ def test_fp16_output_is_rne_of_fp32(kern, dev):
     y16 = layers.fp8_grouped_gemm(*args, out_dtype=torch.float16, zero_uncovered=True)
     assert y16.dtype == torch.float16
     assert torch.equal(y16, y32.half())
+
+
+def _many_expert_counts(E, T, seed):
+    """Ragged expert sizes over E experts summing to T: Zipf-like weights, about 5% empty
+    experts, sizes not multiples of 128."""
+    g = torch.Generator().manual_seed(seed)
+    w = torch.tensor([(e + 1) ** -0.8 for e in range(E)])
+    w[torch.rand(E, generator=g) < 0.05] = 0.0
+    ids = torch.multinomial(w, T, replacement=True, generator=g)
+    return torch.bincount(ids, minlength=E).tolist()
+
+
+@pytest.mark.parametrize("E,T", [(256, 20000), (4100, 3000)])
+def test_grouped_forward_many_experts(kern, dev, E, T):
+    """256 experts (DeepSeek-V3's count): the persistent kernel's prefix-table lookup, several
+    tiles per workgroup; 4100 experts: beyond the LDS prefix table, the one-tile-per-workgroup
+    kernel."""
+    from cinnamon_amd import layers
+    counts = _many_expert_counts(E, T, seed=E)
+    starts, ends = _ranges(counts)
+    K, N = 512, 256
+    g = torch.Generator().manual_seed(E + 1)
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16)
+    w = torch.randn(E, N, K, generator=g) * 0.02
+    xq, xs = orc.quant_rowwise(x)
+    wq, ws = orc.quant_blockwise(w.reshape(E * N, K))
+    wq = wq.view(torch.uint8).view(E, N, K)
+    ws = ws.view(E, N // 128, K // 128)
+    want = orc.grouped_gemm_ref(xq, xs, wq, ws, starts, ends)
+    out = layers.fp8_grouped_gemm(xq.to(dev), xs.to(dev), wq.to(dev), ws.to(dev), starts.to(dev),
+                                  ends.to(dev), out_dtype=torch.float32)
+    _check(out, want, f"grouped forward E={E}")
+
+
+def test_grouped_backward_256_experts(kern, dev):
+    from cinnamon_amd import layers
+    E, T, N, K = 256, 12000, 256, 384
+    counts = _many_expert_counts(E, T, seed=9)
+    starts, ends = _ranges(counts)
+    g = torch.Generator().manual_seed(10)
+    dc = (torch.randn(T, N, generator=g) * 1e-3).to(torch.bfloat16)
+    xq, xs = orc.quant_rowwise(torch.randn(T, K, generator=g).to(torch.bfloat16))
+    w = torch.randn(E, N, K, generator=g) * 0.02
+    dual = orc.grouped_dual_ref(dc, starts, ends)
+    want_w = orc.grouped_wgrad_ref(dual, orc.grouped_requant_ref(xq, xs, starts, ends), E, N, K)
+    sd, ed = starts.to(dev), ends.to(dev)
+    q, s, qt, st = layers.quantize_fp8_dual_grouped(dc.to(dev), sd, ed)
+    xbt, xblk = layers.requantize_grouped_t(xq.to(dev), xs.to(dev), sd, ed)
+    dw = layers.fp8_grouped_wgrad(qt, st, xbt, xblk, sd, ed, T)
+    _check(dw, want_w, "wgrad E=256")
+    for e, c in enumerate(counts):
+        if c == 0:
+            assert torch.count_nonzero(dw[e]) == 0
+    wq, wqt, wsb = kern.quantize_fp8_blockwise_t(w.reshape(E * N, K).to(dev))
+    dx = layers.fp8_grouped_dgrad(q, s, wqt, wsb, sd, ed, N, out_dtype=torch.float32)
+    gq = torch.zeros(T, N, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    gs = torch.ones(T, N // 128)
+    for (e, a, b), d in zip(orc.expert_slices(starts, ends, T), dual):
+        if d is not None:
+            gq[a:b], gs[a:b] = d[0], d[1]
+    want_x = orc.grouped_dgrad_ref(gq, gs, wq.view(torch.uint8).cpu().view(E, N, K),
+                                   wsb.cpu().view(E, N // 128, -1), starts, ends)
+    _check(dx, want_x, "dgrad E=256")
