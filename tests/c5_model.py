@@ -10,8 +10,9 @@ at the sizes of config 5, with three recorded simplifications:
   attention projections are excluded from FP8 by `convert_to_fp8`'s name rules either way
   ("attn", src/kernels.py:863-867), so the FP8 path sees the same layers;
 - the model runs in fp32 (the reference trains under bf16 autocast, src/train.py:344):
-  the comparison isolates the FP8 quantization, and fp32 attention avoids bf16 batched
-  products, which have faulted on these GPUs;
+  the comparison isolates the FP8 quantization, and fp32 attention avoids torch's bf16
+  batched products with transposed right operands, which this GPU pool's operating notes
+  report as having faulted its GPUs (not observed here; the bf16-autocast step is untested);
 - the DSA KL auxiliary loss is absent with the indexer; the MoE balance loss and the MTP
   loss are kept (src/train.py:355-372).
 
