@@ -35,7 +35,7 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "moe_gateup", "moe_down",
+    p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "quant_fwd", "moe_gateup", "moe_down",
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
                                       "moe_wgrad", "moe_dgrad", "moe_layer", "moe_route",
                                       "moe_gather", "moe_combine", "moe_combine_bwd", "indexer", "indexer_wgrad", "indexer_full", "copy", "mfma_ceiling"],
@@ -404,8 +404,8 @@ def main():
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
 
     def step(i):
-        a, sa = kernels.quantize_fp8_rowwise(xs[i % nbuf])
-        b, sb = kernels.quantize_fp8_blockwise(ws[i % nbuf])
+        # X row tiles and W blocks in one launch (cin_quant_fwd), then the GEMM
+        a, sa, b, _, sb = kernels.quantize_fp8_forward(xs[i % nbuf], ws[i % nbuf])
         kernels.fp8_gemm_bs(a, sa, b, sb, torch.bfloat16, out=y)
 
     def gemm(i):
@@ -416,6 +416,9 @@ def main():
 
     def quant_w(i):
         kernels.quantize_fp8_blockwise(ws[i % nbuf])
+
+    def quant_fwd(i):
+        kernels.quantize_fp8_forward(xs[i % nbuf], ws[i % nbuf])
 
     from cinnamon_amd import layers
 
@@ -651,7 +654,7 @@ def main():
                           "us_per_call": us}))
         return
     if args.only:
-        fn = {"step": step, "gemm": gemm, "quant_x": quant_x, "quant_w": quant_w,
+        fn = {"step": step, "gemm": gemm, "quant_x": quant_x, "quant_w": quant_w, "quant_fwd": quant_fwd,
               "moe_gateup": moe_gateup, "moe_down": moe_down, "dual_quant": dual_quant,
               "requant": requant, "dgrad": dgrad, "wgrad": wgrad, "moe_dual": moe_dual,
               "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad,
@@ -669,6 +672,7 @@ def main():
     gemm_us = kernel_loop(gemm, max(args.steps, 50), 5)
     qx_us = kernel_loop(quant_x, max(args.steps, 50), 5)
     qw_us = kernel_loop(quant_w, max(args.steps, 50), 5)
+    qf_us = kernel_loop(quant_fwd, max(args.steps, 50), 5)
     # the MFMA rate this GPU sustains on random e4m3 operands under its power limit, for the
     # GEMM's own MFMA + promotion-FMA mix with no memory traffic at all
     run_ceiling, ceil_flop = mfma_ceiling_setup(dev)
@@ -683,6 +687,7 @@ def main():
     gemm_tflops = flops / (gemm_us * 1e-6) / 1e12
     qx_gbps = qx_bytes / (qx_us * 1e-6) / 1e9
     qw_gbps = qw_bytes / (qw_us * 1e-6) / 1e9
+    qf_gbps = (qx_bytes + qw_bytes) / (qf_us * 1e-6) / 1e9
 
     out = {
         "metric": METRIC,
@@ -732,6 +737,10 @@ def main():
                                 "frac_of_hbm": round(qx_gbps / PEAK_HBM_GBPS, 4), "bytes": qx_bytes},
             "quant_w_blockwise": {"us": round(qw_us, 2), "gbps": round(qw_gbps, 1),
                                   "frac_of_hbm": round(qw_gbps / PEAK_HBM_GBPS, 4), "bytes": qw_bytes},
+            "quant_fwd_fused": {"what": "X row tiles and W blocks in one launch, as in the step",
+                                "us": round(qf_us, 2), "gbps": round(qf_gbps, 1),
+                                "frac_of_hbm": round(qf_gbps / PEAK_HBM_GBPS, 4),
+                                "bytes": qx_bytes + qw_bytes},
         },
     }
     if moe is not None:

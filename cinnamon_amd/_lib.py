@@ -29,6 +29,8 @@ SIGNATURES: dict[str, list] = {
     "cin_quant_blockwise": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64,
                             _p, _i64, _p],
     "cin_dequant": [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p, _i32, _i64, _p],
+    "cin_quant_fwd": [_p, _i32, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64, _p, _i32, _i64, _i64, _p, _i64,
+                      _p, _i64, _p, _i64, _p],
     "cin_quant_dual": [_p, _i32, _i64, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _p,
                        _i64, _p],
     "cin_requant_row_to_block": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p],

@@ -117,22 +117,23 @@ __device__ inline void quant_vals(const float (&v)[NV], float s, float r, uint32
 //   kMapFirstScale: rows as kMapNone, but only each row's first tile scale is written, to
 //                sc[row * ssm] (the DSA indexer uses no other, src/attention.py:296-297).
 constexpr int kMapNone = 0, kMapGather = 1, kMapScatter = 2, kMapFirstScale = 3;
+// The body runs as workgroup `bid` of `nblk` (the kernel's own grid, or a share of a fused
+// launch's).
 template <int DT, int LANES, int U, bool FULL, int MAP = kMapNone>
-__global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict__ x, int64_t N,
-                                                         int64_t sxm, int round_scale,
-                                                         uint8_t* __restrict__ q, int64_t sqm,
-                                                         float* __restrict__ sc, int64_t ssm,
-                                                         uint32_t nb, uint32_t ntiles,
-                                                         const void* __restrict__ rowmap = nullptr,
-                                                         int64_t rowdiv = 1, int64_t src_rows = 0) {
+__device__ __forceinline__ void rowwise128_body(uint32_t bid, uint32_t nblk, const void* __restrict__ x,
+                                                int64_t N, int64_t sxm, int round_scale,
+                                                uint8_t* __restrict__ q, int64_t sqm,
+                                                float* __restrict__ sc, int64_t ssm, uint32_t nb,
+                                                uint32_t ntiles, const void* __restrict__ rowmap,
+                                                int64_t rowdiv, int64_t src_rows) {
   constexpr int ES = DT == CIN_DT_F32 ? 4 : 2;  // input element bytes
   constexpr int EPC = 16 / ES;                   // elements per 16-byte chunk
   constexpr int NC = 128 / (LANES * EPC);        // chunks per lane
   constexpr int EPL = NC * EPC;                  // elements per lane
   static_assert(NC >= 1 && EPL % 4 == 0, "tile split");
   const uint32_t li = threadIdx.x & (LANES - 1);
-  const uint32_t G = (gridDim.x * kThreads) / LANES;
-  const uint32_t g0 = (blockIdx.x * kThreads + threadIdx.x) / LANES;
+  const uint32_t G = (nblk * kThreads) / LANES;
+  const uint32_t g0 = (bid * kThreads + threadIdx.x) / LANES;
   const float floor_v = amax_floor(DT);
   const bool rs = round_scale != 0;
   uint32_t row = g0 / nb, cb = g0 - row * nb;
@@ -244,6 +245,18 @@ __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict_
       }
     }
   }
+}
+
+template <int DT, int LANES, int U, bool FULL, int MAP = kMapNone>
+__global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict__ x, int64_t N,
+                                                         int64_t sxm, int round_scale,
+                                                         uint8_t* __restrict__ q, int64_t sqm,
+                                                         float* __restrict__ sc, int64_t ssm,
+                                                         uint32_t nb, uint32_t ntiles,
+                                                         const void* __restrict__ rowmap = nullptr,
+                                                         int64_t rowdiv = 1, int64_t src_rows = 0) {
+  rowwise128_body<DT, LANES, U, FULL, MAP>(blockIdx.x, gridDim.x, x, N, sxm, round_scale, q, sqm, sc,
+                                           ssm, nb, ntiles, rowmap, rowdiv, src_rows);
 }
 
 template <int LANES, int U, bool FULL, int MAP = kMapNone>
@@ -535,9 +548,8 @@ __device__ inline GroupedTiles grouped_tiles(const int64_t* starts, const int64_
 // tile's use covers that tile only; when no tile is left it loads an empty one (no valid
 // rows: the main launch's buffer range is empty and nothing is read from memory).
 template <typename Raw, typename Geo, typename Load, typename Proc>
-__device__ __forceinline__ void tile_loop(uint32_t ntiles, Geo& geo, Load load, Proc proc) {
-  uint32_t t = blockIdx.x;
-  const uint32_t G = gridDim.x;
+__device__ __forceinline__ void tile_loop_from(uint32_t t, uint32_t G, uint32_t ntiles, Geo& geo,
+                                               Load load, Proc proc) {
   if (t >= ntiles) return;
   Raw ra, rb;
   TileGeo ga, gb;
@@ -568,6 +580,12 @@ __device__ __forceinline__ void tile_loop(uint32_t ntiles, Geo& geo, Load load, 
     if (!h2) break;
     t = t2;
   }
+}
+
+// The walk over the kernel's own grid.
+template <typename Raw, typename Geo, typename Load, typename Proc>
+__device__ __forceinline__ void tile_loop(uint32_t ntiles, Geo& geo, Load load, Proc proc) {
+  tile_loop_from<Raw>(blockIdx.x, gridDim.x, ntiles, geo, load, proc);
 }
 
 // Bytes from a tile's first row to the end of its last valid row (128 elements of
@@ -859,6 +877,37 @@ __global__ __launch_bounds__(kThreads, (DT == CIN_DT_F32 || EDGE) ? 1 : 4) void 
       [&](const TileGeo& g, RawIn<DT>& r) {
         block_body<DT, EDGE>(r, g, N, rs, q, sqm, qt, sqtm, vec_t != 0, sc, ssm, sm);
       });
+}
+
+// ----------------------------- forward-step pair -----------------------------
+// The two quantizations of the reference forward (src/kernels.py:742-747) in one launch:
+// workgroups [0, gw) quantize W's 128 x 128 blocks (one block each; with qt also the
+// transposed codes), the others X's 1 x 128 row tiles.  W's blocks are dispatched first
+// and their load latency overlaps X's streaming, instead of W paying it in a launch of its
+// own (a single round of ~900 blocks).  Same code paths, same results, as
+// k_blockwise128 and k_rowwise128.  W is 16-bit (the register budget of 4 waves per SIMD).
+// X tiles in flight per 8-lane group: the W share's registers hold the launch at 4 waves
+// per SIMD (the row-wise kernel alone runs 8), so each group keeps two tiles' loads out.
+constexpr int kFwdXU = 2;
+template <int XDT, int WDT>
+__global__ __launch_bounds__(kThreads, 4) void k_quant_fwd(
+    const void* __restrict__ x, int64_t xN, int64_t sxm, int xrs, uint8_t* xq, int64_t sxqm, float* xsc,
+    int64_t sxsm, uint32_t xnb, uint32_t xtiles, const void* __restrict__ w, int64_t wM, int64_t wN,
+    int64_t swm, uint8_t* wq, int64_t swqm, uint8_t* wqt, int64_t swqtm, int wvec_t, float* wsc,
+    int64_t swsm, uint32_t wnbc, uint32_t wtiles, uint32_t gw) {
+  static_assert(WDT != CIN_DT_F32, "16-bit W only");
+  __shared__ BlockSmem sm;
+  if (blockIdx.x < gw) {  // uniform per workgroup
+    DenseTiles geo{wM, wnbc, 0};
+    tile_loop_from<RawIn<WDT>>(
+        blockIdx.x, gw, wtiles, geo, [&](const TileGeo& g, RawIn<WDT>& r) { load_in<WDT, false>(w, swm, wN, g, r); },
+        [&](const TileGeo& g, RawIn<WDT>& r) {
+          block_body<WDT, false>(r, g, wN, false, wq, swqm, wqt, swqtm, wvec_t != 0, wsc, swsm, sm);
+        });
+  } else {
+    rowwise128_body<XDT, 8, kFwdXU, true, kMapNone>(blockIdx.x - gw, gridDim.x - gw, x, xN, sxm, xrs, xq, sxqm,
+                                               xsc, sxsm, xnb, xtiles, nullptr, 1, 0);
+  }
 }
 
 // ----------------------------- dual 1x128 / 128x1 -----------------------------
@@ -1562,6 +1611,50 @@ int cin_quant_blockwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_
                        bn, round_scale, q, sqm, qt, sqtm, scales, ssm, nbn);
   }
   return cin_check_launch("quant_blockwise");
+}
+
+int cin_quant_fwd(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm, int round_scale,
+                  uint8_t* xq, int64_t sxqm, float* xs, int64_t sxsm, const void* w, int w_dtype,
+                  int64_t N, int64_t swm, uint8_t* wq, int64_t swqm, uint8_t* wqt, int64_t swqtm,
+                  float* ws, int64_t swsm, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(x_dtype) && valid_dtype(w_dtype), "quant_fwd: unsupported dtype (x %d, w %d)",
+                x_dtype, w_dtype);
+  CIN_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "quant_fwd: negative shape");
+  const int64_t nbk = cdiv(K, 128), nbn = cdiv(N, 128);
+  const int xes = elem_size(x_dtype), wes = elem_size(w_dtype);
+  const bool fuse = M > 0 && N > 0 && K > 0 && K % 128 == 0 && w_dtype != CIN_DT_F32 && x && xq && xs &&
+                    w && ws && (wq || wqt) && aligned(x, 16) && (sxm * xes) % 16 == 0 && sxm >= K &&
+                    aligned(xq, 8) && sxqm % 8 == 0 && sxqm >= K && sxsm >= nbk && M * nbk < ((int64_t)1 << 31) &&
+                    aligned(w, 16) && (swm * wes) % 16 == 0 && swm >= K && tile_fits32(swm * wes) &&
+                    (!wq || (aligned(wq, 8) && swqm % 8 == 0 && swqm >= K && tile_fits32(swqm))) &&
+                    (!wqt || swqtm >= N) && swsm >= nbk && nbn < 65536 && nbn * nbk <= ((int64_t)1 << 22);
+  if (!fuse) {
+    // any other shape, dtype or layout: the two quantizers one after the other
+    const int rc = cin_quant_rowwise(x, x_dtype, M, K, sxm, 1, 128, round_scale, xq, sxqm, xs, sxsm, stream);
+    if (rc != CIN_OK) return rc;
+    return cin_quant_blockwise(w, w_dtype, N, K, swm, 1, 128, 128, 0, wq, swqm, wqt, swqtm, ws, swsm, stream);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint32_t xtiles = (uint32_t)(M * nbk), wtiles = (uint32_t)(nbn * nbk);
+  const int wvec_t = wqt && aligned(wqt, 16) && swqtm % 16 == 0 && tile_fits32(swqtm);
+  const unsigned gx = grid_for(xtiles, (kThreads / 8) * kFwdXU, 16384);
+  const unsigned grid = gx + wtiles;
+#define CIN_QFWD(XT, WT)                                                                                   \
+  hipLaunchKernelGGL((k_quant_fwd<XT, WT>), grid, kThreads, 0, s, x, K, sxm, round_scale, xq, sxqm, xs, sxsm, \
+                     (uint32_t)nbk, xtiles, w, N, K, swm, wq, swqm, wqt, swqtm, wvec_t, ws, swsm,            \
+                     (uint32_t)nbk, wtiles, wtiles)
+#define CIN_QFWD_X(WT)                                    \
+  if (x_dtype == CIN_DT_BF16) CIN_QFWD(CIN_DT_BF16, WT);  \
+  else if (x_dtype == CIN_DT_F16) CIN_QFWD(CIN_DT_F16, WT); \
+  else CIN_QFWD(CIN_DT_F32, WT);
+  if (w_dtype == CIN_DT_BF16) {
+    CIN_QFWD_X(CIN_DT_BF16)
+  } else {
+    CIN_QFWD_X(CIN_DT_F16)
+  }
+#undef CIN_QFWD_X
+#undef CIN_QFWD
+  return cin_check_launch("quant_fwd");
 }
 
 int cin_dequant(const uint8_t* q, int64_t M, int64_t N, int64_t sqm, int64_t sqn,

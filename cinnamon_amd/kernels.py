@@ -14,7 +14,7 @@ Replaced reference items (src/kernels.py):
   dequantize_fp8_rowwise    :262-281  -> cin_dequant (fp32 out)
   dequantize_fp8            :284-314  -> cin_dequant (bf16 out)
   fp8_matmul_dsv3           :667-702  -> cin_gemm_fp8_bs
-  FP8MatmulFunction         :731-794  -> quantizers + cin_quant_dual + cin_requant_row_to_block + GEMMs
+  FP8MatmulFunction         :731-794  -> cin_quant_fwd + cin_quant_dual + cin_requant_row_to_block + GEMMs
   FP8Linear                 :797-840
   convert_to_fp8            :843-905
   moe_grouped_gemm          :526-581  -> cin_grouped_gemm_f16 (unquantized, fp16 MFMA)
@@ -46,6 +46,7 @@ __all__ = [
     "dequantize_fp8",
     "fp8_matmul_dsv3",
     "fp8_gemm_bs",
+    "quantize_fp8_forward",
     "quantize_fp8_dual",
     "requantize_rowwise_to_blockwise",
     "FP8MatmulFunction",
@@ -186,6 +187,56 @@ def _(x, round_scale, with_rowmajor):
     return (x.new_empty((M if with_rowmajor else 0, N), dtype=torch.float8_e4m3fn),
             x.new_empty((N, M), dtype=torch.float8_e4m3fn),
             x.new_empty((_cdiv(M, 128), _cdiv(N, 128)), dtype=torch.float32))
+
+
+def quantize_fp8_forward(x: torch.Tensor, weight: torch.Tensor, round_scale: bool = False,
+                         with_rowmajor: bool = True, with_transposed: bool = False):
+    """Both quantizations of the FP8 linear forward in one launch (reference
+    src/kernels.py:746-747): x [M, K] in 1 x 128 row tiles with round_scale as given, and
+    weight [N, K] in 128 x 128 blocks with round_scale off.  Bit-identical to
+    quantize_fp8_rowwise(x, 128, round_scale) and quantize_fp8_blockwise(weight.float());
+    a 16-bit weight is read as it is, without the fp32 copy.
+
+    Returns (x_fp8 [M, K], x_scale [M, ceil(K/128)], w_fp8 [N, K] or None,
+    w_fp8_t [K, N] or None, w_scale [ceil(N/128), ceil(K/128)]).
+    """
+    _require(x.is_cuda and weight.is_cuda, "Inputs must be on CUDA")
+    _require(x.ndim == 2 and weight.ndim == 2, "Inputs must be 2D")
+    _require(x.shape[1] == weight.shape[1], "x and weight must share K")
+    _require(with_rowmajor or with_transposed, "at least one layout of the weight codes")
+    xq, xs, wq, wqt, ws = _quant_fwd_op(x, weight, bool(round_scale), bool(with_rowmajor),
+                                        bool(with_transposed))
+    return xq, xs, (wq if with_rowmajor else None), (wqt if with_transposed else None), ws
+
+
+@custom_op("quant_fwd", "(Tensor x, Tensor weight, bool round_scale, bool with_rowmajor, "
+           "bool with_transposed) -> (Tensor, Tensor, Tensor, Tensor, Tensor)")
+def _quant_fwd_op(x, weight, round_scale, with_rowmajor, with_transposed):
+    # a weight layout not asked for comes back as an empty [0, ...] placeholder
+    x = x if x.stride(1) == 1 else x.contiguous()
+    weight = weight if weight.stride(1) == 1 else weight.contiguous()
+    (M, K), N = x.shape, weight.shape[0]
+    dev = x.device
+    xq = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=dev)
+    xs = torch.empty((M, _cdiv(K, 128)), dtype=torch.float32, device=dev)
+    wq = torch.empty((N if with_rowmajor else 0, K), dtype=torch.float8_e4m3fn, device=dev)
+    wqt = torch.empty((K if with_transposed else 0, N), dtype=torch.float8_e4m3fn, device=dev)
+    ws = torch.empty((_cdiv(N, 128), _cdiv(K, 128)), dtype=torch.float32, device=dev)
+    call("cin_quant_fwd", ptr(x), dtype_code(x), M, K, x.stride(0), int(round_scale), ptr(xq), K,
+         ptr(xs), xs.stride(0), ptr(weight), dtype_code(weight), N, weight.stride(0),
+         ptr(wq) if with_rowmajor else ptr(None), K, ptr(wqt) if with_transposed else ptr(None), N,
+         ptr(ws), ws.stride(0), stream_of(x))
+    return xq, xs, wq, wqt, ws
+
+
+@_quant_fwd_op.register_fake
+def _(x, weight, round_scale, with_rowmajor, with_transposed):
+    (M, K), N = x.shape, weight.shape[0]
+    return (x.new_empty((M, K), dtype=torch.float8_e4m3fn),
+            x.new_empty((M, _cdiv(K, 128)), dtype=torch.float32),
+            x.new_empty((N if with_rowmajor else 0, K), dtype=torch.float8_e4m3fn),
+            x.new_empty((K if with_transposed else 0, N), dtype=torch.float8_e4m3fn),
+            x.new_empty((_cdiv(N, 128), _cdiv(K, 128)), dtype=torch.float32))
 
 
 def quantize_fp8_dual(dy: torch.Tensor, round_scale: bool = False):
@@ -450,11 +501,14 @@ class FP8MatmulFunction(torch.autograd.Function):
         x_flat = x.reshape(-1, x_shape[-1])
         M, K = x_flat.shape
         N = weight.shape[0]
-        x_fp8, x_scale = quantize_fp8_rowwise(x_flat, block_size=128, round_scale=round_scale)
         if weight_fp8 is None:
-            w = weight if weight.dtype == torch.float32 else weight.float()
-            weight_fp8 = quantize_fp8_blockwise_t(w, round_scale=False)
-        w_fp8, w_fp8_t, w_scale = weight_fp8
+            # x row tiles and weight blocks in one launch; the weight's 16-bit values are
+            # exact in fp32, so this equals quantizing weight.float() as the reference does
+            x_fp8, x_scale, w_fp8, w_fp8_t, w_scale = quantize_fp8_forward(
+                x_flat, weight, round_scale, with_rowmajor=True, with_transposed=True)
+        else:
+            x_fp8, x_scale = quantize_fp8_rowwise(x_flat, block_size=128, round_scale=round_scale)
+            w_fp8, w_fp8_t, w_scale = weight_fp8
         out = fp8_gemm_bs(x_fp8, x_scale, w_fp8, w_scale, torch.bfloat16)
         ctx.save_for_backward(x_fp8, x_scale, w_fp8_t, w_scale)
         ctx.x_shape = x_shape

@@ -72,6 +72,25 @@ int cin_quant_blockwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_
                         uint8_t* qt, int64_t sqtm, float* scales, int64_t ssm, void* stream);
 
 /*
+ * The two quantizations of the FP8 linear forward in one call: X [M, K] in 1 x 128 row
+ * tiles (as cin_quant_rowwise, block 128) and the weight W [N, K] in 128 x 128 blocks
+ * with round_scale off (as cin_quant_blockwise, 128 x 128).
+ * Replaces the pair quantize_fp8_rowwise(x_flat, 128, round_scale) and
+ * quantize_fp8_blockwise(weight.float(), 128, 128) in FP8MatmulFunction.forward
+ * (reference src/kernels.py:746-747).  Codes and scales are bit-identical to those two
+ * calls; with K % 128 == 0, a 16-bit W and 16-byte aligned rows both run in one launch.
+ *   x  [M, K] of dtype x_dtype, row stride sxm (unit column stride)
+ *   xq [M, K] codes (row stride sxqm) and xs [M, ceil(K/128)] (row stride sxsm)
+ *   w  [N, K] of dtype w_dtype, row stride swm (unit column stride)
+ *   wq [N, K] codes (row stride swqm), or NULL; wqt [K, N] transposed codes (row stride
+ *   swqtm), or NULL; at least one of the two.  ws [ceil(N/128), ceil(K/128)] (row stride swsm)
+ */
+int cin_quant_fwd(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm, int round_scale,
+                  uint8_t* xq, int64_t sxqm, float* xs, int64_t sxsm, const void* w, int w_dtype,
+                  int64_t N, int64_t swm, uint8_t* wq, int64_t swqm, uint8_t* wqt, int64_t swqtm,
+                  float* ws, int64_t swsm, void* stream);
+
+/*
  * Dequantization with (bm x bn) block scales; bm = 1 gives row-wise scales.
  * Replaces dequantize_fp8 / dequantize_fp8_kernel (reference src/kernels.py:284-314,
  * :135-173; bf16 output) and dequantize_fp8_rowwise (:262-281; fp32 output).

@@ -15,7 +15,7 @@ from torch.fx.experimental.proxy_tensor import make_fx
 
 from cinnamon_amd import kernels, layers, moe
 
-OPS = ["quant_rowwise", "quant_blockwise", "quant_blockwise_t", "quant_dual", "requant_row_to_block",
+OPS = ["quant_rowwise", "quant_blockwise", "quant_blockwise_t", "quant_fwd", "quant_dual", "requant_row_to_block",
        "dequant_rowwise", "dequant", "gemm_fp8_bs", "transpose_u8", "grouped_gemm_f16",
        "grouped_gemm_fp8", "quant_dual_grouped", "requant_row_to_block_grouped",
        "grouped_wgrad_fp8", "grouped_dgrad_fp8", "silu_mul_quant_rowwise", "swiglu_backward",
@@ -47,6 +47,13 @@ def test_shape_functions_match_the_kernels_outputs():
         assert q.shape == (300, 1100) and qt.shape == (1100, 300) and s.shape == (3, 9)
         q, qt, s = kernels.quantize_fp8_blockwise_t(x, with_rowmajor=False)
         assert q is None and qt.shape == (1100, 300)
+        w = torch.empty(260, 1100, dtype=BF16, device=dev)
+        xq, xs, wq, wqt, ws = kernels.quantize_fp8_forward(x, w, with_transposed=True)
+        assert [t.shape for t in (xq, xs, wq, wqt, ws)] == [(300, 1100), (300, 9), (260, 1100),
+                                                            (1100, 260), (3, 9)]
+        assert [t.dtype for t in (xq, xs, wq, wqt, ws)] == [F8, F32, F8, F8, F32]
+        _, _, wq, wqt, _ = kernels.quantize_fp8_forward(x, w)
+        assert wq.shape == (260, 1100) and wqt is None
         q, s, qt, st = kernels.quantize_fp8_dual(x)
         assert [t.shape for t in (q, s, qt, st)] == [(300, 1100), (300, 9), (1100, 300), (1100, 3)]
         assert [t.dtype for t in (q, s, qt, st)] == [F8, F32, F8, F32]
@@ -140,8 +147,7 @@ def test_fp8_linear_forward_backward_traces_to_operators(round_scale):
         assert _meta(y) == ((4, 64, 384), BF16, "cuda")
         assert _meta(dx) == ((4, 64, 512), BF16, "cuda") and _meta(dw) == ((384, 512), BF16, "cuda")
     ops = _op_targets(gm)
-    for name in ["quant_rowwise", "quant_blockwise_t", "gemm_fp8_bs", "quant_dual",
-                 "requant_row_to_block"]:
+    for name in ["quant_fwd", "gemm_fp8_bs", "quant_dual", "requant_row_to_block"]:
         assert any(f"cinnamon_amd.{name}" in o for o in ops), (name, ops)
 
 
