@@ -38,7 +38,8 @@ def parse():
     p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "quant_fwd", "moe_gateup", "moe_down",
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
                                       "moe_wgrad", "moe_dgrad", "moe_layer", "moe_route",
-                                      "moe_gather", "moe_combine", "moe_combine_bwd", "indexer", "indexer_wgrad", "indexer_full", "copy", "mfma_ceiling"],
+                                      "moe_gather", "moe_combine", "moe_combine_bwd", "indexer", "indexer_wgrad", "indexer_full", "copy", "mfma_ceiling",
+                                      "traffic_ceiling"],
                    default=None,
                    help="run only one kernel in a loop (for profiler runs)")
     p.add_argument("--no-extra", action="store_true",
@@ -100,7 +101,8 @@ def kernel_loop(fn, iters, warmup):
 def mfma_ceiling_setup(dev):
     """bench_ceiling.so (bench_ceiling.hip): the GEMM's inner MFMA + promotion-FMA mix with
     no memory traffic, on random e4m3 operand bytes (NaN codes excluded).  Returns
-    (callable(promote) -> None, FLOP per launch)."""
+    (callable(promote, shape=16) -> None, FLOP per launch); shape 32 runs the same work as
+    32 x 32 x 64 MFMAs."""
     import ctypes
 
     import torch
@@ -110,7 +112,7 @@ def mfma_ceiling_setup(dev):
         raise RuntimeError(f"{path} not found: build it with __graft_entry__.build()")
     lib = ctypes.CDLL(path)
     lib.bench_mfma_ceiling.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
-                                       ctypes.c_int, ctypes.c_void_p]
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     blocks, iters = 256, 200
     g = torch.Generator(device=dev).manual_seed(7)
     codes = torch.randint(0, 256, (blocks * 512 * 48 * 4,), dtype=torch.uint8, device=dev, generator=g)
@@ -118,13 +120,71 @@ def mfma_ceiling_setup(dev):
     out = torch.empty(blocks * 512, dtype=torch.float32, device=dev)
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
-    def run(promote):
+    def run(promote, shape=16):
         rc = lib.bench_mfma_ceiling(ctypes.c_void_p(codes.data_ptr()), ctypes.c_void_p(out.data_ptr()),
-                                    blocks, iters, int(promote), st)
+                                    blocks, iters, int(promote), int(shape), st)
         if rc != 0:
             raise RuntimeError(f"bench_mfma_ceiling failed ({rc})")
 
     return run, float(blocks * 8 * iters * 32) * 2 * 16 * 16 * 128
+
+
+def stream_mix_ceilings(dev, mixes, iters=20):
+    """bench_ceiling.so's k_stream_mix: for each HBM-bound kernel, the rate at which its read
+    : write byte mix moves in linear, coalesced 16-byte order (no arithmetic, no transposes),
+    best over four grids.  mixes: name -> (bytes read, R, W, input buffers rotated); the
+    kernel reads R and writes W chunks per unit, so it writes bytes_read * W / R.  Returns
+    name -> {"gbps", "us", "grid", "bytes"}."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "bench_ceiling.so"))
+    lib.bench_stream_mix.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    res = {}
+    for name, (rd, r, w, nbuf) in mixes.items():
+        units = rd // (16 * r)
+        srcs = [torch.ones(r * units * 16, dtype=torch.uint8, device=dev) for _ in range(nbuf)]
+        dst = torch.empty(w * units * 16, dtype=torch.uint8, device=dev)
+        best = None
+        for grid in (1024, 2048, 4096, 8192):
+            def run(i, grid=grid):
+                rc = lib.bench_stream_mix(ctypes.c_void_p(srcs[i % nbuf].data_ptr()), ctypes.c_void_p(dst.data_ptr()),
+                                          units, r, w, grid, st)
+                if rc != 0:
+                    raise RuntimeError(f"bench_stream_mix failed ({rc})")
+            us = kernel_loop(run, iters, 3)
+            if best is None or us < best[0]:
+                best = (us, grid)
+        moved = units * 16 * (r + w)
+        res[name] = {"gbps": round(moved / best[0] / 1e3, 1), "us": round(best[0], 2), "grid": best[1],
+                     "bytes": moved, "read_write": f"{r}:{w}"}
+        del srcs, dst
+    torch.cuda.empty_cache()
+    return res
+
+
+# config 3 sizes (moe_setup): tokens, top-k, d_model, expert hidden
+C3_T, C3_TOPK, C3_D, C3_H = 16384, 8, 7168, 2048
+
+
+def stream_mixes(nbuf):
+    """The byte mix of each HBM-bound kernel in this benchmark: name -> (bytes read, R, W,
+    input buffers rotated), with R : W its read : write ratio (scales aside)."""
+    A = C3_T * C3_TOPK
+    return {
+        "quant_x_rowwise": (M * K * 2, 2, 1, nbuf),          # bf16 in, e4m3 out
+        "quant_w_blockwise": (N * K * 2, 2, 1, nbuf),
+        "quant_fwd_fused": ((M + N) * K * 2, 2, 1, nbuf),
+        "dual_quant_dy": (M * N * 2, 1, 1, 1),               # bf16 in, two e4m3 layouts out
+        "requant_x_block_t": (M * K, 1, 1, 1),               # e4m3 in, e4m3 out
+        "dual_quant_grouped_dh12": (A * 2 * C3_H * 2, 1, 1, 1),
+        "requant_grouped_x": (A * C3_D, 1, 1, 1),
+        "gather_quant": (C3_T * C3_D * 2, 1, 4, 1),          # bf16 tokens in, k code rows each out
+        "combine": (A * C3_D * 2, 4, 1, 1),                  # fp16 rows in, fp32 tokens out
+    }
 
 
 def _cpu_time(fn, runs, warmup=1):
@@ -639,11 +699,18 @@ def main():
     if args.only == "mfma_ceiling":
         run_ceiling, ceil_flop = mfma_ceiling_setup(dev)
         res = {}
-        for promote in (1, 0):
-            us = kernel_loop(lambda i: run_ceiling(promote), args.steps, args.warmup)
-            res["promotion" if promote else "hardware_accumulation"] = {
-                "us_per_call": us, "tflops": ceil_flop / us / 1e6}
+        # alternating rounds: the power-limited clock drifts over a run
+        for rnd in range(2):
+            for shape in (16, 32):
+                for promote in (1, 0):
+                    us = kernel_loop(lambda i: run_ceiling(promote, shape), args.steps, args.warmup)
+                    key = f"mfma{shape}_" + ("promotion" if promote else "hardware_accumulation")
+                    res.setdefault(key, []).append({"us_per_call": round(us, 2),
+                                                    "tflops": round(ceil_flop / us / 1e6, 1)})
         print(json.dumps({"only": "mfma_ceiling", **res}))
+        return
+    if args.only == "traffic_ceiling":
+        print(json.dumps({"only": "traffic_ceiling", **stream_mix_ceilings(dev, stream_mixes(nbuf), args.steps)}))
         return
     if args.only == "copy":
         # calibration for HBM byte counters: a plain copy of 512 MiB (read 512 MiB, write 512 MiB)
@@ -867,6 +934,30 @@ def main():
             "wgrad": {"us": round(wg_us, 1), "tflops": round(flops / wg_us / 1e6, 1),
                       "frac_of_fp8_peak": round(flops / wg_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
         }
+    # each HBM-bound kernel against its own byte mix moved in the friendliest pattern
+    comps = out["components"]
+    where = {"quant_x_rowwise": comps, "quant_w_blockwise": comps, "quant_fwd_fused": comps,
+             "dual_quant_dy": comps.get("config4_backward"), "requant_x_block_t": comps.get("config4_backward"),
+             "dual_quant_grouped_dh12": comps.get("config3_moe_backward_gateup"),
+             "requant_grouped_x": comps.get("config3_moe_backward_gateup")}
+    mixes = {k: v for k, v in stream_mixes(nbuf).items() if where.get(k) is not None}
+    if "config3_moe_dispatch" in comps:
+        mixes.update({k: stream_mixes(nbuf)[k] for k in ("gather_quant", "combine")})
+    ceil = stream_mix_ceilings(dev, mixes)
+    for k, c in ceil.items():
+        if k in ("gather_quant", "combine"):
+            d = comps["config3_moe_dispatch"]
+            d[f"{k}_traffic_ceiling_gbps"] = c["gbps"]
+            d[f"{k}_frac_of_traffic_ceiling"] = round(d[f"{k}_gbps"] / c["gbps"], 4)
+        else:
+            d = where[k][k]
+            d["traffic_ceiling_gbps"] = c["gbps"]
+            d["frac_of_traffic_ceiling"] = round(d["gbps"] / c["gbps"], 4)
+    out["roofline"]["hbm_traffic_ceilings"] = {
+        "what": "bench_ceiling.hip k_stream_mix: each kernel's read : write byte ratio moved in linear "
+                "16-byte coalesced order with no arithmetic (best of 4 grids); the rate the HBM "
+                "system gives that mix, against which frac_of_traffic_ceiling is taken",
+        **ceil}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))
