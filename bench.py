@@ -35,7 +35,7 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["step", "gemm", "quant_x", "quant_w", "quant_fwd", "moe_gateup", "moe_down",
+    p.add_argument("--only", choices=["step", "gemm", "scaled_mm", "quant_x", "quant_w", "quant_fwd", "moe_gateup", "moe_down",
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
                                       "moe_wgrad", "moe_dgrad", "moe_layer", "moe_route",
                                       "moe_gather", "moe_combine", "moe_combine_bwd", "indexer", "indexer_wgrad", "indexer_full", "copy", "mfma_ceiling",
@@ -471,6 +471,13 @@ def main():
     def gemm(i):
         kernels.fp8_gemm_bs(xq, xsc, wq, wsc, torch.bfloat16, out=y)
 
+    # for comparison: the vendor library's FP8 GEMM (hipBLASLt through torch._scaled_mm) on the
+    # same codes with one scale per tensor, i.e. without the per-block promotion
+    one = torch.ones((), dtype=torch.float32, device=dev)
+
+    def scaled_mm(i):
+        torch._scaled_mm(xq, wq.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+
     def quant_x(i):
         kernels.quantize_fp8_rowwise(xs[i % nbuf])
 
@@ -721,7 +728,7 @@ def main():
                           "us_per_call": us}))
         return
     if args.only:
-        fn = {"step": step, "gemm": gemm, "quant_x": quant_x, "quant_w": quant_w, "quant_fwd": quant_fwd,
+        fn = {"step": step, "gemm": gemm, "scaled_mm": scaled_mm, "quant_x": quant_x, "quant_w": quant_w, "quant_fwd": quant_fwd,
               "moe_gateup": moe_gateup, "moe_down": moe_down, "dual_quant": dual_quant,
               "requant": requant, "dgrad": dgrad, "wgrad": wgrad, "moe_dual": moe_dual,
               "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad,
@@ -737,6 +744,10 @@ def main():
     torch.cuda.synchronize()
     step_us = time_loop(step, args.steps, args.warmup)
     gemm_us = kernel_loop(gemm, max(args.steps, 50), 5)
+    try:
+        smm_us = kernel_loop(scaled_mm, max(args.steps, 50), 5)
+    except RuntimeError as e:  # an FP8 GEMM torch was built without
+        smm_us, smm_err = None, str(e)[:200]
     qx_us = kernel_loop(quant_x, max(args.steps, 50), 5)
     qw_us = kernel_loop(quant_w, max(args.steps, 50), 5)
     qf_us = kernel_loop(quant_fwd, max(args.steps, 50), 5)
@@ -800,6 +811,11 @@ def main():
             "gemm": {"us": round(gemm_us, 2), "tflops": round(gemm_tflops, 2),
                      "frac_of_fp8_peak": round(gemm_tflops / PEAK_FP8_TFLOPS, 4),
                      "min_bytes": gemm_bytes},
+            "hipblaslt_per_tensor_fp8": (
+                {"what": "torch._scaled_mm (hipBLASLt) on the same e4m3 codes with one scale per "
+                         "tensor: the GEMM without per-block promotion, not the block-scaled result",
+                 "us": round(smm_us, 2), "tflops": round(flops / (smm_us * 1e-6) / 1e12, 1)}
+                if smm_us is not None else {"error": smm_err}),
             "quant_x_rowwise": {"us": round(qx_us, 2), "gbps": round(qx_gbps, 1),
                                 "frac_of_hbm": round(qx_gbps / PEAK_HBM_GBPS, 4), "bytes": qx_bytes},
             "quant_w_blockwise": {"us": round(qw_us, 2), "gbps": round(qw_gbps, 1),

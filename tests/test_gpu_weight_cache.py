@@ -16,15 +16,24 @@ pytestmark = pytest.mark.gpu
 
 
 class _Counter:
-    def __init__(self, monkeypatch, module, name):
+    """Counts calls of the named functions of a module (one shared count)."""
+
+    def __init__(self, monkeypatch, module, *names):
         self.n = 0
-        real = getattr(module, name)
+        for name in names:
+            real = getattr(module, name)
 
-        def wrapped(*a, **k):
-            self.n += 1
-            return real(*a, **k)
+            def wrapped(*a, _real=real, **k):
+                self.n += 1
+                return _real(*a, **k)
 
-        monkeypatch.setattr(module, name, wrapped)
+            monkeypatch.setattr(module, name, wrapped)
+
+
+# An FP8 linear's weight is quantized either alone (quantize_fp8_blockwise_t, the cache's
+# refill) or together with its input in one launch (quantize_fp8_forward, the uncached
+# forward): one call of either is one weight quantization.
+LINEAR_WEIGHT_QUANTIZERS = ("quantize_fp8_blockwise_t", "quantize_fp8_forward")
 
 
 def _linear_pair(dev, seed=0):
@@ -40,7 +49,7 @@ def test_linear_cache_bit_identical_and_once_per_step(dev, monkeypatch):
     a, b = _linear_pair(dev)
     opt_a = torch.optim.AdamW(a.parameters(), lr=1e-3)
     opt_b = torch.optim.AdamW(b.parameters(), lr=1e-3)
-    quants = _Counter(monkeypatch, kernels, "quantize_fp8_blockwise_t")
+    quants = _Counter(monkeypatch, kernels, *LINEAR_WEIGHT_QUANTIZERS)
     g = torch.Generator().manual_seed(1)
     for step in range(3):
         for micro in range(4):  # gradient accumulation
@@ -62,7 +71,7 @@ def test_linear_cache_bit_identical_and_once_per_step(dev, monkeypatch):
 def test_linear_cache_invalidation(dev, monkeypatch):
     a, b = _linear_pair(dev, seed=2)
     x = torch.randn(64, 512, device=dev).to(torch.bfloat16)
-    quants = _Counter(monkeypatch, kernels, "quantize_fp8_blockwise_t")
+    quants = _Counter(monkeypatch, kernels, *LINEAR_WEIGHT_QUANTIZERS)
     b(x)
     b(x)
     assert quants.n == 1
