@@ -37,7 +37,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", choices=["step", "gemm", "scaled_mm", "quant_x", "quant_w", "quant_fwd", "moe_gateup", "moe_down",
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
-                                      "moe_wgrad", "moe_dgrad", "moe_layer", "moe_route",
+                                      "moe_wgrad", "moe_dgrad", "moe_layer", "moe_layer_fwd", "moe_route",
                                       "moe_gather", "moe_combine", "moe_combine_bwd", "indexer", "indexer_wgrad", "indexer_full", "copy", "mfma_ceiling",
                                       "traffic_ceiling"],
                    default=None,
@@ -534,7 +534,7 @@ def main():
     # config 3 experts layer end to end (layers.GroupedExperts, FP8 forward and backward):
     # weights quantized inside every call, as in training
     ml = None
-    if full or args.only == "moe_layer":
+    if full or args.only in ("moe_layer", "moe_layer_fwd"):
         if moe is None:
             moe = moe_setup(dev)
         g3 = torch.Generator(device=dev).manual_seed(34)
@@ -732,7 +732,7 @@ def main():
               "moe_gateup": moe_gateup, "moe_down": moe_down, "dual_quant": dual_quant,
               "requant": requant, "dgrad": dgrad, "wgrad": wgrad, "moe_dual": moe_dual,
               "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad,
-              "moe_layer": moe_layer, "moe_route": moe_route, "moe_gather": moe_gather,
+              "moe_layer": moe_layer, "moe_layer_fwd": moe_layer_fwd, "moe_route": moe_route, "moe_gather": moe_gather,
               "moe_combine": moe_combine, "moe_combine_bwd": moe_combine_bwd, "indexer": indexer, "indexer_wgrad": indexer_wgrad,
               "indexer_full": indexer_full}[args.only]
         loop = time_loop if args.only == "step" else kernel_loop

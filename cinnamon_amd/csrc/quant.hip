@@ -588,6 +588,20 @@ __device__ __forceinline__ void tile_loop(uint32_t ntiles, Geo& geo, Load load, 
   tile_loop_from<Raw>(blockIdx.x, gridDim.x, ntiles, geo, load, proc);
 }
 
+// The same walk with one register set: each tile is loaded, then processed.  For inputs
+// whose raw tile is large (fp32: 64 registers a lane), where a second set would halve the
+// resident waves; the other resident workgroups' loads overlap this one's processing.
+template <typename Raw, typename Geo, typename Load, typename Proc>
+__device__ __forceinline__ void tile_loop_single(uint32_t ntiles, Geo& geo, Load load, Proc proc) {
+  Raw r;
+  TileGeo g;
+  for (uint32_t t = blockIdx.x; t < ntiles; t += gridDim.x) {
+    geo(t, g);
+    load(g, r);
+    proc(g, r);
+  }
+}
+
 // Bytes from a tile's first row to the end of its last valid row (128 elements of
 // `es` bytes in), in a row-major operand with rows `rowb` bytes apart.
 __device__ inline int64_t tile_extent(int nr, int64_t rowb, int es) {
@@ -861,9 +875,10 @@ __device__ __forceinline__ void block_body(RawIn<DT>& raw, const TileGeo& g, int
   if (threadIdx.x == 0) sc[(g.t0 >> 7) * ssm + g.cb] = s;
 }
 
-// (4 waves per SIMD fit the bf16/fp16 main kernel without spills)
+// (4 waves per SIMD fit the main kernel without spills: bf16/fp16 with two register sets,
+// fp32 with one, which measured 3-7% faster than two sets at 2 waves per SIMD)
 template <int DT, bool EDGE>
-__global__ __launch_bounds__(kThreads, (DT == CIN_DT_F32 || EDGE) ? 1 : 4) void k_blockwise128(const void* __restrict__ x, int64_t M,
+__global__ __launch_bounds__(kThreads, EDGE ? 1 : 4) void k_blockwise128(const void* __restrict__ x, int64_t M,
                                                            int64_t N, int64_t sxm, int round_scale,
                                                            uint8_t* q, int64_t sqm, uint8_t* qt,
                                                            int64_t sqtm, int vec_t, float* sc,
@@ -872,11 +887,14 @@ __global__ __launch_bounds__(kThreads, (DT == CIN_DT_F32 || EDGE) ? 1 : 4) void 
   __shared__ BlockSmem sm;
   DenseTiles geo{M, nbc, cb0};
   const bool rs = round_scale != 0;
-  tile_loop<RawIn<DT>>(
-      ntiles, geo, [&](const TileGeo& g, RawIn<DT>& r) { load_in<DT, EDGE>(x, sxm, N, g, r); },
-      [&](const TileGeo& g, RawIn<DT>& r) {
-        block_body<DT, EDGE>(r, g, N, rs, q, sqm, qt, sqtm, vec_t != 0, sc, ssm, sm);
-      });
+  auto ld = [&](const TileGeo& g, RawIn<DT>& r) { load_in<DT, EDGE>(x, sxm, N, g, r); };
+  auto pr = [&](const TileGeo& g, RawIn<DT>& r) {
+    block_body<DT, EDGE>(r, g, N, rs, q, sqm, qt, sqtm, vec_t != 0, sc, ssm, sm);
+  };
+  if constexpr (DT == CIN_DT_F32 && !EDGE)
+    tile_loop_single<RawIn<DT>>(ntiles, geo, ld, pr);
+  else
+    tile_loop<RawIn<DT>>(ntiles, geo, ld, pr);
 }
 
 // ----------------------------- forward-step pair -----------------------------
@@ -1015,16 +1033,21 @@ __device__ __forceinline__ void dual_run(Geo& geo, uint32_t ntiles, const void* 
                                          int64_t N, int64_t sxm, bool rs, uint8_t* q, int64_t sqm,
                                          float* s, int64_t ssm, uint8_t* qt, int64_t sqtm, bool vec_t,
                                          float* st, int64_t sstm, DualSmem& sm) {
-  tile_loop<RawIn<DT>>(
-      ntiles, geo, [&](const TileGeo& g, RawIn<DT>& r) { load_in<DT, EDGE>(x, sxm, N, g, r); },
-      [&](const TileGeo& g, RawIn<DT>& r) {
-        if (g.nr == 0) return;  // uniform over the workgroup
-        dual_body<DT, EDGE>(r, g, N, rs, q, sqm, s, ssm, qt, sqtm, vec_t, st, sstm, sm);
-      });
+  auto ld = [&](const TileGeo& g, RawIn<DT>& r) { load_in<DT, EDGE>(x, sxm, N, g, r); };
+  auto pr = [&](const TileGeo& g, RawIn<DT>& r) {
+    if (g.nr == 0) return;  // uniform over the workgroup
+    dual_body<DT, EDGE>(r, g, N, rs, q, sqm, s, ssm, qt, sqtm, vec_t, st, sstm, sm);
+  };
+  // fp32: one register set at 3 waves per SIMD (two sets hold it to 2); measured 2-8%
+  // faster, and 4 waves per SIMD slower on large inputs
+  if constexpr (DT == CIN_DT_F32 && !EDGE)
+    tile_loop_single<RawIn<DT>>(ntiles, geo, ld, pr);
+  else
+    tile_loop<RawIn<DT>>(ntiles, geo, ld, pr);
 }
 
 template <int DT, bool EDGE>
-__global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x, int64_t M,
+__global__ __launch_bounds__(kThreads, (DT == CIN_DT_F32 && !EDGE) ? 3 : 1) void k_dual128(const void* __restrict__ x, int64_t M,
                                                       int64_t N, int64_t sxm, int round_scale,
                                                       uint8_t* q, int64_t sqm, float* s,
                                                       int64_t ssm, uint8_t* qt, int64_t sqtm,
@@ -1039,7 +1062,7 @@ __global__ __launch_bounds__(kThreads) void k_dual128(const void* __restrict__ x
 // Grouped: tiles are 128-token chunks of the experts (cin_grouped.h).  Rows outside
 // every expert range are not quantized.
 template <int DT, bool EDGE>
-__global__ __launch_bounds__(kThreads) void k_dual128_grouped(
+__global__ __launch_bounds__(kThreads, (DT == CIN_DT_F32 && !EDGE) ? 3 : 1) void k_dual128_grouped(
     const void* __restrict__ x, int64_t T, int64_t N, int64_t sxm, int round_scale, uint8_t* q,
     int64_t sqm, float* s, int64_t ssm, uint8_t* qt, int64_t sqtm, int vec_t, float* st,
     int64_t sstm, const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t E,

@@ -288,6 +288,7 @@ def test_dequantizers(kern, dev):
     (1000, 1100, torch.bfloat16),
     (2050, 4100, torch.float16),
     (4096, 640, torch.float32),
+    (12000, 8300, torch.float32),   # ~6000 tiles: several per workgroup in the fp32 one-set walk
 ])
 def test_tile_kernels_ragged_many_tiles(kern, dev, M, N, dtype):
     x = _activations(M, N, seed=11, dtype=dtype)
