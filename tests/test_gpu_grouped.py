@@ -161,13 +161,20 @@ def test_grouped_experts_fwd_bwd(kern, dev, counts):
     # backward).  The device's fp32 GEMM values and the oracle's differ in the last bits
     # (summation order; h12 is also stored in bf16), and where such a value sits on an
     # e4m3 rounding boundary its code moves by one step (1/8 of the element).  One such
-    # term changes an output by ~1% of its magnitude, so the end-to-end bound is that
+    # term changes an output by ~1% of its magnitude, so the end-to-end max bound is that
     # step, not the GEMM tolerance; the stage tests above hold every operand bit-exact and
-    # every GEMM to the GEMM tolerance.
+    # every GEMM to the GEMM tolerance.  Those flips are sparse, so the Frobenius and mean
+    # relative errors stay small and bound any systematic error: measured over 9 cases
+    # (three expert layouts x three seeds) max 0.5-1.6e-2, Frobenius 1.2-2.3e-3, mean
+    # 0.3-1.0e-3 (dx, rounded to bf16: 1.7e-3).  A 0.3% systematic error in every element
+    # would exceed the mean bounds.
     for name, got in (("out", out), ("dx", xd.grad), ("dw12", mod.w12.grad), ("dw3", mod.w3.grad)):
         mr = orc.normwise_max_rel(got.float().cpu(), ref[name])
         fr = orc.frob_rel(got.float().cpu(), ref[name])
-        assert mr <= 4e-2 and fr <= 5e-3, f"{name}: {mr:.3e} {fr:.3e}"
+        g64, r64 = got.float().cpu().double(), ref[name].double()
+        mean = ((g64 - r64).abs().mean() / r64.abs().mean()).item()
+        mean_bound = 2.5e-3 if name == "dx" else 1.5e-3
+        assert mr <= 3e-2 and fr <= 3.5e-3 and mean <= mean_bound, f"{name}: {mr:.3e} {fr:.3e} {mean:.3e}"
 
 
 # ---------------------------------------------------------------------------
