@@ -39,11 +39,11 @@ def parse():
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
                                       "moe_wgrad", "moe_dgrad", "moe_layer", "moe_layer_fwd", "moe_route",
                                       "moe_gather", "moe_combine", "moe_combine_bwd", "indexer", "indexer_wgrad", "indexer_full", "copy", "mfma_ceiling",
-                                      "traffic_ceiling"],
+                                      "traffic_ceiling", "config1", "config5"],
                    default=None,
                    help="run only one kernel in a loop (for profiler runs)")
     p.add_argument("--no-extra", action="store_true",
-                   help="skip the config-3 (MoE) and config-4 (backward) component timings")
+                   help="skip the config-3 (MoE), config-4 (backward) and config-5 (training) timings")
     return p.parse_args()
 
 
@@ -164,6 +164,63 @@ def stream_mix_ceilings(dev, mixes, iters=20):
         del srcs, dst
     torch.cuda.empty_cache()
     return res
+
+
+def config1_step(dev, steps):
+    """Config 1 on the GPU: X[2048,512] bf16, W[1024,512] bf16 (seed 1), the forward
+    quantizer pair in one launch and the GEMM, bf16 out.  Launch-bound at this size: the
+    device time of the two kernels and the step time with its host launch overhead."""
+    import torch
+
+    from cinnamon_amd import kernels
+
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(2048, 512, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(1024, 512, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    y = torch.empty(2048, 1024, dtype=torch.bfloat16, device=dev)
+
+    def step(i):
+        a, sa, b, _, sb = kernels.quantize_fp8_forward(x, w)
+        kernels.fp8_gemm_bs(a, sa, b, sb, torch.bfloat16, out=y)
+
+    dev_us = kernel_loop(step, max(steps, 50), 5)
+    step_us = time_loop(step, max(steps, 50), 5)
+    fl = 2.0 * 2048 * 1024 * 512
+    return {"what": "config 1: forward quantizer pair + GEMM, X[2048,512] x W[1024,512]^T, bf16 out",
+            "device_us": round(dev_us, 2), "step_us": round(step_us, 2),
+            "tflops_device": round(fl / dev_us / 1e6, 1)}
+
+
+def config5_training(dev, steps=4):
+    """Config 5: training steps of the MLA + MoE model of tests/c5_model.py (8 layers,
+    d_model 1024, 16 + 1 experts, batch 16 x 1024 tokens, 633M parameters) with its Linear
+    and expert layers on the FP8 path, against the same model kept in fp32 with the
+    reference's per-expert loop; same weights and token batches.  Tokens per second over
+    the steps after the first (test_c5_training.py checks the losses agree)."""
+    import torch
+
+    from tests.c5_model import C5Config, C5Model, to_fp8, train
+
+    c = C5Config()
+    torch.manual_seed(5)
+    ref = C5Model(c).to(dev)
+    fp8 = to_fp8(ref)
+    g = torch.Generator().manual_seed(5)
+    batches = [torch.randint(0, c.vocab_size, (16, 1025), generator=g).to(dev) for _ in range(steps)]
+    sync = torch.cuda.synchronize
+    l8, _, t8 = train(fp8, batches, sync)
+    del fp8
+    torch.cuda.empty_cache()
+    lr, _, tr = train(ref, batches, sync)
+    del ref
+    torch.cuda.empty_cache()
+    tok = 16 * 1024
+    return {"what": "config 5 training steps (tests/c5_model.py, fp32 model, FP8 Linear and expert layers) "
+                    "against the same model in fp32 with the per-expert loop",
+            "steps": steps, "tokens_per_step": tok,
+            "tokens_per_s_fp8": round(tok * (steps - 1) / sum(t8[1:])),
+            "tokens_per_s_fp32_reference": round(tok * (steps - 1) / sum(tr[1:])),
+            "loss_fp8": [round(v, 4) for v in l8], "loss_fp32_reference": [round(v, 4) for v in lr]}
 
 
 # config 3 sizes (moe_setup): tokens, top-k, d_model, expert hidden
@@ -716,6 +773,12 @@ def main():
                                                     "tflops": round(ceil_flop / us / 1e6, 1)})
         print(json.dumps({"only": "mfma_ceiling", **res}))
         return
+    if args.only == "config1":
+        print(json.dumps({"only": "config1", **config1_step(dev, args.steps)}))
+        return
+    if args.only == "config5":
+        print(json.dumps({"only": "config5", **config5_training(dev)}))
+        return
     if args.only == "traffic_ceiling":
         print(json.dumps({"only": "traffic_ceiling", **stream_mix_ceilings(dev, stream_mixes(nbuf), args.steps)}))
         return
@@ -950,6 +1013,9 @@ def main():
             "wgrad": {"us": round(wg_us, 1), "tflops": round(flops / wg_us / 1e6, 1),
                       "frac_of_fp8_peak": round(flops / wg_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
         }
+    out["components"]["config1"] = config1_step(dev, args.steps)
+    if not args.no_extra:
+        out["components"]["config5_training"] = config5_training(dev)
     # each HBM-bound kernel against its own byte mix moved in the friendliest pattern
     comps = out["components"]
     where = {"quant_x_rowwise": comps, "quant_w_blockwise": comps, "quant_fwd_fused": comps,
