@@ -1644,6 +1644,17 @@ int cin_quant_fwd(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
                 x_dtype, w_dtype);
   CIN_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "quant_fwd: negative shape");
   const int64_t nbk = cdiv(K, 128), nbn = cdiv(N, 128);
+  // both halves are validated before anything is launched, so a rejected call writes nothing
+  if (M > 0 && K > 0) {
+    CIN_CHECK_ARG(x && xq && xs, "quant_fwd: null activation pointer");
+    CIN_CHECK_ARG(sxqm >= K && sxsm >= nbk, "quant_fwd: activation output row stride too small");
+  }
+  if (N > 0 && K > 0) {
+    CIN_CHECK_ARG(w && ws && (wq || wqt), "quant_fwd: null weight pointer");
+    CIN_CHECK_ARG((!wq || swqm >= K) && (!wqt || swqtm >= N) && swsm >= nbk,
+                  "quant_fwd: weight output row stride too small");
+    CIN_CHECK_ARG(nbn < 65536 && nbn * nbk < ((int64_t)1 << 31), "quant_fwd: weight grid too large");
+  }
   const int xes = elem_size(x_dtype), wes = elem_size(w_dtype);
   const bool fuse = M > 0 && N > 0 && K > 0 && K % 128 == 0 && w_dtype != CIN_DT_F32 && x && xq && xs &&
                     w && ws && (wq || wqt) && aligned(x, 16) && (sxm * xes) % 16 == 0 && sxm >= K &&

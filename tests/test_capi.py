@@ -51,6 +51,15 @@ def test_no_rpath_to_a_second_hip_runtime():
     ("cin_gemm_fp8_bs", (None, 32, None, 1, 1, None, 32, None, 1, 1, 4, 4, 24, None, 0, 4, None)),
     ("cin_gemm_fp8_bs", (None, 32, None, 1, 1, None, 32, None, 1, 1, 4, 4, 32, None, 5, 4, None)),
     ("cin_dequant", (None, 4, 4, 4, 1, None, 1, 1, 1, 128, None, 2, 4, None)),            # fp16 out
+    # quant_fwd: x, xdt, M, K, sxm, rs, xq, sxqm, xs, sxsm, w, wdt, N, swm, wq, swqm, wqt, swqtm, ws, swsm, s
+    ("cin_quant_fwd", (None, 9, 4, 256, 256, 0, None, 256, None, 2, None, 0, 256, 256, None, 256, None, 0,
+                       None, 2, None)),                                                     # bad x dtype
+    ("cin_quant_fwd", (None, 0, 4, 256, 256, 0, None, 256, None, 2, None, 0, 256, 256, None, 256, None, 0,
+                       None, 2, None)),                                                     # null pointers
+    ("cin_quant_fwd", (1, 0, 4, 256, 256, 0, 1, 128, 1, 2, 1, 0, 256, 256, 1, 256, None, 0,
+                       1, 2, None)),                                                        # xq stride < K
+    ("cin_quant_fwd", (1, 0, 4, 256, 256, 0, 1, 256, 1, 2, 1, 0, 256, 256, None, 256, None, 0,
+                       1, 2, None)),                                                        # no weight output
     ("cin_moe_route", (None, 16, 2, 0, None, None, None, None, None, None, 0, None)),        # E = 0
     ("cin_moe_route", (None, 16, 2, 5000, None, None, None, None, None, None, 0, None)),     # E > 4096
     ("cin_moe_route", (None, 16, 2, 8, None, None, None, None, None, None, 0, None)),        # null ptrs
@@ -81,6 +90,8 @@ def test_empty_shapes_are_noops():
     assert lib.cin_moe_gather_sum(None, 1, 8, None, 0, 2, 0, 8, None, 1, 8, None) == 0
     assert lib.cin_moe_combine(None, 1, 8, None, 1, 2, None, 0, 2, 0, 8, None, 8, None) == 0
     assert lib.cin_indexer_scores_fp8(None, None, None, None, None, 1, 0, 8, 2, 64, 0.1, None, None) == 0
+    assert lib.cin_quant_fwd(None, 0, 0, 256, 256, 0, None, 256, None, 2, None, 0, 0, 256, None, 256, None, 0,
+                             None, 2, None) == 0
 
 
 def test_indexer_weights_grad_workspace_size():
