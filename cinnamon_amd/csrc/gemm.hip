@@ -274,16 +274,23 @@ struct __attribute__((aligned(16))) Smem {
   float sa[2][TM];  // A-row scales, slot q holds row sa_row(q)
 };
 // After the K loop the same LDS stages a bf16 C tile: 256 rows of 512 bytes, each padded
-// by 32 bytes so that the 16 rows of one fragment store fall on distinct bank groups.
-constexpr int kCStride = TN * 2 + 32;
+// by 16 bytes (a row stride of 132 dwords, 4 banks apart modulo 64): the 8-byte stores of
+// the 16 rows x 2 column groups that one pass of a fragment store serves land on 64
+// distinct banks.  (A 32-byte pad put rows l and l + 8 on the same banks.)
+constexpr int kCStride = TN * 2 + 16;
 union SmemAll {
   Smem s;
   uint8_t c[TM * kCStride];
 };
 
-// Slot q = 128 wm + 8 l + i holds row 128 wm + 16 i + l: the lane (wm, l) finds the
-// scales of its 8 m-tiles in 32 contiguous bytes.
-__device__ inline int sa_row(int q) { return (q & ~127) + (q & 7) * 16 + ((q >> 3) & 15); }
+// Slot q = 128 wm + 64 h + 4 l + e holds row 128 wm + 16 (4 h + e) + l: the lane (wm, l)
+// finds the scales of m-tiles 0-3 in the 16 bytes at slot 128 wm + 4 l and those of m-tiles
+// 4-7 at slot 128 wm + 64 + 4 l, so the 16 lanes of one 16-byte LDS read cover 64
+// consecutive dwords, one per bank.  (32 contiguous bytes per lane put lanes l and l + 8 on
+// the same banks: 0.7 M of the kernel's 1.7 M bank-conflict cycles on the config-2 shape.)
+__device__ inline int sa_row(int q) {
+  return (q & ~127) + (((q >> 6) & 1) * 4 + (q & 3)) * 16 + ((q >> 2) & 15);
+}
 
 // 16-byte chunk c of tile row r lives at slot c ^ f(r), f(r) = (r % 8) ^ ((r / 8) % 2):
 // the 8 rows a 32-bank LDS serves together, and the 8 same-parity rows a 64-bank LDS
@@ -378,7 +385,7 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
   const int fsw = swz_f(l16);
   const uint32_t fa = (uint32_t)((wm * 128 + l16) * TK + (((2 * kq) ^ fsw) << 4));
   const uint32_t fb = (uint32_t)(offsetof(Smem, b) + (wn * 64 + l16) * TK + (((2 * kq) ^ fsw) << 4));
-  const uint32_t fs = (uint32_t)(offsetof(Smem, sa) + (wm * 128 + l16 * 8) * 4);
+  const uint32_t fs = (uint32_t)(offsetof(Smem, sa) + (wm * 128 + l16 * 4) * 4);
 #define CIN_FRAG(base, cofs)                                                                \
   ({                                                                                        \
     const uint4 lo_ = *reinterpret_cast<const uint4*>(lds + (base) + (cofs));               \
@@ -393,7 +400,7 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
 #define CIN_SA8(stg)                                                                        \
   do {                                                                                      \
     const float4 lo_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4)); \
-    const float4 hi_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4 + 16)); \
+    const float4 hi_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4 + 256)); \
     sa8[0] = lo_.x; sa8[1] = lo_.y; sa8[2] = lo_.z; sa8[3] = lo_.w;                         \
     sa8[4] = hi_.x; sa8[5] = hi_.y; sa8[6] = hi_.z; sa8[7] = hi_.w;                         \
   } while (0)
@@ -885,7 +892,7 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
   const int fsw = swz_f(l16);
   const uint32_t fa = (uint32_t)((wm * 128 + l16) * TK + (((2 * kq) ^ fsw) << 4));
   const uint32_t fb = (uint32_t)(offsetof(Smem, b) + (wn * 64 + l16) * TK + (((2 * kq) ^ fsw) << 4));
-  const uint32_t fs = (uint32_t)(offsetof(Smem, sa) + (wm * 128 + l16 * 8) * 4);
+  const uint32_t fs = (uint32_t)(offsetof(Smem, sa) + (wm * 128 + l16 * 4) * 4);
 #define CIN_FRAG(base, cofs)                                                                \
   ({                                                                                        \
     const uint4 lo_ = *reinterpret_cast<const uint4*>(lds + (base) + (cofs));               \
@@ -900,7 +907,7 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
 #define CIN_SA8(stg)                                                                        \
   do {                                                                                      \
     const float4 lo_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4)); \
-    const float4 hi_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4 + 16)); \
+    const float4 hi_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4 + 256)); \
     sa8[0] = lo_.x; sa8[1] = lo_.y; sa8[2] = lo_.z; sa8[3] = lo_.w;                         \
     sa8[4] = hi_.x; sa8[5] = hi_.y; sa8[6] = hi_.z; sa8[7] = hi_.w;                         \
   } while (0)
