@@ -1198,7 +1198,11 @@ __device__ __forceinline__ void requant_run(Geo& geo, uint32_t ntiles, const uin
                                             int64_t ssm, uint8_t* qb, int64_t sqbm, uint8_t* qbt,
                                             int64_t sqbtm, bool vec_t, float* sblk, int64_t ssbm,
                                             RequantSmem& sm) {
-  tile_loop<RawQ>(
+  // One register set: without the second the dense kernel holds 5 waves per SIMD (96
+  // VGPRs, no spills), and the VALU-heavy tiles of more workgroups overlap each other's
+  // loads.  Measured on config-4 X: 27.8 against 30.9 us with two sets at 4 waves; the
+  // grouped kernel (more geometry in registers) at 4 waves: 454 against 463 us on config 3.
+  tile_loop_single<RawQ>(
       ntiles, geo, [&](const TileGeo& g, RawQ& r) { load_q<EDGE>(q, sqm, K, srow, ssm, g, r); },
       [&](const TileGeo& g, RawQ& r) {
         if (g.nr == 0) return;  // uniform over the workgroup
@@ -1207,7 +1211,7 @@ __device__ __forceinline__ void requant_run(Geo& geo, uint32_t ntiles, const uin
 }
 
 template <bool EDGE>
-__global__ __launch_bounds__(kThreads) void k_requant128(const uint8_t* __restrict__ q, int64_t M,
+__global__ __launch_bounds__(kThreads, 5) void k_requant128(const uint8_t* __restrict__ q, int64_t M,
                                                          int64_t K, int64_t sqm,
                                                          const float* __restrict__ srow,
                                                          int64_t ssm, uint8_t* qb, int64_t sqbm,
