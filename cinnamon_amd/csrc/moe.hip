@@ -39,6 +39,7 @@ constexpr int kRounds = 4;         // assignments per thread in a route block
 constexpr int kChunk = kRT * kRounds;
 constexpr int kMaxExperts = 4096;  // LDS counters of the route kernels
 constexpr int kMaxTopK = 16;       // positions a combine thread sorts in registers
+constexpr int kRowBatch = 8;       // rows whose pieces a combine wave loads together
 constexpr int kStage = 8192;       // int32 entries of the count matrix staged in LDS by the scan
 
 inline bool valid_dtype(int dt) { return dt == CIN_DT_BF16 || dt == CIN_DT_F32 || dt == CIN_DT_F16; }
@@ -301,6 +302,38 @@ __device__ inline void load8h(const void* base, int64_t off, int64_t nv, float (
   }
 }
 
+// Word i (compile-time) of a 16-byte piece.
+__device__ __forceinline__ uint32_t word_of(const uint4& q, int i) {
+  return i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
+}
+
+// Element e (compile-time) of W consecutive 16-byte pieces holding DT values, widened to fp32.
+template <int DT, int W>
+__device__ __forceinline__ float piece_elem(const uint4 (&q)[W], int e) {
+  if constexpr (DT == CIN_DT_F32) {
+    return __uint_as_float(word_of(q[e >> 2], e & 3));
+  } else {
+    return half_bits_to_f32(DT, (uint16_t)(word_of(q[e >> 3], (e & 7) >> 1) >> (16 * (e & 1))));
+  }
+}
+
+// W 16-byte pieces of G of a token's rows, pos[j0] .. pos[j0 + G - 1], at byte `cb` of
+// each row (rows `rb` bytes apart), every load issued before any result is used: one wave
+// keeps G W loads in flight instead of one.  Rows at or past n load row pos[j0] again
+// (j0 < n); their pieces are never used.  Needs 16-byte aligned pieces.
+template <int G, int W>
+__device__ __forceinline__ void load_rows(const void* base, int64_t cb, int64_t rb,
+                                          const int32_t (&pos)[kMaxTopK], int j0, int n,
+                                          uint4 (&raw)[G][W]) {
+#pragma unroll
+  for (int jj = 0; jj < G; ++jj) {
+    const int64_t r = j0 + jj < n ? pos[j0 + jj] : pos[j0];
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(base) + r * rb + cb);
+#pragma unroll
+    for (int u = 0; u < W; ++u) raw[jj][u] = p[u];
+  }
+}
+
 template <int OT>
 __device__ inline void store4(void* base, int64_t off, int64_t nv, const float (&v)[4]) {
   if constexpr (OT == CIN_DT_F32) {
@@ -338,17 +371,33 @@ __global__ __launch_bounds__(kRT) void k_moe_gather_sum(const void* __restrict__
   if (t >= T) return;  // uniform per wave
   int32_t pos[kMaxTopK], slot[kMaxTopK];
   const int n = token_positions(inv, t, k, A, pos, slot);
+  // whole chunks of rows whose pieces are 16-byte aligned take the batched loads
+  const bool vec = ((((uintptr_t)g) & 15) == 0) && ((sgm * (GT == CIN_DT_F32 ? 4 : 2)) & 15) == 0;
   if constexpr (GT == CIN_DT_F32) {
     for (int64_t c = (int64_t)lane * 8; c < N; c += 512) {
       float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+      if (vec && c + 8 <= N) {
 #pragma unroll
-      for (int j = 0; j < kMaxTopK; ++j) {
-        if (j < n) {
+        for (int j0 = 0; j0 < kMaxTopK; j0 += kRowBatch) {
+          if (j0 < n) {
+            uint4 raw[kRowBatch][2];
+            load_rows<kRowBatch, 2>(g, c * 4, sgm * 4, pos, j0, n, raw);
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            float v[4];
-            load4<GT>(g, (int64_t)pos[j] * sgm + c + 4 * u, N - c - 4 * u, v);
-            for (int e = 0; e < 4; ++e) acc[u][e] = acc[u][e] + v[e];
+            for (int jj = 0; jj < kRowBatch; ++jj)
+              if (j0 + jj < n)
+                for (int e = 0; e < 8; ++e) acc[e >> 2][e & 3] = acc[e >> 2][e & 3] + piece_elem<GT, 2>(raw[jj], e);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kMaxTopK; ++j) {
+          if (j < n) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              float v[4];
+              load4<GT>(g, (int64_t)pos[j] * sgm + c + 4 * u, N - c - 4 * u, v);
+              for (int e = 0; e < 4; ++e) acc[u][e] = acc[u][e] + v[e];
+            }
           }
         }
       }
@@ -361,14 +410,28 @@ __global__ __launch_bounds__(kRT) void k_moe_gather_sum(const void* __restrict__
       float acc[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+      if (vec && c + 16 <= N) {
 #pragma unroll
-      for (int j = 0; j < kMaxTopK; ++j) {
-        if (j < n) {
+        for (int j0 = 0; j0 < kMaxTopK; j0 += kRowBatch) {
+          if (j0 < n) {
+            uint4 raw[kRowBatch][2];
+            load_rows<kRowBatch, 2>(g, c * 2, sgm * 2, pos, j0, n, raw);
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            float v[8];
-            load8h<GT>(g, (int64_t)pos[j] * sgm + c + 8 * u, N - c - 8 * u, v);
-            for (int e = 0; e < 8; ++e) acc[8 * u + e] = acc[8 * u + e] + v[e];
+            for (int jj = 0; jj < kRowBatch; ++jj)
+              if (j0 + jj < n)
+                for (int e = 0; e < 16; ++e) acc[e] = acc[e] + piece_elem<GT, 2>(raw[jj], e);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kMaxTopK; ++j) {
+          if (j < n) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              float v[8];
+              load8h<GT>(g, (int64_t)pos[j] * sgm + c + 8 * u, N - c - 8 * u, v);
+              for (int e = 0; e < 8; ++e) acc[8 * u + e] = acc[8 * u + e] + v[e];
+            }
           }
         }
       }
@@ -404,17 +467,34 @@ __global__ __launch_bounds__(kRT) void k_moe_combine(const void* __restrict__ y,
   float w[kMaxTopK];
 #pragma unroll
   for (int j = 0; j < kMaxTopK; ++j) w[j] = j < n ? score_at<ST>(scores, t * ssm + slot[j]) : 0.0f;
+  // whole chunks of rows whose pieces are 16-byte aligned take the batched loads
+  const bool vec = ((((uintptr_t)y) & 15) == 0) && ((sym * (YT == CIN_DT_F32 ? 4 : 2)) & 15) == 0;
   if constexpr (YT == CIN_DT_F32) {
     for (int64_t c = (int64_t)lane * 8; c < N; c += 512) {
       float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+      if (vec && c + 8 <= N) {
 #pragma unroll
-      for (int j = 0; j < kMaxTopK; ++j) {
-        if (j < n) {
+        for (int j0 = 0; j0 < kMaxTopK; j0 += kRowBatch) {
+          if (j0 < n) {
+            uint4 raw[kRowBatch][2];
+            load_rows<kRowBatch, 2>(y, c * 4, sym * 4, pos, j0, n, raw);
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            float v[4];
-            load4<YT>(y, (int64_t)pos[j] * sym + c + 4 * u, N - c - 4 * u, v);
-            for (int e = 0; e < 4; ++e) acc[u][e] = acc[u][e] + v[e] * w[j];
+            for (int jj = 0; jj < kRowBatch; ++jj)
+              if (j0 + jj < n)
+                for (int e = 0; e < 8; ++e)
+                  acc[e >> 2][e & 3] = acc[e >> 2][e & 3] + piece_elem<YT, 2>(raw[jj], e) * w[j0 + jj];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kMaxTopK; ++j) {
+          if (j < n) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              float v[4];
+              load4<YT>(y, (int64_t)pos[j] * sym + c + 4 * u, N - c - 4 * u, v);
+              for (int e = 0; e < 4; ++e) acc[u][e] = acc[u][e] + v[e] * w[j];
+            }
           }
         }
       }
@@ -427,14 +507,28 @@ __global__ __launch_bounds__(kRT) void k_moe_combine(const void* __restrict__ y,
       float acc[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+      if (vec && c + 16 <= N) {
 #pragma unroll
-      for (int j = 0; j < kMaxTopK; ++j) {
-        if (j < n) {
+        for (int j0 = 0; j0 < kMaxTopK; j0 += kRowBatch) {
+          if (j0 < n) {
+            uint4 raw[kRowBatch][2];
+            load_rows<kRowBatch, 2>(y, c * 2, sym * 2, pos, j0, n, raw);
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            float v[8];
-            load8h<YT>(y, (int64_t)pos[j] * sym + c + 8 * u, N - c - 8 * u, v);
-            for (int e = 0; e < 8; ++e) acc[8 * u + e] = acc[8 * u + e] + v[e] * w[j];
+            for (int jj = 0; jj < kRowBatch; ++jj)
+              if (j0 + jj < n)
+                for (int e = 0; e < 16; ++e) acc[e] = acc[e] + piece_elem<YT, 2>(raw[jj], e) * w[j0 + jj];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kMaxTopK; ++j) {
+          if (j < n) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              float v[8];
+              load8h<YT>(y, (int64_t)pos[j] * sym + c + 8 * u, N - c - 8 * u, v);
+              for (int e = 0; e < 8; ++e) acc[8 * u + e] = acc[8 * u + e] + v[e] * w[j];
+            }
           }
         }
       }

@@ -114,6 +114,43 @@ def test_gather_sum_in_sorted_order(dev, gdtype, odtype):
     assert torch.equal(out.cpu(), want)
 
 
+def _partial_routing(T, k, E, seed):
+    """Uniform routing with every 7th token's first assignment outside the experts (dropped),
+    so tokens have k or k - 1 rows."""
+    top_idx, scores = _routing(T, k, E, seed=seed, zipf=False)
+    top_idx[::7, 0] = E + 1
+    return top_idx, scores
+
+
+# Rows whose 16-byte pieces are aligned take the batched loads (up to 8 rows of a token at
+# once): k not a multiple of 8, k above 8, dropped assignments, and a last column chunk
+# that is partial (1032 = 64 x 16 + 8) or whole (1040).
+@pytest.mark.parametrize("k,D,gdtype,odtype", [(6, 1032, torch.bfloat16, torch.float32),
+                                               (12, 1040, torch.float32, torch.bfloat16),
+                                               (3, 1032, torch.float16, torch.float32),
+                                               (9, 1032, torch.float32, torch.float32)])
+def test_gather_sum_batched_rows(dev, k, D, gdtype, odtype):
+    T, E = 257, 11
+    top_idx, _ = _partial_routing(T, k, E, seed=21 + k)
+    perm, inv, *_ = moe.moe_route(top_idx.to(dev), E)
+    g = torch.randn(T * k, D, generator=torch.Generator().manual_seed(22)).to(gdtype)
+    out = moe.moe_gather_sum(g.to(dev), inv, k, odtype)
+    want = _ordered_token_sums(g.float(), inv.cpu(), T, k).to(odtype)
+    assert torch.equal(out.cpu(), want)
+
+
+@pytest.mark.parametrize("k,D,ydtype", [(6, 1032, torch.float16), (12, 1032, torch.float32),
+                                        (3, 1040, torch.bfloat16), (8, 1032, torch.float16)])
+def test_combine_batched_rows(dev, k, D, ydtype):
+    T, E = 257, 11
+    top_idx, scores = _partial_routing(T, k, E, seed=31 + k)
+    perm, inv, *_ = moe.moe_route(top_idx.to(dev), E)
+    y = torch.randn(T * k, D, generator=torch.Generator().manual_seed(32)).to(ydtype)
+    out = moe.moe_combine(y.to(dev), scores.to(dev), inv)
+    want = _ordered_token_sums(y.float(), inv.cpu(), T, k, weights=scores)
+    assert torch.equal(out.cpu(), want)
+
+
 @pytest.mark.parametrize("sdtype,ydtype", [(torch.bfloat16, torch.float32), (torch.float32, torch.float32),
                                            (torch.float32, torch.float16), (torch.bfloat16, torch.float16)])
 def test_combine_equals_reference_scatter_add(dev, sdtype, ydtype):
