@@ -383,20 +383,26 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
   // (stage, m/n-tile) offset; the high half is chunk 2kq+1, i.e. byte offset ^ 16.
   const uint8_t* lds = reinterpret_cast<const uint8_t*>(&sm);
   const int fsw = swz_f(l16);
-  const uint32_t fa = (uint32_t)((wm * 128 + l16) * TK + (((2 * kq) ^ fsw) << 4));
-  const uint32_t fb = (uint32_t)(offsetof(Smem, b) + (wn * 64 + l16) * TK + (((2 * kq) ^ fsw) << 4));
-  const uint32_t fs = (uint32_t)(offsetof(Smem, sa) + (wm * 128 + l16 * 4) * 4);
-#define CIN_FRAG(base, cofs)                                                                \
+  // Per-lane LDS addresses of the fragment reads, hidden from the compiler: it would
+  // otherwise split each into a lane part and a constant and, where the constant passes
+  // the 64 KB immediate-offset range (B's second stage, the scales), keep one register per
+  // (stage, tile) address.  Each read below is one of these bases plus an offset < 64 KB.
+  uint32_t fa = (uint32_t)((wm * 128 + l16) * TK + (((2 * kq) ^ fsw) << 4));
+  uint32_t fb = (uint32_t)(offsetof(Smem, b) + (wn * 64 + l16) * TK + (((2 * kq) ^ fsw) << 4));
+  uint32_t fs = (uint32_t)(offsetof(Smem, sa) + (wm * 128 + l16 * 4) * 4);
+  uint32_t fa_hi = fa ^ 16u, fb_hi = fb ^ 16u;  // the fragments' high halves: chunk 2 kq + 1
+  asm volatile("" : "+v"(fa), "+v"(fb), "+v"(fs), "+v"(fa_hi), "+v"(fb_hi));
+#define CIN_FRAG(base, base_hi, cofs)                                                       \
   ({                                                                                        \
     const uint4 lo_ = *reinterpret_cast<const uint4*>(lds + (base) + (cofs));               \
-    const uint4 hi_ = *reinterpret_cast<const uint4*>(lds + ((base) ^ 16u) + (cofs));       \
+    const uint4 hi_ = *reinterpret_cast<const uint4*>(lds + (base_hi) + (cofs));            \
     v8i v_;                                                                                 \
     v_[0] = (int)lo_.x; v_[1] = (int)lo_.y; v_[2] = (int)lo_.z; v_[3] = (int)lo_.w;         \
     v_[4] = (int)hi_.x; v_[5] = (int)hi_.y; v_[6] = (int)hi_.z; v_[7] = (int)hi_.w;         \
     v_;                                                                                     \
   })
-#define CIN_AFRAG(stg, mt) CIN_FRAG(fa, (uint32_t)((stg) * kTileBytes + (mt) * 16 * TK))
-#define CIN_BFRAG(stg, nt) CIN_FRAG(fb, (uint32_t)((stg) * kTileBytes + (nt) * 16 * TK))
+#define CIN_AFRAG(stg, mt) CIN_FRAG(fa, fa_hi, (uint32_t)((stg) * kTileBytes + (mt) * 16 * TK))
+#define CIN_BFRAG(stg, nt) CIN_FRAG(fb, fb_hi, (uint32_t)((stg) * kTileBytes + (nt) * 16 * TK))
 #define CIN_SA8(stg)                                                                        \
   do {                                                                                      \
     const float4 lo_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4)); \
@@ -890,20 +896,26 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
   } while (0)
   const uint8_t* lds = reinterpret_cast<const uint8_t*>(&sm);
   const int fsw = swz_f(l16);
-  const uint32_t fa = (uint32_t)((wm * 128 + l16) * TK + (((2 * kq) ^ fsw) << 4));
-  const uint32_t fb = (uint32_t)(offsetof(Smem, b) + (wn * 64 + l16) * TK + (((2 * kq) ^ fsw) << 4));
-  const uint32_t fs = (uint32_t)(offsetof(Smem, sa) + (wm * 128 + l16 * 4) * 4);
-#define CIN_FRAG(base, cofs)                                                                \
+  // Per-lane LDS addresses of the fragment reads, hidden from the compiler: it would
+  // otherwise split each into a lane part and a constant and, where the constant passes
+  // the 64 KB immediate-offset range (B's second stage, the scales), keep one register per
+  // (stage, tile) address.  Each read below is one of these bases plus an offset < 64 KB.
+  uint32_t fa = (uint32_t)((wm * 128 + l16) * TK + (((2 * kq) ^ fsw) << 4));
+  uint32_t fb = (uint32_t)(offsetof(Smem, b) + (wn * 64 + l16) * TK + (((2 * kq) ^ fsw) << 4));
+  uint32_t fs = (uint32_t)(offsetof(Smem, sa) + (wm * 128 + l16 * 4) * 4);
+  uint32_t fa_hi = fa ^ 16u, fb_hi = fb ^ 16u;  // the fragments' high halves: chunk 2 kq + 1
+  asm volatile("" : "+v"(fa), "+v"(fb), "+v"(fs), "+v"(fa_hi), "+v"(fb_hi));
+#define CIN_FRAG(base, base_hi, cofs)                                                       \
   ({                                                                                        \
     const uint4 lo_ = *reinterpret_cast<const uint4*>(lds + (base) + (cofs));               \
-    const uint4 hi_ = *reinterpret_cast<const uint4*>(lds + ((base) ^ 16u) + (cofs));       \
+    const uint4 hi_ = *reinterpret_cast<const uint4*>(lds + (base_hi) + (cofs));            \
     v8i v_;                                                                                 \
     v_[0] = (int)lo_.x; v_[1] = (int)lo_.y; v_[2] = (int)lo_.z; v_[3] = (int)lo_.w;         \
     v_[4] = (int)hi_.x; v_[5] = (int)hi_.y; v_[6] = (int)hi_.z; v_[7] = (int)hi_.w;         \
     v_;                                                                                     \
   })
-#define CIN_AFRAG(stg, mt) CIN_FRAG(fa, (uint32_t)((stg) * kTileBytes + (mt) * 16 * TK))
-#define CIN_BFRAG(stg, nt) CIN_FRAG(fb, (uint32_t)((stg) * kTileBytes + (nt) * 16 * TK))
+#define CIN_AFRAG(stg, mt) CIN_FRAG(fa, fa_hi, (uint32_t)((stg) * kTileBytes + (mt) * 16 * TK))
+#define CIN_BFRAG(stg, nt) CIN_FRAG(fb, fb_hi, (uint32_t)((stg) * kTileBytes + (nt) * 16 * TK))
 #define CIN_SA8(stg)                                                                        \
   do {                                                                                      \
     const float4 lo_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4)); \
