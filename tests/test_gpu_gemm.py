@@ -55,6 +55,8 @@ def _run_fp32_and_bf16(kern, dev, xq, xs, wq, ws):
     (129, 257, 144),      # K not a multiple of 128
     (1, 128, 128),
     (16368, 1024, 1024),  # config 5 MTP rows
+    (4100, 4224, 512),    # more 256 x 256 tiles than CUs (persistent walk), last row and column shifted
+    (2304, 7296, 4096),   # persistent walk with the XCD-rotated K order (32 K blocks)
 ])
 def test_gemm_parity(kern, dev, M, N, K):
     xq, xs, wq, ws = _operands(M, N, K, seed=M + N + K)
