@@ -1169,6 +1169,15 @@ int device_cus() {
 
 }  // namespace
 
+namespace {
+// C[m, 0 .. w) = 0 for m < rows, in 16-bit words, rows `ld` words apart (grid-stride).
+__global__ void k_zero_rows16(uint16_t* __restrict__ c, int64_t rows, int64_t w, int64_t ld) {
+  const int64_t n = rows * w;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    c[(i / w) * ld + i % w] = 0;
+}
+}  // namespace
+
 extern "C" {
 
 int cin_gemm_fp8_bs(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam, int64_t ssak,
@@ -1187,11 +1196,13 @@ int cin_gemm_fp8_bs(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam
   CIN_CHECK_ARG(cdiv(M, BM) * cdiv(N, BN) < ((int64_t)1 << 31), "gemm_fp8_bs: grid too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (K == 0) {
-    // empty reduction: C = 0 (same as the reference's zero-initialised accumulator)
-    hipError_t e = hipMemset2DAsync(C, ldc * (c_dtype == CIN_DT_F32 ? 4 : 2), 0,
-                                    N * (c_dtype == CIN_DT_F32 ? 4 : 2), M, s);
-    if (e != hipSuccess) return cin_set_error(CIN_ERR_HIP, "gemm_fp8_bs: %s", hipGetErrorString(e));
-    return CIN_OK;
+    // empty reduction: C = 0 (same as the reference's zero-initialised accumulator), by a
+    // kernel rather than a memset node, so the call can be captured in a graph
+    const int64_t es = c_dtype == CIN_DT_F32 ? 4 : 2;
+    const int64_t words = M * N * es / 2;
+    const unsigned grid = (unsigned)(cdiv(words, 256) < 65536 ? cdiv(words, 256) : 65536);
+    hipLaunchKernelGGL(k_zero_rows16, grid, 256, 0, s, static_cast<uint16_t*>(C), M, N * es / 2, ldc * es / 2);
+    return cin_check_launch("gemm_fp8_bs");
   }
   if (K % big::TK == 0 && M >= big::TM && N >= big::TN && N % 128 == 0) {
     const uint32_t tm = (uint32_t)cdiv(M, big::TM), tn = (uint32_t)cdiv(N, big::TN);

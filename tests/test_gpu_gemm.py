@@ -187,3 +187,20 @@ def test_grouped_equals_dense_for_one_expert(kern, dev):
                                 ends.to(dev), out_dtype=torch.float32)
     b = kern.fp8_gemm_bs(xq.to(dev), xs.to(dev), wq[0].to(dev), ws[0].to(dev), torch.float32)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gemm_empty_reduction_zeroes_c(dev, dtype):
+    """K = 0: C[:M, :N] = 0 (the reference's zero accumulator), written by a kernel; the
+    columns past N in each row of a strided C are left alone."""
+    from cinnamon_amd import _lib
+    M, N, ld = 300, 136, 160
+    c = torch.full((M, ld), float("nan"), dtype=dtype, device=dev)
+    a = torch.zeros(M, 16, dtype=torch.uint8, device=dev)
+    b = torch.zeros(N, 16, dtype=torch.uint8, device=dev)
+    s = torch.ones(M, 1, dtype=torch.float32, device=dev)
+    _lib.call("cin_gemm_fp8_bs", _lib.ptr(a), 16, _lib.ptr(s), 1, 1, _lib.ptr(b), 16, _lib.ptr(s), 1, 1,
+              M, N, 0, _lib.ptr(c), _lib.dtype_code(c), ld, _lib.stream_of(c))
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(c[:, :N].float())) == 0
+    assert bool(torch.isnan(c[:, N:].float()).all())
