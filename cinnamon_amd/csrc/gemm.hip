@@ -309,6 +309,13 @@ __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, ui
 }
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima)
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// Vector memory operations a wave issues for one K block's DMA: 4 row groups x (A, B), plus
+// the A scales on waves 0-3.  s_waitcnt vmcnt(8): everything but the last 8 has completed.
+constexpr int kDmaOpsPerBlock = 8;
+__device__ __forceinline__ void wait_dma_but_block() {
+  static_assert(kDmaOpsPerBlock == 8, "encoding below is vmcnt(8)");
+  __builtin_amdgcn_s_waitcnt(0x0F78);
+}
 
 // One full 256 x 256 tile.  A / sa point at the tile's first row, B / sb at its first
 // column block; the tile stores local rows [row_lo, row_hi) and local columns >= col_lo.
@@ -417,10 +424,17 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  // prologue: blocks 0 and 1 into stages 0 and 1
+  // prologue: blocks 0 and 1 into stages 0 and 1.  The loop starts once block 0 has
+  // landed: block 1's DMA is at least kDmaOpsPerBlock operations issued after block 0's,
+  // vector memory operations retire from vmcnt in issue order, and block 1 is waited for
+  // at the first K block's barrier.
   CIN_DMA(0, 0);
-  if (nk > 1) CIN_DMA(1, 1);
-  wait_dma();
+  if (nk > 1) {
+    CIN_DMA(1, 1);
+    wait_dma_but_block();
+  } else {
+    wait_dma();
+  }
   __syncthreads();
 
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
