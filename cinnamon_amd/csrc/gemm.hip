@@ -1142,6 +1142,16 @@ int device_cus() {
   return cached[dev];
 }
 
+// The 256 x 256 kernels address a tile's operands by 32-bit offsets from its first row
+// (DMA descriptors): 255 rows of A and B plus a K span of `klen` bytes, and 255 rows of
+// A-scales plus klen / 128 K blocks of them.  Shapes past that take the 128 x 128 kernels,
+// which use 64-bit addresses.
+bool big_offsets_fit(int64_t lda, int64_t ldb, int64_t klen, int64_t ssam, int64_t ssak) {
+  const int64_t lim = (int64_t)1 << 32;
+  const int64_t nkb = klen / 128 > 0 ? klen / 128 : 1;
+  return 255 * lda + klen < lim && 255 * ldb + klen < lim && (255 * ssam + (nkb - 1) * ssak + 1) * 4 < lim;
+}
+
 }  // namespace
 
 namespace {
@@ -1179,7 +1189,7 @@ int cin_gemm_fp8_bs(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam
     hipLaunchKernelGGL(k_zero_rows16, grid, 256, 0, s, static_cast<uint16_t*>(C), M, N * es / 2, ldc * es / 2);
     return cin_check_launch("gemm_fp8_bs");
   }
-  if (K % big::TK == 0 && M >= big::TM && N >= big::TN && N % 128 == 0) {
+  if (K % big::TK == 0 && M >= big::TM && N >= big::TN && N % 128 == 0 && big_offsets_fit(lda, ldb, K, ssam, ssak)) {
     const uint32_t tm = (uint32_t)cdiv(M, big::TM), tn = (uint32_t)cdiv(N, big::TN);
     hipLaunchKernelGGL(big::k_gemm_fp8_bs_256, tm * tn, big::kThreads, 0, s, A, lda, sa, ssam,
                        ssak, B, ldb, sb, ssbn, ssbk, M, N, K, C, c_dtype, ldc, tm, tn);
@@ -1208,7 +1218,7 @@ int cin_grouped_gemm_fp8(const uint8_t* A, int64_t lda, const float* sa, int64_t
                     aligned16(A) && aligned16(B),
                 "grouped_gemm_fp8: A/B rows must be 16-byte aligned and K-contiguous");
   CIN_CHECK_ARG(ldc >= N, "grouped_gemm_fp8: bad C stride");
-  if (K % big::TK == 0 && T >= big::TM && N >= big::TN && N % 128 == 0) {
+  if (K % big::TK == 0 && T >= big::TM && N >= big::TN && N % 128 == 0 && big_offsets_fit(lda, ldb, K, ssam, ssak)) {
     const int64_t mt = cdiv(T, big::TM) + E;
     const uint32_t tn = (uint32_t)cdiv(N, big::TN);
     CIN_CHECK_ARG(mt * tn < ((int64_t)1 << 31), "grouped_gemm_fp8: grid too large");
@@ -1256,6 +1266,8 @@ int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, i
                 "grouped_wgrad_fp8: padded capacity exceeds the operand rows");
   CIN_CHECK_ARG(ldc >= K && sce >= N * ldc, "grouped_wgrad_fp8: bad C strides");
   CIN_CHECK_ARG(ssbm >= K / 128, "grouped_wgrad_fp8: bad B-scale stride");
+  CIN_CHECK_ARG(big_offsets_fit(lda, ldb, tcap, ssam, 1),
+                "grouped_wgrad_fp8: operand rows too long for the 256 x 256 tile's 32-bit offsets");
   const int64_t tm = cdiv(N, big::TM), tn = cdiv(K, big::TN);
   CIN_CHECK_ARG(E * tm * tn < ((int64_t)1 << 31), "grouped_wgrad_fp8: grid too large");
   const uint32_t ntot = (uint32_t)(E * tm * tn);

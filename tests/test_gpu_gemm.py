@@ -204,3 +204,21 @@ def test_gemm_empty_reduction_zeroes_c(dev, dtype):
     torch.cuda.synchronize()
     assert int(torch.count_nonzero(c[:, :N].float())) == 0
     assert bool(torch.isnan(c[:, N:].float()).all())
+
+
+def test_gemm_rows_past_32bit_tile_offsets(kern, dev):
+    """Row strides past the 256 x 256 kernel's 32-bit tile offsets (255 * ld + K >= 2^32)
+    take the 128 x 128 kernel, which addresses in 64 bits: results within tolerance."""
+    M, N, K = 256, 256, 256
+    ld = (1 << 24) + 256  # bytes per row of A and of B
+    xq, xs, wq, ws = _operands(M, N, K, seed=77)
+    a = torch.empty(M, ld, dtype=torch.uint8, device=dev)[:, :K]
+    b = torch.empty(N, ld, dtype=torch.uint8, device=dev)[:, :K]
+    a.copy_(xq.view(torch.uint8).to(dev))
+    b.copy_(wq.view(torch.uint8).to(dev))
+    y = kern.fp8_gemm_bs(a.view(torch.float8_e4m3fn), xs.to(dev), b.view(torch.float8_e4m3fn), ws.to(dev),
+                         torch.float32)
+    torch.cuda.synchronize()
+    want = orc.gemm_ref(xq, xs, wq.view(torch.uint8).t().contiguous(), ws.t().contiguous())
+    _check(y, want, "gemm with 16 MiB rows")
+    del a, b
