@@ -751,6 +751,7 @@ using big::TK;
 using big::TM;
 using big::TN;
 using big::wait_dma;
+using big::wait_dma_but_block;
 constexpr int kThreads = big::kThreads;
 
 // Scales and expert ranges do not change during a kernel: read through the constant address
@@ -851,6 +852,42 @@ __device__ __forceinline__ void store_direct(const Tile& T, const v4f (&acc)[8][
   }
 }
 
+// Where the lanes of store_counted whose element lies outside the tile's rows or columns
+// write instead: one 8-byte slot per lane, never read.
+__device__ uint2 g_store_sink[64];
+
+// 16-bit C of one tile with exactly kEpiStores 8-byte stores per wave, whatever the tile's
+// row and column limits: a lane outside them writes its slot of g_store_sink.  The fixed
+// count lets the next tile wait for its first K block with vmcnt(kEpiStores + 8): that
+// block was issued before these stores and block 1 (at most 9 operations) after it, and
+// vector memory operations retire from the count in issue order, so the stores drain while
+// the next tile starts.  C must be 8-byte aligned with ldc a multiple of 4.
+constexpr int kEpiStores = 32;
+__device__ __forceinline__ void store_counted(const Tile& T, const v4f (&acc)[8][4], int wm, int wn, int l16,
+                                              int kq, int c_dtype, int64_t ldc) {
+  const int rl = wm * 128 + l16, cl = wn * 64 + kq * 4;
+  uint16_t* c0 = static_cast<uint16_t*>(T.C) + (int64_t)rl * ldc + cl;
+  uint2* sink = &g_store_sink[threadIdx.x & 63];
+  const uint32_t rows = (uint32_t)(T.row_hi - T.row_lo);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bool rok = (uint32_t)(rl + 16 * i - T.row_lo) < rows;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool ok = rok && cl + 16 * j >= T.col_lo;
+      uint2* p = ok ? reinterpret_cast<uint2*>(c0 + (int64_t)(16 * i) * ldc + 16 * j) : sink;
+      const uint32_t b0 = f32_to_half_bits(c_dtype, acc[i][j][0]), b1 = f32_to_half_bits(c_dtype, acc[i][j][1]);
+      const uint32_t b2 = f32_to_half_bits(c_dtype, acc[i][j][2]), b3 = f32_to_half_bits(c_dtype, acc[i][j][3]);
+      *p = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+    }
+  }
+}
+// s_waitcnt vmcnt(kEpiStores + 8): all but the last 40 vector memory operations done
+__device__ __forceinline__ void wait_dma_past_stores() {
+  static_assert(kEpiStores + 8 == 40, "encoding below is vmcnt(40)");
+  __builtin_amdgcn_s_waitcnt(0x8F78);
+}
+
 // A pointer as a wave-uniform value (the DMA's buffer descriptor lives in SGPRs).
 template <class P>
 __device__ __forceinline__ P* uniform_ptr(P* p) {
@@ -860,7 +897,9 @@ __device__ __forceinline__ P* uniform_ptr(P* p) {
   return (P*)(uintptr_t)((hi << 32) | lo);
 }
 
-template <class Src>
+// OUT16: 16-bit C, 8-byte aligned, ldc a multiple of 4 (the counted epilogue); otherwise
+// every tile stores with store_direct and the next tile waits for everything.
+template <bool OUT16, class Src>
 __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t ssam, int64_t ssak,
                                           int64_t ldb, int64_t ssbn, int64_t ssbk, int64_t K,
                                           int c_dtype, int64_t ldc) {
@@ -949,6 +988,7 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
     if (nk > 1) CIN_DMA_P(pA, pB, pS, 1, 1);
   }
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  bool first = true;  // the first tile: both blocks' DMA and nothing after them
   for (;;) {
     // this tile's operands (its blocks 0 and 1 are already on their way)
     const uint8_t* pA;
@@ -963,7 +1003,14 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
       pS = uniform_ptr(T.sa);
       sbp = (const cfloat*)uniform_ptr(T.sb + (int64_t)(wn >> 1) * ssbn);
     }
-    wait_dma();
+    // block 0 has landed: block 1 (and, with OUT16, the previous tile's stores) may still
+    // be in flight; they are waited for at the first K block's barrier
+    if (nk > 1 && first)
+      wait_dma_but_block();
+    else if (OUT16 && nk > 1)
+      wait_dma_past_stores();
+    else
+      wait_dma();
     __syncthreads();
     v4f acc[8][4];
 #pragma unroll
@@ -1061,8 +1108,12 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
       }
       return;
     }
-    store_direct(T, acc, wm, wn, l16, kq, c_dtype, ldc);
+    if constexpr (OUT16)
+      store_counted(T, acc, wm, wn, l16, kq, c_dtype, ldc);
+    else
+      store_direct(T, acc, wm, wn, l16, kq, c_dtype, ldc);
     if (!next) return;
+    first = false;
     v += G;
   }
 #undef CIN_DMA_P
@@ -1075,6 +1126,7 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
 
 constexpr int kMaxExpertsLds = 4096;
 
+template <bool OUT16>
 __global__ __launch_bounds__(kThreads, 1) void k_grouped_gemm_fp8_pers(
     const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
     int64_t ssak, const uint8_t* __restrict__ B, int64_t sbe, int64_t ldb,
@@ -1121,7 +1173,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_gemm_fp8_pers(
   src.lda = lda; src.ssam = ssam; src.ldb = ldb; src.sbe = sbe; src.ssbe = ssbe; src.ssbn = ssbn;
   src.ldc = ldc; src.Tn = Tn; src.N = N; src.es = c_dtype == CIN_DT_F32 ? 4 : 2;
   src.tiles_n = tiles_n; src.starts = starts; src.ends = ends; src.E = E; src.tpre = tpre;
-  run_tiles(src, lda, ssam, ssak, ldb, ssbn, ssbk, K, c_dtype, ldc);
+  run_tiles<OUT16>(src, lda, ssam, ssak, ldb, ssbn, ssbk, K, c_dtype, ldc);
 }
 
 }  // namespace pers
@@ -1225,9 +1277,15 @@ int cin_grouped_gemm_fp8(const uint8_t* A, int64_t lda, const float* sa, int64_t
     if (E <= pers::kMaxExpertsLds) {
       const int64_t ncu = device_cus();
       const unsigned grid = (unsigned)(mt * tn < ncu ? mt * tn : ncu);
-      hipLaunchKernelGGL(pers::k_grouped_gemm_fp8_pers, grid, big::kThreads, 0,
-                         static_cast<hipStream_t>(stream), A, lda, sa, ssam, ssak, B, sbe, ldb, sb,
-                         ssbe, ssbn, ssbk, starts, ends, (int)E, T, N, K, C, c_dtype, ldc, tn);
+      const bool out16 = c_dtype != CIN_DT_F32 && (((uintptr_t)C) & 7) == 0 && ldc % 4 == 0;
+      if (out16)
+        hipLaunchKernelGGL(pers::k_grouped_gemm_fp8_pers<true>, grid, big::kThreads, 0,
+                           static_cast<hipStream_t>(stream), A, lda, sa, ssam, ssak, B, sbe, ldb, sb,
+                           ssbe, ssbn, ssbk, starts, ends, (int)E, T, N, K, C, c_dtype, ldc, tn);
+      else
+        hipLaunchKernelGGL(pers::k_grouped_gemm_fp8_pers<false>, grid, big::kThreads, 0,
+                           static_cast<hipStream_t>(stream), A, lda, sa, ssam, ssak, B, sbe, ldb, sb,
+                           ssbe, ssbn, ssbk, starts, ends, (int)E, T, N, K, C, c_dtype, ldc, tn);
       return cin_check_launch("grouped_gemm_fp8");
     }
     hipLaunchKernelGGL(big::k_grouped_gemm_fp8_256, (unsigned)(mt * tn), big::kThreads, 0,

@@ -180,6 +180,33 @@ def test_grouped_gemm_parity(kern, dev, counts, N, K):
     assert torch.equal(out16.cpu(), out.cpu().to(torch.bfloat16))
 
 
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_grouped_gemm_leaves_rows_outside_ranges(kern, dev, out_dtype):
+    """Expert ranges with gaps between them (rows no expert covers), a partial last n-tile
+    (N = 640) and partial expert tiles: every covered element equals the fp32 result
+    rounded to the output type, and every other element of a NaN-filled output stays NaN
+    (16-bit outputs take the fixed-count epilogue, whose out-of-tile lanes write elsewhere)."""
+    from cinnamon_amd import layers
+    N, K = 640, 512
+    xq, xs, wq, ws, _, _ = _grouped_case([520, 300, 900, 280], N, K, seed=31)
+    starts = torch.tensor([0, 600, 1000, 1900], dtype=torch.int64)
+    ends = torch.tensor([420, 870, 1850, 2000], dtype=torch.int64)
+    want = orc.grouped_gemm_ref(xq, xs, wq, ws, starts, ends)
+    ref32 = layers.fp8_grouped_gemm(xq.to(dev), xs.to(dev), wq.to(dev), ws.to(dev), starts.to(dev),
+                                    ends.to(dev), out_dtype=torch.float32)
+    out = torch.full((2000, N), float("nan"), dtype=out_dtype, device=dev)
+    layers.fp8_grouped_gemm(xq.to(dev), xs.to(dev), wq.to(dev), ws.to(dev), starts.to(dev), ends.to(dev),
+                            out_dtype=out_dtype, out=out)
+    torch.cuda.synchronize()
+    covered = torch.zeros(2000, dtype=torch.bool)
+    for s0, s1 in zip(starts.tolist(), ends.tolist()):
+        covered[s0:s1] = True
+    got = out.cpu()
+    assert bool(torch.isnan(got[~covered].float()).all())
+    assert torch.equal(got[covered], ref32.cpu()[covered].to(out_dtype))
+    _check(ref32.cpu()[covered], want[covered], "grouped with gaps")
+
+
 def test_grouped_equals_dense_for_one_expert(kern, dev):
     from cinnamon_amd import layers
     xq, xs, wq, ws, starts, ends = _grouped_case([1000], 256, 384, seed=21)
