@@ -779,6 +779,32 @@ __device__ inline uint32_t first_tile(uint32_t b, uint32_t G) {
   return (G & 7u) ? b : (b & 7u) * (G >> 3) + (b >> 3);
 }
 
+// Dense: tile v -> (tm, tn) by the grouped raster; the last tile of a row / column shifts
+// back onto its neighbour and stores only its own rows / columns.
+struct DenseSrc {
+  const uint8_t* A; const float* sa; const uint8_t* B; const float* sb; uint8_t* C;
+  int64_t lda, ssam, ldb, ssbn, ldc, M, N;
+  int es;
+  uint32_t tiles_m, tiles_n;
+  __device__ bool get(uint32_t v, Tile& t) const {
+    if (v >= tiles_m * tiles_n) return false;
+    uint32_t tm, tn;
+    raster(v, tiles_m, tiles_n, tm, tn);
+    const int64_t m_nom = (int64_t)tm * TM, n_nom = (int64_t)tn * TN;
+    const int64_t m0 = m_nom + TM <= M ? m_nom : M - TM;
+    const int64_t n0 = n_nom + TN <= N ? n_nom : N - TN;
+    t.A = A + m0 * lda;
+    t.sa = sa + m0 * ssam;
+    t.B = B + n0 * ldb;
+    t.sb = sb + (n0 >> 7) * ssbn;
+    t.C = C + (m0 * ldc + n0) * es;
+    t.row_lo = (int)(m_nom - m0);
+    t.row_hi = TM;
+    t.col_lo = (int)(n_nom - n0);
+    return true;
+  }
+};
+
 // Grouped forward: global m-tile gm of the concatenated experts -> expert by binary search
 // in tpre (tpre[e] = 256-row tiles of the experts before e, tpre[E] = all of them).
 struct GroupedSrc {
@@ -1124,6 +1150,20 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
 #undef CIN_SA8
 }
 
+template <bool OUT16>
+__global__ __launch_bounds__(kThreads, 1) void k_gemm_fp8_bs_pers(
+    const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
+    int64_t ssak, const uint8_t* __restrict__ B, int64_t ldb, const float* __restrict__ sb,
+    int64_t ssbn, int64_t ssbk, int64_t M, int64_t N, int64_t K, void* C, int c_dtype,
+    int64_t ldc, uint32_t tiles_m, uint32_t tiles_n) {
+  DenseSrc src;
+  src.A = A; src.sa = sa; src.B = B; src.sb = sb; src.C = static_cast<uint8_t*>(C);
+  src.lda = lda; src.ssam = ssam; src.ldb = ldb; src.ssbn = ssbn; src.ldc = ldc; src.M = M; src.N = N;
+  src.es = c_dtype == CIN_DT_F32 ? 4 : 2;
+  src.tiles_m = tiles_m; src.tiles_n = tiles_n;
+  run_tiles<OUT16>(src, lda, ssam, ssak, ldb, ssbn, ssbk, K, c_dtype, ldc);
+}
+
 constexpr int kMaxExpertsLds = 4096;
 
 template <bool OUT16>
@@ -1243,6 +1283,20 @@ int cin_gemm_fp8_bs(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam
   }
   if (K % big::TK == 0 && M >= big::TM && N >= big::TN && N % 128 == 0 && big_offsets_fit(lda, ldb, K, ssam, ssak)) {
     const uint32_t tm = (uint32_t)cdiv(M, big::TM), tn = (uint32_t)cdiv(N, big::TN);
+    const uint32_t ncu = (uint32_t)device_cus();
+    if (tm * tn > ncu) {
+      // more tiles than CUs: the persistent walk, whose next tile's DMA overlaps this tile's
+      // stores (16-bit C: the fixed-count epilogue).  Every output dtype takes it, so the K
+      // order of a tile, and with it the fp32 sum, does not depend on the dtype.
+      const bool out16 = c_dtype != CIN_DT_F32 && (((uintptr_t)C) & 7) == 0 && ldc % 4 == 0;
+      if (out16)
+        hipLaunchKernelGGL(pers::k_gemm_fp8_bs_pers<true>, ncu, big::kThreads, 0, s, A, lda, sa, ssam,
+                           ssak, B, ldb, sb, ssbn, ssbk, M, N, K, C, c_dtype, ldc, tm, tn);
+      else
+        hipLaunchKernelGGL(pers::k_gemm_fp8_bs_pers<false>, ncu, big::kThreads, 0, s, A, lda, sa, ssam,
+                           ssak, B, ldb, sb, ssbn, ssbk, M, N, K, C, c_dtype, ldc, tm, tn);
+      return cin_check_launch("gemm_fp8_bs");
+    }
     hipLaunchKernelGGL(big::k_gemm_fp8_bs_256, tm * tn, big::kThreads, 0, s, A, lda, sa, ssam,
                        ssak, B, ldb, sb, ssbn, ssbk, M, N, K, C, c_dtype, ldc, tm, tn);
     return cin_check_launch("gemm_fp8_bs");
