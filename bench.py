@@ -47,9 +47,33 @@ def parse():
     return p.parse_args()
 
 
-def time_loop(fn, iters, warmup):
+# Untimed steps run before the warmup steps of the step timing.  After any idle spell (50 ms
+# is enough) the GPU comes back at a lower working clock and needs ~150 config-2 steps
+# (~25 ms) to reach its steady rate: measured in blocks of 10 steps from a cold start,
+# 174, 195, 182, 174, ... 156, 153, 151, 150 us per step.  A training loop runs at that
+# steady rate; a timed region of a few ms right after the setup's idle spell would time the
+# ramp instead.  The timed region is unchanged: exactly `steps` steps.
+SETTLE_MS = 60.0
+
+
+def settle(fn, ms=SETTLE_MS):
+    """Run fn untimed until `ms` of wall time have passed; returns the number of calls."""
     import torch
 
+    n, t0 = 0, time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(10):
+            fn(n)
+            n += 1
+        torch.cuda.synchronize()
+    return n
+
+
+def time_loop(fn, iters, warmup, settle_ms=0.0):
+    import torch
+
+    if settle_ms > 0:
+        settle(fn, settle_ms)
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -65,13 +89,16 @@ def time_loop(fn, iters, warmup):
 _BUSY = []
 
 
-def kernel_loop(fn, iters, warmup):
+def kernel_loop(fn, iters, warmup, settle_ms=30.0):
     """Device time per call of a component.  Copies of a 256 MiB buffer queued first keep
     the GPU busy (at its working clock) while the host enqueues the `iters` calls, so the
     events bracket back-to-back kernels and not the host's launch overhead (which the step
-    timing above does include)."""
+    timing above does include).  Untimed calls for `settle_ms` first bring the clock to its
+    steady rate for this component."""
     import torch
 
+    if settle_ms > 0:
+        settle(fn, settle_ms)
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -798,14 +825,16 @@ def main():
               "moe_layer": moe_layer, "moe_layer_fwd": moe_layer_fwd, "moe_route": moe_route, "moe_gather": moe_gather,
               "moe_combine": moe_combine, "moe_combine_bwd": moe_combine_bwd, "indexer": indexer, "indexer_wgrad": indexer_wgrad,
               "indexer_full": indexer_full}[args.only]
-        loop = time_loop if args.only == "step" else kernel_loop
-        us = loop(fn, args.steps, args.warmup)
+        if args.only == "step":
+            us = time_loop(fn, args.steps, args.warmup, settle_ms=SETTLE_MS)
+        else:
+            us = kernel_loop(fn, args.steps, args.warmup)
         print(json.dumps({"only": args.only, "us_per_call": us}))
         return
 
     # the timed region: exactly `steps` steps, synchronized on both sides
     torch.cuda.synchronize()
-    step_us = time_loop(step, args.steps, args.warmup)
+    step_us = time_loop(step, args.steps, args.warmup, settle_ms=SETTLE_MS)
     gemm_us = kernel_loop(gemm, max(args.steps, 50), 5)
     try:
         smm_us = kernel_loop(scaled_mm, max(args.steps, 50), 5)
@@ -837,6 +866,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": SETTLE_MS,
         "ms_per_step": round(step_us / 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
