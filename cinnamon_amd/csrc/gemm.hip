@@ -726,15 +726,16 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_wgrad_fp8_256(
 }  // namespace big
 
 // ---------------------------------------------------------------------------
-// Persistent grouped GEMM: one workgroup per CU walks the tiles v, v + G, v + 2G, ...
-// (G = workgroups), so a CU never waits for a workgroup to exit and the next one to start,
-// and the next tile's first two K blocks go out by DMA while the current tile's C stores
-// drain.  The K loop is big::tile_body's.  A tile's expert comes from a prefix table of
-// the experts' tile counts, built once per workgroup in LDS and searched by bisection
-// (no per-tile scan over the experts).  Measured on config 3 against the one-tile-per-
-// workgroup kernel (same box, interleaved): gate/up 4372 -> 4124 us, down 2593 -> 2494 us.
-// The dense kernel stays one tile per workgroup: on config 2 (one tile per CU) and the
-// config-4 dgrad (3.5 tiles per CU) the persistent form measured the same or 2% slower.
+// Persistent GEMM (grouped, and dense above one round of tiles): one workgroup per CU
+// walks the tiles v, v + G, v + 2G, ... (G = workgroups), so a CU never waits for a
+// workgroup to exit and the next one to start, and the next tile's first two K blocks go
+// out by DMA while the current tile's C stores drain.  The K loop is big::tile_body's.  A
+// grouped tile's expert comes from a prefix table of the experts' tile counts, built once
+// per workgroup in LDS and searched by bisection (no per-tile scan over the experts).
+// Measured on config 3 against the one-tile-per-workgroup kernel (same box, interleaved):
+// gate/up 4372 -> 4124 us, down 2593 -> 2494 us.  Dense GEMMs of one round or less (config
+// 2: one tile per CU) keep big::k_gemm_fp8_bs_256; above that (the config-4 dgrad, 3.5
+// tiles per CU) the walk with the counted epilogue measured 2% faster.
 // ---------------------------------------------------------------------------
 namespace pers {
 
