@@ -326,6 +326,7 @@ struct Tile {
   const float* sb;
   void* C;  // element (0, 0) of the tile
   int row_lo, row_hi, col_lo;
+  int nk = 0;  // K blocks of this tile, where they vary per tile (grouped wgrad)
 };
 
 __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ssam, int64_t ssak,
@@ -926,7 +927,8 @@ __device__ __forceinline__ P* uniform_ptr(P* p) {
 
 // OUT16: 16-bit C, 8-byte aligned, ldc a multiple of 4 (the counted epilogue); otherwise
 // every tile stores with store_direct and the next tile waits for everything.
-template <bool OUT16, class Src>
+// VARK: the K blocks vary per tile (Tile::nk, at least 1); K is then unused.
+template <bool OUT16, class Src, bool VARK = false>
 __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t ssam, int64_t ssak,
                                           int64_t ldb, int64_t ssbn, int64_t ssbk, int64_t K,
                                           int c_dtype, int64_t ldc) {
@@ -943,8 +945,8 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
   const int l16 = lane & 15, kq = lane >> 4;
-  const int nk = (int)(K / TK);
-  const int kl = nk - 1;
+  int nk = (int)(K / TK);
+  int kl = nk - 1;
   const int r0 = tid >> 3;
   const uint32_t q16 = (uint32_t)(((tid & 7) ^ swz_f(r0)) * 16);
   const uint32_t offA = (uint32_t)(r0 * lda) + q16;
@@ -952,10 +954,19 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
   const uint32_t stepa = (uint32_t)(64 * lda), stepb = (uint32_t)(64 * ldb);
   const uint32_t offS = (uint32_t)(sa_row((wave & 3) * 64 + lane) * ssam * 4);
   const uint32_t stepsa = (uint32_t)(ssak * 4);
-  const int64_t bytesA = 255 * lda + K, bytesB = 255 * ldb + K;
-  const int64_t bytesS = (255 * ssam + (int64_t)kl * ssak + 1) * 4;
-  const int kb0 = nk >= 16 ? (int)(((blockIdx.x & 7u) * (uint32_t)nk) >> 3) : 0;
+  int64_t bytesA = 255 * lda + K, bytesB = 255 * ldb + K;
+  int64_t bytesS = (255 * ssam + (int64_t)kl * ssak + 1) * 4;
+  int kb0 = nk >= 16 ? (int)(((blockIdx.x & 7u) * (uint32_t)nk) >> 3) : 0;
   auto kphys = [&](int kb) { const int p = kb + kb0; return p < nk ? p : p - nk; };
+  // the K geometry of a tile with n blocks (VARK: set before the tile's first DMA)
+  auto set_k = [&](int n) {
+    nk = n;
+    kl = n - 1;
+    bytesA = 255 * lda + (int64_t)n * TK;
+    bytesB = 255 * ldb + (int64_t)n * TK;
+    bytesS = (255 * ssam + (int64_t)kl * ssak + 1) * 4;
+    kb0 = n >= 16 ? (int)(((blockIdx.x & 7u) * (uint32_t)n) >> 3) : 0;
+  };
   const uint32_t lds_a = (uint32_t)(uintptr_t)&sm.a[0][0] + (uint32_t)(wave * 64 * 16);
   const uint32_t lds_b = (uint32_t)(uintptr_t)&sm.b[0][0] + (uint32_t)(wave * 64 * 16);
   const uint32_t lds_s = (uint32_t)(uintptr_t)&sm.sa[0][0] + (uint32_t)((wave & 3) * 64 * 4);
@@ -1008,6 +1019,7 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
   {
     Tile T0;
     src.get(v, T0);
+    if constexpr (VARK) set_k(T0.nk);
     const uint8_t* pA = uniform_ptr(T0.A);
     const uint8_t* pB = uniform_ptr(T0.B);
     const float* pS = uniform_ptr(T0.sa);
@@ -1022,6 +1034,11 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
     const uint8_t* pB;
     const float* pS;
     const cfloat* sbp;  // B-block scales, read as scalar loads (see cfloat)
+    // VARK: this tile and the next are looked up here, before the accumulators are live,
+    // and kept through the K loop (the lookup's divisions at the loop's end pushed the
+    // accumulators' neighbours into scratch)
+    Tile Tcur, Tnxt;
+    bool has_next = false;
     {
       Tile T;
       src.get(v, T);
@@ -1029,6 +1046,10 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
       pB = uniform_ptr(T.B);
       pS = uniform_ptr(T.sa);
       sbp = (const cfloat*)uniform_ptr(T.sb + (int64_t)(wn >> 1) * ssbn);
+      if constexpr (VARK) {
+        Tcur = T;
+        has_next = src.get(v + G, Tnxt);
+      }
     }
     // block 0 has landed: block 1 (and, with OUT16, the previous tile's stores) may still
     // be in flight; they are waited for at the first K block's barrier
@@ -1099,9 +1120,16 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
     }
     __syncthreads();  // every wave is past its last fragment read: both stages are free
     Tile Tn;
-    const bool next = src.get(v + G, Tn);  // uniform per workgroup
+    bool next;  // uniform per workgroup
+    if constexpr (VARK) {
+      next = has_next;
+      Tn = Tnxt;
+    } else {
+      next = src.get(v + G, Tn);
+    }
     if (next) {
       // the next tile's blocks 0 and 1 go out first, then this tile's stores
+      if constexpr (VARK) set_k(Tn.nk);  // this tile's K loop is done
       const uint8_t* nA = uniform_ptr(Tn.A);
       const uint8_t* nB = uniform_ptr(Tn.B);
       const float* nS = uniform_ptr(Tn.sa);
@@ -1109,7 +1137,10 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
       if (nk > 1) CIN_DMA_P(nA, nB, nS, 1, 1);
     }
     Tile T;
-    src.get(v, T);
+    if constexpr (VARK)
+      T = Tcur;
+    else
+      src.get(v, T);
     if (!next && c_dtype != CIN_DT_F32 && ((((uintptr_t)T.C) & 15) == 0) && (ldc & 7) == 0) {
       // last tile of this workgroup: the LDS-staged epilogue of big::tile_body
 #pragma unroll
@@ -1215,6 +1246,128 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_gemm_fp8_pers(
   src.ldc = ldc; src.Tn = Tn; src.N = N; src.es = c_dtype == CIN_DT_F32 ? 4 : 2;
   src.tiles_n = tiles_n; src.starts = starts; src.ends = ends; src.E = E; src.tpre = tpre;
   run_tiles<OUT16>(src, lda, ssam, ssak, ldb, ssbn, ssbk, K, c_dtype, ldc);
+}
+
+// Grouped weight gradient on the persistent walk (same operands and result as
+// big::k_grouped_wgrad_fp8_256): dW_e[n, k] = sum over expert e's tokens of dC[t, n] X[t, k],
+// a 256 x 256 tile's reduction running over e's padded token range, so the K blocks vary
+// per tile.  Each workgroup builds, in LDS, every expert's padded offset and K blocks and
+// the experts with tokens in descending order of K blocks (ties by id).  Walk index v ->
+// tile: every other full round of G tiles is taken in reverse, so with the experts sorted
+// the long tiles are dealt out evenly and the static walk stays balanced.
+constexpr int kMaxWgradExperts = 512;
+
+struct WgradSrc {
+  const uint8_t* A; const float* sa; const uint8_t* B; const float* sb; uint8_t* C;
+  int64_t lda, ssam, ldb, ssbm, ldc, sce, M, N;
+  int es;
+  uint32_t tiles_m, tiles_n, G, total;  // total = tiles of the experts with tokens
+  const int* order;    // experts with tokens, most K blocks first
+  const int* enk;      // K blocks per expert (0: no tokens, or a range past the operands)
+  const int64_t* poff; // padded token offset per expert
+  __device__ bool get(uint32_t v, Tile& t) const {
+    if (v >= total) return false;
+    const uint32_t i = v / G, b = v - i * G;
+    const uint32_t u = ((i & 1u) && (i + 1) * G <= total) ? i * G + (G - 1 - b) : v;
+    const uint32_t per = tiles_m * tiles_n;
+    const uint32_t rank = u / per, r = u - rank * per;
+    // LDS reads are per lane to the compiler: made wave-uniform, what follows stays scalar
+    const int e = __builtin_amdgcn_readfirstlane(order[rank]);
+    uint32_t tm, tn;
+    raster(r, tiles_m, tiles_n, tm, tn);  // an XCD's 32 tiles share 4 A and 8 B panels
+    const uint64_t pu = (uint64_t)poff[e];
+    const int64_t p = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(pu >> 32)) << 32) |
+                                (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)pu));
+    const int64_t m_nom = (int64_t)tm * TM, n_nom = (int64_t)tn * TN;
+    const int64_t m0 = m_nom + TM <= M ? m_nom : M - TM;
+    const int64_t n0 = n_nom + TN <= N ? n_nom : N - TN;
+    t.A = A + m0 * lda + p;
+    t.sa = sa + m0 * ssam + p / TK;
+    t.B = B + n0 * ldb + p;
+    t.sb = sb + (p / TK) * ssbm + (n0 >> 7);
+    t.C = C + ((int64_t)e * sce + m0 * ldc + n0) * es;
+    t.row_lo = (int)(m_nom - m0);
+    t.row_hi = TM;
+    t.col_lo = (int)(n_nom - n0);
+    t.nk = __builtin_amdgcn_readfirstlane(enk[e]);
+    return true;
+  }
+};
+
+template <bool OUT16>
+__global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad_fp8_pers(
+    const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
+    const uint8_t* __restrict__ B, int64_t ldb, const float* __restrict__ sb, int64_t ssbm,
+    const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int E, int64_t Tn,
+    int64_t tcap, int64_t M, int64_t N, void* C, int c_dtype, int64_t ldc, int64_t sce,
+    uint32_t tiles_m, uint32_t tiles_n) {
+  __shared__ int order[kMaxWgradExperts];
+  __shared__ int enk[kMaxWgradExperts];
+  __shared__ int64_t poff[kMaxWgradExperts];
+  __shared__ int wtot[kThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // thread t owns expert t (E <= kThreads): K blocks, then the exclusive prefix of the
+  // padded sizes 128 * nk (the padded token axis of the operands)
+  int nkt = 0;
+  if (tid < E) {
+    int64_t s0, s1;
+    clamp_range(starts, ends, tid, Tn, s0, s1);
+    nkt = (int)((s1 - s0 + TK - 1) / TK);
+  }
+  int incl = nkt;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) wtot[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += wtot[w];
+  if (tid < E) {
+    const int64_t p = (int64_t)(base + incl - nkt) * TK;
+    poff[tid] = p;
+    // ranges inconsistent with the operands' columns: the expert's dW is zero, as for an
+    // expert without tokens
+    enk[tid] = p + (int64_t)nkt * TK <= tcap ? nkt : 0;
+  }
+  __syncthreads();
+  int nz = 0;
+  if (tid < E && enk[tid] > 0) {
+    const int mine = enk[tid];
+    int rank = 0;
+    for (int x = 0; x < E; ++x) {
+      const int o = enk[x];
+      rank += (o > mine || (o == mine && x < tid)) ? 1 : 0;
+    }
+    order[rank] = tid;
+  }
+  for (int x = 0; x < E; ++x) nz += enk[x] > 0 ? 1 : 0;
+  __syncthreads();
+  // experts without tokens: every workgroup zeroes its share of their dW.  These stores
+  // come before any operand DMA, so the in-order waits of the walk cover them.
+  if (nz < E) {
+    const int64_t gid = (int64_t)blockIdx.x * kThreads + tid, gstride = (int64_t)gridDim.x * kThreads;
+    for (int e = 0; e < E; ++e) {
+      if (enk[e] != 0) continue;  // uniform
+      for (int64_t idx = gid; idx < M * N; idx += gstride) {
+        const int64_t rr = idx / N, cc = idx - rr * N;
+        const int64_t off = (int64_t)e * sce + rr * ldc + cc;
+        if (c_dtype == CIN_DT_F32)
+          static_cast<float*>(C)[off] = 0.0f;
+        else
+          static_cast<uint16_t*>(C)[off] = 0;
+      }
+    }
+  }
+  WgradSrc src;
+  src.A = A; src.sa = sa; src.B = B; src.sb = sb; src.C = static_cast<uint8_t*>(C);
+  src.lda = lda; src.ssam = ssam; src.ldb = ldb; src.ssbm = ssbm; src.ldc = ldc; src.sce = sce;
+  src.M = M; src.N = N; src.es = c_dtype == CIN_DT_F32 ? 4 : 2;
+  src.tiles_m = tiles_m; src.tiles_n = tiles_n; src.G = gridDim.x;
+  src.total = (uint32_t)nz * tiles_m * tiles_n;
+  src.order = order; src.enk = enk; src.poff = poff;
+  run_tiles<OUT16, WgradSrc, true>(src, lda, ssam, 1, ldb, 1, ssbm, 0, c_dtype, ldc);
 }
 
 }  // namespace pers
@@ -1384,6 +1537,21 @@ int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, i
   const int64_t tm = cdiv(N, big::TM), tn = cdiv(K, big::TN);
   CIN_CHECK_ARG(E * tm * tn < ((int64_t)1 << 31), "grouped_wgrad_fp8: grid too large");
   const uint32_t ntot = (uint32_t)(E * tm * tn);
+  if (E <= pers::kMaxWgradExperts) {
+    // one workgroup per CU on the persistent walk; the 16-bit counted epilogue needs every
+    // expert's dW 8-byte aligned with rows a multiple of 4 elements apart
+    const unsigned ncu = (unsigned)device_cus();
+    const bool out16 = c_dtype != CIN_DT_F32 && (((uintptr_t)C) & 7) == 0 && ldc % 4 == 0 && sce % 4 == 0;
+    if (out16)
+      hipLaunchKernelGGL(pers::k_grouped_wgrad_fp8_pers<true>, ncu, big::kThreads, 0,
+                         static_cast<hipStream_t>(stream), A, lda, sa, ssam, B, ldb, sb, ssbm, starts,
+                         ends, (int)E, T, tcap, N, K, C, c_dtype, ldc, sce, (uint32_t)tm, (uint32_t)tn);
+    else
+      hipLaunchKernelGGL(pers::k_grouped_wgrad_fp8_pers<false>, ncu, big::kThreads, 0,
+                         static_cast<hipStream_t>(stream), A, lda, sa, ssam, B, ldb, sb, ssbm, starts,
+                         ends, (int)E, T, tcap, N, K, C, c_dtype, ldc, sce, (uint32_t)tm, (uint32_t)tn);
+    return cin_check_launch("grouped_wgrad_fp8");
+  }
   hipLaunchKernelGGL(big::k_grouped_wgrad_fp8_256, ntot, big::kThreads, 0,
                      static_cast<hipStream_t>(stream), A, lda, sa, ssam, B, ldb, sb, ssbm, starts,
                      ends, T, tcap, N, K, C, c_dtype, ldc, sce, (uint32_t)tm, (uint32_t)tn, ntot);
