@@ -321,3 +321,30 @@ def test_grouped_backward_256_experts(kern, dev):
     want_x = orc.grouped_dgrad_ref(gq, gs, wq.view(torch.uint8).cpu().view(E, N, K),
                                    wsb.cpu().view(E, N // 128, -1), starts, ends)
     _check(dx, want_x, "dgrad E=256")
+
+
+@pytest.mark.parametrize("E", [600, 512])
+def test_grouped_wgrad_both_kernels(kern, dev, E):
+    """The wgrad takes the persistent walk up to 512 experts (its LDS tables) and the
+    one-tile-per-workgroup kernel above: the fp32 result against the oracle, with empty
+    experts zeroed, and the bf16 one (the 16-bit counted epilogue) equal to RNE of it."""
+    from cinnamon_amd import layers
+    T, N, K = 9000, 256, 384
+    counts = _many_expert_counts(E, T, seed=12)
+    assert 0 in counts
+    starts, ends = _ranges(counts)
+    g = torch.Generator().manual_seed(13)
+    dc = (torch.randn(T, N, generator=g) * 1e-3).to(torch.bfloat16)
+    xq, xs = orc.quant_rowwise(torch.randn(T, K, generator=g).to(torch.bfloat16))
+    dual = orc.grouped_dual_ref(dc, starts, ends)
+    want_w = orc.grouped_wgrad_ref(dual, orc.grouped_requant_ref(xq, xs, starts, ends), E, N, K)
+    sd, ed = starts.to(dev), ends.to(dev)
+    _, _, qt, st = layers.quantize_fp8_dual_grouped(dc.to(dev), sd, ed)
+    xbt, xblk = layers.requantize_grouped_t(xq.to(dev), xs.to(dev), sd, ed)
+    dw = layers.fp8_grouped_wgrad(qt, st, xbt, xblk, sd, ed, T, out_dtype=torch.float32)
+    _check(dw, want_w, f"wgrad E={E}")
+    dw16 = layers.fp8_grouped_wgrad(qt, st, xbt, xblk, sd, ed, T, out_dtype=torch.bfloat16)
+    assert torch.equal(dw16, dw.to(torch.bfloat16)), "bf16 wgrad is not RNE(fp32 wgrad)"
+    for e, c in enumerate(counts):
+        if c == 0:
+            assert torch.count_nonzero(dw[e]) == 0 and torch.count_nonzero(dw16[e]) == 0, f"expert {e}"
