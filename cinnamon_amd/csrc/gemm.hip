@@ -762,14 +762,16 @@ constexpr int kThreads = big::kThreads;
 typedef __attribute__((address_space(4))) const float cfloat;
 typedef __attribute__((address_space(4))) const int64_t cint64;
 
-constexpr uint32_t kGroupM = 4;   // m-tiles per raster group: 32 consecutive tiles = 4 m x 8 n
-
-// Tile index v -> (tm, tn): groups of kGroupM m-tiles swept n by n, m fastest, so the 32
-// tiles an XCD runs at once share 4 A row panels and 8 B column panels.
+// Tile index v -> (tm, tn): groups of GM m-tiles swept n by n, m fastest, so the 32 tiles
+// an XCD runs at once share GM A row panels and 32 / GM B column panels.  Measured on
+// config 3 (alternating in one process, two runs): GM = 8 took the grouped gate/up GEMM
+// 4055 -> 3991 us and its dgrad 4486 -> 4370 us against GM = 4 (down the same); the
+// grouped wgrad and the config-4 dgrad keep GM = 4 (8 was 0.6% slower, and the same).
+template <uint32_t GM>
 __device__ inline void raster(uint32_t v, uint32_t tiles_m, uint32_t tiles_n, uint32_t& tm, uint32_t& tn) {
-  const uint32_t gsz = kGroupM * tiles_n;
-  const uint32_t grp = v / gsz, first = grp * kGroupM;
-  const uint32_t gm = tiles_m - first < kGroupM ? tiles_m - first : kGroupM;
+  const uint32_t gsz = GM * tiles_n;
+  const uint32_t grp = v / gsz, first = grp * GM;
+  const uint32_t gm = tiles_m - first < GM ? tiles_m - first : GM;
   const uint32_t w = v - grp * gsz;
   tm = first + w % gm;
   tn = w / gm;
@@ -791,7 +793,7 @@ struct DenseSrc {
   __device__ bool get(uint32_t v, Tile& t) const {
     if (v >= tiles_m * tiles_n) return false;
     uint32_t tm, tn;
-    raster(v, tiles_m, tiles_n, tm, tn);
+    raster<4>(v, tiles_m, tiles_n, tm, tn);
     const int64_t m_nom = (int64_t)tm * TM, n_nom = (int64_t)tn * TN;
     const int64_t m0 = m_nom + TM <= M ? m_nom : M - TM;
     const int64_t n0 = n_nom + TN <= N ? n_nom : N - TN;
@@ -821,7 +823,7 @@ struct GroupedSrc {
     const uint32_t total_m = (uint32_t)tpre[E];
     if (v >= total_m * tiles_n) return false;
     uint32_t gm, tn;
-    raster(v, total_m, tiles_n, gm, tn);
+    raster<8>(v, total_m, tiles_n, gm, tn);
     int lo = 0, hi = E;  // largest e with tpre[e] <= gm (then gm < tpre[e + 1])
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
@@ -1274,7 +1276,7 @@ struct WgradSrc {
     // LDS reads are per lane to the compiler: made wave-uniform, what follows stays scalar
     const int e = __builtin_amdgcn_readfirstlane(order[rank]);
     uint32_t tm, tn;
-    raster(r, tiles_m, tiles_n, tm, tn);  // an XCD's 32 tiles share 4 A and 8 B panels
+    raster<4>(r, tiles_m, tiles_n, tm, tn);  // an XCD's 32 tiles share 4 A and 8 B panels
     const uint64_t pu = (uint64_t)poff[e];
     const int64_t p = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(pu >> 32)) << 32) |
                                 (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)pu));
