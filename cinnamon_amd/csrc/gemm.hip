@@ -578,6 +578,23 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
 
 // XCD-aware order: workgroup b runs on XCD b % 8; give each XCD a contiguous run of
 // tile ids (n fastest) so its CUs share A row panels and B in their L2.
+// Tile index v -> (tm, tn): groups of GM m-tiles swept n by n, m fastest, so the 32 tiles
+// an XCD runs at once share GM A row panels and 32 / GM B column panels.  Measured
+// alternating in one process: GM = 8 took the config-3 grouped gate/up GEMM 4055 -> 3991
+// us and its dgrad 4486 -> 4370 us against GM = 4 (down the same); the grouped wgrad and
+// the config-4 dgrad keep GM = 4 (8 was 0.6% slower, and the same).  In the one-round
+// kernel, GM = 4 took the config-4 wgrad (8 x 28 tiles) 125.5 -> 113.1 us against whole
+// m rows per XCD, where every XCD read all of B; config 2 maps the same either way.
+template <uint32_t GM>
+__device__ inline void raster(uint32_t v, uint32_t tiles_m, uint32_t tiles_n, uint32_t& tm, uint32_t& tn) {
+  const uint32_t gsz = GM * tiles_n;
+  const uint32_t grp = v / gsz, first = grp * GM;
+  const uint32_t gm = tiles_m - first < GM ? tiles_m - first : GM;
+  const uint32_t w = v - grp * gsz;
+  tm = first + w % gm;
+  tn = w / gm;
+}
+
 __device__ inline uint32_t xcd_remap(uint32_t b, uint32_t G) {
   const uint32_t Gfull = G & ~7u;
   return b < Gfull ? (b & 7u) * (Gfull >> 3) + (b >> 3) : b;
@@ -592,7 +609,8 @@ __global__ __launch_bounds__(kThreads, 2) void k_gemm_fp8_bs_256(
     int64_t ssbn, int64_t ssbk, int64_t M, int64_t N, int64_t K, void* C, int c_dtype,
     int64_t ldc, uint32_t tiles_m, uint32_t tiles_n) {
   const uint32_t b = xcd_remap(blockIdx.x, tiles_m * tiles_n);
-  const uint32_t tm = b / tiles_n, tn = b - tm * tiles_n;
+  uint32_t tm, tn;
+  raster<4>(b, tiles_m, tiles_n, tm, tn);
   const int64_t m_nom = (int64_t)tm * TM, n_nom = (int64_t)tn * TN;
   const int64_t m0 = m_nom + TM <= M ? m_nom : M - TM;
   const int64_t n0 = n_nom + TN <= N ? n_nom : N - TN;
@@ -762,20 +780,7 @@ constexpr int kThreads = big::kThreads;
 typedef __attribute__((address_space(4))) const float cfloat;
 typedef __attribute__((address_space(4))) const int64_t cint64;
 
-// Tile index v -> (tm, tn): groups of GM m-tiles swept n by n, m fastest, so the 32 tiles
-// an XCD runs at once share GM A row panels and 32 / GM B column panels.  Measured on
-// config 3 (alternating in one process, two runs): GM = 8 took the grouped gate/up GEMM
-// 4055 -> 3991 us and its dgrad 4486 -> 4370 us against GM = 4 (down the same); the
-// grouped wgrad and the config-4 dgrad keep GM = 4 (8 was 0.6% slower, and the same).
-template <uint32_t GM>
-__device__ inline void raster(uint32_t v, uint32_t tiles_m, uint32_t tiles_n, uint32_t& tm, uint32_t& tn) {
-  const uint32_t gsz = GM * tiles_n;
-  const uint32_t grp = v / gsz, first = grp * GM;
-  const uint32_t gm = tiles_m - first < GM ? tiles_m - first : GM;
-  const uint32_t w = v - grp * gsz;
-  tm = first + w % gm;
-  tn = w / gm;
-}
+using big::raster;
 
 // First tile of workgroup b: workgroup b runs on XCD b % 8, so XCD x's workgroups take the
 // contiguous tile range [x G/8, (x+1) G/8) of each round of G tiles.
