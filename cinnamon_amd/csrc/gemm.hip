@@ -923,6 +923,33 @@ __device__ __forceinline__ void wait_dma_past_stores() {
   __builtin_amdgcn_s_waitcnt(0x8F78);
 }
 
+// fp32 C of one tile with exactly kEpiStores 16-byte stores per wave (a lane holds 4
+// consecutive columns of one row), the same count as store_counted, so the next tile
+// waits with the same vmcnt.  C must be 16-byte aligned with ldc a multiple of 4.
+__device__ float4 g_store_sink32[64];
+__device__ __forceinline__ void store_counted32(const Tile& T, const v4f (&acc)[8][4], int wm, int wn, int l16,
+                                                int kq, int64_t ldc) {
+  const int rl = wm * 128 + l16, cl = wn * 64 + kq * 4;
+  float* c0 = static_cast<float*>(T.C) + (int64_t)rl * ldc + cl;
+  float4* sink = &g_store_sink32[threadIdx.x & 63];
+  const uint32_t rows = (uint32_t)(T.row_hi - T.row_lo);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bool rok = (uint32_t)(rl + 16 * i - T.row_lo) < rows;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool ok = rok && cl + 16 * j >= T.col_lo;
+      float4* p = ok ? reinterpret_cast<float4*>(c0 + (int64_t)(16 * i) * ldc + 16 * j) : sink;
+      *p = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+    }
+  }
+}
+
+// How a persistent kernel stores C: every tile with store_direct (the next tile then waits
+// for everything), or with a fixed count of stores per wave that the next tile's first wait
+// looks past (16-bit C: store_counted; fp32 C: store_counted32).
+constexpr int kEpiDirect = 0, kEpiCounted16 = 1, kEpiCounted32 = 2;
+
 // A pointer as a wave-uniform value (the DMA's buffer descriptor lives in SGPRs).
 template <class P>
 __device__ __forceinline__ P* uniform_ptr(P* p) {
@@ -932,10 +959,10 @@ __device__ __forceinline__ P* uniform_ptr(P* p) {
   return (P*)(uintptr_t)((hi << 32) | lo);
 }
 
-// OUT16: 16-bit C, 8-byte aligned, ldc a multiple of 4 (the counted epilogue); otherwise
-// every tile stores with store_direct and the next tile waits for everything.
+// EPI: kEpiCounted16 needs 16-bit C 8-byte aligned with ldc a multiple of 4,
+// kEpiCounted32 fp32 C 16-byte aligned with ldc a multiple of 4; kEpiDirect takes any C.
 // VARK: the K blocks vary per tile (Tile::nk, at least 1); K is then unused.
-template <bool OUT16, class Src, bool VARK = false>
+template <int EPI, class Src, bool VARK = false>
 __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t ssam, int64_t ssak,
                                           int64_t ldb, int64_t ssbn, int64_t ssbk, int64_t K,
                                           int c_dtype, int64_t ldc) {
@@ -1058,11 +1085,11 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
         has_next = src.get(v + G, Tnxt);
       }
     }
-    // block 0 has landed: block 1 (and, with OUT16, the previous tile's stores) may still
+    // block 0 has landed: block 1 (and, counted, the previous tile's stores) may still
     // be in flight; they are waited for at the first K block's barrier
     if (nk > 1 && first)
       wait_dma_but_block();
-    else if (OUT16 && nk > 1)
+    else if (EPI != kEpiDirect && nk > 1)
       wait_dma_past_stores();
     else
       wait_dma();
@@ -1173,8 +1200,10 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
       }
       return;
     }
-    if constexpr (OUT16)
+    if constexpr (EPI == kEpiCounted16)
       store_counted(T, acc, wm, wn, l16, kq, c_dtype, ldc);
+    else if constexpr (EPI == kEpiCounted32)
+      store_counted32(T, acc, wm, wn, l16, kq, ldc);
     else
       store_direct(T, acc, wm, wn, l16, kq, c_dtype, ldc);
     if (!next) return;
@@ -1189,7 +1218,7 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
 #undef CIN_SA8
 }
 
-template <bool OUT16>
+template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void k_gemm_fp8_bs_pers(
     const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
     int64_t ssak, const uint8_t* __restrict__ B, int64_t ldb, const float* __restrict__ sb,
@@ -1200,12 +1229,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_gemm_fp8_bs_pers(
   src.lda = lda; src.ssam = ssam; src.ldb = ldb; src.ssbn = ssbn; src.ldc = ldc; src.M = M; src.N = N;
   src.es = c_dtype == CIN_DT_F32 ? 4 : 2;
   src.tiles_m = tiles_m; src.tiles_n = tiles_n;
-  run_tiles<OUT16>(src, lda, ssam, ssak, ldb, ssbn, ssbk, K, c_dtype, ldc);
+  run_tiles<EPI>(src, lda, ssam, ssak, ldb, ssbn, ssbk, K, c_dtype, ldc);
 }
 
 constexpr int kMaxExpertsLds = 4096;
 
-template <bool OUT16>
+template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void k_grouped_gemm_fp8_pers(
     const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
     int64_t ssak, const uint8_t* __restrict__ B, int64_t sbe, int64_t ldb,
@@ -1252,7 +1281,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_gemm_fp8_pers(
   src.lda = lda; src.ssam = ssam; src.ldb = ldb; src.sbe = sbe; src.ssbe = ssbe; src.ssbn = ssbn;
   src.ldc = ldc; src.Tn = Tn; src.N = N; src.es = c_dtype == CIN_DT_F32 ? 4 : 2;
   src.tiles_n = tiles_n; src.starts = starts; src.ends = ends; src.E = E; src.tpre = tpre;
-  run_tiles<OUT16>(src, lda, ssam, ssak, ldb, ssbn, ssbk, K, c_dtype, ldc);
+  run_tiles<EPI>(src, lda, ssam, ssak, ldb, ssbn, ssbk, K, c_dtype, ldc);
 }
 
 // Grouped weight gradient on the persistent walk (same operands and result as
@@ -1301,7 +1330,7 @@ struct WgradSrc {
   }
 };
 
-template <bool OUT16>
+template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad_fp8_pers(
     const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
     const uint8_t* __restrict__ B, int64_t ldb, const float* __restrict__ sb, int64_t ssbm,
@@ -1374,7 +1403,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad_fp8_pers(
   src.tiles_m = tiles_m; src.tiles_n = tiles_n; src.G = gridDim.x;
   src.total = (uint32_t)nz * tiles_m * tiles_n;
   src.order = order; src.enk = enk; src.poff = poff;
-  run_tiles<OUT16, WgradSrc, true>(src, lda, ssam, 1, ldb, 1, ssbm, 0, c_dtype, ldc);
+  run_tiles<EPI, WgradSrc, true>(src, lda, ssam, 1, ldb, 1, ssbm, 0, c_dtype, ldc);
 }
 
 }  // namespace pers
@@ -1383,6 +1412,15 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Compute units of the current device (the persistent grid runs one workgroup per CU),
 // looked up once per device.
+// The persistent kernels' epilogue for this C (pers::kEpi*); sce is the wgrad's expert
+// stride in elements (0 elsewhere).
+int pers_epi(int c_dtype, const void* C, int64_t ldc, int64_t sce) {
+  const uintptr_t a = (uintptr_t)C;
+  if (c_dtype == CIN_DT_F32)
+    return (a & 15) == 0 && ldc % 4 == 0 && sce % 4 == 0 ? pers::kEpiCounted32 : pers::kEpiDirect;
+  return (a & 7) == 0 && ldc % 4 == 0 && sce % 4 == 0 ? pers::kEpiCounted16 : pers::kEpiDirect;
+}
+
 int device_cus() {
   static int cached[64] = {};
   int dev = 0;
@@ -1449,13 +1487,17 @@ int cin_gemm_fp8_bs(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam
       // more tiles than CUs: the persistent walk, whose next tile's DMA overlaps this tile's
       // stores (16-bit C: the fixed-count epilogue).  Every output dtype takes it, so the K
       // order of a tile, and with it the fp32 sum, does not depend on the dtype.
-      const bool out16 = c_dtype != CIN_DT_F32 && (((uintptr_t)C) & 7) == 0 && ldc % 4 == 0;
-      if (out16)
-        hipLaunchKernelGGL(pers::k_gemm_fp8_bs_pers<true>, ncu, big::kThreads, 0, s, A, lda, sa, ssam,
-                           ssak, B, ldb, sb, ssbn, ssbk, M, N, K, C, c_dtype, ldc, tm, tn);
+#define CIN_LAUNCH_DENSE_PERS(EPI_)                                                                  \
+  hipLaunchKernelGGL(pers::k_gemm_fp8_bs_pers<EPI_>, ncu, big::kThreads, 0, s, A, lda, sa, ssam, ssak, B, \
+                     ldb, sb, ssbn, ssbk, M, N, K, C, c_dtype, ldc, tm, tn)
+      const int epi = pers_epi(c_dtype, C, ldc, 0);
+      if (epi == pers::kEpiCounted16)
+        CIN_LAUNCH_DENSE_PERS(pers::kEpiCounted16);
+      else if (epi == pers::kEpiCounted32)
+        CIN_LAUNCH_DENSE_PERS(pers::kEpiCounted32);
       else
-        hipLaunchKernelGGL(pers::k_gemm_fp8_bs_pers<false>, ncu, big::kThreads, 0, s, A, lda, sa, ssam,
-                           ssak, B, ldb, sb, ssbn, ssbk, M, N, K, C, c_dtype, ldc, tm, tn);
+        CIN_LAUNCH_DENSE_PERS(pers::kEpiDirect);
+#undef CIN_LAUNCH_DENSE_PERS
       return cin_check_launch("gemm_fp8_bs");
     }
     hipLaunchKernelGGL(big::k_gemm_fp8_bs_256, tm * tn, big::kThreads, 0, s, A, lda, sa, ssam,
@@ -1492,15 +1534,18 @@ int cin_grouped_gemm_fp8(const uint8_t* A, int64_t lda, const float* sa, int64_t
     if (E <= pers::kMaxExpertsLds) {
       const int64_t ncu = device_cus();
       const unsigned grid = (unsigned)(mt * tn < ncu ? mt * tn : ncu);
-      const bool out16 = c_dtype != CIN_DT_F32 && (((uintptr_t)C) & 7) == 0 && ldc % 4 == 0;
-      if (out16)
-        hipLaunchKernelGGL(pers::k_grouped_gemm_fp8_pers<true>, grid, big::kThreads, 0,
-                           static_cast<hipStream_t>(stream), A, lda, sa, ssam, ssak, B, sbe, ldb, sb,
-                           ssbe, ssbn, ssbk, starts, ends, (int)E, T, N, K, C, c_dtype, ldc, tn);
+#define CIN_LAUNCH_GROUPED_PERS(EPI_)                                                                \
+  hipLaunchKernelGGL(pers::k_grouped_gemm_fp8_pers<EPI_>, grid, big::kThreads, 0,                      \
+                     static_cast<hipStream_t>(stream), A, lda, sa, ssam, ssak, B, sbe, ldb, sb, ssbe, ssbn, \
+                     ssbk, starts, ends, (int)E, T, N, K, C, c_dtype, ldc, tn)
+      const int epi = pers_epi(c_dtype, C, ldc, 0);
+      if (epi == pers::kEpiCounted16)
+        CIN_LAUNCH_GROUPED_PERS(pers::kEpiCounted16);
+      else if (epi == pers::kEpiCounted32)
+        CIN_LAUNCH_GROUPED_PERS(pers::kEpiCounted32);
       else
-        hipLaunchKernelGGL(pers::k_grouped_gemm_fp8_pers<false>, grid, big::kThreads, 0,
-                           static_cast<hipStream_t>(stream), A, lda, sa, ssam, ssak, B, sbe, ldb, sb,
-                           ssbe, ssbn, ssbk, starts, ends, (int)E, T, N, K, C, c_dtype, ldc, tn);
+        CIN_LAUNCH_GROUPED_PERS(pers::kEpiDirect);
+#undef CIN_LAUNCH_GROUPED_PERS
       return cin_check_launch("grouped_gemm_fp8");
     }
     hipLaunchKernelGGL(big::k_grouped_gemm_fp8_256, (unsigned)(mt * tn), big::kThreads, 0,
@@ -1545,18 +1590,21 @@ int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, i
   CIN_CHECK_ARG(E * tm * tn < ((int64_t)1 << 31), "grouped_wgrad_fp8: grid too large");
   const uint32_t ntot = (uint32_t)(E * tm * tn);
   if (E <= pers::kMaxWgradExperts) {
-    // one workgroup per CU on the persistent walk; the 16-bit counted epilogue needs every
-    // expert's dW 8-byte aligned with rows a multiple of 4 elements apart
+    // one workgroup per CU on the persistent walk; the counted epilogues need every expert's
+    // dW aligned as the first one (sce a multiple of 4 elements)
     const unsigned ncu = (unsigned)device_cus();
-    const bool out16 = c_dtype != CIN_DT_F32 && (((uintptr_t)C) & 7) == 0 && ldc % 4 == 0 && sce % 4 == 0;
-    if (out16)
-      hipLaunchKernelGGL(pers::k_grouped_wgrad_fp8_pers<true>, ncu, big::kThreads, 0,
-                         static_cast<hipStream_t>(stream), A, lda, sa, ssam, B, ldb, sb, ssbm, starts,
-                         ends, (int)E, T, tcap, N, K, C, c_dtype, ldc, sce, (uint32_t)tm, (uint32_t)tn);
+#define CIN_LAUNCH_WGRAD_PERS(EPI_)                                                                   \
+  hipLaunchKernelGGL(pers::k_grouped_wgrad_fp8_pers<EPI_>, ncu, big::kThreads, 0,                       \
+                     static_cast<hipStream_t>(stream), A, lda, sa, ssam, B, ldb, sb, ssbm, starts, ends, \
+                     (int)E, T, tcap, N, K, C, c_dtype, ldc, sce, (uint32_t)tm, (uint32_t)tn)
+    const int epi = pers_epi(c_dtype, C, ldc, sce);
+    if (epi == pers::kEpiCounted16)
+      CIN_LAUNCH_WGRAD_PERS(pers::kEpiCounted16);
+    else if (epi == pers::kEpiCounted32)
+      CIN_LAUNCH_WGRAD_PERS(pers::kEpiCounted32);
     else
-      hipLaunchKernelGGL(pers::k_grouped_wgrad_fp8_pers<false>, ncu, big::kThreads, 0,
-                         static_cast<hipStream_t>(stream), A, lda, sa, ssam, B, ldb, sb, ssbm, starts,
-                         ends, (int)E, T, tcap, N, K, C, c_dtype, ldc, sce, (uint32_t)tm, (uint32_t)tn);
+      CIN_LAUNCH_WGRAD_PERS(pers::kEpiDirect);
+#undef CIN_LAUNCH_WGRAD_PERS
     return cin_check_launch("grouped_wgrad_fp8");
   }
   hipLaunchKernelGGL(big::k_grouped_wgrad_fp8_256, ntot, big::kThreads, 0,
