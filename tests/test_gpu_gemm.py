@@ -249,3 +249,22 @@ def test_gemm_rows_past_32bit_tile_offsets(kern, dev):
     want = orc.gemm_ref(xq, xs, wq.view(torch.uint8).t().contiguous(), ws.t().contiguous())
     _check(y, want, "gemm with 16 MiB rows")
     del a, b
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("pad", [1, 2, 4])
+def test_persistent_gemm_into_strided_c(kern, dev, out_dtype, pad):
+    """More tiles than CUs (9 x 29): the persistent walk, whose epilogue depends on C's
+    alignment (fixed-count 16-bit or fp32 stores, or direct stores for rows that are not
+    aligned).  A C with row stride N + pad gets the same values as a contiguous C, bit for
+    bit (same kernel, same K order), and the padding columns are left alone."""
+    M, N, K = 2304, 7296, 512
+    g = torch.Generator(device=dev).manual_seed(21)
+    xq, xs = kern.quantize_fp8_rowwise(torch.randn(M, K, device=dev, generator=g).to(torch.bfloat16))
+    wq, ws = kern.quantize_fp8_blockwise((torch.randn(N, K, device=dev, generator=g) * 0.02).to(torch.bfloat16))
+    want = kern.fp8_gemm_bs(xq, xs, wq, ws, out_dtype)
+    big = torch.full((M, N + pad), 7.0, dtype=out_dtype, device=dev)
+    got = kern.fp8_gemm_bs(xq, xs, wq, ws, out_dtype, out=big[:, :N])
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), f"strided C (ldc = N + {pad}) differs from contiguous C"
+    assert bool((big[:, N:] == 7.0).all()), "padding columns were written"
