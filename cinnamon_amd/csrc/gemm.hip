@@ -1292,6 +1292,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_gemm_fp8_pers(
 // tile: every other full round of G tiles is taken in reverse, so with the experts sorted
 // the long tiles are dealt out evenly and the static walk stays balanced.
 constexpr int kMaxWgradExperts = 512;
+static_assert(kMaxWgradExperts <= kThreads, "the wgrad's LDS tables give each thread one expert");
 
 struct WgradSrc {
   const uint8_t* A; const float* sa; const uint8_t* B; const float* sb; uint8_t* C;
