@@ -1069,8 +1069,8 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
     const float* pS;
     const cfloat* sbp;  // B-block scales, read as scalar loads (see cfloat)
     // VARK: this tile and the next are looked up here, before the accumulators are live,
-    // and kept through the K loop (the lookup's divisions at the loop's end pushed the
-    // accumulators' neighbours into scratch)
+    // and kept (in scalar registers) through the K loop rather than looked up again after
+    // it, where the accumulators are live
     Tile Tcur, Tnxt;
     bool has_next = false;
     {
