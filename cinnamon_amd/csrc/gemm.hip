@@ -581,7 +581,8 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
 // Tile index v -> (tm, tn): groups of GM m-tiles swept n by n, m fastest, so the 32 tiles
 // an XCD runs at once share GM A row panels and 32 / GM B column panels.  Measured
 // alternating in one process: GM = 8 took the config-3 grouped gate/up GEMM 4055 -> 3991
-// us and its dgrad 4486 -> 4370 us against GM = 4 (down the same); the grouped wgrad and
+// us and its dgrad 4486 -> 4370 us against GM = 4 (down the same; GM = 16 was 1.5-2%
+// slower than 8 on all three); the grouped wgrad and
 // the config-4 dgrad keep GM = 4 (8 was 0.6% slower, and the same).  In the one-round
 // kernel, GM = 4 took the config-4 wgrad (8 x 28 tiles) 125.5 -> 113.1 us against whole
 // m rows per XCD, where every XCD read all of B; config 2 maps the same either way.
