@@ -699,7 +699,8 @@ def main():
         moe_ops.moe_combine(md["ys16"], md["scores"], md["inv"])
 
     def moe_combine_bwd(i):
-        moe_ops.moe_combine_backward(md["dout"], md["ys16"], md["scores"], md["perm"], md["inv"])
+        moe_ops.moe_combine_backward(md["dout"], md["ys16"], md["scores"], md["perm"], md["inv"],
+                                     dy_dtype=torch.bfloat16)
 
     def moe_dispatch_fused(i):
         perm, inv, *_ = moe_ops.moe_route(md["sel"], moe["E"])

@@ -693,6 +693,9 @@ int cin_moe_route_noalloc(const int64_t* idx, int64_t T, int64_t k, int64_t E, i
                           int32_t* inv, int64_t* counts, int64_t* starts, int64_t* ends,
                           void* stream) {
   CIN_CHECK_ARG(T >= 0 && k >= 1 && E >= 1, "moe_route_noalloc: need T >= 0, k >= 1, E >= 1");
+  // bound E and T*k before forming the scratch size, so its product cannot overflow
+  CIN_CHECK_ARG(E <= kMaxExperts, "moe_route_noalloc: at most %d experts", kMaxExperts);
+  CIN_CHECK_ARG(T <= (((int64_t)1 << 31) - 1) / k, "moe_route_noalloc: T*k must fit in 31 bits");
   const int64_t need = 2 * cdiv(T * k, kChunk) * E;
   CIN_CHECK_ARG(need <= kRouteScratchElems,
                 "moe_route_noalloc: needs %lld int32 of scratch (2 * ceil(T*k / %d) * E), the "
@@ -707,6 +710,7 @@ int cin_moe_route_noalloc(const int64_t* idx, int64_t T, int64_t k, int64_t E, i
 
 int cin_moe_route_workspace(int64_t T, int64_t k, int64_t E) {
   if (T < 0 || k < 1 || E < 1) return 0;
+  if (E > kMaxExperts || T > (((int64_t)1 << 31) - 1) / k) return INT32_MAX;  // the route rejects these
   const int64_t n = 2 * cdiv(T * k, kChunk) * E;
   return n > INT32_MAX ? INT32_MAX : (int)n;
 }

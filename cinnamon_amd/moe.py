@@ -223,14 +223,15 @@ def moe_combine_backward(dout: torch.Tensor, sorted_out: torch.Tensor, top_score
                          perm: torch.Tensor, inv: torch.Tensor, dy_dtype: torch.dtype | None = None):
     """Gradients of moe_combine: (d sorted_out [A, D], d top_scores [T, k] fp32).
 
-    d sorted_out is the fp32 product dout * score rounded (RNE) to dy_dtype.  By default that
-    is fp32 for fp32 sorted outputs and bf16 for 16-bit ones: a loss averaged over many
-    tokens gives row gradients of 1e-6 and below, which fp16 holds only as subnormals (and
-    flushes below 6e-8), while bf16 keeps fp32's range, and the experts' FP8 quantizer that
-    reads it keeps 3 mantissa bits in any case."""
+    d sorted_out is the fp32 product dout * score rounded (RNE) to dy_dtype, by default
+    sorted_out's dtype (the dtype autograd gives the gradient of a tensor).  For fp16 sorted
+    outputs, dy_dtype=torch.bfloat16 keeps tiny gradients: a loss averaged over many tokens
+    gives row gradients of 1e-6 and below, which fp16 holds only as subnormals (and flushes
+    below 6e-8), while bf16 keeps fp32's range at the same traffic; RoutedExpertsFunction
+    asks for it."""
     _require(dout.is_cuda and sorted_out.is_cuda, "Input must be on CUDA")
     if dy_dtype is None:
-        dy_dtype = torch.float32 if sorted_out.dtype == torch.float32 else torch.bfloat16
+        dy_dtype = sorted_out.dtype
     _require(dy_dtype in (torch.float32, torch.bfloat16, torch.float16), "dy_dtype must be fp32, bf16 or fp16")
     return _combine_bwd_op(dout.float(), sorted_out, top_scores, perm.to(torch.int64),
                            inv.to(torch.int32), dy_dtype)
@@ -286,7 +287,8 @@ class RoutedExpertsFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         *saved, ys, top_scores, perm, inv = ctx.saved_tensors
-        dy, ds = moe_combine_backward(dout, ys, top_scores, perm, inv)
+        dy, ds = moe_combine_backward(dout, ys, top_scores, perm, inv,
+                                      dy_dtype=torch.float32 if ys.dtype == torch.float32 else torch.bfloat16)
         dx, dw12, dw3 = RoutedExpertsFunction.experts_backward(tuple(saved), dy, inv, ctx.top_k, ctx.x_dtype)
         return (dx, dw12.to(ctx.w_dtypes[0]), dw3.to(ctx.w_dtypes[1]), ds.to(top_scores.dtype),
                 None, None, None, None, None, None)

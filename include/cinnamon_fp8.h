@@ -351,7 +351,10 @@ int cin_moe_route_workspace(int64_t T, int64_t k, int64_t E);
  * 2 * ceil(T*k / 1024) * E <= 1,048,576 (= cin_moe_route_workspace(T, k, E)), and rejects
  * larger routes with CIN_ERR_ARG.  Same outputs as cin_moe_route.  Calls that overlap on
  * one GPU (two streams or two host threads) share the array and race; the array needs no
- * clearing between calls.
+ * clearing between calls.  The first call on each device looks up the array's device
+ * address (hipGetSymbolAddress, no stream work): a caller that captures the route in a HIP
+ * graph makes one call outside the capture first (tests/test_zz_no_alloc.py replays such a
+ * graph).
  * No counterpart in the reference: it is for callers that cannot allocate (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  */

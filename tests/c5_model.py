@@ -169,12 +169,22 @@ class MoE(nn.Module):
         self.router = nn.Linear(c.d_model, c.n_routed, bias=False)
         self.register_buffer("expert_bias", torch.zeros(c.n_routed))
         self.device_dispatch = False  # FP8 mode: route / dispatch / combine with cinnamon_amd.moe
+        # per-layer checks: the top-k choice of a recorded forward (last_top_idx, kept when
+        # record_route is set) can be imposed on a later one (route_override)
+        self.record_route = False
+        self.route_override = None
+        self.last_top_idx = None
 
     def forward(self, x):
         B, L, d = x.shape
         shared = sum(e(x) for e in self.shared_experts)
         scores = torch.sigmoid(self.router(x))
-        _, top_idx = (scores + self.expert_bias).topk(self.top_k, dim=-1)
+        if self.route_override is not None:
+            top_idx = self.route_override
+        else:
+            _, top_idx = (scores + self.expert_bias).topk(self.top_k, dim=-1)
+        if self.record_route:
+            self.last_top_idx = top_idx.detach().clone()
         gates = scores.gather(-1, top_idx)
         gates = gates / (gates.sum(-1, keepdim=True) + 1e-9)
         flat = x.reshape(-1, d)
@@ -289,6 +299,39 @@ def to_fp8(model: C5Model) -> C5Model:
         blk.moe.routed_experts = new
         blk.moe.device_dispatch = True
     return kernels.convert_to_fp8(model)
+
+
+def capture_fp8_layer_io(model: C5Model, ids):
+    """One forward and backward of the loss through `model` (the fp32 mode), recording for
+    every MoE module and every MTP projection its input and the gradient of its output, and
+    each MoE module's top-k expert choice.  Returns ({module name: {"x": input, "dout":
+    output gradient[, "top_idx": experts]}}, {parameter name: grad})."""
+    caps, handles = {}, []
+
+    def hook(name):
+        def f(mod, inp, out):
+            caps[name] = {"x": inp[0].detach().clone()}
+            t = out[0] if isinstance(out, tuple) else out
+            t.register_hook(lambda g: caps[name].__setitem__("dout", g.detach().clone()))
+        return f
+
+    for n, m in model.named_modules():
+        if isinstance(m, MoE) or n.endswith(".proj"):
+            handles.append(m.register_forward_hook(hook(n)))
+        if isinstance(m, MoE):
+            m.record_route = True
+    model.train()
+    model.zero_grad(set_to_none=True)
+    loss, _ = loss_fn(model, ids)
+    loss.backward()
+    for h in handles:
+        h.remove()
+    for n, m in model.named_modules():
+        if isinstance(m, MoE):
+            m.record_route = False
+            caps[n]["top_idx"] = m.last_top_idx
+    grads = {n: p.grad.detach().clone() for n, p in model.named_parameters() if p.grad is not None}
+    return caps, grads
 
 
 def make_optimizer(model: C5Model):

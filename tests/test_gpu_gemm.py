@@ -127,6 +127,53 @@ def test_fp8_linear_fwd_bwd(kern, dev, M, N, K, rs):
         assert mr <= MAX_REL + 2 ** -8 and fr <= FROB_REL + 2 ** -8, f"{name}: {mr:.3e} {fr:.3e}"
 
 
+@pytest.mark.parametrize("which", ["dgrad", "wgrad"])
+def test_config4_backward_gemms_tight(kern, dev, which):
+    """Config 4's two GEMMs at their exact shapes, at the GEMM bar (2e-3 normwise, 1e-3
+    Frobenius, fp32 epilogue), fed the operands the backward itself produces on the GPU:
+    - dgrad dX[8192, 7168] = dY . W (src/kernels.py:774): A = the dual quantizer's dY row
+      tiles, B = the forward quantizer's transposed weight codes Wt[7168, 2048] with the
+      weight's block scales read transposed (the persistent walk, 16 K blocks per tile);
+    - wgrad dW[2048, 7168] = dY^T . X (src/kernels.py:781-788): A = the dual quantizer's
+      dY^T row tiles [2048, 8192], B = the re-quantized X codes, transposed to [7168, 8192]
+      (one round of 256 x 256 tiles, 64 K blocks, XCD-rotated K order).
+    Those operands are checked bit-exact against the oracle's chain first, and the bf16
+    output must equal RNE of the fp32 output."""
+    M, N, K = 8192, 2048, 7168
+    g = torch.Generator().manual_seed(44)
+    x = torch.randn(M, K, generator=g)
+    x[torch.rand(M, K, generator=g) < 0.01] *= 20
+    x = x.to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    dy = (torch.randn(M, N, generator=g) * 1e-3).to(torch.bfloat16)
+    x_fp8, x_s, w_fp8, w_fp8_t, w_s = kern.quantize_fp8_forward(
+        x.to(dev), w.to(dev), False, with_rowmajor=True, with_transposed=True)
+    g_fp8, g_s, g_fp8_t, g_s_t = kern.quantize_fp8_dual(dy.to(dev))
+    u8 = lambda t: t.view(torch.uint8).cpu()  # noqa: E731
+    if which == "dgrad":
+        rq, rs = orc.quant_rowwise(dy)
+        wq, ws = orc.quant_blockwise(w.float())
+        assert torch.equal(u8(g_fp8), rq.view(torch.uint8)) and torch.equal(g_s.cpu(), rs)
+        assert torch.equal(u8(w_fp8_t), wq.view(torch.uint8).t()) and torch.equal(w_s.cpu(), ws)
+        y32 = kern.fp8_gemm_bs(g_fp8, g_s, w_fp8_t, w_s.t(), torch.float32)
+        y16 = kern.fp8_gemm_bs(g_fp8, g_s, w_fp8_t, w_s.t(), torch.bfloat16)
+        want = orc.gemm_ref(rq, rs, wq, ws)                            # [M, K]
+    else:
+        xb_t, xb_s = kern.requantize_rowwise_to_blockwise(x_fp8, x_s, transposed=True)
+        rq, rs = orc.quant_rowwise(dy.t().contiguous())
+        xq, xs = orc.quant_rowwise(x)
+        xb, xbs = orc.quant_blockwise(orc.dequant_rowwise(xq, xs, 128))
+        assert torch.equal(u8(g_fp8_t), rq.view(torch.uint8)) and torch.equal(g_s_t.cpu(), rs)
+        assert torch.equal(u8(xb_t), xb.view(torch.uint8).t()) and torch.equal(xb_s.cpu(), xbs)
+        y32 = kern.fp8_gemm_bs(g_fp8_t, g_s_t, xb_t, xb_s.t(), torch.float32)
+        y16 = kern.fp8_gemm_bs(g_fp8_t, g_s_t, xb_t, xb_s.t(), torch.bfloat16)
+        want = orc.gemm_ref(rq, rs, xb, xbs)                            # [N, K]
+    torch.cuda.synchronize()
+    mr, fr = _check(y32, want, f"config-4 {which}")
+    print(f"\nconfig-4 {which} {tuple(y32.shape)}: normwise max rel {mr:.2e}, frob rel {fr:.2e}", flush=True)
+    assert torch.equal(y16.cpu(), y32.cpu().to(torch.bfloat16)), "bf16 output is not RNE(fp32 output)"
+
+
 def test_fp8_linear_backward_operands_bit_exact(kern, dev):
     """The quantized operands the backward GEMMs consume are bit-exact to the reference chain."""
     M, N, K = 1024, 512, 768

@@ -270,15 +270,16 @@ def _many_expert_counts(E, T, seed):
     return torch.bincount(ids, minlength=E).tolist()
 
 
-@pytest.mark.parametrize("E,T", [(256, 20000), (4100, 3000)])
+@pytest.mark.parametrize("E,T", [(256, 20000), (600, 20000), (4096, 30000), (4100, 3000)])
 def test_grouped_forward_many_experts(kern, dev, E, T):
     """256 experts (DeepSeek-V3's count): the persistent kernel's prefix-table lookup, several
-    tiles per workgroup; 4100 experts: beyond the LDS prefix table, the one-tile-per-workgroup
-    kernel."""
+    tiles per workgroup; 600 and 4096 experts: each of the 512 threads that build the prefix
+    table sums the tile counts of 2 and 8 experts; 4100 experts: beyond the LDS prefix table,
+    the one-tile-per-workgroup kernel."""
     from cinnamon_amd import layers
     counts = _many_expert_counts(E, T, seed=E)
     starts, ends = _ranges(counts)
-    K, N = 512, 256
+    K, N = (256 if E >= 4096 else 512), 256  # the weights of 4096 experts: 268M codes
     g = torch.Generator().manual_seed(E + 1)
     x = torch.randn(T, K, generator=g).to(torch.bfloat16)
     w = torch.randn(E, N, K, generator=g) * 0.02
@@ -348,3 +349,32 @@ def test_grouped_wgrad_both_kernels(kern, dev, E):
     for e, c in enumerate(counts):
         if c == 0:
             assert torch.count_nonzero(dw[e]) == 0 and torch.count_nonzero(dw16[e]) == 0, f"expert {e}"
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_grouped_wgrad_direct_epilogue(kern, dev, out_dtype):
+    """An expert stride (sce) that is not a multiple of 4 elements sends the persistent wgrad
+    to its direct-store epilogue: every expert's dW equals the contiguous call's bit for bit
+    (same kernel walk, same K order), and the element between two experts' blocks is left
+    alone."""
+    from cinnamon_amd import _lib, layers
+    E, T, N, K = 8, 3000, 256, 384
+    counts = [700, 0, 128, 1, 555, 64, 900, 652]
+    starts, ends = _ranges(counts)
+    g = torch.Generator().manual_seed(17)
+    dc = (torch.randn(T, N, generator=g) * 1e-3).to(torch.bfloat16)
+    xq, xs = orc.quant_rowwise(torch.randn(T, K, generator=g).to(torch.bfloat16))
+    sd, ed = starts.to(dev), ends.to(dev)
+    _, _, qt, st = layers.quantize_fp8_dual_grouped(dc.to(dev), sd, ed)
+    xbt, xblk = layers.requantize_grouped_t(xq.to(dev), xs.to(dev), sd, ed)
+    want = layers.fp8_grouped_wgrad(qt, st, xbt, xblk, sd, ed, T, out_dtype=out_dtype)
+    sce = N * K + 1
+    buf = torch.full((E * sce,), 5.0, dtype=out_dtype, device=dev)
+    a, b = qt.view(torch.uint8), xbt.view(torch.uint8)
+    _lib.call("cin_grouped_gemm_fp8_wgrad", _lib.ptr(a), a.stride(0), _lib.ptr(st), st.stride(0), _lib.ptr(b),
+              b.stride(0), _lib.ptr(xblk), xblk.stride(0), _lib.ptr(sd), _lib.ptr(ed), E, T, a.shape[1], N, K,
+              _lib.ptr(buf), _lib.dtype_code(buf), K, sce, _lib.stream_of(a))
+    torch.cuda.synchronize()
+    for e in range(E):
+        assert torch.equal(buf[e * sce:e * sce + N * K].view(N, K), want[e]), f"expert {e}"
+        assert float(buf[e * sce + N * K]) == 5.0, f"the element after expert {e}'s block was written"

@@ -174,7 +174,10 @@ def test_combine_backward(dev, ydtype):
     y = torch.randn(T * k, D, generator=g).to(ydtype).float()
     dout = torch.randn(T, D, generator=g)
     perm, inv, *_ = moe.moe_route(top_idx.to(dev), E)
-    dy, ds = moe.moe_combine_backward(dout.to(dev), y.to(ydtype).to(dev), scores.to(dev), perm, inv)
+    dyd, _ = moe.moe_combine_backward(dout.to(dev), y.to(ydtype).to(dev), scores.to(dev), perm, inv)
+    assert dyd.dtype == ydtype  # by default the gradient takes sorted_out's dtype
+    dy, ds = moe.moe_combine_backward(dout.to(dev), y.to(ydtype).to(dev), scores.to(dev), perm, inv,
+                                      dy_dtype=torch.float32 if ydtype == torch.float32 else torch.bfloat16)
     # the row gradient: RNE of the fp32 product, in fp32 for fp32 y and bf16 for 16-bit y
     assert dy.dtype == (torch.float32 if ydtype == torch.float32 else torch.bfloat16)
     # reference autograd of weighted_out = sorted_out * sorted_scores[:, None] + scatter_add_
@@ -186,6 +189,7 @@ def test_combine_backward(dev, ydtype):
     dy16, _ = moe.moe_combine_backward(dout.to(dev), y.to(ydtype).to(dev), scores.to(dev), perm, inv,
                                        dy_dtype=torch.float16)
     assert dy16.dtype == torch.float16 and torch.equal(dy16.cpu(), yr.grad.half())
+    assert torch.equal(dyd.cpu(), yr.grad.to(ydtype))
     exact = torch.zeros(T, k, dtype=torch.float64)
     pos = inv.cpu().long().view(T, k)
     for j in range(k):
@@ -204,7 +208,8 @@ def test_combine_backward_keeps_tiny_gradients(dev):
     y = torch.randn(T * k, D, generator=g).half()
     dout = torch.randn(T, D, generator=g) * 1e-6
     perm, inv, *_ = moe.moe_route(top_idx.to(dev), E)
-    dy, _ = moe.moe_combine_backward(dout.to(dev), y.to(dev), scores.to(dev), perm, inv)
+    dy, _ = moe.moe_combine_backward(dout.to(dev), y.to(dev), scores.to(dev), perm, inv,
+                                     dy_dtype=torch.bfloat16)
     assert dy.dtype == torch.bfloat16
     order, *_ = orc.moe_dispatch_ref(top_idx, E)
     exact = dout[order // k] * scores.reshape(-1)[order][:, None]      # fp32 products

@@ -186,7 +186,7 @@ def test_moe_dispatch_shape_functions_and_trace():
         perm, inv, counts, starts, ends = moe.moe_route(top_idx, E)
         ys, saved = moe.RoutedExpertsFunction.experts(x, w12, w3, perm, inv, starts, ends, k)
         out = moe.moe_combine(ys, scores, inv)
-        dys, dsc = moe.moe_combine_backward(dout, ys, scores, perm, inv)
+        dys, dsc = moe.moe_combine_backward(dout, ys, scores, perm, inv, dy_dtype=BF16)
         dx, dw12, dw3 = moe.RoutedExpertsFunction.experts_backward(saved, dys, inv, k, x.dtype)
         return perm, inv, counts, ys, out, dys, dsc, dx, dw12, dw3
 

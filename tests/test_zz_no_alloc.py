@@ -3,7 +3,8 @@ workspace argument) against cin_moe_route with a caller workspace, through the C
 
 Two calls in a row share the GPU's scratch array; the second one is smaller, so it runs
 over what the first left there.  A route that needs more scratch than the library holds
-is rejected before any GPU work.
+is rejected before any GPU work.  Captured in a HIP graph (after a first call outside the
+capture has looked up the array's address), every replay equals the workspace route.
 """
 import ctypes
 
@@ -68,3 +69,34 @@ def test_noalloc_route_rejects_routes_beyond_its_scratch(dev):
     assert rc == _lib.CIN_ERR_ARG
     assert "scratch" in _lib.last_error()
     assert isinstance(lib.cin_moe_route_noalloc, ctypes._CFuncPtr)
+
+
+def test_noalloc_route_in_a_captured_graph(dev):
+    """Warm the entry point once (its first call on a device looks up the scratch array's
+    address), capture it in a torch.cuda.CUDAGraph, then replay the graph on new routing ids
+    copied into its input buffer, with eager work and synchronizations between the replays:
+    every replay's outputs equal cin_moe_route's on the same ids."""
+    lib = _lib.load()
+    T, k, E = 4096, 8, 64
+    idx = _zipf_ids(T, k, E, seed=1).to(dev)
+    perm = torch.empty(T * k, dtype=torch.int64, device=dev)
+    inv = torch.empty(T * k, dtype=torch.int32, device=dev)
+    counts, starts, ends = (torch.empty(E, dtype=torch.int64, device=dev) for _ in range(3))
+    outs = [_lib.ptr(t) for t in (perm, inv, counts, starts, ends)]
+    assert lib.cin_moe_route_noalloc(_lib.ptr(idx), T, k, E, *outs, _lib.stream_of(idx)) == 0
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.cin_moe_route_noalloc(_lib.ptr(idx), T, k, E, *outs, _lib.stream_of(idx))
+    assert rc == 0, _lib.last_error()
+    for rep in range(4):
+        new = _zipf_ids(T, k, E, seed=50 + rep).to(dev)
+        idx.copy_(new)
+        for t in (perm, inv, counts, starts, ends):
+            t.fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (perm.cpu(), inv.cpu(), counts.cpu(), starts.cpu(), ends.cpu())
+        want = _route(new, E, noalloc=False)
+        for a, b, name in zip(got, want, ("perm", "inv", "counts", "starts", "ends")):
+            assert torch.equal(a, b), f"replay {rep}: {name} differs"
