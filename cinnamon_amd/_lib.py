@@ -34,6 +34,8 @@ SIGNATURES: dict[str, list] = {
     "cin_quant_dual": [_p, _i32, _i64, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _p,
                        _i64, _p],
     "cin_requant_row_to_block": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p],
+    "cin_quant_backward": [_p, _i32, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _p, _i64,
+                           _p, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p],
     "cin_transpose_u8": [_p, _i64, _i64, _i64, _p, _i64, _p],
     "cin_gemm_fp8_bs": [_p, _i64, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p,
                         _i32, _i64, _p],

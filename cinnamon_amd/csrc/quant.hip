@@ -1239,6 +1239,51 @@ __global__ __launch_bounds__(kThreads) void k_requant128_grouped(
                     sm);
 }
 
+// ----------------------------- backward pair in one launch -----------------------------
+// FP8MatmulFunction.backward needs both quantizations of dY (src/kernels.py:771, :781-783)
+// and the 128 x 128 re-quantization of the saved X codes (:784-787).  One launch walks both
+// tile sets: walk index t < nd is dual tile t of dY (row-block major, as k_dual128), the rest
+// are re-quantization tiles of X (column-block major, as k_requant128).  With the dual tiles
+// first, the first round of workgroups holds both kinds, so the memory-bound dual tiles and
+// the VALU-heavy re-quantization tiles share the CUs, and the second launch's ramp is gone.
+// Each tile is loaded, then processed (one register set); the other resident workgroups'
+// loads overlap a tile's arithmetic.  Same tile bodies as the two kernels, so the same bits.
+union BwdSmem {
+  DualSmem d;
+  RequantSmem r;
+};
+
+template <int DT>
+__global__ __launch_bounds__(kThreads, 5) void k_quant_bwd(
+    const void* __restrict__ dy, int64_t M, int64_t N, int64_t sdm, int round_scale, uint8_t* q,
+    int64_t sqm, float* s, int64_t ssm, uint8_t* qt, int64_t sqtm, int dvec_t, float* st, int64_t sstm,
+    const uint8_t* __restrict__ xq, int64_t K, int64_t sxqm, const float* __restrict__ srow,
+    int64_t ssrm, uint8_t* xbt, int64_t sxbtm, int rvec_t, float* sblk, int64_t ssbm, uint32_t nd,
+    uint32_t ntiles) {
+  static_assert(DT != CIN_DT_F32, "the pair launch takes 16-bit dY");
+  __shared__ BwdSmem sm;
+  uint32_t t = blockIdx.x;
+  {
+    const DenseTiles dgeo{M, (uint32_t)(N >> 7), 0};
+    for (; t < nd; t += gridDim.x) {
+      TileGeo g;
+      dgeo(t, g);
+      RawIn<DT> r;
+      load_in<DT, false>(dy, sdm, N, g, r);
+      dual_body<DT, false>(r, g, N, round_scale != 0, q, sqm, s, ssm, qt, sqtm, dvec_t != 0, st, sstm, sm.d);
+    }
+  }
+  __syncthreads();  // the union's other member: every thread is past its dual tiles
+  const DenseTilesCM rgeo{M, (uint32_t)((M + 127) >> 7), 0};
+  for (; t < ntiles; t += gridDim.x) {
+    TileGeo g;
+    rgeo(t - nd, g);
+    RawQ r;
+    load_q<false>(xq, sxqm, K, srow, ssrm, g, r);
+    requant_body<false>(r, g, K, nullptr, 0, xbt, sxbtm, rvec_t != 0, sblk, ssbm, sm.r);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Dequantization: out = fp32(code) * scale[m / bm, n / bn]  (fp32 product),
 // stored as fp32 or as bf16 (round-to-nearest-even).  Thread = 8 columns.
@@ -1867,6 +1912,52 @@ int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm
   if (K % 128 != 0) CIN_REQ(true, 1, nfull);
 #undef CIN_REQ
   return cin_check_launch("requant_row_to_block");
+}
+
+int cin_quant_backward(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t sdm,
+                       int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, uint8_t* qt,
+                       int64_t sqtm, float* st, int64_t sstm, const uint8_t* xq, int64_t K,
+                       int64_t sxqm, const float* xs, int64_t sxsm, uint8_t* xbt, int64_t sxbtm,
+                       float* sblk, int64_t ssbm, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(dy_dtype), "quant_backward: unsupported dtype %d", dy_dtype);
+  CIN_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "quant_backward: negative shape");
+  if (M == 0 || (N == 0 && K == 0)) return CIN_OK;
+  CIN_CHECK_ARG(dy && q && s && qt && st && xq && xs && xbt && sblk, "quant_backward: null pointer");
+  CIN_CHECK_ARG(sqm >= N && sqtm >= M && ssm >= cdiv(N, 128) && sstm >= cdiv(M, 128),
+                "quant_backward: dY output row stride too small");
+  CIN_CHECK_ARG(aligned(xq, 8) && sxqm % 8 == 0 && sxqm >= K && sxsm >= cdiv(K, 128) &&
+                    sxbtm >= M && ssbm >= cdiv(K, 128),
+                "quant_backward: bad X codes, scales or outputs");
+  const int es = elem_size(dy_dtype);
+  // one launch: 16-bit dY and both widths whole 128-column blocks, with the layouts the two
+  // kernels' fast paths take
+  const bool pair = (dy_dtype == CIN_DT_BF16 || dy_dtype == CIN_DT_F16) && N > 0 && K > 0 &&
+                    N % 128 == 0 && K % 128 == 0 && aligned(dy, 16) && (sdm * es) % 16 == 0 &&
+                    sdm >= N && aligned(q, 8) && sqm % 8 == 0 && tile_fits32(sdm * es) &&
+                    tile_fits32(sqm) && tile_fits32(sxqm) && tile_fits32(sxsm * 4) &&
+                    cdiv(M, 128) * (N / 128 + K / 128) < ((int64_t)1 << 31);
+  if (!pair) {
+    int rc = cin_quant_dual(dy, dy_dtype, M, N, sdm, 1, round_scale, q, sqm, s, ssm, qt, sqtm, st,
+                            sstm, stream);
+    if (rc != CIN_OK) return rc;
+    return cin_requant_row_to_block(xq, M, K, sxqm, xs, sxsm, nullptr, 0, xbt, sxbtm, sblk, ssbm,
+                                    stream);
+  }
+  const int dvec_t = aligned(qt, 16) && sqtm % 16 == 0 && tile_fits32(sqtm);
+  const int rvec_t = aligned(xbt, 16) && sxbtm % 16 == 0 && tile_fits32(sxbtm);
+  const uint32_t nrb = (uint32_t)cdiv(M, 128);
+  const uint32_t nd = nrb * (uint32_t)(N / 128), nt = nd + nrb * (uint32_t)(K / 128);
+  hipStream_t stream_ = static_cast<hipStream_t>(stream);
+#define CIN_QBWD(DT)                                                                               \
+  hipLaunchKernelGGL((k_quant_bwd<DT>), resident_grid<k_quant_bwd<DT>>(nt), kThreads, 0, stream_, dy, \
+                     M, N, sdm, round_scale, q, sqm, s, ssm, qt, sqtm, dvec_t, st, sstm, xq, K, sxqm, xs, \
+                     sxsm, xbt, sxbtm, rvec_t, sblk, ssbm, nd, nt)
+  if (dy_dtype == CIN_DT_BF16)
+    CIN_QBWD(CIN_DT_BF16);
+  else
+    CIN_QBWD(CIN_DT_F16);
+#undef CIN_QBWD
+  return cin_check_launch("quant_backward");
 }
 
 int cin_silu_mul_quant_rowwise(const void* h12, int in_dtype, int64_t M, int64_t H, int64_t s12,

@@ -48,6 +48,7 @@ __all__ = [
     "fp8_gemm_bs",
     "quantize_fp8_forward",
     "quantize_fp8_dual",
+    "quantize_fp8_backward",
     "requantize_rowwise_to_blockwise",
     "FP8MatmulFunction",
     "FP8Linear",
@@ -317,6 +318,60 @@ def _(x_fp8, x_scale, transposed):
             x_fp8.new_empty((_cdiv(M, 128), _cdiv(K, 128)), dtype=torch.float32))
 
 
+def quantize_fp8_backward(grad: torch.Tensor, x_fp8: torch.Tensor, x_scale: torch.Tensor,
+                          round_scale: bool = False):
+    """The three quantizations of FP8MatmulFunction.backward in one launch (reference
+    src/kernels.py:771, :781-783, :784-787): dY [M, N] in 1 x 128 row tiles, dY^T in row
+    tiles, and the saved row-wise X codes [M, K] re-quantized into 128 x 128 blocks, stored
+    transposed.  Bit-identical to quantize_fp8_dual(grad, round_scale) followed by
+    requantize_rowwise_to_blockwise(x_fp8, x_scale, transposed=True).
+
+    Returns (g_fp8 [M, N], g_scale, g_fp8_t [N, M], g_scale_t, x_blk_t [K, M], x_sblk).
+    """
+    _require(grad.is_cuda and x_fp8.is_cuda, "Inputs must be on CUDA")
+    _require(grad.ndim == 2 and x_fp8.ndim == 2, "Inputs must be 2D")
+    M, K = x_fp8.shape
+    _require(grad.shape[0] == M, "grad and x_fp8 must share M")
+    _require(x_fp8.dtype in (torch.float8_e4m3fn, torch.uint8),
+             f"expected float8_e4m3fn codes, got {x_fp8.dtype}")
+    _require(x_scale.shape == (M, _cdiv(K, 128)), "row scales must be [M, ceil(K/128)]")
+    return _quant_bwd_op(grad, x_fp8, x_scale, bool(round_scale))
+
+
+@custom_op("quant_bwd", "(Tensor grad, Tensor x_fp8, Tensor x_scale, bool round_scale) -> "
+           "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
+def _quant_bwd_op(grad, x_fp8, x_scale, round_scale):
+    dy = grad if grad.stride(1) == 1 else grad.contiguous()
+    M, N = dy.shape
+    K = x_fp8.shape[1]
+    dev = dy.device
+    xq = _rows8(_codes_u8(x_fp8))
+    xs = x_scale if x_scale.stride(1) == 1 else x_scale.contiguous()
+    q = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty((M, _cdiv(N, 128)), dtype=torch.float32, device=dev)
+    qt = torch.empty((N, M), dtype=torch.float8_e4m3fn, device=dev)
+    st = torch.empty((N, _cdiv(M, 128)), dtype=torch.float32, device=dev)
+    xbt = torch.empty((K, M), dtype=torch.float8_e4m3fn, device=dev)
+    sblk = torch.empty((_cdiv(M, 128), _cdiv(K, 128)), dtype=torch.float32, device=dev)
+    call("cin_quant_backward", ptr(dy), dtype_code(dy), M, N, dy.stride(0), int(round_scale), ptr(q),
+         q.stride(0), ptr(s), s.stride(0), ptr(qt), qt.stride(0), ptr(st), st.stride(0), ptr(xq), K,
+         xq.stride(0), ptr(xs), xs.stride(0), ptr(xbt), xbt.stride(0), ptr(sblk), sblk.stride(0),
+         stream_of(dy))
+    return q, s, qt, st, xbt, sblk
+
+
+@_quant_bwd_op.register_fake
+def _(grad, x_fp8, x_scale, round_scale):
+    M, N = grad.shape
+    K = x_fp8.shape[1]
+    return (grad.new_empty((M, N), dtype=torch.float8_e4m3fn),
+            grad.new_empty((M, _cdiv(N, 128)), dtype=torch.float32),
+            grad.new_empty((N, M), dtype=torch.float8_e4m3fn),
+            grad.new_empty((N, _cdiv(M, 128)), dtype=torch.float32),
+            grad.new_empty((K, M), dtype=torch.float8_e4m3fn),
+            grad.new_empty((_cdiv(M, 128), _cdiv(K, 128)), dtype=torch.float32))
+
+
 # ---------------------------------------------------------------------------
 # Dequantization (reference src/kernels.py:262-314)
 # ---------------------------------------------------------------------------
@@ -488,9 +543,9 @@ class FP8MatmulFunction(torch.autograd.Function):
 
     Forward quantizes x row-wise and the weight block-wise (emitting the transposed
     weight codes for dgrad) and runs one GEMM.  Backward quantizes dY once into row
-    tiles and dY^T row tiles (cin_quant_dual), re-quantizes the saved x codes into
-    transposed 128x128 blocks (cin_requant_row_to_block) and runs the dgrad and wgrad
-    GEMMs, with the same operands and rounding steps as the reference.
+    tiles and dY^T row tiles and re-quantizes the saved x codes into transposed 128x128
+    blocks, all in one launch (cin_quant_backward), and runs the dgrad and wgrad GEMMs,
+    with the same operands and rounding steps as the reference.
     """
 
     @staticmethod
@@ -520,11 +575,12 @@ class FP8MatmulFunction(torch.autograd.Function):
         x_fp8, x_scale, w_fp8_t, w_scale = ctx.saved_tensors
         x_shape = ctx.x_shape
         grad_flat = grad_output.reshape(-1, grad_output.shape[-1])
-        g_fp8, g_scale, g_fp8_t, g_scale_t = quantize_fp8_dual(grad_flat, ctx.round_scale)
+        # dY row tiles, dY^T row tiles and X^T blocks in one launch
+        g_fp8, g_scale, g_fp8_t, g_scale_t, x_blk_t, x_sblk = quantize_fp8_backward(
+            grad_flat, x_fp8, x_scale, ctx.round_scale)
         # dgrad: dX[M, K] = dY[M, N] . W[N, K]; B^T = W^T [K, N], block scales read as [kb, nb]
         grad_x = fp8_gemm_bs(g_fp8, g_scale, w_fp8_t, w_scale.t(), torch.bfloat16)
         # wgrad: dW[N, K] = dY^T[N, M] . X[M, K]; B^T = X^T block codes [K, M]
-        x_blk_t, x_sblk = requantize_rowwise_to_blockwise(x_fp8, x_scale, transposed=True)
         grad_w = fp8_gemm_bs(g_fp8_t, g_scale_t, x_blk_t, x_sblk.t(), torch.bfloat16)
         return grad_x.reshape(x_shape), grad_w, None, None
 

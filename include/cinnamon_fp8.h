@@ -130,6 +130,24 @@ int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm
                              uint8_t* qbt, int64_t sqbtm, float* sblk, int64_t ssbm, void* stream);
 
 /*
+ * The backward's three quantizations in one launch: cin_quant_dual of dy [M, N] (unit
+ * column stride) and cin_requant_row_to_block of the saved X codes [M, K] into transposed
+ * block codes only (qb = NULL), with the same outputs, bit for bit, as those two calls.
+ * Replaces, in FP8MatmulFunction.backward, quantize_fp8_rowwise(grad_flat) (reference
+ * src/kernels.py:771), quantize_fp8_rowwise(grad_flat.t().contiguous()) (:781-783) and
+ * quantize_fp8_blockwise(dequantize_fp8_rowwise(x_fp8, x_scale)) (:784-787).
+ *   dy, q, s, qt, st           as cin_quant_dual (sdn = 1)
+ *   xq [M, K], xs [M, ceil(K/128)]   the forward's row-wise X codes and scales
+ *   xbt [K, M] block codes of X^T (row stride sxbtm), sblk [ceil(M/128), ceil(K/128)]
+ * One launch for 16-bit dy with N and K multiples of 128; otherwise the two calls in turn.
+ */
+int cin_quant_backward(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t sdm,
+                       int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, uint8_t* qt,
+                       int64_t sqtm, float* st, int64_t sstm, const uint8_t* xq, int64_t K,
+                       int64_t sxqm, const float* xs, int64_t sxsm, uint8_t* xbt, int64_t sxbtm,
+                       float* sblk, int64_t ssbm, void* stream);
+
+/*
  * Byte transpose: dst[c, r] = src[r, c] for an [R, C] matrix of codes.
  * Replaces the code-layout copies w_fp8.t().contiguous() (reference src/kernels.py:748).
  */

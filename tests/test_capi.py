@@ -60,6 +60,14 @@ def test_no_rpath_to_a_second_hip_runtime():
                        1, 2, None)),                                                        # xq stride < K
     ("cin_quant_fwd", (1, 0, 4, 256, 256, 0, 1, 256, 1, 2, 1, 0, 256, 256, None, 256, None, 0,
                        1, 2, None)),                                                        # no weight output
+    # quant_backward: dy, dt, M, N, sdm, rs, q, sqm, s, ssm, qt, sqtm, st, sstm, xq, K, sxqm, xs, sxsm,
+    #                 xbt, sxbtm, sblk, ssbm, stream
+    ("cin_quant_backward", (None, 9, 256, 256, 256, 0, None, 256, None, 2, None, 256, None, 2, None, 256, 256,
+                            None, 2, None, 256, None, 2, None)),                            # bad dtype
+    ("cin_quant_backward", (None, 0, 256, 256, 256, 0, None, 256, None, 2, None, 256, None, 2, None, 256, 256,
+                            None, 2, None, 256, None, 2, None)),                            # null pointers
+    ("cin_quant_backward", (1, 0, 256, 256, 256, 0, 1, 256, 1, 2, 1, 256, 1, 2, 8, 256, 128,
+                            1, 2, 8, 256, 1, 2, None)),                                     # X stride < K
     ("cin_moe_route", (None, 16, 2, 0, None, None, None, None, None, None, 0, None)),        # E = 0
     ("cin_moe_route", (None, 16, 2, 5000, None, None, None, None, None, None, 0, None)),     # E > 4096
     ("cin_moe_route", (None, 16, 2, 8, None, None, None, None, None, None, 0, None)),        # null ptrs
@@ -92,6 +100,8 @@ def test_empty_shapes_are_noops():
     assert lib.cin_indexer_scores_fp8(None, None, None, None, None, 1, 0, 8, 2, 64, 0.1, None, None) == 0
     assert lib.cin_quant_fwd(None, 0, 0, 256, 256, 0, None, 256, None, 2, None, 0, 0, 256, None, 256, None, 0,
                              None, 2, None) == 0
+    assert lib.cin_quant_backward(None, 0, 0, 256, 256, 0, None, 256, None, 2, None, 0, None, 0, None, 256,
+                                  256, None, 2, None, 0, None, 2, None) == 0
 
 
 def test_indexer_weights_grad_workspace_size():

@@ -257,6 +257,34 @@ def test_requant_bit_exact(kern, dev, shape):
     _assert_scales_equal(sbt, want_s, "requant transposed scales")
 
 
+@pytest.mark.parametrize("M,N,K,dtype,rs", [
+    (8192, 2048, 7168, torch.bfloat16, False),   # config 4: one launch
+    (300, 256, 384, torch.float16, True),        # one launch, last row block partial
+    (1024, 512, 768, torch.bfloat16, False),
+    (260, 200, 384, torch.bfloat16, False),      # N % 128 != 0: the two launches
+    (256, 256, 200, torch.bfloat16, False),      # K % 128 != 0: the two launches
+    (384, 256, 256, torch.float32, False),       # fp32 dY: the two launches
+])
+def test_backward_triple_bit_exact(kern, dev, M, N, K, dtype, rs):
+    """quantize_fp8_backward (the backward's three quantizations in one launch) against the
+    oracle chain (src/kernels.py:771, :781-787), with specials in dY's first tile."""
+    dy = _activations(M, N, seed=M + N, dtype=torch.float32, std=1e-3)
+    dy[0, :4] = torch.tensor([float("nan"), float("inf"), -0.0, 0.0])
+    dy = dy.to(dtype)
+    x = _activations(M, K, seed=K)
+    rq, rs_ = orc.quant_rowwise(x)
+    gq, gs = orc.quant_rowwise(dy, 128, rs)
+    gqt, gst = orc.quant_rowwise(dy.t().contiguous(), 128, rs)
+    bq, bs = orc.quant_blockwise(orc.dequant_rowwise(rq, rs_), 128, 128, False)
+    got = kern.quantize_fp8_backward(dy.to(dev), rq.to(dev), rs_.to(dev), rs)
+    torch.cuda.synchronize()
+    for g, w, what in zip(got[0::2], (gq, gqt, bq.view(torch.uint8).t().contiguous()),
+                          ("dY codes", "dY^T codes", "X^T block codes")):
+        _assert_codes_equal(g, w, what)
+    for g, w, what in zip(got[1::2], (gs, gst, bs), ("dY scales", "dY^T scales", "X block scales")):
+        _assert_scales_equal(g, w, what)
+
+
 def test_requant_against_golden(kern, dev):
     d = np.load(GOLDEN)
     q = torch.from_numpy(d["xc_row_q"]).to(dev)

@@ -15,7 +15,8 @@ from torch.fx.experimental.proxy_tensor import make_fx
 
 from cinnamon_amd import kernels, layers, moe
 
-OPS = ["quant_rowwise", "quant_blockwise", "quant_blockwise_t", "quant_fwd", "quant_dual", "requant_row_to_block",
+OPS = ["quant_rowwise", "quant_blockwise", "quant_blockwise_t", "quant_fwd", "quant_dual", "quant_bwd",
+       "requant_row_to_block",
        "dequant_rowwise", "dequant", "gemm_fp8_bs", "transpose_u8", "grouped_gemm_f16",
        "grouped_gemm_fp8", "quant_dual_grouped", "requant_row_to_block_grouped",
        "grouped_wgrad_fp8", "grouped_dgrad_fp8", "silu_mul_quant_rowwise", "swiglu_backward",
@@ -58,6 +59,10 @@ def test_shape_functions_match_the_kernels_outputs():
         assert [t.shape for t in (q, s, qt, st)] == [(300, 1100), (300, 9), (1100, 300), (1100, 3)]
         assert [t.dtype for t in (q, s, qt, st)] == [F8, F32, F8, F32]
         xq, xs = kernels.quantize_fp8_rowwise(x)
+        gy = torch.empty(300, 260, dtype=BF16, device=dev)
+        outs = kernels.quantize_fp8_backward(gy, xq, xs)
+        assert [t.shape for t in outs] == [(300, 260), (300, 3), (260, 300), (260, 3), (1100, 300), (3, 9)]
+        assert [t.dtype for t in outs] == [F8, F32, F8, F32, F8, F32]
         b, bs = kernels.requantize_rowwise_to_blockwise(xq, xs)
         assert _meta(b) == ((300, 1100), F8, "cuda") and bs.shape == (3, 9)
         b, bs = kernels.requantize_rowwise_to_blockwise(xq, xs, transposed=True)
@@ -147,7 +152,7 @@ def test_fp8_linear_forward_backward_traces_to_operators(round_scale):
         assert _meta(y) == ((4, 64, 384), BF16, "cuda")
         assert _meta(dx) == ((4, 64, 512), BF16, "cuda") and _meta(dw) == ((384, 512), BF16, "cuda")
     ops = _op_targets(gm)
-    for name in ["quant_fwd", "gemm_fp8_bs", "quant_dual", "requant_row_to_block"]:
+    for name in ["quant_fwd", "gemm_fp8_bs", "quant_bwd"]:
         assert any(f"cinnamon_amd.{name}" in o for o in ops), (name, ops)
 
 
