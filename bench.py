@@ -35,7 +35,7 @@ def parse():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--only", choices=["step", "gemm", "scaled_mm", "quant_x", "quant_w", "quant_fwd", "moe_gateup", "moe_down",
+    p.add_argument("--only", choices=["step", "gemm", "scaled_mm", "quant_x", "quant_w", "quant_fwd", "moe_gateup", "moe_down", "bwd_pair",
                                       "dual_quant", "requant", "dgrad", "wgrad", "moe_dual", "moe_requant",
                                       "moe_wgrad", "moe_dgrad", "moe_layer", "moe_layer_fwd", "moe_route",
                                       "moe_gather", "moe_combine", "moe_combine_bwd", "indexer", "indexer_wgrad", "indexer_full", "copy", "mfma_ceiling",
@@ -769,7 +769,7 @@ def main():
         logits = torch.relu(logits) * (qsc.view(IB, IL, IH) * w * 0.125).unsqueeze(-1)
         (logits.sum(dim=2) * ksc.view(IB, IL).unsqueeze(1)).backward(ix["g"])
 
-    if full or args.only in ("dual_quant", "requant", "dgrad", "wgrad"):
+    if full or args.only in ("dual_quant", "requant", "dgrad", "wgrad", "bwd_pair"):
         bwd = bwd_setup(dev, xs[0], ws[0])
         gq, gs, gqt, gst = kernels.quantize_fp8_dual(bwd["dy"])
         xbt, xbs = kernels.requantize_rowwise_to_blockwise(bwd["xq"], bwd["xs"], transposed=True)
@@ -781,6 +781,10 @@ def main():
 
     def requant(i):
         kernels.requantize_rowwise_to_blockwise(bwd["xq"], bwd["xs"], transposed=True)
+
+    def bwd_pair(i):
+        # both quantizations above in one launch (FP8MatmulFunction.backward calls this)
+        kernels.quantize_fp8_backward(bwd["dy"], bwd["xq"], bwd["xs"])
 
     def dgrad(i):
         kernels.fp8_gemm_bs(gq, gs, bwd["wqt"], bwd["ws"].t(), torch.bfloat16, out=dx)
@@ -821,6 +825,7 @@ def main():
     if args.only:
         fn = {"step": step, "gemm": gemm, "scaled_mm": scaled_mm, "quant_x": quant_x, "quant_w": quant_w, "quant_fwd": quant_fwd,
               "moe_gateup": moe_gateup, "moe_down": moe_down, "dual_quant": dual_quant,
+              "bwd_pair": bwd_pair,
               "requant": requant, "dgrad": dgrad, "wgrad": wgrad, "moe_dual": moe_dual,
               "moe_requant": moe_requant, "moe_wgrad": moe_wgrad, "moe_dgrad": moe_dgrad,
               "moe_layer": moe_layer, "moe_layer_fwd": moe_layer_fwd, "moe_route": moe_route, "moe_gather": moe_gather,
@@ -1030,6 +1035,7 @@ def main():
     if bwd is not None:
         dq_us = kernel_loop(dual_quant, 20, 3)
         rq_us = kernel_loop(requant, 20, 3)
+        bp_us = kernel_loop(bwd_pair, 20, 3)
         dg_us = kernel_loop(dgrad, 20, 3)
         wg_us = kernel_loop(wgrad, 20, 3)
         dq_bytes = M * N * 2 + 2 * M * N + 4 * (M * (N // 128) + N * (M // 128))
@@ -1039,6 +1045,9 @@ def main():
                               "frac_of_hbm": round(dq_bytes / dq_us / 1e3 / PEAK_HBM_GBPS, 4)},
             "requant_x_block_t": {"us": round(rq_us, 2), "gbps": round(rq_bytes / rq_us / 1e3, 1),
                                   "frac_of_hbm": round(rq_bytes / rq_us / 1e3 / PEAK_HBM_GBPS, 4)},
+            "dual_and_requant_one_launch": {"us": round(bp_us, 2),
+                                            "gbps": round((dq_bytes + rq_bytes) / bp_us / 1e3, 1),
+                                            "frac_of_hbm": round((dq_bytes + rq_bytes) / bp_us / 1e3 / PEAK_HBM_GBPS, 4)},
             "dgrad": {"us": round(dg_us, 1), "tflops": round(flops / dg_us / 1e6, 1),
                       "frac_of_fp8_peak": round(flops / dg_us / 1e6 / PEAK_FP8_TFLOPS, 4)},
             "wgrad": {"us": round(wg_us, 1), "tflops": round(flops / wg_us / 1e6, 1),
