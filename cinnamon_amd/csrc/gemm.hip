@@ -252,18 +252,16 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_gemm_fp8(
 namespace big {
 
 // Workgroup tile 256 x 256 x 128, 8 waves (2 per SIMD), wave tile 128 (m) x 64 (n), two
-// LDS stages.  Per K block a wave issues 32 MFMAs (8 m-tiles x 4 n-tiles) and, before
-// each, the 4 scale-FMAs of the MFMA three steps earlier: the partials live in a ring of
-// 4 slots, so an FMA reads a result whose MFMA finished long ago and no wave ever waits
-// on its own MFMA.  The ring runs across K blocks.
+// LDS stages.  Per K block a wave issues 32 MFMAs (8 m-tiles x 4 n-tiles) and the 4
+// scale-FMAs of each, from a 4-slot partial ring (an FMA reads the MFMA three steps back,
+// long finished, so no wave waits on its own MFMA).  The one-round kernels here run the
+// ping-pong schedule of tile_body; the persistent kernels (namespace pers) interleave each
+// wave's fragment reads with its own MFMAs instead.
 //
-// Operands move global -> LDS by DMA (buffer_load ... lds), one K block ahead: right
-// after the barrier of block kb frees a stage, the DMA of block kb+2 into it starts (its
-// four row groups are issued at steps 28, 30, 2 and 6), and it has most of a block to
-// land.  No VGPR staging and no ds_write.  The barrier sits
-// before the last m-tile group, so the next block's fragments are read while that
-// group's MFMAs run.  The DMA is issued from inline assembly: the compiler treats its
-// own LDS-DMA builtin as aliasing every LDS read and would wait for it before each one.
+// Operands move global -> LDS by DMA (buffer_load ... lds), one K block ahead, with no
+// VGPR staging and no ds_write.  The DMA is issued from inline assembly: the compiler
+// treats its own LDS-DMA builtin as aliasing every LDS read and would wait for it before
+// each one.
 constexpr int TM = 256, TN = 256, TK = 128;
 constexpr int kThreads = 512;
 constexpr int kTileBytes = TM * TK;  // 32 KB per operand per stage
@@ -329,191 +327,12 @@ struct Tile {
   int nk = 0;  // K blocks of this tile, where they vary per tile (grouped wgrad)
 };
 
-__device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ssam, int64_t ssak,
-                                          int64_t ldb, int64_t ssbn, int64_t ssbk, int64_t K,
-                                          int c_dtype, int64_t ldc) {
-  __shared__ SmemAll smu;
-  Smem& sm = smu.s;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+// The finished 256 x 256 tile out of the accumulators: lane (wave, lane) holds rows
+// 128 wm + 16 i + l16 and columns 64 wn + 16 j + 4 kq .. + 3 of m-tile i, n-tile j.
+__device__ __forceinline__ void store_tile(const Tile& T, const v4f (&acc)[8][4], SmemAll& smu, int wave,
+                                           int lane, int c_dtype, int64_t ldc) {
   const int wm = wave >> 2, wn = wave & 3;
   const int l16 = lane & 15, kq = lane >> 4;
-  const int nk = (int)(K / TK);
-  const int kl = nk - 1;
-
-  // DMA round i of an operand covers tile rows i*64 .. i*64+63: thread tid fetches row
-  // i*64 + tid/8, chunk (tid % 8) ^ swz_f(row), which lands at LDS slot i*512 + tid, i.e.
-  // wave w's lanes fill the 1 KB at slot i*512 + 64 w.
-  const int r0 = tid >> 3;
-  const uint32_t q16 = (uint32_t)(((tid & 7) ^ swz_f(r0)) * 16);
-  const uint32_t offA = (uint32_t)(r0 * lda) + q16;
-  const uint32_t offB = (uint32_t)(r0 * ldb) + q16;
-  const uint32_t stepa = (uint32_t)(64 * lda), stepb = (uint32_t)(64 * ldb);
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(T.A, 255 * lda + K);
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(T.B, 255 * ldb + K);
-  // A-row scales: waves 0-3 fill the 256 slots; lane t of wave w loads row sa_row(64 w + t)
-  const __amdgpu_buffer_rsrc_t rsa = make_rsrc(T.sa, (255 * ssam + (int64_t)kl * ssak + 1) * 4);
-  const uint32_t offS = (uint32_t)(sa_row((wave & 3) * 64 + lane) * ssam * 4);
-  const uint32_t stepsa = (uint32_t)(ssak * 4);
-  // the wave's B-block scales (its 64 columns lie in one 128-column block)
-  const float* sbp = T.sb + (int64_t)(wn >> 1) * ssbn;
-  // A long K loop starts at block x·nk/8 on XCD x (workgroup b runs on XCD b % 8) and
-  // wraps.  The XCDs then read different K slices of the operand they all share (B) at any
-  // moment: when B is not yet in the Infinity Cache (weights quantized just before), one
-  // XCD's miss brings a slice in for the others instead of all eight missing on it at once
-  // (config-2 quantize + GEMM step 3.3% faster; the GEMM alone on cached operands 0.9%
-  // slower).  The order of the K blocks in a tile's sum depends only on the workgroup, so
-  // results stay deterministic.  Short loops, whose XCDs never drift apart, keep order 0..nk-1.
-  const int kb0 = nk >= 16 ? (int)(((blockIdx.x & 7u) * (uint32_t)nk) >> 3) : 0;
-  auto kphys = [&](int kb) { const int p = kb + kb0; return p < nk ? p : p - nk; };
-  const uint32_t lds_a = (uint32_t)(uintptr_t)&sm.a[0][0] + (uint32_t)(wave * 64 * 16);
-  const uint32_t lds_b = (uint32_t)(uintptr_t)&sm.b[0][0] + (uint32_t)(wave * 64 * 16);
-  const uint32_t lds_s = (uint32_t)(uintptr_t)&sm.sa[0][0] + (uint32_t)((wave & 3) * 64 * 4);
-// Row group g (tile rows 64 g .. 64 g + 63) of both operands for block kb into stage stg;
-// group 0 also brings the block's A-row scales.
-#define CIN_DMA_GROUP(kb, stg, g)                                                             \
-  do {                                                                                        \
-    const uint32_t ko = (uint32_t)kphys(kb) * TK;                                             \
-    const uint32_t so = (uint32_t)(stg) * kTileBytes;                                         \
-    dma16(ra, offA, ko + (g) * stepa, lds_a + so + (g) * kThreads * 16);                      \
-    dma16(rb, offB, ko + (g) * stepb, lds_b + so + (g) * kThreads * 16);                      \
-    if ((g) == 0 && wave < 4)                                                                 \
-      dma4(rsa, offS, (uint32_t)kphys(kb) * stepsa, lds_s + (uint32_t)(stg) * TM * 4);        \
-  } while (0)
-#define CIN_DMA(kb, stg)                                                                      \
-  do {                                                                                        \
-    _Pragma("unroll") for (int g_ = 0; g_ < 4; ++g_) CIN_DMA_GROUP(kb, stg, g_);              \
-  } while (0)
-
-  // Fragment addresses.  Every fragment row is (16-aligned base) + l16, so its swizzle
-  // f(row) = f(l16) and a fragment is two ds_read_b128 at a per-lane base plus an
-  // (stage, m/n-tile) offset; the high half is chunk 2kq+1, i.e. byte offset ^ 16.
-  const uint8_t* lds = reinterpret_cast<const uint8_t*>(&sm);
-  const int fsw = swz_f(l16);
-  // Per-lane LDS addresses of the fragment reads, hidden from the compiler: it would
-  // otherwise split each into a lane part and a constant and, where the constant passes
-  // the 64 KB immediate-offset range (B's second stage, the scales), keep one register per
-  // (stage, tile) address.  Each read below is one of these bases plus an offset < 64 KB.
-  uint32_t fa = (uint32_t)((wm * 128 + l16) * TK + (((2 * kq) ^ fsw) << 4));
-  uint32_t fb = (uint32_t)(offsetof(Smem, b) + (wn * 64 + l16) * TK + (((2 * kq) ^ fsw) << 4));
-  uint32_t fs = (uint32_t)(offsetof(Smem, sa) + (wm * 128 + l16 * 4) * 4);
-  uint32_t fa_hi = fa ^ 16u, fb_hi = fb ^ 16u;  // the fragments' high halves: chunk 2 kq + 1
-  asm volatile("" : "+v"(fa), "+v"(fb), "+v"(fs), "+v"(fa_hi), "+v"(fb_hi));
-#define CIN_FRAG(base, base_hi, cofs)                                                       \
-  ({                                                                                        \
-    const uint4 lo_ = *reinterpret_cast<const uint4*>(lds + (base) + (cofs));               \
-    const uint4 hi_ = *reinterpret_cast<const uint4*>(lds + (base_hi) + (cofs));            \
-    v8i v_;                                                                                 \
-    v_[0] = (int)lo_.x; v_[1] = (int)lo_.y; v_[2] = (int)lo_.z; v_[3] = (int)lo_.w;         \
-    v_[4] = (int)hi_.x; v_[5] = (int)hi_.y; v_[6] = (int)hi_.z; v_[7] = (int)hi_.w;         \
-    v_;                                                                                     \
-  })
-#define CIN_AFRAG(stg, mt) CIN_FRAG(fa, fa_hi, (uint32_t)((stg) * kTileBytes + (mt) * 16 * TK))
-#define CIN_BFRAG(stg, nt) CIN_FRAG(fb, fb_hi, (uint32_t)((stg) * kTileBytes + (nt) * 16 * TK))
-#define CIN_SA8(stg)                                                                        \
-  do {                                                                                      \
-    const float4 lo_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4)); \
-    const float4 hi_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4 + 256)); \
-    sa8[0] = lo_.x; sa8[1] = lo_.y; sa8[2] = lo_.z; sa8[3] = lo_.w;                         \
-    sa8[4] = hi_.x; sa8[5] = hi_.y; sa8[6] = hi_.z; sa8[7] = hi_.w;                         \
-  } while (0)
-
-  v4f acc[8][4];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  // prologue: blocks 0 and 1 into stages 0 and 1.  The loop starts once block 0 has
-  // landed: block 1's DMA is at least kDmaOpsPerBlock operations issued after block 0's,
-  // vector memory operations retire from vmcnt in issue order, and block 1 is waited for
-  // at the first K block's barrier.
-  CIN_DMA(0, 0);
-  if (nk > 1) {
-    CIN_DMA(1, 1);
-    wait_dma_but_block();
-  } else {
-    wait_dma();
-  }
-  __syncthreads();
-
-  const v4f zero = {0.f, 0.f, 0.f, 0.f};
-  v8i bf[4], af[2];
-  float cs[2], sa8[8];
-  v4f p[4] = {zero, zero, zero, zero};  // partial ring; slot s % 4 holds MFMA(s)
-  float sbv = sbp[(int64_t)kphys(0) * ssbk];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) bf[j] = CIN_BFRAG(0, j);
-  af[0] = CIN_AFRAG(0, 0);
-  CIN_SA8(0);
-  cs[0] = sa8[0] * sbv;
-  cs[1] = 0.0f;  // the "previous block" FMAs of block 0 add 0 * 0
-
-  // Step s8 = 4 i + j of a K block issues the scale-FMAs of MFMA(s8 - 3) (for s8 < 3, of
-  // m-tile 7 of the previous block) and MFMA(s8).
-  for (int kb = 0; kb < nk; ++kb) {
-    const int st = kb & 1;
-    const bool more = kb < kl;
-    const float sbn = sbp[(int64_t)kphys(more ? kb + 1 : kb) * ssbk];
-#pragma unroll
-    for (int s8 = 0; s8 < 32; ++s8) {
-      const int i = s8 >> 2, j = s8 & 3;
-      {
-        const int ti = s8 >= 3 ? (s8 - 3) >> 2 : 7;
-        const int tj = (s8 + 1) & 3;
-        const float c = cs[s8 >= 3 ? ((s8 - 3) >> 2) & 1 : 1];
-        asm volatile("" : "+v"(acc[ti][tj]));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[ti][tj][r] = fmaf(p[(s8 + 1) & 3][r], c, acc[ti][tj][r]);
-        asm volatile("" : "+v"(acc[ti][tj]));
-      }
-      // MFMA(s8), pinned between two operand fences so the FMAs cannot cross it
-      asm volatile("" : "+v"(bf[j]));
-      p[s8 & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af[i & 1], zero, 0, 0, 0, 0, 0, 0);
-      asm volatile("" : "+v"(bf[j]));
-      // row groups 2 and 3 of block kb+1 (groups 0 and 1 went out after the previous
-      // barrier), 4 steps apart: a burst of DMA issues stalls the MFMA issue, and
-      // issuing them early leaves them 22 steps to land before the next barrier
-      if ((s8 == 2 || s8 == 6) && kb >= 1 && kb + 1 < nk)
-        CIN_DMA_GROUP(kb + 1, st ^ 1, s8 == 2 ? 2 : 3);
-      // fragment of m-tile i+1 (its slot's previous user, m-tile i-1, is done)
-      if (j == 0 && i < 7) af[(i + 1) & 1] = CIN_AFRAG(st, i + 1);
-      // scale of m-tile i+1 (its slot's previous user, the FMAs of m-tile i-1, are done)
-      if (j == 3 && i < 7) cs[(i + 1) & 1] = sa8[i + 1] * sbv;
-      if (more) {
-        if (s8 == 28) {
-          // block kb+1's DMA (issued since the previous barrier) has landed in stage st^1,
-          // and stage st is no longer read (its last fragment, m-tile 7, was read at step
-          // 24): after the barrier, block kb+2 starts into stage st (row group 0 now,
-          // group 1 at step 30, groups 2 and 3 early in the next block) and the next
-          // block's fragments are read
-          wait_dma();
-          __syncthreads();
-          if (kb + 2 < nk) CIN_DMA_GROUP(kb + 2, st, 0);
-          af[0] = CIN_AFRAG(st ^ 1, 0);
-          CIN_SA8(st ^ 1);
-        }
-        if (s8 == 30 && kb + 2 < nk) CIN_DMA_GROUP(kb + 2, st, 1);
-        if (s8 >= 28) bf[j] = CIN_BFRAG(st ^ 1, j);
-        if (s8 == 31) cs[0] = sa8[0] * sbn;
-      }
-    }
-    sbv = sbn;
-  }
-  // drain: FMAs of the last block's MFMAs 29-31 (m-tile 7)
-#pragma unroll
-  for (int s8 = 29; s8 < 32; ++s8) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[7][s8 & 3][r] = fmaf(p[s8 & 3][r], cs[1], acc[7][s8 & 3][r]);
-  }
-#undef CIN_DMA
-#undef CIN_DMA_GROUP
-#undef CIN_FRAG
-#undef CIN_AFRAG
-#undef CIN_BFRAG
-#undef CIN_SA8
-
   // bf16 epilogue through LDS: the fragments go to a row-major tile, then every wave
   // stores 32 whole rows, 512 contiguous bytes per row (the direct stores below write
   // each row in 32-byte pieces).  All tiles finish together, so the 32 MB or so of C
@@ -574,6 +393,227 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
       }
     }
   }
+}
+
+// s_waitcnt lgkmcnt(0) (vmcnt and expcnt left at their maxima), then a workgroup barrier
+// that the compiler may not move LDS accesses across.  No vmcnt wait: operand DMA stays in
+// flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// One full tile, scheduled as a ping-pong between the two waves of each SIMD.  Waves 0-3
+// (rows 0-127, one per SIMD) and waves 4-7 (rows 128-255) run half a K block apart: while
+// one wave of a SIMD issues the 16 MFMAs of half a K block (m-tiles 4h .. 4h+3 against its
+// 4 n-tiles) from fragments already in its registers, at raised issue priority, the other
+// reads its next half's fragments from LDS and issues operand DMA.  A K block is four slots:
+//   A: waves 0-3 compute (kb, 0); waves 4-7 read (kb, 0) and DMA B of block kb+1
+//   B: waves 4-7 compute (kb, 0); waves 0-3 read (kb, 1)
+//   C: waves 0-3 compute (kb, 1); waves 4-7 read (kb, 1); then block kb+1 has landed
+//   D: waves 4-7 compute (kb, 1); waves 0-3 read (kb+1, 0) and DMA A of block kb+2
+// One barrier per K block, after C: block kb's stage is no longer read and block kb+1's DMA
+// is complete.  (A barrier after every slot, to hold the alternation exactly, measured
+// slower.)  Before MFMA s of a half, the wave issues the 4 scale-FMAs of MFMA s - 3 from a
+// 4-slot partial ring that runs across halves and K blocks, so an FMA reads a result whose
+// MFMA finished long ago.
+__device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ssam, int64_t ssak,
+                                          int64_t ldb, int64_t ssbn, int64_t ssbk, int64_t K,
+                                          int c_dtype, int64_t ldc) {
+  __shared__ SmemAll smu;
+  Smem& sm = smu.s;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, w4 = wave & 3;
+  const int wm = grp, wn = w4;
+  const int l16 = lane & 15, kq = lane >> 4;
+  const int nk = (int)(K / TK);
+
+  // prologue DMA (blocks 0 and 1, all eight waves): as in tile_body
+  const int r0 = tid >> 3;
+  const uint32_t q16 = (uint32_t)(((tid & 7) ^ swz_f(r0)) * 16);
+  const uint32_t offA = (uint32_t)(r0 * lda) + q16;
+  const uint32_t offB = (uint32_t)(r0 * ldb) + q16;
+  const uint32_t stepa = (uint32_t)(64 * lda), stepb = (uint32_t)(64 * ldb);
+  // loop DMA, one group of four waves per operand: operation i of wave w4 covers tile rows
+  // 32 i + 8 w4 .. + 7 (lane t: row 32 i + 8 w4 + t / 8, chunk (t % 8) ^ f(row)), landing
+  // at LDS slot 256 i + 64 w4 + t -- the layout the eight-wave DMA writes
+  const int r4 = 8 * w4 + (lane >> 3);
+  const uint32_t q4 = (uint32_t)(((lane & 7) ^ swz_f(r4)) * 16);
+  const uint32_t offA4 = (uint32_t)(r4 * lda) + q4, offB4 = (uint32_t)(r4 * ldb) + q4;
+  const uint32_t stepa4 = (uint32_t)(32 * lda), stepb4 = (uint32_t)(32 * ldb);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(T.A, 255 * lda + K);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(T.B, 255 * ldb + K);
+  const int kl = nk - 1;
+  const __amdgpu_buffer_rsrc_t rsa = make_rsrc(T.sa, (255 * ssam + (int64_t)kl * ssak + 1) * 4);
+  const uint32_t offS = (uint32_t)(sa_row(w4 * 64 + lane) * ssam * 4);
+  const uint32_t stepsa = (uint32_t)(ssak * 4);
+  const float* sbp = T.sb + (int64_t)(wn >> 1) * ssbn;
+  const int kb0 = nk >= 16 ? (int)(((blockIdx.x & 7u) * (uint32_t)nk) >> 3) : 0;
+  auto kphys = [&](int kb) { const int p = kb + kb0; return p < nk ? p : p - nk; };
+  const uint32_t lds_a = (uint32_t)(uintptr_t)&sm.a[0][0] + (uint32_t)(wave * 64 * 16);
+  const uint32_t lds_b = (uint32_t)(uintptr_t)&sm.b[0][0] + (uint32_t)(wave * 64 * 16);
+  const uint32_t lds_a4 = (uint32_t)(uintptr_t)&sm.a[0][0] + (uint32_t)(w4 * 64 * 16);
+  const uint32_t lds_b4 = (uint32_t)(uintptr_t)&sm.b[0][0] + (uint32_t)(w4 * 64 * 16);
+  const uint32_t lds_s = (uint32_t)(uintptr_t)&sm.sa[0][0] + (uint32_t)(w4 * 64 * 4);
+#define CIN_DMA_GROUP(kb, stg, g)                                                             \
+  do {                                                                                        \
+    const uint32_t ko = (uint32_t)kphys(kb) * TK;                                             \
+    const uint32_t so = (uint32_t)(stg) * kTileBytes;                                         \
+    dma16(ra, offA, ko + (g) * stepa, lds_a + so + (g) * kThreads * 16);                      \
+    dma16(rb, offB, ko + (g) * stepb, lds_b + so + (g) * kThreads * 16);                      \
+    if ((g) == 0 && wave < 4)                                                                 \
+      dma4(rsa, offS, (uint32_t)kphys(kb) * stepsa, lds_s + (uint32_t)(stg) * TM * 4);        \
+  } while (0)
+#define CIN_DMA(kb, stg)                                                                      \
+  do {                                                                                        \
+    _Pragma("unroll") for (int g_ = 0; g_ < 4; ++g_) CIN_DMA_GROUP(kb, stg, g_);              \
+  } while (0)
+// all of block kb's A rows and A scales into stage stg (waves 0-3), or all its B rows (4-7)
+#define CIN_DMA_A4(kb, stg)                                                                   \
+  do {                                                                                        \
+    const uint32_t ko = (uint32_t)kphys(kb) * TK;                                             \
+    const uint32_t so = (uint32_t)(stg) * kTileBytes;                                         \
+    _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_)                                          \
+      dma16(ra, offA4, ko + i_ * stepa4, lds_a4 + so + i_ * 4096);                            \
+    dma4(rsa, offS, (uint32_t)kphys(kb) * stepsa, lds_s + (uint32_t)(stg) * TM * 4);          \
+  } while (0)
+#define CIN_DMA_B4(kb, stg)                                                                   \
+  do {                                                                                        \
+    const uint32_t ko = (uint32_t)kphys(kb) * TK;                                             \
+    const uint32_t so = (uint32_t)(stg) * kTileBytes;                                         \
+    _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_)                                          \
+      dma16(rb, offB4, ko + i_ * stepb4, lds_b4 + so + i_ * 4096);                            \
+  } while (0)
+
+  const uint8_t* lds = reinterpret_cast<const uint8_t*>(&sm);
+  const int fsw = swz_f(l16);
+  uint32_t fa = (uint32_t)((wm * 128 + l16) * TK + (((2 * kq) ^ fsw) << 4));
+  uint32_t fb = (uint32_t)(offsetof(Smem, b) + (wn * 64 + l16) * TK + (((2 * kq) ^ fsw) << 4));
+  uint32_t fs = (uint32_t)(offsetof(Smem, sa) + (wm * 128 + l16 * 4) * 4);
+  uint32_t fa_hi = fa ^ 16u, fb_hi = fb ^ 16u;
+  asm volatile("" : "+v"(fa), "+v"(fb), "+v"(fs), "+v"(fa_hi), "+v"(fb_hi));
+#define CIN_FRAG(base, base_hi, cofs)                                                       \
+  ({                                                                                        \
+    const uint4 lo_ = *reinterpret_cast<const uint4*>(lds + (base) + (cofs));               \
+    const uint4 hi_ = *reinterpret_cast<const uint4*>(lds + (base_hi) + (cofs));            \
+    v8i v_;                                                                                 \
+    v_[0] = (int)lo_.x; v_[1] = (int)lo_.y; v_[2] = (int)lo_.z; v_[3] = (int)lo_.w;         \
+    v_[4] = (int)hi_.x; v_[5] = (int)hi_.y; v_[6] = (int)hi_.z; v_[7] = (int)hi_.w;         \
+    v_;                                                                                     \
+  })
+#define CIN_AFRAG(stg, mt) CIN_FRAG(fa, fa_hi, (uint32_t)((stg) * kTileBytes + (mt) * 16 * TK))
+#define CIN_BFRAG(stg, nt) CIN_FRAG(fb, fb_hi, (uint32_t)((stg) * kTileBytes + (nt) * 16 * TK))
+
+  v4f acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  v8i af[4], bf[4];
+  float cs[8];
+  float cprev = 0.0f;  // the "previous half" FMAs of the first half add 0 * 0
+  v4f p[4] = {zero, zero, zero, zero};  // partial ring; slot s % 4 holds MFMA(s) of a half
+
+// Read half H of block kb: its four A fragments, and for H = 0 the B fragments and the
+// combined scales sa * sb of the wave's eight m-tiles
+#define CIN_PP_LOAD(kb, H)                                                                    \
+  do {                                                                                        \
+    const int stg_ = (kb) & 1;                                                                \
+    if ((H) == 0) {                                                                           \
+      _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_) bf[j_] = CIN_BFRAG(stg_, j_);          \
+      const float4 lo_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)(stg_ * TM * 4)); \
+      const float4 hi_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)(stg_ * TM * 4 + 256)); \
+      const float sb_ = sbp[(int64_t)kphys(kb) * ssbk];                                       \
+      cs[0] = lo_.x * sb_; cs[1] = lo_.y * sb_; cs[2] = lo_.z * sb_; cs[3] = lo_.w * sb_;     \
+      cs[4] = hi_.x * sb_; cs[5] = hi_.y * sb_; cs[6] = hi_.z * sb_; cs[7] = hi_.w * sb_;     \
+    }                                                                                         \
+    _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_) af[q_] = CIN_AFRAG(stg_, 4 * (H) + q_);  \
+  } while (0)
+// The 16 MFMAs of half H; before MFMA s, the scale-FMAs of MFMA s - 3 (for s < 3, of the
+// previous half's last m-tile, whose combined scale is cprev)
+#define CIN_PP_COMPUTE(H)                                                                     \
+  do {                                                                                        \
+    __builtin_amdgcn_s_setprio(1);                                                            \
+    _Pragma("unroll") for (int s_ = 0; s_ < 16; ++s_) {                                       \
+      {                                                                                       \
+        const int ti = s_ >= 3 ? 4 * (H) + ((s_ - 3) >> 2) : ((H) ? 3 : 7);                   \
+        const int tj = (s_ + 1) & 3;                                                          \
+        const float c = s_ >= 3 ? cs[4 * (H) + ((s_ - 3) >> 2)] : cprev;                      \
+        asm volatile("" : "+v"(acc[ti][tj]));                                                 \
+        _Pragma("unroll") for (int r = 0; r < 4; ++r)                                         \
+          acc[ti][tj][r] = fmaf(p[(s_ + 1) & 3][r], c, acc[ti][tj][r]);                       \
+        asm volatile("" : "+v"(acc[ti][tj]));                                                 \
+      }                                                                                       \
+      asm volatile("" : "+v"(bf[s_ & 3]));                                                    \
+      p[s_ & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[s_ & 3], af[s_ >> 2], zero, 0, 0, 0, 0, 0, 0); \
+      asm volatile("" : "+v"(bf[s_ & 3]));                                                    \
+    }                                                                                         \
+    cprev = cs[4 * (H) + 3];                                                                  \
+    __builtin_amdgcn_s_setprio(0);                                                            \
+  } while (0)
+
+  // prologue: blocks 0 and 1 into stages 0 and 1; block 0 visible to all, then waves 0-3
+  // read their first half
+  CIN_DMA(0, 0);
+  if (nk > 1) {
+    CIN_DMA(1, 1);
+    wait_dma_but_block();
+  } else {
+    wait_dma();
+  }
+  lds_barrier();
+  // each group runs its own copy of the K loop (the same barriers in the same order), so
+  // the compiler sees one straight sequence of slots per wave
+  if (grp == 0) {
+    CIN_PP_LOAD(0, 0);
+    for (int kb = 0; kb < nk; ++kb) {
+      const int st = kb & 1;
+      const bool more = kb < kl;
+      CIN_PP_COMPUTE(0);  // slot A
+      CIN_PP_LOAD(kb, 1);  // slot B
+      CIN_PP_COMPUTE(1);  // slot C: block kb's stage is read for the last time; kb+1 lands
+      wait_dma();
+      lds_barrier();
+      if (more) {  // slot D
+        if (kb + 2 < nk) CIN_DMA_A4(kb + 2, st);
+        CIN_PP_LOAD(kb + 1, 0);
+      }
+    }
+  } else {
+    for (int kb = 0; kb < nk; ++kb) {
+      const int st = kb & 1;
+      const bool more = kb < kl;
+      if (kb >= 1 && more) CIN_DMA_B4(kb + 1, st ^ 1);  // slot A
+      CIN_PP_LOAD(kb, 0);
+      CIN_PP_COMPUTE(0);  // slot B
+      CIN_PP_LOAD(kb, 1);  // slot C
+      wait_dma();
+      lds_barrier();
+      CIN_PP_COMPUTE(1);  // slot D
+    }
+  }
+  // drain: FMAs of the last half's MFMAs 13-15 (m-tile 7)
+#pragma unroll
+  for (int s = 13; s < 16; ++s) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[7][s & 3][r] = fmaf(p[s & 3][r], cprev, acc[7][s & 3][r]);
+  }
+#undef CIN_DMA
+#undef CIN_DMA_GROUP
+#undef CIN_DMA_A4
+#undef CIN_DMA_B4
+#undef CIN_FRAG
+#undef CIN_AFRAG
+#undef CIN_BFRAG
+#undef CIN_PP_LOAD
+#undef CIN_PP_COMPUTE
+
+  store_tile(T, acc, smu, wave, lane, c_dtype, ldc);
 }
 
 // XCD-aware order: workgroup b runs on XCD b % 8; give each XCD a contiguous run of
