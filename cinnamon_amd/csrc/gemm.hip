@@ -405,6 +405,89 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Read half H of block kb: its four A fragments, and for H = 0 the B fragments and the
+// combined scales sa * sb of the wave's eight m-tiles
+#define CIN_PP_LOAD(kb, H)                                                                    \
+  do {                                                                                        \
+    const int stg_ = (kb) & 1;                                                                \
+    if ((H) == 0) {                                                                           \
+      _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_) bf[j_] = CIN_BFRAG(stg_, j_);          \
+      const float4 lo_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)(stg_ * TM * 4)); \
+      const float4 hi_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)(stg_ * TM * 4 + 256)); \
+      const float sb_ = sbp[(int64_t)kphys(kb) * ssbk];                                       \
+      cs[0] = lo_.x * sb_; cs[1] = lo_.y * sb_; cs[2] = lo_.z * sb_; cs[3] = lo_.w * sb_;     \
+      cs[4] = hi_.x * sb_; cs[5] = hi_.y * sb_; cs[6] = hi_.z * sb_; cs[7] = hi_.w * sb_;     \
+    }                                                                                         \
+    _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_) af[q_] = CIN_AFRAG(stg_, 4 * (H) + q_);  \
+  } while (0)
+// The 16 MFMAs of half H; before MFMA s, the scale-FMAs of MFMA s - 3 (for s < 3, of the
+// previous half's last m-tile, whose combined scale is cprev)
+#define CIN_PP_COMPUTE(H)                                                                     \
+  do {                                                                                        \
+    __builtin_amdgcn_s_setprio(1);                                                            \
+    _Pragma("unroll") for (int s_ = 0; s_ < 16; ++s_) {                                       \
+      {                                                                                       \
+        const int ti = s_ >= 3 ? 4 * (H) + ((s_ - 3) >> 2) : ((H) ? 3 : 7);                   \
+        const int tj = (s_ + 1) & 3;                                                          \
+        const float c = s_ >= 3 ? cs[4 * (H) + ((s_ - 3) >> 2)] : cprev;                      \
+        asm volatile("" : "+v"(acc[ti][tj]));                                                 \
+        _Pragma("unroll") for (int r = 0; r < 4; ++r)                                         \
+          acc[ti][tj][r] = fmaf(p[(s_ + 1) & 3][r], c, acc[ti][tj][r]);                       \
+        asm volatile("" : "+v"(acc[ti][tj]));                                                 \
+      }                                                                                       \
+      asm volatile("" : "+v"(bf[s_ & 3]));                                                    \
+      p[s_ & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[s_ & 3], af[s_ >> 2], zero, 0, 0, 0, 0, 0, 0); \
+      asm volatile("" : "+v"(bf[s_ & 3]));                                                    \
+    }                                                                                         \
+    cprev = cs[4 * (H) + 3];                                                                  \
+    __builtin_amdgcn_s_setprio(0);                                                            \
+  } while (0)
+
+// The K loop of the ping-pong schedule and its drain, for a workgroup whose operands of
+// block 0 have landed (blocks 0 and 1 DMA'd by all eight waves, block 0 waited for and a
+// barrier passed).  The enclosing function defines the per-group DMA of the loop:
+// CIN_DMA_A4(kb, stg) (waves 0-3: block kb's A rows and A scales) and CIN_DMA_B4(kb, stg)
+// (waves 4-7: block kb's B rows), and the fragment reads CIN_AFRAG / CIN_BFRAG.
+#define CIN_PP_KLOOP()                                                                              \
+  do {                                                                                              \
+/* each group runs its own copy of the K loop (the same barriers in the same order), so */          \
+/* the compiler sees one straight sequence of slots per wave */                                     \
+  if (grp == 0) {                                                                                   \
+    CIN_PP_LOAD(0, 0);                                                                              \
+    for (int kb = 0; kb < nk; ++kb) {                                                               \
+      const int st = kb & 1;                                                                        \
+      const bool more = kb < kl;                                                                    \
+      CIN_PP_COMPUTE(0);  /* slot A */                                                              \
+      CIN_PP_LOAD(kb, 1);  /* slot B */                                                             \
+      CIN_PP_COMPUTE(1);  /* slot C: block kb's stage is read for the last time; kb+1 lands */      \
+      wait_dma();                                                                                   \
+      lds_barrier();                                                                                \
+      if (more) {  /* slot D */                                                                     \
+        if (kb + 2 < nk) CIN_DMA_A4(kb + 2, st);                                                    \
+        CIN_PP_LOAD(kb + 1, 0);                                                                     \
+      }                                                                                             \
+    }                                                                                               \
+  } else {                                                                                          \
+    for (int kb = 0; kb < nk; ++kb) {                                                               \
+      const int st = kb & 1;                                                                        \
+      const bool more = kb < kl;                                                                    \
+      if (kb >= 1 && more) CIN_DMA_B4(kb + 1, st ^ 1);  /* slot A */                                \
+      CIN_PP_LOAD(kb, 0);                                                                           \
+      CIN_PP_COMPUTE(0);  /* slot B */                                                              \
+      CIN_PP_LOAD(kb, 1);  /* slot C */                                                             \
+      wait_dma();                                                                                   \
+      lds_barrier();                                                                                \
+      CIN_PP_COMPUTE(1);  /* slot D */                                                              \
+    }                                                                                               \
+  }                                                                                                 \
+/* drain: FMAs of the last half's MFMAs 13-15 (m-tile 7) */                                         \
+_Pragma("unroll")                                                                                   \
+  for (int s = 13; s < 16; ++s) {                                                                   \
+_Pragma("unroll")                                                                                   \
+    for (int r = 0; r < 4; ++r) acc[7][s & 3][r] = fmaf(p[s & 3][r], cprev, acc[7][s & 3][r]);      \
+  }                                                                                                 \
+  } while (0)
+
 // One full tile, scheduled as a ping-pong between the two waves of each SIMD.  Waves 0-3
 // (rows 0-127, one per SIMD) and waves 4-7 (rows 128-255) run half a K block apart: while
 // one wave of a SIMD issues the 16 MFMAs of half a K block (m-tiles 4h .. 4h+3 against its
@@ -519,44 +602,6 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
   float cprev = 0.0f;  // the "previous half" FMAs of the first half add 0 * 0
   v4f p[4] = {zero, zero, zero, zero};  // partial ring; slot s % 4 holds MFMA(s) of a half
 
-// Read half H of block kb: its four A fragments, and for H = 0 the B fragments and the
-// combined scales sa * sb of the wave's eight m-tiles
-#define CIN_PP_LOAD(kb, H)                                                                    \
-  do {                                                                                        \
-    const int stg_ = (kb) & 1;                                                                \
-    if ((H) == 0) {                                                                           \
-      _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_) bf[j_] = CIN_BFRAG(stg_, j_);          \
-      const float4 lo_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)(stg_ * TM * 4)); \
-      const float4 hi_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)(stg_ * TM * 4 + 256)); \
-      const float sb_ = sbp[(int64_t)kphys(kb) * ssbk];                                       \
-      cs[0] = lo_.x * sb_; cs[1] = lo_.y * sb_; cs[2] = lo_.z * sb_; cs[3] = lo_.w * sb_;     \
-      cs[4] = hi_.x * sb_; cs[5] = hi_.y * sb_; cs[6] = hi_.z * sb_; cs[7] = hi_.w * sb_;     \
-    }                                                                                         \
-    _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_) af[q_] = CIN_AFRAG(stg_, 4 * (H) + q_);  \
-  } while (0)
-// The 16 MFMAs of half H; before MFMA s, the scale-FMAs of MFMA s - 3 (for s < 3, of the
-// previous half's last m-tile, whose combined scale is cprev)
-#define CIN_PP_COMPUTE(H)                                                                     \
-  do {                                                                                        \
-    __builtin_amdgcn_s_setprio(1);                                                            \
-    _Pragma("unroll") for (int s_ = 0; s_ < 16; ++s_) {                                       \
-      {                                                                                       \
-        const int ti = s_ >= 3 ? 4 * (H) + ((s_ - 3) >> 2) : ((H) ? 3 : 7);                   \
-        const int tj = (s_ + 1) & 3;                                                          \
-        const float c = s_ >= 3 ? cs[4 * (H) + ((s_ - 3) >> 2)] : cprev;                      \
-        asm volatile("" : "+v"(acc[ti][tj]));                                                 \
-        _Pragma("unroll") for (int r = 0; r < 4; ++r)                                         \
-          acc[ti][tj][r] = fmaf(p[(s_ + 1) & 3][r], c, acc[ti][tj][r]);                       \
-        asm volatile("" : "+v"(acc[ti][tj]));                                                 \
-      }                                                                                       \
-      asm volatile("" : "+v"(bf[s_ & 3]));                                                    \
-      p[s_ & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[s_ & 3], af[s_ >> 2], zero, 0, 0, 0, 0, 0, 0); \
-      asm volatile("" : "+v"(bf[s_ & 3]));                                                    \
-    }                                                                                         \
-    cprev = cs[4 * (H) + 3];                                                                  \
-    __builtin_amdgcn_s_setprio(0);                                                            \
-  } while (0)
-
   // prologue: blocks 0 and 1 into stages 0 and 1; block 0 visible to all, then waves 0-3
   // read their first half
   CIN_DMA(0, 0);
@@ -567,42 +612,7 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
     wait_dma();
   }
   lds_barrier();
-  // each group runs its own copy of the K loop (the same barriers in the same order), so
-  // the compiler sees one straight sequence of slots per wave
-  if (grp == 0) {
-    CIN_PP_LOAD(0, 0);
-    for (int kb = 0; kb < nk; ++kb) {
-      const int st = kb & 1;
-      const bool more = kb < kl;
-      CIN_PP_COMPUTE(0);  // slot A
-      CIN_PP_LOAD(kb, 1);  // slot B
-      CIN_PP_COMPUTE(1);  // slot C: block kb's stage is read for the last time; kb+1 lands
-      wait_dma();
-      lds_barrier();
-      if (more) {  // slot D
-        if (kb + 2 < nk) CIN_DMA_A4(kb + 2, st);
-        CIN_PP_LOAD(kb + 1, 0);
-      }
-    }
-  } else {
-    for (int kb = 0; kb < nk; ++kb) {
-      const int st = kb & 1;
-      const bool more = kb < kl;
-      if (kb >= 1 && more) CIN_DMA_B4(kb + 1, st ^ 1);  // slot A
-      CIN_PP_LOAD(kb, 0);
-      CIN_PP_COMPUTE(0);  // slot B
-      CIN_PP_LOAD(kb, 1);  // slot C
-      wait_dma();
-      lds_barrier();
-      CIN_PP_COMPUTE(1);  // slot D
-    }
-  }
-  // drain: FMAs of the last half's MFMAs 13-15 (m-tile 7)
-#pragma unroll
-  for (int s = 13; s < 16; ++s) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[7][s & 3][r] = fmaf(p[s & 3][r], cprev, acc[7][s & 3][r]);
-  }
+  CIN_PP_KLOOP();
 #undef CIN_DMA
 #undef CIN_DMA_GROUP
 #undef CIN_DMA_A4
@@ -610,8 +620,6 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
 #undef CIN_FRAG
 #undef CIN_AFRAG
 #undef CIN_BFRAG
-#undef CIN_PP_LOAD
-#undef CIN_PP_COMPUTE
 
   store_tile(T, acc, smu, wave, lane, c_dtype, ldc);
 }
@@ -813,6 +821,7 @@ using big::TM;
 using big::TN;
 using big::wait_dma;
 using big::wait_dma_but_block;
+using big::lds_barrier;
 constexpr int kThreads = big::kThreads;
 
 // Scales and expert ranges do not change during a kernel: read through the constant address
@@ -1027,6 +1036,12 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
   const uint32_t offA = (uint32_t)(r0 * lda) + q16;
   const uint32_t offB = (uint32_t)(r0 * ldb) + q16;
   const uint32_t stepa = (uint32_t)(64 * lda), stepb = (uint32_t)(64 * ldb);
+  // the K loop's DMA, one group of four waves per operand (as in big::tile_body)
+  const int grp = wm;
+  const int r4 = 8 * wn + (lane >> 3);
+  const uint32_t q4 = (uint32_t)(((lane & 7) ^ swz_f(r4)) * 16);
+  const uint32_t offA4 = (uint32_t)(r4 * lda) + q4, offB4 = (uint32_t)(r4 * ldb) + q4;
+  const uint32_t stepa4 = (uint32_t)(32 * lda), stepb4 = (uint32_t)(32 * ldb);
   const uint32_t offS = (uint32_t)(sa_row((wave & 3) * 64 + lane) * ssam * 4);
   const uint32_t stepsa = (uint32_t)(ssak * 4);
   int64_t bytesA = 255 * lda + K, bytesB = 255 * ldb + K;
@@ -1045,6 +1060,8 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
   const uint32_t lds_a = (uint32_t)(uintptr_t)&sm.a[0][0] + (uint32_t)(wave * 64 * 16);
   const uint32_t lds_b = (uint32_t)(uintptr_t)&sm.b[0][0] + (uint32_t)(wave * 64 * 16);
   const uint32_t lds_s = (uint32_t)(uintptr_t)&sm.sa[0][0] + (uint32_t)((wave & 3) * 64 * 4);
+  const uint32_t lds_a4 = (uint32_t)(uintptr_t)&sm.a[0][0] + (uint32_t)(wn * 64 * 16);
+  const uint32_t lds_b4 = (uint32_t)(uintptr_t)&sm.b[0][0] + (uint32_t)(wn * 64 * 16);
   // Row group g of the operands of the tile at (pA, pB, pS), block kb, into stage stg
 #define CIN_DMA_GROUP_P(pA, pB, pS, kb, stg, g)                                               \
   do {                                                                                        \
@@ -1059,6 +1076,25 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
 #define CIN_DMA_P(pA, pB, pS, kb, stg)                                                        \
   do {                                                                                        \
     _Pragma("unroll") for (int g_ = 0; g_ < 4; ++g_) CIN_DMA_GROUP_P(pA, pB, pS, kb, stg, g_); \
+  } while (0)
+// The K loop's DMA of this tile (pA, pB, pS): all of block kb's A rows and A scales into
+// stage stg (waves 0-3), or all its B rows (waves 4-7)
+#define CIN_DMA_A4(kb, stg)                                                                   \
+  do {                                                                                        \
+    const uint32_t ko = (uint32_t)kphys(kb) * TK;                                             \
+    const uint32_t so = (uint32_t)(stg) * kTileBytes;                                         \
+    const __amdgpu_buffer_rsrc_t ra_ = make_rsrc(pA, bytesA);                                 \
+    _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_)                                          \
+      dma16(ra_, offA4, ko + i_ * stepa4, lds_a4 + so + i_ * 4096);                           \
+    dma4(make_rsrc(pS, bytesS), offS, (uint32_t)kphys(kb) * stepsa, lds_s + (uint32_t)(stg) * TM * 4); \
+  } while (0)
+#define CIN_DMA_B4(kb, stg)                                                                   \
+  do {                                                                                        \
+    const uint32_t ko = (uint32_t)kphys(kb) * TK;                                             \
+    const uint32_t so = (uint32_t)(stg) * kTileBytes;                                         \
+    const __amdgpu_buffer_rsrc_t rb_ = make_rsrc(pB, bytesB);                                 \
+    _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_)                                          \
+      dma16(rb_, offB4, ko + i_ * stepb4, lds_b4 + so + i_ * 4096);                           \
   } while (0)
   const uint8_t* lds = reinterpret_cast<const uint8_t*>(&sm);
   const int fsw = swz_f(l16);
@@ -1082,13 +1118,6 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
   })
 #define CIN_AFRAG(stg, mt) CIN_FRAG(fa, fa_hi, (uint32_t)((stg) * kTileBytes + (mt) * 16 * TK))
 #define CIN_BFRAG(stg, nt) CIN_FRAG(fb, fb_hi, (uint32_t)((stg) * kTileBytes + (nt) * 16 * TK))
-#define CIN_SA8(stg)                                                                        \
-  do {                                                                                      \
-    const float4 lo_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4)); \
-    const float4 hi_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)((stg) * TM * 4 + 256)); \
-    sa8[0] = lo_.x; sa8[1] = lo_.y; sa8[2] = lo_.z; sa8[3] = lo_.w;                         \
-    sa8[4] = hi_.x; sa8[5] = hi_.y; sa8[6] = hi_.z; sa8[7] = hi_.w;                         \
-  } while (0)
 
   // prologue of the first tile: blocks 0 and 1 into stages 0 and 1
   {
@@ -1140,59 +1169,11 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = zero;
-    v8i bf[4], af[2];
-    float cs[2], sa8[8];
+    v8i af[4], bf[4];
+    float cs[8];
+    float cprev = 0.0f;
     v4f p[4] = {zero, zero, zero, zero};
-    float sbv = sbp[(int64_t)kphys(0) * ssbk];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bf[j] = CIN_BFRAG(0, j);
-    af[0] = CIN_AFRAG(0, 0);
-    CIN_SA8(0);
-    cs[0] = sa8[0] * sbv;
-    cs[1] = 0.0f;
-    for (int kb = 0; kb < nk; ++kb) {
-      const int st = kb & 1;
-      const bool more = kb < kl;
-      const float sbn = sbp[(int64_t)kphys(more ? kb + 1 : kb) * ssbk];
-#pragma unroll
-      for (int s8 = 0; s8 < 32; ++s8) {
-        const int i = s8 >> 2, j = s8 & 3;
-        {
-          const int ti = s8 >= 3 ? (s8 - 3) >> 2 : 7;
-          const int tj = (s8 + 1) & 3;
-          const float c = cs[s8 >= 3 ? ((s8 - 3) >> 2) & 1 : 1];
-          asm volatile("" : "+v"(acc[ti][tj]));
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[ti][tj][r] = fmaf(p[(s8 + 1) & 3][r], c, acc[ti][tj][r]);
-          asm volatile("" : "+v"(acc[ti][tj]));
-        }
-        asm volatile("" : "+v"(bf[j]));
-        p[s8 & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af[i & 1], zero, 0, 0, 0, 0, 0, 0);
-        asm volatile("" : "+v"(bf[j]));
-        if ((s8 == 2 || s8 == 6) && kb >= 1 && kb + 1 < nk)
-          CIN_DMA_GROUP_P(pA, pB, pS, kb + 1, st ^ 1, s8 == 2 ? 2 : 3);
-        if (j == 0 && i < 7) af[(i + 1) & 1] = CIN_AFRAG(st, i + 1);
-        if (j == 3 && i < 7) cs[(i + 1) & 1] = sa8[i + 1] * sbv;
-        if (more) {
-          if (s8 == 28) {
-            wait_dma();
-            __syncthreads();
-            if (kb + 2 < nk) CIN_DMA_GROUP_P(pA, pB, pS, kb + 2, st, 0);
-            af[0] = CIN_AFRAG(st ^ 1, 0);
-            CIN_SA8(st ^ 1);
-          }
-          if (s8 == 30 && kb + 2 < nk) CIN_DMA_GROUP_P(pA, pB, pS, kb + 2, st, 1);
-          if (s8 >= 28) bf[j] = CIN_BFRAG(st ^ 1, j);
-          if (s8 == 31) cs[0] = sa8[0] * sbn;
-        }
-      }
-      sbv = sbn;
-    }
-#pragma unroll
-    for (int s8 = 29; s8 < 32; ++s8) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[7][s8 & 3][r] = fmaf(p[s8 & 3][r], cs[1], acc[7][s8 & 3][r]);
-    }
+    CIN_PP_KLOOP();
     __syncthreads();  // every wave is past its last fragment read: both stages are free
     Tile Tn;
     bool next;  // uniform per workgroup
@@ -1253,11 +1234,15 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
   }
 #undef CIN_DMA_P
 #undef CIN_DMA_GROUP_P
+#undef CIN_DMA_A4
+#undef CIN_DMA_B4
 #undef CIN_FRAG
 #undef CIN_AFRAG
 #undef CIN_BFRAG
-#undef CIN_SA8
 }
+#undef CIN_PP_LOAD
+#undef CIN_PP_COMPUTE
+#undef CIN_PP_KLOOP
 
 template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void k_gemm_fp8_bs_pers(
