@@ -443,6 +443,35 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_s_setprio(0);                                                            \
   } while (0)
 
+// CIN_PP_COMPUTE(0) with the reads of half 1's A fragments of the same block interleaved:
+// A fragment q of half 1 right after MFMA 4q + 3, the last MFMA to read af[q].  (Reading the
+// next block's half 0 the same way under half 1 measured no faster.)
+#define CIN_PP_COMPUTE0_READ1(kbl)                                                            \
+  do {                                                                                        \
+    const int stgl_ = (kbl) & 1;                                                              \
+    __builtin_amdgcn_s_setprio(1);                                                            \
+    _Pragma("unroll") for (int s_ = 0; s_ < 16; ++s_) {                                       \
+      {                                                                                       \
+        const int ti = s_ >= 3 ? (s_ - 3) >> 2 : 7;                                           \
+        const int tj = (s_ + 1) & 3;                                                          \
+        const float c = s_ >= 3 ? cs[(s_ - 3) >> 2] : cprev;                                  \
+        asm volatile("" : "+v"(acc[ti][tj]));                                                 \
+        _Pragma("unroll") for (int r = 0; r < 4; ++r)                                         \
+          acc[ti][tj][r] = fmaf(p[(s_ + 1) & 3][r], c, acc[ti][tj][r]);                       \
+        asm volatile("" : "+v"(acc[ti][tj]));                                                 \
+      }                                                                                       \
+      asm volatile("" : "+v"(bf[s_ & 3]));                                                    \
+      p[s_ & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[s_ & 3], af[s_ >> 2], zero, 0, 0, 0, 0, 0, 0); \
+      asm volatile("" : "+v"(bf[s_ & 3]));                                                    \
+      if ((s_ & 3) == 3) {                                                                    \
+        asm volatile("" : "+v"(af[s_ >> 2]));                                                 \
+        af[s_ >> 2] = CIN_AFRAG(stgl_, 4 + (s_ >> 2));                                        \
+      }                                                                                       \
+    }                                                                                         \
+    cprev = cs[3];                                                                            \
+    __builtin_amdgcn_s_setprio(0);                                                            \
+  } while (0)
+
 // The K loop of the ping-pong schedule and its drain, for a workgroup whose operands of
 // block 0 have landed (blocks 0 and 1 DMA'd by all eight waves, block 0 waited for and a
 // barrier passed).  The enclosing function defines the per-group DMA of the loop:
@@ -457,8 +486,7 @@ __device__ __forceinline__ void lds_barrier() {
     for (int kb = 0; kb < nk; ++kb) {                                                               \
       const int st = kb & 1;                                                                        \
       const bool more = kb < kl;                                                                    \
-      CIN_PP_COMPUTE(0);  /* slot A */                                                              \
-      CIN_PP_LOAD(kb, 1);  /* slot B */                                                             \
+      CIN_PP_COMPUTE0_READ1(kb);  /* slots A and B: half 1's A fragments read under half 0 */       \
       CIN_PP_COMPUTE(1);  /* slot C: block kb's stage is read for the last time; kb+1 lands */      \
       wait_dma();                                                                                   \
       lds_barrier();                                                                                \
@@ -473,11 +501,10 @@ __device__ __forceinline__ void lds_barrier() {
       const bool more = kb < kl;                                                                    \
       if (kb >= 1 && more) CIN_DMA_B4(kb + 1, st ^ 1);  /* slot A */                                \
       CIN_PP_LOAD(kb, 0);                                                                           \
-      CIN_PP_COMPUTE(0);  /* slot B */                                                              \
-      CIN_PP_LOAD(kb, 1);  /* slot C */                                                             \
+      CIN_PP_COMPUTE0_READ1(kb);  /* slots B and C */                                               \
       wait_dma();                                                                                   \
       lds_barrier();                                                                                \
-      CIN_PP_COMPUTE(1);  /* slot D */                                                              \
+      CIN_PP_COMPUTE(1);                                                                            \
     }                                                                                               \
   }                                                                                                 \
 /* drain: FMAs of the last half's MFMAs 13-15 (m-tile 7) */                                         \
@@ -497,6 +524,8 @@ _Pragma("unroll")                                                               
 //   B: waves 4-7 compute (kb, 0); waves 0-3 read (kb, 1)
 //   C: waves 0-3 compute (kb, 1); waves 4-7 read (kb, 1); then block kb+1 has landed
 //   D: waves 4-7 compute (kb, 1); waves 0-3 read (kb+1, 0) and DMA A of block kb+2
+// (Both groups read half 1's A fragments between half 0's MFMAs, as each MFMA frees its
+// fragment registers, so a wave does not wait for them at its next half.)
 // One barrier per K block, after C: block kb's stage is no longer read and block kb+1's DMA
 // is complete.  (A barrier after every slot, to hold the alternation exactly, measured
 // slower.)  Before MFMA s of a half, the wave issues the 4 scale-FMAs of MFMA s - 3 from a
@@ -1242,6 +1271,7 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
 }
 #undef CIN_PP_LOAD
 #undef CIN_PP_COMPUTE
+#undef CIN_PP_COMPUTE0_READ1
 #undef CIN_PP_KLOOP
 
 template <int EPI>
