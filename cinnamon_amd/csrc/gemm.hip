@@ -474,7 +474,11 @@ __device__ __forceinline__ void lds_barrier() {
 
 // The K loop of the ping-pong schedule and its drain, for a workgroup whose operands of
 // block 0 have landed (blocks 0 and 1 DMA'd by all eight waves, block 0 waited for and a
-// barrier passed).  The enclosing function defines the per-group DMA of the loop:
+// barrier passed).  kLoadsFirst (a constant of the enclosing function) orders a group's
+// fragment reads before its DMA burst in the same slot, so the reads do not queue behind
+// DMA issue stalls: faster in the persistent walks (C4 dgrad 150.8 -> 144.8 us, C3 down
+// 2304 -> 2281 us), 0.8 us slower on the one-round C2 GEMM, which keeps the DMA first.
+// The enclosing function defines the per-group DMA of the loop:
 // CIN_DMA_A4(kb, stg) (waves 0-3: block kb's A rows and A scales) and CIN_DMA_B4(kb, stg)
 // (waves 4-7: block kb's B rows), and the fragment reads CIN_AFRAG / CIN_BFRAG.
 #define CIN_PP_KLOOP()                                                                              \
@@ -491,16 +495,18 @@ __device__ __forceinline__ void lds_barrier() {
       wait_dma();                                                                                   \
       lds_barrier();                                                                                \
       if (more) {  /* slot D */                                                                     \
-        if (kb + 2 < nk) CIN_DMA_A4(kb + 2, st);                                                    \
+        if (!kLoadsFirst && kb + 2 < nk) CIN_DMA_A4(kb + 2, st);                                    \
         CIN_PP_LOAD(kb + 1, 0);                                                                     \
+        if (kLoadsFirst && kb + 2 < nk) CIN_DMA_A4(kb + 2, st);                                     \
       }                                                                                             \
     }                                                                                               \
   } else {                                                                                          \
     for (int kb = 0; kb < nk; ++kb) {                                                               \
       const int st = kb & 1;                                                                        \
       const bool more = kb < kl;                                                                    \
-      if (kb >= 1 && more) CIN_DMA_B4(kb + 1, st ^ 1);  /* slot A */                                \
+      if (!kLoadsFirst && kb >= 1 && more) CIN_DMA_B4(kb + 1, st ^ 1);  /* slot A */                \
       CIN_PP_LOAD(kb, 0);                                                                           \
+      if (kLoadsFirst && kb >= 1 && more) CIN_DMA_B4(kb + 1, st ^ 1);                               \
       CIN_PP_COMPUTE0_READ1(kb);  /* slots B and C */                                               \
       wait_dma();                                                                                   \
       lds_barrier();                                                                                \
@@ -626,6 +632,7 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
+  constexpr bool kLoadsFirst = false;
   v8i af[4], bf[4];
   float cs[8];
   float cprev = 0.0f;  // the "previous half" FMAs of the first half add 0 * 0
@@ -1198,6 +1205,7 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = zero;
+    constexpr bool kLoadsFirst = true;
     v8i af[4], bf[4];
     float cs[8];
     float cprev = 0.0f;
