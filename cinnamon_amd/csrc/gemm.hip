@@ -881,6 +881,7 @@ struct DenseSrc {
   int64_t lda, ssam, ldb, ssbn, ldc, M, N;
   int es;
   uint32_t tiles_m, tiles_n;
+  __device__ uint32_t count() const { return tiles_m * tiles_n; }
   __device__ bool get(uint32_t v, Tile& t) const {
     if (v >= tiles_m * tiles_n) return false;
     uint32_t tm, tn;
@@ -910,6 +911,7 @@ struct GroupedSrc {
   const int64_t* starts; const int64_t* ends;
   int E;
   const int* tpre;
+  __device__ uint32_t count() const { return (uint32_t)tpre[E] * tiles_n; }
   __device__ bool get(uint32_t v, Tile& t) const {
     const uint32_t total_m = (uint32_t)tpre[E];
     if (v >= total_m * tiles_n) return false;
@@ -1009,6 +1011,47 @@ __device__ __forceinline__ void wait_dma_past_stores() {
   __builtin_amdgcn_s_waitcnt(0x8F78);
 }
 
+// 16-bit C of one tile with kEpiStoresX4 16-byte stores per wave.  Entries (i, j) and
+// (i, j + 1) hold columns 16 j + 4 kq .. + 3 and 16 j + 16 + 4 kq .. + 3 of row l16 in
+// each lane; v_permlane16_swap trades the odd 16-lane rows of the first with the even rows
+// of the second, after which a lane with even kq holds 8 consecutive columns of entry j
+// and a lane with odd kq 8 of entry j + 1, so the four lanes of a row write one 64-byte
+// run (32 bytes per run with store_counted).  Same sink rule and drain-by-count as
+// store_counted.  C must be 16-byte aligned with ldc a multiple of 8; col_lo must be a
+// multiple of 8 (it is 0 or 128 here, as N is a multiple of 128).
+constexpr int kEpiStoresX4 = 16;
+__device__ uint4 g_store_sink16[64];
+__device__ __forceinline__ void store_counted_x4(const Tile& T, const v4f (&acc)[8][4], int wm, int wn, int l16,
+                                                 int kq, int c_dtype, int64_t ldc) {
+  const int rl = wm * 128 + l16, cl = wn * 64 + 4 * kq + ((kq & 1) ? 12 : 0);
+  uint16_t* c0 = static_cast<uint16_t*>(T.C) + (int64_t)rl * ldc + cl;
+  uint4* sink = &g_store_sink16[threadIdx.x & 63];
+  const uint32_t rows = (uint32_t)(T.row_hi - T.row_lo);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bool rok = (uint32_t)(rl + 16 * i - T.row_lo) < rows;
+#pragma unroll
+    for (int jp = 0; jp < 2; ++jp) {
+      const v4f& X = acc[i][2 * jp];
+      const v4f& Y = acc[i][2 * jp + 1];
+      const uint32_t x0 = f32_to_half_bits(c_dtype, X[0]) | (f32_to_half_bits(c_dtype, X[1]) << 16);
+      const uint32_t x1 = f32_to_half_bits(c_dtype, X[2]) | (f32_to_half_bits(c_dtype, X[3]) << 16);
+      const uint32_t y0 = f32_to_half_bits(c_dtype, Y[0]) | (f32_to_half_bits(c_dtype, Y[1]) << 16);
+      const uint32_t y1 = f32_to_half_bits(c_dtype, Y[2]) | (f32_to_half_bits(c_dtype, Y[3]) << 16);
+      const auto s0 = __builtin_amdgcn_permlane16_swap(x0, y0, false, false);
+      const auto s1 = __builtin_amdgcn_permlane16_swap(x1, y1, false, false);
+      const bool ok = rok && cl + 32 * jp >= T.col_lo;
+      uint4* p = ok ? reinterpret_cast<uint4*>(c0 + (int64_t)(16 * i) * ldc + 32 * jp) : sink;
+      *p = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+    }
+  }
+}
+// s_waitcnt vmcnt(kEpiStoresX4 + 8)
+__device__ __forceinline__ void wait_dma_past_stores_x4() {
+  static_assert(kEpiStoresX4 + 8 == 24, "encoding below is vmcnt(24)");
+  __builtin_amdgcn_s_waitcnt(0x4F78);
+}
+
 // fp32 C of one tile with exactly kEpiStores 16-byte stores per wave (a lane holds 4
 // consecutive columns of one row), the same count as store_counted, so the next tile
 // waits with the same vmcnt.  C must be 16-byte aligned with ldc a multiple of 4.
@@ -1033,8 +1076,27 @@ __device__ __forceinline__ void store_counted32(const Tile& T, const v4f (&acc)[
 
 // How a persistent kernel stores C: every tile with store_direct (the next tile then waits
 // for everything), or with a fixed count of stores per wave that the next tile's first wait
-// looks past (16-bit C: store_counted; fp32 C: store_counted32).
-constexpr int kEpiDirect = 0, kEpiCounted16 = 1, kEpiCounted32 = 2;
+// looks past (16-bit C: store_counted_x4, or store_counted where C is only 8-byte aligned;
+// fp32 C: store_counted32).
+constexpr int kEpiDirect = 0, kEpiCounted16 = 1, kEpiCounted32 = 2, kEpiCounted16x4 = 3;
+
+// Idles the wave for about `ticks` periods of the 100 MHz real-time clock (bounded: at
+// most 2^16 sleeps of about 1000 cycles each).
+__device__ __forceinline__ void idle_for(uint64_t ticks) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < (1 << 16); ++it) {
+    if (__builtin_amdgcn_s_memrealtime() - t0 >= ticks) break;
+    __builtin_amdgcn_s_sleep(16);
+  }
+}
+// Start offset of a persistent workgroup that owns one tile fewer than the busiest ones,
+// in real-time ticks (10 ns) per K block of its first tile.  Tiles of equal K take about
+// equal time, so workgroups that start together reach every tile boundary together, and
+// all of them then store C and fetch their next tile's first blocks at once; starting the
+// short workgroups late puts their boundaries inside the others' K loops.  Owning one
+// tile fewer, they lose nothing while the offset stays under a tile's duration (about
+// 130 ticks per K block at full clock).
+constexpr uint32_t kLateStartPerBlock = 30;
 
 // A pointer as a wave-uniform value (the DMA's buffer descriptor lives in SGPRs).
 template <class P>
@@ -1045,7 +1107,8 @@ __device__ __forceinline__ P* uniform_ptr(P* p) {
   return (P*)(uintptr_t)((hi << 32) | lo);
 }
 
-// EPI: kEpiCounted16 needs 16-bit C 8-byte aligned with ldc a multiple of 4,
+// EPI: kEpiCounted16x4 needs 16-bit C 16-byte aligned with ldc a multiple of 8,
+// kEpiCounted16 16-bit C 8-byte aligned with ldc a multiple of 4,
 // kEpiCounted32 fp32 C 16-byte aligned with ldc a multiple of 4; kEpiDirect takes any C.
 // VARK: the K blocks vary per tile (Tile::nk, at least 1); K is then unused.
 template <int EPI, class Src, bool VARK = false>
@@ -1155,6 +1218,12 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
 #define CIN_AFRAG(stg, mt) CIN_FRAG(fa, fa_hi, (uint32_t)((stg) * kTileBytes + (mt) * 16 * TK))
 #define CIN_BFRAG(stg, nt) CIN_FRAG(fb, fb_hi, (uint32_t)((stg) * kTileBytes + (nt) * 16 * TK))
 
+  {
+    // v < G here; the workgroups with v >= total % G own one tile fewer
+    const uint32_t total = src.count();
+    const uint32_t rem = total % G;
+    if (total > G && rem != 0 && v >= rem) idle_for((uint64_t)nk * kLateStartPerBlock);
+  }
   // prologue of the first tile: blocks 0 and 1 into stages 0 and 1
   {
     Tile T0;
@@ -1195,6 +1264,8 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
     // be in flight; they are waited for at the first K block's barrier
     if (nk > 1 && first)
       wait_dma_but_block();
+    else if (EPI == kEpiCounted16x4 && nk > 1)
+      wait_dma_past_stores_x4();
     else if (EPI != kEpiDirect && nk > 1)
       wait_dma_past_stores();
     else
@@ -1259,7 +1330,9 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
       }
       return;
     }
-    if constexpr (EPI == kEpiCounted16)
+    if constexpr (EPI == kEpiCounted16x4)
+      store_counted_x4(T, acc, wm, wn, l16, kq, c_dtype, ldc);
+    else if constexpr (EPI == kEpiCounted16)
       store_counted(T, acc, wm, wn, l16, kq, c_dtype, ldc);
     else if constexpr (EPI == kEpiCounted32)
       store_counted32(T, acc, wm, wn, l16, kq, ldc);
@@ -1366,6 +1439,9 @@ struct WgradSrc {
   const int* order;    // experts with tokens, most K blocks first
   const int* enk;      // K blocks per expert (0: no tokens, or a range past the operands)
   const int64_t* poff; // padded token offset per expert
+  // no start offsets (run_tiles): the tiles' K lengths differ, so owning one tile fewer
+  // says little about finishing earlier
+  __device__ uint32_t count() const { return 0; }
   __device__ bool get(uint32_t v, Tile& t) const {
     if (v >= total) return false;
     const uint32_t i = v / G, b = v - i * G;
@@ -1483,6 +1559,7 @@ int pers_epi(int c_dtype, const void* C, int64_t ldc, int64_t sce) {
   const uintptr_t a = (uintptr_t)C;
   if (c_dtype == CIN_DT_F32)
     return (a & 15) == 0 && ldc % 4 == 0 && sce % 4 == 0 ? pers::kEpiCounted32 : pers::kEpiDirect;
+  if ((a & 15) == 0 && ldc % 8 == 0 && sce % 8 == 0) return pers::kEpiCounted16x4;
   return (a & 7) == 0 && ldc % 4 == 0 && sce % 4 == 0 ? pers::kEpiCounted16 : pers::kEpiDirect;
 }
 
@@ -1556,7 +1633,9 @@ int cin_gemm_fp8_bs(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam
   hipLaunchKernelGGL(pers::k_gemm_fp8_bs_pers<EPI_>, ncu, big::kThreads, 0, s, A, lda, sa, ssam, ssak, B, \
                      ldb, sb, ssbn, ssbk, M, N, K, C, c_dtype, ldc, tm, tn)
       const int epi = pers_epi(c_dtype, C, ldc, 0);
-      if (epi == pers::kEpiCounted16)
+      if (epi == pers::kEpiCounted16x4)
+        CIN_LAUNCH_DENSE_PERS(pers::kEpiCounted16x4);
+      else if (epi == pers::kEpiCounted16)
         CIN_LAUNCH_DENSE_PERS(pers::kEpiCounted16);
       else if (epi == pers::kEpiCounted32)
         CIN_LAUNCH_DENSE_PERS(pers::kEpiCounted32);
@@ -1604,7 +1683,9 @@ int cin_grouped_gemm_fp8(const uint8_t* A, int64_t lda, const float* sa, int64_t
                      static_cast<hipStream_t>(stream), A, lda, sa, ssam, ssak, B, sbe, ldb, sb, ssbe, ssbn, \
                      ssbk, starts, ends, (int)E, T, N, K, C, c_dtype, ldc, tn)
       const int epi = pers_epi(c_dtype, C, ldc, 0);
-      if (epi == pers::kEpiCounted16)
+      if (epi == pers::kEpiCounted16x4)
+        CIN_LAUNCH_GROUPED_PERS(pers::kEpiCounted16x4);
+      else if (epi == pers::kEpiCounted16)
         CIN_LAUNCH_GROUPED_PERS(pers::kEpiCounted16);
       else if (epi == pers::kEpiCounted32)
         CIN_LAUNCH_GROUPED_PERS(pers::kEpiCounted32);
@@ -1663,7 +1744,9 @@ int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, i
                      static_cast<hipStream_t>(stream), A, lda, sa, ssam, B, ldb, sb, ssbm, starts, ends, \
                      (int)E, T, tcap, N, K, C, c_dtype, ldc, sce, (uint32_t)tm, (uint32_t)tn)
     const int epi = pers_epi(c_dtype, C, ldc, sce);
-    if (epi == pers::kEpiCounted16)
+    if (epi == pers::kEpiCounted16x4)
+      CIN_LAUNCH_WGRAD_PERS(pers::kEpiCounted16x4);
+    else if (epi == pers::kEpiCounted16)
       CIN_LAUNCH_WGRAD_PERS(pers::kEpiCounted16);
     else if (epi == pers::kEpiCounted32)
       CIN_LAUNCH_WGRAD_PERS(pers::kEpiCounted32);
