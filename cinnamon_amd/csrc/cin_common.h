@@ -109,12 +109,23 @@ __device__ inline float e4m3_to_f32(uint32_t c) {
 __device__ inline float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// fp32 -> bf16 bits with round-to-nearest-even (NaN kept quiet).
+// Two fp32 values -> packed bf16 bits (lo in bits 0-15), by gfx950's v_cvt_pk_bf16_f32:
+// round to nearest even, a NaN kept quiet with its sign and upper payload (bits 16-31 of
+// the input, quiet bit set), denormals kept.  That is, per value: u = bits of f; NaN ->
+// (u >> 16) | 0x40, else (u + 0x7fff + ((u >> 16) & 1)) >> 16 -- the instruction gives
+// exactly this on every one of the 2^32 inputs (checked exhaustively on an MI355X against
+// the integer formula, which is what this file computed before).  gfx950 has no
+// instruction that fuses a multiply-add with a bf16 rounding, so unlike the fp16 case
+// below the inputs need no pinning as fp32 values.
+typedef __bf16 cin_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t f32x2_to_bf16x2_bits(float lo, float hi) {
+  const cin_bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// fp32 -> bf16 bits with round-to-nearest-even (NaN kept quiet), as above.
 __device__ inline uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return f32x2_to_bf16x2_bits(f, 0.0f) & 0xffffu;
 }
 
 // fp32 -> fp16 bits, round to nearest even (overflow to inf, as a torch .half()).  The
@@ -132,6 +143,17 @@ __device__ inline uint16_t f32_to_f16_bits(float f) {
 // fp32 -> the bits of a 16-bit output dtype (CIN_DT_F16 or CIN_DT_BF16), RNE.
 __device__ inline uint32_t f32_to_half_bits(int dt, float f) {
   return dt == CIN_DT_F16 ? (uint32_t)f32_to_f16_bits(f) : f32_to_bf16_bits(f);
+}
+
+// Two fp32 values -> packed bits (lo in bits 0-15) of the 16-bit dtype OUT, RNE.  OUT is
+// a template argument so that loops over many values carry no per-value dtype test.
+template <int OUT>
+__device__ inline uint32_t f32x2_to_half2_bits(float lo, float hi) {
+  static_assert(OUT == CIN_DT_BF16 || OUT == CIN_DT_F16, "16-bit output dtype");
+  if constexpr (OUT == CIN_DT_BF16)
+    return f32x2_to_bf16x2_bits(lo, hi);
+  else
+    return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
 }
 
 // The bits of a 16-bit dtype (CIN_DT_F16 or CIN_DT_BF16) widened to fp32 (exact).

@@ -327,6 +327,28 @@ struct Tile {
   int nk = 0;  // K blocks of this tile, where they vary per tile (grouped wgrad)
 };
 
+// Four consecutive fp32 columns of one accumulator entry -> four packed values of the
+// 16-bit dtype OUT (two 32-bit words, lowest column in the lowest bits).
+template <int OUT>
+__device__ __forceinline__ uint2 pack4(const v4f& a) {
+  return make_uint2(f32x2_to_half2_bits<OUT>(a[0], a[1]), f32x2_to_half2_bits<OUT>(a[2], a[3]));
+}
+
+// The 16-bit tile into LDS as a row-major 256 x 256 array (row stride kCStride bytes).
+template <int OUT>
+__device__ __forceinline__ void stage_tile16(const v4f (&acc)[8][4], SmemAll& smu, int wm, int wn,
+                                             int l16, int kq) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int m = wm * 128 + i * 16 + l16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = wn * 64 + j * 16 + kq * 4;
+      *reinterpret_cast<uint2*>(&smu.c[m * kCStride + n * 2]) = pack4<OUT>(acc[i][j]);
+    }
+  }
+}
+
 // The finished 256 x 256 tile out of the accumulators: lane (wave, lane) holds rows
 // 128 wm + 16 i + l16 and columns 64 wn + 16 j + 4 kq .. + 3 of m-tile i, n-tile j.
 __device__ __forceinline__ void store_tile(const Tile& T, const v4f (&acc)[8][4], SmemAll& smu, int wave,
@@ -340,18 +362,10 @@ __device__ __forceinline__ void store_tile(const Tile& T, const v4f (&acc)[8][4]
   // and non-temporal stores (C is not read again by this kernel) shave ~1% more.
   if (c_dtype != CIN_DT_F32 && ((((uintptr_t)T.C) & 15) == 0) && (ldc & 7) == 0) {
     __syncthreads();  // every wave is past its last fragment read
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int m = wm * 128 + i * 16 + l16;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = wn * 64 + j * 16 + kq * 4;
-        const uint32_t b0 = f32_to_half_bits(c_dtype, acc[i][j][0]), b1 = f32_to_half_bits(c_dtype, acc[i][j][1]);
-        const uint32_t b2 = f32_to_half_bits(c_dtype, acc[i][j][2]), b3 = f32_to_half_bits(c_dtype, acc[i][j][3]);
-        *reinterpret_cast<uint2*>(&smu.c[m * kCStride + n * 2]) =
-            make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
-      }
-    }
+    if (c_dtype == CIN_DT_F16)
+      stage_tile16<CIN_DT_F16>(acc, smu, wm, wn, l16, kq);
+    else
+      stage_tile16<CIN_DT_BF16>(acc, smu, wm, wn, l16, kq);
     __syncthreads();
     const int half = lane >> 5, c16 = lane & 31;  // lane: row half, 16-byte column chunk
 #pragma unroll
@@ -986,8 +1000,9 @@ __device__ uint2 g_store_sink[64];
 // vector memory operations retire from the count in issue order, so the stores drain while
 // the next tile starts.  C must be 8-byte aligned with ldc a multiple of 4.
 constexpr int kEpiStores = 32;
-__device__ __forceinline__ void store_counted(const Tile& T, const v4f (&acc)[8][4], int wm, int wn, int l16,
-                                              int kq, int c_dtype, int64_t ldc) {
+template <int OUT>
+__device__ __forceinline__ void store_counted_t(const Tile& T, const v4f (&acc)[8][4], int wm, int wn, int l16,
+                                                int kq, int64_t ldc) {
   const int rl = wm * 128 + l16, cl = wn * 64 + kq * 4;
   uint16_t* c0 = static_cast<uint16_t*>(T.C) + (int64_t)rl * ldc + cl;
   uint2* sink = &g_store_sink[threadIdx.x & 63];
@@ -999,11 +1014,16 @@ __device__ __forceinline__ void store_counted(const Tile& T, const v4f (&acc)[8]
     for (int j = 0; j < 4; ++j) {
       const bool ok = rok && cl + 16 * j >= T.col_lo;
       uint2* p = ok ? reinterpret_cast<uint2*>(c0 + (int64_t)(16 * i) * ldc + 16 * j) : sink;
-      const uint32_t b0 = f32_to_half_bits(c_dtype, acc[i][j][0]), b1 = f32_to_half_bits(c_dtype, acc[i][j][1]);
-      const uint32_t b2 = f32_to_half_bits(c_dtype, acc[i][j][2]), b3 = f32_to_half_bits(c_dtype, acc[i][j][3]);
-      *p = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
+      *p = big::pack4<OUT>(acc[i][j]);
     }
   }
+}
+__device__ __forceinline__ void store_counted(const Tile& T, const v4f (&acc)[8][4], int wm, int wn, int l16,
+                                              int kq, int c_dtype, int64_t ldc) {
+  if (c_dtype == CIN_DT_F16)
+    store_counted_t<CIN_DT_F16>(T, acc, wm, wn, l16, kq, ldc);
+  else
+    store_counted_t<CIN_DT_BF16>(T, acc, wm, wn, l16, kq, ldc);
 }
 // s_waitcnt vmcnt(kEpiStores + 8): all but the last 40 vector memory operations done
 __device__ __forceinline__ void wait_dma_past_stores() {
@@ -1021,8 +1041,9 @@ __device__ __forceinline__ void wait_dma_past_stores() {
 // multiple of 8 (it is 0 or 128 here, as N is a multiple of 128).
 constexpr int kEpiStoresX4 = 16;
 __device__ uint4 g_store_sink16[64];
-__device__ __forceinline__ void store_counted_x4(const Tile& T, const v4f (&acc)[8][4], int wm, int wn, int l16,
-                                                 int kq, int c_dtype, int64_t ldc) {
+template <int OUT>
+__device__ __forceinline__ void store_counted_x4_t(const Tile& T, const v4f (&acc)[8][4], int wm, int wn, int l16,
+                                                   int kq, int64_t ldc) {
   const int rl = wm * 128 + l16, cl = wn * 64 + 4 * kq + ((kq & 1) ? 12 : 0);
   uint16_t* c0 = static_cast<uint16_t*>(T.C) + (int64_t)rl * ldc + cl;
   uint4* sink = &g_store_sink16[threadIdx.x & 63];
@@ -1034,10 +1055,8 @@ __device__ __forceinline__ void store_counted_x4(const Tile& T, const v4f (&acc)
     for (int jp = 0; jp < 2; ++jp) {
       const v4f& X = acc[i][2 * jp];
       const v4f& Y = acc[i][2 * jp + 1];
-      const uint32_t x0 = f32_to_half_bits(c_dtype, X[0]) | (f32_to_half_bits(c_dtype, X[1]) << 16);
-      const uint32_t x1 = f32_to_half_bits(c_dtype, X[2]) | (f32_to_half_bits(c_dtype, X[3]) << 16);
-      const uint32_t y0 = f32_to_half_bits(c_dtype, Y[0]) | (f32_to_half_bits(c_dtype, Y[1]) << 16);
-      const uint32_t y1 = f32_to_half_bits(c_dtype, Y[2]) | (f32_to_half_bits(c_dtype, Y[3]) << 16);
+      const uint32_t x0 = f32x2_to_half2_bits<OUT>(X[0], X[1]), x1 = f32x2_to_half2_bits<OUT>(X[2], X[3]);
+      const uint32_t y0 = f32x2_to_half2_bits<OUT>(Y[0], Y[1]), y1 = f32x2_to_half2_bits<OUT>(Y[2], Y[3]);
       const auto s0 = __builtin_amdgcn_permlane16_swap(x0, y0, false, false);
       const auto s1 = __builtin_amdgcn_permlane16_swap(x1, y1, false, false);
       const bool ok = rok && cl + 32 * jp >= T.col_lo;
@@ -1045,6 +1064,13 @@ __device__ __forceinline__ void store_counted_x4(const Tile& T, const v4f (&acc)
       *p = make_uint4(s0[0], s1[0], s0[1], s1[1]);
     }
   }
+}
+__device__ __forceinline__ void store_counted_x4(const Tile& T, const v4f (&acc)[8][4], int wm, int wn, int l16,
+                                                 int kq, int c_dtype, int64_t ldc) {
+  if (c_dtype == CIN_DT_F16)
+    store_counted_x4_t<CIN_DT_F16>(T, acc, wm, wn, l16, kq, ldc);
+  else
+    store_counted_x4_t<CIN_DT_BF16>(T, acc, wm, wn, l16, kq, ldc);
 }
 // s_waitcnt vmcnt(kEpiStoresX4 + 8)
 __device__ __forceinline__ void wait_dma_past_stores_x4() {
@@ -1307,17 +1333,10 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
       src.get(v, T);
     if (!next && c_dtype != CIN_DT_F32 && ((((uintptr_t)T.C) & 15) == 0) && (ldc & 7) == 0) {
       // last tile of this workgroup: the LDS-staged epilogue of big::tile_body
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int m = wm * 128 + i * 16 + l16;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int n = wn * 64 + j * 16 + kq * 4;
-          const uint32_t b0 = f32_to_half_bits(c_dtype, acc[i][j][0]), b1 = f32_to_half_bits(c_dtype, acc[i][j][1]);
-          const uint32_t b2 = f32_to_half_bits(c_dtype, acc[i][j][2]), b3 = f32_to_half_bits(c_dtype, acc[i][j][3]);
-          *reinterpret_cast<uint2*>(&smu.c[m * kCStride + n * 2]) = make_uint2(b0 | (b1 << 16), b2 | (b3 << 16));
-        }
-      }
+      if (c_dtype == CIN_DT_F16)
+        big::stage_tile16<CIN_DT_F16>(acc, smu, wm, wn, l16, kq);
+      else
+        big::stage_tile16<CIN_DT_BF16>(acc, smu, wm, wn, l16, kq);
       __syncthreads();
       const int half = lane >> 5, c16 = lane & 31;
 #pragma unroll
