@@ -316,3 +316,93 @@ def test_persistent_gemm_into_strided_c(kern, dev, out_dtype, pad):
     torch.cuda.synchronize()
     assert torch.equal(got, want), f"strided C (ldc = N + {pad}) differs from contiguous C"
     assert bool((big[:, N:] == 7.0).all()), "padding columns were written"
+
+
+def _bf16_rne_bits(u32):
+    """fp32 bit patterns -> bf16 bit patterns: round to nearest even; a NaN keeps its sign
+    and upper payload with the quiet bit set (the integer formula the epilogue follows)."""
+    u = u32.astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    return np.where(nan, ((u >> 16) | 0x40) & 0xFFFF, r).astype(np.uint16)
+
+
+def _special_scale_patterns():
+    """fp32 bit patterns for the row scales: ties below and above an even bf16 mantissa,
+    one ulp either side of a tie, fp32 denormals, values next to FLT_MAX (some round to inf
+    in bf16), infinities, NaNs with payloads, signed zeros and plain random values."""
+    rng = np.random.default_rng(5)
+    hi = rng.integers(0, 1 << 16, size=96, dtype=np.uint64) << 16
+    pats = []
+    for low in (0x8000, 0x7FFF, 0x8001, 0x0000, 0xFFFF):
+        pats.append(hi | low)
+    pats.append(rng.integers(0x00000001, 0x00800000, size=64, dtype=np.uint64))  # denormals
+    pats.append(rng.integers(0x80000001, 0x80800000, size=32, dtype=np.uint64))  # negative denormals
+    pats.append(np.array([0x7F7FFFFF, 0x7F7F8000, 0x7F7F7FFF, 0x7F7E8000, 0xFF7FFFFF, 0xFF7F8000,
+                          0x7F800000, 0xFF800000, 0x7FC00000, 0x7FC12345, 0xFFC0ABCD, 0x7F812345,
+                          0x00000000, 0x80000000, 0x3F808000, 0x3F818000], dtype=np.uint64))
+    pats.append(rng.integers(0, 1 << 32, size=400, dtype=np.uint64))
+    p = np.concatenate(pats).astype(np.uint32)
+    return p
+
+
+@pytest.mark.parametrize("M,N", [(512, 512), (4352, 4096)])
+@pytest.mark.parametrize("path", ["dense_bf16", "grouped_bf16", "grouped_f16"])
+def test_gemm_half_output_rounding_special_values(kern, dev, M, N, path):
+    """The 16-bit epilogues round the fp32 result exactly as the fp32 output rounded to
+    nearest even.  Dense: the one-round LDS-staged tile at 2 x 2 tiles, the persistent
+    16-byte stores and its last-tile LDS path at 17 x 16 tiles; grouped (one expert over
+    every row): the persistent walk at both sizes, bf16 and fp16.  One K block in which row
+    m of A and row n of B hold a single non-zero code, so C[m, n] = b_n * sa[m] with b_n
+    mostly a power of two, which carries the chosen scale bit patterns (ties, denormals,
+    overflow, NaN payloads) into C unchanged.  bf16: bit-exact against the integer RNE of
+    the fp32 output bits, NaN payloads included; fp16: bit-exact against numpy's IEEE
+    conversion of the fp32 output, NaNs by position."""
+    from cinnamon_amd import layers
+    K = 128
+    pats = _special_scale_patterns()
+    sa_bits = np.resize(pats, M).astype(np.uint32)
+    sa = torch.from_numpy(sa_bits.view(np.float32).copy()).reshape(M, 1).to(dev)
+    # e4m3 codes of b_n: 1, 2, 0.5, 4, 0.25, -1, 256, 2^-6 (powers of two) and 1.125, 3.5
+    codes_b = np.array([0x38, 0x40, 0x30, 0x48, 0x28, 0xB8, 0x78, 0x08, 0x39, 0x46], dtype=np.uint8)
+    a = torch.zeros(M, K, dtype=torch.uint8)
+    a[:, 0] = 0x38  # 1.0
+    b = torch.zeros(N, K, dtype=torch.uint8)
+    b[:, 0] = torch.from_numpy(np.resize(codes_b, N))
+    sb = torch.ones(N // 128, 1, device=dev)
+    a8, b8 = a.view(torch.float8_e4m3fn).to(dev), b.view(torch.float8_e4m3fn).to(dev)
+    out_dtype = torch.float16 if path == "grouped_f16" else torch.bfloat16
+    if path == "dense_bf16":
+        y32 = kern.fp8_gemm_bs(a8, sa, b8, sb, torch.float32)
+        y16 = kern.fp8_gemm_bs(a8, sa, b8, sb, out_dtype)
+    else:
+        starts = torch.zeros(1, dtype=torch.int64, device=dev)
+        ends = torch.full((1,), M, dtype=torch.int64, device=dev)
+        w8, ws = b8.unsqueeze(0).contiguous(), sb.unsqueeze(0).contiguous()
+        y32 = layers.fp8_grouped_gemm(a8, sa, w8, ws, starts, ends, out_dtype=torch.float32)
+        y16 = layers.fp8_grouped_gemm(a8, sa, w8, ws, starts, ends, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    f32 = y32.cpu().numpy()
+    u32 = f32.view(np.uint32)
+    # the construction reached the cases it is meant to reach
+    assert int(((u32 & 0xFFFF) == 0x8000).sum()) > 1000, "no exact bf16 ties in C"
+    assert int(((np.abs(f32) < np.float32(1.1754944e-38)) & (f32 != 0)).sum()) > 100, "no denormals in C"
+    assert bool(np.isnan(f32).any()) and bool(np.isinf(f32).any())
+    got = y16.cpu().view(torch.int16).numpy().view(np.uint16)
+    if out_dtype == torch.bfloat16:
+        want = _bf16_rne_bits(u32)
+        bad = np.argwhere(got != want)
+        if bad.size:
+            r, c = bad[0]
+            raise AssertionError(f"{len(bad)} bf16 values differ from RNE; first at ({r}, {c}): fp32 "
+                                 f"{u32[r, c]:08x} got {got[r, c]:04x} want {want[r, c]:04x}")
+    else:
+        with np.errstate(over="ignore"):  # values past fp16's range become inf, as intended
+            want16 = f32.astype(np.float16)
+        nan = np.isnan(want16)
+        assert bool((np.isnan(got.view(np.float16)) == nan).all()), "fp16 NaN positions differ"
+        bad = np.argwhere((got != want16.view(np.uint16)) & ~nan)
+        if bad.size:
+            r, c = bad[0]
+            raise AssertionError(f"{len(bad)} fp16 values differ from RNE; first at ({r}, {c}): fp32 "
+                                 f"{u32[r, c]:08x} got {got[r, c]:04x} want {want16.view(np.uint16)[r, c]:04x}")
