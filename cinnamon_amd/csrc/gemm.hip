@@ -428,7 +428,7 @@ __device__ __forceinline__ void lds_barrier() {
       _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_) bf[j_] = CIN_BFRAG(stg_, j_);          \
       const float4 lo_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)(stg_ * TM * 4)); \
       const float4 hi_ = *reinterpret_cast<const float4*>(lds + fs + (uint32_t)(stg_ * TM * 4 + 256)); \
-      const float sb_ = sbp[(int64_t)kphys(kb) * ssbk];                                       \
+      const float sb_ = kSbEarly ? sbn : (float)sbp[(int64_t)kphys(kb) * ssbk];               \
       cs[0] = lo_.x * sb_; cs[1] = lo_.y * sb_; cs[2] = lo_.z * sb_; cs[3] = lo_.w * sb_;     \
       cs[4] = hi_.x * sb_; cs[5] = hi_.y * sb_; cs[6] = hi_.z * sb_; cs[7] = hi_.w * sb_;     \
     }                                                                                         \
@@ -436,7 +436,7 @@ __device__ __forceinline__ void lds_barrier() {
   } while (0)
 // The 16 MFMAs of half H; before MFMA s, the scale-FMAs of MFMA s - 3 (for s < 3, of the
 // previous half's last m-tile, whose combined scale is cprev)
-#define CIN_PP_COMPUTE(H)                                                                     \
+#define CIN_PP_COMPUTE(H, SBL)                                                                \
   do {                                                                                        \
     __builtin_amdgcn_s_setprio(1);                                                            \
     _Pragma("unroll") for (int s_ = 0; s_ < 16; ++s_) {                                       \
@@ -452,6 +452,7 @@ __device__ __forceinline__ void lds_barrier() {
       asm volatile("" : "+v"(bf[s_ & 3]));                                                    \
       p[s_ & 3] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[s_ & 3], af[s_ >> 2], zero, 0, 0, 0, 0, 0, 0); \
       asm volatile("" : "+v"(bf[s_ & 3]));                                                    \
+      if (kSbEarly && (SBL) && s_ == 12) CIN_PP_SB_NEXT();                                    \
     }                                                                                         \
     cprev = cs[4 * (H) + 3];                                                                  \
     __builtin_amdgcn_s_setprio(0);                                                            \
@@ -460,7 +461,7 @@ __device__ __forceinline__ void lds_barrier() {
 // CIN_PP_COMPUTE(0) with the reads of half 1's A fragments of the same block interleaved:
 // A fragment q of half 1 right after MFMA 4q + 3, the last MFMA to read af[q].  (Reading the
 // next block's half 0 the same way under half 1 measured no faster.)
-#define CIN_PP_COMPUTE0_READ1(kbl)                                                            \
+#define CIN_PP_COMPUTE0_READ1(kbl, SBL)                                                       \
   do {                                                                                        \
     const int stgl_ = (kbl) & 1;                                                              \
     __builtin_amdgcn_s_setprio(1);                                                            \
@@ -481,10 +482,22 @@ __device__ __forceinline__ void lds_barrier() {
         asm volatile("" : "+v"(af[s_ >> 2]));                                                 \
         af[s_ >> 2] = CIN_AFRAG(stgl_, 4 + (s_ >> 2));                                        \
       }                                                                                       \
+      if (kSbEarly && (SBL) && s_ == 12) CIN_PP_SB_NEXT();                                    \
     }                                                                                         \
     cprev = cs[3];                                                                            \
     __builtin_amdgcn_s_setprio(0);                                                            \
   } while (0)
+
+// kSbEarly (a constant of the enclosing function): the next block's B-block scale (a scalar
+// load; the loop defines kb and more) is issued after MFMA 12 of the compute half that
+// precedes the block's barrier, where every fragment that half reads has been waited for and
+// the barrier's lgkmcnt(0) covers the load.  Otherwise it is loaded with the block's
+// fragments; scalar loads return out of order with LDS reads, so the wait before the scale
+// products is then lgkmcnt(0), behind every fragment read issued so far.  Early, on two
+// boxes: C2 100.5 -> 99.3 and 101.0 -> 100.4 us, C4 wgrad 108.1 -> 105.5 and 105.4 -> 105.7
+// us; in the persistent walks 0.7-1.1% slower (C3 gate/up, down), which keep the loads
+// together.
+#define CIN_PP_SB_NEXT() (sbn = sbp[(int64_t)kphys(more ? kb + 1 : kb) * ssbk])
 
 // The K loop of the ping-pong schedule and its drain, for a workgroup whose operands of
 // block 0 have landed (blocks 0 and 1 DMA'd by all eight waves, block 0 waited for and a
@@ -499,13 +512,14 @@ __device__ __forceinline__ void lds_barrier() {
   do {                                                                                              \
 /* each group runs its own copy of the K loop (the same barriers in the same order), so */          \
 /* the compiler sees one straight sequence of slots per wave */                                     \
+  float sbn = kSbEarly ? (float)sbp[(int64_t)kphys(0) * ssbk] : 0.0f;                              \
   if (grp == 0) {                                                                                   \
     CIN_PP_LOAD(0, 0);                                                                              \
     for (int kb = 0; kb < nk; ++kb) {                                                               \
       const int st = kb & 1;                                                                        \
       const bool more = kb < kl;                                                                    \
-      CIN_PP_COMPUTE0_READ1(kb);  /* slots A and B: half 1's A fragments read under half 0 */       \
-      CIN_PP_COMPUTE(1);  /* slot C: block kb's stage is read for the last time; kb+1 lands */      \
+      CIN_PP_COMPUTE0_READ1(kb, 0);  /* slots A and B: half 1's A fragments read under half 0 */    \
+      CIN_PP_COMPUTE(1, 1);  /* slot C: block kb's stage is read for the last time; kb+1 lands */   \
       wait_dma();                                                                                   \
       lds_barrier();                                                                                \
       if (more) {  /* slot D */                                                                     \
@@ -513,6 +527,8 @@ __device__ __forceinline__ void lds_barrier() {
         CIN_PP_LOAD(kb + 1, 0);                                                                     \
         if (kLoadsFirst && kb + 2 < nk) CIN_DMA_A4(kb + 2, st);                                     \
       }                                                                                             \
+      /* a use outside slot D, so the scale load is not sunk past the barrier into it */            \
+      if (kSbEarly) asm volatile("" ::"s"(sbn));                                                    \
     }                                                                                               \
   } else {                                                                                          \
     for (int kb = 0; kb < nk; ++kb) {                                                               \
@@ -521,10 +537,10 @@ __device__ __forceinline__ void lds_barrier() {
       if (!kLoadsFirst && kb >= 1 && more) CIN_DMA_B4(kb + 1, st ^ 1);  /* slot A */                \
       CIN_PP_LOAD(kb, 0);                                                                           \
       if (kLoadsFirst && kb >= 1 && more) CIN_DMA_B4(kb + 1, st ^ 1);                               \
-      CIN_PP_COMPUTE0_READ1(kb);  /* slots B and C */                                               \
+      CIN_PP_COMPUTE0_READ1(kb, 1);  /* slots B and C */                                            \
       wait_dma();                                                                                   \
       lds_barrier();                                                                                \
-      CIN_PP_COMPUTE(1);                                                                            \
+      CIN_PP_COMPUTE(1, 0);                                                                         \
     }                                                                                               \
   }                                                                                                 \
 /* drain: FMAs of the last half's MFMAs 13-15 (m-tile 7) */                                         \
@@ -647,6 +663,7 @@ __device__ __forceinline__ void tile_body(const Tile& T, int64_t lda, int64_t ss
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
   constexpr bool kLoadsFirst = false;
+  constexpr bool kSbEarly = true;
   v8i af[4], bf[4];
   float cs[8];
   float cprev = 0.0f;  // the "previous half" FMAs of the first half add 0 * 0
@@ -1303,6 +1320,7 @@ __device__ __forceinline__ void run_tiles(const Src& src, int64_t lda, int64_t s
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = zero;
     constexpr bool kLoadsFirst = true;
+    constexpr bool kSbEarly = false;
     v8i af[4], bf[4];
     float cs[8];
     float cprev = 0.0f;
