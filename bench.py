@@ -207,7 +207,7 @@ def config1_step(dev, steps):
     y = torch.empty(2048, 1024, dtype=torch.bfloat16, device=dev)
 
     def step(i):
-        a, sa, b, _, sb = kernels.quantize_fp8_forward(x, w)
+        a, sa, b, _, sb = kernels.quantize_fp8_forward(x, w, col_scales=True)
         kernels.fp8_gemm_bs(a, sa, b, sb, torch.bfloat16, out=y)
 
     dev_us = kernel_loop(step, max(steps, 50), 5)
@@ -515,7 +515,7 @@ def bwd_setup(dev, xs0, w0):
 
     g = torch.Generator(device=dev).manual_seed(4)
     dy = (torch.randn(M, N, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
-    xq, xs = kernels.quantize_fp8_rowwise(xs0)
+    xq, xs = kernels.quantize_fp8_rowwise(xs0, col_scales=True)
     _, wqt, ws = kernels.quantize_fp8_blockwise_t(w0.float(), with_rowmajor=False)
     return dict(dy=dy, xq=xq, xs=xs, wqt=wqt, ws=ws)
 
@@ -543,13 +543,14 @@ def main():
     del x
 
     # pre-quantized operands for the GEMM-only timing
-    xq, xsc = kernels.quantize_fp8_rowwise(xs[0])
+    xq, xsc = kernels.quantize_fp8_rowwise(xs[0], col_scales=True)
     wq, wsc = kernels.quantize_fp8_blockwise(ws[0])
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
 
     def step(i):
-        # X row tiles and W blocks in one launch (cin_quant_fwd), then the GEMM
-        a, sa, b, _, sb = kernels.quantize_fp8_forward(xs[i % nbuf], ws[i % nbuf])
+        # X row tiles and W blocks in one launch (cin_quant_fwd), then the GEMM; X's scales
+        # column-major, as the FP8 linear keeps them
+        a, sa, b, _, sb = kernels.quantize_fp8_forward(xs[i % nbuf], ws[i % nbuf], col_scales=True)
         kernels.fp8_gemm_bs(a, sa, b, sb, torch.bfloat16, out=y)
 
     def gemm(i):
@@ -569,7 +570,7 @@ def main():
         kernels.quantize_fp8_blockwise(ws[i % nbuf])
 
     def quant_fwd(i):
-        kernels.quantize_fp8_forward(xs[i % nbuf], ws[i % nbuf])
+        kernels.quantize_fp8_forward(xs[i % nbuf], ws[i % nbuf], col_scales=True)
 
     from cinnamon_amd import layers
 
@@ -771,20 +772,20 @@ def main():
 
     if full or args.only in ("dual_quant", "requant", "dgrad", "wgrad", "bwd_pair"):
         bwd = bwd_setup(dev, xs[0], ws[0])
-        gq, gs, gqt, gst = kernels.quantize_fp8_dual(bwd["dy"])
+        gq, gs, gqt, gst = kernels.quantize_fp8_dual(bwd["dy"], col_scales=True)
         xbt, xbs = kernels.requantize_rowwise_to_blockwise(bwd["xq"], bwd["xs"], transposed=True)
         dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
         dw = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
 
     def dual_quant(i):
-        kernels.quantize_fp8_dual(bwd["dy"])
+        kernels.quantize_fp8_dual(bwd["dy"], col_scales=True)
 
     def requant(i):
         kernels.requantize_rowwise_to_blockwise(bwd["xq"], bwd["xs"], transposed=True)
 
     def bwd_pair(i):
         # both quantizations above in one launch (FP8MatmulFunction.backward calls this)
-        kernels.quantize_fp8_backward(bwd["dy"], bwd["xq"], bwd["xs"])
+        kernels.quantize_fp8_backward(bwd["dy"], bwd["xq"], bwd["xs"], col_scales=True)
 
     def dgrad(i):
         kernels.fp8_gemm_bs(gq, gs, bwd["wqt"], bwd["ws"].t(), torch.bfloat16, out=dx)

@@ -25,31 +25,31 @@ _p, _i64, _i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
 # name -> argtypes (all return int)
 SIGNATURES: dict[str, list] = {
     "cin_abi_version": [],
-    "cin_quant_rowwise": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64, _p],
+    "cin_quant_rowwise": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64, _i64, _p],
     "cin_quant_blockwise": [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64,
                             _p, _i64, _p],
     "cin_dequant": [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _p, _i32, _i64, _p],
-    "cin_quant_fwd": [_p, _i32, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64, _p, _i32, _i64, _i64, _p, _i64,
-                      _p, _i64, _p, _i64, _p],
-    "cin_quant_dual": [_p, _i32, _i64, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _p,
-                       _i64, _p],
-    "cin_requant_row_to_block": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p],
-    "cin_quant_backward": [_p, _i32, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _p, _i64,
-                           _p, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p],
+    "cin_quant_fwd": [_p, _i32, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64, _i64, _p, _i32, _i64, _i64, _p,
+                      _i64, _p, _i64, _p, _i64, _p],
+    "cin_quant_dual": [_p, _i32, _i64, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64, _i64, _p, _i64, _p,
+                       _i64, _i64, _p],
+    "cin_requant_row_to_block": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p, _i64, _p, _i64, _p],
+    "cin_quant_backward": [_p, _i32, _i64, _i64, _i64, _i32, _p, _i64, _p, _i64, _i64, _p, _i64, _p,
+                           _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _p, _i64, _p],
     "cin_transpose_u8": [_p, _i64, _i64, _i64, _p, _i64, _p],
     "cin_gemm_fp8_bs": [_p, _i64, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _p,
                         _i32, _i64, _p],
     "cin_grouped_gemm_fp8": [_p, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i64, _p,
                              _p, _i64, _i64, _i64, _i64, _p, _i32, _i64, _p],
     "cin_quant_dual_grouped": [_p, _i32, _i64, _i64, _i64, _p, _p, _i64, _i32, _p, _i64, _p, _i64,
-                               _p, _i64, _p, _i64, _p],
-    "cin_requant_row_to_block_grouped": [_p, _i64, _i64, _i64, _p, _i64, _p, _p, _i64, _p, _i64,
-                                         _p, _i64, _p],
+                               _i64, _p, _i64, _p, _i64, _i64, _p],
+    "cin_requant_row_to_block_grouped": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p,
+                                         _i64, _p, _i64, _p],
     "cin_grouped_gemm_f16": [_p, _i32, _i64, _p, _i32, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64,
                              _p, _i64, _p],
-    "cin_grouped_gemm_fp8_wgrad": [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i64,
+    "cin_grouped_gemm_fp8_wgrad": [_p, _i64, _p, _i64, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _i64,
                                    _i64, _i64, _i64, _p, _i32, _i64, _i64, _p],
-    "cin_silu_mul_quant_rowwise": [_p, _i32, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p, _i64, _p],
+    "cin_silu_mul_quant_rowwise": [_p, _i32, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p, _i64, _i64, _p],
     "cin_swiglu_backward": [_p, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p],
     "cin_zero_rows_outside_ranges": [_p, _i64, _i64, _i64, _p, _p, _i64, _p],
     "cin_indexer_quantize": [_p, _i32, _p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p],
@@ -62,10 +62,10 @@ SIGNATURES: dict[str, list] = {
     "cin_moe_route_workspace": [_i64, _i64, _i64],
     "cin_moe_route_noalloc": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p],
     "cin_moe_gather_quant_rowwise": [_p, _i32, _i64, _i64, _i64, _p, _i64, _i64, _i32, _p, _i64, _p,
-                                     _i64, _p],
+                                     _i64, _i64, _p],
     "cin_moe_gather_sum": [_p, _i32, _i64, _p, _i64, _i64, _i64, _i64, _p, _i32, _i64, _p],
     "cin_moe_scatter_quant_rowwise": [_p, _i32, _i64, _i64, _i64, _p, _i64, _p, _i64, _i32, _p, _i64,
-                                      _p, _i64, _p],
+                                      _p, _i64, _i64, _p],
     "cin_moe_combine": [_p, _i32, _i64, _p, _i32, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "cin_moe_combine_backward": [_p, _i64, _p, _i32, _i64, _p, _i32, _i64, _p, _p, _i64, _i64, _i64,
                                  _i64, _p, _i32, _i64, _p, _p],

@@ -794,7 +794,7 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_gemm_fp8_256(
 // columns hold code 0.  An expert without tokens gets dW_e = 0.
 __global__ __launch_bounds__(kThreads, 2) void k_grouped_wgrad_fp8_256(
     const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
-    const uint8_t* __restrict__ B, int64_t ldb, const float* __restrict__ sb, int64_t ssbm,
+    int64_t ssak, const uint8_t* __restrict__ B, int64_t ldb, const float* __restrict__ sb, int64_t ssbm,
     const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t Tn, int64_t tcap,
     int64_t M, int64_t N, void* C, int c_dtype, int64_t ldc, int64_t sce, uint32_t tiles_m,
     uint32_t tiles_n, uint32_t ntot) {
@@ -848,14 +848,14 @@ __global__ __launch_bounds__(kThreads, 2) void k_grouped_wgrad_fp8_256(
   }
   Tile t;
   t.A = A + m0 * lda + p;
-  t.sa = sa + m0 * ssam + p / TK;
+  t.sa = sa + m0 * ssam + (p / TK) * ssak;
   t.B = B + n0 * ldb + p;
   t.sb = sb + (p / TK) * ssbm + (n0 >> 7);
   t.C = Ce;
   t.row_lo = row_lo;
   t.row_hi = TM;
   t.col_lo = col_lo;
-  tile_body(t, lda, ssam, 1, ldb, 1, ssbm, (int64_t)nk * TK, c_dtype, ldc);
+  tile_body(t, lda, ssam, ssak, ldb, 1, ssbm, (int64_t)nk * TK, c_dtype, ldc);
 }
 
 }  // namespace big
@@ -1470,7 +1470,7 @@ static_assert(kMaxWgradExperts <= kThreads, "the wgrad's LDS tables give each th
 
 struct WgradSrc {
   const uint8_t* A; const float* sa; const uint8_t* B; const float* sb; uint8_t* C;
-  int64_t lda, ssam, ldb, ssbm, ldc, sce, M, N;
+  int64_t lda, ssam, ssak, ldb, ssbm, ldc, sce, M, N;
   int es;
   uint32_t tiles_m, tiles_n, G, total;  // total = tiles of the experts with tokens
   const int* order;    // experts with tokens, most K blocks first
@@ -1496,7 +1496,7 @@ struct WgradSrc {
     const int64_t m0 = m_nom + TM <= M ? m_nom : M - TM;
     const int64_t n0 = n_nom + TN <= N ? n_nom : N - TN;
     t.A = A + m0 * lda + p;
-    t.sa = sa + m0 * ssam + p / TK;
+    t.sa = sa + m0 * ssam + (p / TK) * ssak;
     t.B = B + n0 * ldb + p;
     t.sb = sb + (p / TK) * ssbm + (n0 >> 7);
     t.C = C + ((int64_t)e * sce + m0 * ldc + n0) * es;
@@ -1511,7 +1511,7 @@ struct WgradSrc {
 template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad_fp8_pers(
     const uint8_t* __restrict__ A, int64_t lda, const float* __restrict__ sa, int64_t ssam,
-    const uint8_t* __restrict__ B, int64_t ldb, const float* __restrict__ sb, int64_t ssbm,
+    int64_t ssak, const uint8_t* __restrict__ B, int64_t ldb, const float* __restrict__ sb, int64_t ssbm,
     const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int E, int64_t Tn,
     int64_t tcap, int64_t M, int64_t N, void* C, int c_dtype, int64_t ldc, int64_t sce,
     uint32_t tiles_m, uint32_t tiles_n) {
@@ -1576,12 +1576,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad_fp8_pers(
   }
   WgradSrc src;
   src.A = A; src.sa = sa; src.B = B; src.sb = sb; src.C = static_cast<uint8_t*>(C);
-  src.lda = lda; src.ssam = ssam; src.ldb = ldb; src.ssbm = ssbm; src.ldc = ldc; src.sce = sce;
+  src.lda = lda; src.ssam = ssam; src.ssak = ssak; src.ldb = ldb; src.ssbm = ssbm; src.ldc = ldc; src.sce = sce;
   src.M = M; src.N = N; src.es = c_dtype == CIN_DT_F32 ? 4 : 2;
   src.tiles_m = tiles_m; src.tiles_n = tiles_n; src.G = gridDim.x;
   src.total = (uint32_t)nz * tiles_m * tiles_n;
   src.order = order; src.enk = enk; src.poff = poff;
-  run_tiles<EPI, WgradSrc, true>(src, lda, ssam, 1, ldb, 1, ssbm, 0, c_dtype, ldc);
+  run_tiles<EPI, WgradSrc, true>(src, lda, ssam, ssak, ldb, 1, ssbm, 0, c_dtype, ldc);
 }
 
 }  // namespace pers
@@ -1748,7 +1748,7 @@ int cin_grouped_gemm_fp8(const uint8_t* A, int64_t lda, const float* sa, int64_t
 }
 
 int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam,
-                               const uint8_t* B, int64_t ldb, const float* sb, int64_t ssbm,
+                               int64_t ssak, const uint8_t* B, int64_t ldb, const float* sb, int64_t ssbm,
                                const int64_t* starts, const int64_t* ends, int64_t E, int64_t T,
                                int64_t tcap, int64_t N, int64_t K, void* C, int c_dtype, int64_t ldc,
                                int64_t sce, void* stream) {
@@ -1762,12 +1762,13 @@ int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, i
                 (long long)N, (long long)K);
   CIN_CHECK_ARG(lda % 16 == 0 && ldb % 16 == 0 && aligned16(A) && aligned16(B),
                 "grouped_wgrad_fp8: A/B rows must be 16-byte aligned");
-  CIN_CHECK_ARG(tcap >= 0 && tcap <= lda && tcap <= ldb && tcap <= ssam * 128 &&
-                    (ssam == 0 || tcap / 128 <= ssam),
-                "grouped_wgrad_fp8: padded capacity exceeds the operand rows");
+  // A's scales [N, tcap / 128]: row-major (ssak == 1) or column-major (ssam == 1)
+  const bool sa_ok = (ssak == 1 && ssam >= tcap / 128) || (ssam == 1 && ssak >= N);
+  CIN_CHECK_ARG(tcap >= 0 && tcap <= lda && tcap <= ldb && sa_ok,
+                "grouped_wgrad_fp8: padded capacity exceeds the operand rows, or A-scale strides overlap");
   CIN_CHECK_ARG(ldc >= K && sce >= N * ldc, "grouped_wgrad_fp8: bad C strides");
   CIN_CHECK_ARG(ssbm >= K / 128, "grouped_wgrad_fp8: bad B-scale stride");
-  CIN_CHECK_ARG(big_offsets_fit(lda, ldb, tcap, ssam, 1),
+  CIN_CHECK_ARG(big_offsets_fit(lda, ldb, tcap, ssam, ssak),
                 "grouped_wgrad_fp8: operand rows too long for the 256 x 256 tile's 32-bit offsets");
   const int64_t tm = cdiv(N, big::TM), tn = cdiv(K, big::TN);
   CIN_CHECK_ARG(E * tm * tn < ((int64_t)1 << 31), "grouped_wgrad_fp8: grid too large");
@@ -1778,8 +1779,8 @@ int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, i
     const unsigned ncu = (unsigned)device_cus();
 #define CIN_LAUNCH_WGRAD_PERS(EPI_)                                                                   \
   hipLaunchKernelGGL(pers::k_grouped_wgrad_fp8_pers<EPI_>, ncu, big::kThreads, 0,                       \
-                     static_cast<hipStream_t>(stream), A, lda, sa, ssam, B, ldb, sb, ssbm, starts, ends, \
-                     (int)E, T, tcap, N, K, C, c_dtype, ldc, sce, (uint32_t)tm, (uint32_t)tn)
+                     static_cast<hipStream_t>(stream), A, lda, sa, ssam, ssak, B, ldb, sb, ssbm, starts,   \
+                     ends, (int)E, T, tcap, N, K, C, c_dtype, ldc, sce, (uint32_t)tm, (uint32_t)tn)
     const int epi = pers_epi(c_dtype, C, ldc, sce);
     if (epi == pers::kEpiCounted16x4)
       CIN_LAUNCH_WGRAD_PERS(pers::kEpiCounted16x4);
@@ -1793,7 +1794,7 @@ int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, i
     return cin_check_launch("grouped_wgrad_fp8");
   }
   hipLaunchKernelGGL(big::k_grouped_wgrad_fp8_256, ntot, big::kThreads, 0,
-                     static_cast<hipStream_t>(stream), A, lda, sa, ssam, B, ldb, sb, ssbm, starts,
+                     static_cast<hipStream_t>(stream), A, lda, sa, ssam, ssak, B, ldb, sb, ssbm, starts,
                      ends, T, tcap, N, K, C, c_dtype, ldc, sce, (uint32_t)tm, (uint32_t)tn, ntot);
   return cin_check_launch("grouped_wgrad_fp8");
 }

@@ -123,8 +123,9 @@ template <int DT, int LANES, int U, bool FULL, int MAP = kMapNone>
 __device__ __forceinline__ void rowwise128_body(uint32_t bid, uint32_t nblk, const void* __restrict__ x,
                                                 int64_t N, int64_t sxm, int round_scale,
                                                 uint8_t* __restrict__ q, int64_t sqm,
-                                                float* __restrict__ sc, int64_t ssm, uint32_t nb,
-                                                uint32_t ntiles, const void* __restrict__ rowmap,
+                                                float* __restrict__ sc, int64_t ssm, int64_t ssk,
+                                                uint32_t nb, uint32_t ntiles,
+                                                const void* __restrict__ rowmap,
                                                 int64_t rowdiv, int64_t src_rows) {
   constexpr int ES = DT == CIN_DT_F32 ? 4 : 2;  // input element bytes
   constexpr int EPC = 16 / ES;                   // elements per 16-byte chunk
@@ -239,7 +240,7 @@ __device__ __forceinline__ void rowwise128_body(uint32_t bid, uint32_t nblk, con
           if constexpr (MAP == kMapFirstScale) {
             if (cbs[u] == 0) sc[orow * ssm] = s;
           } else {
-            sc[orow * ssm + cbs[u]] = s;
+            sc[orow * ssm + (int64_t)cbs[u] * ssk] = s;
           }
         }
       }
@@ -252,39 +253,39 @@ __global__ __launch_bounds__(kThreads) void k_rowwise128(const void* __restrict_
                                                          int64_t sxm, int round_scale,
                                                          uint8_t* __restrict__ q, int64_t sqm,
                                                          float* __restrict__ sc, int64_t ssm,
-                                                         uint32_t nb, uint32_t ntiles,
+                                                         int64_t ssk, uint32_t nb, uint32_t ntiles,
                                                          const void* __restrict__ rowmap = nullptr,
                                                          int64_t rowdiv = 1, int64_t src_rows = 0) {
   rowwise128_body<DT, LANES, U, FULL, MAP>(blockIdx.x, gridDim.x, x, N, sxm, round_scale, q, sqm, sc,
-                                           ssm, nb, ntiles, rowmap, rowdiv, src_rows);
+                                           ssm, ssk, nb, ntiles, rowmap, rowdiv, src_rows);
 }
 
 template <int LANES, int U, bool FULL, int MAP = kMapNone>
 void launch_rowwise128_t(const void* x, int dt, int64_t N, int64_t sxm, int rs, uint8_t* q,
-                         int64_t sqm, float* sc, int64_t ssm, uint32_t nb, uint32_t ntiles,
+                         int64_t sqm, float* sc, int64_t ssm, int64_t ssk, uint32_t nb, uint32_t ntiles,
                          unsigned grid, hipStream_t st, const void* rowmap = nullptr,
                          int64_t rowdiv = 1, int64_t src_rows = 0) {
   if (dt == CIN_DT_BF16)
     hipLaunchKernelGGL((k_rowwise128<CIN_DT_BF16, LANES, U, FULL, MAP>), grid, kThreads, 0, st,
-                       x, N, sxm, rs, q, sqm, sc, ssm, nb, ntiles, rowmap, rowdiv, src_rows);
+                       x, N, sxm, rs, q, sqm, sc, ssm, ssk, nb, ntiles, rowmap, rowdiv, src_rows);
   else if (dt == CIN_DT_F16)
     hipLaunchKernelGGL((k_rowwise128<CIN_DT_F16, LANES, U, FULL, MAP>), grid, kThreads, 0, st,
-                       x, N, sxm, rs, q, sqm, sc, ssm, nb, ntiles, rowmap, rowdiv, src_rows);
+                       x, N, sxm, rs, q, sqm, sc, ssm, ssk, nb, ntiles, rowmap, rowdiv, src_rows);
   else
     hipLaunchKernelGGL((k_rowwise128<CIN_DT_F32, LANES, U, FULL, MAP>), grid, kThreads, 0, st,
-                       x, N, sxm, rs, q, sqm, sc, ssm, nb, ntiles, rowmap, rowdiv, src_rows);
+                       x, N, sxm, rs, q, sqm, sc, ssm, ssk, nb, ntiles, rowmap, rowdiv, src_rows);
 }
 
 template <int LANES, int U>
 void launch_rowwise128(const void* x, int dt, int64_t M, int64_t N, int64_t sxm, int rs,
-                       uint8_t* q, int64_t sqm, float* sc, int64_t ssm, int64_t nb, int gridcap,
-                       hipStream_t st) {
+                       uint8_t* q, int64_t sqm, float* sc, int64_t ssm, int64_t ssk, int64_t nb,
+                       int gridcap, hipStream_t st) {
   const uint32_t ntiles = (uint32_t)(M * nb);
   const unsigned grid = grid_for(ntiles, (kThreads / LANES) * U, gridcap);
   if (N % 128 == 0)
-    launch_rowwise128_t<LANES, U, true>(x, dt, N, sxm, rs, q, sqm, sc, ssm, (uint32_t)nb, ntiles, grid, st);
+    launch_rowwise128_t<LANES, U, true>(x, dt, N, sxm, rs, q, sqm, sc, ssm, ssk, (uint32_t)nb, ntiles, grid, st);
   else
-    launch_rowwise128_t<LANES, U, false>(x, dt, N, sxm, rs, q, sqm, sc, ssm, (uint32_t)nb, ntiles, grid, st);
+    launch_rowwise128_t<LANES, U, false>(x, dt, N, sxm, rs, q, sqm, sc, ssm, ssk, (uint32_t)nb, ntiles, grid, st);
 }
 
 // Generic row-wise: one wave per (row, tile), any block size / strides / dtype.
@@ -293,7 +294,7 @@ __global__ __launch_bounds__(kThreads) void k_rowwise_generic(const void* __rest
                                                               int64_t sxn, int64_t block,
                                                               int round_scale, uint8_t* q,
                                                               int64_t sqm, float* sc, int64_t ssm,
-                                                              int64_t nb) {
+                                                              int64_t ssk, int64_t nb) {
   const int lane = threadIdx.x & 63;
   const int64_t w = ((int64_t)blockIdx.x * kThreads + threadIdx.x) >> 6;
   const int64_t W = ((int64_t)gridDim.x * kThreads) >> 6;
@@ -311,7 +312,7 @@ __global__ __launch_bounds__(kThreads) void k_rowwise_generic(const void* __rest
       float y = clamp448(load_elem(x, dt, row * sxm + c * sxn) / s);
       q[row * sqm + c] = (uint8_t)cvt2_e4m3(y, 0.0f);
     }
-    if (lane == 0) sc[row * ssm + cb] = s;
+    if (lane == 0) sc[row * ssm + cb * ssk] = s;
   }
 }
 
@@ -910,7 +911,7 @@ constexpr int kFwdXU = 2;
 template <int XDT, int WDT>
 __global__ __launch_bounds__(kThreads, 4) void k_quant_fwd(
     const void* __restrict__ x, int64_t xN, int64_t sxm, int xrs, uint8_t* xq, int64_t sxqm, float* xsc,
-    int64_t sxsm, uint32_t xnb, uint32_t xtiles, const void* __restrict__ w, int64_t wM, int64_t wN,
+    int64_t sxsm, int64_t sxsk, uint32_t xnb, uint32_t xtiles, const void* __restrict__ w, int64_t wM, int64_t wN,
     int64_t swm, uint8_t* wq, int64_t swqm, uint8_t* wqt, int64_t swqtm, int wvec_t, float* wsc,
     int64_t swsm, uint32_t wnbc, uint32_t wtiles, uint32_t gw) {
   static_assert(WDT != CIN_DT_F32, "16-bit W only");
@@ -924,7 +925,7 @@ __global__ __launch_bounds__(kThreads, 4) void k_quant_fwd(
         });
   } else {
     rowwise128_body<XDT, 8, kFwdXU, true, kMapNone>(blockIdx.x - gw, gridDim.x - gw, x, xN, sxm, xrs, xq, sxqm,
-                                               xsc, sxsm, xnb, xtiles, nullptr, 1, 0);
+                                               xsc, sxsm, sxsk, xnb, xtiles, nullptr, 1, 0);
   }
 }
 
@@ -943,8 +944,8 @@ struct DualSmem {
 template <int DT, bool EDGE>
 __device__ __forceinline__ void dual_body(RawIn<DT>& raw, const TileGeo& g, int64_t N, bool rs,
                                           uint8_t* q, int64_t sqm, float* s, int64_t ssm,
-                                          uint8_t* qt, int64_t sqtm, bool vec_t, float* st,
-                                          int64_t sstm, DualSmem& sm) {
+                                          int64_t ssk, uint8_t* qt, int64_t sqtm, bool vec_t,
+                                          float* st, int64_t sstm, int64_t sstk, DualSmem& sm) {
   constexpr int NW = (int)(sizeof(raw.w[0]) / sizeof(raw.w[0][0]));
   const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
   const float floor_v = amax_floor(DT);
@@ -989,7 +990,7 @@ __device__ __forceinline__ void dual_body(RawIn<DT>& raw, const TileGeo& g, int6
       out.put(i, w);
     }
     const int ro = rg * 8 + (lane16 & 7);
-    if (lane16 < 8 && ro < g.nr) s[(g.r0 + ro) * ssm + g.cb] = own;
+    if (lane16 < 8 && ro < g.nr) s[(g.r0 + ro) * ssm + (int64_t)g.cb * ssk] = own;
   }
   __syncthreads();
   if (threadIdx.x < 128) {
@@ -1000,7 +1001,7 @@ __device__ __forceinline__ void dual_body(RawIn<DT>& raw, const TileGeo& g, int6
     sm.coldiv[threadIdx.x] = divisor(sc);
     sm.colrcp[threadIdx.x] = 1.0f / sc;
     const int64_t n = (int64_t)g.cb * 128 + threadIdx.x;
-    if (!EDGE || n < N) st[n * sstm + (g.t0 >> 7)] = sc;
+    if (!EDGE || n < N) st[n * sstm + (int64_t)(g.t0 >> 7) * sstk] = sc;
   }
   __syncthreads();
   {
@@ -1031,12 +1032,13 @@ __device__ __forceinline__ void dual_body(RawIn<DT>& raw, const TileGeo& g, int6
 template <int DT, bool EDGE, typename Geo>
 __device__ __forceinline__ void dual_run(Geo& geo, uint32_t ntiles, const void* __restrict__ x,
                                          int64_t N, int64_t sxm, bool rs, uint8_t* q, int64_t sqm,
-                                         float* s, int64_t ssm, uint8_t* qt, int64_t sqtm, bool vec_t,
-                                         float* st, int64_t sstm, DualSmem& sm) {
+                                         float* s, int64_t ssm, int64_t ssk, uint8_t* qt, int64_t sqtm,
+                                         bool vec_t, float* st, int64_t sstm, int64_t sstk,
+                                         DualSmem& sm) {
   auto ld = [&](const TileGeo& g, RawIn<DT>& r) { load_in<DT, EDGE>(x, sxm, N, g, r); };
   auto pr = [&](const TileGeo& g, RawIn<DT>& r) {
     if (g.nr == 0) return;  // uniform over the workgroup
-    dual_body<DT, EDGE>(r, g, N, rs, q, sqm, s, ssm, qt, sqtm, vec_t, st, sstm, sm);
+    dual_body<DT, EDGE>(r, g, N, rs, q, sqm, s, ssm, ssk, qt, sqtm, vec_t, st, sstm, sstk, sm);
   };
   // fp32: one register set at 3 waves per SIMD (two sets hold it to 2); measured 2-8%
   // faster, and 4 waves per SIMD slower on large inputs
@@ -1050,13 +1052,14 @@ template <int DT, bool EDGE>
 __global__ __launch_bounds__(kThreads, (DT == CIN_DT_F32 && !EDGE) ? 3 : 1) void k_dual128(const void* __restrict__ x, int64_t M,
                                                       int64_t N, int64_t sxm, int round_scale,
                                                       uint8_t* q, int64_t sqm, float* s,
-                                                      int64_t ssm, uint8_t* qt, int64_t sqtm,
-                                                      int vec_t, float* st, int64_t sstm,
-                                                      uint32_t nbc, uint32_t cb0, uint32_t ntiles) {
+                                                      int64_t ssm, int64_t ssk, uint8_t* qt,
+                                                      int64_t sqtm, int vec_t, float* st,
+                                                      int64_t sstm, int64_t sstk, uint32_t nbc,
+                                                      uint32_t cb0, uint32_t ntiles) {
   __shared__ DualSmem sm;
   DenseTiles geo{M, nbc, cb0};
-  dual_run<DT, EDGE>(geo, ntiles, x, N, sxm, round_scale != 0, q, sqm, s, ssm, qt, sqtm, vec_t != 0,
-                     st, sstm, sm);
+  dual_run<DT, EDGE>(geo, ntiles, x, N, sxm, round_scale != 0, q, sqm, s, ssm, ssk, qt, sqtm,
+                     vec_t != 0, st, sstm, sstk, sm);
 }
 
 // Grouped: tiles are 128-token chunks of the experts (cin_grouped.h).  Rows outside
@@ -1064,13 +1067,13 @@ __global__ __launch_bounds__(kThreads, (DT == CIN_DT_F32 && !EDGE) ? 3 : 1) void
 template <int DT, bool EDGE>
 __global__ __launch_bounds__(kThreads, (DT == CIN_DT_F32 && !EDGE) ? 3 : 1) void k_dual128_grouped(
     const void* __restrict__ x, int64_t T, int64_t N, int64_t sxm, int round_scale, uint8_t* q,
-    int64_t sqm, float* s, int64_t ssm, uint8_t* qt, int64_t sqtm, int vec_t, float* st,
-    int64_t sstm, const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t E,
-    int64_t tcap, uint32_t nbc, uint32_t cb0, uint32_t ntiles) {
+    int64_t sqm, float* s, int64_t ssm, int64_t ssk, uint8_t* qt, int64_t sqtm, int vec_t, float* st,
+    int64_t sstm, int64_t sstk, const int64_t* __restrict__ starts, const int64_t* __restrict__ ends,
+    int64_t E, int64_t tcap, uint32_t nbc, uint32_t cb0, uint32_t ntiles) {
   __shared__ DualSmem sm;
   GroupedTiles geo = grouped_tiles(starts, ends, E, T, tcap, nbc, cb0);
-  dual_run<DT, EDGE>(geo, ntiles, x, N, sxm, round_scale != 0, q, sqm, s, ssm, qt, sqtm, vec_t != 0,
-                     st, sstm, sm);
+  dual_run<DT, EDGE>(geo, ntiles, x, N, sxm, round_scale != 0, q, sqm, s, ssm, ssk, qt, sqtm,
+                     vec_t != 0, st, sstm, sstk, sm);
 }
 
 // ----------------------------- row -> block re-quantization -----------------------------
@@ -1084,14 +1087,14 @@ struct RawQ {
 
 template <bool EDGE>
 __device__ __forceinline__ void load_q(const uint8_t* __restrict__ q, int64_t sqm, int64_t K,
-                                       const float* __restrict__ srow, int64_t ssm,
+                                       const float* __restrict__ srow, int64_t ssm, int64_t ssk,
                                        const TileGeo& g, RawQ& o) {
   const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
   if constexpr (!EDGE) {
     const __amdgpu_buffer_rsrc_t r =
         make_rsrc(q + g.r0 * sqm + (int64_t)g.cb * 128, tile_extent(g.nr, sqm, 1));
     const __amdgpu_buffer_rsrc_t rsc =
-        make_rsrc(srow + g.r0 * ssm + g.cb, g.nr > 0 ? ((int64_t)(g.nr - 1) * ssm + 1) * 4 : 0);
+        make_rsrc(srow + g.r0 * ssm + (int64_t)g.cb * ssk, g.nr > 0 ? ((int64_t)(g.nr - 1) * ssm + 1) * 4 : 0);
     const uint32_t v0 = (uint32_t)(rg * 8) * (uint32_t)sqm + (uint32_t)(lane16 * 8);
     const uint32_t s0 = (uint32_t)(rg * 8) * (uint32_t)(ssm * 4);
 #pragma unroll
@@ -1110,7 +1113,7 @@ __device__ __forceinline__ void load_q(const uint8_t* __restrict__ q, int64_t sq
       const int ri = rg * 8 + i;
       const bool rok = ri < g.nr;
       const int64_t row = g.r0 + (ri < lastr ? ri : lastr);
-      const float sv = srow[row * ssm + g.cb];
+      const float sv = srow[row * ssm + (int64_t)g.cb * ssk];
       o.sr[i] = rok ? sv : 0.0f;
       o.w[i][0] = o.w[i][1] = 0u;
 #pragma unroll
@@ -1195,7 +1198,7 @@ __device__ __forceinline__ void requant_body(RawQ& raw, const TileGeo& g, int64_
 template <bool EDGE, typename Geo>
 __device__ __forceinline__ void requant_run(Geo& geo, uint32_t ntiles, const uint8_t* __restrict__ q,
                                             int64_t K, int64_t sqm, const float* __restrict__ srow,
-                                            int64_t ssm, uint8_t* qb, int64_t sqbm, uint8_t* qbt,
+                                            int64_t ssm, int64_t ssk, uint8_t* qb, int64_t sqbm, uint8_t* qbt,
                                             int64_t sqbtm, bool vec_t, float* sblk, int64_t ssbm,
                                             RequantSmem& sm) {
   // One register set: without the second the dense kernel holds 5 waves per SIMD (96
@@ -1203,7 +1206,7 @@ __device__ __forceinline__ void requant_run(Geo& geo, uint32_t ntiles, const uin
   // loads.  Measured on config-4 X: 27.8 against 30.9 us with two sets at 4 waves; the
   // grouped kernel (more geometry in registers) at 4 waves: 454 against 463 us on config 3.
   tile_loop_single<RawQ>(
-      ntiles, geo, [&](const TileGeo& g, RawQ& r) { load_q<EDGE>(q, sqm, K, srow, ssm, g, r); },
+      ntiles, geo, [&](const TileGeo& g, RawQ& r) { load_q<EDGE>(q, sqm, K, srow, ssm, ssk, g, r); },
       [&](const TileGeo& g, RawQ& r) {
         if (g.nr == 0) return;  // uniform over the workgroup
         requant_body<EDGE>(r, g, K, qb, sqbm, qbt, sqbtm, vec_t, sblk, ssbm, sm);
@@ -1214,15 +1217,15 @@ template <bool EDGE>
 __global__ __launch_bounds__(kThreads, 5) void k_requant128(const uint8_t* __restrict__ q, int64_t M,
                                                          int64_t K, int64_t sqm,
                                                          const float* __restrict__ srow,
-                                                         int64_t ssm, uint8_t* qb, int64_t sqbm,
+                                                         int64_t ssm, int64_t ssk, uint8_t* qb, int64_t sqbm,
                                                          uint8_t* qbt, int64_t sqbtm, int vec_t,
                                                          float* sblk, int64_t ssbm, uint32_t nbc,
                                                          uint32_t cb0, uint32_t ntiles) {
   __shared__ RequantSmem sm;
   (void)nbc;
   DenseTilesCM geo{M, (uint32_t)((M + 127) >> 7), cb0};
-  requant_run<EDGE>(geo, ntiles, q, K, sqm, srow, ssm, qb, sqbm, qbt, sqbtm, vec_t != 0, sblk, ssbm,
-                    sm);
+  requant_run<EDGE>(geo, ntiles, q, K, sqm, srow, ssm, ssk, qb, sqbm, qbt, sqbtm, vec_t != 0, sblk,
+                    ssbm, sm);
 }
 
 // Grouped: tiles are 128-token chunks of the experts; block scales are indexed by the
@@ -1230,13 +1233,13 @@ __global__ __launch_bounds__(kThreads, 5) void k_requant128(const uint8_t* __res
 template <bool EDGE>
 __global__ __launch_bounds__(kThreads) void k_requant128_grouped(
     const uint8_t* __restrict__ q, int64_t T, int64_t K, int64_t sqm, const float* __restrict__ srow,
-    int64_t ssm, uint8_t* qb, int64_t sqbm, uint8_t* qbt, int64_t sqbtm, int vec_t, float* sblk,
+    int64_t ssm, int64_t ssk, uint8_t* qb, int64_t sqbm, uint8_t* qbt, int64_t sqbtm, int vec_t, float* sblk,
     int64_t ssbm, const int64_t* __restrict__ starts, const int64_t* __restrict__ ends, int64_t E,
     int64_t tcap, uint32_t nbc, uint32_t cb0, uint32_t ntiles) {
   __shared__ RequantSmem sm;
   GroupedTiles geo = grouped_tiles(starts, ends, E, T, tcap, nbc, cb0);
-  requant_run<EDGE>(geo, ntiles, q, K, sqm, srow, ssm, qb, sqbm, qbt, sqbtm, vec_t != 0, sblk, ssbm,
-                    sm);
+  requant_run<EDGE>(geo, ntiles, q, K, sqm, srow, ssm, ssk, qb, sqbm, qbt, sqbtm, vec_t != 0, sblk,
+                    ssbm, sm);
 }
 
 // ----------------------------- backward pair in one launch -----------------------------
@@ -1256,9 +1259,9 @@ union BwdSmem {
 template <int DT>
 __global__ __launch_bounds__(kThreads, 5) void k_quant_bwd(
     const void* __restrict__ dy, int64_t M, int64_t N, int64_t sdm, int round_scale, uint8_t* q,
-    int64_t sqm, float* s, int64_t ssm, uint8_t* qt, int64_t sqtm, int dvec_t, float* st, int64_t sstm,
-    const uint8_t* __restrict__ xq, int64_t K, int64_t sxqm, const float* __restrict__ srow,
-    int64_t ssrm, uint8_t* xbt, int64_t sxbtm, int rvec_t, float* sblk, int64_t ssbm, uint32_t nd,
+    int64_t sqm, float* s, int64_t ssm, int64_t ssk, uint8_t* qt, int64_t sqtm, int dvec_t, float* st,
+    int64_t sstm, int64_t sstk, const uint8_t* __restrict__ xq, int64_t K, int64_t sxqm,
+    const float* __restrict__ srow, int64_t ssrm, int64_t ssrk, uint8_t* xbt, int64_t sxbtm, int rvec_t, float* sblk, int64_t ssbm, uint32_t nd,
     uint32_t ntiles) {
   static_assert(DT != CIN_DT_F32, "the pair launch takes 16-bit dY");
   __shared__ BwdSmem sm;
@@ -1270,7 +1273,8 @@ __global__ __launch_bounds__(kThreads, 5) void k_quant_bwd(
       dgeo(t, g);
       RawIn<DT> r;
       load_in<DT, false>(dy, sdm, N, g, r);
-      dual_body<DT, false>(r, g, N, round_scale != 0, q, sqm, s, ssm, qt, sqtm, dvec_t != 0, st, sstm, sm.d);
+      dual_body<DT, false>(r, g, N, round_scale != 0, q, sqm, s, ssm, ssk, qt, sqtm, dvec_t != 0, st, sstm,
+                           sstk, sm.d);
     }
   }
   __syncthreads();  // the union's other member: every thread is past its dual tiles
@@ -1279,7 +1283,7 @@ __global__ __launch_bounds__(kThreads, 5) void k_quant_bwd(
     TileGeo g;
     rgeo(t - nd, g);
     RawQ r;
-    load_q<false>(xq, sxqm, K, srow, ssrm, g, r);
+    load_q<false>(xq, sxqm, K, srow, ssrm, ssrk, g, r);
     requant_body<false>(r, g, K, nullptr, 0, xbt, sxbtm, rvec_t != 0, sblk, ssbm, sm.r);
   }
 }
@@ -1361,7 +1365,7 @@ __device__ __forceinline__ float round_to(float h) {
 template <int IT, int OT>
 __global__ __launch_bounds__(kThreads) void k_silu_mul_rowwise128(
     const void* __restrict__ h12, int64_t s12, int64_t H, int round_scale, uint8_t* __restrict__ q,
-    int64_t sqm, float* __restrict__ sc, int64_t ssm, uint32_t nb, uint32_t ntiles) {
+    int64_t sqm, float* __restrict__ sc, int64_t ssm, int64_t ssk, uint32_t nb, uint32_t ntiles) {
   const int li = threadIdx.x & 15;
   const uint32_t G = (gridDim.x * kThreads) / 16;
   const bool rs = round_scale != 0;
@@ -1392,7 +1396,7 @@ __global__ __launch_bounds__(kThreads) void k_silu_mul_rowwise128(
     } else {
       for (int j = 0; j < nv; ++j) qp[j] = (uint8_t)((w[j >> 2] >> (8 * (j & 3))) & 0xffu);
     }
-    if (li == 0) sc[(int64_t)row * ssm + cb] = sv;
+    if (li == 0) sc[(int64_t)row * ssm + (int64_t)cb * ssk] = sv;
   }
 }
 
@@ -1488,15 +1492,26 @@ unsigned resident_grid(uint32_t ntiles) {
 __global__ __launch_bounds__(kThreads) void k_zero_unrouted(const int64_t* __restrict__ perm,
                                                             int64_t rows, int64_t N, int dt,
                                                             int round_scale, uint8_t* q,
-                                                            int64_t sqm, float* sc, int64_t ssm) {
+                                                            int64_t sqm, float* sc, int64_t ssm,
+                                                            int64_t ssk) {
   const int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (r >= rows || perm[r] >= 0) return;
   const float s = compute_scale(amax_floor(dt), round_scale != 0);
-  for (int64_t b = 0; b < (N + 127) / 128; ++b) sc[r * ssm + b] = s;
+  for (int64_t b = 0; b < (N + 127) / 128; ++b) sc[r * ssm + b * ssk] = s;
   uint8_t* p = q + r * sqm;  // 8-byte aligned (q and sqm are)
   int64_t c = 0;
   for (; c + 8 <= N; c += 8) *reinterpret_cast<uint2*>(p + c) = make_uint2(0u, 0u);
   for (; c < N; ++c) p[c] = 0;
+}
+
+// An R x C matrix of scales at strides (sr, sc) whose elements do not overlap: row-major
+// (sc == 1, sr >= C) or column-major (sr == 1, sc >= R); a single row or column takes any
+// positive stride.
+inline bool scale_layout_ok(int64_t R, int64_t C, int64_t sr, int64_t sc) {
+  if (R <= 1 && C <= 1) return true;
+  if (R <= 1) return sc >= 1;
+  if (C <= 1) return sr >= 1;
+  return (sc == 1 && sr >= C) || (sr == 1 && sc >= R);
 }
 
 }  // namespace
@@ -1505,7 +1520,7 @@ extern "C" {
 
 int cin_quant_rowwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t sxm, int64_t sxn,
                       int64_t block, int round_scale, uint8_t* q, int64_t sqm, float* scales,
-                      int64_t ssm, void* stream) {
+                      int64_t ssm, int64_t ssk, void* stream) {
   CIN_CHECK_ARG(valid_dtype(x_dtype), "quant_rowwise: unsupported x dtype %d", x_dtype);
   CIN_CHECK_ARG(M >= 0 && N >= 0, "quant_rowwise: negative shape");
   CIN_CHECK_ARG(block >= 1 && block <= 1024, "quant_rowwise: block %lld outside [1, 1024]",
@@ -1513,17 +1528,18 @@ int cin_quant_rowwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
   if (M == 0 || N == 0) return CIN_OK;
   CIN_CHECK_ARG(x && q && scales, "quant_rowwise: null pointer");
   const int64_t nb = cdiv(N, block);
-  CIN_CHECK_ARG(sqm >= N && ssm >= nb, "quant_rowwise: output row stride too small");
+  CIN_CHECK_ARG(sqm >= N, "quant_rowwise: output row stride too small");
+  CIN_CHECK_ARG(scale_layout_ok(M, nb, ssm, ssk), "quant_rowwise: scale strides overlap");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int es = elem_size(x_dtype);
   const bool fast = block == 128 && sxn == 1 && aligned(x, 16) && ((sxm * es) % 16 == 0) &&
                     aligned(q, 8) && (sqm % 8 == 0) && M * nb < (int64_t)1 << 31;
   if (fast) {
-    launch_rowwise128<8, 1>(x, x_dtype, M, N, sxm, round_scale, q, sqm, scales, ssm, nb, 16384, s);
+    launch_rowwise128<8, 1>(x, x_dtype, M, N, sxm, round_scale, q, sqm, scales, ssm, ssk, nb, 16384, s);
   } else {
     const unsigned grid = grid_for(M * nb, kThreads / 64, 65536);
     hipLaunchKernelGGL(k_rowwise_generic, grid, kThreads, 0, s, x, x_dtype, M, N, sxm, sxn, block,
-                       round_scale, q, sqm, scales, ssm, nb);
+                       round_scale, q, sqm, scales, ssm, ssk, nb);
   }
   return cin_check_launch("quant_rowwise");
 }
@@ -1553,18 +1569,18 @@ int cin_indexer_quantize(const void* q, int q_dtype, const void* k, int k_dtype,
     if (ntiles < 32768) {
       const unsigned grid = grid_for(ntiles, kThreads / 16, 16384);
       if (full)
-        launch_rowwise128_t<16, 1, true, kMapFirstScale>(sd.x, sd.dt, d, d, 0, sd.codes, d, sd.scales, 1,
+        launch_rowwise128_t<16, 1, true, kMapFirstScale>(sd.x, sd.dt, d, d, 0, sd.codes, d, sd.scales, 1, 0,
                                                          (uint32_t)nb, ntiles, grid, st);
       else
-        launch_rowwise128_t<16, 1, false, kMapFirstScale>(sd.x, sd.dt, d, d, 0, sd.codes, d, sd.scales, 1,
+        launch_rowwise128_t<16, 1, false, kMapFirstScale>(sd.x, sd.dt, d, d, 0, sd.codes, d, sd.scales, 1, 0,
                                                           (uint32_t)nb, ntiles, grid, st);
     } else {
       const unsigned grid = grid_for(ntiles, kThreads / 8, 16384);
       if (full)
-        launch_rowwise128_t<8, 1, true, kMapFirstScale>(sd.x, sd.dt, d, d, 0, sd.codes, d, sd.scales, 1,
+        launch_rowwise128_t<8, 1, true, kMapFirstScale>(sd.x, sd.dt, d, d, 0, sd.codes, d, sd.scales, 1, 0,
                                                         (uint32_t)nb, ntiles, grid, st);
       else
-        launch_rowwise128_t<8, 1, false, kMapFirstScale>(sd.x, sd.dt, d, d, 0, sd.codes, d, sd.scales, 1,
+        launch_rowwise128_t<8, 1, false, kMapFirstScale>(sd.x, sd.dt, d, d, 0, sd.codes, d, sd.scales, 1, 0,
                                                          (uint32_t)nb, ntiles, grid, st);
     }
   }
@@ -1574,14 +1590,15 @@ int cin_indexer_quantize(const void* q, int q_dtype, const void* k, int k_dtype,
 int cin_moe_gather_quant_rowwise(const void* x, int x_dtype, int64_t src_rows, int64_t N,
                                  int64_t sxm, const int64_t* rowmap, int64_t rows, int64_t rowdiv,
                                  int round_scale, uint8_t* q, int64_t sqm, float* scales,
-                                 int64_t ssm, void* stream) {
+                                 int64_t ssm, int64_t ssk, void* stream) {
   CIN_CHECK_ARG(valid_dtype(x_dtype), "moe_gather_quant: unsupported x dtype %d", x_dtype);
   CIN_CHECK_ARG(src_rows >= 0 && N >= 0 && rows >= 0 && rowdiv >= 1,
                 "moe_gather_quant: negative shape or row divisor < 1");
   if (rows == 0 || N == 0) return CIN_OK;
   CIN_CHECK_ARG(x && rowmap && q && scales, "moe_gather_quant: null pointer");
   const int64_t nb = cdiv(N, 128);
-  CIN_CHECK_ARG(sqm >= N && ssm >= nb, "moe_gather_quant: output row stride too small");
+  CIN_CHECK_ARG(sqm >= N, "moe_gather_quant: output row stride too small");
+  CIN_CHECK_ARG(scale_layout_ok(rows, nb, ssm, ssk), "moe_gather_quant: scale strides overlap");
   const int es = elem_size(x_dtype);
   CIN_CHECK_ARG(aligned(x, 16) && (sxm * es) % 16 == 0 && sxm >= N && aligned(q, 8) && sqm % 8 == 0,
                 "moe_gather_quant: x rows must be contiguous and 16-byte aligned, q rows 8-byte aligned");
@@ -1591,11 +1608,11 @@ int cin_moe_gather_quant_rowwise(const void* x, int x_dtype, int64_t src_rows, i
   const unsigned grid = grid_for(ntiles, kThreads / 8, 16384);
   if (N % 128 == 0)
     launch_rowwise128_t<8, 1, true, kMapGather>(x, x_dtype, N, sxm, round_scale, q, sqm, scales,
-                                                ssm, (uint32_t)nb, ntiles, grid, s, rowmap, rowdiv,
+                                                ssm, ssk, (uint32_t)nb, ntiles, grid, s, rowmap, rowdiv,
                                                 src_rows);
   else
     launch_rowwise128_t<8, 1, false, kMapGather>(x, x_dtype, N, sxm, round_scale, q, sqm, scales,
-                                                 ssm, (uint32_t)nb, ntiles, grid, s, rowmap,
+                                                 ssm, ssk, (uint32_t)nb, ntiles, grid, s, rowmap,
                                                  rowdiv, src_rows);
   return cin_check_launch("moe_gather_quant_rowwise");
 }
@@ -1603,13 +1620,14 @@ int cin_moe_gather_quant_rowwise(const void* x, int x_dtype, int64_t src_rows, i
 int cin_moe_scatter_quant_rowwise(const void* x, int x_dtype, int64_t T, int64_t N, int64_t sxm,
                                   const int32_t* inv, int64_t k, const int64_t* perm, int64_t rows,
                                   int round_scale, uint8_t* q, int64_t sqm, float* scales,
-                                  int64_t ssm, void* stream) {
+                                  int64_t ssm, int64_t ssk, void* stream) {
   CIN_CHECK_ARG(valid_dtype(x_dtype), "moe_scatter_quant: unsupported x dtype %d", x_dtype);
   CIN_CHECK_ARG(T >= 0 && N >= 0 && rows >= 0 && k >= 1, "moe_scatter_quant: bad sizes");
   if (N == 0 || (T == 0 && rows == 0)) return CIN_OK;
   CIN_CHECK_ARG(x && inv && perm && q && scales, "moe_scatter_quant: null pointer");
   const int64_t nb = cdiv(N, 128);
-  CIN_CHECK_ARG(sqm >= N && ssm >= nb, "moe_scatter_quant: output row stride too small");
+  CIN_CHECK_ARG(sqm >= N, "moe_scatter_quant: output row stride too small");
+  CIN_CHECK_ARG(scale_layout_ok(rows, nb, ssm, ssk), "moe_scatter_quant: scale strides overlap");
   const int es = elem_size(x_dtype);
   CIN_CHECK_ARG(aligned(x, 16) && (sxm * es) % 16 == 0 && sxm >= N && aligned(q, 8) && sqm % 8 == 0,
                 "moe_scatter_quant: x rows must be contiguous and 16-byte aligned, q rows 8-byte aligned");
@@ -1621,14 +1639,14 @@ int cin_moe_scatter_quant_rowwise(const void* x, int x_dtype, int64_t T, int64_t
     const unsigned grid = grid_for(ntiles, kThreads / 8, 16384);
     if (N % 128 == 0)
       launch_rowwise128_t<8, 1, true, kMapScatter>(x, x_dtype, N, sxm, round_scale, q, sqm, scales,
-                                                   ssm, (uint32_t)nb, ntiles, grid, s, inv, k, rows);
+                                                   ssm, ssk, (uint32_t)nb, ntiles, grid, s, inv, k, rows);
     else
       launch_rowwise128_t<8, 1, false, kMapScatter>(x, x_dtype, N, sxm, round_scale, q, sqm, scales,
-                                                    ssm, (uint32_t)nb, ntiles, grid, s, inv, k, rows);
+                                                    ssm, ssk, (uint32_t)nb, ntiles, grid, s, inv, k, rows);
   }
   if (rows > 0)
     hipLaunchKernelGGL(k_zero_unrouted, (unsigned)cdiv(rows, kThreads), kThreads, 0, s, perm, rows, N,
-                       x_dtype, round_scale, q, sqm, scales, ssm);
+                       x_dtype, round_scale, q, sqm, scales, ssm, ssk);
   return cin_check_launch("moe_scatter_quant_rowwise");
 }
 
@@ -1686,9 +1704,9 @@ int cin_quant_blockwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_
 }
 
 int cin_quant_fwd(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm, int round_scale,
-                  uint8_t* xq, int64_t sxqm, float* xs, int64_t sxsm, const void* w, int w_dtype,
-                  int64_t N, int64_t swm, uint8_t* wq, int64_t swqm, uint8_t* wqt, int64_t swqtm,
-                  float* ws, int64_t swsm, void* stream) {
+                  uint8_t* xq, int64_t sxqm, float* xs, int64_t sxsm, int64_t sxsk, const void* w,
+                  int w_dtype, int64_t N, int64_t swm, uint8_t* wq, int64_t swqm, uint8_t* wqt,
+                  int64_t swqtm, float* ws, int64_t swsm, void* stream) {
   CIN_CHECK_ARG(valid_dtype(x_dtype) && valid_dtype(w_dtype), "quant_fwd: unsupported dtype (x %d, w %d)",
                 x_dtype, w_dtype);
   CIN_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "quant_fwd: negative shape");
@@ -1696,7 +1714,8 @@ int cin_quant_fwd(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
   // both halves are validated before anything is launched, so a rejected call writes nothing
   if (M > 0 && K > 0) {
     CIN_CHECK_ARG(x && xq && xs, "quant_fwd: null activation pointer");
-    CIN_CHECK_ARG(sxqm >= K && sxsm >= nbk, "quant_fwd: activation output row stride too small");
+    CIN_CHECK_ARG(sxqm >= K, "quant_fwd: activation output row stride too small");
+    CIN_CHECK_ARG(scale_layout_ok(M, nbk, sxsm, sxsk), "quant_fwd: activation scale strides overlap");
   }
   if (N > 0 && K > 0) {
     CIN_CHECK_ARG(w && ws && (wq || wqt), "quant_fwd: null weight pointer");
@@ -1707,13 +1726,14 @@ int cin_quant_fwd(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
   const int xes = elem_size(x_dtype), wes = elem_size(w_dtype);
   const bool fuse = M > 0 && N > 0 && K > 0 && K % 128 == 0 && w_dtype != CIN_DT_F32 && x && xq && xs &&
                     w && ws && (wq || wqt) && aligned(x, 16) && (sxm * xes) % 16 == 0 && sxm >= K &&
-                    aligned(xq, 8) && sxqm % 8 == 0 && sxqm >= K && sxsm >= nbk && M * nbk < ((int64_t)1 << 31) &&
+                    aligned(xq, 8) && sxqm % 8 == 0 && sxqm >= K && M * nbk < ((int64_t)1 << 31) &&
                     aligned(w, 16) && (swm * wes) % 16 == 0 && swm >= K && tile_fits32(swm * wes) &&
                     (!wq || (aligned(wq, 8) && swqm % 8 == 0 && swqm >= K && tile_fits32(swqm))) &&
                     (!wqt || swqtm >= N) && swsm >= nbk && nbn < 65536 && nbn * nbk <= ((int64_t)1 << 22);
   if (!fuse) {
     // any other shape, dtype or layout: the two quantizers one after the other
-    const int rc = cin_quant_rowwise(x, x_dtype, M, K, sxm, 1, 128, round_scale, xq, sxqm, xs, sxsm, stream);
+    const int rc = cin_quant_rowwise(x, x_dtype, M, K, sxm, 1, 128, round_scale, xq, sxqm, xs, sxsm, sxsk,
+                                     stream);
     if (rc != CIN_OK) return rc;
     return cin_quant_blockwise(w, w_dtype, N, K, swm, 1, 128, 128, 0, wq, swqm, wqt, swqtm, ws, swsm, stream);
   }
@@ -1723,7 +1743,7 @@ int cin_quant_fwd(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm,
   const unsigned gx = grid_for(xtiles, (kThreads / 8) * kFwdXU, 16384);
   const unsigned grid = gx + wtiles;
 #define CIN_QFWD(XT, WT)                                                                                   \
-  hipLaunchKernelGGL((k_quant_fwd<XT, WT>), grid, kThreads, 0, s, x, K, sxm, round_scale, xq, sxqm, xs, sxsm, \
+  hipLaunchKernelGGL((k_quant_fwd<XT, WT>), grid, kThreads, 0, s, x, K, sxm, round_scale, xq, sxqm, xs, sxsm, sxsk, \
                      (uint32_t)nbk, xtiles, w, N, K, swm, wq, swqm, wqt, swqtm, wvec_t, ws, swsm,            \
                      (uint32_t)nbk, wtiles, wtiles)
 #define CIN_QFWD_X(WT)                                    \
@@ -1757,14 +1777,15 @@ int cin_dequant(const uint8_t* q, int64_t M, int64_t N, int64_t sqm, int64_t sqn
 }
 
 int cin_quant_dual(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t sdm, int64_t sdn,
-                   int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, uint8_t* qt,
-                   int64_t sqtm, float* st, int64_t sstm, void* stream) {
+                   int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, int64_t ssk,
+                   uint8_t* qt, int64_t sqtm, float* st, int64_t sstm, int64_t sstk, void* stream) {
   CIN_CHECK_ARG(valid_dtype(dy_dtype), "quant_dual: unsupported dtype %d", dy_dtype);
   CIN_CHECK_ARG(M >= 0 && N >= 0, "quant_dual: negative shape");
   if (M == 0 || N == 0) return CIN_OK;
   CIN_CHECK_ARG(dy && q && s && qt && st, "quant_dual: null pointer");
-  CIN_CHECK_ARG(sqm >= N && sqtm >= M && ssm >= cdiv(N, 128) && sstm >= cdiv(M, 128),
-                "quant_dual: output row stride too small");
+  CIN_CHECK_ARG(sqm >= N && sqtm >= M, "quant_dual: output row stride too small");
+  CIN_CHECK_ARG(scale_layout_ok(M, cdiv(N, 128), ssm, ssk) && scale_layout_ok(N, cdiv(M, 128), sstm, sstk),
+                "quant_dual: scale strides overlap");
   hipStream_t stream_ = static_cast<hipStream_t>(stream);
   const int es = elem_size(dy_dtype);
   const bool fast = sdn == 1 && aligned(dy, 16) && ((sdm * es) % 16 == 0) && aligned(q, 8) &&
@@ -1778,8 +1799,8 @@ int cin_quant_dual(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t s
     const uint32_t nt = nrb * (NBC);                                                           \
     const unsigned grid_ = resident_grid<k_dual128<DT, EDGE>>(nt);                             \
     hipLaunchKernelGGL((k_dual128<DT, EDGE>), grid_, kThreads, 0,                              \
-                       stream_, dy, M, N, sdm, round_scale, q, sqm, s, ssm, qt, sqtm, vec_t, st,  \
-                       sstm,                                                                   \
+                       stream_, dy, M, N, sdm, round_scale, q, sqm, s, ssm, ssk, qt, sqtm, vec_t, \
+                       st, sstm, sstk,                                                         \
                        (uint32_t)(NBC), (uint32_t)(CB0), nt);                                  \
   } while (0)
 #define CIN_DUAL128_ALL(DT)                                   \
@@ -1798,16 +1819,16 @@ int cin_quant_dual(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t s
     return cin_check_launch("quant_dual");
   }
   // Strided input: two generic row-wise passes (dy, then dy^T through strides).
-  int rc = cin_quant_rowwise(dy, dy_dtype, M, N, sdm, sdn, 128, round_scale, q, sqm, s, ssm, stream);
+  int rc = cin_quant_rowwise(dy, dy_dtype, M, N, sdm, sdn, 128, round_scale, q, sqm, s, ssm, ssk, stream);
   if (rc != CIN_OK) return rc;
-  return cin_quant_rowwise(dy, dy_dtype, N, M, sdn, sdm, 128, round_scale, qt, sqtm, st, sstm,
+  return cin_quant_rowwise(dy, dy_dtype, N, M, sdn, sdm, 128, round_scale, qt, sqtm, st, sstm, sstk,
                            stream);
 }
 
 int cin_quant_dual_grouped(const void* dy, int dy_dtype, int64_t T, int64_t N, int64_t sdm,
                            const int64_t* starts, const int64_t* ends, int64_t E, int round_scale,
-                           uint8_t* q, int64_t sqm, float* s, int64_t ssm, uint8_t* qt,
-                           int64_t sqtm, float* st, int64_t sstm, void* stream) {
+                           uint8_t* q, int64_t sqm, float* s, int64_t ssm, int64_t ssk, uint8_t* qt,
+                           int64_t sqtm, float* st, int64_t sstm, int64_t sstk, void* stream) {
   CIN_CHECK_ARG(valid_dtype(dy_dtype), "quant_dual_grouped: unsupported dtype %d", dy_dtype);
   CIN_CHECK_ARG(T >= 0 && N >= 0 && E >= 0, "quant_dual_grouped: negative shape");
   if (T == 0 || N == 0 || E == 0) return CIN_OK;
@@ -1815,9 +1836,9 @@ int cin_quant_dual_grouped(const void* dy, int dy_dtype, int64_t T, int64_t N, i
   const int es = elem_size(dy_dtype);
   CIN_CHECK_ARG(aligned(dy, 16) && (sdm * es) % 16 == 0 && sdm >= N,
                 "quant_dual_grouped: dy rows must be contiguous and 16-byte aligned");
-  CIN_CHECK_ARG(aligned(q, 8) && sqm % 8 == 0 && sqm >= N && ssm >= cdiv(N, 128),
+  CIN_CHECK_ARG(aligned(q, 8) && sqm % 8 == 0 && sqm >= N && scale_layout_ok(T, cdiv(N, 128), ssm, ssk),
                 "quant_dual_grouped: bad row-wise outputs");
-  CIN_CHECK_ARG(sqtm >= 128 && sstm >= sqtm / 128,
+  CIN_CHECK_ARG(sqtm >= 128 && scale_layout_ok(N, sqtm / 128, sstm, sstk),
                 "quant_dual_grouped: transposed rows must hold the padded token axis");
   CIN_CHECK_ARG((cdiv(T, 128) + E) * cdiv(N, 128) < ((int64_t)1 << 31),
                 "quant_dual_grouped: too many tiles");
@@ -1831,8 +1852,9 @@ int cin_quant_dual_grouped(const void* dy, int dy_dtype, int64_t T, int64_t N, i
     const uint32_t nt = nch * (NBC);                                                            \
     const unsigned grid_ = resident_grid<k_dual128_grouped<DT, EDGE>>(nt);                      \
     hipLaunchKernelGGL((k_dual128_grouped<DT, EDGE>), grid_,                                    \
-                       kThreads, 0, stream_, dy, T, N, sdm, round_scale, q, sqm, s, ssm, qt, sqtm, \
-                       vec_t, st, sstm, starts, ends, E, sqtm, (uint32_t)(NBC), (uint32_t)(CB0), nt); \
+                       kThreads, 0, stream_, dy, T, N, sdm, round_scale, q, sqm, s, ssm, ssk, qt,  \
+                       sqtm, vec_t, st, sstm, sstk, starts, ends, E, sqtm, (uint32_t)(NBC),        \
+                       (uint32_t)(CB0), nt);                                                       \
   } while (0)
 #define CIN_DUALG_ALL(DT)                                   \
   do {                                                      \
@@ -1851,14 +1873,15 @@ int cin_quant_dual_grouped(const void* dy, int dy_dtype, int64_t T, int64_t N, i
 }
 
 int cin_requant_row_to_block_grouped(const uint8_t* q, int64_t T, int64_t K, int64_t sqm,
-                                     const float* srow, int64_t ssm, const int64_t* starts,
-                                     const int64_t* ends, int64_t E, uint8_t* qbt, int64_t sqbtm,
-                                     float* sblk, int64_t ssbm, void* stream) {
+                                     const float* srow, int64_t ssm, int64_t ssk,
+                                     const int64_t* starts, const int64_t* ends, int64_t E,
+                                     uint8_t* qbt, int64_t sqbtm, float* sblk, int64_t ssbm,
+                                     void* stream) {
   CIN_CHECK_ARG(T >= 0 && K >= 0 && E >= 0, "requant_grouped: negative shape");
   if (T == 0 || K == 0 || E == 0) return CIN_OK;
   CIN_CHECK_ARG(q && srow && qbt && sblk && starts && ends, "requant_grouped: null pointer");
   CIN_CHECK_ARG(aligned(q, 8) && sqm % 8 == 0 && sqm >= K, "requant_grouped: q must be 8-byte aligned rows");
-  CIN_CHECK_ARG(sqbtm >= 128 && ssm >= cdiv(K, 128) && ssbm >= cdiv(K, 128),
+  CIN_CHECK_ARG(sqbtm >= 128 && scale_layout_ok(T, cdiv(K, 128), ssm, ssk) && ssbm >= cdiv(K, 128),
                 "requant_grouped: bad output strides");
   CIN_CHECK_ARG((cdiv(T, 128) + E) * cdiv(K, 128) < ((int64_t)1 << 31),
                 "requant_grouped: too many tiles");
@@ -1872,7 +1895,7 @@ int cin_requant_row_to_block_grouped(const uint8_t* q, int64_t T, int64_t K, int
     const uint32_t nt = nch * (NBC);                                                              \
     const unsigned grid_ = resident_grid<k_requant128_grouped<EDGE>>(nt);                         \
     hipLaunchKernelGGL(k_requant128_grouped<EDGE>, grid_,                                         \
-                       kThreads, 0, s, q, T, K, sqm, srow, ssm, (uint8_t*)nullptr, (int64_t)0, qbt, \
+                       kThreads, 0, s, q, T, K, sqm, srow, ssm, ssk, (uint8_t*)nullptr, (int64_t)0, qbt, \
                        sqbtm, vec_t, sblk, ssbm, starts, ends, E, sqbtm, (uint32_t)(NBC),         \
                        (uint32_t)(CB0), nt);                                                        \
   } while (0)
@@ -1883,8 +1906,8 @@ int cin_requant_row_to_block_grouped(const uint8_t* q, int64_t T, int64_t K, int
 }
 
 int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm,
-                             const float* srow, int64_t ssm, uint8_t* qb, int64_t sqbm,
-                             uint8_t* qbt, int64_t sqbtm, float* sblk, int64_t ssbm,
+                             const float* srow, int64_t ssm, int64_t ssk, uint8_t* qb,
+                             int64_t sqbm, uint8_t* qbt, int64_t sqbtm, float* sblk, int64_t ssbm,
                              void* stream) {
   CIN_CHECK_ARG(M >= 0 && K >= 0, "requant: negative shape");
   if (M == 0 || K == 0) return CIN_OK;
@@ -1893,7 +1916,7 @@ int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm
   CIN_CHECK_ARG(!qb || (aligned(qb, 8) && sqbm % 8 == 0 && sqbm >= K),
                 "requant: qb must be 8-byte aligned rows");
   CIN_CHECK_ARG(!qbt || sqbtm >= M, "requant: qbt row stride too small");
-  CIN_CHECK_ARG(ssm >= cdiv(K, 128) && ssbm >= cdiv(K, 128), "requant: bad scale stride");
+  CIN_CHECK_ARG(scale_layout_ok(M, cdiv(K, 128), ssm, ssk) && ssbm >= cdiv(K, 128), "requant: bad scale stride");
   CIN_CHECK_ARG(cdiv(M, 128) * cdiv(K, 128) < ((int64_t)1 << 31), "requant: too many tiles");
   CIN_CHECK_ARG(tile_fits32(sqm) && tile_fits32(ssm * 4) && (!qb || tile_fits32(sqbm)),
                 "requant: row strides too large");
@@ -1905,7 +1928,7 @@ int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm
     const uint32_t nt = nrb * (NBC);                                                            \
     const unsigned grid_ = resident_grid<k_requant128<EDGE>>(nt);                               \
     hipLaunchKernelGGL(k_requant128<EDGE>, grid_, kThreads, 0, s, q,                            \
-                       M, K, sqm, srow, ssm, qb, sqbm, qbt, sqbtm, vec_t, sblk, ssbm, (uint32_t)(NBC), \
+                       M, K, sqm, srow, ssm, ssk, qb, sqbm, qbt, sqbtm, vec_t, sblk, ssbm, (uint32_t)(NBC), \
                        (uint32_t)(CB0), nt);                                                    \
   } while (0)
   if (nfull > 0) CIN_REQ(false, nfull, 0);
@@ -1915,17 +1938,19 @@ int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm
 }
 
 int cin_quant_backward(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t sdm,
-                       int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, uint8_t* qt,
-                       int64_t sqtm, float* st, int64_t sstm, const uint8_t* xq, int64_t K,
-                       int64_t sxqm, const float* xs, int64_t sxsm, uint8_t* xbt, int64_t sxbtm,
-                       float* sblk, int64_t ssbm, void* stream) {
+                       int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, int64_t ssk,
+                       uint8_t* qt, int64_t sqtm, float* st, int64_t sstm, int64_t sstk,
+                       const uint8_t* xq, int64_t K, int64_t sxqm, const float* xs, int64_t sxsm,
+                       int64_t sxsk, uint8_t* xbt, int64_t sxbtm, float* sblk, int64_t ssbm,
+                       void* stream) {
   CIN_CHECK_ARG(valid_dtype(dy_dtype), "quant_backward: unsupported dtype %d", dy_dtype);
   CIN_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "quant_backward: negative shape");
   if (M == 0 || (N == 0 && K == 0)) return CIN_OK;
   CIN_CHECK_ARG(dy && q && s && qt && st && xq && xs && xbt && sblk, "quant_backward: null pointer");
-  CIN_CHECK_ARG(sqm >= N && sqtm >= M && ssm >= cdiv(N, 128) && sstm >= cdiv(M, 128),
-                "quant_backward: dY output row stride too small");
-  CIN_CHECK_ARG(aligned(xq, 8) && sxqm % 8 == 0 && sxqm >= K && sxsm >= cdiv(K, 128) &&
+  CIN_CHECK_ARG(sqm >= N && sqtm >= M && scale_layout_ok(M, cdiv(N, 128), ssm, ssk) &&
+                    scale_layout_ok(N, cdiv(M, 128), sstm, sstk),
+                "quant_backward: dY output row stride too small or scale strides overlap");
+  CIN_CHECK_ARG(aligned(xq, 8) && sxqm % 8 == 0 && sxqm >= K && scale_layout_ok(M, cdiv(K, 128), sxsm, sxsk) &&
                     sxbtm >= M && ssbm >= cdiv(K, 128),
                 "quant_backward: bad X codes, scales or outputs");
   const int es = elem_size(dy_dtype);
@@ -1937,10 +1962,10 @@ int cin_quant_backward(const void* dy, int dy_dtype, int64_t M, int64_t N, int64
                     tile_fits32(sqm) && tile_fits32(sxqm) && tile_fits32(sxsm * 4) &&
                     cdiv(M, 128) * (N / 128 + K / 128) < ((int64_t)1 << 31);
   if (!pair) {
-    int rc = cin_quant_dual(dy, dy_dtype, M, N, sdm, 1, round_scale, q, sqm, s, ssm, qt, sqtm, st,
-                            sstm, stream);
+    int rc = cin_quant_dual(dy, dy_dtype, M, N, sdm, 1, round_scale, q, sqm, s, ssm, ssk, qt, sqtm, st,
+                            sstm, sstk, stream);
     if (rc != CIN_OK) return rc;
-    return cin_requant_row_to_block(xq, M, K, sxqm, xs, sxsm, nullptr, 0, xbt, sxbtm, sblk, ssbm,
+    return cin_requant_row_to_block(xq, M, K, sxqm, xs, sxsm, sxsk, nullptr, 0, xbt, sxbtm, sblk, ssbm,
                                     stream);
   }
   const int dvec_t = aligned(qt, 16) && sqtm % 16 == 0 && tile_fits32(sqtm);
@@ -1950,8 +1975,8 @@ int cin_quant_backward(const void* dy, int dy_dtype, int64_t M, int64_t N, int64
   hipStream_t stream_ = static_cast<hipStream_t>(stream);
 #define CIN_QBWD(DT)                                                                               \
   hipLaunchKernelGGL((k_quant_bwd<DT>), resident_grid<k_quant_bwd<DT>>(nt), kThreads, 0, stream_, dy, \
-                     M, N, sdm, round_scale, q, sqm, s, ssm, qt, sqtm, dvec_t, st, sstm, xq, K, sxqm, xs, \
-                     sxsm, xbt, sxbtm, rvec_t, sblk, ssbm, nd, nt)
+                     M, N, sdm, round_scale, q, sqm, s, ssm, ssk, qt, sqtm, dvec_t, st, sstm, sstk, xq, K, \
+                     sxqm, xs, sxsm, sxsk, xbt, sxbtm, rvec_t, sblk, ssbm, nd, nt)
   if (dy_dtype == CIN_DT_BF16)
     CIN_QBWD(CIN_DT_BF16);
   else
@@ -1962,7 +1987,7 @@ int cin_quant_backward(const void* dy, int dy_dtype, int64_t M, int64_t N, int64
 
 int cin_silu_mul_quant_rowwise(const void* h12, int in_dtype, int64_t M, int64_t H, int64_t s12,
                                int out_dtype, int round_scale, uint8_t* q, int64_t sqm,
-                               float* scales, int64_t ssm, void* stream) {
+                               float* scales, int64_t ssm, int64_t ssk, void* stream) {
   CIN_CHECK_ARG(valid_dtype(in_dtype) && valid_dtype(out_dtype), "silu_mul_quant: unsupported dtype");
   CIN_CHECK_ARG(M >= 0 && H >= 0, "silu_mul_quant: negative shape");
   if (M == 0 || H == 0) return CIN_OK;
@@ -1970,7 +1995,7 @@ int cin_silu_mul_quant_rowwise(const void* h12, int in_dtype, int64_t M, int64_t
   const int es = elem_size(in_dtype);
   CIN_CHECK_ARG(aligned(h12, 16) && (s12 * es) % 16 == 0 && (H * es) % 16 == 0 && s12 >= 2 * H,
                 "silu_mul_quant: h12 rows must hold 2H elements at 16-byte aligned offsets");
-  CIN_CHECK_ARG(aligned(q, 8) && sqm % 8 == 0 && sqm >= H && ssm >= cdiv(H, 128),
+  CIN_CHECK_ARG(aligned(q, 8) && sqm % 8 == 0 && sqm >= H && scale_layout_ok(M, cdiv(H, 128), ssm, ssk),
                 "silu_mul_quant: bad outputs");
   const int64_t nb = cdiv(H, 128);
   CIN_CHECK_ARG(M * nb < ((int64_t)1 << 31), "silu_mul_quant: too many tiles");
@@ -1979,7 +2004,7 @@ int cin_silu_mul_quant_rowwise(const void* h12, int in_dtype, int64_t M, int64_t
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define CIN_SILU(IT, OT)                                                                        \
   hipLaunchKernelGGL((k_silu_mul_rowwise128<IT, OT>), grid, kThreads, 0, s, h12, s12, H,         \
-                     round_scale, q, sqm, scales, ssm, (uint32_t)nb, ntiles)
+                     round_scale, q, sqm, scales, ssm, ssk, (uint32_t)nb, ntiles)
 #define CIN_SILU_OT(IT)                                                                         \
   do {                                                                                          \
     if (out_dtype == CIN_DT_BF16) CIN_SILU(IT, CIN_DT_BF16);                                    \

@@ -24,7 +24,7 @@ int cin_check_launch(const char* what) {
 
 extern "C" {
 
-int cin_abi_version(void) { return 2; }
+int cin_abi_version(void) { return 3; }
 
 const char* cin_last_error(void) { return g_err; }
 

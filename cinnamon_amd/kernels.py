@@ -87,6 +87,17 @@ def _codes_u8(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def _scales_2d(sc: torch.Tensor) -> torch.Tensor:
+    """A 2-D fp32 scale tensor the kernels can address with (row, column) strides: itself
+    when it is row-major (unit column stride, rows not overlapping) or column-major (unit row
+    stride), else a row-major copy."""
+    R, C = sc.shape
+    if sc.dtype == torch.float32 and ((sc.stride(1) == 1 and sc.stride(0) >= max(C, 1)) or
+                                      (sc.stride(0) == 1 and sc.stride(1) >= max(R, 1))):
+        return sc
+    return sc.to(torch.float32).contiguous()
+
+
 def _rows8(q: torch.Tensor) -> torch.Tensor:
     """2-D uint8 codes with unit column stride and 8-byte aligned rows (the tile kernels
     read 8 codes at a time): q itself when it qualifies, else a copy whose rows are padded
@@ -102,30 +113,44 @@ def _rows8(q: torch.Tensor) -> torch.Tensor:
 # ---------------------------------------------------------------------------
 # Quantization (reference src/kernels.py:178-259)
 # ---------------------------------------------------------------------------
+def _scale_buf(like: torch.Tensor, rows: int, cols: int, col_major: bool) -> torch.Tensor:
+    """An fp32 [rows, cols] scale tensor, row-major (the reference's layout) or column-major
+    (strides (1, rows): the scales of one 128-column block of consecutive rows side by
+    side, which the GEMM reads as one run per K block).  ``like`` gives the device (or the
+    fake-tensor mode)."""
+    if col_major:
+        return like.new_empty((cols, rows), dtype=torch.float32).t()
+    return like.new_empty((rows, cols), dtype=torch.float32)
+
+
 def quantize_fp8_rowwise(x: torch.Tensor, block_size: int = 128,
-                         round_scale: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
-    """1 x block_size e4m3 quantization -> (codes [M, N] float8_e4m3fn, scales [M, ceil(N/bs)] fp32)."""
+                         round_scale: bool = False,
+                         col_scales: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """1 x block_size e4m3 quantization -> (codes [M, N] float8_e4m3fn, scales [M, ceil(N/bs)] fp32).
+
+    col_scales: the scales come back column-major (same values, strides (1, M)); the
+    reference's layout is row-major."""
     _require(x.is_cuda, "Input must be on CUDA")
     _require(x.ndim == 2, "Input must be 2D for now")
-    return _quant_rowwise_op(x, int(block_size), bool(round_scale))
+    return _quant_rowwise_op(x, int(block_size), bool(round_scale), bool(col_scales))
 
 
-@custom_op("quant_rowwise", "(Tensor x, int block_size, bool round_scale) -> (Tensor, Tensor)")
-def _quant_rowwise_op(x, block_size, round_scale):
+@custom_op("quant_rowwise", "(Tensor x, int block_size, bool round_scale, bool col_scales) -> (Tensor, Tensor)")
+def _quant_rowwise_op(x, block_size, round_scale, col_scales):
     M, N = x.shape
     x_fp8 = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=x.device)
-    scales = torch.empty((M, _cdiv(N, block_size)), dtype=torch.float32, device=x.device)
+    scales = _scale_buf(x, M, _cdiv(N, block_size), col_scales)
     call("cin_quant_rowwise", ptr(x), dtype_code(x), M, N, x.stride(0), x.stride(1), block_size,
          int(round_scale), ptr(x_fp8), x_fp8.stride(0), ptr(scales), scales.stride(0),
-         stream_of(x))
+         scales.stride(1), stream_of(x))
     return x_fp8, scales
 
 
 @_quant_rowwise_op.register_fake
-def _(x, block_size, round_scale):
+def _(x, block_size, round_scale, col_scales):
     M, N = x.shape
     return (x.new_empty((M, N), dtype=torch.float8_e4m3fn),
-            x.new_empty((M, _cdiv(N, block_size)), dtype=torch.float32))
+            _scale_buf(x, M, _cdiv(N, block_size), col_scales))
 
 
 def quantize_fp8_blockwise(x: torch.Tensor, block_m: int = 128, block_n: int = 128,
@@ -191,7 +216,8 @@ def _(x, round_scale, with_rowmajor):
 
 
 def quantize_fp8_forward(x: torch.Tensor, weight: torch.Tensor, round_scale: bool = False,
-                         with_rowmajor: bool = True, with_transposed: bool = False):
+                         with_rowmajor: bool = True, with_transposed: bool = False,
+                         col_scales: bool = False):
     """Both quantizations of the FP8 linear forward in one launch (reference
     src/kernels.py:746-747): x [M, K] in 1 x 128 row tiles with round_scale as given, and
     weight [N, K] in 128 x 128 blocks with round_scale off.  Bit-identical to
@@ -199,78 +225,80 @@ def quantize_fp8_forward(x: torch.Tensor, weight: torch.Tensor, round_scale: boo
     a 16-bit weight is read as it is, without the fp32 copy.
 
     Returns (x_fp8 [M, K], x_scale [M, ceil(K/128)], w_fp8 [N, K] or None,
-    w_fp8_t [K, N] or None, w_scale [ceil(N/128), ceil(K/128)]).
+    w_fp8_t [K, N] or None, w_scale [ceil(N/128), ceil(K/128)]); x_scale column-major with
+    col_scales.
     """
     _require(x.is_cuda and weight.is_cuda, "Inputs must be on CUDA")
     _require(x.ndim == 2 and weight.ndim == 2, "Inputs must be 2D")
     _require(x.shape[1] == weight.shape[1], "x and weight must share K")
     _require(with_rowmajor or with_transposed, "at least one layout of the weight codes")
     xq, xs, wq, wqt, ws = _quant_fwd_op(x, weight, bool(round_scale), bool(with_rowmajor),
-                                        bool(with_transposed))
+                                        bool(with_transposed), bool(col_scales))
     return xq, xs, (wq if with_rowmajor else None), (wqt if with_transposed else None), ws
 
 
 @custom_op("quant_fwd", "(Tensor x, Tensor weight, bool round_scale, bool with_rowmajor, "
-           "bool with_transposed) -> (Tensor, Tensor, Tensor, Tensor, Tensor)")
-def _quant_fwd_op(x, weight, round_scale, with_rowmajor, with_transposed):
+           "bool with_transposed, bool col_scales) -> (Tensor, Tensor, Tensor, Tensor, Tensor)")
+def _quant_fwd_op(x, weight, round_scale, with_rowmajor, with_transposed, col_scales):
     # a weight layout not asked for comes back as an empty [0, ...] placeholder
     x = x if x.stride(1) == 1 else x.contiguous()
     weight = weight if weight.stride(1) == 1 else weight.contiguous()
     (M, K), N = x.shape, weight.shape[0]
     dev = x.device
     xq = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=dev)
-    xs = torch.empty((M, _cdiv(K, 128)), dtype=torch.float32, device=dev)
+    xs = _scale_buf(x, M, _cdiv(K, 128), col_scales)
     wq = torch.empty((N if with_rowmajor else 0, K), dtype=torch.float8_e4m3fn, device=dev)
     wqt = torch.empty((K if with_transposed else 0, N), dtype=torch.float8_e4m3fn, device=dev)
     ws = torch.empty((_cdiv(N, 128), _cdiv(K, 128)), dtype=torch.float32, device=dev)
     call("cin_quant_fwd", ptr(x), dtype_code(x), M, K, x.stride(0), int(round_scale), ptr(xq), K,
-         ptr(xs), xs.stride(0), ptr(weight), dtype_code(weight), N, weight.stride(0),
+         ptr(xs), xs.stride(0), xs.stride(1), ptr(weight), dtype_code(weight), N, weight.stride(0),
          ptr(wq) if with_rowmajor else ptr(None), K, ptr(wqt) if with_transposed else ptr(None), N,
          ptr(ws), ws.stride(0), stream_of(x))
     return xq, xs, wq, wqt, ws
 
 
 @_quant_fwd_op.register_fake
-def _(x, weight, round_scale, with_rowmajor, with_transposed):
+def _(x, weight, round_scale, with_rowmajor, with_transposed, col_scales):
     (M, K), N = x.shape, weight.shape[0]
     return (x.new_empty((M, K), dtype=torch.float8_e4m3fn),
-            x.new_empty((M, _cdiv(K, 128)), dtype=torch.float32),
+            _scale_buf(x, M, _cdiv(K, 128), col_scales),
             x.new_empty((N if with_rowmajor else 0, K), dtype=torch.float8_e4m3fn),
             x.new_empty((K if with_transposed else 0, N), dtype=torch.float8_e4m3fn),
             x.new_empty((_cdiv(N, 128), _cdiv(K, 128)), dtype=torch.float32))
 
 
-def quantize_fp8_dual(dy: torch.Tensor, round_scale: bool = False):
+def quantize_fp8_dual(dy: torch.Tensor, round_scale: bool = False, col_scales: bool = False):
     """Row tiles of dy and of dy^T from one read (reference src/kernels.py:771, :781-783).
 
     Returns (q [M, N], s [M, ceil(N/128)], qt [N, M], st [N, ceil(M/128)]), bit-identical to
-    quantize_fp8_rowwise(dy) and quantize_fp8_rowwise(dy.t().contiguous()).
+    quantize_fp8_rowwise(dy) and quantize_fp8_rowwise(dy.t().contiguous()); s and st
+    column-major with col_scales.
     """
     _require(dy.is_cuda, "Input must be on CUDA")
     _require(dy.ndim == 2, "Input must be 2D")
-    return _quant_dual_op(dy, bool(round_scale))
+    return _quant_dual_op(dy, bool(round_scale), bool(col_scales))
 
 
-@custom_op("quant_dual", "(Tensor dy, bool round_scale) -> (Tensor, Tensor, Tensor, Tensor)")
-def _quant_dual_op(dy, round_scale):
+@custom_op("quant_dual", "(Tensor dy, bool round_scale, bool col_scales) -> (Tensor, Tensor, Tensor, Tensor)")
+def _quant_dual_op(dy, round_scale, col_scales):
     M, N = dy.shape
     q = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=dy.device)
-    s = torch.empty((M, _cdiv(N, 128)), dtype=torch.float32, device=dy.device)
+    s = _scale_buf(dy, M, _cdiv(N, 128), col_scales)
     qt = torch.empty((N, M), dtype=torch.float8_e4m3fn, device=dy.device)
-    st = torch.empty((N, _cdiv(M, 128)), dtype=torch.float32, device=dy.device)
+    st = _scale_buf(dy, N, _cdiv(M, 128), col_scales)
     call("cin_quant_dual", ptr(dy), dtype_code(dy), M, N, dy.stride(0), dy.stride(1),
-         int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), ptr(qt), qt.stride(0),
-         ptr(st), st.stride(0), stream_of(dy))
+         int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), s.stride(1), ptr(qt),
+         qt.stride(0), ptr(st), st.stride(0), st.stride(1), stream_of(dy))
     return q, s, qt, st
 
 
 @_quant_dual_op.register_fake
-def _(dy, round_scale):
+def _(dy, round_scale, col_scales):
     M, N = dy.shape
     return (dy.new_empty((M, N), dtype=torch.float8_e4m3fn),
-            dy.new_empty((M, _cdiv(N, 128)), dtype=torch.float32),
+            _scale_buf(dy, M, _cdiv(N, 128), col_scales),
             dy.new_empty((N, M), dtype=torch.float8_e4m3fn),
-            dy.new_empty((N, _cdiv(M, 128)), dtype=torch.float32))
+            _scale_buf(dy, N, _cdiv(M, 128), col_scales))
 
 
 def requantize_rowwise_to_blockwise(x_fp8: torch.Tensor, x_scale: torch.Tensor,
@@ -293,19 +321,21 @@ def requantize_rowwise_to_blockwise(x_fp8: torch.Tensor, x_scale: torch.Tensor,
 def _requant_op(x_fp8, x_scale, transposed):
     M, K = x_fp8.shape
     q = _rows8(_codes_u8(x_fp8))
-    xs = x_scale if x_scale.stride(1) == 1 else x_scale.contiguous()
+    xs = _scales_2d(x_scale)
     sblk = torch.empty((_cdiv(M, 128), _cdiv(K, 128)), dtype=torch.float32, device=x_fp8.device)
     if transposed:
         out = torch.empty((K, M), dtype=torch.float8_e4m3fn, device=x_fp8.device)
         call("cin_requant_row_to_block", ptr(q), M, K, q.stride(0), ptr(xs), xs.stride(0),
-             ptr(None), 0, ptr(out), out.stride(0), ptr(sblk), sblk.stride(0), stream_of(q))
+             xs.stride(1), ptr(None), 0, ptr(out), out.stride(0), ptr(sblk), sblk.stride(0),
+             stream_of(q))
     else:
         # the kernel stores 8 codes at a time: rows of a K that is not a multiple of 8 go
         # to a padded buffer, and the caller gets a contiguous copy
         K8 = _cdiv(K, 8) * 8
         out = torch.empty((M, K8), dtype=torch.float8_e4m3fn, device=x_fp8.device)
         call("cin_requant_row_to_block", ptr(q), M, K, q.stride(0), ptr(xs), xs.stride(0),
-             ptr(out), out.stride(0), ptr(None), 0, ptr(sblk), sblk.stride(0), stream_of(q))
+             xs.stride(1), ptr(out), out.stride(0), ptr(None), 0, ptr(sblk), sblk.stride(0),
+             stream_of(q))
         if K8 != K:
             out = out[:, :K].contiguous()
     return out, sblk
@@ -319,14 +349,15 @@ def _(x_fp8, x_scale, transposed):
 
 
 def quantize_fp8_backward(grad: torch.Tensor, x_fp8: torch.Tensor, x_scale: torch.Tensor,
-                          round_scale: bool = False):
+                          round_scale: bool = False, col_scales: bool = False):
     """The three quantizations of FP8MatmulFunction.backward in one launch (reference
     src/kernels.py:771, :781-783, :784-787): dY [M, N] in 1 x 128 row tiles, dY^T in row
     tiles, and the saved row-wise X codes [M, K] re-quantized into 128 x 128 blocks, stored
     transposed.  Bit-identical to quantize_fp8_dual(grad, round_scale) followed by
     requantize_rowwise_to_blockwise(x_fp8, x_scale, transposed=True).
 
-    Returns (g_fp8 [M, N], g_scale, g_fp8_t [N, M], g_scale_t, x_blk_t [K, M], x_sblk).
+    Returns (g_fp8 [M, N], g_scale, g_fp8_t [N, M], g_scale_t, x_blk_t [K, M], x_sblk);
+    g_scale and g_scale_t column-major with col_scales.  x_scale may have either layout.
     """
     _require(grad.is_cuda and x_fp8.is_cuda, "Inputs must be on CUDA")
     _require(grad.ndim == 2 and x_fp8.ndim == 2, "Inputs must be 2D")
@@ -335,39 +366,39 @@ def quantize_fp8_backward(grad: torch.Tensor, x_fp8: torch.Tensor, x_scale: torc
     _require(x_fp8.dtype in (torch.float8_e4m3fn, torch.uint8),
              f"expected float8_e4m3fn codes, got {x_fp8.dtype}")
     _require(x_scale.shape == (M, _cdiv(K, 128)), "row scales must be [M, ceil(K/128)]")
-    return _quant_bwd_op(grad, x_fp8, x_scale, bool(round_scale))
+    return _quant_bwd_op(grad, x_fp8, x_scale, bool(round_scale), bool(col_scales))
 
 
-@custom_op("quant_bwd", "(Tensor grad, Tensor x_fp8, Tensor x_scale, bool round_scale) -> "
+@custom_op("quant_bwd", "(Tensor grad, Tensor x_fp8, Tensor x_scale, bool round_scale, bool col_scales) -> "
            "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)")
-def _quant_bwd_op(grad, x_fp8, x_scale, round_scale):
+def _quant_bwd_op(grad, x_fp8, x_scale, round_scale, col_scales):
     dy = grad if grad.stride(1) == 1 else grad.contiguous()
     M, N = dy.shape
     K = x_fp8.shape[1]
     dev = dy.device
     xq = _rows8(_codes_u8(x_fp8))
-    xs = x_scale if x_scale.stride(1) == 1 else x_scale.contiguous()
+    xs = _scales_2d(x_scale)
     q = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=dev)
-    s = torch.empty((M, _cdiv(N, 128)), dtype=torch.float32, device=dev)
+    s = _scale_buf(dy, M, _cdiv(N, 128), col_scales)
     qt = torch.empty((N, M), dtype=torch.float8_e4m3fn, device=dev)
-    st = torch.empty((N, _cdiv(M, 128)), dtype=torch.float32, device=dev)
+    st = _scale_buf(dy, N, _cdiv(M, 128), col_scales)
     xbt = torch.empty((K, M), dtype=torch.float8_e4m3fn, device=dev)
     sblk = torch.empty((_cdiv(M, 128), _cdiv(K, 128)), dtype=torch.float32, device=dev)
     call("cin_quant_backward", ptr(dy), dtype_code(dy), M, N, dy.stride(0), int(round_scale), ptr(q),
-         q.stride(0), ptr(s), s.stride(0), ptr(qt), qt.stride(0), ptr(st), st.stride(0), ptr(xq), K,
-         xq.stride(0), ptr(xs), xs.stride(0), ptr(xbt), xbt.stride(0), ptr(sblk), sblk.stride(0),
-         stream_of(dy))
+         q.stride(0), ptr(s), s.stride(0), s.stride(1), ptr(qt), qt.stride(0), ptr(st), st.stride(0),
+         st.stride(1), ptr(xq), K, xq.stride(0), ptr(xs), xs.stride(0), xs.stride(1), ptr(xbt),
+         xbt.stride(0), ptr(sblk), sblk.stride(0), stream_of(dy))
     return q, s, qt, st, xbt, sblk
 
 
 @_quant_bwd_op.register_fake
-def _(grad, x_fp8, x_scale, round_scale):
+def _(grad, x_fp8, x_scale, round_scale, col_scales):
     M, N = grad.shape
     K = x_fp8.shape[1]
     return (grad.new_empty((M, N), dtype=torch.float8_e4m3fn),
-            grad.new_empty((M, _cdiv(N, 128)), dtype=torch.float32),
+            _scale_buf(grad, M, _cdiv(N, 128), col_scales),
             grad.new_empty((N, M), dtype=torch.float8_e4m3fn),
-            grad.new_empty((N, _cdiv(M, 128)), dtype=torch.float32),
+            _scale_buf(grad, N, _cdiv(M, 128), col_scales),
             grad.new_empty((K, M), dtype=torch.float8_e4m3fn),
             grad.new_empty((_cdiv(M, 128), _cdiv(K, 128)), dtype=torch.float32))
 
@@ -560,9 +591,10 @@ class FP8MatmulFunction(torch.autograd.Function):
             # x row tiles and weight blocks in one launch; the weight's 16-bit values are
             # exact in fp32, so this equals quantizing weight.float() as the reference does
             x_fp8, x_scale, w_fp8, w_fp8_t, w_scale = quantize_fp8_forward(
-                x_flat, weight, round_scale, with_rowmajor=True, with_transposed=True)
+                x_flat, weight, round_scale, with_rowmajor=True, with_transposed=True, col_scales=True)
         else:
-            x_fp8, x_scale = quantize_fp8_rowwise(x_flat, block_size=128, round_scale=round_scale)
+            x_fp8, x_scale = quantize_fp8_rowwise(x_flat, block_size=128, round_scale=round_scale,
+                                                  col_scales=True)
             w_fp8, w_fp8_t, w_scale = weight_fp8
         out = fp8_gemm_bs(x_fp8, x_scale, w_fp8, w_scale, torch.bfloat16)
         ctx.save_for_backward(x_fp8, x_scale, w_fp8_t, w_scale)
@@ -577,7 +609,7 @@ class FP8MatmulFunction(torch.autograd.Function):
         grad_flat = grad_output.reshape(-1, grad_output.shape[-1])
         # dY row tiles, dY^T row tiles and X^T blocks in one launch
         g_fp8, g_scale, g_fp8_t, g_scale_t, x_blk_t, x_sblk = quantize_fp8_backward(
-            grad_flat, x_fp8, x_scale, ctx.round_scale)
+            grad_flat, x_fp8, x_scale, ctx.round_scale, col_scales=True)
         # dgrad: dX[M, K] = dY[M, N] . W[N, K]; B^T = W^T [K, N], block scales read as [kb, nb]
         grad_x = fp8_gemm_bs(g_fp8, g_scale, w_fp8_t, w_scale.t(), torch.bfloat16)
         # wgrad: dW[N, K] = dY^T[N, M] . X[M, K]; B^T = X^T block codes [K, M]

@@ -11,7 +11,7 @@ from __future__ import annotations
 import torch
 
 from ._lib import call, dtype_code, ptr, stream_of
-from .kernels import (WeightCache, _cdiv, _codes_u8, _rows8, _kcontig, _require,
+from .kernels import (WeightCache, _cdiv, _codes_u8, _rows8, _kcontig, _require, _scale_buf, _scales_2d,
                       _weight_cache_active, custom_op, quantize_fp8_blockwise_t,
                       quantize_fp8_rowwise)
 
@@ -93,7 +93,8 @@ def _ranges(expert_starts: torch.Tensor, expert_ends: torch.Tensor):
 
 
 def quantize_fp8_dual_grouped(grad: torch.Tensor, expert_starts: torch.Tensor,
-                              expert_ends: torch.Tensor, round_scale: bool = False):
+                              expert_ends: torch.Tensor, round_scale: bool = False,
+                              col_scales: bool = False):
     """Grouped dual quantization of an output gradient dC [T, N].
 
     Returns (q [T, N], s [T, ceil(N/128)], qt [N, Tcap], st [N, Tcap/128]):
@@ -105,12 +106,13 @@ def quantize_fp8_dual_grouped(grad: torch.Tensor, expert_starts: torch.Tensor,
     _require(grad.is_cuda, "Input must be on CUDA")
     _require(grad.ndim == 2, "Input must be 2D")
     starts, ends = _ranges(expert_starts, expert_ends)
-    return _dual_grouped_op(grad, starts, ends, bool(round_scale))
+    return _dual_grouped_op(grad, starts, ends, bool(round_scale), bool(col_scales))
 
 
 @custom_op("quant_dual_grouped",
-           "(Tensor grad, Tensor starts, Tensor ends, bool round_scale) -> (Tensor, Tensor, Tensor, Tensor)")
-def _dual_grouped_op(grad, starts, ends, round_scale):
+           "(Tensor grad, Tensor starts, Tensor ends, bool round_scale, bool col_scales) -> "
+           "(Tensor, Tensor, Tensor, Tensor)")
+def _dual_grouped_op(grad, starts, ends, round_scale, col_scales):
     if grad.stride(1) != 1 or (grad.stride(0) * grad.element_size()) % 16 or grad.data_ptr() % 16:
         grad = grad.contiguous()
     T, N = grad.shape
@@ -118,23 +120,23 @@ def _dual_grouped_op(grad, starts, ends, round_scale):
     cap = padded_capacity(T, E)
     dev = grad.device
     q = torch.empty((T, N), dtype=torch.float8_e4m3fn, device=dev)
-    s = torch.empty((T, _cdiv(N, 128)), dtype=torch.float32, device=dev)
+    s = _scale_buf(grad, T, _cdiv(N, 128), col_scales)
     qt = torch.empty((N, cap), dtype=torch.float8_e4m3fn, device=dev)
-    st = torch.empty((N, cap // 128), dtype=torch.float32, device=dev)
+    st = _scale_buf(grad, N, cap // 128, col_scales)
     call("cin_quant_dual_grouped", ptr(grad), dtype_code(grad), T, N, grad.stride(0), ptr(starts),
-         ptr(ends), E, int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), ptr(qt),
-         qt.stride(0), ptr(st), st.stride(0), stream_of(grad))
+         ptr(ends), E, int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), s.stride(1), ptr(qt),
+         qt.stride(0), ptr(st), st.stride(0), st.stride(1), stream_of(grad))
     return q, s, qt, st
 
 
 @_dual_grouped_op.register_fake
-def _(grad, starts, ends, round_scale):
+def _(grad, starts, ends, round_scale, col_scales):
     T, N = grad.shape
     cap = padded_capacity(T, starts.numel())
     return (grad.new_empty((T, N), dtype=torch.float8_e4m3fn),
-            grad.new_empty((T, _cdiv(N, 128)), dtype=torch.float32),
+            _scale_buf(grad, T, _cdiv(N, 128), col_scales),
             grad.new_empty((N, cap), dtype=torch.float8_e4m3fn),
-            grad.new_empty((N, cap // 128), dtype=torch.float32))
+            _scale_buf(grad, N, cap // 128, col_scales))
 
 
 def requantize_grouped_t(x_fp8: torch.Tensor, x_scale: torch.Tensor, expert_starts: torch.Tensor,
@@ -158,8 +160,9 @@ def _requant_grouped_op(x_fp8, x_scale, starts, ends):
     cap = padded_capacity(T, E)
     qbt = torch.empty((K, cap), dtype=torch.float8_e4m3fn, device=q.device)
     sblk = torch.empty((cap // 128, _cdiv(K, 128)), dtype=torch.float32, device=q.device)
-    call("cin_requant_row_to_block_grouped", ptr(q), T, K, q.stride(0), ptr(x_scale),
-         x_scale.stride(0), ptr(starts), ptr(ends), E, ptr(qbt), qbt.stride(0), ptr(sblk),
+    xs = _scales_2d(x_scale)
+    call("cin_requant_row_to_block_grouped", ptr(q), T, K, q.stride(0), ptr(xs), xs.stride(0),
+         xs.stride(1), ptr(starts), ptr(ends), E, ptr(qbt), qbt.stride(0), ptr(sblk),
          sblk.stride(0), stream_of(q))
     return qbt, sblk
 
@@ -194,7 +197,8 @@ def _grouped_wgrad_op(g_t, g_st, x_bt, x_blk, starts, ends, num_tokens, out_dtyp
     a = g_t.view(torch.uint8)
     b = x_bt.view(torch.uint8)
     out = torch.empty((E, N, K), dtype=out_dtype, device=g_t.device)
-    call("cin_grouped_gemm_fp8_wgrad", ptr(a), a.stride(0), ptr(g_st), g_st.stride(0), ptr(b),
+    st = _scales_2d(g_st)
+    call("cin_grouped_gemm_fp8_wgrad", ptr(a), a.stride(0), ptr(st), st.stride(0), st.stride(1), ptr(b),
          b.stride(0), ptr(x_blk), x_blk.stride(0), ptr(starts), ptr(ends), E, int(num_tokens), cap,
          N, K, ptr(out), dtype_code(out), out.stride(1), out.stride(0), stream_of(a))
     return out
@@ -268,33 +272,34 @@ def _empty_rows_zeroed(T: int, ncols: int, dtype: torch.dtype, device, starts, e
 
 
 def silu_mul_quantize_fp8(h12: torch.Tensor, out_dtype: torch.dtype | None = None,
-                          round_scale: bool = False):
+                          round_scale: bool = False, col_scales: bool = False):
     """quantize_fp8_rowwise((silu(h1) * h2).to(out_dtype)) with [h1 h2] = h12.float().chunk(2, -1),
     in one pass over h12 (reference src/layers.py:72-74 feeding src/kernels.py:178-216).
     h12 [M, 2H] (bf16, fp16 or fp32, H a multiple of 8); out_dtype defaults to h12's dtype.
     Returns (codes float8_e4m3fn [M, H], scales fp32 [M, ceil(H/128)])."""
     _require(h12.is_cuda, "Input must be on CUDA")
     _require(h12.ndim == 2 and h12.shape[1] % 2 == 0, "h12 must be [M, 2H]")
-    return _silu_mul_quant_op(h12, out_dtype or h12.dtype, bool(round_scale))
+    return _silu_mul_quant_op(h12, out_dtype or h12.dtype, bool(round_scale), bool(col_scales))
 
 
-@custom_op("silu_mul_quant_rowwise", "(Tensor h12, ScalarType out_dtype, bool round_scale) -> (Tensor, Tensor)")
-def _silu_mul_quant_op(h12, out_dtype, round_scale):
+@custom_op("silu_mul_quant_rowwise",
+           "(Tensor h12, ScalarType out_dtype, bool round_scale, bool col_scales) -> (Tensor, Tensor)")
+def _silu_mul_quant_op(h12, out_dtype, round_scale, col_scales):
     M, H = h12.shape[0], h12.shape[1] // 2
     x = h12 if (h12.stride(1) == 1 and h12.data_ptr() % 16 == 0
                 and (h12.stride(0) * h12.element_size()) % 16 == 0) else h12.contiguous()
     q = torch.empty((M, H), dtype=torch.float8_e4m3fn, device=h12.device)
-    s = torch.empty((M, _cdiv(H, 128)), dtype=torch.float32, device=h12.device)
+    s = _scale_buf(h12, M, _cdiv(H, 128), col_scales)
     call("cin_silu_mul_quant_rowwise", ptr(x), dtype_code(x), M, H, x.stride(0), dtype_code(out_dtype),
-         int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), stream_of(x))
+         int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), s.stride(1), stream_of(x))
     return q, s
 
 
 @_silu_mul_quant_op.register_fake
-def _(h12, out_dtype, round_scale):
+def _(h12, out_dtype, round_scale, col_scales):
     M, H = h12.shape[0], h12.shape[1] // 2
     return (h12.new_empty((M, H), dtype=torch.float8_e4m3fn),
-            h12.new_empty((M, _cdiv(H, 128)), dtype=torch.float32))
+            _scale_buf(h12, M, _cdiv(H, 128), col_scales))
 
 
 def swiglu_backward(dh: torch.Tensor, h12: torch.Tensor) -> torch.Tensor:
@@ -352,7 +357,7 @@ def experts_forward(xq: torch.Tensor, xs: torch.Tensor, w12: torch.Tensor, w3: t
     (w12q, w12qt, w12s), (w3q, w3qt, w3s) = weights_fp8
     h12 = fp8_grouped_gemm(xq, xs, w12q.view(E, H2, D), w12s.view(E, H2 // 128, -1),
                            starts, ends, out_dtype=torch.bfloat16, zero_uncovered=True)
-    hq, hs = silu_mul_quantize_fp8(h12, out_dtype=h_dtype)
+    hq, hs = silu_mul_quantize_fp8(h12, out_dtype=h_dtype, col_scales=True)
     out = fp8_grouped_gemm(hq, hs, w3q.view(E, D, H), w3s.view(E, D // 128, -1), starts, ends,
                            out_dtype=out_dtype, zero_uncovered=True)
     return out, (xq, xs, w12qt, w12s, h12, hq, hs, w3qt, w3s, starts, ends)
@@ -366,14 +371,14 @@ def experts_backward(saved, grad_out: torch.Tensor, dx_dtype: torch.dtype):
     D = xq.shape[1]
     H = hq.shape[1]
     g = grad_out.contiguous()
-    gq, gs, gqt, gst = quantize_fp8_dual_grouped(g, starts, ends)
+    gq, gs, gqt, gst = quantize_fp8_dual_grouped(g, starts, ends, col_scales=True)
     dh = fp8_grouped_dgrad(gq, gs, w3qt, w3s, starts, ends, D, out_dtype=torch.float32,
                            zero_uncovered=True)
     hbt, hblk = requantize_grouped_t(hq, hs, starts, ends)
     dw3 = fp8_grouped_wgrad(gqt, gst, hbt, hblk, starts, ends, g.shape[0])
     # silu(h1) * h2 in fp32 (the forward's cast to the input dtype passes the gradient)
     dh12 = swiglu_backward(dh, h12)
-    dq, ds, dqt, dst = quantize_fp8_dual_grouped(dh12, starts, ends)
+    dq, ds, dqt, dst = quantize_fp8_dual_grouped(dh12, starts, ends, col_scales=True)
     dx = fp8_grouped_dgrad(dq, ds, w12qt, w12s, starts, ends, 2 * H, out_dtype=dx_dtype,
                            zero_uncovered=True)
     xbt, xblk = requantize_grouped_t(xq, xs, starts, ends)
@@ -393,7 +398,7 @@ class FP8GroupedExpertsFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, sorted_x, w12, w3, expert_starts, expert_ends, weights_fp8=None):
         starts, ends = _ranges(expert_starts, expert_ends)
-        xq, xs = quantize_fp8_rowwise(sorted_x)
+        xq, xs = quantize_fp8_rowwise(sorted_x, col_scales=True)
         out, saved = experts_forward(xq, xs, w12, w3, starts, ends, sorted_x.dtype, weights_fp8)
         ctx.save_for_backward(*saved)
         ctx.x_dtype = sorted_x.dtype

@@ -23,7 +23,7 @@ import torch
 
 from . import layers
 from ._lib import call, dtype_code, ptr, stream_of
-from .kernels import _cdiv, _require, custom_op
+from .kernels import _cdiv, _require, _scale_buf, custom_op
 
 _ROUTE_CHUNK = 1024  # assignments per route workgroup (csrc/moe.hip kChunk)
 MAX_EXPERTS = 4096
@@ -80,7 +80,7 @@ def _(idx, n_experts):
 # Gather fused into the 1x128 quantization, and its backward (reference :139-141)
 # ---------------------------------------------------------------------------
 def moe_gather_quantize(x: torch.Tensor, perm: torch.Tensor, top_k: int, round_scale: bool = False,
-                        inv: torch.Tensor | None = None):
+                        inv: torch.Tensor | None = None, col_scales: bool = False):
     """quantize_fp8_rowwise(x[perm // top_k]) bit for bit, without the gathered rows:
     (codes float8_e4m3fn [A, D], scales fp32 [A, ceil(D/128)]); rows where perm is -1 get the
     quantization of a zero row.  With ``inv`` (moe_route's inverse map) each token row is
@@ -92,8 +92,8 @@ def moe_gather_quantize(x: torch.Tensor, perm: torch.Tensor, top_k: int, round_s
     if inv is not None:
         _require(inv.numel() == x.shape[0] * top_k, "inv must hold n_tokens * top_k entries")
         return _scatter_quant_op(x, perm.to(torch.int64), inv.to(torch.int32), int(top_k),
-                                 bool(round_scale))
-    return _gather_quant_op(x, perm.to(torch.int64), int(top_k), bool(round_scale))
+                                 bool(round_scale), bool(col_scales))
+    return _gather_quant_op(x, perm.to(torch.int64), int(top_k), bool(round_scale), bool(col_scales))
 
 
 def _codes_rows8(A, D, like):
@@ -105,23 +105,23 @@ def _codes_rows8(A, D, like):
 
 
 @custom_op("moe_gather_quant_rowwise",
-           "(Tensor x, Tensor perm, int top_k, bool round_scale) -> (Tensor, Tensor)")
-def _gather_quant_op(x, perm, top_k, round_scale):
+           "(Tensor x, Tensor perm, int top_k, bool round_scale, bool col_scales) -> (Tensor, Tensor)")
+def _gather_quant_op(x, perm, top_k, round_scale, col_scales):
     x = _x_rows16(x)
     A = perm.numel()
     T, D = x.shape
     pm = perm.contiguous()
     q = _codes_rows8(A, D, x)
-    s = torch.empty((A, _cdiv(D, 128)), dtype=torch.float32, device=x.device)
+    s = _scale_buf(x, A, _cdiv(D, 128), col_scales)
     call("cin_moe_gather_quant_rowwise", ptr(x), dtype_code(x), T, D, x.stride(0), ptr(pm), A, top_k,
-         int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), stream_of(x))
+         int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), s.stride(1), stream_of(x))
     return q, s
 
 
 @_gather_quant_op.register_fake
-def _(x, perm, top_k, round_scale):
+def _(x, perm, top_k, round_scale, col_scales):
     A, D = perm.shape[0], x.shape[1]
-    return _codes_rows8(A, D, x), x.new_empty((A, _cdiv(D, 128)), dtype=torch.float32)
+    return _codes_rows8(A, D, x), _scale_buf(x, A, _cdiv(D, 128), col_scales)
 
 
 def _x_rows16(x):
@@ -139,23 +139,25 @@ def _x_rows16(x):
 
 
 @custom_op("moe_scatter_quant_rowwise",
-           "(Tensor x, Tensor perm, Tensor inv, int top_k, bool round_scale) -> (Tensor, Tensor)")
-def _scatter_quant_op(x, perm, inv, top_k, round_scale):
+           "(Tensor x, Tensor perm, Tensor inv, int top_k, bool round_scale, bool col_scales) -> "
+           "(Tensor, Tensor)")
+def _scatter_quant_op(x, perm, inv, top_k, round_scale, col_scales):
     x = _x_rows16(x)
     A = perm.numel()
     T, D = x.shape
     pm, iv = perm.contiguous(), inv.contiguous()
     q = _codes_rows8(A, D, x)
-    s = torch.empty((A, _cdiv(D, 128)), dtype=torch.float32, device=x.device)
+    s = _scale_buf(x, A, _cdiv(D, 128), col_scales)
     call("cin_moe_scatter_quant_rowwise", ptr(x), dtype_code(x), T, D, x.stride(0), ptr(iv), top_k,
-         ptr(pm), A, int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), stream_of(x))
+         ptr(pm), A, int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0), s.stride(1),
+         stream_of(x))
     return q, s
 
 
 @_scatter_quant_op.register_fake
-def _(x, perm, inv, top_k, round_scale):
+def _(x, perm, inv, top_k, round_scale, col_scales):
     A, D = perm.shape[0], x.shape[1]
-    return _codes_rows8(A, D, x), x.new_empty((A, _cdiv(D, 128)), dtype=torch.float32)
+    return _codes_rows8(A, D, x), _scale_buf(x, A, _cdiv(D, 128), col_scales)
 
 
 def moe_gather_sum(g: torch.Tensor, inv: torch.Tensor, top_k: int,
@@ -296,7 +298,7 @@ class RoutedExpertsFunction(torch.autograd.Function):
     @staticmethod
     def experts(x, w12, w3, perm, inv, starts, ends, top_k, weights_fp8=None):
         """Sorted expert outputs (fp16 [A, D]) and the tensors their backward needs."""
-        xq, xs = moe_gather_quantize(x, perm, top_k, inv=inv)
+        xq, xs = moe_gather_quantize(x, perm, top_k, inv=inv, col_scales=True)
         return layers.experts_forward(xq, xs, w12, w3, starts, ends, x.dtype, weights_fp8,
                                       out_dtype=torch.float16)
 

@@ -40,6 +40,17 @@ enum cin_status {
 /* Library ABI version (bumped on any signature change). */
 int cin_abi_version(void);
 
+/*
+ * Scale matrices.  Every matrix of per-row (1 x 128) scales below is addressed with two
+ * strides, scale[r, c] = base[r * row stride + c * column stride], and may be row-major
+ * (column stride 1, row stride >= its columns: the reference's layout) or column-major
+ * (row stride 1, column stride >= its rows).  Column-major puts the scales of one
+ * 128-column block of consecutive rows next to each other: the GEMMs read the A scales of
+ * a K block as one contiguous run, and the 128 x 128 tile quantizers write and read a
+ * tile's 128 row scales as one run.  The reference's Python API keeps row-major; the FP8
+ * linear and the experts layer use column-major internally.
+ */
+
 /* Message for the last failing call on this thread ("" if none). */
 const char* cin_last_error(void);
 
@@ -49,12 +60,12 @@ const char* cin_last_error(void);
  * (reference src/kernels.py:178-216 and :19-71).
  *   x      [M, N] of dtype x_dtype, strides (sxm, sxn)
  *   q      [M, N] e4m3 codes, row stride sqm, column stride 1
- *   scales [M, ceil(N/block)] fp32, row stride ssm, column stride 1
+ *   scales [M, ceil(N/block)] fp32, strides (ssm, ssk)
  * block in [1, 1024]; round_scale != 0 selects power-of-two scales.
  */
 int cin_quant_rowwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t sxm, int64_t sxn,
                       int64_t block, int round_scale, uint8_t* q, int64_t sqm, float* scales,
-                      int64_t ssm, void* stream);
+                      int64_t ssm, int64_t ssk, void* stream);
 
 /*
  * Block-wise (bm x bn) quantization.
@@ -80,15 +91,15 @@ int cin_quant_blockwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_
  * (reference src/kernels.py:746-747).  Codes and scales are bit-identical to those two
  * calls; with K % 128 == 0, a 16-bit W and 16-byte aligned rows both run in one launch.
  *   x  [M, K] of dtype x_dtype, row stride sxm (unit column stride)
- *   xq [M, K] codes (row stride sxqm) and xs [M, ceil(K/128)] (row stride sxsm)
+ *   xq [M, K] codes (row stride sxqm) and xs [M, ceil(K/128)] (strides (sxsm, sxsk))
  *   w  [N, K] of dtype w_dtype, row stride swm (unit column stride)
  *   wq [N, K] codes (row stride swqm), or NULL; wqt [K, N] transposed codes (row stride
  *   swqtm), or NULL; at least one of the two.  ws [ceil(N/128), ceil(K/128)] (row stride swsm)
  */
 int cin_quant_fwd(const void* x, int x_dtype, int64_t M, int64_t K, int64_t sxm, int round_scale,
-                  uint8_t* xq, int64_t sxqm, float* xs, int64_t sxsm, const void* w, int w_dtype,
-                  int64_t N, int64_t swm, uint8_t* wq, int64_t swqm, uint8_t* wqt, int64_t swqtm,
-                  float* ws, int64_t swsm, void* stream);
+                  uint8_t* xq, int64_t sxqm, float* xs, int64_t sxsm, int64_t sxsk, const void* w,
+                  int w_dtype, int64_t N, int64_t swm, uint8_t* wq, int64_t swqm, uint8_t* wqt,
+                  int64_t swqtm, float* ws, int64_t swsm, void* stream);
 
 /*
  * Dequantization with (bm x bn) block scales; bm = 1 gives row-wise scales.
@@ -109,24 +120,24 @@ int cin_dequant(const uint8_t* q, int64_t M, int64_t N, int64_t sqm, int64_t sqn
  * quantize_fp8_rowwise(grad_flat.t().contiguous()) in FP8MatmulFunction.backward
  * (reference src/kernels.py:771 and :781-783).
  *   dy [M, N] of dtype dy_dtype, strides (sdm, sdn)
- *   q  [M, N] codes (row stride sqm) and s  [M, ceil(N/128)] (row stride ssm)
- *   qt [N, M] codes (row stride sqtm) and st [N, ceil(M/128)] (row stride sstm)
+ *   q  [M, N] codes (row stride sqm) and s  [M, ceil(N/128)] (strides (ssm, ssk))
+ *   qt [N, M] codes (row stride sqtm) and st [N, ceil(M/128)] (strides (sstm, sstk))
  */
 int cin_quant_dual(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t sdm, int64_t sdn,
-                   int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm,
-                   uint8_t* qt, int64_t sqtm, float* st, int64_t sstm, void* stream);
+                   int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, int64_t ssk,
+                   uint8_t* qt, int64_t sqtm, float* st, int64_t sstm, int64_t sstk, void* stream);
 
 /*
  * Re-quantize 1x128 row-quantized codes into 128x128 blocks, bit-identical to
  * quantize_fp8_blockwise(dequantize_fp8_rowwise(q, s), round_scale=False)
  * (reference src/kernels.py:784-787), without the fp32 temporary.
- *   q    [M, K] codes (row stride sqm), srow [M, ceil(K/128)] (row stride ssm)
+ *   q    [M, K] codes (row stride sqm), srow [M, ceil(K/128)] (strides (ssm, ssk))
  *   qb   optional [M, K] block codes (row stride sqbm) or NULL
  *   qbt  optional [K, M] block codes of the transpose (row stride sqbtm) or NULL
  *   sblk [ceil(M/128), ceil(K/128)] block scales (row stride ssbm)
  */
 int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm,
-                             const float* srow, int64_t ssm, uint8_t* qb, int64_t sqbm,
+                             const float* srow, int64_t ssm, int64_t ssk, uint8_t* qb, int64_t sqbm,
                              uint8_t* qbt, int64_t sqbtm, float* sblk, int64_t ssbm, void* stream);
 
 /*
@@ -137,15 +148,17 @@ int cin_requant_row_to_block(const uint8_t* q, int64_t M, int64_t K, int64_t sqm
  * src/kernels.py:771), quantize_fp8_rowwise(grad_flat.t().contiguous()) (:781-783) and
  * quantize_fp8_blockwise(dequantize_fp8_rowwise(x_fp8, x_scale)) (:784-787).
  *   dy, q, s, qt, st           as cin_quant_dual (sdn = 1)
- *   xq [M, K], xs [M, ceil(K/128)]   the forward's row-wise X codes and scales
+ *   xq [M, K], xs [M, ceil(K/128)]   the forward's row-wise X codes and scales (xs strides
+ *                                    (sxsm, sxsk))
  *   xbt [K, M] block codes of X^T (row stride sxbtm), sblk [ceil(M/128), ceil(K/128)]
  * One launch for 16-bit dy with N and K multiples of 128; otherwise the two calls in turn.
  */
 int cin_quant_backward(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t sdm,
-                       int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, uint8_t* qt,
-                       int64_t sqtm, float* st, int64_t sstm, const uint8_t* xq, int64_t K,
-                       int64_t sxqm, const float* xs, int64_t sxsm, uint8_t* xbt, int64_t sxbtm,
-                       float* sblk, int64_t ssbm, void* stream);
+                       int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, int64_t ssk,
+                       uint8_t* qt, int64_t sqtm, float* st, int64_t sstm, int64_t sstk,
+                       const uint8_t* xq, int64_t K, int64_t sxqm, const float* xs, int64_t sxsm,
+                       int64_t sxsk, uint8_t* xbt, int64_t sxbtm, float* sblk, int64_t ssbm,
+                       void* stream);
 
 /*
  * Byte transpose: dst[c, r] = src[r, c] for an [R, C] matrix of codes.
@@ -206,35 +219,37 @@ int cin_grouped_gemm_fp8(const uint8_t* A, int64_t lda, const float* sa, int64_t
 
 /*
  * Grouped dual quantization of the output gradient dC [T, N] (contiguous rows):
- *   q  [T, N] 1x128 row tiles (row stride sqm), s [T, ceil(N/128)] (row stride ssm)
+ *   q  [T, N] 1x128 row tiles (row stride sqm), s [T, ceil(N/128)] (strides (ssm, ssk))
  *      -- the dgrad operand, as quantize_fp8_rowwise(dC) for every row inside a range;
  *   qt [N, Tpad] per-expert 128x1 column tiles on the padded axis (row stride sqtm =
- *      the padded capacity), st [N, sqtm / 128] (row stride sstm >= sqtm / 128)
+ *      the padded capacity), st [N, sqtm / 128] (strides (sstm, sstk))
  *      -- the wgrad operand, as quantize_fp8_rowwise(dC[s_e:e_e].t()) for each expert.
  */
 int cin_quant_dual_grouped(const void* dy, int dy_dtype, int64_t T, int64_t N, int64_t sdm,
                            const int64_t* starts, const int64_t* ends, int64_t E, int round_scale,
-                           uint8_t* q, int64_t sqm, float* s, int64_t ssm, uint8_t* qt,
-                           int64_t sqtm, float* st, int64_t sstm, void* stream);
+                           uint8_t* q, int64_t sqm, float* s, int64_t ssm, int64_t ssk, uint8_t* qt,
+                           int64_t sqtm, float* st, int64_t sstm, int64_t sstk, void* stream);
 
 /*
  * Grouped re-quantization of the expert inputs for wgrad: for each expert, 128x128 blocks
  * of quantize_fp8_blockwise(dequantize_fp8_rowwise(q, srow)[s_e:e_e]) (reference
  * src/kernels.py:784-787 per slice), written transposed on the padded axis:
- *   q    [T, K] row-wise codes (row stride sqm), srow [T, ceil(K/128)] (row stride ssm)
+ *   q    [T, K] row-wise codes (row stride sqm), srow [T, ceil(K/128)] (strides (ssm, ssk))
  *   qbt  [K, Tpad] block codes (row stride sqbtm = padded capacity)
  *   sblk [sqbtm / 128, ceil(K/128)] block scales, row = padded chunk (row stride ssbm)
  */
 int cin_requant_row_to_block_grouped(const uint8_t* q, int64_t T, int64_t K, int64_t sqm,
-                                     const float* srow, int64_t ssm, const int64_t* starts,
-                                     const int64_t* ends, int64_t E, uint8_t* qbt, int64_t sqbtm,
-                                     float* sblk, int64_t ssbm, void* stream);
+                                     const float* srow, int64_t ssm, int64_t ssk,
+                                     const int64_t* starts, const int64_t* ends, int64_t E,
+                                     uint8_t* qbt, int64_t sqbtm, float* sblk, int64_t ssbm,
+                                     void* stream);
 
 /*
  * Grouped weight gradient, one launch over all experts:
  *   C_e[n, k] = sum over expert e's padded chunks j of
  *               sa[n, j] * sb[j, k / 128] * sum_{t in chunk j} A[n, t] * B[k, t]
- * i.e. dW_e = dC_e^T X_e with A = qt/st of cin_quant_dual_grouped (A[N, Tpad], lda) and
+ * i.e. dW_e = dC_e^T X_e with A = qt/st of cin_quant_dual_grouped (A[N, Tpad], lda; st
+ * strides (ssam, ssak), row- or column-major) and
  * B = qbt/sblk of cin_requant_row_to_block_grouped (B[K, Tpad], ldb; sb row stride ssbm).
  * T is the token count the ranges refer to; tcap the padded columns A and B hold (an
  * expert whose padded range would pass tcap gets zeros).  C is [E, N, K] (row stride
@@ -242,7 +257,7 @@ int cin_requant_row_to_block_grouped(const uint8_t* q, int64_t T, int64_t K, int
  * Needs N >= 256, K >= 256, K % 128 == 0.
  */
 int cin_grouped_gemm_fp8_wgrad(const uint8_t* A, int64_t lda, const float* sa, int64_t ssam,
-                               const uint8_t* B, int64_t ldb, const float* sb, int64_t ssbm,
+                               int64_t ssak, const uint8_t* B, int64_t ldb, const float* sb, int64_t ssbm,
                                const int64_t* starts, const int64_t* ends, int64_t E, int64_t T,
                                int64_t tcap, int64_t N, int64_t K, void* C, int c_dtype,
                                int64_t ldc, int64_t sce, void* stream);
@@ -268,13 +283,13 @@ int cin_grouped_gemm_f16(const void* A, int a_dtype, int64_t lda, const void* B,
  *   h1, h2 = h12.float().chunk(2, -1);  h = (silu(h1) * h2).to(dtype)
  * followed by quantize_fp8_rowwise(h) (src/kernels.py:178-216) before the down GEMM:
  *   h12    [M, 2H] of in_dtype (row stride s12; both halves 16-byte aligned)
- *   q      [M, H] codes (row stride sqm), scales [M, ceil(H/128)] (row stride ssm)
+ *   q      [M, H] codes (row stride sqm), scales [M, ceil(H/128)] (strides (ssm, ssk))
  *   out_dtype is the dtype h is rounded to before quantization (the activation dtype).
  * silu(a) = a / (1 + exp(-a)) with an IEEE division, torch's GPU formula.
  */
 int cin_silu_mul_quant_rowwise(const void* h12, int in_dtype, int64_t M, int64_t H, int64_t s12,
                                int out_dtype, int round_scale, uint8_t* q, int64_t sqm,
-                               float* scales, int64_t ssm, void* stream);
+                               float* scales, int64_t ssm, int64_t ssk, void* stream);
 
 /*
  * SwiGLU backward in one pass, replacing the elementwise chain of the experts' backward
@@ -388,24 +403,25 @@ int cin_moe_route_noalloc(const int64_t* idx, int64_t T, int64_t k, int64_t E, i
  * (src/kernels.py:178-216): the gathered bf16 rows are never written.
  *   x [src_rows, N], rows 16-byte aligned (sxm elements apart); rowmap [rows] int64
  *   (perm from cin_moe_route, rowdiv = k); q [rows, N] (8-byte aligned rows),
- *   scales [rows, ceil(N/128)] fp32.
+ *   scales [rows, ceil(N/128)] fp32 (strides (ssm, ssk)).
  */
 int cin_moe_gather_quant_rowwise(const void* x, int x_dtype, int64_t src_rows, int64_t N,
                                  int64_t sxm, const int64_t* rowmap, int64_t rows, int64_t rowdiv,
                                  int round_scale, uint8_t* q, int64_t sqm, float* scales,
-                                 int64_t ssm, void* stream);
+                                 int64_t ssm, int64_t ssk, void* stream);
 
 /*
  * The same codes and scales as cin_moe_gather_quant_rowwise(x, perm, k), computed from the
  * token side: token row t is quantized once and written to its sorted rows inv[t*k + j]
  * (one read of x instead of k); rows r with perm[r] < 0 get the zero-row quantization.
  *   x [T, N] (16-byte aligned rows), inv [T*k] int32 and perm [rows] int64 from
- *   cin_moe_route, q [rows, N] (8-byte aligned rows), scales [rows, ceil(N/128)].
+ *   cin_moe_route, q [rows, N] (8-byte aligned rows), scales [rows, ceil(N/128)] (strides
+ *   (ssm, ssk)).
  */
 int cin_moe_scatter_quant_rowwise(const void* x, int x_dtype, int64_t T, int64_t N, int64_t sxm,
                                   const int32_t* inv, int64_t k, const int64_t* perm, int64_t rows,
                                   int round_scale, uint8_t* q, int64_t sqm, float* scales,
-                                  int64_t ssm, void* stream);
+                                  int64_t ssm, int64_t ssk, void* stream);
 
 /*
  * Backward of the dispatch gather: out[t] = sum over token t's sorted positions r

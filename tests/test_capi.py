@@ -34,7 +34,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().cin_abi_version() == 2
+    assert _lib.load().cin_abi_version() == 3
 
 
 def test_no_rpath_to_a_second_hip_runtime():
@@ -44,37 +44,43 @@ def test_no_rpath_to_a_second_hip_runtime():
 
 
 @pytest.mark.parametrize("call", [
-    ("cin_quant_rowwise", (None, 7, 4, 128, 128, 1, 128, 0, None, 128, None, 1, None)),   # bad dtype
-    ("cin_quant_rowwise", (None, 0, 4, 128, 128, 1, 0, 0, None, 128, None, 1, None)),     # block 0
-    ("cin_quant_rowwise", (None, 0, 4, 128, 128, 1, 128, 0, None, 128, None, 1, None)),   # null ptr
+    ("cin_quant_rowwise", (None, 7, 4, 128, 128, 1, 128, 0, None, 128, None, 1, 1, None)),   # bad dtype
+    ("cin_quant_rowwise", (None, 0, 4, 128, 128, 1, 0, 0, None, 128, None, 1, 1, None)),     # block 0
+    ("cin_quant_rowwise", (None, 0, 4, 128, 128, 1, 128, 0, None, 128, None, 1, 1, None)),   # null ptr
+    ("cin_quant_rowwise", (1, 0, 4, 256, 256, 1, 128, 0, 1, 256, 1, 2, 2, None)),            # scales overlap
     ("cin_quant_blockwise", (None, 0, 4, 4, 4, 1, 2048, 2048, 0, None, 4, None, 0, None, 1, None)),
     ("cin_gemm_fp8_bs", (None, 32, None, 1, 1, None, 32, None, 1, 1, 4, 4, 24, None, 0, 4, None)),
     ("cin_gemm_fp8_bs", (None, 32, None, 1, 1, None, 32, None, 1, 1, 4, 4, 32, None, 5, 4, None)),
     ("cin_dequant", (None, 4, 4, 4, 1, None, 1, 1, 1, 128, None, 2, 4, None)),            # fp16 out
-    # quant_fwd: x, xdt, M, K, sxm, rs, xq, sxqm, xs, sxsm, w, wdt, N, swm, wq, swqm, wqt, swqtm, ws, swsm, s
-    ("cin_quant_fwd", (None, 9, 4, 256, 256, 0, None, 256, None, 2, None, 0, 256, 256, None, 256, None, 0,
+    # quant_fwd: x, xdt, M, K, sxm, rs, xq, sxqm, xs, sxsm, sxsk, w, wdt, N, swm, wq, swqm, wqt, swqtm, ws,
+    #            swsm, s
+    ("cin_quant_fwd", (None, 9, 4, 256, 256, 0, None, 256, None, 2, 1, None, 0, 256, 256, None, 256, None, 0,
                        None, 2, None)),                                                     # bad x dtype
-    ("cin_quant_fwd", (None, 0, 4, 256, 256, 0, None, 256, None, 2, None, 0, 256, 256, None, 256, None, 0,
+    ("cin_quant_fwd", (None, 0, 4, 256, 256, 0, None, 256, None, 2, 1, None, 0, 256, 256, None, 256, None, 0,
                        None, 2, None)),                                                     # null pointers
-    ("cin_quant_fwd", (1, 0, 4, 256, 256, 0, 1, 128, 1, 2, 1, 0, 256, 256, 1, 256, None, 0,
+    ("cin_quant_fwd", (1, 0, 4, 256, 256, 0, 1, 128, 1, 2, 1, 1, 0, 256, 256, 1, 256, None, 0,
                        1, 2, None)),                                                        # xq stride < K
-    ("cin_quant_fwd", (1, 0, 4, 256, 256, 0, 1, 256, 1, 2, 1, 0, 256, 256, None, 256, None, 0,
+    ("cin_quant_fwd", (1, 0, 4, 256, 256, 0, 1, 256, 1, 2, 1, 1, 0, 256, 256, None, 256, None, 0,
                        1, 2, None)),                                                        # no weight output
-    # quant_backward: dy, dt, M, N, sdm, rs, q, sqm, s, ssm, qt, sqtm, st, sstm, xq, K, sxqm, xs, sxsm,
-    #                 xbt, sxbtm, sblk, ssbm, stream
-    ("cin_quant_backward", (None, 9, 256, 256, 256, 0, None, 256, None, 2, None, 256, None, 2, None, 256, 256,
-                            None, 2, None, 256, None, 2, None)),                            # bad dtype
-    ("cin_quant_backward", (None, 0, 256, 256, 256, 0, None, 256, None, 2, None, 256, None, 2, None, 256, 256,
-                            None, 2, None, 256, None, 2, None)),                            # null pointers
-    ("cin_quant_backward", (1, 0, 256, 256, 256, 0, 1, 256, 1, 2, 1, 256, 1, 2, 8, 256, 128,
-                            1, 2, 8, 256, 1, 2, None)),                                     # X stride < K
+    ("cin_quant_fwd", (1, 0, 4, 256, 256, 0, 1, 256, 1, 1, 3, 1, 0, 256, 256, 1, 256, None, 0,
+                       1, 2, None)),                                                        # xs column stride < M
+    # quant_backward: dy, dt, M, N, sdm, rs, q, sqm, s, ssm, ssk, qt, sqtm, st, sstm, sstk, xq, K, sxqm,
+    #                 xs, sxsm, sxsk, xbt, sxbtm, sblk, ssbm, stream
+    ("cin_quant_backward", (None, 9, 256, 256, 256, 0, None, 256, None, 2, 1, None, 256, None, 2, 1, None, 256,
+                            256, None, 2, 1, None, 256, None, 2, None)),                    # bad dtype
+    ("cin_quant_backward", (None, 0, 256, 256, 256, 0, None, 256, None, 2, 1, None, 256, None, 2, 1, None, 256,
+                            256, None, 2, 1, None, 256, None, 2, None)),                    # null pointers
+    ("cin_quant_backward", (1, 0, 256, 256, 256, 0, 1, 256, 1, 2, 1, 1, 256, 1, 2, 1, 8, 256, 128,
+                            1, 2, 1, 8, 256, 1, 2, None)),                                  # X stride < K
+    ("cin_quant_backward", (1, 0, 256, 256, 256, 0, 1, 256, 1, 1, 2, 1, 256, 1, 2, 1, 8, 256, 256,
+                            1, 2, 1, 8, 256, 1, 2, None)),                                  # s column stride < M
     ("cin_moe_route", (None, 16, 2, 0, None, None, None, None, None, None, 0, None)),        # E = 0
     ("cin_moe_route", (None, 16, 2, 5000, None, None, None, None, None, None, 0, None)),     # E > 4096
     ("cin_moe_route", (None, 16, 2, 8, None, None, None, None, None, None, 0, None)),        # null ptrs
     ("cin_moe_gather_sum", (None, 1, 8, None, 4, 17, 68, 8, None, 1, 8, None)),              # k > 16
     ("cin_moe_combine", (None, 1, 8, None, 7, 2, None, 4, 2, 8, 8, None, 8, None)),          # bad score dtype
     ("cin_moe_combine", (None, 5, 8, None, 1, 2, None, 4, 2, 8, 8, None, 8, None)),          # bad y dtype
-    ("cin_moe_gather_quant_rowwise", (None, 0, 4, 256, 256, None, 8, 0, 0, None, 256, None, 2, None)),
+    ("cin_moe_gather_quant_rowwise", (None, 0, 4, 256, 256, None, 8, 0, 0, None, 256, None, 2, 1, None)),
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 2, 48, 0.1, None, None)),   # d % 32
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 2, 288, 0.1, None, None)),  # d > 256
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 0, 64, 0.1, None, None)),   # H = 0
@@ -93,15 +99,15 @@ def test_invalid_arguments_rejected_without_gpu(call):
 def test_empty_shapes_are_noops():
     lib = _lib.load()
     # M == 0: nothing to do, no device touched
-    assert lib.cin_quant_rowwise(None, 0, 0, 128, 128, 1, 128, 0, None, 128, None, 1, None) == 0
+    assert lib.cin_quant_rowwise(None, 0, 0, 128, 128, 1, 128, 0, None, 128, None, 1, 1, None) == 0
     assert lib.cin_gemm_fp8_bs(None, 32, None, 1, 1, None, 32, None, 1, 1, 0, 4, 32, None, 0, 4, None) == 0
     assert lib.cin_moe_gather_sum(None, 1, 8, None, 0, 2, 0, 8, None, 1, 8, None) == 0
     assert lib.cin_moe_combine(None, 1, 8, None, 1, 2, None, 0, 2, 0, 8, None, 8, None) == 0
     assert lib.cin_indexer_scores_fp8(None, None, None, None, None, 1, 0, 8, 2, 64, 0.1, None, None) == 0
-    assert lib.cin_quant_fwd(None, 0, 0, 256, 256, 0, None, 256, None, 2, None, 0, 0, 256, None, 256, None, 0,
-                             None, 2, None) == 0
-    assert lib.cin_quant_backward(None, 0, 0, 256, 256, 0, None, 256, None, 2, None, 0, None, 0, None, 256,
-                                  256, None, 2, None, 0, None, 2, None) == 0
+    assert lib.cin_quant_fwd(None, 0, 0, 256, 256, 0, None, 256, None, 2, 1, None, 0, 0, 256, None, 256, None,
+                             0, None, 2, None) == 0
+    assert lib.cin_quant_backward(None, 0, 0, 256, 256, 0, None, 256, None, 2, 1, None, 0, None, 0, 1, None,
+                                  256, 256, None, 2, 1, None, 0, None, 2, None) == 0
 
 
 def test_indexer_weights_grad_workspace_size():

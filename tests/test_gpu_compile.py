@@ -91,10 +91,11 @@ def test_opcheck_operators(dev):
     # only, and fp8 inputs go in as their uint8 views (the operators take either)
     full, f8 = ("test_schema", "test_faketensor"), ("test_faketensor",)
     ops = torch.ops.cinnamon_amd
-    torch.library.opcheck(ops.quant_rowwise.default, (x, 128, False), test_utils=f8)
+    for col in (False, True):  # row-major and column-major scale outputs (same strides in the fake)
+        torch.library.opcheck(ops.quant_rowwise.default, (x, 128, False, col), test_utils=f8)
+        torch.library.opcheck(ops.quant_dual.default, (x, False, col), test_utils=f8)
     torch.library.opcheck(ops.quant_blockwise.default, (x, 128, 128, True), test_utils=f8)
     torch.library.opcheck(ops.quant_blockwise_t.default, (x.float(), False, False), test_utils=f8)
-    torch.library.opcheck(ops.quant_dual.default, (x, False), test_utils=f8)
     q, s = kernels.quantize_fp8_rowwise(x)
     torch.library.opcheck(ops.requant_row_to_block.default, (q, s, True), test_utils=f8)
     q8 = q.view(torch.uint8)
@@ -105,8 +106,9 @@ def test_opcheck_operators(dev):
     torch.library.opcheck(ops.gemm_fp8_bs.default, (q8, s, wq8, ws, torch.float32), test_utils=full)
     torch.library.opcheck(ops.transpose_u8.default, (q8,), test_utils=full)
     h12 = torch.randn(256, 512, device=dev, generator=g).to(torch.bfloat16)
-    torch.library.opcheck(ops.silu_mul_quant_rowwise.default, (h12, torch.bfloat16, False),
-                          test_utils=f8)
+    for col in (False, True):
+        torch.library.opcheck(ops.silu_mul_quant_rowwise.default, (h12, torch.bfloat16, False, col),
+                              test_utils=f8)
     dh = torch.randn(256, 256, device=dev, generator=g)
     torch.library.opcheck(ops.swiglu_backward.default, (dh, h12), test_utils=full)
     # indexer: quantization (fp8 outputs), scores and weights gradient (uint8 code inputs)

@@ -371,7 +371,8 @@ def test_grouped_wgrad_direct_epilogue(kern, dev, out_dtype):
     sce = N * K + 1
     buf = torch.full((E * sce,), 5.0, dtype=out_dtype, device=dev)
     a, b = qt.view(torch.uint8), xbt.view(torch.uint8)
-    _lib.call("cin_grouped_gemm_fp8_wgrad", _lib.ptr(a), a.stride(0), _lib.ptr(st), st.stride(0), _lib.ptr(b),
+    _lib.call("cin_grouped_gemm_fp8_wgrad", _lib.ptr(a), a.stride(0), _lib.ptr(st), st.stride(0), st.stride(1),
+              _lib.ptr(b),
               b.stride(0), _lib.ptr(xblk), xblk.stride(0), _lib.ptr(sd), _lib.ptr(ed), E, T, a.shape[1], N, K,
               _lib.ptr(buf), _lib.dtype_code(buf), K, sce, _lib.stream_of(a))
     torch.cuda.synchronize()
