@@ -578,8 +578,9 @@ def main():
     full = args.only is None and not args.no_extra
     if full or (args.only or "").startswith("moe"):
         moe = moe_setup(dev)
-        hq, hs = kernels.quantize_fp8_rowwise(moe["h"])
-        xq3, xs3 = kernels.quantize_fp8_rowwise(moe["x"])
+        # the experts' activation scales are column-major, as layers.experts_forward keeps them
+        hq, hs = kernels.quantize_fp8_rowwise(moe["h"], col_scales=True)
+        xq3, xs3 = kernels.quantize_fp8_rowwise(moe["x"], col_scales=True)
         y12 = torch.empty((moe["A"], 2 * moe["H"]), dtype=torch.bfloat16, device=dev)
         y3 = torch.empty((moe["A"], moe["D"]), dtype=torch.bfloat16, device=dev)
 
@@ -596,14 +597,15 @@ def main():
     if full or args.only in ("moe_dual", "moe_requant", "moe_wgrad", "moe_dgrad"):
         if moe is None:
             moe = moe_setup(dev)
-            xq3, xs3 = kernels.quantize_fp8_rowwise(moe["x"])
+            xq3, xs3 = kernels.quantize_fp8_rowwise(moe["x"], col_scales=True)
         mb = moe_bwd_setup(dev, moe)
-        gq3, gs3, gqt3, gst3 = layers.quantize_fp8_dual_grouped(mb["dh12"], moe["starts"], moe["ends"])
+        gq3, gs3, gqt3, gst3 = layers.quantize_fp8_dual_grouped(mb["dh12"], moe["starts"], moe["ends"],
+                                                                col_scales=True)
         xbt3, xbs3 = layers.requantize_grouped_t(xq3, xs3, moe["starts"], moe["ends"])
         dx3 = torch.empty((moe["A"], moe["D"]), dtype=torch.bfloat16, device=dev)
 
     def moe_dual(i):
-        layers.quantize_fp8_dual_grouped(mb["dh12"], moe["starts"], moe["ends"])
+        layers.quantize_fp8_dual_grouped(mb["dh12"], moe["starts"], moe["ends"], col_scales=True)
 
     def moe_requant(i):
         layers.requantize_grouped_t(xq3, xs3, moe["starts"], moe["ends"])
@@ -694,7 +696,7 @@ def main():
         moe_ops.moe_route(md["sel"], moe["E"])
 
     def moe_gather(i):
-        moe_ops.moe_gather_quantize(md["x"], md["perm"], moe["topk"], inv=md["inv"])
+        moe_ops.moe_gather_quantize(md["x"], md["perm"], moe["topk"], inv=md["inv"], col_scales=True)
 
     def moe_combine(i):
         moe_ops.moe_combine(md["ys16"], md["scores"], md["inv"])
@@ -705,7 +707,7 @@ def main():
 
     def moe_dispatch_fused(i):
         perm, inv, *_ = moe_ops.moe_route(md["sel"], moe["E"])
-        moe_ops.moe_gather_quantize(md["x"], perm, moe["topk"], inv=inv)
+        moe_ops.moe_gather_quantize(md["x"], perm, moe["topk"], inv=inv, col_scales=True)
 
     def moe_dispatch_torch(i):
         k = moe["topk"]
