@@ -51,6 +51,8 @@ SIGNATURES: dict[str, list] = {
                                    _i64, _i64, _i64, _p, _i32, _i64, _i64, _p],
     "cin_silu_mul_quant_rowwise": [_p, _i32, _i64, _i64, _i64, _i32, _i32, _p, _i64, _p, _i64, _i64, _p],
     "cin_swiglu_backward": [_p, _i64, _p, _i32, _i64, _i64, _i64, _p, _i64, _p],
+    "cin_swiglu_dual_grouped": [_p, _i64, _p, _i32, _i64, _i64, _i64, _p, _p, _i64, _i32, _p, _i64, _p,
+                                _i64, _i64, _p, _i64, _p, _i64, _i64, _p],
     "cin_zero_rows_outside_ranges": [_p, _i64, _i64, _i64, _p, _p, _i64, _p],
     "cin_indexer_quantize": [_p, _i32, _p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p],
     "cin_indexer_scores_fp8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p,

@@ -1192,6 +1192,72 @@ __global__ __launch_bounds__(kThreads, (DT == CIN_DT_F32 && !EDGE) ? 3 : 1) void
                      vec_t != 0, st, sstm, sstk, sm);
 }
 
+// ----------------------------- SwiGLU backward + grouped dual -----------------------------
+// The experts' backward computes dh12 = [dh * h2 * silu'(h1), dh * silu(h1)] ([h1 h2] = h12)
+// and quantizes it both ways (k_swiglu_backward, then k_dual128_grouped).  This kernel does
+// both in registers, so the fp32 dh12 [T, 2H] is never written or read back: a tile is a
+// 128-token chunk x 128 columns of the first half; its pieces of dh, h1 and h2 give the
+// dh12 tile of column block cb (first half) and of cb + H / 128 (second half, the same dh and
+// h1), each quantized by dual_body.  The arithmetic is k_swiglu_backward's, operation for
+// operation, and the tiles are k_dual128_grouped's, so the codes and scales are the same.
+// H % 128 == 0 (a column block never straddles the halves).
+template <int IT>
+struct SwiRaw {
+  RawIn<CIN_DT_F32> dh;
+  RawIn<IT> a, b;  // h1, h2
+};
+
+template <int IT>
+__device__ __forceinline__ void swiglu_dual_vals(const SwiRaw<IT>& r, RawIn<CIN_DT_F32>& d1,
+                                                 RawIn<CIN_DT_F32>& d2) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float gv = in_val<CIN_DT_F32>(r.dh, i, j);
+      const float a = in_val<IT>(r.a, i, j), b = in_val<IT>(r.b, i, j);
+      const float sig = 1.0f / (1.0f + expf(-a));
+      const float t = sig * (1.0f + a * (1.0f - sig));
+      d1.w[i][j] = __float_as_uint(gv * b * t);
+      d2.w[i][j] = __float_as_uint(gv * (a * sig));
+      // both values held as computed: otherwise the second is formed after the first
+      // tile's quantization, keeping dh, h1 and the sigmoid live across it
+      opaque(d1.w[i][j]);
+      opaque(d2.w[i][j]);
+    }
+  }
+}
+
+template <int IT>
+__global__ __launch_bounds__(kThreads, 2) void k_swiglu_dual128_grouped(
+    const float* __restrict__ dh, int64_t sdm, const void* __restrict__ h12, int64_t s12, int64_t T,
+    int64_t H, int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, int64_t ssk, uint8_t* qt,
+    int64_t sqtm, int vec_t, float* st, int64_t sstm, int64_t sstk, const int64_t* __restrict__ starts,
+    const int64_t* __restrict__ ends, int64_t E, int64_t tcap, uint32_t nbh, uint32_t ntiles) {
+  __shared__ DualSmem sm;
+  GroupedTiles geo = grouped_tiles(starts, ends, E, T, tcap, nbh, 0);
+  const int64_t N = 2 * H;
+  auto ld = [&](const TileGeo& g, SwiRaw<IT>& r) {
+    load_in<CIN_DT_F32, false>(dh, sdm, H, g, r.dh);
+    load_in<IT, false>(h12, s12, N, g, r.a);
+    TileGeo g2 = g;
+    g2.cb += nbh;
+    load_in<IT, false>(h12, s12, N, g2, r.b);
+  };
+  auto pr = [&](const TileGeo& g, SwiRaw<IT>& r) {
+    if (g.nr == 0) return;  // uniform over the workgroup
+    RawIn<CIN_DT_F32> d1, d2;
+    swiglu_dual_vals<IT>(r, d1, d2);
+    dual_body<CIN_DT_F32, false>(d1, g, N, round_scale != 0, q, sqm, s, ssm, ssk, qt, sqtm, vec_t != 0, st,
+                                 sstm, sstk, sm);
+    TileGeo g2 = g;
+    g2.cb += nbh;
+    dual_body<CIN_DT_F32, false>(d2, g2, N, round_scale != 0, q, sqm, s, ssm, ssk, qt, sqtm, vec_t != 0, st,
+                                 sstm, sstk, sm);
+  };
+  tile_loop_single<SwiRaw<IT>>(ntiles, geo, ld, pr);
+}
+
 // ----------------------------- row -> block re-quantization -----------------------------
 // x = fp32(code) * srow (fp32 product, as the reference's dequantize_fp8_rowwise), then
 // the block quantizer with the fp32 floor and round_scale = False (reference
@@ -1996,6 +2062,44 @@ int cin_quant_dual_grouped(const void* dy, int dy_dtype, int64_t T, int64_t N, i
 #undef CIN_DUALG_ALL
 #undef CIN_DUALG
   return cin_check_launch("quant_dual_grouped");
+}
+
+int cin_swiglu_dual_grouped(const float* dh, int64_t sdm, const void* h12, int h12_dtype, int64_t s12,
+                            int64_t T, int64_t H, const int64_t* starts, const int64_t* ends, int64_t E,
+                            int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, int64_t ssk,
+                            uint8_t* qt, int64_t sqtm, float* st, int64_t sstm, int64_t sstk, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(h12_dtype), "swiglu_dual_grouped: unsupported h12 dtype %d", h12_dtype);
+  CIN_CHECK_ARG(T >= 0 && H >= 0 && E >= 0, "swiglu_dual_grouped: negative shape");
+  if (T == 0 || H == 0 || E == 0) return CIN_OK;
+  CIN_CHECK_ARG(dh && h12 && q && s && qt && st && starts && ends, "swiglu_dual_grouped: null pointer");
+  CIN_CHECK_ARG(H % 128 == 0, "swiglu_dual_grouped: H (%lld) must be a multiple of 128", (long long)H);
+  const int es = elem_size(h12_dtype);
+  const int64_t N = 2 * H;
+  CIN_CHECK_ARG(aligned(dh, 16) && (sdm * 4) % 16 == 0 && sdm >= H && aligned(h12, 16) &&
+                    (s12 * es) % 16 == 0 && s12 >= N,
+                "swiglu_dual_grouped: dh and h12 rows must be contiguous and 16-byte aligned");
+  CIN_CHECK_ARG(aligned(q, 8) && sqm % 8 == 0 && sqm >= N && scale_layout_ok(T, N / 128, ssm, ssk),
+                "swiglu_dual_grouped: bad row-wise outputs");
+  CIN_CHECK_ARG(sqtm >= 128 && scale_layout_ok(N, sqtm / 128, sstm, sstk),
+                "swiglu_dual_grouped: transposed rows must hold the padded token axis");
+  CIN_CHECK_ARG((cdiv(T, 128) + E) * (H / 128) < ((int64_t)1 << 31), "swiglu_dual_grouped: too many tiles");
+  CIN_CHECK_ARG(tile_fits32(sdm * 4) && tile_fits32(s12 * es) && tile_fits32(sqm) && tile_fits32(sqtm),
+                "swiglu_dual_grouped: row strides too large");
+  const int vec_t = aligned(qt, 16) && sqtm % 16 == 0;
+  const uint32_t nbh = (uint32_t)(H / 128), nt = (uint32_t)(cdiv(T, 128) + E) * nbh;
+  hipStream_t stream_ = static_cast<hipStream_t>(stream);
+#define CIN_SWID(IT)                                                                                   \
+  hipLaunchKernelGGL((k_swiglu_dual128_grouped<IT>), resident_grid<k_swiglu_dual128_grouped<IT>>(nt),  \
+                     kThreads, 0, stream_, dh, sdm, h12, s12, T, H, round_scale, q, sqm, s, ssm, ssk, qt,  \
+                     sqtm, vec_t, st, sstm, sstk, starts, ends, E, sqtm, nbh, nt)
+  if (h12_dtype == CIN_DT_BF16)
+    CIN_SWID(CIN_DT_BF16);
+  else if (h12_dtype == CIN_DT_F16)
+    CIN_SWID(CIN_DT_F16);
+  else
+    CIN_SWID(CIN_DT_F32);
+#undef CIN_SWID
+  return cin_check_launch("swiglu_dual_grouped");
 }
 
 int cin_requant_row_to_block_grouped(const uint8_t* q, int64_t T, int64_t K, int64_t sqm,

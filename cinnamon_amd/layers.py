@@ -328,6 +328,54 @@ def _(dh, h12):
     return dh.new_empty((dh.shape[0], 2 * dh.shape[1]), dtype=torch.float32)
 
 
+def swiglu_backward_dual_grouped(dh: torch.Tensor, h12: torch.Tensor, expert_starts: torch.Tensor,
+                                  expert_ends: torch.Tensor, round_scale: bool = False,
+                                  col_scales: bool = False):
+    """quantize_fp8_dual_grouped(swiglu_backward(dh, h12), ...) in one pass, with the same
+    outputs bit for bit: the fp32 gradient [T, 2H] is formed tile by tile and never stored.
+    H % 128 == 0; other widths take the two calls."""
+    _require(dh.is_cuda and h12.is_cuda, "Input must be on CUDA")
+    T, H = dh.shape
+    _require(h12.shape == (T, 2 * H), "h12 must be [T, 2H]")
+    starts, ends = _ranges(expert_starts, expert_ends)
+    if H % 128 != 0:
+        return _dual_grouped_op(_swiglu_backward_op(dh, h12), starts, ends, bool(round_scale),
+                                bool(col_scales))
+    return _swiglu_dual_grouped_op(dh, h12, starts, ends, bool(round_scale), bool(col_scales))
+
+
+@custom_op("swiglu_dual_grouped",
+           "(Tensor dh, Tensor h12, Tensor starts, Tensor ends, bool round_scale, bool col_scales) -> "
+           "(Tensor, Tensor, Tensor, Tensor)")
+def _swiglu_dual_grouped_op(dh, h12, starts, ends, round_scale, col_scales):
+    T, H = dh.shape
+    g = dh if (dh.dtype == torch.float32 and dh.stride(1) == 1 and dh.stride(0) % 4 == 0
+               and dh.data_ptr() % 16 == 0) else dh.float().contiguous()
+    x = h12 if (h12.stride(1) == 1 and (h12.stride(0) * h12.element_size()) % 16 == 0
+                and h12.data_ptr() % 16 == 0) else h12.contiguous()
+    E = starts.numel()
+    cap = padded_capacity(T, E)
+    dev = dh.device
+    q = torch.empty((T, 2 * H), dtype=torch.float8_e4m3fn, device=dev)
+    s = _scale_buf(g, T, 2 * H // 128, col_scales)
+    qt = torch.empty((2 * H, cap), dtype=torch.float8_e4m3fn, device=dev)
+    st = _scale_buf(g, 2 * H, cap // 128, col_scales)
+    call("cin_swiglu_dual_grouped", ptr(g), g.stride(0), ptr(x), dtype_code(x), x.stride(0), T, H,
+         ptr(starts), ptr(ends), E, int(round_scale), ptr(q), q.stride(0), ptr(s), s.stride(0),
+         s.stride(1), ptr(qt), qt.stride(0), ptr(st), st.stride(0), st.stride(1), stream_of(g))
+    return q, s, qt, st
+
+
+@_swiglu_dual_grouped_op.register_fake
+def _(dh, h12, starts, ends, round_scale, col_scales):
+    T, H = dh.shape
+    cap = padded_capacity(T, starts.numel())
+    return (dh.new_empty((T, 2 * H), dtype=torch.float8_e4m3fn),
+            _scale_buf(dh, T, 2 * H // 128, col_scales),
+            dh.new_empty((2 * H, cap), dtype=torch.float8_e4m3fn),
+            _scale_buf(dh, 2 * H, cap // 128, col_scales))
+
+
 def quantize_expert_weights(w12: torch.Tensor, w3: torch.Tensor):
     """Per-expert 128x128 quantization of the stacked SwiGLU weights, with the transposed
     codes the backward needs: ((w12q, w12qt, w12s), (w3q, w3qt, w3s)) from
@@ -376,9 +424,9 @@ def experts_backward(saved, grad_out: torch.Tensor, dx_dtype: torch.dtype):
                            zero_uncovered=True)
     hbt, hblk = requantize_grouped_t(hq, hs, starts, ends)
     dw3 = fp8_grouped_wgrad(gqt, gst, hbt, hblk, starts, ends, g.shape[0])
-    # silu(h1) * h2 in fp32 (the forward's cast to the input dtype passes the gradient)
-    dh12 = swiglu_backward(dh, h12)
-    dq, ds, dqt, dst = quantize_fp8_dual_grouped(dh12, starts, ends, col_scales=True)
+    # silu(h1) * h2 in fp32 (the forward's cast to the input dtype passes the gradient),
+    # its gradient quantized both ways in the same pass
+    dq, ds, dqt, dst = swiglu_backward_dual_grouped(dh, h12, starts, ends, col_scales=True)
     dx = fp8_grouped_dgrad(dq, ds, w12qt, w12s, starts, ends, 2 * H, out_dtype=dx_dtype,
                            zero_uncovered=True)
     xbt, xblk = requantize_grouped_t(xq, xs, starts, ends)

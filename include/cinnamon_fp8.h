@@ -305,6 +305,19 @@ int cin_swiglu_backward(const float* dh, int64_t sdm, const void* h12, int h12_d
                         int64_t M, int64_t H, float* dh12, int64_t som, void* stream);
 
 /*
+ * cin_swiglu_backward followed by cin_quant_dual_grouped of its output, in one pass: the
+ * fp32 dh12 [T, 2H] is formed tile by tile in registers and never stored.  Arguments as the
+ * two calls' (dh, h12 as cin_swiglu_backward's with M = T; the outputs and ranges as
+ * cin_quant_dual_grouped's with N = 2H); the codes and scales are bit for bit those of the
+ * two calls.  H % 128 == 0; dh and h12 rows 16-byte aligned.  No counterpart in the
+ * reference (its grouped GEMM has no backward); the FP8 experts' backward calls it.
+ */
+int cin_swiglu_dual_grouped(const float* dh, int64_t sdm, const void* h12, int h12_dtype, int64_t s12,
+                            int64_t T, int64_t H, const int64_t* starts, const int64_t* ends, int64_t E,
+                            int round_scale, uint8_t* q, int64_t sqm, float* s, int64_t ssm, int64_t ssk,
+                            uint8_t* qt, int64_t sqtm, float* st, int64_t sstm, int64_t sstk, void* stream);
+
+/*
  * Zero the rows r of a [T, *] matrix (rows ldc_bytes apart, row_bytes written) with r outside
  * every range [starts[e], ends[e]).  The grouped GEMMs leave such rows untouched (as the
  * reference's moe_grouped_gemm leaves them unset, src/kernels.py:550); callers that need

@@ -74,6 +74,14 @@ def test_no_rpath_to_a_second_hip_runtime():
                             1, 2, 1, 8, 256, 1, 2, None)),                                  # X stride < K
     ("cin_quant_backward", (1, 0, 256, 256, 256, 0, 1, 256, 1, 1, 2, 1, 256, 1, 2, 1, 8, 256, 256,
                             1, 2, 1, 8, 256, 1, 2, None)),                                  # s column stride < M
+    # swiglu_dual_grouped: dh, sdm, h12, dt, s12, T, H, starts, ends, E, rs, q, sqm, s, ssm, ssk, qt, sqtm,
+    #                      st, sstm, sstk, stream
+    ("cin_swiglu_dual_grouped", (1, 200, 1, 9, 400, 16, 200, 1, 1, 1, 0, 1, 400, 1, 1, 16, 1, 128, 1, 1, 1,
+                                 None)),                                                     # bad h12 dtype
+    ("cin_swiglu_dual_grouped", (1, 200, 1, 0, 400, 16, 200, 1, 1, 1, 0, 1, 400, 1, 1, 16, 1, 128, 1, 1, 1,
+                                 None)),                                                     # H % 128
+    ("cin_swiglu_dual_grouped", (None, 256, 1, 0, 512, 16, 256, 1, 1, 1, 0, 1, 512, 1, 1, 16, 1, 128, 1, 1, 1,
+                                 None)),                                                     # null dh
     ("cin_moe_route", (None, 16, 2, 0, None, None, None, None, None, None, 0, None)),        # E = 0
     ("cin_moe_route", (None, 16, 2, 5000, None, None, None, None, None, None, 0, None)),     # E > 4096
     ("cin_moe_route", (None, 16, 2, 8, None, None, None, None, None, None, 0, None)),        # null ptrs

@@ -111,6 +111,9 @@ def test_opcheck_operators(dev):
                               test_utils=f8)
     dh = torch.randn(256, 256, device=dev, generator=g)
     torch.library.opcheck(ops.swiglu_backward.default, (dh, h12), test_utils=full)
+    se = (torch.tensor([0, 100], device=dev), torch.tensor([100, 256], device=dev))
+    for col in (False, True):
+        torch.library.opcheck(ops.swiglu_dual_grouped.default, (dh, h12, *se, False, col), test_utils=f8)
     # indexer: quantization (fp8 outputs), scores and weights gradient (uint8 code inputs)
     qi = torch.randn(2, 70, 4, 128, device=dev, generator=g).to(torch.bfloat16)
     ki = torch.randn(2, 90, 128, device=dev, generator=g).to(torch.bfloat16)

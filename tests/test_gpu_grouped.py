@@ -226,6 +226,38 @@ def test_swiglu_backward_equals_elementwise_chain(kern, dev, dt):
     assert torch.equal(got, want), f"max abs diff {(got - want).abs().max().item()}"
 
 
+@pytest.mark.parametrize("counts,H", [(COUNTS[0], 384), ([0, 1, 257], 128), ([300, 260], 200)])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("round_scale,col_scales", [(False, True), (True, False)])
+def test_swiglu_dual_grouped_equals_two_calls(kern, dev, counts, H, dt, round_scale, col_scales):
+    """The fused SwiGLU backward + grouped dual quantization against swiglu_backward followed
+    by quantize_fp8_dual_grouped (each pinned by its own test): codes and scales bit for bit,
+    on the covered rows and up to the experts' padded end.  H = 200 takes the two calls."""
+    from cinnamon_amd import layers
+
+    starts, ends = _ranges(counts)
+    T = int(ends[-1])
+    g = torch.Generator().manual_seed(T + H)
+    h12 = torch.randn(T, 2 * H, generator=g) * 4
+    h12[::7, :8] = torch.tensor([100.0, -100.0, 0.0, -0.0, 30.0, -30.0, 1e-30, -88.0])  # sigmoid ends
+    dh = torch.randn(T, H, generator=g) * 1e-3
+    dh[5::11, 3] = 0.0
+    h12, dh = h12.to(dt).to(dev), dh.to(dev)
+    sd, ed = starts.to(dev), ends.to(dev)
+    got = layers.swiglu_backward_dual_grouped(dh, h12, sd, ed, round_scale=round_scale,
+                                              col_scales=col_scales)
+    want = layers.quantize_fp8_dual_grouped(layers.swiglu_backward(dh, h12), sd, ed,
+                                            round_scale=round_scale, col_scales=col_scales)
+    cov = torch.zeros(T, dtype=torch.bool)
+    for a, b in zip(starts.tolist(), ends.tolist()):
+        cov[a:b] = True
+    P = int(sum(-(-c // 128) * 128 for c in counts))
+    assert torch.equal(_u8(got[0])[cov], _u8(want[0])[cov]), "row codes"
+    assert torch.equal(got[1].cpu()[cov], want[1].cpu()[cov]), "row scales"
+    assert torch.equal(_u8(got[2])[:, :P], _u8(want[2])[:, :P]), "transposed codes"
+    assert torch.equal(got[3].cpu()[:, :P // 128], want[3].cpu()[:, :P // 128]), "transposed scales"
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
 def test_zero_rows_outside_ranges(kern, dev, dt):
     from cinnamon_amd import layers

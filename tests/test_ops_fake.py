@@ -20,7 +20,7 @@ OPS = ["quant_rowwise", "quant_blockwise", "quant_blockwise_t", "quant_fwd", "qu
        "dequant_rowwise", "dequant", "gemm_fp8_bs", "transpose_u8", "grouped_gemm_f16",
        "grouped_gemm_fp8", "quant_dual_grouped", "requant_row_to_block_grouped",
        "grouped_wgrad_fp8", "grouped_dgrad_fp8", "silu_mul_quant_rowwise", "swiglu_backward",
-       "moe_route", "moe_gather_quant_rowwise", "moe_scatter_quant_rowwise", "moe_gather_sum",
+       "swiglu_dual_grouped", "moe_route", "moe_gather_quant_rowwise", "moe_scatter_quant_rowwise", "moe_gather_sum",
        "moe_combine", "moe_combine_backward", "indexer_scores_fp8", "indexer_weights_grad_fp8", "indexer_quantize"]
 F8, F32, BF16 = torch.float8_e4m3fn, torch.float32, torch.bfloat16
 
@@ -104,6 +104,9 @@ def test_shape_functions_match_the_kernels_outputs():
         assert _meta(hq) == ((T, H), F8, "cuda") and hs.shape == (T, 3)
         dh = torch.empty(T, H, dtype=F32, device=dev)
         assert _meta(layers.swiglu_backward(dh, h12)) == ((T, 2 * H), F32, "cuda")
+        dq, ds, dqt, dst = layers.swiglu_backward_dual_grouped(dh, h12, starts, ends)
+        assert [t.shape for t in (dq, ds, dqt, dst)] == [(T, 2 * H), (T, 6), (2 * H, cap),
+                                                         (2 * H, cap // 128)]
         # indexer scores
         qi = torch.empty(2, 100, 4, 128, dtype=BF16, device=dev)
         ki = torch.empty(2, 90, 128, dtype=BF16, device=dev)
@@ -180,7 +183,7 @@ def test_grouped_experts_forward_backward_traces_to_operators():
     ops = _op_targets(gm)
     for name in ["grouped_gemm_fp8", "silu_mul_quant_rowwise", "quant_dual_grouped",
                  "grouped_dgrad_fp8", "requant_row_to_block_grouped", "grouped_wgrad_fp8",
-                 "swiglu_backward"]:
+                 "swiglu_dual_grouped"]:
         assert any(f"cinnamon_amd.{name}" in o for o in ops), (name, ops)
 
 
