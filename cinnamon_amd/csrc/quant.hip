@@ -1057,11 +1057,18 @@ struct DualSmem {
   TileT tileT;
 };
 
-template <int DT, bool EDGE>
+struct NoOp {
+  __device__ void operator()() const {}
+};
+
+// after_raw() runs once the raw tile is no longer read (its registers may take the next
+// tile's load), before the transposed tile leaves LDS.
+template <int DT, bool EDGE, typename After = NoOp>
 __device__ __forceinline__ void dual_body(RawIn<DT>& raw, const TileGeo& g, int64_t N, bool rs,
                                           uint8_t* q, int64_t sqm, float* s, int64_t ssm,
                                           int64_t ssk, uint8_t* qt, int64_t sqtm, bool vec_t,
-                                          float* st, int64_t sstm, int64_t sstk, DualSmem& sm) {
+                                          float* st, int64_t sstm, int64_t sstk, DualSmem& sm,
+                                          After after_raw = After()) {
   constexpr int NW = (int)(sizeof(raw.w[0]) / sizeof(raw.w[0][0]));
   const int lane16 = threadIdx.x & 15, rg = threadIdx.x >> 4;
   const float floor_v = amax_floor(DT);
@@ -1141,6 +1148,7 @@ __device__ __forceinline__ void dual_body(RawIn<DT>& raw, const TileGeo& g, int6
       put_col8(sm.tileT, lane16 * 8 + j, rg, w[0], w[1]);
     }
   }
+  after_raw();
   __syncthreads();
   put_tile_t<EDGE>(sm.tileT, qt, sqtm, N, g, vec_t);
 }
@@ -1157,11 +1165,37 @@ __device__ __forceinline__ void dual_run(Geo& geo, uint32_t ntiles, const void* 
     dual_body<DT, EDGE>(r, g, N, rs, q, sqm, s, ssm, ssk, qt, sqtm, vec_t, st, sstm, sstk, sm);
   };
   // fp32: one register set at 3 waves per SIMD (two sets hold it to 2); measured 2-8%
-  // faster, and 4 waves per SIMD slower on large inputs
-  if constexpr (DT == CIN_DT_F32 && !EDGE)
-    tile_loop_single<RawIn<DT>>(ntiles, geo, ld, pr);
-  else
+  // faster, and 4 waves per SIMD slower on large inputs.  The next tile's load is issued
+  // from inside dual_body, once the set is free (1% faster than loading after it).
+  if constexpr (DT == CIN_DT_F32 && !EDGE) {
+    // one register set; the next tile's load starts once this tile's values are coded
+    uint32_t t = blockIdx.x;
+    if (t >= ntiles) return;
+    RawIn<DT> r;
+    TileGeo g, gn;
+    geo(t, g);
+    ld(g, r);
+    for (;;) {
+      const uint32_t t1 = t + gridDim.x;
+      const bool more = t1 < ntiles;
+      if (more) {
+        geo(t1, gn);
+      } else {
+        gn = g;
+        gn.nr = 0;
+      }
+      if (g.nr != 0)  // uniform over the workgroup
+        dual_body<DT, EDGE>(r, g, N, rs, q, sqm, s, ssm, ssk, qt, sqtm, vec_t, st, sstm, sstk, sm,
+                            [&]() { ld(gn, r); });
+      else
+        ld(gn, r);
+      if (!more) break;
+      g = gn;
+      t = t1;
+    }
+  } else {
     tile_loop<RawIn<DT>>(ntiles, geo, ld, pr);
+  }
 }
 
 template <int DT, bool EDGE>
@@ -1237,25 +1271,50 @@ __global__ __launch_bounds__(kThreads, 2) void k_swiglu_dual128_grouped(
   __shared__ DualSmem sm;
   GroupedTiles geo = grouped_tiles(starts, ends, E, T, tcap, nbh, 0);
   const int64_t N = 2 * H;
-  auto ld = [&](const TileGeo& g, SwiRaw<IT>& r) {
-    load_in<CIN_DT_F32, false>(dh, sdm, H, g, r.dh);
-    load_in<IT, false>(h12, s12, N, g, r.a);
-    TileGeo g2 = g;
-    g2.cb += nbh;
-    load_in<IT, false>(h12, s12, N, g2, r.b);
-  };
-  auto pr = [&](const TileGeo& g, SwiRaw<IT>& r) {
-    if (g.nr == 0) return;  // uniform over the workgroup
+  const bool rs = round_scale != 0, vt = vec_t != 0;
+  uint32_t t = blockIdx.x;
+  if (t >= ntiles) return;
+  SwiRaw<IT> r;
+  TileGeo g, gn;
+  geo(t, g);
+  load_in<CIN_DT_F32, false>(dh, sdm, H, g, r.dh);
+  load_in<IT, false>(h12, s12, N, g, r.a);
+  {
+    TileGeo gb = g;
+    gb.cb += nbh;
+    load_in<IT, false>(h12, s12, N, gb, r.b);
+  }
+  // The next tile's inputs load while this tile is quantized: dh after the first half's
+  // tile, h1 and h2 after the second's (their registers are free then: the values live
+  // in d1 and d2).  Measured 1.29 -> 0.78 ms at 131072 x 2048.
+  for (;;) {
     RawIn<CIN_DT_F32> d1, d2;
     swiglu_dual_vals<IT>(r, d1, d2);
-    dual_body<CIN_DT_F32, false>(d1, g, N, round_scale != 0, q, sqm, s, ssm, ssk, qt, sqtm, vec_t != 0, st,
-                                 sstm, sstk, sm);
+    const uint32_t t1 = t + gridDim.x;
+    const bool more = t1 < ntiles;
+    if (more) {
+      geo(t1, gn);
+    } else {
+      gn = g;
+      gn.nr = 0;
+    }
     TileGeo g2 = g;
     g2.cb += nbh;
-    dual_body<CIN_DT_F32, false>(d2, g2, N, round_scale != 0, q, sqm, s, ssm, ssk, qt, sqtm, vec_t != 0, st,
-                                 sstm, sstk, sm);
-  };
-  tile_loop_single<SwiRaw<IT>>(ntiles, geo, ld, pr);
+    if (g.nr != 0)  // uniform over the workgroup
+      dual_body<CIN_DT_F32, false>(d1, g, N, rs, q, sqm, s, ssm, ssk, qt, sqtm, vt, st, sstm, sstk, sm);
+    load_in<CIN_DT_F32, false>(dh, sdm, H, gn, r.dh);
+    if (g.nr != 0)
+      dual_body<CIN_DT_F32, false>(d2, g2, N, rs, q, sqm, s, ssm, ssk, qt, sqtm, vt, st, sstm, sstk, sm);
+    load_in<IT, false>(h12, s12, N, gn, r.a);
+    {
+      TileGeo gb = gn;
+      gb.cb += nbh;
+      load_in<IT, false>(h12, s12, N, gb, r.b);
+    }
+    if (!more) break;
+    g = gn;
+    t = t1;
+  }
 }
 
 // ----------------------------- row -> block re-quantization -----------------------------
