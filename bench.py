@@ -264,7 +264,7 @@ def stream_mixes(nbuf):
         "quant_fwd_fused": ((M + N) * K * 2, 2, 1, nbuf),
         "dual_quant_dy": (M * N * 2, 1, 1, 1),               # bf16 in, two e4m3 layouts out
         "requant_x_block_t": (M * K, 1, 1, 1),               # e4m3 in, e4m3 out
-        "dual_quant_grouped_dh12": (A * 2 * C3_H * 2, 1, 1, 1),
+        "swiglu_dual_grouped_dh12": (A * C3_H * 4 + A * 2 * C3_H * 2, 2, 1, 1),  # dh fp32 + h12 bf16 in
         "requant_grouped_x": (A * C3_D, 1, 1, 1),
         "gather_quant": (C3_T * C3_D * 2, 1, 4, 1),          # bf16 tokens in, k code rows each out
         "combine": (A * C3_D * 2, 4, 1, 1),                  # fp16 rows in, fp32 tokens out
@@ -492,19 +492,21 @@ def moe_setup(dev):
 
 
 def moe_bwd_setup(dev, moe):
-    """Config-3 backward operands for the gate/up GEMM: dH12 [A, 2H] bf16 ~N(0, 1e-3) and the
-    stacked transposed w12 codes [D, E*2H] (the grouped dgrad's B operand)."""
+    """Config-3 backward operands for the gate/up GEMM: dH [A, H] fp32 ~N(0, 1e-3) (the down
+    GEMM's dgrad output), the saved gate/up output h12 [A, 2H] bf16 ~N(0, 1), and the stacked
+    transposed w12 codes [D, E*2H] (the grouped dgrad's B operand)."""
     import torch
 
     from cinnamon_amd import kernels
 
     g = torch.Generator(device=dev).manual_seed(33)
     E, D, H, A = moe["E"], moe["D"], moe["H"], moe["A"]
-    dh12 = (torch.randn(A, 2 * H, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
+    dh = torch.randn(A, H, device=dev, generator=g) * 1e-3
+    h12 = torch.randn(A, 2 * H, device=dev, generator=g).to(torch.bfloat16)
     w12 = (torch.randn(E * 2 * H, D, device=dev, generator=g) * 0.02).to(torch.bfloat16)
     _, w12qt, w12s = kernels.quantize_fp8_blockwise_t(w12, with_rowmajor=False)
     del w12
-    return dict(dh12=dh12, w12qt=w12qt, w12s=w12s)
+    return dict(dh=dh, h12=h12, w12qt=w12qt, w12s=w12s)
 
 
 def bwd_setup(dev, xs0, w0):
@@ -590,8 +592,8 @@ def main():
     def moe_down(i):
         layers.fp8_grouped_gemm(hq, hs, moe["w3q"], moe["w3s"], moe["starts"], moe["ends"], out=y3)
 
-    # config-3 backward of the gate/up GEMM (the larger one): grouped dual quantization of
-    # dH12 [A, 2H], grouped re-quantization of the saved X codes, grouped wgrad
+    # config-3 backward of the gate/up GEMM (the larger one): SwiGLU backward fused with the
+    # grouped dual quantization of its output dH12 [A, 2H], grouped re-quantization of the saved X codes, grouped wgrad
     # dW12 [E, 2H, D] and grouped dgrad dX [A, D]
     mb = None
     if full or args.only in ("moe_dual", "moe_requant", "moe_wgrad", "moe_dgrad"):
@@ -599,13 +601,13 @@ def main():
             moe = moe_setup(dev)
             xq3, xs3 = kernels.quantize_fp8_rowwise(moe["x"], col_scales=True)
         mb = moe_bwd_setup(dev, moe)
-        gq3, gs3, gqt3, gst3 = layers.quantize_fp8_dual_grouped(mb["dh12"], moe["starts"], moe["ends"],
-                                                                col_scales=True)
+        gq3, gs3, gqt3, gst3 = layers.swiglu_backward_dual_grouped(mb["dh"], mb["h12"], moe["starts"],
+                                                                   moe["ends"], col_scales=True)
         xbt3, xbs3 = layers.requantize_grouped_t(xq3, xs3, moe["starts"], moe["ends"])
         dx3 = torch.empty((moe["A"], moe["D"]), dtype=torch.bfloat16, device=dev)
 
     def moe_dual(i):
-        layers.quantize_fp8_dual_grouped(mb["dh12"], moe["starts"], moe["ends"], col_scales=True)
+        layers.swiglu_backward_dual_grouped(mb["dh"], mb["h12"], moe["starts"], moe["ends"], col_scales=True)
 
     def moe_requant(i):
         layers.requantize_grouped_t(xq3, xs3, moe["starts"], moe["ends"])
@@ -1021,13 +1023,14 @@ def main():
         mw_us = kernel_loop(moe_wgrad, 3, 1)
         mg_us = kernel_loop(moe_dgrad, 3, 1)
         fl = 2.0 * A * D * 2 * H
-        # bytes: dual reads dH12 bf16, writes row codes + scales and padded column codes + scales;
+        # bytes: the fused SwiGLU backward + dual reads dH fp32 and h12 bf16, writes dH12's row
+        # codes + scales and padded column codes + scales;
         # requant reads X codes + row scales, writes padded transposed codes + block scales
-        md_bytes = A * 2 * H * 2 + A * 2 * H + A * (2 * H // 128) * 4 + 2 * H * cap + 2 * H * (cap // 128) * 4
+        md_bytes = A * H * 4 + A * 2 * H * 2 + A * 2 * H + A * (2 * H // 128) * 4 + 2 * H * cap + 2 * H * (cap // 128) * 4
         mr_bytes = A * D + A * (D // 128) * 4 + D * cap + (cap // 128) * (D // 128) * 4
         out["components"]["config3_moe_backward_gateup"] = {
-            "dual_quant_grouped_dh12": {"us": round(md_us, 1), "gbps": round(md_bytes / md_us / 1e3, 1),
-                                        "frac_of_hbm": round(md_bytes / md_us / 1e3 / PEAK_HBM_GBPS, 4)},
+            "swiglu_dual_grouped_dh12": {"us": round(md_us, 1), "gbps": round(md_bytes / md_us / 1e3, 1),
+                                         "frac_of_hbm": round(md_bytes / md_us / 1e3 / PEAK_HBM_GBPS, 4)},
             "requant_grouped_x": {"us": round(mr_us, 1), "gbps": round(mr_bytes / mr_us / 1e3, 1),
                                   "frac_of_hbm": round(mr_bytes / mr_us / 1e3 / PEAK_HBM_GBPS, 4)},
             "wgrad_grouped_dw12": {"us": round(mw_us, 1), "tflops": round(fl / mw_us / 1e6, 1),
@@ -1063,7 +1066,7 @@ def main():
     comps = out["components"]
     where = {"quant_x_rowwise": comps, "quant_w_blockwise": comps, "quant_fwd_fused": comps,
              "dual_quant_dy": comps.get("config4_backward"), "requant_x_block_t": comps.get("config4_backward"),
-             "dual_quant_grouped_dh12": comps.get("config3_moe_backward_gateup"),
+             "swiglu_dual_grouped_dh12": comps.get("config3_moe_backward_gateup"),
              "requant_grouped_x": comps.get("config3_moe_backward_gateup")}
     mixes = {k: v for k, v in stream_mixes(nbuf).items() if where.get(k) is not None}
     if "config3_moe_dispatch" in comps:
