@@ -123,12 +123,14 @@ def test_weights_gradient_is_deterministic(dev):
 @pytest.mark.parametrize("rows,d,dtype", [(300, 128, torch.bfloat16), (77, 192, torch.float32),
                                           (65, 96, torch.float16), (5, 256, torch.bfloat16),
                                           (6000, 128, torch.bfloat16), (6000, 192, torch.float32)])
-def test_indexer_quantize_equals_the_rowwise_quantizer(dev, rows, d, dtype):
-    """Codes and first scales equal quantize_fp8_rowwise(block 128) and its [..., 0], on both
-    launch shapes (16 lanes per tile below 32768 tiles, 8 above)."""
+@pytest.mark.parametrize("kdtype", [None, torch.float32])
+def test_indexer_quantize_equals_the_rowwise_quantizer(dev, rows, d, dtype, kdtype):
+    """Codes and first scales equal quantize_fp8_rowwise(block 128) and its [..., 0]: q and k
+    of one dtype in the one-launch kernel (k 16 lanes per tile, q 8), of two dtypes in two
+    launches (16 lanes per tile below 32768 tiles, 8 above)."""
     g = torch.Generator().manual_seed(rows + d)
     q = (torch.randn(2, rows, 3, d, generator=g) * 4).to(dtype).to(dev)
-    k = (torch.randn(2, rows + 7, d, generator=g) * 4).to(dtype).to(dev)
+    k = (torch.randn(2, rows + 7, d, generator=g) * 4).to(kdtype or dtype).to(dev)
     q[0, 1] = 0  # zero rows take the floor scale
     q8, qs, k8, ks = torch.ops.cinnamon_amd.indexer_quantize(q, k)
     for x, c, sc in ((q, q8, qs), (k, k8, ks)):
