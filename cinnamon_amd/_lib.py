@@ -68,6 +68,8 @@ SIGNATURES: dict[str, list] = {
     "cin_moe_gather_sum": [_p, _i32, _i64, _p, _i64, _i64, _i64, _i64, _p, _i32, _i64, _p],
     "cin_moe_scatter_quant_rowwise": [_p, _i32, _i64, _i64, _i64, _p, _i64, _p, _i64, _i32, _p, _i64,
                                       _p, _i64, _i64, _p],
+    "cin_moe_scatter_quant_rowwise_ws": [_p, _i32, _i64, _i64, _i64, _p, _i64, _p, _i64, _i32, _p, _i64,
+                                         _p, _i64, _i64, _p, _p],
     "cin_moe_combine": [_p, _i32, _i64, _p, _i32, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "cin_moe_combine_backward": [_p, _i64, _p, _i32, _i64, _p, _i32, _i64, _p, _p, _i64, _i64, _i64,
                                  _i64, _p, _i32, _i64, _p, _p],

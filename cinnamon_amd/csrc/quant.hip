@@ -115,8 +115,11 @@ __device__ inline void quant_vals(const float (&v)[NV], float s, float r, uint32
 //                rows rowmap[t * rowdiv + j] (int32 map), j < rowdiv, that lie in
 //                [0, src_rows) (src_rows = output rows here);
 //   kMapFirstScale: rows as kMapNone, but only each row's first tile scale is written, to
-//                sc[row * ssm] (the DSA indexer uses no other, src/attention.py:296-297).
-constexpr int kMapNone = 0, kMapGather = 1, kMapScatter = 2, kMapFirstScale = 3;
+//                sc[row * ssm] (the DSA indexer uses no other, src/attention.py:296-297);
+//   kMapScatterTok: codes as kMapScatter, but each scale is written once, by input row, to
+//                sc[t * ssm + cb * ssk] (a token-major table that a second pass spreads
+//                over the output rows).
+constexpr int kMapNone = 0, kMapGather = 1, kMapScatter = 2, kMapFirstScale = 3, kMapScatterTok = 4;
 // The body runs as workgroup `bid` of `nblk` (the kernel's own grid, or a share of a fused
 // launch's).
 template <int DT, int LANES, int U, bool FULL, int MAP = kMapNone>
@@ -213,10 +216,11 @@ __device__ __forceinline__ void rowwise128_body(uint32_t bid, uint32_t nblk, con
       const float s = compute_scale(a, rs);
       uint32_t codes[EPL / 4];
       quant_vals<EPL, kDivSteps<DT>>(v[u], s, 1.0f / s, codes);
-      const int nout = MAP == kMapScatter ? (int)rowdiv : 1;
+      constexpr bool kScat = MAP == kMapScatter || MAP == kMapScatterTok;
+      const int nout = kScat ? (int)rowdiv : 1;
       for (int j = 0; j < nout; ++j) {
         int64_t orow = rows[u];
-        if constexpr (MAP == kMapScatter) {
+        if constexpr (kScat) {
           orow = static_cast<const int32_t*>(rowmap)[(int64_t)rows[u] * rowdiv + j];
           if (orow < 0 || orow >= src_rows) continue;
         }
@@ -239,10 +243,13 @@ __device__ __forceinline__ void rowwise128_body(uint32_t bid, uint32_t nblk, con
         if (li == 0) {
           if constexpr (MAP == kMapFirstScale) {
             if (cbs[u] == 0) sc[orow * ssm] = s;
-          } else {
+          } else if constexpr (MAP != kMapScatterTok) {
             sc[orow * ssm + (int64_t)cbs[u] * ssk] = s;
           }
         }
+      }
+      if constexpr (MAP == kMapScatterTok) {
+        if (li == 0) sc[(int64_t)rows[u] * ssm + (int64_t)cbs[u] * ssk] = s;
       }
     }
   }
@@ -1729,16 +1736,29 @@ unsigned resident_grid(uint32_t ntiles) {
 
 // Output rows that no assignment reaches (perm[r] < 0: the tail after dropped ids) get the
 // quantization of a zero row: codes 0 and the scale of the amax floor.  A thread owns a
-// row; routed rows (all of them when no id was dropped) return at once.
+// row; routed rows (all of them when no id was dropped) return at once, or, with a
+// token-major scale table tok [T, nb] (kMapScatterTok), copy their token's scales: row r's
+// scales are tok[perm[r] / k], and threads of consecutive rows store consecutive addresses
+// in either layout (column-major: one run per column block; row-major: whole rows).
 __global__ __launch_bounds__(kThreads) void k_zero_unrouted(const int64_t* __restrict__ perm,
                                                             int64_t rows, int64_t N, int dt,
                                                             int round_scale, uint8_t* q,
                                                             int64_t sqm, float* sc, int64_t ssm,
-                                                            int64_t ssk) {
+                                                            int64_t ssk, const float* __restrict__ tok = nullptr,
+                                                            int64_t k = 1, int64_t ntok = 0) {
   const int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (r >= rows || perm[r] >= 0) return;
+  if (r >= rows) return;
+  const int64_t a = perm[r];
+  const int64_t nb = (N + 127) / 128;
+  if (a >= 0) {
+    const int64_t t = a / k;
+    if (tok == nullptr || t >= ntok) return;  // (an assignment past the tokens: left as is)
+    const float* src = tok + t * nb;
+    for (int64_t b = 0; b < nb; ++b) sc[r * ssm + b * ssk] = src[b];
+    return;
+  }
   const float s = compute_scale(amax_floor(dt), round_scale != 0);
-  for (int64_t b = 0; b < (N + 127) / 128; ++b) sc[r * ssm + b * ssk] = s;
+  for (int64_t b = 0; b < nb; ++b) sc[r * ssm + b * ssk] = s;
   uint8_t* p = q + r * sqm;  // 8-byte aligned (q and sqm are)
   int64_t c = 0;
   for (; c + 8 <= N; c += 8) *reinterpret_cast<uint2*>(p + c) = make_uint2(0u, 0u);
@@ -1937,6 +1957,39 @@ int cin_moe_scatter_quant_rowwise(const void* x, int x_dtype, int64_t T, int64_t
     hipLaunchKernelGGL(k_zero_unrouted, (unsigned)cdiv(rows, kThreads), kThreads, 0, s, perm, rows, N,
                        x_dtype, round_scale, q, sqm, scales, ssm, ssk);
   return cin_check_launch("moe_scatter_quant_rowwise");
+}
+
+int cin_moe_scatter_quant_rowwise_ws(const void* x, int x_dtype, int64_t T, int64_t N, int64_t sxm,
+                                     const int32_t* inv, int64_t k, const int64_t* perm, int64_t rows,
+                                     int round_scale, uint8_t* q, int64_t sqm, float* scales,
+                                     int64_t ssm, int64_t ssk, float* ws, void* stream) {
+  CIN_CHECK_ARG(valid_dtype(x_dtype), "moe_scatter_quant_ws: unsupported x dtype %d", x_dtype);
+  CIN_CHECK_ARG(T >= 0 && N >= 0 && rows >= 0 && k >= 1, "moe_scatter_quant_ws: bad sizes");
+  if (N == 0 || (T == 0 && rows == 0)) return CIN_OK;
+  CIN_CHECK_ARG(x && inv && perm && q && scales && ws, "moe_scatter_quant_ws: null pointer");
+  const int64_t nb = cdiv(N, 128);
+  CIN_CHECK_ARG(sqm >= N, "moe_scatter_quant_ws: output row stride too small");
+  CIN_CHECK_ARG(scale_layout_ok(rows, nb, ssm, ssk), "moe_scatter_quant_ws: scale strides overlap");
+  const int es = elem_size(x_dtype);
+  CIN_CHECK_ARG(aligned(x, 16) && (sxm * es) % 16 == 0 && sxm >= N && aligned(q, 8) && sqm % 8 == 0,
+                "moe_scatter_quant_ws: x rows must be contiguous and 16-byte aligned, q rows 8-byte aligned");
+  CIN_CHECK_ARG(T * nb < (int64_t)1 << 31 && cdiv(rows, kThreads) < (int64_t)1 << 31,
+                "moe_scatter_quant_ws: too many tiles");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (T > 0) {
+    const uint32_t ntiles = (uint32_t)(T * nb);
+    const unsigned grid = grid_for(ntiles, kThreads / 8, 16384);
+    if (N % 128 == 0)
+      launch_rowwise128_t<8, 1, true, kMapScatterTok>(x, x_dtype, N, sxm, round_scale, q, sqm, ws, nb, 1,
+                                                      (uint32_t)nb, ntiles, grid, s, inv, k, rows);
+    else
+      launch_rowwise128_t<8, 1, false, kMapScatterTok>(x, x_dtype, N, sxm, round_scale, q, sqm, ws, nb, 1,
+                                                       (uint32_t)nb, ntiles, grid, s, inv, k, rows);
+  }
+  if (rows > 0)
+    hipLaunchKernelGGL(k_zero_unrouted, (unsigned)cdiv(rows, kThreads), kThreads, 0, s, perm, rows, N,
+                       x_dtype, round_scale, q, sqm, scales, ssm, ssk, ws, k, T);
+  return cin_check_launch("moe_scatter_quant_rowwise_ws");
 }
 
 int cin_quant_blockwise(const void* x, int x_dtype, int64_t M, int64_t N, int64_t sxm, int64_t sxn,

@@ -437,6 +437,18 @@ int cin_moe_scatter_quant_rowwise(const void* x, int x_dtype, int64_t T, int64_t
                                   int64_t ssm, int64_t ssk, void* stream);
 
 /*
+ * cin_moe_scatter_quant_rowwise with a workspace ws [T, ceil(N/128)] fp32 (T * ceil(N/128)
+ * floats, contents on entry ignored): each token's scales are written once into ws, and a
+ * second pass over the sorted rows copies them into scales (threads of consecutive rows store
+ * consecutive addresses), instead of k scattered 4-byte stores per token scale.  Same codes
+ * and scales.  No counterpart in the reference; the MoE dispatch (moe.py) calls it.
+ */
+int cin_moe_scatter_quant_rowwise_ws(const void* x, int x_dtype, int64_t T, int64_t N, int64_t sxm,
+                                     const int32_t* inv, int64_t k, const int64_t* perm, int64_t rows,
+                                     int round_scale, uint8_t* q, int64_t sqm, float* scales,
+                                     int64_t ssm, int64_t ssk, float* ws, void* stream);
+
+/*
  * Backward of the dispatch gather: out[t] = sum over token t's sorted positions r
  * (increasing r, fp32 sums) of g[r]; the gradient of flat_x[token_indices] (reference
  * src/layers.py:140).  g [A, N] (g_dtype, row stride sgm), inv [T*k] from cin_moe_route,

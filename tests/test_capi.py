@@ -89,6 +89,9 @@ def test_no_rpath_to_a_second_hip_runtime():
     ("cin_moe_combine", (None, 1, 8, None, 7, 2, None, 4, 2, 8, 8, None, 8, None)),          # bad score dtype
     ("cin_moe_combine", (None, 5, 8, None, 1, 2, None, 4, 2, 8, 8, None, 8, None)),          # bad y dtype
     ("cin_moe_gather_quant_rowwise", (None, 0, 4, 256, 256, None, 8, 0, 0, None, 256, None, 2, 1, None)),
+    # scatter_quant_ws: x, dt, T, N, sxm, inv, k, perm, rows, rs, q, sqm, s, ssm, ssk, ws, stream
+    ("cin_moe_scatter_quant_rowwise_ws", (1, 0, 4, 256, 256, 1, 2, 1, 8, 0, 1, 256, 1, 1, 8, None, None)),  # no ws
+    ("cin_moe_scatter_quant_rowwise_ws", (1, 9, 4, 256, 256, 1, 2, 1, 8, 0, 1, 256, 1, 1, 8, 1, None)),     # dtype
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 2, 48, 0.1, None, None)),   # d % 32
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 2, 288, 0.1, None, None)),  # d > 256
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 0, 64, 0.1, None, None)),   # H = 0
