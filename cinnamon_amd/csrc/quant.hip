@@ -1754,7 +1754,15 @@ __global__ __launch_bounds__(kThreads) void k_zero_unrouted(const int64_t* __res
     const int64_t t = a / k;
     if (tok == nullptr || t >= ntok) return;  // (an assignment past the tokens: left as is)
     const float* src = tok + t * nb;
-    for (int64_t b = 0; b < nb; ++b) sc[r * ssm + b * ssk] = src[b];
+    if ((nb & 3) == 0) {  // 16-byte rows of the table (it is 16-byte aligned)
+      for (int64_t b = 0; b < nb; b += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(src + b);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[r * ssm + (b + e) * ssk] = v[e];
+      }
+    } else {
+      for (int64_t b = 0; b < nb; ++b) sc[r * ssm + b * ssk] = src[b];
+    }
     return;
   }
   const float s = compute_scale(amax_floor(dt), round_scale != 0);

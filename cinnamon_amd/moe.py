@@ -150,7 +150,7 @@ def _scatter_quant_op(x, perm, inv, top_k, round_scale, col_scales):
     s = _scale_buf(x, A, _cdiv(D, 128), col_scales)
     if col_scales:
         # a token's scales go once into a token-major table, then to its sorted rows with
-        # stores that run along the rows (308 -> 269 us at config 3; with row-major scales
+        # stores that run along the rows (308 -> 252 us at config 3; with row-major scales
         # the stores the kernel makes itself are faster, 263 against 326 us)
         ws = torch.empty(T * _cdiv(D, 128), dtype=torch.float32, device=x.device)
         call("cin_moe_scatter_quant_rowwise_ws", ptr(x), dtype_code(x), T, D, x.stride(0), ptr(iv),
