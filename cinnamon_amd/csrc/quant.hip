@@ -1975,6 +1975,7 @@ int cin_moe_scatter_quant_rowwise_ws(const void* x, int x_dtype, int64_t T, int6
   CIN_CHECK_ARG(T >= 0 && N >= 0 && rows >= 0 && k >= 1, "moe_scatter_quant_ws: bad sizes");
   if (N == 0 || (T == 0 && rows == 0)) return CIN_OK;
   CIN_CHECK_ARG(x && inv && perm && q && scales && ws, "moe_scatter_quant_ws: null pointer");
+  CIN_CHECK_ARG(aligned(ws, 16), "moe_scatter_quant_ws: ws must be 16-byte aligned");
   const int64_t nb = cdiv(N, 128);
   CIN_CHECK_ARG(sqm >= N, "moe_scatter_quant_ws: output row stride too small");
   CIN_CHECK_ARG(scale_layout_ok(rows, nb, ssm, ssk), "moe_scatter_quant_ws: scale strides overlap");

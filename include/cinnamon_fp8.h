@@ -438,7 +438,7 @@ int cin_moe_scatter_quant_rowwise(const void* x, int x_dtype, int64_t T, int64_t
 
 /*
  * cin_moe_scatter_quant_rowwise with a workspace ws [T, ceil(N/128)] fp32 (T * ceil(N/128)
- * floats, contents on entry ignored): each token's scales are written once into ws, and a
+ * floats, 16-byte aligned, contents on entry ignored): each token's scales are written once into ws, and a
  * second pass over the sorted rows copies them into scales (threads of consecutive rows store
  * consecutive addresses), instead of k scattered 4-byte stores per token scale.  Same codes
  * and scales.  No counterpart in the reference; the MoE dispatch (moe.py) calls it.

@@ -92,6 +92,7 @@ def test_no_rpath_to_a_second_hip_runtime():
     # scatter_quant_ws: x, dt, T, N, sxm, inv, k, perm, rows, rs, q, sqm, s, ssm, ssk, ws, stream
     ("cin_moe_scatter_quant_rowwise_ws", (1, 0, 4, 256, 256, 1, 2, 1, 8, 0, 1, 256, 1, 1, 8, None, None)),  # no ws
     ("cin_moe_scatter_quant_rowwise_ws", (1, 9, 4, 256, 256, 1, 2, 1, 8, 0, 1, 256, 1, 1, 8, 1, None)),     # dtype
+    ("cin_moe_scatter_quant_rowwise_ws", (16, 0, 4, 256, 256, 8, 2, 8, 8, 0, 8, 256, 8, 1, 8, 4, None)),    # ws align
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 2, 48, 0.1, None, None)),   # d % 32
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 2, 288, 0.1, None, None)),  # d > 256
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 0, 64, 0.1, None, None)),   # H = 0
