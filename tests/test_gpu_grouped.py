@@ -226,13 +226,15 @@ def test_swiglu_backward_equals_elementwise_chain(kern, dev, dt):
     assert torch.equal(got, want), f"max abs diff {(got - want).abs().max().item()}"
 
 
-@pytest.mark.parametrize("counts,H", [(COUNTS[0], 384), ([0, 1, 257], 128), ([300, 260], 200)])
+@pytest.mark.parametrize("counts,H", [(COUNTS[0], 384), ([0, 1, 257], 128), ([300, 260], 200),
+                                     ([4000, 2000, 1000, 700, 300, 127, 64, 0, 9], 2048)])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("round_scale,col_scales", [(False, True), (True, False)])
 def test_swiglu_dual_grouped_equals_two_calls(kern, dev, counts, H, dt, round_scale, col_scales):
     """The fused SwiGLU backward + grouped dual quantization against swiglu_backward followed
     by quantize_fp8_dual_grouped (each pinned by its own test): codes and scales bit for bit,
-    on the covered rows and up to the experts' padded end.  H = 200 takes the two calls."""
+    on the covered rows and up to the experts' padded end.  H = 200 takes the two calls; H = 2048
+    with Zipf-like expert sizes is the config-3 hidden width (many tiles per workgroup)."""
     from cinnamon_amd import layers
 
     starts, ends = _ranges(counts)
