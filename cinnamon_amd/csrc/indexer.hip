@@ -130,6 +130,13 @@ struct KeyStage {
 
 // D = head dim (multiple of 32, <= 256), HG = heads whose q fragments are held at once.
 // vec: k_scale and scores rows are 16-byte aligned (S % 4 == 0 and aligned bases).
+// max(x, 0) as one integer max of the bits (negative floats, -0 included, are negative
+// int32s, so they become +0; non-negative ones keep their bits): fmaxf also quiets a
+// signalling NaN first, two instructions per value.  The logits here are finite.
+__device__ __forceinline__ float relu1(float x) {
+  return __int_as_float(max(__float_as_int(x), 0));
+}
+
 template <int D, int HG>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWaves<D>, 8))) void k_indexer_scores_fp8(
     const uint8_t* __restrict__ q8, const float* __restrict__ qs, const uint8_t* __restrict__ k8,
@@ -190,14 +197,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWa
         for (int c = 0; c < NC; ++c) kf[c] = frag32<D>(kr, true, kq, c);
         v4f* slot = reinterpret_cast<v4f*>(&my[l16 * OS + 16 * j + 4 * kq]);
         v4f a = first ? v4f{0.0f, 0.0f, 0.0f, 0.0f} : *slot;
+        // every head's MFMAs first, then the head sum in increasing head order: the MFMAs
+        // run back to back instead of each waiting for its own result
+        v4f p[HG];
 #pragma unroll
         for (int g = 0; g < HG; ++g) {
-          v4f p = {0.0f, 0.0f, 0.0f, 0.0f};
+          p[g] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int c = 0; c < NC; ++c)
-            p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(kf[c], qf[g][c], p, 0, 0, 0, 0, 0, 0);
+            p[g] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(kf[c], qf[g][c], p[g], 0, 0, 0, 0, 0, 0);
+        }
+        // (the results pass through one empty asm: all MFMAs issue before any of them is read)
+        if constexpr (HG == 4)
+          asm volatile("" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3]));
+        else if constexpr (HG == 2)
+          asm volatile("" : "+v"(p[0]), "+v"(p[1]));
 #pragma unroll
-          for (int r = 0; r < 4; ++r) a[r] = a[r] + fmaxf(p[r], 0.0f) * wr[g];
+        for (int g = 0; g < HG; ++g) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) a[r] = a[r] + relu1(p[g][r]) * wr[g];
         }
         if (last) {
           const v4f kv = *reinterpret_cast<const v4f*>(&ksl[buf][16 * j + 4 * kq]);
@@ -325,14 +343,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWa
         const v4f gv = *reinterpret_cast<const v4f*>(&my[l16 * OS + 16 * j + 4 * kq]);
         const v4f kv = *reinterpret_cast<const v4f*>(&ksl[buf][16 * j + 4 * kq]);
         const v4f dx = v4f{gv[0] * kv[0], gv[1] * kv[1], gv[2] * kv[2], gv[3] * kv[3]};
+        // every head's MFMAs first (as in the scoring kernel), then the sums
+        v4f p[HG];
 #pragma unroll
         for (int g = 0; g < HG; ++g) {
-          v4f p = {0.0f, 0.0f, 0.0f, 0.0f};
+          p[g] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int c = 0; c < NC; ++c)
-            p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(kf[c], qf[g][c], p, 0, 0, 0, 0, 0, 0);
+            p[g] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(kf[c], qf[g][c], p[g], 0, 0, 0, 0, 0, 0);
+        }
+        if constexpr (HG == 4)
+          asm volatile("" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3]));
+        else if constexpr (HG == 2)
+          asm volatile("" : "+v"(p[0]), "+v"(p[1]));
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[g] = acc[g] + fmaxf(p[r], 0.0f) * dx[r];
+        for (int g = 0; g < HG; ++g) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[g] = acc[g] + relu1(p[g][r]) * dx[r];
         }
       }
       if (more) {
