@@ -215,7 +215,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWa
 #pragma unroll
         for (int g = 0; g < HG; ++g) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) a[r] = a[r] + relu1(p[g][r]) * wr[g];
+          // relu * weight added with one rounding (an FMA), not two: within the scores'
+          // tolerance either way, and 4% faster in this VALU-paced loop
+          for (int r = 0; r < 4; ++r) a[r] = __builtin_fmaf(relu1(p[g][r]), wr[g], a[r]);
         }
         if (last) {
           const v4f kv = *reinterpret_cast<const v4f*>(&ksl[buf][16 * j + 4 * kq]);
@@ -359,7 +361,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWa
 #pragma unroll
         for (int g = 0; g < HG; ++g) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) acc[g] = acc[g] + relu1(p[g][r]) * dx[r];
+          for (int r = 0; r < 4; ++r) acc[g] = __builtin_fmaf(relu1(p[g][r]), dx[r], acc[g]);
         }
       }
       if (more) {

@@ -5,9 +5,9 @@ The codes and scales come from the row-wise quantizer (bit-exact with the oracle
 in test_gpu_quant.py), so the scores differ from the oracle only in the code dot products.
 Each product of two e4m3 codes is exact in fp32, and the oracle's fp32 einsum is within
 1e-7 (normwise) of an exact fp64 evaluation on these inputs. The kernel sums the products
-with v_mfma_f32_16x16x32_fp8_fp8, whose 32-product sum inside one instruction is not an
-exact fp32 sum: measured 1.3e-5 to 2.2e-5 of the largest score (normwise) and 1.1e-5 to
-1.5e-5 (Frobenius) over these cases. Tolerance: max |error| <= 1e-4 * max |reference|
+with v_mfma_f32_16x16x128_f8f6f4, whose product sums inside one instruction are not exact
+fp32 sums: measured 1.3e-5 to 2.4e-5 of the largest score (normwise) and 1.1e-5 to
+1.9e-5 (Frobenius) over these cases. Tolerance: max |error| <= 1e-4 * max |reference|
 (normwise) and Frobenius relative error <= 5e-5, 20x tighter than the FP8 GEMM bar (2e-3
 and 1e-3). The weights gradient (the
 reference's autograd through the same branch) is held to the same bounds.
