@@ -58,6 +58,8 @@ def _run_fp32_and_bf16(kern, dev, xq, xs, wq, ws):
     (4100, 4224, 512),    # more 256 x 256 tiles than CUs (persistent walk), last row and column shifted
     (2304, 7296, 4096),   # persistent walk with the XCD-rotated K order (32 K blocks)
     (8192, 2176, 384),    # 288 tiles (persistent walk), N % 256 = 128: the last column tile shifted back
+    (6400, 5376, 256),    # 525 tiles: XCD-major ranges of 65 and 66 tiles, three rounds
+    (2560, 6912, 256),    # 270 tiles: ranges of 33 and 34 tiles, the last partly empty
 ])
 def test_gemm_parity(kern, dev, M, N, K):
     xq, xs, wq, ws = _operands(M, N, K, seed=M + N + K)
