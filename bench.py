@@ -753,6 +753,14 @@ def main():
     def indexer_full(i):
         kernels.indexer_scores_fp8(ix["q"], ix["k"], ix["w"], 0.125)
 
+    def indexer_two_call(i):
+        # both quantizations in one launch, then the scoring kernel on the codes
+        c = torch.ops.cinnamon_amd.indexer_quantize(ix["q"], ix["k"])
+        torch.ops.cinnamon_amd.indexer_scores_fp8(*c, ix["w"], 0.125)
+
+    def indexer_fused(i):
+        torch.ops.cinnamon_amd.indexer_scores_fp8_q(ix["q"], ix["k8"], ix["ks"], ix["w"], 0.125, False)
+
     def indexer_full_fwd_bwd(i):
         w = ix["w"].detach().requires_grad_(True)
         kernels.indexer_scores_fp8(ix["q"], ix["k"], w, 0.125).backward(ix["g"])
@@ -993,6 +1001,9 @@ def main():
     if ix is not None:
         IB, IL, IH, ID = ix["shape"]
         k_us = kernel_loop(indexer, 20, 3)
+        kf_us = kernel_loop(indexer_fused, 20, 3)
+        kc_us = kernel_loop(indexer_full, 20, 3)
+        k2_us = kernel_loop(indexer_two_call, 20, 3)
         kb_us = kernel_loop(indexer_wgrad, 20, 3)
         f_us = time_loop(indexer_full, 10, 2)
         t_us = time_loop(indexer_torch, 5, 1)
@@ -1004,10 +1015,16 @@ def main():
         out["components"]["config5_indexer_scores"] = {
             "what": "kernels.indexer_scores_fp8 on 16 x 1024 tokens, 4 heads, d 128, against the "
                     "reference's FP8 einsum formulation (quantize, fp32 einsum, relu, weight, head "
-                    "sum) on the same GPU",
+                    "sum) on the same GPU.  kernel_us: the scoring kernel on codes; fused_q_kernel_us: "
+                    "the one that quantizes q itself; call_device_us: the whole call's device time "
+                    "(k quantization + fused kernel), against the two-call form (both "
+                    "quantizations, then scoring on codes)",
             "kernel_us": round(k_us, 1), "kernel_gbps": round(i_bytes / k_us / 1e3, 1),
             "kernel_frac_of_hbm": round(i_bytes / k_us / 1e3 / PEAK_HBM_GBPS, 4),
             "kernel_tflops": round(i_flops / k_us / 1e6, 1),
+            "fused_q_kernel_us": round(kf_us, 1),
+            "call_device_us": round(kc_us, 1),
+            "call_device_us_two_call": round(k2_us, 1),
             "weights_grad_kernel_us": round(kb_us, 1),
             "weights_grad_kernel_frac_of_hbm": round(i_bytes / kb_us / 1e3 / PEAK_HBM_GBPS, 4),
             "with_quantization_us": round(f_us, 1),

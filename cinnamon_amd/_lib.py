@@ -57,6 +57,8 @@ SIGNATURES: dict[str, list] = {
     "cin_indexer_quantize": [_p, _i32, _p, _i32, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p],
     "cin_indexer_scores_fp8": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p,
                                _p],
+    "cin_indexer_scores_fp8_q": [_p, _i32, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p,
+                                 _p, _p, _p],
     "cin_indexer_weights_grad": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p,
                                  _i64, _p, _p],
     "cin_indexer_weights_grad_workspace": [_i64, _i64, _i64, _i64],

@@ -93,6 +93,25 @@ __device__ inline uint32_t cvt4_e4m3(float a, float b, float c, float d) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
 }
 
+// Quantize NV (multiple of 4) values with scale s / reciprocal r into packed codes.
+// STEPS = correction steps of div_by_scale (1 for bf16/fp16 tiles, 2 for fp32).
+template <int NV, int STEPS>
+__device__ inline void quant_vals(const float (&v)[NV], float s, float r, uint32_t (&out)[NV / 4]) {
+  float y[NV];
+  if (s < __builtin_inff()) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) y[i] = div_by_scale<STEPS>(v[i], s, r);
+  } else {
+    // infinite amax: x / inf is a signed zero, inf / inf NaN
+#pragma unroll
+    for (int i = 0; i < NV; ++i) y[i] = v[i] / s;
+  }
+#pragma unroll
+  for (int i = 0; i < NV / 4; ++i)
+    out[i] = cvt4_e4m3(clamp448(y[4 * i]), clamp448(y[4 * i + 1]), clamp448(y[4 * i + 2]),
+                       clamp448(y[4 * i + 3]));
+}
+
 // e4m3fn code -> fp32 (exact).
 __device__ inline float e4m3_to_f32(uint32_t c) {
   uint32_t s = (c & 0x80u) << 24;

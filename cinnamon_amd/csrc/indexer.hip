@@ -137,12 +137,104 @@ __device__ __forceinline__ float relu1(float x) {
   return __int_as_float(max(__float_as_int(x), 0));
 }
 
-template <int D, int HG>
+// The fused form's q quantization.  Lane (l16, kq) holds bytes [128 c + 32 kq, + 32) of each
+// of its token's head rows (the MFMA's B-operand layout), so a 1 x 128 tile of a row lies in
+// the four lanes l16, l16 + 16, l16 + 32, l16 + 48.  The arithmetic is the row-wise
+// quantizer's (k_rowwise128 with 1 x 128 tiles: maxnum of |x| from 0, the fp32(1e-4) floor,
+// amax / 448, RN(x / scale) clamped to +-448, e4m3 RNE), so codes and scales are the ones
+// cin_indexer_quantize writes.  QDT is the input dtype.
+template <int QDT>
+struct RawSlice {
+  static constexpr int ES = QDT == CIN_DT_F32 ? 4 : 2;
+  static constexpr int NW = 32 * ES / 16;  // 16-byte words for 32 elements
+  uint4 w[NW];
+};
+
+// 32 input elements at element offset 128 c + 32 kq of a d-element row, zero past d or when
+// !ok (a zero slice leaves the tile's amax as it is).
+template <int D, int QDT>
+__device__ inline void load_slice(const void* row, bool ok, int kq, int c, RawSlice<QDT>& r) {
+  const int off = c * 128 + 32 * kq;
+#pragma unroll
+  for (int i = 0; i < RawSlice<QDT>::NW; ++i) r.w[i] = uint4{0u, 0u, 0u, 0u};
+  if (ok && off < D) {
+    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(row) +
+                                                    (int64_t)off * RawSlice<QDT>::ES);
+#pragma unroll
+    for (int i = 0; i < RawSlice<QDT>::NW; ++i) r.w[i] = p[i];
+  }
+}
+
+// Codes of a lane's 32 elements as the MFMA fragment, and the tile's scale.  Every lane of
+// the wave calls it (the tile's amax is exchanged across lanes).
+template <int QDT>
+__device__ inline v8i quant_slice(const RawSlice<QDT>& r, float& scale) {
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < RawSlice<QDT>::NW; ++i) {
+    const uint4 w = r.w[i];
+    const uint32_t e[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (QDT == CIN_DT_F32) {
+        v[4 * i + j] = __uint_as_float(e[j]);
+      } else if constexpr (QDT == CIN_DT_BF16) {
+        v[8 * i + 2 * j] = bf16_lo(e[j]);
+        v[8 * i + 2 * j + 1] = bf16_hi(e[j]);
+      } else {
+        v[8 * i + 2 * j] = half_bits_to_f32(CIN_DT_F16, (uint16_t)(e[j] & 0xffffu));
+        v[8 * i + 2 * j + 1] = half_bits_to_f32(CIN_DT_F16, (uint16_t)(e[j] >> 16));
+      }
+    }
+  }
+  float a = 0.0f;
+  if constexpr (QDT == CIN_DT_F32) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) a = fmaxf(a, fabsf(v[i]));
+  } else {
+    // 16-bit inputs: the magnitudes' bit patterns order as unsigned integers (infinity
+    // above every finite value, NaN above infinity), so two at a time with a packed 16-bit
+    // max; a NaN among them sends the lane to maxnum, which skips NaNs.  Widening to fp32 is
+    // exact and keeps the order, so the result is maxnum's.
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 m = {0, 0};
+#pragma unroll
+    for (int i = 0; i < RawSlice<QDT>::NW; ++i) {
+      const uint32_t e[4] = {r.w[i].x, r.w[i].y, r.w[i].z, r.w[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, e[j] & 0x7fff7fffu));
+    }
+    const uint32_t mag = m[0] > m[1] ? m[0] : m[1];
+    constexpr uint32_t kInf = QDT == CIN_DT_BF16 ? 0x7f80u : 0x7c00u;
+    if (mag <= kInf) {
+      a = QDT == CIN_DT_BF16 ? __uint_as_float(mag << 16) : half_bits_to_f32(CIN_DT_F16, (uint16_t)mag);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) a = fmaxf(a, fabsf(v[i]));
+    }
+  }
+  // a >= 0 and never NaN (maxnum from 0): the bit patterns order as unsigned integers
+  uint32_t u = __float_as_uint(a);
+  u = max(u, (uint32_t)__shfl_xor((int)u, 16));
+  u = max(u, (uint32_t)__shfl_xor((int)u, 32));
+  const float s = compute_scale(fmaxf(__uint_as_float(u), amax_floor(QDT)), false);
+  uint32_t out[8];
+  quant_vals<32, kDivSteps<QDT>>(v, s, 1.0f / s, out);
+  scale = s;
+  return v8i{(int)out[0], (int)out[1], (int)out[2], (int)out[3],
+             (int)out[4], (int)out[5], (int)out[6], (int)out[7]};
+}
+
+// QDT < 0: q arrives as codes q8 with first scales qs.  QDT = an input dtype (the fused form):
+// q arrives unquantized and each wave quantizes its own tokens' rows (H <= HG, so once per
+// workgroup); when q8_out is not null the codes go to q8_out and the first scales to qs_out,
+// each head's by one of the workgroups that share the tokens.
+template <int D, int HG, int QDT = -1>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWaves<D>, 8))) void k_indexer_scores_fp8(
-    const uint8_t* __restrict__ q8, const float* __restrict__ qs, const uint8_t* __restrict__ k8,
+    const void* __restrict__ qin, const float* __restrict__ qs, const uint8_t* __restrict__ k8,
     const float* __restrict__ ks, const float* __restrict__ w, int64_t L, int64_t S, int64_t H,
     float softmax_scale, float* __restrict__ out, int64_t tiles_t, int64_t tiles_s, int xcd_rotate,
-    int vec) {
+    int vec, uint8_t* __restrict__ q8_out = nullptr, float* __restrict__ qs_out = nullptr) {
   constexpr int NC = (D + 127) / 128;           // 128-byte slices of d
   constexpr int RS = KeyStage<D>::RS;
   constexpr int OS = kKT + 4;                   // staging row stride (floats)
@@ -159,23 +251,85 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWa
   // the wave's tokens: q fragments and head weights for HG heads
   const int64_t tok = tl.tt * kTT + wave * 16 + l16;
   const bool tok_ok = tok < L;
-  const uint8_t* qrow = q8 + (b * L + (tok_ok ? tok : 0)) * H * D;
   const int64_t orow = (b * L + (tok_ok ? tok : 0)) * H;
   v8i qf[HG][NC];
   float wr[HG];
   auto load_q = [&](int64_t h0) {
+    if constexpr (QDT < 0) {
+      const uint8_t* qrow = static_cast<const uint8_t*>(qin) + orow * D;
 #pragma unroll
-    for (int g = 0; g < HG; ++g) {
-      const bool ok = tok_ok && h0 + g < H;
+      for (int g = 0; g < HG; ++g) {
+        const bool ok = tok_ok && h0 + g < H;
 #pragma unroll
-      for (int c = 0; c < NC; ++c) qf[g][c] = frag32<D>(qrow + (h0 + g) * D, ok, kq, c);
-      wr[g] = ok ? (qs[orow + h0 + g] * w[orow + h0 + g]) * softmax_scale : 0.0f;
+        for (int c = 0; c < NC; ++c) qf[g][c] = frag32<D>(qrow + (h0 + g) * D, ok, kq, c);
+        wr[g] = ok ? (qs[orow + h0 + g] * w[orow + h0 + g]) * softmax_scale : 0.0f;
+      }
+    }
+  };
+  // The fused form: q's rows as loaded (after the first key sub-tile's loads: issuing them
+  // first measured slower), then quantized.
+  constexpr int RW = QDT < 0 ? 1 : HG;
+  constexpr int RC = QDT < 0 ? 1 : NC;
+  RawSlice<QDT < 0 ? CIN_DT_BF16 : QDT> raw[RW][RC];
+  float wv[RW];
+  auto load_q_raw = [&]() {
+    if constexpr (QDT >= 0) {
+      const uint8_t* qrow = static_cast<const uint8_t*>(qin) + orow * D * RawSlice<QDT>::ES;
+#pragma unroll
+      for (int g = 0; g < HG; ++g) {
+        const bool ok = tok_ok && g < H;
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+          load_slice<D, QDT>(qrow + g * D * RawSlice<QDT>::ES, ok, kq, c, raw[g][c]);
+        wv[g] = ok ? w[orow + g] : 0.0f;
+      }
+    }
+  };
+  auto quant_q = [&]() {
+    if constexpr (QDT >= 0) {
+      float s0[HG];
+#pragma unroll
+      for (int g = 0; g < HG; ++g) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          float sc;
+          qf[g][c] = quant_slice<QDT>(raw[g][c], sc);
+          if (c == 0) s0[g] = sc;
+        }
+        const bool ok = tok_ok && g < H;
+        wr[g] = ok ? (s0[g] * wv[g]) * softmax_scale : 0.0f;
+      }
+      if (q8_out != nullptr) {
+        // every workgroup of the 64 tokens holds all their codes: head h is written by the
+        // one of key range h % tiles_s, so the writes spread over the ranges
+#pragma unroll
+        for (int g = 0; g < HG; ++g) {
+          if (!(tok_ok && g < H) || g % tiles_s != tl.sw) continue;
+          uint8_t* dst = q8_out + (orow + g) * D;
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            const int off = c * 128 + 32 * kq;
+            if (off < D) {
+              const v8i f = qf[g][c];
+              *reinterpret_cast<uint4*>(dst + off) = uint4{(uint32_t)f[0], (uint32_t)f[1], (uint32_t)f[2], (uint32_t)f[3]};
+              *reinterpret_cast<uint4*>(dst + off + 16) = uint4{(uint32_t)f[4], (uint32_t)f[5], (uint32_t)f[6], (uint32_t)f[7]};
+            }
+          }
+          if (kq == 0) qs_out[orow + g] = s0[g];
+        }
+      }
     }
   };
   const bool one_group = H <= HG;
 
-  stage.load(k8, ks, b, S, tl.s_begin, tl.s_end, vec);
-  load_q(0);
+  if constexpr (QDT < 0) {
+    stage.load(k8, ks, b, S, tl.s_begin, tl.s_end, vec);
+    load_q(0);
+  } else {
+    stage.load(k8, ks, b, S, tl.s_begin, tl.s_end, vec);
+    load_q_raw();
+    quant_q();
+  }
   stage.store(kl[0], ksl[0]);
   __syncthreads();
   float* my = ost + wave * 16 * OS;
@@ -187,7 +341,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWa
     // belong to this wave alone and a wave's LDS accesses complete in order, so no
     // workgroup barrier is needed around them.
     for (int64_t h0 = 0; h0 < H; h0 += HG) {
-      if (!one_group) load_q(h0);
+      if constexpr (QDT < 0) {
+        if (!one_group) load_q(h0);
+      }
       const bool first = h0 == 0, last = h0 + HG >= H;
 #pragma unroll 2
       for (int j = 0; j < 8; ++j) {
@@ -406,6 +562,23 @@ void launch_indexer(unsigned grid, hipStream_t st, const uint8_t* q8, const floa
 }
 
 template <int D, int HG>
+void launch_indexer_q(int q_dtype, unsigned grid, hipStream_t st, const void* q, const uint8_t* k8,
+                      const float* ks, const float* w, int64_t L, int64_t S, int64_t H,
+                      float softmax_scale, float* out, int64_t tiles_t, int64_t tiles_s,
+                      int xcd_rotate, int vec, uint8_t* q8_out, float* qs_out) {
+#define CIN_IQ_LAUNCH(DT)                                                                         \
+  hipLaunchKernelGGL((k_indexer_scores_fp8<D, HG, DT>), grid, kThreads, 0, st, q, nullptr, k8, ks, w, \
+                     L, S, H, softmax_scale, out, tiles_t, tiles_s, xcd_rotate, vec, q8_out, qs_out)
+  if (q_dtype == CIN_DT_BF16)
+    CIN_IQ_LAUNCH(CIN_DT_BF16);
+  else if (q_dtype == CIN_DT_F16)
+    CIN_IQ_LAUNCH(CIN_DT_F16);
+  else
+    CIN_IQ_LAUNCH(CIN_DT_F32);
+#undef CIN_IQ_LAUNCH
+}
+
+template <int D, int HG>
 void launch_wgrad(unsigned grid, hipStream_t st, const uint8_t* q8, const uint8_t* k8,
                   const float* ks, const float* gs, int64_t B, int64_t L, int64_t S, int64_t H,
                   float* partial, int64_t tiles_t, int64_t tiles_s, int xcd_rotate, int vec) {
@@ -446,6 +619,52 @@ int cin_indexer_scores_fp8(const uint8_t* q8, const float* q_scale, const uint8_
 #undef CIN_INDEXER_CASE
   }
   return cin_check_launch("indexer_scores_fp8");
+}
+
+int cin_indexer_scores_fp8_q(const void* q, int q_dtype, const uint8_t* k8, const float* k_scale,
+                             const float* weights, int64_t B, int64_t L, int64_t S, int64_t H, int64_t d,
+                             float softmax_scale, float* scores, uint8_t* q8, float* q_scale,
+                             void* stream) {
+  CIN_CHECK_ARG(q_dtype == CIN_DT_BF16 || q_dtype == CIN_DT_F16 || q_dtype == CIN_DT_F32,
+                "indexer_scores_fp8_q: unsupported q dtype %d", q_dtype);
+  CIN_CHECK_ARG(B >= 0 && L >= 0 && S >= 0 && H >= 1, "indexer_scores_fp8_q: bad sizes");
+  CIN_CHECK_ARG(d >= 32 && d <= 256 && d % 32 == 0,
+                "indexer_scores_fp8_q: head dim %lld must be a multiple of 32 in [32, 256]", (long long)d);
+  const int64_t hg = d <= 128 ? 4 : 2;
+  CIN_CHECK_ARG(H <= hg,
+                "indexer_scores_fp8_q: %lld heads at head dim %lld, at most %lld (quantize q with "
+                "cin_indexer_quantize and call cin_indexer_scores_fp8)", (long long)H, (long long)d,
+                (long long)hg);
+  CIN_CHECK_ARG((q8 == nullptr) == (q_scale == nullptr),
+                "indexer_scores_fp8_q: q8 and q_scale are both given or both null");
+  if (B == 0 || L == 0) return CIN_OK;
+  CIN_CHECK_ARG(q != nullptr, "indexer_scores_fp8_q: null pointer");
+  CIN_CHECK_ARG((((uintptr_t)q) & 15) == 0 && (((uintptr_t)q8) & 15) == 0,
+                "indexer_scores_fp8_q: q and q8 must be 16-byte aligned");
+  if (S == 0) {  // no scores to write; the codes are still asked for
+    if (q8 == nullptr) return CIN_OK;
+    return cin_indexer_quantize(q, q_dtype, q, q_dtype, B, L, 0, H, d, q8, q_scale, nullptr, nullptr,
+                                stream);
+  }
+  CIN_CHECK_ARG(k8 && k_scale && weights && scores, "indexer_scores_fp8_q: null pointer");
+  CIN_CHECK_ARG((((uintptr_t)k8) & 15) == 0, "indexer_scores_fp8_q: k8 must be 16-byte aligned");
+  const int64_t tiles_t = cdiv(L, kTT), tiles_s = cdiv(S, kKPW);
+  CIN_CHECK_ARG(B * tiles_t * tiles_s < ((int64_t)1 << 31), "indexer_scores_fp8_q: grid too large");
+  const unsigned grid = (unsigned)(B * tiles_t * tiles_s);
+  const int xcd_rotate = grid % 8 == 0;
+  const int vec = S % 4 == 0 && (((uintptr_t)k_scale) & 15) == 0 && (((uintptr_t)scores) & 15) == 0;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (d / 32) {
+#define CIN_INDEXER_Q_CASE(n, hgv)                                                                  \
+  case n:                                                                                           \
+    launch_indexer_q<32 * n, hgv>(q_dtype, grid, st, q, k8, k_scale, weights, L, S, H, softmax_scale, \
+                                  scores, tiles_t, tiles_s, xcd_rotate, vec, q8, q_scale);          \
+    break;
+    CIN_INDEXER_Q_CASE(1, 4) CIN_INDEXER_Q_CASE(2, 4) CIN_INDEXER_Q_CASE(3, 4) CIN_INDEXER_Q_CASE(4, 4)
+    CIN_INDEXER_Q_CASE(5, 2) CIN_INDEXER_Q_CASE(6, 2) CIN_INDEXER_Q_CASE(7, 2) CIN_INDEXER_Q_CASE(8, 2)
+#undef CIN_INDEXER_Q_CASE
+  }
+  return cin_check_launch("indexer_scores_fp8_q");
 }
 
 int64_t cin_indexer_weights_grad_workspace(int64_t B, int64_t L, int64_t S, int64_t H) {

@@ -85,25 +85,6 @@ __device__ inline float row8_max(float v) {
   return v;
 }
 
-// Quantize NV (multiple of 4) values with scale s / reciprocal r into packed codes.
-// STEPS = correction steps of div_by_scale (1 for bf16/fp16 tiles, 2 for fp32).
-template <int NV, int STEPS>
-__device__ inline void quant_vals(const float (&v)[NV], float s, float r, uint32_t (&out)[NV / 4]) {
-  float y[NV];
-  if (s < __builtin_inff()) {
-#pragma unroll
-    for (int i = 0; i < NV; ++i) y[i] = div_by_scale<STEPS>(v[i], s, r);
-  } else {
-    // infinite amax: x / inf is a signed zero, inf / inf NaN
-#pragma unroll
-    for (int i = 0; i < NV; ++i) y[i] = v[i] / s;
-  }
-#pragma unroll
-  for (int i = 0; i < NV / 4; ++i)
-    out[i] = cvt4_e4m3(clamp448(y[4 * i]), clamp448(y[4 * i + 1]), clamp448(y[4 * i + 2]),
-                       clamp448(y[4 * i + 3]));
-}
-
 // Row-wise 1x128 with contiguous rows: LANES lanes (8 or 16, a DPP half-row or
 // row) own one tile.  Each lane loads NC 16-byte chunks, chunk c of lane i sitting at
 // tile chunk c * LANES + i so every load instruction reads whole 16*LANES-byte runs.

@@ -788,10 +788,12 @@ def indexer_scores_fp8(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor,
     """The FP8 branch of DSAIndexer.forward up to the mask (reference
     src/attention.py:288-300): q [B, L, H, d] and k [B, S, d] quantized row-wise (1x128,
     the first scale of each row), scores [B, L, S] fp32 = k_scale * sum_h
-    relu(q_codes . k_codes) * (q_scale * weights * softmax_scale).  Two launches: both
-    quantizations (first scales only), then one scoring kernel; the reference's
-    [B, L, H, S] fp32 logits are never written.  weights [B, L, H]; d a multiple of 32 up
-    to 256.
+    relu(q_codes . k_codes) * (q_scale * weights * softmax_scale).  Two launches: k's
+    quantization, then one scoring kernel that quantizes q itself (H <= 4 for d <= 128,
+    H <= 2 above; with more heads both quantizations run first, in one launch, and the
+    scoring kernel takes the codes).  Scores, codes and scales are the same either way; the
+    reference's [B, L, H, S] fp32 logits are never written.  weights [B, L, H]; d a multiple
+    of 32 up to 256.
 
     Differentiable in `weights` only, as the reference's branch is: its q and k pass through
     the quantizer, which carries no gradient (the scores feed the indexer's KL loss,
@@ -803,8 +805,14 @@ def indexer_scores_fp8(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor,
     _require(k.shape[0] == B and k.shape[2] == d, "k must be [B, S, d] with q's B and d")
     _require(d % 32 == 0 and 32 <= d <= 256, "head dim must be a multiple of 32 in [32, 256]")
     S = k.shape[1]
+    w = weights.float().contiguous()
+    if H <= (4 if d <= 128 else 2):
+        k8, ks = _indexer_quant_k_op(k.detach(), H)
+        # the q codes are kept only for the weights' gradient
+        save_q = torch.is_grad_enabled() and w.requires_grad
+        return _indexer_q_op(q.detach(), k8, ks, w, float(softmax_scale), save_q)[0]
     q8, qs, k8, ks = _indexer_quant_op(q.detach(), k.detach())
-    return _indexer_op(q8, qs, k8, ks, weights.float().contiguous(), float(softmax_scale))
+    return _indexer_op(q8, qs, k8, ks, w, float(softmax_scale))
 
 
 def _aligned16(t: torch.Tensor) -> torch.Tensor:
@@ -835,6 +843,73 @@ def _(q, k):
     S = k.shape[1]
     return (q.new_empty((B, L, H, d), dtype=torch.float8_e4m3fn), q.new_empty((B, L, H), dtype=torch.float32),
             q.new_empty((B, S, d), dtype=torch.float8_e4m3fn), q.new_empty((B, S), dtype=torch.float32))
+
+
+@custom_op("indexer_quantize_k", "(Tensor k, int H) -> (Tensor, Tensor)")
+def _indexer_quant_k_op(k, H):
+    """k's side of indexer_quantize alone: (codes [B, S, d], first scales [B, S])."""
+    B, S, d = k.shape
+    k = _aligned16(k)
+    k8 = torch.empty((B, S, d), dtype=torch.float8_e4m3fn, device=k.device)
+    ks = torch.empty((B, S), dtype=torch.float32, device=k.device)
+    # (L = 0: no q rows; q's pointer and dtype are k's)
+    call("cin_indexer_quantize", ptr(k), dtype_code(k), ptr(k), dtype_code(k), B, 0, S, H, d, None, None,
+         ptr(k8), ptr(ks), stream_of(k))
+    return k8, ks
+
+
+@_indexer_quant_k_op.register_fake
+def _(k, H):
+    B, S, d = k.shape
+    return k.new_empty((B, S, d), dtype=torch.float8_e4m3fn), k.new_empty((B, S), dtype=torch.float32)
+
+
+@custom_op("indexer_scores_fp8_q", "(Tensor q, Tensor k8, Tensor k_scale, Tensor weights, float softmax_scale, "
+           "bool save_q) -> (Tensor, Tensor, Tensor)")
+def _indexer_q_op(q, k8, k_scale, weights, softmax_scale, save_q):
+    """Scores from unquantized q (cin_indexer_scores_fp8_q): (scores [B, L, S], q codes
+    [B, L, H, d], q first scales [B, L, H]), the last two empty unless save_q."""
+    B, L, H, d = q.shape
+    S = k8.shape[1]
+    q = _aligned16(q)
+    kc = _codes_u8(k8).contiguous()
+    out = torch.empty((B, L, S), dtype=torch.float32, device=q.device)
+    q8 = torch.empty((B, L, H, d) if save_q else (0,), dtype=torch.float8_e4m3fn, device=q.device)
+    qs = torch.empty((B, L, H) if save_q else (0,), dtype=torch.float32, device=q.device)
+    call("cin_indexer_scores_fp8_q", ptr(q), dtype_code(q), ptr(kc), ptr(k_scale.contiguous()),
+         ptr(weights.contiguous()), B, L, S, H, d, softmax_scale, ptr(out), ptr(q8) if save_q else None,
+         ptr(qs) if save_q else None, stream_of(q))
+    return out, q8, qs
+
+
+@_indexer_q_op.register_fake
+def _(q, k8, k_scale, weights, softmax_scale, save_q):
+    B, L, H, d = q.shape
+    return (q.new_empty((B, L, k8.shape[1]), dtype=torch.float32),
+            q.new_empty((B, L, H, d) if save_q else (0,), dtype=torch.float8_e4m3fn),
+            q.new_empty((B, L, H) if save_q else (0,), dtype=torch.float32))
+
+
+def _indexer_q_setup(ctx, inputs, output):
+    _q, k8, k_scale, _weights, softmax_scale, save_q = inputs
+    _out, q8, q_scale = output
+    ctx.mark_non_differentiable(q8, q_scale)
+    ctx.save_q = save_q
+    if save_q:
+        ctx.save_for_backward(q8, q_scale, k8, k_scale)
+    ctx.softmax_scale = softmax_scale
+
+
+def _indexer_q_backward(ctx, grad, _grad_q8, _grad_qs):
+    dw = None
+    if ctx.needs_input_grad[3]:
+        _require(ctx.save_q, "indexer_scores_fp8_q: the weights' gradient needs save_q=True")
+        q8, q_scale, k8, k_scale = ctx.saved_tensors
+        dw = _indexer_wgrad_op(q8, q_scale, k8, k_scale, grad, ctx.softmax_scale)
+    return None, None, None, dw, None, None
+
+
+_indexer_q_op.register_autograd(_indexer_q_backward, setup_context=_indexer_q_setup)
 
 
 @custom_op("indexer_scores_fp8",

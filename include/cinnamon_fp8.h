@@ -355,6 +355,22 @@ int cin_indexer_scores_fp8(const uint8_t* q8, const float* q_scale, const uint8_
                            void* stream);
 
 /*
+ * cin_indexer_quantize's q side and cin_indexer_scores_fp8 in one launch (no counterpart in
+ * the reference, whose FP8 branch quantizes q as a separate step, src/attention.py:292-297):
+ * q [B, L, H, d] arrives unquantized (bf16, fp16 or fp32, contiguous, 16-byte aligned) and
+ * each workgroup quantizes its own tokens' rows with cin_indexer_quantize's arithmetic, so
+ * the scores are bit-identical to the two calls.  k8 / k_scale as for cin_indexer_scores_fp8
+ * (cin_indexer_quantize with L = 0 makes them).  When q8 and q_scale are not null the codes
+ * [B, L, H, d] and first scales [B, L, H] are written as well (what
+ * cin_indexer_weights_grad takes); both null skips them.  H <= 4 for d <= 128 and H <= 2
+ * above; more heads are rejected (use the two calls).
+ */
+int cin_indexer_scores_fp8_q(const void* q, int q_dtype, const uint8_t* k8, const float* k_scale,
+                             const float* weights, int64_t B, int64_t L, int64_t S, int64_t H, int64_t d,
+                             float softmax_scale, float* scores, uint8_t* q8, float* q_scale,
+                             void* stream);
+
+/*
  * Gradient of cin_indexer_scores_fp8's scores with respect to `weights`, the reference's
  * autograd through its FP8 branch (src/attention.py:298-300; the codes come from the
  * quantizer and carry no gradient, so q and k get none):

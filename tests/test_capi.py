@@ -97,6 +97,14 @@ def test_no_rpath_to_a_second_hip_runtime():
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 2, 288, 0.1, None, None)),  # d > 256
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 0, 64, 0.1, None, None)),   # H = 0
     ("cin_indexer_scores_fp8", (None, None, None, None, None, 1, 8, 8, 2, 64, 0.1, None, None)),   # null ptrs
+    # scores_fp8_q: q, q_dtype, k8, k_scale, weights, B, L, S, H, d, softmax_scale, scores, q8, q_scale, stream
+    ("cin_indexer_scores_fp8_q", (16, 9, None, None, None, 1, 8, 8, 2, 64, 0.1, None, None, None, None)),   # dtype
+    ("cin_indexer_scores_fp8_q", (16, 0, None, None, None, 1, 8, 8, 5, 64, 0.1, None, None, None, None)),   # H > 4
+    ("cin_indexer_scores_fp8_q", (16, 0, None, None, None, 1, 8, 8, 3, 192, 0.1, None, None, None, None)),  # H > 2
+    ("cin_indexer_scores_fp8_q", (16, 0, None, None, None, 1, 8, 8, 2, 64, 0.1, None, 16, None, None)),     # q8 alone
+    ("cin_indexer_scores_fp8_q", (None, 0, None, None, None, 1, 8, 8, 2, 64, 0.1, None, None, None, None)), # null q
+    ("cin_indexer_scores_fp8_q", (8, 0, None, None, None, 1, 8, 8, 2, 64, 0.1, None, None, None, None)),    # q align
+    ("cin_indexer_scores_fp8_q", (16, 0, None, None, None, 1, 8, 8, 2, 64, 0.1, None, None, None, None)),   # null k8
     ("cin_indexer_weights_grad", (None, None, None, None, None, 1, 8, 8, 2, 48, 0.1, None, 16, None, None)),
     ("cin_indexer_weights_grad", (None, None, None, None, None, 1, 8, 8, 2, 64, 0.1, None, 15, None, None)),
 ])
@@ -116,6 +124,8 @@ def test_empty_shapes_are_noops():
     assert lib.cin_moe_gather_sum(None, 1, 8, None, 0, 2, 0, 8, None, 1, 8, None) == 0
     assert lib.cin_moe_combine(None, 1, 8, None, 1, 2, None, 0, 2, 0, 8, None, 8, None) == 0
     assert lib.cin_indexer_scores_fp8(None, None, None, None, None, 1, 0, 8, 2, 64, 0.1, None, None) == 0
+    assert lib.cin_indexer_scores_fp8_q(None, 0, None, None, None, 1, 0, 8, 2, 64, 0.1, None, None, None,
+                                        None) == 0
     assert lib.cin_quant_fwd(None, 0, 0, 256, 256, 0, None, 256, None, 2, 1, None, 0, 0, 256, None, 256, None,
                              0, None, 2, None) == 0
     assert lib.cin_quant_backward(None, 0, 0, 256, 256, 0, None, 256, None, 2, 1, None, 0, None, 0, 1, None,

@@ -124,3 +124,7 @@ def test_opcheck_operators(dev):
     torch.library.opcheck(ops.indexer_scores_fp8.default, (*args, wi, 0.125), test_utils=full)
     gsi = torch.randn(2, 70, 90, device=dev, generator=g)
     torch.library.opcheck(ops.indexer_weights_grad_fp8.default, (*args, gsi, 0.125), test_utils=full)
+    torch.library.opcheck(ops.indexer_quantize_k.default, (ki, 4), test_utils=f8)
+    for save in (True, False):
+        torch.library.opcheck(ops.indexer_scores_fp8_q.default, (qi, args[2], ksi, wi, 0.125, save),
+                              test_utils=f8)

@@ -52,6 +52,42 @@ def test_scores_match_the_oracle(dev, B, L, S, H, d, dtype):
     _check(got, orc.indexer_scores_fp8_ref(q, k, w, scale))
 
 
+@pytest.mark.parametrize("B,L,S,H,d,dtype", [
+    (2, 1024, 1024, 4, 128, torch.bfloat16),   # the config-5 shape: two key ranges per token tile
+    (2, 100, 300, 4, 128, torch.float16),
+    (2, 70, 513, 3, 96, torch.float32),        # ragged token and key tiles, a partial 1x128 tile
+    (1, 130, 700, 2, 256, torch.bfloat16),     # two 1x128 tiles per row
+    (2, 65, 1030, 2, 160, torch.float32),      # three key ranges, the second tile 32 wide
+    (1, 64, 5, 1, 32, torch.float16),          # S % 4 != 0: the scalar score stores
+    (1, 33, 0, 2, 64, torch.bfloat16),         # no keys: only the codes are written
+])
+def test_fused_q_quantization_equals_the_two_calls(dev, B, L, S, H, d, dtype):
+    """cin_indexer_scores_fp8_q quantizes q inside the scoring kernel with the row-wise
+    quantizer's arithmetic: its scores must equal, bit for bit, cin_indexer_quantize +
+    cin_indexer_scores_fp8 on the same inputs, and the codes and first scales it writes
+    (save_q) must equal cin_indexer_quantize's.  q carries NaN and +-inf elements: a 16-bit
+    lane holding a NaN takes the maxnum path, an infinite amax the division path."""
+    q, k, w = _inputs(B, L, S, H, d, dtype, seed=B * 7 + L + S + d)
+    flat = q.view(-1)
+    flat[::97] *= 50
+    flat[5::1031] = float("nan")
+    flat[7::2063] = float("inf")
+    flat[9::4099] = -float("inf")
+    q, k, w = q.to(dev), k.to(dev), w.to(dev)
+    ops = torch.ops.cinnamon_amd
+    q8, qs, k8, ks = ops.indexer_quantize(q, k)
+    want = ops.indexer_scores_fp8(q8, qs, k8, ks, w, 0.125)
+    k8b, ksb = ops.indexer_quantize_k(k, H)
+    assert torch.equal(k8b.view(torch.uint8), k8.view(torch.uint8)) and torch.equal(ksb, ks)
+    for save in (True, False):
+        got, q8b, qsb = ops.indexer_scores_fp8_q(q, k8b, ksb, w, 0.125, save)
+        assert torch.equal(got.view(torch.int32), want.view(torch.int32))  # NaN scores too
+        if save:
+            assert torch.equal(q8b.view(torch.uint8), q8.view(torch.uint8)) and torch.equal(qsb, qs)
+        else:
+            assert q8b.numel() == 0 and qsb.numel() == 0
+
+
 def test_zero_rows_and_negative_weights(dev):
     q, k, w = _inputs(2, 100, 96, 4, 64, torch.bfloat16, seed=7)
     q[0, 3] = 0          # all heads of one query: zero row -> floor scale, zero scores

@@ -21,7 +21,8 @@ OPS = ["quant_rowwise", "quant_blockwise", "quant_blockwise_t", "quant_fwd", "qu
        "grouped_gemm_fp8", "quant_dual_grouped", "requant_row_to_block_grouped",
        "grouped_wgrad_fp8", "grouped_dgrad_fp8", "silu_mul_quant_rowwise", "swiglu_backward",
        "swiglu_dual_grouped", "moe_route", "moe_gather_quant_rowwise", "moe_scatter_quant_rowwise", "moe_gather_sum",
-       "moe_combine", "moe_combine_backward", "indexer_scores_fp8", "indexer_weights_grad_fp8", "indexer_quantize"]
+       "moe_combine", "moe_combine_backward", "indexer_scores_fp8", "indexer_weights_grad_fp8", "indexer_quantize",
+       "indexer_quantize_k", "indexer_scores_fp8_q"]
 F8, F32, BF16 = torch.float8_e4m3fn, torch.float32, torch.bfloat16
 
 
