@@ -807,9 +807,11 @@ def indexer_scores_fp8(q: torch.Tensor, k: torch.Tensor, weights: torch.Tensor,
     S = k.shape[1]
     w = weights.float().contiguous()
     if H <= (4 if d <= 128 else 2):
-        k8, ks = _indexer_quant_k_op(k.detach(), H)
         # the q codes are kept only for the weights' gradient
         save_q = torch.is_grad_enabled() and w.requires_grad
+        if _plain_eager(q, k, w):
+            return _IndexerScoresQ.apply(q.detach(), k.detach(), w, float(softmax_scale), save_q)
+        k8, ks = _indexer_quant_k_op(k.detach(), H)
         return _indexer_q_op(q.detach(), k8, ks, w, float(softmax_scale), save_q)[0]
     q8, qs, k8, ks = _indexer_quant_op(q.detach(), k.detach())
     return _indexer_op(q8, qs, k8, ks, w, float(softmax_scale))
@@ -845,9 +847,7 @@ def _(q, k):
             q.new_empty((B, S, d), dtype=torch.float8_e4m3fn), q.new_empty((B, S), dtype=torch.float32))
 
 
-@custom_op("indexer_quantize_k", "(Tensor k, int H) -> (Tensor, Tensor)")
-def _indexer_quant_k_op(k, H):
-    """k's side of indexer_quantize alone: (codes [B, S, d], first scales [B, S])."""
+def _launch_quant_k(k, H):
     B, S, d = k.shape
     k = _aligned16(k)
     k8 = torch.empty((B, S, d), dtype=torch.float8_e4m3fn, device=k.device)
@@ -856,6 +856,70 @@ def _indexer_quant_k_op(k, H):
     call("cin_indexer_quantize", ptr(k), dtype_code(k), ptr(k), dtype_code(k), B, 0, S, H, d, None, None,
          ptr(k8), ptr(ks), stream_of(k))
     return k8, ks
+
+
+def _launch_scores_q(q, k8, k_scale, weights, softmax_scale, save_q):
+    B, L, H, d = q.shape
+    S = k8.shape[1]
+    q = _aligned16(q)
+    kc = _codes_u8(k8).contiguous()
+    out = torch.empty((B, L, S), dtype=torch.float32, device=q.device)
+    q8 = torch.empty((B, L, H, d) if save_q else (0,), dtype=torch.float8_e4m3fn, device=q.device)
+    qs = torch.empty((B, L, H) if save_q else (0,), dtype=torch.float32, device=q.device)
+    call("cin_indexer_scores_fp8_q", ptr(q), dtype_code(q), ptr(kc), ptr(k_scale.contiguous()),
+         ptr(weights.contiguous()), B, L, S, H, d, softmax_scale, ptr(out), ptr(q8) if save_q else None,
+         ptr(qs) if save_q else None, stream_of(q))
+    return out, q8, qs
+
+
+def _launch_wgrad(q8, q_scale, k8, k_scale, grad_scores, softmax_scale):
+    B, L, H, d = q8.shape
+    S = k8.shape[1]
+    qc, kc = _codes_u8(q8).contiguous(), _codes_u8(k8).contiguous()
+    g = grad_scores.float().contiguous()
+    nws = max(1, _cdiv(S, 512) * B * L * H)  # one partial per 512-key range
+    ws = torch.empty(nws, dtype=torch.float32, device=q8.device)
+    dw = torch.empty((B, L, H), dtype=torch.float32, device=q8.device)
+    call("cin_indexer_weights_grad", ptr(qc), ptr(q_scale.contiguous()), ptr(kc), ptr(k_scale.contiguous()),
+         ptr(g), B, L, S, H, d, softmax_scale, ptr(ws), nws, ptr(dw), stream_of(qc))
+    return dw
+
+
+def _plain_eager(*tensors) -> bool:
+    """True outside tracing: no torch.compile, no dispatch mode (FakeTensor, make_fx,
+    functionalization), no functorch transform, and plain tensors.  Then the indexer runs
+    through _IndexerScoresQ, which calls the library directly; the operators below do the
+    same launches but go through torch's dispatcher (its per-call host cost exceeds these
+    kernels' device time at the indexer's shapes)."""
+    from torch.utils._python_dispatch import _get_current_dispatch_mode
+    return (not torch.compiler.is_compiling() and _get_current_dispatch_mode() is None
+            and not torch._C._are_functorch_transforms_active()
+            and all(type(t) is torch.Tensor for t in tensors))
+
+
+class _IndexerScoresQ(torch.autograd.Function):
+    """kernels.indexer_scores_fp8 in eager mode: the launches of indexer_quantize_k and
+    indexer_scores_fp8_q, and in backward indexer_weights_grad_fp8's, called directly."""
+
+    @staticmethod
+    def forward(ctx, q, k, w, softmax_scale, save_q):
+        k8, ks = _launch_quant_k(k, q.shape[2])
+        out, q8, qs = _launch_scores_q(q, k8, ks, w, softmax_scale, save_q)
+        if save_q:
+            ctx.save_for_backward(q8, qs, k8, ks)
+        ctx.softmax_scale = softmax_scale
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        q8, qs, k8, ks = ctx.saved_tensors
+        return None, None, _launch_wgrad(q8, qs, k8, ks, grad, ctx.softmax_scale), None, None
+
+
+@custom_op("indexer_quantize_k", "(Tensor k, int H) -> (Tensor, Tensor)")
+def _indexer_quant_k_op(k, H):
+    """k's side of indexer_quantize alone: (codes [B, S, d], first scales [B, S])."""
+    return _launch_quant_k(k, H)
 
 
 @_indexer_quant_k_op.register_fake
@@ -869,17 +933,7 @@ def _(k, H):
 def _indexer_q_op(q, k8, k_scale, weights, softmax_scale, save_q):
     """Scores from unquantized q (cin_indexer_scores_fp8_q): (scores [B, L, S], q codes
     [B, L, H, d], q first scales [B, L, H]), the last two empty unless save_q."""
-    B, L, H, d = q.shape
-    S = k8.shape[1]
-    q = _aligned16(q)
-    kc = _codes_u8(k8).contiguous()
-    out = torch.empty((B, L, S), dtype=torch.float32, device=q.device)
-    q8 = torch.empty((B, L, H, d) if save_q else (0,), dtype=torch.float8_e4m3fn, device=q.device)
-    qs = torch.empty((B, L, H) if save_q else (0,), dtype=torch.float32, device=q.device)
-    call("cin_indexer_scores_fp8_q", ptr(q), dtype_code(q), ptr(kc), ptr(k_scale.contiguous()),
-         ptr(weights.contiguous()), B, L, S, H, d, softmax_scale, ptr(out), ptr(q8) if save_q else None,
-         ptr(qs) if save_q else None, stream_of(q))
-    return out, q8, qs
+    return _launch_scores_q(q, k8, k_scale, weights, softmax_scale, save_q)
 
 
 @_indexer_q_op.register_fake
@@ -932,16 +986,7 @@ def _(q8, q_scale, k8, k_scale, weights, softmax_scale):
 @custom_op("indexer_weights_grad_fp8",
            "(Tensor q8, Tensor q_scale, Tensor k8, Tensor k_scale, Tensor grad_scores, float softmax_scale) -> Tensor")
 def _indexer_wgrad_op(q8, q_scale, k8, k_scale, grad_scores, softmax_scale):
-    B, L, H, d = q8.shape
-    S = k8.shape[1]
-    qc, kc = _codes_u8(q8).contiguous(), _codes_u8(k8).contiguous()
-    g = grad_scores.float().contiguous()
-    nws = max(1, _cdiv(S, 512) * B * L * H)  # one partial per 512-key range
-    ws = torch.empty(nws, dtype=torch.float32, device=q8.device)
-    dw = torch.empty((B, L, H), dtype=torch.float32, device=q8.device)
-    call("cin_indexer_weights_grad", ptr(qc), ptr(q_scale.contiguous()), ptr(kc), ptr(k_scale.contiguous()),
-         ptr(g), B, L, S, H, d, softmax_scale, ptr(ws), nws, ptr(dw), stream_of(qc))
-    return dw
+    return _launch_wgrad(q8, q_scale, k8, k_scale, grad_scores, softmax_scale)
 
 
 @_indexer_wgrad_op.register_fake
