@@ -112,6 +112,26 @@ __device__ inline void quant_vals(const float (&v)[NV], float s, float r, uint32
                        clamp448(y[4 * i + 3]));
 }
 
+// 1 / d for d >= 1 (the sigmoid's 1 / (1 + e^-x)), equal to the IEEE division 1.0f / d:
+// v_rcp_f32 followed by one Newton step r + r (1 - d r) in FMAs returns the correctly rounded
+// reciprocal for every fp32 d in [1, 2^126) (compared with the division on all 2^30 such
+// values on an MI355X).  Above 2^126 the reciprocal is a denormal, which v_rcp_f32 flushes:
+// those d, infinity and NaN take the division (a branch that sigmoid inputs above -87 never
+// enter).
+// recip_ge1_fast is the first form alone: callers that take it for d outside [1, 2^126)
+// must redo those values with the division (d >= 1 has bits >= 0x3f800000, and every d at or
+// above 2^126, infinity and NaN have bits >= kRecipFastLimitBits, so an unsigned max of the
+// bits tells whether any value needs it).
+constexpr uint32_t kRecipFastLimitBits = 0x7e800000u;  // 2^126
+__device__ inline float recip_ge1_fast(float d) {
+  const float r = __builtin_amdgcn_rcpf(d);
+  return __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
+}
+__device__ inline float recip_ge1(float d) {
+  if (__builtin_expect(__float_as_uint(d) < kRecipFastLimitBits, 1)) return recip_ge1_fast(d);
+  return 1.0f / d;
+}
+
 // e4m3fn code -> fp32 (exact).
 __device__ inline float e4m3_to_f32(uint32_t c) {
   uint32_t s = (c & 0x80u) << 24;

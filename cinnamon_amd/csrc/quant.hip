@@ -1238,7 +1238,7 @@ __device__ __forceinline__ void swiglu_dual_vals(const SwiRaw<IT>& r, RawIn<CIN_
     for (int j = 0; j < 8; ++j) {
       const float gv = in_val<CIN_DT_F32>(r.dh, i, j);
       const float a = in_val<IT>(r.a, i, j), b = in_val<IT>(r.b, i, j);
-      const float sig = 1.0f / (1.0f + expf(-a));
+      const float sig = recip_ge1(1.0f + expf(-a));
       const float t = sig * (1.0f + a * (1.0f - sig));
       d1.w[i][j] = __float_as_uint(gv * b * t);
       d2.w[i][j] = __float_as_uint(gv * (a * sig));
@@ -1656,7 +1656,7 @@ __global__ __launch_bounds__(kThreads) void k_swiglu_backward(
     float d1[4], d2[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float sig = 1.0f / (1.0f + expf(-a[k]));
+      const float sig = recip_ge1(1.0f + expf(-a[k]));
       const float t = sig * (1.0f + a[k] * (1.0f - sig));
       d1[k] = gv[k] * b[k] * t;
       d2[k] = gv[k] * (a[k] * sig);

@@ -226,6 +226,39 @@ def test_swiglu_backward_equals_elementwise_chain(kern, dev, dt):
     assert torch.equal(got, want), f"max abs diff {(got - want).abs().max().item()}"
 
 
+def test_swiglu_backward_every_bf16_h1(kern, dev):
+    """The sigmoid's 1 / (1 + e^-h1) is formed by v_rcp_f32 and one Newton step, and by the
+    division where 1 + e^-h1 >= 2^126 (h1 <= -87.3), is infinite or NaN.  Every bf16 bit
+    pattern as h1 (zeros, denormals, the values that take the division, +-inf, NaNs): the
+    standalone backward against torch's sigmoid chain, and the fused kernel's codes and scales
+    against the standalone backward followed by the grouped dual quantization."""
+    from cinnamon_amd import layers
+
+    g = torch.Generator().manual_seed(43)
+    M, H = 128, 512
+    h1 = (torch.arange(65536, dtype=torch.int32) - 32768).to(torch.int16).view(torch.bfloat16).view(M, H)
+    h2 = torch.randn(M, H, generator=g).to(torch.bfloat16)
+    h12 = torch.cat([h1, h2], dim=-1).to(dev)
+    dh = (torch.randn(M, H, generator=g) * 1e-3).to(dev)
+    got = layers.swiglu_backward(dh, h12)
+    a, b = h12.float().chunk(2, dim=-1)
+    sig = torch.sigmoid(a)
+    want = torch.cat([dh * b * (sig * (1.0 + a * (1.0 - sig))), dh * (a * sig)], dim=-1)
+    nan = torch.isnan(want)
+    assert torch.equal(torch.isnan(got), nan)
+    assert torch.equal(got[~nan], want[~nan]), f"{(got[~nan] != want[~nan]).sum().item()} values differ"
+    sd, ed = torch.tensor([0], device=dev), torch.tensor([M], device=dev)
+    fused = layers.swiglu_backward_dual_grouped(dh, h12, sd, ed, col_scales=True)
+    two = layers.quantize_fp8_dual_grouped(got, sd, ed, col_scales=True)
+    # (the transposed outputs are padded past the expert's 128 rows: compare those rows only)
+    for x, y, cols in zip(fused, two, (None, None, M, M // 128)):
+        x = x.view(torch.uint8) if x.dtype == torch.float8_e4m3fn else x.view(torch.int32)
+        y = y.view(torch.uint8) if y.dtype == torch.float8_e4m3fn else y.view(torch.int32)
+        if cols is not None:
+            x, y = x[:, :cols], y[:, :cols]
+        assert torch.equal(x, y)
+
+
 @pytest.mark.parametrize("counts,H", [(COUNTS[0], 384), ([0, 1, 257], 128), ([300, 260], 200),
                                      ([4000, 2000, 1000, 700, 300, 127, 64, 0, 9], 2048)])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
