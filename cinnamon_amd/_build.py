@@ -86,6 +86,25 @@ def build_bench_ceiling() -> str:
     return out
 
 
+def build_test_checks() -> list[str]:
+    """Compile the test suite's device checks (tests/gpu_checks/*.hip, test infrastructure
+    that exercises the library's device helpers) into lib<name>.so beside each source."""
+    root = os.path.dirname(HERE)
+    d = os.path.join(root, "tests", "gpu_checks")
+    outs = []
+    for f in sorted(os.listdir(d)):
+        if not f.endswith(".hip"):
+            continue
+        src, out = os.path.join(d, f), os.path.join(d, "lib" + f[:-4] + ".so")
+        cmd = [HIPCC, *COMMON, "-shared", src, "-o", out]
+        p = subprocess.run(cmd, capture_output=True, text=True)
+        if p.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{p.stdout}\n{p.stderr}")
+        outs.append(out)
+    return outs
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
     print(build_bench_ceiling())
+    print(build_test_checks())
