@@ -564,10 +564,41 @@ __global__ __launch_bounds__(kRT) void k_moe_combine_bwd_tokens(
     acc[j] = 0.0f;
   }
   const int64_t db = t * sdm;
+  // 16-bit rows whose 16-byte pieces are aligned: up to kRowBatch rows' pieces are loaded
+  // together before any is used (the per-row form has one row's load in flight per wave);
+  // the same products and sums in the same order either way
+  const bool vec = YT != CIN_DT_F32 && ((((uintptr_t)y) & 15) == 0) && (((sym * 2) & 15) == 0);
   for (int64_t c = (int64_t)lane * 8; c < N; c += 512) {
     float a[2][4];
     load4<CIN_DT_F32>(dout, db + c, N - c, a[0]);
     load4<CIN_DT_F32>(dout, db + c + 4, N - c - 4, a[1]);
+    if constexpr (YT != CIN_DT_F32) {
+      if (vec && c + 8 <= N) {
+#pragma unroll
+        for (int j0 = 0; j0 < kMaxTopK; j0 += kRowBatch) {
+          if (j0 < n) {
+            uint4 raw[kRowBatch][1];
+            load_rows<kRowBatch, 1>(y, c * 2, sym * 2, pos, j0, n, raw);
+#pragma unroll
+            for (int jj = 0; jj < kRowBatch; ++jj) {
+              const int j = j0 + jj;
+              if (j < n) {
+                for (int e = 0; e < 8; ++e) acc[j] += a[e >> 2][e & 3] * piece_elem<YT, 1>(raw[jj], e);
+                float d0[4], d1[4];
+                for (int e = 0; e < 4; ++e) {
+                  d0[e] = a[0][e] * w[j];
+                  d1[e] = a[1][e] * w[j];
+                }
+                const int64_t ob = (int64_t)pos[j] * sdym;
+                store4<DT>(dy, ob + c, N - c, d0);
+                store4<DT>(dy, ob + c + 4, N - c - 4, d1);
+              }
+            }
+          }
+        }
+        continue;
+      }
+    }
 #pragma unroll
     for (int j = 0; j < kMaxTopK; ++j) {
       if (j < n) {
