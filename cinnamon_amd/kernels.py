@@ -32,6 +32,7 @@ kernels.
 from __future__ import annotations
 
 import torch
+from torch.utils._python_dispatch import _get_current_dispatch_mode
 
 from . import _lib
 from ._lib import call, dtype_code, ptr, stream_of
@@ -61,13 +62,37 @@ __all__ = [
 ]
 
 
+# operator -> the launch function it was made from (see _run)
+_LAUNCH: dict = {}
+
+
 def custom_op(name: str, schema: str):
     """Register the decorated launch as the torch operator cinnamon_amd::<name> with an
     explicit schema; the caller attaches its shape function with ``register_fake``.  The
     operators allocate their outputs and never mutate their inputs."""
     def deco(fn):
-        return torch.library.custom_op(f"cinnamon_amd::{name}", fn, mutates_args=(), schema=schema)
+        op = torch.library.custom_op(f"cinnamon_amd::{name}", fn, mutates_args=(), schema=schema)
+        _LAUNCH[op] = fn
+        return op
     return deco
+
+
+def _plain_eager(*tensors) -> bool:
+    """True outside tracing: no torch.compile, no dispatch mode (FakeTensor, make_fx,
+    functionalization), no functorch transform, and plain tensors."""
+    return (not torch.compiler.is_compiling() and _get_current_dispatch_mode() is None
+            and not torch._C._are_functorch_transforms_active()
+            and all(type(t) is torch.Tensor for t in tensors))
+
+
+def _run(op, *args):
+    """op(*args); in plain eager mode its launch function is called directly instead: the
+    same kernels on the same arguments, without torch's dispatcher, whose host cost per call
+    exceeds the device time of a small launch.  Only for operators without an autograd
+    formula (these run inside the autograd Functions, or where no gradient is defined)."""
+    if _plain_eager(*(a for a in args if isinstance(a, torch.Tensor))):
+        return _LAUNCH[op](*args)
+    return op(*args)
 
 
 def _require(cond: bool, msg: str) -> None:
@@ -132,7 +157,7 @@ def quantize_fp8_rowwise(x: torch.Tensor, block_size: int = 128,
     reference's layout is row-major."""
     _require(x.is_cuda, "Input must be on CUDA")
     _require(x.ndim == 2, "Input must be 2D for now")
-    return _quant_rowwise_op(x, int(block_size), bool(round_scale), bool(col_scales))
+    return _run(_quant_rowwise_op, x, int(block_size), bool(round_scale), bool(col_scales))
 
 
 @custom_op("quant_rowwise", "(Tensor x, int block_size, bool round_scale, bool col_scales) -> (Tensor, Tensor)")
@@ -158,7 +183,7 @@ def quantize_fp8_blockwise(x: torch.Tensor, block_m: int = 128, block_n: int = 1
     """block_m x block_n e4m3 quantization -> (codes [M, N], scales [ceil(M/bm), ceil(N/bn)] fp32)."""
     _require(x.is_cuda, "Input must be on CUDA")
     _require(x.ndim == 2, "Input must be 2D")
-    return _quant_blockwise_op(x, int(block_m), int(block_n), bool(round_scale))
+    return _run(_quant_blockwise_op, x, int(block_m), int(block_n), bool(round_scale))
 
 
 @custom_op("quant_blockwise",
@@ -189,7 +214,7 @@ def quantize_fp8_blockwise_t(x: torch.Tensor, round_scale: bool = False,
     """
     _require(x.is_cuda, "Input must be on CUDA")
     _require(x.ndim == 2, "Input must be 2D")
-    q, qt, scales = _quant_blockwise_t_op(x, bool(round_scale), bool(with_rowmajor))
+    q, qt, scales = _run(_quant_blockwise_t_op, x, bool(round_scale), bool(with_rowmajor))
     return (q if with_rowmajor else None), qt, scales
 
 
@@ -232,7 +257,7 @@ def quantize_fp8_forward(x: torch.Tensor, weight: torch.Tensor, round_scale: boo
     _require(x.ndim == 2 and weight.ndim == 2, "Inputs must be 2D")
     _require(x.shape[1] == weight.shape[1], "x and weight must share K")
     _require(with_rowmajor or with_transposed, "at least one layout of the weight codes")
-    xq, xs, wq, wqt, ws = _quant_fwd_op(x, weight, bool(round_scale), bool(with_rowmajor),
+    xq, xs, wq, wqt, ws = _run(_quant_fwd_op, x, weight, bool(round_scale), bool(with_rowmajor),
                                         bool(with_transposed), bool(col_scales))
     return xq, xs, (wq if with_rowmajor else None), (wqt if with_transposed else None), ws
 
@@ -276,7 +301,7 @@ def quantize_fp8_dual(dy: torch.Tensor, round_scale: bool = False, col_scales: b
     """
     _require(dy.is_cuda, "Input must be on CUDA")
     _require(dy.ndim == 2, "Input must be 2D")
-    return _quant_dual_op(dy, bool(round_scale), bool(col_scales))
+    return _run(_quant_dual_op, dy, bool(round_scale), bool(col_scales))
 
 
 @custom_op("quant_dual", "(Tensor dy, bool round_scale, bool col_scales) -> (Tensor, Tensor, Tensor, Tensor)")
@@ -314,7 +339,7 @@ def requantize_rowwise_to_blockwise(x_fp8: torch.Tensor, x_scale: torch.Tensor,
     _require(x_fp8.dtype in (torch.float8_e4m3fn, torch.uint8),
              f"expected float8_e4m3fn codes, got {x_fp8.dtype}")
     _require(x_scale.shape == (M, _cdiv(K, 128)), "row scales must be [M, ceil(K/128)]")
-    return _requant_op(x_fp8, x_scale, bool(transposed))
+    return _run(_requant_op, x_fp8, x_scale, bool(transposed))
 
 
 @custom_op("requant_row_to_block", "(Tensor x_fp8, Tensor x_scale, bool transposed) -> (Tensor, Tensor)")
@@ -366,7 +391,7 @@ def quantize_fp8_backward(grad: torch.Tensor, x_fp8: torch.Tensor, x_scale: torc
     _require(x_fp8.dtype in (torch.float8_e4m3fn, torch.uint8),
              f"expected float8_e4m3fn codes, got {x_fp8.dtype}")
     _require(x_scale.shape == (M, _cdiv(K, 128)), "row scales must be [M, ceil(K/128)]")
-    return _quant_bwd_op(grad, x_fp8, x_scale, bool(round_scale), bool(col_scales))
+    return _run(_quant_bwd_op, grad, x_fp8, x_scale, bool(round_scale), bool(col_scales))
 
 
 @custom_op("quant_bwd", "(Tensor grad, Tensor x_fp8, Tensor x_scale, bool round_scale, bool col_scales) -> "
@@ -424,7 +449,7 @@ def dequantize_fp8_rowwise(x_fp8: torch.Tensor, scales: torch.Tensor,
         return x[:, :N] if pad > 0 else x
     _require(x_fp8.is_cuda, "Input must be on CUDA")
     _codes_u8(x_fp8)
-    return _dequant_rowwise_op(x_fp8, scales, int(block_size))
+    return _run(_dequant_rowwise_op, x_fp8, scales, int(block_size))
 
 
 @custom_op("dequant_rowwise", "(Tensor x_fp8, Tensor scales, int block_size) -> Tensor")
@@ -450,7 +475,7 @@ def dequantize_fp8(x_fp8: torch.Tensor, scales: torch.Tensor, block_m: int = 128
     _codes_u8(x_fp8)
     _require(scales.numel() >= _cdiv(M, block_m) * _cdiv(N, block_n),
              "scales too small for the block grid")
-    return _dequant_op(x_fp8, scales, int(block_m), int(block_n))
+    return _run(_dequant_op, x_fp8, scales, int(block_m), int(block_n))
 
 
 @custom_op("dequant", "(Tensor x_fp8, Tensor scales, int block_m, int block_n) -> Tensor")
@@ -504,7 +529,7 @@ def fp8_gemm_bs(a: torch.Tensor, a_scales: torch.Tensor, b_t: torch.Tensor,
              "b_scales too small")
     if out is None:
         _require(out_dtype in (torch.bfloat16, torch.float32), "out_dtype must be bf16 or fp32")
-        return _gemm_bs_op(a, a_scales, b_t, b_scales_nk, out_dtype)
+        return _run(_gemm_bs_op, a, a_scales, b_t, b_scales_nk, out_dtype)
     _require(out.dtype in (torch.bfloat16, torch.float32) and out.stride(1) == 1,
              "out must be bf16/fp32 with unit column stride")
     return _gemm_bs_into(a, a_scales, b_t, b_scales_nk, out)
@@ -546,7 +571,7 @@ def fp8_matmul_dsv3(a: torch.Tensor, b: torch.Tensor, a_scales: torch.Tensor,
     if bq.stride(0) == 1 and bq.stride(1) % 16 == 0 and bq.data_ptr() % 16 == 0 and K % 16 == 0:
         b_t = bq.t()
     else:
-        b_t = _transpose_u8_op(bq)
+        b_t = _run(_transpose_u8_op, bq)
     # b_scales is [kb, nb]; the GEMM reads it as [nb, kb] through swapped strides
     return fp8_gemm_bs(a, a_scales, b_t, b_scales.t(), torch.bfloat16)
 
@@ -761,7 +786,7 @@ def moe_grouped_gemm(sorted_x: torch.Tensor, weights: torch.Tensor, expert_start
     starts = expert_starts.to(device=a.device, dtype=torch.int64).contiguous()
     ends = expert_ends.to(device=a.device, dtype=torch.int64).contiguous()
     _require(starts.numel() == E and ends.numel() == E, "expert ranges must have n_experts entries")
-    return _grouped_f16_op(a, w, starts, ends)
+    return _run(_grouped_f16_op, a, w, starts, ends)
 
 
 @custom_op("grouped_gemm_f16", "(Tensor a, Tensor w, Tensor starts, Tensor ends) -> Tensor")
@@ -883,18 +908,6 @@ def _launch_wgrad(q8, q_scale, k8, k_scale, grad_scores, softmax_scale):
     call("cin_indexer_weights_grad", ptr(qc), ptr(q_scale.contiguous()), ptr(kc), ptr(k_scale.contiguous()),
          ptr(g), B, L, S, H, d, softmax_scale, ptr(ws), nws, ptr(dw), stream_of(qc))
     return dw
-
-
-def _plain_eager(*tensors) -> bool:
-    """True outside tracing: no torch.compile, no dispatch mode (FakeTensor, make_fx,
-    functionalization), no functorch transform, and plain tensors.  Then the indexer runs
-    through _IndexerScoresQ, which calls the library directly; the operators below do the
-    same launches but go through torch's dispatcher (its per-call host cost exceeds these
-    kernels' device time at the indexer's shapes)."""
-    from torch.utils._python_dispatch import _get_current_dispatch_mode
-    return (not torch.compiler.is_compiling() and _get_current_dispatch_mode() is None
-            and not torch._C._are_functorch_transforms_active()
-            and all(type(t) is torch.Tensor for t in tensors))
 
 
 class _IndexerScoresQ(torch.autograd.Function):
