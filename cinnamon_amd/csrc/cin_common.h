@@ -114,10 +114,10 @@ __device__ inline void quant_vals(const float (&v)[NV], float s, float r, uint32
 
 // 1 / d for d >= 1 (the sigmoid's 1 / (1 + e^-x)), equal to the IEEE division 1.0f / d:
 // v_rcp_f32 followed by one Newton step r + r (1 - d r) in FMAs returns the correctly rounded
-// reciprocal for every fp32 d in [1, 2^126) (compared with the division on all 2^30 such
-// values on an MI355X).  Above 2^126 the reciprocal is a denormal, which v_rcp_f32 flushes:
-// those d, infinity and NaN take the division (a branch that sigmoid inputs above -87 never
-// enter).
+// reciprocal for every fp32 d in [1, 2^126).  Above 2^126 the reciprocal is a denormal, which
+// v_rcp_f32 flushes: those d, infinity and NaN take the division (a branch that sigmoid inputs
+// above -87 never enter).  tests/test_gpu_recip.py compares recip_ge1 with the division on
+// the device for every fp32 d >= 1.
 // recip_ge1_fast is the first form alone: callers that take it for d outside [1, 2^126)
 // must redo those values with the division (d >= 1 has bits >= 0x3f800000, and every d at or
 // above 2^126, infinity and NaN have bits >= kRecipFastLimitBits, so an unsigned max of the
