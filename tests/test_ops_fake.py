@@ -224,3 +224,20 @@ def test_moe_dispatch_shape_functions_and_trace():
     for name in ["moe_route", "moe_scatter_quant_rowwise", "moe_combine", "moe_combine_backward",
                  "moe_gather_sum", "grouped_gemm_fp8", "grouped_wgrad_fp8"]:
         assert any(f"cinnamon_amd.{name}" in o for o in ops), (name, ops)
+
+
+def test_eager_calls_bypass_the_dispatcher_only_outside_tracing():
+    """kernels._run calls an operator's launch function directly only for plain tensors
+    outside tracing; FakeTensorMode, make_fx and torch.compile keep the operators (their shape
+    functions and schemas are what tracing needs)."""
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    t = torch.zeros(4)
+    assert kernels._plain_eager(t, t)
+    with FakeTensorMode():
+        assert not kernels._plain_eager(torch.empty(4))
+    seen = []
+    make_fx(lambda x: seen.append(kernels._plain_eager(x)) or x + 1)(t)
+    assert seen == [False]
+    assert all(op in kernels._LAUNCH for op in (kernels._quant_fwd_op, kernels._gemm_bs_op,
+                                                 kernels._quant_bwd_op, kernels._quant_rowwise_op))
