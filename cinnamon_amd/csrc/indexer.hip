@@ -97,18 +97,19 @@ struct KeyStage {
   v4f kpre;
 
   __device__ void load(const uint8_t* k8, const float* ks, int64_t b, int64_t S, int64_t s_sub,
-                       int64_t s_end, int vec) {
+                       int64_t s_end, int vec, int tid = -1) {
+    if (tid < 0) tid = threadIdx.x;  // tid: this thread's index among the 256 that share the stage
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
-      const int idx = threadIdx.x + u * kThreads;
+      const int idx = tid + u * kThreads;
       const int row = idx / CH, c = idx - row * CH;
       const int64_t s = s_sub + row;
       pre[u] = uint4{0u, 0u, 0u, 0u};
       if (idx < kKT * CH && s < s_end) pre[u] = *reinterpret_cast<const uint4*>(k8 + (b * S + s) * D + 16 * c);
     }
     kpre = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    if (threadIdx.x < kKT / 4) {
-      const int64_t s0 = s_sub + 4 * threadIdx.x;
+    if (tid < kKT / 4) {
+      const int64_t s0 = s_sub + 4 * tid;
       if (vec && s0 + 4 <= s_end) {
         kpre = *reinterpret_cast<const v4f*>(ks + b * S + s0);
       } else {
@@ -117,14 +118,15 @@ struct KeyStage {
       }
     }
   }
-  __device__ void store(uint8_t* kl, float* ksl) const {
+  __device__ void store(uint8_t* kl, float* ksl, int tid = -1) const {
+    if (tid < 0) tid = threadIdx.x;
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
-      const int idx = threadIdx.x + u * kThreads;
+      const int idx = tid + u * kThreads;
       const int row = idx / CH, c = idx - row * CH;
       if (idx < kKT * CH) *reinterpret_cast<uint4*>(&kl[row * RS + 16 * c]) = pre[u];
     }
-    if (threadIdx.x < kKT / 4) *reinterpret_cast<v4f*>(&ksl[4 * threadIdx.x]) = kpre;
+    if (tid < kKT / 4) *reinterpret_cast<v4f*>(&ksl[4 * tid]) = kpre;
   }
 };
 
@@ -408,6 +410,171 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWa
   }
 }
 
+// The fused form with 8 waves per workgroup (d <= 128, H <= 4, more than 512 keys): a
+// workgroup owns 64 tokens x 1024 keys.  Waves 4h .. 4h+3 (half h) take keys
+// [512 h, 512 h + 512) of the range, each half with its own key stages, and wave 4h + w the
+// same 16 tokens in both halves.  Half h quantizes heads 2h and 2h + 1 of its tokens and the
+// halves trade fragments and head weights through LDS, so each token's q is read and
+// quantized once per 1024 keys instead of once per 512.  Every wave runs the loop nsub times
+// (half 0's count, the larger) and meets every barrier; a half past its last sub-tile only
+// waits at them.
+constexpr int kPairThreads = 512;
+constexpr int64_t kKPW2 = 2 * kKPW;
+
+template <int D, int QDT>
+__global__ __launch_bounds__(kPairThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_indexer_scores_fp8_pair(
+    const void* __restrict__ qin, const uint8_t* __restrict__ k8, const float* __restrict__ ks,
+    const float* __restrict__ w, int64_t L, int64_t S, int64_t H, float softmax_scale,
+    float* __restrict__ out, int64_t tiles_t, int64_t tiles_s, int xcd_rotate, int vec,
+    uint8_t* __restrict__ q8_out, float* __restrict__ qs_out) {
+  static_assert(D <= 128, "one 128-byte slice per head row");
+  constexpr int HG = 4;
+  constexpr int RS = KeyStage<D>::RS;
+  constexpr int OS = kKT + 4;
+  constexpr int ES = RawSlice<QDT>::ES;
+  __shared__ __attribute__((aligned(16))) uint8_t kl[2][2][kKT * RS];
+  __shared__ __attribute__((aligned(16))) float ksl[2][2][kKT];
+  __shared__ __attribute__((aligned(16))) float ost[8 * 16 * OS];
+
+  int64_t tile = blockIdx.x;
+  if (xcd_rotate) {
+    const int64_t per = gridDim.x >> 3;
+    tile = (tile & 7) * per + (tile >> 3);
+  }
+  const int64_t b = tile / (tiles_t * tiles_s);
+  const int64_t rem = tile - b * tiles_t * tiles_s;
+  const int64_t tt = rem / tiles_s, sw = rem - tt * tiles_s;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int half = wave >> 2, wq = wave & 3;
+  const int l16 = lane & 15, kq = lane >> 4;
+  const int tid = threadIdx.x & 255;  // index within the half (its key stage's 256 threads)
+  const int64_t r_begin = sw * kKPW2, r_end = r_begin + kKPW2 < S ? r_begin + kKPW2 : S;
+  const int64_t h_begin = r_begin + half * kKPW;
+  const int64_t h_end = h_begin + kKPW < r_end ? h_begin + kKPW : r_end;
+  const int nsub_h = h_end > h_begin ? (int)((h_end - h_begin + kKT - 1) / kKT) : 0;
+  const int64_t e0 = r_begin + kKPW < r_end ? r_begin + kKPW : r_end;
+  const int nsub = (int)((e0 - r_begin + kKT - 1) / kKT);  // half 0's, the same in every wave
+
+  const int64_t tok = tt * kTT + wq * 16 + l16;
+  const bool tok_ok = tok < L;
+  const int64_t orow = (b * L + (tok_ok ? tok : 0)) * H;
+  KeyStage<D> stage;
+  stage.load(k8, ks, b, S, h_begin, h_end, vec, tid);  // (keys past h_end read as zero)
+
+  // this half's two heads: raw rows, codes, scales, head weights
+  const uint8_t* qrow = static_cast<const uint8_t*>(qin) + orow * D * ES;
+  RawSlice<QDT> raw[2];
+  float wv[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int g = 2 * half + j;
+    const bool ok = tok_ok && g < H;
+    load_slice<D, QDT>(qrow + (int64_t)g * D * ES, ok, kq, 0, raw[j]);
+    wv[j] = ok ? w[orow + g] : 0.0f;
+  }
+  v8i own[2];
+  float own_w[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int g = 2 * half + j;
+    const bool ok = tok_ok && g < H;
+    float sc;
+    own[j] = quant_slice<QDT>(raw[j], sc);
+    own_w[j] = ok ? (sc * wv[j]) * softmax_scale : 0.0f;
+    if (q8_out != nullptr && ok && g % tiles_s == sw) {
+      const int off = 32 * kq;
+      if (off < D) {
+        uint8_t* dst = q8_out + (orow + g) * D + off;
+        const v8i f = own[j];
+        *reinterpret_cast<uint4*>(dst) = uint4{(uint32_t)f[0], (uint32_t)f[1], (uint32_t)f[2], (uint32_t)f[3]};
+        *reinterpret_cast<uint4*>(dst + 16) = uint4{(uint32_t)f[4], (uint32_t)f[5], (uint32_t)f[6], (uint32_t)f[7]};
+      }
+      if (kq == 0) qs_out[orow + g] = sc;
+    }
+  }
+  // trade through the (not yet used) staging area: [wave in half][head][lane][8 codes + weight]
+  uint32_t* xch = reinterpret_cast<uint32_t*>(ost);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    uint32_t* p = xch + ((wq * HG + 2 * half + j) * 64 + lane) * 9;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) p[e] = (uint32_t)own[j][e];
+    p[8] = __float_as_uint(own_w[j]);
+  }
+  __syncthreads();
+  v8i oth[2];
+  float oth_w[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t* p = xch + ((wq * HG + 2 * (1 - half) + j) * 64 + lane) * 9;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) oth[j][e] = (int)p[e];
+    oth_w[j] = __uint_as_float(p[8]);
+  }
+  v8i qf[HG];
+  float wr[HG];
+  qf[0] = half == 0 ? own[0] : oth[0];
+  qf[1] = half == 0 ? own[1] : oth[1];
+  qf[2] = half == 0 ? oth[0] : own[0];
+  qf[3] = half == 0 ? oth[1] : own[1];
+  wr[0] = half == 0 ? own_w[0] : oth_w[0];
+  wr[1] = half == 0 ? own_w[1] : oth_w[1];
+  wr[2] = half == 0 ? oth_w[0] : own_w[0];
+  wr[3] = half == 0 ? oth_w[1] : own_w[1];
+  stage.store(kl[half][0], ksl[half][0], tid);
+  __syncthreads();  // the trade's reads are done before any wave stages scores over it
+
+  float* my = ost + wave * 16 * OS;
+  for (int i = 0; i < nsub; ++i) {
+    const int buf = i & 1;
+    if (i + 1 < nsub_h) stage.load(k8, ks, b, S, h_begin + (int64_t)(i + 1) * kKT, h_end, vec, tid);
+    if (i < nsub_h) {
+#pragma unroll 2
+      for (int j = 0; j < 8; ++j) {
+        const uint8_t* kr = &kl[half][buf][(16 * j + l16) * RS];
+        const v8i kf = frag32<D>(kr, true, kq, 0);
+        v4f p[HG];
+#pragma unroll
+        for (int g = 0; g < HG; ++g)
+          p[g] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(kf, qf[g], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0,
+                                                                  0, 0, 0);
+        asm volatile("" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3]));
+        v4f a = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int g = 0; g < HG; ++g) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) a[r] = __builtin_fmaf(relu1(p[g][r]), wr[g], a[r]);
+        }
+        const v4f kv = *reinterpret_cast<const v4f*>(&ksl[half][buf][16 * j + 4 * kq]);
+        a = v4f{a[0] * kv[0], a[1] * kv[1], a[2] * kv[2], a[3] * kv[3]};
+        *reinterpret_cast<v4f*>(&my[l16 * OS + 16 * j + 4 * kq]) = a;
+      }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int row = 2 * it + (lane >> 5), c4 = lane & 31;
+        const int64_t t = tt * kTT + wq * 16 + row;
+        const int64_t s0 = h_begin + (int64_t)i * kKT + 4 * c4;
+        const v4f v = *reinterpret_cast<const v4f*>(&my[row * OS + 4 * c4]);
+        if (t < L) {
+          float* o = out + (b * L + t) * S + s0;
+          if (vec && s0 + 4 <= h_end) {
+            __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(o));
+          } else {
+            for (int r = 0; r < 4; ++r)
+              if (s0 + r < h_end) o[r] = v[r];
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (i + 1 < nsub) {
+      if (i + 1 < nsub_h) stage.store(kl[half][buf ^ 1], ksl[half][buf ^ 1], tid);
+      __syncthreads();
+    }
+  }
+}
+
 // Gradient of the scores with respect to the head weights (the reference's autograd through
 // src/attention.py:298-300; q and k come from the non-differentiable quantizer):
 //   G[b, t, h] = sum_s relu(logit[b, t, h, s]) * (dscores[b, t, s] * k_scale[b, s])
@@ -578,6 +745,23 @@ void launch_indexer_q(int q_dtype, unsigned grid, hipStream_t st, const void* q,
 #undef CIN_IQ_LAUNCH
 }
 
+template <int D>
+void launch_indexer_pair(int q_dtype, unsigned grid, hipStream_t st, const void* q, const uint8_t* k8,
+                         const float* ks, const float* w, int64_t L, int64_t S, int64_t H,
+                         float softmax_scale, float* out, int64_t tiles_t, int64_t tiles_s,
+                         int xcd_rotate, int vec, uint8_t* q8_out, float* qs_out) {
+#define CIN_IQP_LAUNCH(DT)                                                                              \
+  hipLaunchKernelGGL((k_indexer_scores_fp8_pair<D, DT>), grid, kPairThreads, 0, st, q, k8, ks, w, L, S, H, \
+                     softmax_scale, out, tiles_t, tiles_s, xcd_rotate, vec, q8_out, qs_out)
+  if (q_dtype == CIN_DT_BF16)
+    CIN_IQP_LAUNCH(CIN_DT_BF16);
+  else if (q_dtype == CIN_DT_F16)
+    CIN_IQP_LAUNCH(CIN_DT_F16);
+  else
+    CIN_IQP_LAUNCH(CIN_DT_F32);
+#undef CIN_IQP_LAUNCH
+}
+
 template <int D, int HG>
 void launch_wgrad(unsigned grid, hipStream_t st, const uint8_t* q8, const uint8_t* k8,
                   const float* ks, const float* gs, int64_t B, int64_t L, int64_t S, int64_t H,
@@ -648,12 +832,29 @@ int cin_indexer_scores_fp8_q(const void* q, int q_dtype, const uint8_t* k8, cons
   }
   CIN_CHECK_ARG(k8 && k_scale && weights && scores, "indexer_scores_fp8_q: null pointer");
   CIN_CHECK_ARG((((uintptr_t)k8) & 15) == 0, "indexer_scores_fp8_q: k8 must be 16-byte aligned");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const int vec = S % 4 == 0 && (((uintptr_t)k_scale) & 15) == 0 && (((uintptr_t)scores) & 15) == 0;
+  if (d <= 128 && S > kKPW) {
+    // 8 waves per 64 tokens x 1024 keys: q read and quantized once per 1024 keys
+    const int64_t tiles_t2 = cdiv(L, kTT), tiles_s2 = cdiv(S, kKPW2);
+    CIN_CHECK_ARG(B * tiles_t2 * tiles_s2 < ((int64_t)1 << 31), "indexer_scores_fp8_q: grid too large");
+    const unsigned grid2 = (unsigned)(B * tiles_t2 * tiles_s2);
+    const int xr2 = grid2 % 8 == 0;
+    switch (d / 32) {
+#define CIN_INDEXER_P_CASE(n)                                                                      \
+  case n:                                                                                          \
+    launch_indexer_pair<32 * n>(q_dtype, grid2, st, q, k8, k_scale, weights, L, S, H, softmax_scale, \
+                                scores, tiles_t2, tiles_s2, xr2, vec, q8, q_scale);                \
+    break;
+      CIN_INDEXER_P_CASE(1) CIN_INDEXER_P_CASE(2) CIN_INDEXER_P_CASE(3) CIN_INDEXER_P_CASE(4)
+#undef CIN_INDEXER_P_CASE
+    }
+    return cin_check_launch("indexer_scores_fp8_q");
+  }
   const int64_t tiles_t = cdiv(L, kTT), tiles_s = cdiv(S, kKPW);
   CIN_CHECK_ARG(B * tiles_t * tiles_s < ((int64_t)1 << 31), "indexer_scores_fp8_q: grid too large");
   const unsigned grid = (unsigned)(B * tiles_t * tiles_s);
   const int xcd_rotate = grid % 8 == 0;
-  const int vec = S % 4 == 0 && (((uintptr_t)k_scale) & 15) == 0 && (((uintptr_t)scores) & 15) == 0;
-  const hipStream_t st = static_cast<hipStream_t>(stream);
   switch (d / 32) {
 #define CIN_INDEXER_Q_CASE(n, hgv)                                                                  \
   case n:                                                                                           \

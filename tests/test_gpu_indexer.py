@@ -60,6 +60,12 @@ def test_scores_match_the_oracle(dev, B, L, S, H, d, dtype):
     (2, 65, 1030, 2, 160, torch.float32),      # three key ranges, the second tile 32 wide
     (1, 64, 5, 1, 32, torch.float16),          # S % 4 != 0: the scalar score stores
     (1, 33, 0, 2, 64, torch.bfloat16),         # no keys: only the codes are written
+    # the 8-wave form (d <= 128, S > 512): a second half with 1 key, an empty second half in
+    # the last 1024-key range, three ranges, one head
+    (3, 100, 600, 4, 128, torch.bfloat16),
+    (1, 200, 1500, 4, 64, torch.float16),
+    (1, 77, 2049, 2, 32, torch.bfloat16),
+    (2, 64, 1088, 1, 128, torch.float32),
 ])
 def test_fused_q_quantization_equals_the_two_calls(dev, B, L, S, H, d, dtype):
     """cin_indexer_scores_fp8_q quantizes q inside the scoring kernel with the row-wise
