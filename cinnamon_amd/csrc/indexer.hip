@@ -708,6 +708,161 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWa
   }
 }
 
+// The weights gradient with 8 waves per 64 tokens x 1024 keys (d <= 128, H <= 4, more than
+// 512 keys), the scoring kernel's pair tiling: half h sums over keys [512 h, 512 h + 512) of
+// the range exactly as k_indexer_wgrad_fp8 sums over one 512-key range, so its per-range
+// partial sum is the same.  With one 1024-key range (S <= 1024) the workgroup finishes in
+// place: dweights = (((0 + half 0's sum) + half 1's sum) * softmax_scale) * q_scale, the
+// finish kernel's arithmetic; with more it writes the two partial sums for that kernel.
+// Every wave runs half 0's loop count and meets every barrier.
+template <int D>
+__global__ __launch_bounds__(kPairThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_indexer_wgrad_fp8_pair(
+    const uint8_t* __restrict__ q8, const float* __restrict__ qs, const uint8_t* __restrict__ k8,
+    const float* __restrict__ ks, const float* __restrict__ gs, int64_t B, int64_t L, int64_t S,
+    int64_t H, float softmax_scale, float* __restrict__ partial, float* __restrict__ dw,
+    int64_t tiles_t, int64_t tiles_s, int xcd_rotate, int vec) {
+  static_assert(D <= 128, "one 128-byte slice per head row");
+  constexpr int HG = 4;
+  constexpr int RS = KeyStage<D>::RS;
+  constexpr int OS = kKT + 4;
+  __shared__ __attribute__((aligned(16))) uint8_t kl[2][2][kKT * RS];
+  __shared__ __attribute__((aligned(16))) float ksl[2][2][kKT];
+  __shared__ __attribute__((aligned(16))) float gst[8 * 16 * OS];
+
+  int64_t tile = blockIdx.x;
+  if (xcd_rotate) {
+    const int64_t per = gridDim.x >> 3;
+    tile = (tile & 7) * per + (tile >> 3);
+  }
+  const int64_t b = tile / (tiles_t * tiles_s);
+  const int64_t rem = tile - b * tiles_t * tiles_s;
+  const int64_t tt = rem / tiles_s, sw = rem - tt * tiles_s;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int half = wave >> 2, wq = wave & 3;
+  const int l16 = lane & 15, kq = lane >> 4;
+  const int tid = threadIdx.x & 255;
+  const int64_t r_begin = sw * kKPW2, r_end = r_begin + kKPW2 < S ? r_begin + kKPW2 : S;
+  const int64_t h_begin = r_begin + half * kKPW;
+  const int64_t h_end = h_begin + kKPW < r_end ? h_begin + kKPW : r_end;
+  const int nsub_h = h_end > h_begin ? (int)((h_end - h_begin + kKT - 1) / kKT) : 0;
+  const int64_t e0 = r_begin + kKPW < r_end ? r_begin + kKPW : r_end;
+  const int nsub = (int)((e0 - r_begin + kKT - 1) / kKT);  // half 0's, the same in every wave
+
+  const int64_t tok = tt * kTT + wq * 16 + l16;
+  const bool tok_ok = tok < L;
+  const uint8_t* qrow = q8 + (b * L + (tok_ok ? tok : 0)) * H * D;
+  float* my = gst + wave * 16 * OS;
+  KeyStage<D> stage;
+
+  v4f gpre[8];
+  auto load_g = [&](int64_t s_sub) {
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int row = 2 * it + (lane >> 5), c4 = lane & 31;
+      const int64_t t = tt * kTT + wq * 16 + row;
+      const int64_t s0 = s_sub + 4 * c4;
+      gpre[it] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      if (t < L) {
+        const float* g = gs + (b * L + t) * S + s0;
+        if (vec && s0 + 4 <= h_end) {
+          gpre[it] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(g));
+        } else {
+          for (int r = 0; r < 4; ++r)
+            if (s0 + r < h_end) gpre[it][r] = g[r];
+        }
+      }
+    }
+  };
+  auto store_g = [&]() {
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int row = 2 * it + (lane >> 5), c4 = lane & 31;
+      *reinterpret_cast<v4f*>(&my[row * OS + 4 * c4]) = gpre[it];
+    }
+  };
+
+  v8i qf[HG];
+#pragma unroll
+  for (int g = 0; g < HG; ++g) qf[g] = frag32<D>(qrow + g * D, tok_ok && g < H, kq, 0);
+  float acc[HG];
+#pragma unroll
+  for (int g = 0; g < HG; ++g) acc[g] = 0.0f;
+  stage.load(k8, ks, b, S, h_begin, h_end, vec, tid);  // (keys past h_end read as zero)
+  load_g(h_begin);
+  stage.store(kl[half][0], ksl[half][0], tid);
+  store_g();
+  __syncthreads();
+  for (int i = 0; i < nsub; ++i) {
+    const int buf = i & 1;
+    const bool more = i + 1 < nsub_h;
+    if (more) {
+      stage.load(k8, ks, b, S, h_begin + (int64_t)(i + 1) * kKT, h_end, vec, tid);
+      load_g(h_begin + (int64_t)(i + 1) * kKT);
+    }
+    if (i < nsub_h) {
+#pragma unroll 2
+      for (int j = 0; j < 8; ++j) {
+        const uint8_t* kr = &kl[half][buf][(16 * j + l16) * RS];
+        const v8i kf = frag32<D>(kr, true, kq, 0);
+        const v4f gv = *reinterpret_cast<const v4f*>(&my[l16 * OS + 16 * j + 4 * kq]);
+        const v4f kv = *reinterpret_cast<const v4f*>(&ksl[half][buf][16 * j + 4 * kq]);
+        const v4f dx = v4f{gv[0] * kv[0], gv[1] * kv[1], gv[2] * kv[2], gv[3] * kv[3]};
+        v4f p[HG];
+#pragma unroll
+        for (int g = 0; g < HG; ++g)
+          p[g] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(kf, qf[g], v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0,
+                                                                  0, 0, 0);
+        asm volatile("" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3]));
+#pragma unroll
+        for (int g = 0; g < HG; ++g) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[g] = __builtin_fmaf(relu1(p[g][r]), dx[r], acc[g]);
+        }
+      }
+    }
+    if (i + 1 < nsub) {
+      if (more) {
+        // this wave's reads of its staging rows precede the overwrite (in-order LDS)
+        store_g();
+        stage.store(kl[half][buf ^ 1], ksl[half][buf ^ 1], tid);
+      }
+      __syncthreads();
+    }
+  }
+  // lanes l16, l16 + 16, l16 + 32, l16 + 48 hold the same token: add them
+#pragma unroll
+  for (int g = 0; g < HG; ++g) {
+    acc[g] += __shfl_xor(acc[g], 16);
+    acc[g] += __shfl_xor(acc[g], 32);
+  }
+  if (tiles_s == 1) {
+    // half 1's sums to LDS (over its staging rows, read by now: the barrier below orders
+    // every wave's last staging reads before half 1 writes), half 0 finishes
+    __syncthreads();
+    float* xs = gst;  // [wave in half][lane][head]
+    if (half == 1) {
+#pragma unroll
+      for (int g = 0; g < HG; ++g) xs[(wq * 64 + lane) * HG + g] = acc[g];
+    }
+    __syncthreads();
+    if (half == 0 && kq == 0 && tok_ok) {
+      const int64_t o = (b * L + tok) * H;
+#pragma unroll
+      for (int g = 0; g < HG; ++g) {
+        if (g < H) {
+          const float tot = (0.0f + acc[g]) + xs[(wq * 64 + lane) * HG + g];
+          dw[o + g] = (tot * softmax_scale) * qs[o + g];
+        }
+      }
+    }
+  } else if (kq == 0 && tok_ok && nsub_h > 0) {
+    const int64_t r = 2 * sw + half;  // 512-key range index
+#pragma unroll
+    for (int g = 0; g < HG; ++g)
+      if (g < H) partial[((r * B + b) * L + tok) * H + g] = acc[g];
+  }
+}
+
 // dweights[i] = ((sum over key ranges, increasing) * softmax_scale) * q_scale[i], i over B L H.
 __global__ void k_indexer_wgrad_finish(const float* __restrict__ partial, const float* __restrict__ qs,
                                        int64_t n, int64_t ranges, float softmax_scale,
@@ -889,6 +1044,31 @@ int cin_indexer_weights_grad(const uint8_t* q8, const float* q_scale, const uint
   CIN_CHECK_ARG(B * tiles_t * tiles_s < ((int64_t)1 << 31) && B * L * H < ((int64_t)1 << 38),
                 "indexer_weights_grad: grid too large");  // finish grid: B L H / 256 < 2^30
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (S > kKPW && d <= 128 && H <= 4) {
+    // 8 waves per 64 tokens x 1024 keys; with one such range (S <= 1024) no finishing pass
+    CIN_CHECK_ARG(q8 && k8 && k_scale && grad_scores && workspace, "indexer_weights_grad: null pointer");
+    CIN_CHECK_ARG((((uintptr_t)q8) & 15) == 0 && (((uintptr_t)k8) & 15) == 0,
+                  "indexer_weights_grad: code buffers must be 16-byte aligned");
+    const int64_t tiles_s2 = cdiv(S, kKPW2);
+    const unsigned grid2 = (unsigned)(B * tiles_t * tiles_s2);
+    const int xr2 = grid2 % 8 == 0;
+    const int vec = S % 4 == 0 && (((uintptr_t)k_scale) & 15) == 0 && (((uintptr_t)grad_scores) & 15) == 0;
+    switch (d / 32) {
+#define CIN_WGRAD_P_CASE(n)                                                                         \
+  case n:                                                                                           \
+    hipLaunchKernelGGL((k_indexer_wgrad_fp8_pair<32 * n>), grid2, kPairThreads, 0, st, q8, q_scale, k8, \
+                       k_scale, grad_scores, B, L, S, H, softmax_scale, workspace, grad_weights,     \
+                       tiles_t, tiles_s2, xr2, vec);                                                 \
+    break;
+      CIN_WGRAD_P_CASE(1) CIN_WGRAD_P_CASE(2) CIN_WGRAD_P_CASE(3) CIN_WGRAD_P_CASE(4)
+#undef CIN_WGRAD_P_CASE
+    }
+    if (tiles_s2 == 1) return cin_check_launch("indexer_weights_grad");
+    const int64_t n = B * L * H;
+    hipLaunchKernelGGL(k_indexer_wgrad_finish, (unsigned)cdiv(n, 256), 256, 0, st, workspace, q_scale, n,
+                       tiles_s, softmax_scale, grad_weights);
+    return cin_check_launch("indexer_weights_grad");
+  }
   if (S > 0) {
     CIN_CHECK_ARG(q8 && k8 && k_scale && grad_scores && workspace, "indexer_weights_grad: null pointer");
     CIN_CHECK_ARG((((uintptr_t)q8) & 15) == 0 && (((uintptr_t)k8) & 15) == 0,

@@ -106,7 +106,10 @@ def test_zero_rows_and_negative_weights(dev):
 
 
 @pytest.mark.parametrize("B,L,S,H,d", [(2, 1024, 1024, 4, 128), (1, 77, 700, 3, 192), (2, 65, 63, 8, 64),
-                                       (1, 130, 1100, 5, 256)])
+                                       (1, 130, 1100, 5, 256),
+                                       # the 8-wave form: finished in place (S <= 1024), and
+                                       # per-range sums with a one-key last range
+                                       (2, 70, 600, 3, 96), (1, 77, 2049, 2, 32)])
 def test_weights_gradient_matches_the_reference_autograd(dev, B, L, S, H, d):
     """The reference's autograd through its FP8 branch reaches `weights` only (the codes come
     from the quantizer); the oracle's restatement run under CPU autograd is the reference.
