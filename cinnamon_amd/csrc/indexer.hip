@@ -421,17 +421,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMinWa
 constexpr int kPairThreads = 512;
 constexpr int64_t kKPW2 = 2 * kKPW;
 
+// QDT < 0: q arrives as codes with first scales qs (cin_indexer_scores_fp8); each half loads
+// all four heads' fragments and nothing is traded.
 template <int D, int QDT>
 __global__ __launch_bounds__(kPairThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) void k_indexer_scores_fp8_pair(
     const void* __restrict__ qin, const uint8_t* __restrict__ k8, const float* __restrict__ ks,
     const float* __restrict__ w, int64_t L, int64_t S, int64_t H, float softmax_scale,
     float* __restrict__ out, int64_t tiles_t, int64_t tiles_s, int xcd_rotate, int vec,
-    uint8_t* __restrict__ q8_out, float* __restrict__ qs_out) {
+    uint8_t* __restrict__ q8_out, float* __restrict__ qs_out, const float* __restrict__ qs = nullptr) {
   static_assert(D <= 128, "one 128-byte slice per head row");
   constexpr int HG = 4;
   constexpr int RS = KeyStage<D>::RS;
   constexpr int OS = kKT + 4;
-  constexpr int ES = RawSlice<QDT>::ES;
+  constexpr int ES = RawSlice<QDT < 0 ? CIN_DT_BF16 : QDT>::ES;
   __shared__ __attribute__((aligned(16))) uint8_t kl[2][2][kKT * RS];
   __shared__ __attribute__((aligned(16))) float ksl[2][2][kKT];
   __shared__ __attribute__((aligned(16))) float ost[8 * 16 * OS];
@@ -461,66 +463,76 @@ __global__ __launch_bounds__(kPairThreads) __attribute__((amdgpu_waves_per_eu(2,
   KeyStage<D> stage;
   stage.load(k8, ks, b, S, h_begin, h_end, vec, tid);  // (keys past h_end read as zero)
 
-  // this half's two heads: raw rows, codes, scales, head weights
-  const uint8_t* qrow = static_cast<const uint8_t*>(qin) + orow * D * ES;
-  RawSlice<QDT> raw[2];
-  float wv[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int g = 2 * half + j;
-    const bool ok = tok_ok && g < H;
-    load_slice<D, QDT>(qrow + (int64_t)g * D * ES, ok, kq, 0, raw[j]);
-    wv[j] = ok ? w[orow + g] : 0.0f;
-  }
-  v8i own[2];
-  float own_w[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int g = 2 * half + j;
-    const bool ok = tok_ok && g < H;
-    float sc;
-    own[j] = quant_slice<QDT>(raw[j], sc);
-    own_w[j] = ok ? (sc * wv[j]) * softmax_scale : 0.0f;
-    if (q8_out != nullptr && ok && g % tiles_s == sw) {
-      const int off = 32 * kq;
-      if (off < D) {
-        uint8_t* dst = q8_out + (orow + g) * D + off;
-        const v8i f = own[j];
-        *reinterpret_cast<uint4*>(dst) = uint4{(uint32_t)f[0], (uint32_t)f[1], (uint32_t)f[2], (uint32_t)f[3]};
-        *reinterpret_cast<uint4*>(dst + 16) = uint4{(uint32_t)f[4], (uint32_t)f[5], (uint32_t)f[6], (uint32_t)f[7]};
-      }
-      if (kq == 0) qs_out[orow + g] = sc;
-    }
-  }
-  // trade through the (not yet used) staging area: [wave in half][head][lane][8 codes + weight]
-  uint32_t* xch = reinterpret_cast<uint32_t*>(ost);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    uint32_t* p = xch + ((wq * HG + 2 * half + j) * 64 + lane) * 9;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) p[e] = (uint32_t)own[j][e];
-    p[8] = __float_as_uint(own_w[j]);
-  }
-  __syncthreads();
-  v8i oth[2];
-  float oth_w[2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const uint32_t* p = xch + ((wq * HG + 2 * (1 - half) + j) * 64 + lane) * 9;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) oth[j][e] = (int)p[e];
-    oth_w[j] = __uint_as_float(p[8]);
-  }
   v8i qf[HG];
   float wr[HG];
-  qf[0] = half == 0 ? own[0] : oth[0];
-  qf[1] = half == 0 ? own[1] : oth[1];
-  qf[2] = half == 0 ? oth[0] : own[0];
-  qf[3] = half == 0 ? oth[1] : own[1];
-  wr[0] = half == 0 ? own_w[0] : oth_w[0];
-  wr[1] = half == 0 ? own_w[1] : oth_w[1];
-  wr[2] = half == 0 ? oth_w[0] : own_w[0];
-  wr[3] = half == 0 ? oth_w[1] : own_w[1];
+  if constexpr (QDT < 0) {
+    const uint8_t* qrow = static_cast<const uint8_t*>(qin) + orow * D;
+#pragma unroll
+    for (int g = 0; g < HG; ++g) {
+      const bool ok = tok_ok && g < H;
+      qf[g] = frag32<D>(qrow + g * D, ok, kq, 0);
+      wr[g] = ok ? (qs[orow + g] * w[orow + g]) * softmax_scale : 0.0f;
+    }
+  } else {
+    // this half's two heads: raw rows, codes, scales, head weights
+    const uint8_t* qrow = static_cast<const uint8_t*>(qin) + orow * D * ES;
+    RawSlice<QDT> raw[2];
+    float wv[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int g = 2 * half + j;
+      const bool ok = tok_ok && g < H;
+      load_slice<D, QDT>(qrow + (int64_t)g * D * ES, ok, kq, 0, raw[j]);
+      wv[j] = ok ? w[orow + g] : 0.0f;
+    }
+    v8i own[2];
+    float own_w[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int g = 2 * half + j;
+      const bool ok = tok_ok && g < H;
+      float sc;
+      own[j] = quant_slice<QDT>(raw[j], sc);
+      own_w[j] = ok ? (sc * wv[j]) * softmax_scale : 0.0f;
+      if (q8_out != nullptr && ok && g % tiles_s == sw) {
+        const int off = 32 * kq;
+        if (off < D) {
+          uint8_t* dst = q8_out + (orow + g) * D + off;
+          const v8i f = own[j];
+          *reinterpret_cast<uint4*>(dst) = uint4{(uint32_t)f[0], (uint32_t)f[1], (uint32_t)f[2], (uint32_t)f[3]};
+          *reinterpret_cast<uint4*>(dst + 16) = uint4{(uint32_t)f[4], (uint32_t)f[5], (uint32_t)f[6], (uint32_t)f[7]};
+        }
+        if (kq == 0) qs_out[orow + g] = sc;
+      }
+    }
+    // trade through the (not yet used) staging area: [wave in half][head][lane][8 codes + weight]
+    uint32_t* xch = reinterpret_cast<uint32_t*>(ost);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uint32_t* p = xch + ((wq * HG + 2 * half + j) * 64 + lane) * 9;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) p[e] = (uint32_t)own[j][e];
+      p[8] = __float_as_uint(own_w[j]);
+    }
+    __syncthreads();
+    v8i oth[2];
+    float oth_w[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t* p = xch + ((wq * HG + 2 * (1 - half) + j) * 64 + lane) * 9;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) oth[j][e] = (int)p[e];
+      oth_w[j] = __uint_as_float(p[8]);
+    }
+    qf[0] = half == 0 ? own[0] : oth[0];
+    qf[1] = half == 0 ? own[1] : oth[1];
+    qf[2] = half == 0 ? oth[0] : own[0];
+    qf[3] = half == 0 ? oth[1] : own[1];
+    wr[0] = half == 0 ? own_w[0] : oth_w[0];
+    wr[1] = half == 0 ? own_w[1] : oth_w[1];
+    wr[2] = half == 0 ? oth_w[0] : own_w[0];
+    wr[3] = half == 0 ? oth_w[1] : own_w[1];
+  }
   stage.store(kl[half][0], ksl[half][0], tid);
   __syncthreads();  // the trade's reads are done before any wave stages scores over it
 
@@ -947,6 +959,23 @@ int cin_indexer_scores_fp8(const uint8_t* q8, const float* q_scale, const uint8_
   const int xcd_rotate = grid % 8 == 0;
   const int vec = S % 4 == 0 && (((uintptr_t)k_scale) & 15) == 0 && (((uintptr_t)scores) & 15) == 0;
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (d <= 128 && H <= 4 && S > kKPW) {
+    // 8 waves per 64 tokens x 1024 keys: q's codes read once per 1024 keys
+    const int64_t tiles_s2 = cdiv(S, kKPW2);
+    const unsigned grid2 = (unsigned)(B * tiles_t * tiles_s2);
+    const int xr2 = grid2 % 8 == 0;
+    switch (d / 32) {
+#define CIN_INDEXER_PC_CASE(n)                                                                        \
+  case n:                                                                                             \
+    hipLaunchKernelGGL((k_indexer_scores_fp8_pair<32 * n, -1>), grid2, kPairThreads, 0, st, q8, k8, k_scale, \
+                       weights, L, S, H, softmax_scale, scores, tiles_t, tiles_s2, xr2, vec, nullptr,       \
+                       nullptr, q_scale);                                                             \
+    break;
+      CIN_INDEXER_PC_CASE(1) CIN_INDEXER_PC_CASE(2) CIN_INDEXER_PC_CASE(3) CIN_INDEXER_PC_CASE(4)
+#undef CIN_INDEXER_PC_CASE
+    }
+    return cin_check_launch("indexer_scores_fp8");
+  }
   switch (d / 32) {
 #define CIN_INDEXER_CASE(n, hg)                                                                 \
   case n:                                                                                       \

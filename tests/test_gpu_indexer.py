@@ -94,6 +94,17 @@ def test_fused_q_quantization_equals_the_two_calls(dev, B, L, S, H, d, dtype):
             assert q8b.numel() == 0 and qsb.numel() == 0
 
 
+@pytest.mark.parametrize("B,L,S,H,d", [(2, 1024, 1024, 4, 128), (1, 77, 2049, 2, 32), (2, 70, 600, 3, 96)])
+def test_codes_entry_matches_the_oracle(dev, B, L, S, H, d):
+    """cin_indexer_scores_fp8 on codes (the C entry for callers that quantize q themselves;
+    8 waves per 1024 keys at these shapes) against the oracle, same bounds as above."""
+    q, k, w = _inputs(B, L, S, H, d, torch.bfloat16, seed=B * 31 + L + S)
+    ops = torch.ops.cinnamon_amd
+    q8, qs, k8, ks = ops.indexer_quantize(q.to(dev), k.to(dev))
+    got = ops.indexer_scores_fp8(q8, qs, k8, ks, w.to(dev), 0.125).cpu()
+    _check(got, orc.indexer_scores_fp8_ref(q, k, w, 0.125))
+
+
 def test_zero_rows_and_negative_weights(dev):
     q, k, w = _inputs(2, 100, 96, 4, 64, torch.bfloat16, seed=7)
     q[0, 3] = 0          # all heads of one query: zero row -> floor scale, zero scores
